@@ -1,0 +1,74 @@
+/* kmamba_km.h - libkmamba extensions with no single counterpart in the
+ * reference API: batched and strided scan layouts, bf16 I/O, explicit HIP
+ * streams and error reporting.
+ *
+ * All pointers are device pointers. Entry points are asynchronous on the
+ * given stream (a hipStream_t passed as void*, NULL for the null stream) and
+ * return 0 on success, -1 on invalid arguments or a launch failure; the
+ * reason is available from km_last_error(). No entry point allocates device
+ * memory on the hot path.
+ */
+#ifndef KMAMBA_KM_H
+#define KMAMBA_KM_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Last error message of the calling thread ("" when none). */
+const char *km_last_error(void);
+void km_clear_error(void);
+
+/* Library version string. */
+const char *km_version(void);
+
+typedef enum {
+    KM_F32 = 0,   /* IEEE fp32 */
+    KM_BF16 = 1   /* bfloat16 storage, fp32 arithmetic, round-to-nearest-even on store */
+} KMDtype;
+
+/* Batched, strided Scan1D forward.
+ *
+ * Generalises the reference scan1d (cpu/scan1d.asm:40-179) to a batch and to
+ * B/C operands shared over channels. For every b, d, n and t:
+ *   e     = exp(delta[b,t,d] * A[d,n])
+ *   h     = e * h + B(b,t,d,n) * (delta[b,t,d] * x[b,t,d])
+ *   h     = clamp(h, -1000, 1000)            when clamp != 0
+ *   y[b,t,d] = sum_n C(b,t,d,n) * h
+ * x, delta, y : [B, L, D] contiguous, dtype
+ * A           : [D, N] fp32
+ * B(b,t,d,n)  : Bm[b*bc_sb + t*bc_st + d*bc_sd + n], dtype (same for Cm).
+ *               Shared over channels: bc_sd = 0 (e.g. [B, L, N]).
+ *               Reference API layout [L, D, N]: bc_sd = N, bc_st = D*N.
+ * h0          : [B, D, N] fp32 initial state, NULL for zero
+ * h_final     : [B, D, N] fp32 final state, may be NULL (may alias h0)
+ * h_hist      : [B, L, D, N] fp32 state after every step, may be NULL
+ * The +-1000 clamp is not associative; the kernel runs the unclamped
+ * chunked scan and re-runs any (b, channel group) whose state left
+ * [-1000, 1000] with the sequential clamped recurrence, so results follow the
+ * per-step clamp exactly as the reference CPU path does. */
+typedef struct {
+    const void  *x;
+    const void  *delta;
+    const float *A;
+    const void  *Bm;
+    const void  *Cm;
+    void        *y;
+    const float *h0;
+    float       *h_final;
+    float       *h_hist;
+    long B, L, D, N;
+    long bc_sb, bc_st, bc_sd;
+    int  dtype;
+    int  clamp;
+} KMScan1DFwd;
+
+int km_scan1d_fwd(const KMScan1DFwd *a, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KMAMBA_KM_H */

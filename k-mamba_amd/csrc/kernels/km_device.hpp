@@ -1,0 +1,82 @@
+// km_device.hpp - device-side helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace km {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Element type tags. Storage is fp32 or bfloat16; arithmetic is always fp32.
+struct f32_t  { using storage = float; };
+struct bf16_t { using storage = uint16_t; };
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) {
+    return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16; NaN stays NaN (quiet bit forced).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+template <typename T> struct io;
+template <> struct io<f32_t> {
+    using S = float;
+    static __device__ __forceinline__ float ld(const void *p, long i) {
+        return static_cast<const float *>(p)[i];
+    }
+    static __device__ __forceinline__ void st(void *p, long i, float v) {
+        static_cast<float *>(p)[i] = v;
+    }
+};
+template <> struct io<bf16_t> {
+    using S = uint16_t;
+    static __device__ __forceinline__ float ld(const void *p, long i) {
+        return bf16_to_f32(static_cast<const uint16_t *>(p)[i]);
+    }
+    static __device__ __forceinline__ void st(void *p, long i, float v) {
+        static_cast<uint16_t *>(p)[i] = f32_to_bf16(v);
+    }
+};
+
+// 2^x on the transcendental unit (v_exp_f32, ~1 ulp).
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Raw buffer resource over [base, base + bytes): loads past the end return 0
+// and stores past the end are dropped by the hardware range check. Word 3 is
+// the gfx9 raw-buffer format (no swizzle, 32-bit data).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, long bytes) {
+    const int n = bytes > 0x7fffffffL ? 0x7fffffff : static_cast<int>(bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, n, 0x00020000);
+}
+
+// Element loads/stores through a buffer resource. voff: per-lane byte offset
+// (range-checked); soff: wave-uniform SGPR byte offset, which the gfx9 raw
+// buffer range check does NOT cover, so callers keep it 0 unless the access
+// is known to be in bounds.
+template <typename T> struct bio;
+template <> struct bio<f32_t> {
+    static constexpr int size = 4;
+    static __device__ __forceinline__ float ld(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+    }
+    static __device__ __forceinline__ void st(__amdgpu_buffer_rsrc_t r, int voff, int soff, float v) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, voff, soff, 0);
+    }
+};
+template <> struct bio<bf16_t> {
+    static constexpr int size = 2;
+    static __device__ __forceinline__ float ld(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+        return bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0));
+    }
+    static __device__ __forceinline__ void st(__amdgpu_buffer_rsrc_t r, int voff, int soff, float v) {
+        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), r, voff, soff, 0);
+    }
+};
+
+}  // namespace km

@@ -1,0 +1,634 @@
+// scan1d_fwd.hip - Scan1D selective-scan forward for gfx950.
+//
+// Recurrence (reference cpu/scan1d.asm:53-169, per batch element):
+//   e = exp(delta*A[d,n]);  h = e*h + B*(delta*x);  y = sum_n C*h
+//
+// Design (one kernel, no scratch memory):
+//  * A wave covers DL = 64/NS channels; its lanes split the N states into NS
+//    groups of NPL states kept in registers (N=16: 32 channels x 2 halves), so
+//    x/delta/y rows are read and written as whole 128-byte lines and the
+//    B/C operand a lane needs is one LDS broadcast row.
+//  * A workgroup of W waves owns one (batch, channel group) for the whole
+//    sequence and walks it in super-chunks of W*TC steps. Wave w runs a local
+//    pass over its TC steps from a zero state, keeping every exp in registers,
+//    and publishes its chunk map h -> P*h + h_loc (P = exp2(A*log2e*sum
+//    delta)) through LDS. After one barrier each wave folds the carry and the
+//    maps of the waves before it, then replays its steps from the exact
+//    incoming state with the stored exps, writing y (and the state history
+//    when asked). The last wave's state is the next super-chunk's carry.
+//  * Shared B/C ([B, L, N], stride over channels 0) are staged per
+//    super-chunk into LDS, double-buffered and prefetched one super-chunk
+//    ahead; per-channel B/C (the reference [L, D, M] layout) are read
+//    straight from memory. x/delta of the next super-chunk are prefetched into
+//    registers.
+//  * The reference clamps the state to +-1000 after every step
+//    (cpu/scan1d.asm:136-140), which is not associative. The chunked pass runs
+//    unclamped and tracks max|h| and NaN; a workgroup that saw either re-runs
+//    its whole sequence with the sequential clamped recurrence, so results
+//    follow the per-step clamp exactly.
+#include <cstdlib>
+
+#include "km_device.hpp"
+#include "../km_runtime.hpp"
+#include "kmamba_km.h"
+#include "scan.h"
+#include "mamba_scan.h"
+#include "mamba_scan_cuda.h"
+
+namespace km {
+
+struct Scan1DFwdArgs {
+    const void *x, *dt;
+    const float *A;
+    const void *Bm, *Cm;
+    void *y;
+    const float *h0;
+    float *hfin;
+    float *hist;
+    long B, L, D, N;
+    long sb, st, sd;
+    int clamp;
+};
+
+// Sequential clamped recurrence for the lanes of one wave (the clamp
+// fallback): the reference's step order, one (batch, channel, state group)
+// per lane.
+template <typename T, int NPL, int NS, bool SHARED, bool HIST>
+__device__ void scan1d_serial_wave(const Scan1DFwdArgs &p, long b, long d, bool dvalid,
+                                   int n0, const float *Ap) {
+    using IO = io<T>;
+    const long dc = dvalid ? d : p.D - 1;
+    const long N = p.N;
+    float hs[NPL];
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) hs[j] = p.h0 ? p.h0[(b * p.D + dc) * N + n0 + j] : 0.f;
+    for (long t = 0; t < p.L; ++t) {
+        const long xi = (b * p.L + t) * p.D + dc;
+        const float xv = IO::ld(p.x, xi), dv = IO::ld(p.dt, xi);
+        const long bc = b * p.sb + t * p.st + (SHARED ? 0 : dc * p.sd) + n0;
+        float yp = 0.f;
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+            const float e = exp2_fast(dv * Ap[j]);
+            const float dB = __fmul_rn(IO::ld(p.Bm, bc + j), dv);
+            float hn = __fadd_rn(__fmul_rn(e, hs[j]), __fmul_rn(dB, xv));
+            hn = (hn < 1000.f) ? hn : 1000.f;
+            hn = (hn > -1000.f) ? hn : -1000.f;
+            hs[j] = hn;
+            yp = __fadd_rn(yp, __fmul_rn(IO::ld(p.Cm, bc + j), hn));
+        }
+        if (NS >= 4) yp += __shfl_xor(yp, 16);
+        if (NS >= 2) yp += __shfl_xor(yp, 32);
+        if (dvalid) {
+            if (n0 == 0) IO::st(p.y, xi, yp);
+            if (HIST) {
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) p.hist[xi * N + n0 + j] = hs[j];
+            }
+        }
+    }
+    if (p.hfin && dvalid) {
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) p.hfin[(b * p.D + d) * N + n0 + j] = hs[j];
+    }
+}
+
+// Powers e1^(n0+1), ..., e1^(n0+NPL) of a lane's state group, n0 = ns*NPL:
+// the decays exp(delta*A[d,n]) when A[d,n] = (n+1)*A[d,0] (S4D-real
+// initialisation). Branch-free: the power e1^n0 is assembled from the
+// squarings e1^NPL, e1^(2*NPL), ... selected by the bits of n0.
+template <int NPL, int NS>
+__device__ __forceinline__ void pow_chain(float e1, int n0, float (&e)[NPL]) {
+    float pw = e1;
+    if constexpr (NS > 1) {
+        float sq = e1;
+#pragma unroll
+        for (int k = 1; k < NPL; k <<= 1) sq *= sq;          // e1^NPL
+#pragma unroll
+        for (int bit = NPL; bit < NPL * NS; bit <<= 1) {
+            pw *= (n0 & bit) ? sq : 1.0f;
+            sq *= sq;
+        }
+    }
+    e[0] = pw;
+#pragma unroll
+    for (int j = 1; j < NPL; ++j) e[j] = e[j - 1] * e1;
+}
+
+// OCC: waves per SIMD the register allocation must allow (2 workgroups of
+// 8 waves per CU need 4).
+template <typename T, int NPL, int NS, int W, int TC, bool SHARED, bool HIST, bool STORE_BU, int OCC>
+__global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs p) {
+    using IO = bio<T>;
+    constexpr int DL = 64 / NS;      // channels per wave
+    constexpr int N = NPL * NS;      // states per channel
+    constexpr int SC = W * TC;       // steps per super-chunk
+    constexpr int TILE = SC * N;     // B (or C) values per super-chunk
+    constexpr int NT = 64 * W;
+    constexpr int TPT = (TILE + NT - 1) / NT;
+    constexpr int TS = IO::size;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, kept in an SGPR
+    const int dl = lane % DL;
+    const int ns = lane / DL;
+    const int n0 = ns * NPL;
+    const long ngroups = (p.D + DL - 1) / DL;
+    const long b = blockIdx.x / ngroups;
+    const long d = (blockIdx.x - b * ngroups) * DL + dl;
+    const bool dvalid = d < p.D;
+    const int dc = static_cast<int>(dvalid ? d : p.D - 1);
+    const int L = static_cast<int>(p.L);
+    const int Dm = static_cast<int>(p.D);
+    const int nit = (L + SC - 1) / SC;
+    const bool store_y = dvalid && ns == 0;
+
+    // Per-batch-element windows addressed with 32-bit byte offsets (the
+    // launcher keeps every window and offset below 1 GiB). Every variable
+    // offset goes in the VGPR offset so the hardware range check applies:
+    // rows past L load as 0 and their stores are dropped.
+    const long xoff = b * p.L * p.D;
+    const auto rx = make_rsrc(static_cast<const char *>(p.x) + xoff * TS, p.L * p.D * TS);
+    const auto rdt = make_rsrc(static_cast<const char *>(p.dt) + xoff * TS, p.L * p.D * TS);
+    const auto ry = make_rsrc(static_cast<char *>(p.y) + xoff * TS, p.L * p.D * TS);
+    const auto rB = make_rsrc(static_cast<const char *>(p.Bm) + b * p.sb * TS, p.L * p.st * TS);
+    const auto rC = make_rsrc(static_cast<const char *>(p.Cm) + b * p.sb * TS, p.L * p.st * TS);
+    const auto rh = make_rsrc(p.hist ? p.hist + xoff * p.N : nullptr, HIST ? p.L * p.D * p.N * 4 : 0);
+    const int vx = dc * TS;                             // lane byte offset in an x row
+    const int rowx = Dm * TS;                           // bytes per x row
+    const int rowbc = static_cast<int>(p.st) * TS;      // bytes per B/C row
+    const int vbc = SHARED ? 0 : (dc * static_cast<int>(p.sd) + n0) * TS;
+    const int vh = (dc * N + n0) * 4;
+
+    __shared__ float sB[SHARED ? 3 : 1][SHARED ? TILE : 1];
+    __shared__ float sC[SHARED ? 3 : 1][SHARED ? TILE : 1];
+    // Chunk maps and incoming states are written between two barriers and
+    // read before the next write can start, so one buffer each suffices; the
+    // carry is read and rewritten in the same phase and keeps two.
+    __shared__ float aggP[W][NPL][64];
+    __shared__ float aggH[W][NPL][64];
+    __shared__ float carry[2][NPL][64];
+    __shared__ float pin[W][NPL][64];       // incoming state of each wave
+
+    float Ap[NPL];
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) Ap[j] = p.A[dc * N + n0 + j] * kLog2e;
+    const float A0p = p.A[dc * N] * kLog2e;
+    // Structured decays (A[d,n] == (n+1)*A[d,0] for every state of every
+    // channel of the workgroup) switch exp per state for a power chain.
+    bool structured = (n0 == 0 || (n0 & (n0 - 1)) == 0);
+#pragma unroll
+    for (int j = 0; j < NPL; ++j)
+        structured = structured && (p.A[dc * N + n0 + j] == static_cast<float>(n0 + j + 1) * p.A[dc * N]);
+    const bool fast = __builtin_amdgcn_readfirstlane(__syncthreads_and(structured)) != 0;
+
+    if (w == 0) {
+#pragma unroll
+        for (int j = 0; j < NPL; ++j)
+            carry[0][j][lane] = p.h0 ? p.h0[(b * Dm + dc) * N + n0 + j] : 0.f;
+    }
+
+    // B/C tile of super-chunk s: element e = (step, state) at row s*SC + e/N.
+    float rb[TPT], rc[TPT];
+    auto load_tile = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < TPT; ++i) {
+            const int e = tid + i * NT;
+            const int t = s * SC + e / N;
+            const int off = (e % N) * TS;
+            const int so = t * rowbc;
+            rb[i] = (e < TILE) ? IO::ld(rB, off + so, 0) : 0.f;
+            rc[i] = (e < TILE) ? IO::ld(rC, off + so, 0) : 0.f;
+        }
+    };
+    auto store_tile = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < TPT; ++i) {
+            const int e = tid + i * NT;
+            if (e < TILE) {
+                sB[slot][e] = rb[i];
+                sC[slot][e] = rc[i];
+            }
+        }
+    };
+    auto load_xd = [&](int s, float (&xo)[TC], float (&dto)[TC]) {
+#pragma unroll
+        for (int k = 0; k < TC; ++k) {
+            const int so = (s * SC + w * TC + k) * rowx;   // rows past L read as 0
+            xo[k] = IO::ld(rx, vx + so, 0);
+            dto[k] = IO::ld(rdt, vx + so, 0);
+        }
+    };
+    auto bc_row = [&](const float (*tile)[SHARED ? TILE : 1], __amdgpu_buffer_rsrc_t r, int slot,
+                      int s, int k, float (&out)[NPL]) {
+        if constexpr (SHARED) {
+            const float *row = &tile[slot][(w * TC + k) * N + n0];
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) out[j] = row[j];
+        } else {
+            const int so = (s * SC + w * TC + k) * rowbc;
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) out[j] = IO::ld(r, vbc + j * TS + so, 0);
+        }
+    };
+
+    if constexpr (SHARED) {
+        load_tile(0);
+        store_tile(0);
+        if (nit > 1) load_tile(1);
+    }
+    float X0[TC], D0[TC], X1[TC], D1[TC];
+    load_xd(0, X0, D0);
+    __syncthreads();
+
+    float h[NPL];
+    float hmax = 0.f;
+    bool nan_seen = false;
+
+    auto body = [&](int s, float (&xs)[TC], float (&ds)[TC], float (&xn)[TC], float (&dn)[TC]) {
+        const int cur = s & 1;
+        const int slot = s % 3;
+        if constexpr (SHARED) {
+            if (s + 1 < nit) {           // tile s+1 -> LDS (slot last read in s-2)
+                store_tile((s + 1) % 3);
+                if (s + 2 < nit) load_tile(s + 2);
+            }
+        }
+        if (s + 1 < nit) load_xd(s + 1, xn, dn);
+
+        // Local pass from a zero state; decays (and optionally B*u) kept for
+        // the replay.
+        float e[TC][NPL];
+        float bus[STORE_BU ? TC : 1][NPL];
+        float hl[NPL];
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) hl[j] = 0.f;
+        float dsum = 0.f;
+        float bln[NPL];
+        bc_row(sB, rB, slot, s, 0, bln);
+#pragma unroll
+        for (int k = 0; k < TC; ++k) {
+            float bv[NPL];
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) bv[j] = bln[j];
+            if (k + 1 < TC) bc_row(sB, rB, slot, s, k + 1, bln);
+            const float u = ds[k] * xs[k];
+            dsum += ds[k];
+            if (fast) {
+                pow_chain<NPL, NS>(exp2_fast(ds[k] * A0p), n0, e[k]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) e[k][j] = exp2_fast(ds[k] * Ap[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) {
+                const float bu = bv[j] * u;
+                if constexpr (STORE_BU) bus[k][j] = bu;
+                hl[j] = fmaf(e[k][j], hl[j], bu);
+            }
+        }
+        float P[NPL];
+        if (fast) {
+            pow_chain<NPL, NS>(exp2_fast(dsum * A0p), n0, P);
+        } else {
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) P[j] = exp2_fast(Ap[j] * dsum);
+        }
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+            aggP[w][j][lane] = P[j];
+            aggH[w][j][lane] = hl[j];
+        }
+        __syncthreads();
+
+        // Balanced prefix over the W chunk maps: thread (w, lane) scans the
+        // states j = w, w+W, ... of its lane across all waves, writing each
+        // wave's incoming state and the super-chunk's outgoing carry.
+        for (int j = w; j < NPL; j += W) {
+            float pv[W], hv[W];
+#pragma unroll
+            for (int v = 0; v < W; ++v) {
+                pv[v] = aggP[v][j][lane];
+                hv[v] = aggH[v][j][lane];
+            }
+            float run = carry[cur][j][lane];
+#pragma unroll
+            for (int v = 0; v < W; ++v) {
+                pin[v][j][lane] = run;
+                run = fmaf(pv[v], run, hv[v]);
+            }
+            carry[cur ^ 1][j][lane] = run;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) h[j] = pin[w][j][lane];
+
+        // Replay from the exact incoming state; B/C rows of step k+1 are read
+        // while step k computes.
+        float bvn[NPL], cvn[NPL];
+        if constexpr (!STORE_BU) bc_row(sB, rB, slot, s, 0, bvn);
+        bc_row(sC, rC, slot, s, 0, cvn);
+#pragma unroll
+        for (int k = 0; k < TC; ++k) {
+            const int t = s * SC + w * TC + k;
+            float bv[NPL], cv[NPL];
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) {
+                bv[j] = bvn[j];
+                cv[j] = cvn[j];
+            }
+            if (k + 1 < TC) {
+                if constexpr (!STORE_BU) bc_row(sB, rB, slot, s, k + 1, bvn);
+                bc_row(sC, rC, slot, s, k + 1, cvn);
+            }
+            const float u = ds[k] * xs[k];
+            float yp = 0.f;
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) {
+                const float bu = STORE_BU ? bus[k][j] : bv[j] * u;
+                h[j] = fmaf(e[k][j], h[j], bu);
+                yp = fmaf(cv[j], h[j], yp);
+                hmax = fmaxf(hmax, fabsf(h[j]));
+            }
+            // Sum the state groups of this channel (lanes dl + DL*ns).
+            if constexpr (NS >= 4) yp += __shfl_xor(yp, 16);
+            if constexpr (NS >= 2) yp += __shfl_xor(yp, 32);
+            nan_seen |= (yp != yp);
+            if (store_y) IO::st(ry, vx + t * rowx, 0, yp);       // rows past L dropped
+            if constexpr (HIST) {
+                if (dvalid) {
+#pragma unroll
+                    for (int j = 0; j < NPL; ++j)
+                        bio<f32_t>::st(rh, vh + j * 4 + t * Dm * N * 4, 0, h[j]);
+                }
+            }
+        }
+    };
+
+    for (int s = 0; s < nit; s += 2) {
+        body(s, X0, D0, X1, D1);
+        if (s + 1 < nit) body(s + 1, X1, D1, X0, D0);
+    }
+
+    const int bad = p.clamp && (nan_seen || hmax > 1000.f);
+    if (__syncthreads_or(bad)) {
+        if (w == 0) scan1d_serial_wave<T, NPL, NS, SHARED, HIST>(p, b, d, dvalid, n0, Ap);
+        return;
+    }
+    if (w == W - 1 && p.hfin && dvalid) {
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) p.hfin[(b * Dm + d) * N + n0 + j] = h[j];
+    }
+}
+
+// Fallback for state sizes without a register-blocked instantiation
+// (N not in {1, 2, 4, 8, 16}, N <= 64): one thread per (batch, channel), the
+// reference's sequential step order with the per-step clamp.
+template <typename T, bool HIST>
+__global__ void __launch_bounds__(256) scan1d_fwd_serial(Scan1DFwdArgs p) {
+    using IO = io<T>;
+    const long gid = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid >= p.B * p.D) return;
+    const long b = gid / p.D, d = gid % p.D;
+    const long N = p.N;
+    float st[64];
+    for (long m = 0; m < N; ++m) st[m] = p.h0 ? p.h0[(b * p.D + d) * N + m] : 0.f;
+    for (long t = 0; t < p.L; ++t) {
+        const long xi = (b * p.L + t) * p.D + d;
+        const float xv = IO::ld(p.x, xi), dv = IO::ld(p.dt, xi);
+        const long bc = b * p.sb + t * p.st + d * p.sd;
+        float y = 0.f;
+        for (long m = 0; m < N; ++m) {
+            const float e = exp2_fast(dv * p.A[d * N + m] * kLog2e);
+            const float dB = __fmul_rn(IO::ld(p.Bm, bc + m), dv);
+            float hn = __fadd_rn(__fmul_rn(e, st[m]), __fmul_rn(dB, xv));
+            if (p.clamp) {
+                hn = (hn < 1000.f) ? hn : 1000.f;
+                hn = (hn > -1000.f) ? hn : -1000.f;
+            }
+            st[m] = hn;
+            if (HIST) p.hist[xi * N + m] = hn;
+            y = __fadd_rn(y, __fmul_rn(IO::ld(p.Cm, bc + m), hn));
+        }
+        IO::st(p.y, xi, y);
+    }
+    if (p.hfin)
+        for (long m = 0; m < N; ++m) p.hfin[(b * p.D + d) * N + m] = st[m];
+}
+
+template <typename T, int NPL, int NS, int W, int TC, bool SBU = false, int OCC = 2>
+static int launch_chunked(const Scan1DFwdArgs &a, bool shared, bool hist, hipStream_t s) {
+    const long DL = 64 / NS;
+    const long grid = a.B * ((a.D + DL - 1) / DL);
+    if (grid <= 0 || grid > 0x7fffffffL) {
+        set_error("km_scan1d_fwd: grid of %ld workgroups out of range", grid);
+        return -1;
+    }
+    dim3 g(static_cast<unsigned>(grid)), blk(64 * W);
+    if (shared) {
+        if (hist) hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, W, TC, true, true, SBU, OCC>), g, blk, 0, s, a);
+        else      hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, W, TC, true, false, SBU, OCC>), g, blk, 0, s, a);
+    } else {
+        if (hist) hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, W, TC, false, true, SBU, OCC>), g, blk, 0, s, a);
+        else      hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, W, TC, false, false, SBU, OCC>), g, blk, 0, s, a);
+    }
+    KM_HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+// Tuning knob for N = 16 (KM_SCAN1D_CFG, read once): 0 = 32 channels x 2
+// state halves, 8 waves, 8 steps per wave; 1 = 16 channels x 4 state
+// quarters, 8 waves, 8 steps, 4 waves/SIMD (two workgroups per CU); 2 = as 1
+// with 16 steps at 2 waves/SIMD; 3 = as 1 with B*u kept in registers; 4 = as
+// 1 at 3 waves/SIMD; 5 = 16x4, 4 waves, 16 steps, 2 waves/SIMD; 6 (default,
+// fastest measured on MI355X) = as 0 with B*u kept in registers.
+static int scan1d_cfg16() {
+    static int cfg = [] {
+        const char *e = std::getenv("KM_SCAN1D_CFG");
+        return e ? std::atoi(e) : 6;
+    }();
+    return cfg;
+}
+
+template <typename T>
+static int launch_n16(const Scan1DFwdArgs &a, bool shared, bool hist, hipStream_t s) {
+    switch (scan1d_cfg16()) {
+    case 0: return launch_chunked<T, 8, 2, 8, 8>(a, shared, hist, s);
+    case 2: return launch_chunked<T, 4, 4, 8, 16>(a, shared, hist, s);
+    case 3: return launch_chunked<T, 4, 4, 8, 8, true, 4>(a, shared, hist, s);
+    case 4: return launch_chunked<T, 4, 4, 8, 8, false, 3>(a, shared, hist, s);
+    case 5: return launch_chunked<T, 4, 4, 4, 16>(a, shared, hist, s);
+    case 1: return launch_chunked<T, 4, 4, 8, 8, false, 4>(a, shared, hist, s);
+    case 6:
+    default: return launch_chunked<T, 8, 2, 8, 8, true>(a, shared, hist, s);
+    }
+}
+
+template <typename T>
+static int launch_serial(const Scan1DFwdArgs &a, bool hist, hipStream_t s) {
+    const long threads = a.B * a.D;
+    const long grid = (threads + 255) / 256;
+    if (grid > 0x7fffffffL) {
+        set_error("km_scan1d_fwd: grid out of range");
+        return -1;
+    }
+    if (hist) hipLaunchKernelGGL((scan1d_fwd_serial<T, true>), dim3(grid), dim3(256), 0, s, a);
+    else      hipLaunchKernelGGL((scan1d_fwd_serial<T, false>), dim3(grid), dim3(256), 0, s, a);
+    KM_HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream) {
+    if (!k) { set_error("km_scan1d_fwd: NULL arguments"); return -1; }
+    if (!k->x || !k->delta || !k->A || !k->Bm || !k->Cm || !k->y) {
+        set_error("km_scan1d_fwd: NULL tensor pointer");
+        return -1;
+    }
+    if (k->B <= 0 || k->L < 0 || k->D <= 0 || k->N <= 0 || k->N > 64) {
+        set_error("km_scan1d_fwd: invalid sizes B=%ld L=%ld D=%ld N=%ld (need N <= 64)",
+                  k->B, k->L, k->D, k->N);
+        return -1;
+    }
+    if (k->dtype != KM_F32 && k->dtype != KM_BF16) {
+        set_error("km_scan1d_fwd: unknown dtype %d", k->dtype);
+        return -1;
+    }
+    if (!gpu_ready()) return -1;
+    if (k->L == 0) {   // no steps: the final state is the initial state
+        if (k->h_final && k->h_final != k->h0) {
+            const size_t bytes = sizeof(float) * k->B * k->D * k->N;
+            if (k->h0) KM_HIP_TRY(hipMemcpyAsync(k->h_final, k->h0, bytes, hipMemcpyDeviceToDevice, stream));
+            else       KM_HIP_TRY(hipMemsetAsync(k->h_final, 0, bytes, stream));
+        }
+        return 0;
+    }
+    Scan1DFwdArgs a{k->x, k->delta, k->A, k->Bm, k->Cm, k->y, k->h0, k->h_final, k->h_hist,
+                    k->B, k->L, k->D, k->N, k->bc_sb, k->bc_st, k->bc_sd, k->clamp};
+    // The register-blocked kernel addresses each batch element's windows with
+    // 32-bit byte offsets; larger problems take the sequential kernel.
+    const long es = (k->dtype == KM_BF16) ? 2 : 4;
+    const long lim = 0x3fffffffL;   // offsets reach (L + W*TC) rows
+    const bool small_windows = k->L * k->D * es < lim && k->L * k->bc_st * es < lim &&
+                               (!k->h_hist || k->L * k->D * k->N * 4 < lim) &&
+                               k->bc_st >= 0 && k->bc_sd >= 0 && k->bc_sb >= 0;
+    const bool shared = (k->bc_sd == 0);
+    const bool hist = (k->h_hist != nullptr);
+    const bool bf = (k->dtype == KM_BF16);
+    if (!small_windows)
+        return bf ? launch_serial<bf16_t>(a, hist, stream) : launch_serial<f32_t>(a, hist, stream);
+    switch (k->N) {
+    case 16:
+        return bf ? launch_n16<bf16_t>(a, shared, hist, stream)
+                  : launch_n16<f32_t>(a, shared, hist, stream);
+    case 8:
+        if (!bf) return launch_chunked<f32_t, 8, 1, 8, 8>(a, shared, hist, stream);
+        break;
+    case 4:
+        if (!bf) return launch_chunked<f32_t, 4, 1, 8, 8>(a, shared, hist, stream);
+        break;
+    case 2:
+        if (!bf) return launch_chunked<f32_t, 2, 1, 8, 16>(a, shared, hist, stream);
+        break;
+    case 1:
+        if (!bf) return launch_chunked<f32_t, 1, 1, 8, 16>(a, shared, hist, stream);
+        break;
+    default:
+        break;
+    }
+    return bf ? launch_serial<bf16_t>(a, hist, stream) : launch_serial<f32_t>(a, hist, stream);
+}
+
+}  // namespace km
+
+extern "C" {
+
+int km_scan1d_fwd(const KMScan1DFwd *a, void *stream) {
+    km::clear_error();
+    return km::scan1d_fwd_launch(a, static_cast<hipStream_t>(stream));
+}
+
+// Reference cuda/scan1d.cu:258-310: B, C, h are [L, D, M]; h receives the
+// whole state history; zero initial state; per-step clamp as on the CPU.
+void om_scan1d_forward(const float *d_x, const float *d_A, const float *d_B, const float *d_C,
+                       const float *d_dt, float *d_y, float *d_h, int L, int D, int M) {
+    km::clear_error();
+    if (L < 0 || D <= 0 || M <= 0) {
+        km::set_error("om_scan1d_forward: invalid sizes L=%d D=%d M=%d", L, D, M);
+        return;
+    }
+    KMScan1DFwd a{};
+    a.x = d_x; a.delta = d_dt; a.A = d_A; a.Bm = d_B; a.Cm = d_C; a.y = d_y;
+    a.h0 = nullptr; a.h_final = nullptr; a.h_hist = d_h;
+    a.B = 1; a.L = L; a.D = D; a.N = M;
+    a.bc_sb = static_cast<long>(L) * D * M; a.bc_st = static_cast<long>(D) * M; a.bc_sd = M;
+    a.dtype = KM_F32; a.clamp = 1;
+    if (km::scan1d_fwd_launch(&a, nullptr) != 0) return;
+    if (hipStreamSynchronize(nullptr) != hipSuccess)
+        km::set_error("om_scan1d_forward: %s", hipGetErrorString(hipGetLastError()));
+}
+
+void mamba_scan1d_cuda_forward(const float *d_x, const float *d_A, const float *d_B,
+                               const float *d_C, const float *d_dt, float *d_y, float *d_h,
+                               int L, int D, int M) {
+    om_scan1d_forward(d_x, d_A, d_B, d_C, d_dt, d_y, d_h, L, D, M);
+}
+
+// Reference scan1d (cpu/scan1d.asm:40-179): host or device pointers; h is
+// the running [D, M] state (read, then overwritten with the final state).
+void scan1d(ScanParams *p) {
+    km::clear_error();
+    if (!p || !p->x || !p->A || !p->B || !p->C || !p->delta || !p->h || !p->y ||
+        p->L < 0 || p->D <= 0 || p->M <= 0) {
+        km::set_error("scan1d: invalid parameters");
+        return;
+    }
+    if (!km::gpu_ready()) return;
+    const long L = p->L, D = p->D, M = p->M;
+    const size_t nLD = L * D, nDM = D * M, nLDM = L * D * M;
+    KMScan1DFwd a{};
+    a.B = 1; a.L = L; a.D = D; a.N = M;
+    a.bc_sb = nLDM; a.bc_st = D * M; a.bc_sd = M;
+    a.dtype = KM_F32; a.clamp = 1;
+    const bool dev = km::is_device_ptr(p->x) && km::is_device_ptr(p->y) &&
+                     km::is_device_ptr(p->B) && km::is_device_ptr(p->C) &&
+                     km::is_device_ptr(p->delta) && km::is_device_ptr(p->A) &&
+                     km::is_device_ptr(p->h);
+    if (dev) {
+        a.x = p->x; a.delta = p->delta; a.A = p->A; a.Bm = p->B; a.Cm = p->C; a.y = p->y;
+        a.h0 = p->h; a.h_final = p->h;
+        if (km::scan1d_fwd_launch(&a, nullptr) == 0 && hipStreamSynchronize(nullptr) != hipSuccess)
+            km::set_error("scan1d: %s", hipGetErrorString(hipGetLastError()));
+        return;
+    }
+    km::Staging::lock();
+    const size_t bytes = sizeof(float) * (3 * nLD + nDM * 2 + 2 * nLDM) + 8 * 256;
+    void *base = km::Staging::reserve(bytes);
+    if (base) {
+        km::Carver c(base);
+        float *x = c.take<float>(nLD), *dt = c.take<float>(nLD), *y = c.take<float>(nLD);
+        float *A = c.take<float>(nDM), *h = c.take<float>(nDM);
+        float *Bm = c.take<float>(nLDM), *Cm = c.take<float>(nLDM);
+        bool ok = hipMemcpy(x, p->x, nLD * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                  hipMemcpy(dt, p->delta, nLD * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                  hipMemcpy(A, p->A, nDM * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                  hipMemcpy(h, p->h, nDM * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                  hipMemcpy(Bm, p->B, nLDM * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                  hipMemcpy(Cm, p->C, nLDM * 4, hipMemcpyHostToDevice) == hipSuccess;
+        if (!ok) {
+            km::set_error("scan1d: host-to-device copy failed");
+        } else {
+            a.x = x; a.delta = dt; a.A = A; a.Bm = Bm; a.Cm = Cm; a.y = y; a.h0 = h; a.h_final = h;
+            if (km::scan1d_fwd_launch(&a, nullptr) == 0) {
+                if (hipMemcpy(p->y, y, nLD * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+                    hipMemcpy(p->h, h, nDM * 4, hipMemcpyDeviceToHost) != hipSuccess)
+                    km::set_error("scan1d: device-to-host copy failed");
+            }
+        }
+    }
+    km::Staging::unlock();
+}
+
+void mamba_scan1d_forward(MambaScan1DParams *p) { scan1d(p); }
+
+}  // extern "C"

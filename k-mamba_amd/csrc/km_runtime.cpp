@@ -1,0 +1,174 @@
+// km_runtime.cpp - error reporting, backend selection and staging memory.
+#include "km_runtime.hpp"
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <strings.h>
+
+#include "kmamba_cuda_utils.h"
+#include "kmamba_km.h"
+
+namespace {
+thread_local char g_err[512] = "";
+
+std::once_flag g_backend_once;
+std::once_flag g_probe_once;
+int g_device_count = 0;
+int g_usable = 0;
+char g_probe_msg[256] = "";
+
+void probe_devices() {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        std::snprintf(g_probe_msg, sizeof g_probe_msg, "hipGetDeviceCount: %s (count %d)",
+                      hipGetErrorString(e), n);
+        (void)hipGetLastError();
+        g_device_count = 0;
+        g_usable = 0;
+        return;
+    }
+    g_device_count = n;
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, 0);
+    g_usable = (e == hipSuccess) ? 1 : 0;
+    if (!g_usable)
+        std::snprintf(g_probe_msg, sizeof g_probe_msg, "hipGetDeviceProperties: %s",
+                      hipGetErrorString(e));
+}
+
+void parse_backend_env() {
+    const char *env = std::getenv("KMAMBA_BACKEND");
+    if (!env || strcasecmp(env, "auto") == 0) {
+        kmamba_backend_preference = KMAMBA_BACKEND_AUTO;
+    } else if (strcasecmp(env, "cpu") == 0) {
+        kmamba_backend_preference = KMAMBA_BACKEND_CPU;
+        std::fprintf(stderr, "[k-mamba] Backend forced to CPU via environment "
+                             "(this library has no CPU compute path)\n");
+    } else if (strcasecmp(env, "gpu") == 0 || strcasecmp(env, "cuda") == 0) {
+        kmamba_backend_preference = KMAMBA_BACKEND_GPU;
+        std::fprintf(stderr, "[k-mamba] Backend forced to GPU via environment\n");
+    } else {
+        std::fprintf(stderr, "[k-mamba] Warning: Unknown KMAMBA_BACKEND='%s', using auto\n", env);
+        kmamba_backend_preference = KMAMBA_BACKEND_AUTO;
+    }
+}
+
+std::mutex g_stage_mu;
+void *g_stage_ptr[64] = {};
+size_t g_stage_size[64] = {};
+}  // namespace
+
+extern "C" {
+
+KMambaBackend kmamba_backend_preference = KMAMBA_BACKEND_AUTO;
+
+int kmamba_cuda_available(void) {
+    std::call_once(g_probe_once, probe_devices);
+    if (!g_usable && g_probe_msg[0]) km::set_error("%s", g_probe_msg);
+    return g_usable;
+}
+
+int kmamba_cuda_device_count(void) {
+    std::call_once(g_probe_once, probe_devices);
+    return g_device_count;
+}
+
+int kmamba_cuda_current_device(void) {
+    if (!kmamba_cuda_available()) return -1;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) return -1;
+    return dev;
+}
+
+void kmamba_backend_init(void) { std::call_once(g_backend_once, parse_backend_env); }
+
+KMambaBackend kmamba_backend_select(void) {
+    kmamba_backend_init();
+    switch (kmamba_backend_preference) {
+    case KMAMBA_BACKEND_CPU:
+        return KMAMBA_BACKEND_CPU;
+    case KMAMBA_BACKEND_GPU:
+        if (!kmamba_cuda_available()) {
+            std::fprintf(stderr, "[k-mamba] Error: GPU requested but not available\n");
+            return KMAMBA_BACKEND_CPU;
+        }
+        return KMAMBA_BACKEND_GPU;
+    case KMAMBA_BACKEND_AUTO:
+    default:
+        return kmamba_cuda_available() ? KMAMBA_BACKEND_GPU : KMAMBA_BACKEND_CPU;
+    }
+}
+
+const char *km_last_error(void) { return g_err; }
+void km_clear_error(void) { g_err[0] = '\0'; }
+const char *km_version(void) { return "libkmamba-mi355x 0.1 (gfx950)"; }
+
+}  // extern "C"
+
+namespace km {
+
+void set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+void clear_error() { g_err[0] = '\0'; }
+
+bool gpu_ready() {
+    if (kmamba_backend_select() != KMAMBA_BACKEND_GPU) {
+        if (kmamba_backend_preference == KMAMBA_BACKEND_CPU)
+            set_error("KMAMBA_BACKEND=cpu: libkmamba has no CPU compute path");
+        else if (g_probe_msg[0])
+            set_error("no usable HIP device (%s)", g_probe_msg);
+        else
+            set_error("no usable HIP device");
+        return false;
+    }
+    return true;
+}
+
+bool is_device_ptr(const void *p) {
+    if (!p) return false;
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();   // unregistered host memory reports an error
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
+}
+
+void *Staging::reserve(size_t bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        set_error("staging: no current HIP device");
+        return nullptr;
+    }
+    if (g_stage_size[dev] >= bytes && g_stage_ptr[dev]) return g_stage_ptr[dev];
+    if (g_stage_ptr[dev]) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(g_stage_ptr[dev]);
+        g_stage_ptr[dev] = nullptr;
+        g_stage_size[dev] = 0;
+    }
+    size_t want = align_up(bytes, size_t(1) << 20);
+    void *p = nullptr;
+    if (hipMalloc(&p, want) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error("staging: hipMalloc(%zu) failed", want);
+        return nullptr;
+    }
+    g_stage_ptr[dev] = p;
+    g_stage_size[dev] = want;
+    return p;
+}
+
+void Staging::lock() { g_stage_mu.lock(); }
+void Staging::unlock() { g_stage_mu.unlock(); }
+
+}  // namespace km

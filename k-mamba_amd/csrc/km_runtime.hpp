@@ -1,0 +1,68 @@
+// km_runtime.hpp - internal runtime helpers of libkmamba (not installed).
+//
+// Thread-local error reporting, HIP error checks that return -1 instead of
+// exiting (the reference's OM_CHECK exits the process, include/scan.h:18-26),
+// host/device pointer classification, and the per-device staging workspace
+// used by the host-pointer entry points.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+
+namespace km {
+
+void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+// True when the library may use the GPU: KMAMBA_BACKEND is not "cpu" and a
+// HIP device is present. Sets an error message otherwise.
+bool gpu_ready();
+
+// True when p is device or managed memory that kernels may dereference.
+bool is_device_ptr(const void *p);
+
+// Per-device staging arena for the host-pointer API. reserve() grows it (the
+// only allocation on these paths) and returns a base pointer; the caller
+// carves sub-buffers with carve(). Not reentrant across threads for the same
+// device: a mutex serialises host-pointer calls.
+struct Staging {
+    static void *reserve(size_t bytes);      // nullptr on failure (error set)
+    static void lock();
+    static void unlock();
+};
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Bump allocator over a reserved staging block.
+struct Carver {
+    char *base;
+    size_t off = 0;
+    explicit Carver(void *b) : base(static_cast<char *>(b)) {}
+    template <typename T> T *take(size_t count) {
+        T *p = reinterpret_cast<T *>(base + off);
+        off = align_up(off + count * sizeof(T), 256);
+        return p;
+    }
+};
+
+// Host <-> device helpers for the staging path: copy when the pointer is host
+// memory, pass through when it is already device memory.
+struct Staged {
+    const void *host;   // caller pointer
+    void *dev;          // device pointer used by kernels
+    size_t bytes;
+    bool copied;
+};
+
+}  // namespace km
+
+#define KM_HIP_TRY(call)                                                        \
+    do {                                                                        \
+        hipError_t _e = (call);                                                 \
+        if (_e != hipSuccess) {                                                 \
+            ::km::set_error("%s:%d: %s failed: %s", __FILE__, __LINE__, #call,  \
+                            hipGetErrorString(_e));                             \
+            return -1;                                                          \
+        }                                                                       \
+    } while (0)

@@ -1,0 +1,198 @@
+"""Python mirror of libkmamba's C ABI (ctypes), used by the tests and bench.
+
+The library is the product: hand-written HIP kernels for gfx950 behind the
+reference k-mamba C API (include/*.h). This module only loads
+lib/libkmamba.so, declares the C structures with the reference layouts and
+offers thin helpers that pass torch device buffers to the C entry points.
+Importing it fails loudly when the shared library has not been built: there is
+no Python or CPU fallback for any kernel.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+PKG_ROOT = Path(__file__).resolve().parent.parent          # k-mamba_amd/
+LIB_PATH = PKG_ROOT / "lib" / "libkmamba.so"
+INCLUDE_DIR = PKG_ROOT.parent / "include"
+
+if not LIB_PATH.exists():
+    raise ImportError(
+        f"{LIB_PATH} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()' "
+        "or make -C k-mamba_amd)")
+
+# Load torch's HIP runtime first when torch is present, so the process holds
+# a single libamdhip64 shared by torch allocations and libkmamba kernels.
+try:
+    import torch  # noqa: F401
+except ImportError:  # C-only use of the mirror (host-side functions)
+    torch = None
+
+lib = C.CDLL(str(LIB_PATH))
+
+c_long_p = C.POINTER(C.c_long)
+c_float_p = C.POINTER(C.c_float)
+
+KM_F32 = 0
+KM_BF16 = 1
+
+KMAMBA_BACKEND_AUTO, KMAMBA_BACKEND_CPU, KMAMBA_BACKEND_GPU = 0, 1, 2
+CONVND_FORWARD, CONVND_BACKWARD, CONVND_COMPLETE = 1, 2, 3
+
+
+class ScanParams(C.Structure):            # include/scan.h (ref include/scan.h:45-56)
+    _fields_ = [(n, C.c_void_p) for n in ("x", "A", "B", "C", "delta", "h", "y")] + \
+               [(n, C.c_long) for n in ("L", "D", "M")]
+
+
+class ScanBackwardParams(C.Structure):    # ref include/scan.h:61-78
+    _fields_ = [(n, C.c_void_p) for n in ("x", "A", "B", "C", "delta", "h0", "h", "dy",
+                                          "dx", "dA", "dB", "dC", "ddelta")] + \
+               [(n, C.c_long) for n in ("L", "D", "M")]
+
+
+class ScanBackwardSharedParams(C.Structure):   # ref include/scan.h:83-100
+    _fields_ = [(n, C.c_void_p) for n in ("x", "A", "A_diag", "B", "C", "delta", "h0", "h", "dy",
+                                          "dx", "dA", "dB", "dC", "ddelta")] + \
+               [(n, C.c_long) for n in ("L", "D")]
+
+
+class Scan2DParams(C.Structure):          # ref include/scan.h:117-131
+    _fields_ = [(n, C.c_void_p) for n in ("x", "A1", "A2", "B", "C", "delta1", "delta2", "h", "y")] + \
+               [(n, C.c_long) for n in ("d1", "d2", "D", "M")]
+
+
+class ScanNDParams(C.Structure):          # ref include/scan_nd.h:40-55
+    _fields_ = [("dims", c_long_p), ("ndims", C.c_long), ("D", C.c_long), ("M", C.c_long)] + \
+               [(n, C.c_void_p) for n in ("x", "A", "B", "C", "delta", "h", "y", "theta", "lambda_")]
+
+
+class ConvNDParams(C.Structure):          # ref include/convnd.h:10-23
+    _fields_ = [(n, C.c_void_p) for n in ("input", "kernel", "bias", "output", "dy", "dinput",
+                                          "dkernel", "dbias")] + \
+               [("dims", c_long_p), ("ndims", C.c_long), ("D", C.c_long), ("K", C.c_long)]
+
+
+class KMWavefrontPlan(C.Structure):       # ref include/wavefront_plan.h:27-35
+    _fields_ = [("dims", c_long_p), ("ndims", C.c_long), ("total_points", C.c_long),
+                ("max_level", C.c_long), ("max_level_size", C.c_long),
+                ("level_starts", c_long_p), ("level_offsets", c_long_p)]
+
+
+class KMScan1DFwd(C.Structure):           # include/kmamba_km.h
+    _fields_ = [(n, C.c_void_p) for n in ("x", "delta", "A", "Bm", "Cm", "y", "h0",
+                                          "h_final", "h_hist")] + \
+               [(n, C.c_long) for n in ("B", "L", "D", "N", "bc_sb", "bc_st", "bc_sd")] + \
+               [("dtype", C.c_int), ("clamp", C.c_int)]
+
+
+VisitFn = C.CFUNCTYPE(C.c_int, c_long_p, C.c_long, C.c_long, C.c_long, C.c_void_p)
+
+
+def _decl(name, restype, argtypes):
+    fn = getattr(lib, name)
+    fn.restype = restype
+    fn.argtypes = argtypes
+    return fn
+
+
+# --- host-side topology / plan (run on the CPU, no GPU needed) -------------
+wavefront_nd_validate_dims = _decl("wavefront_nd_validate_dims", C.c_int, [c_long_p, C.c_long])
+wavefront_nd_total_points = _decl("wavefront_nd_total_points", C.c_long, [c_long_p, C.c_long])
+wavefront_nd_max_level = _decl("wavefront_nd_max_level", C.c_long, [c_long_p, C.c_long])
+wavefront_nd_row_major_offset = _decl("wavefront_nd_row_major_offset", C.c_long,
+                                      [c_long_p, c_long_p, C.c_long])
+wavefront_nd_level_size = _decl("wavefront_nd_level_size", C.c_long, [c_long_p, C.c_long, C.c_long])
+wavefront_nd_for_level = _decl("wavefront_nd_for_level", C.c_int,
+                               [c_long_p, C.c_long, C.c_long, c_long_p, VisitFn, C.c_void_p])
+wavefront_nd_for_each_level = _decl("wavefront_nd_for_each_level", C.c_int,
+                                    [c_long_p, C.c_long, c_long_p, VisitFn, C.c_void_p])
+km_wavefront_plan_create = _decl("km_wavefront_plan_create", C.POINTER(KMWavefrontPlan),
+                                 [c_long_p, C.c_long])
+km_wavefront_plan_free = _decl("km_wavefront_plan_free", None, [C.POINTER(KMWavefrontPlan)])
+km_wavefront_plan_matches_dims = _decl("km_wavefront_plan_matches_dims", C.c_int,
+                                       [C.POINTER(KMWavefrontPlan), c_long_p, C.c_long])
+km_wavefront_plan_level_size = _decl("km_wavefront_plan_level_size", C.c_long,
+                                     [C.POINTER(KMWavefrontPlan), C.c_long])
+km_wavefront_plan_level_offsets = _decl("km_wavefront_plan_level_offsets", c_long_p,
+                                        [C.POINTER(KMWavefrontPlan), C.c_long])
+km_spatial_dims_product = _decl("km_spatial_dims_product", C.c_int,
+                                [c_long_p, C.c_long, C.POINTER(C.c_size_t)])
+km_make_row_major_strides = _decl("km_make_row_major_strides", C.c_int, [c_long_p, C.c_long, c_long_p])
+km_unravel_index = _decl("km_unravel_index", None, [C.c_long, c_long_p, c_long_p, C.c_long, c_long_p])
+km_ravel_index = _decl("km_ravel_index", C.c_long, [c_long_p, c_long_p, c_long_p, C.c_long])
+km_power_long = _decl("km_power_long", C.c_long, [C.c_long, C.c_long])
+km_normalize_spatial_topology = _decl("km_normalize_spatial_topology", C.c_int,
+                                      [c_long_p, c_long_p, C.c_size_t, C.c_int, c_long_p, C.c_long])
+
+# --- backend / errors --------------------------------------------------------
+kmamba_cuda_available = _decl("kmamba_cuda_available", C.c_int, [])
+kmamba_cuda_device_count = _decl("kmamba_cuda_device_count", C.c_int, [])
+kmamba_cuda_current_device = _decl("kmamba_cuda_current_device", C.c_int, [])
+kmamba_backend_init = _decl("kmamba_backend_init", None, [])
+kmamba_backend_select = _decl("kmamba_backend_select", C.c_int, [])
+km_last_error_c = _decl("km_last_error", C.c_char_p, [])
+km_clear_error = _decl("km_clear_error", None, [])
+km_version = _decl("km_version", C.c_char_p, [])
+
+# --- scans -------------------------------------------------------------------
+scan1d = _decl("scan1d", None, [C.POINTER(ScanParams)])
+mamba_scan1d_forward = _decl("mamba_scan1d_forward", None, [C.POINTER(ScanParams)])
+om_scan1d_forward = _decl("om_scan1d_forward", None,
+                          [C.c_void_p] * 7 + [C.c_int] * 3)
+mamba_scan1d_cuda_forward = _decl("mamba_scan1d_cuda_forward", None,
+                                  [C.c_void_p] * 7 + [C.c_int] * 3)
+km_scan1d_fwd_c = _decl("km_scan1d_fwd", C.c_int, [C.POINTER(KMScan1DFwd), C.c_void_p])
+
+
+def km_last_error() -> str:
+    return km_last_error_c().decode()
+
+
+def longs(values):
+    arr = (C.c_long * len(values))(*values)
+    return arr
+
+
+def ptr(t):
+    """Device (or host numpy) buffer address for the C ABI; None -> NULL."""
+    if t is None:
+        return None
+    if hasattr(t, "data_ptr"):
+        return t.data_ptr()
+    if hasattr(t, "ctypes"):
+        return t.ctypes.data
+    raise TypeError(type(t))
+
+
+def check(rc: int, what: str):
+    if rc != 0:
+        raise RuntimeError(f"{what} failed: {km_last_error()}")
+
+
+def stream_handle(stream=None):
+    """hipStream_t of a torch stream (current stream when None)."""
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def scan1d_fwd(x, delta, A, Bm, Cm, y, *, h0=None, h_final=None, h_hist=None,
+               bc_strides=None, clamp=True, stream=None):
+    """km_scan1d_fwd on torch device tensors.
+
+    x, delta, y: [B, L, D]; A: [D, N] fp32; Bm/Cm: [B, L, N] shared over
+    channels (default strides) or any layout described by bc_strides =
+    (sb, st, sd) in elements with N contiguous.
+    """
+    import torch
+    Bsz, L, D = x.shape
+    N = A.shape[1]
+    if bc_strides is None:
+        assert Bm.shape == (Bsz, L, N) and Bm.is_contiguous()
+        bc_strides = (L * N, N, 0)
+    dt = KM_BF16 if x.dtype == torch.bfloat16 else KM_F32
+    args = KMScan1DFwd(ptr(x), ptr(delta), ptr(A), ptr(Bm), ptr(Cm), ptr(y), ptr(h0),
+                       ptr(h_final), ptr(h_hist), Bsz, L, D, N, *bc_strides, dt, int(clamp))
+    check(km_scan1d_fwd_c(C.byref(args), C.c_void_p(stream_handle(stream))), "km_scan1d_fwd")

@@ -1,0 +1,111 @@
+/* kmoracle.h - CPU restatement of the reference k-mamba hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP
+ * kernels of libkmamba: only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load it. The product never links it and
+ * has no CPU fallback to it.
+ *
+ * Each function restates one reference function in the same arithmetic order
+ * (fp32, no FMA contraction, glibc expf), citing the reference file:line it
+ * follows. Struct layouts mirror the reference headers (8-byte pointers and
+ * longs) so the same ctypes structures drive the oracle and the library.
+ */
+#ifndef KMORACLE_H
+#define KMORACLE_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct {
+    float *x, *A, *B, *C, *delta, *h, *y;
+    long L, D, M;
+} OrcScanParams;                         /* ref include/scan.h:45-56 */
+
+typedef struct {
+    float *x, *A, *B, *C, *delta, *h0, *h, *dy, *dx, *dA, *dB, *dC, *ddelta;
+    long L, D, M;
+} OrcScanBackwardParams;                 /* ref include/scan.h:61-78 */
+
+typedef struct {
+    float *x, *A, *A_diag, *B, *C, *delta, *h0, *h, *dy, *dx, *dA, *dB, *dC, *ddelta;
+    long L, D;
+} OrcScanBackwardSharedParams;           /* ref include/scan.h:83-100 */
+
+typedef struct {
+    float *x, *A1, *A2, *B, *C, *delta1, *delta2, *h, *y;
+    long d1, d2, D, M;
+} OrcScan2DParams;                       /* ref include/scan.h:117-131 */
+
+typedef struct {
+    const long *dims;
+    long ndims, D, M;
+    const float *x, *A, *B, *C, *delta;
+    float *h, *y;
+    const float *theta, *lambda;
+} OrcScanNDParams;                       /* ref include/scan_nd.h:40-55 */
+
+typedef struct {
+    float *input;
+    const float *kernel, *bias;
+    float *output, *dy, *dinput, *dkernel, *dbias;
+    const long *dims;
+    long ndims, D, K;
+} OrcConvNDParams;                       /* ref include/convnd.h:10-23 */
+
+typedef struct {
+    long *dims;
+    long ndims, total_points, max_level, max_level_size;
+    long *level_starts, *level_offsets;
+} OrcPlan;                               /* ref include/wavefront_plan.h:27-35 */
+
+/* ---- Scan1D ---------------------------------------------------------- */
+void orc_scan1d(OrcScanParams *p);
+void orc_scan1d_batched(const float *x, const float *delta, const float *A,
+                        const float *Bm, const float *Cm, float *y,
+                        float *h, float *h_hist,
+                        long B, long L, long D, long N,
+                        long bc_sb, long bc_st, long bc_sd,
+                        int clamp, int nthreads);
+void orc_scan1d_backward(OrcScanBackwardParams *p);
+void orc_scan1d_backward_m1_shared_bc(OrcScanBackwardSharedParams *p);
+void orc_scan1d_batched_backward(const float *x, const float *delta, const float *A,
+                                 const float *Bm, const float *Cm, const float *dy,
+                                 const float *h0, const float *h_hist,
+                                 float *dx, float *ddelta, float *dA,
+                                 float *dB, float *dC,
+                                 long B, long L, long D, long N,
+                                 long bc_sb, long bc_st, long bc_sd, int nthreads);
+
+/* ---- Scan2D / ScanND -------------------------------------------------- */
+void orc_scan2d(OrcScan2DParams *p);
+int  orc_scannd_validate(const OrcScanNDParams *p);
+int  orc_scannd_ref_with_plan(OrcScanNDParams *p, const OrcPlan *plan, int nthreads);
+int  orc_scannd_ref(OrcScanNDParams *p, int nthreads);
+int  orc_scannd(OrcScanNDParams *p, int nthreads);
+
+/* ---- ConvND ----------------------------------------------------------- */
+long orc_convnd_kernel_volume(long ndims, long K);
+void orc_convnd_forward(OrcConvNDParams *p, int nthreads);
+void orc_convnd_backward(OrcConvNDParams *p);
+
+/* ---- Wavefront / plan / topology -------------------------------------- */
+int  orc_wavefront_validate_dims(const long *dims, long ndims);
+long orc_wavefront_total_points(const long *dims, long ndims);
+long orc_wavefront_max_level(const long *dims, long ndims);
+long orc_wavefront_row_major_offset(const long *dims, const long *idx, long ndims);
+long orc_wavefront_level_size(const long *dims, long ndims, long level);
+OrcPlan *orc_plan_create(const long *dims, long ndims);
+void orc_plan_free(OrcPlan *plan);
+int  orc_make_row_major_strides(const long *dims, long ndims, long *strides);
+void orc_unravel_index(long linear, const long *dims, const long *strides, long ndims, long *coords);
+long orc_ravel_index(const long *coords, const long *dims, const long *strides, long ndims);
+long orc_power_long(long base, long exp);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

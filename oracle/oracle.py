@@ -1,0 +1,335 @@
+"""ctypes binding of the CPU oracle (test infrastructure only).
+
+Loads oracle/liboracle.so (the C restatement of the reference CPU path,
+kmoracle.c) and, when it was built in this container from /root/reference,
+oracle/_ref/libkmref.so (the reference's own C compiled in place). Only the
+tests, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
+module; the product never does.
+
+All wrappers take and return numpy float32 / int64 arrays.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_SO = HERE / "liboracle.so"
+ORACLE_FAST_SO = HERE / "liboracle_fast.so"
+REF_SO = HERE / "_ref" / "libkmref.so"
+
+if not ORACLE_SO.exists():
+    raise ImportError(f"{ORACLE_SO} missing: run make -C oracle")
+
+orc = C.CDLL(str(ORACLE_SO))
+orc_fast = C.CDLL(str(ORACLE_FAST_SO)) if ORACLE_FAST_SO.exists() else orc
+ref = C.CDLL(str(REF_SO)) if REF_SO.exists() else None
+
+vp = C.c_void_p
+lp = C.POINTER(C.c_long)
+
+
+def P(a):
+    """Address of a numpy array (None -> NULL)."""
+    return None if a is None else a.ctypes.data_as(vp)
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def longs(vals):
+    return (C.c_long * len(vals))(*[int(v) for v in vals])
+
+
+class ScanParams(C.Structure):
+    _fields_ = [(n, vp) for n in ("x", "A", "B", "C", "delta", "h", "y")] + \
+               [(n, C.c_long) for n in ("L", "D", "M")]
+
+
+class ScanBackwardParams(C.Structure):
+    _fields_ = [(n, vp) for n in ("x", "A", "B", "C", "delta", "h0", "h", "dy",
+                                  "dx", "dA", "dB", "dC", "ddelta")] + \
+               [(n, C.c_long) for n in ("L", "D", "M")]
+
+
+class ScanBackwardSharedParams(C.Structure):
+    _fields_ = [(n, vp) for n in ("x", "A", "A_diag", "B", "C", "delta", "h0", "h", "dy",
+                                  "dx", "dA", "dB", "dC", "ddelta")] + \
+               [(n, C.c_long) for n in ("L", "D")]
+
+
+class Scan2DParams(C.Structure):
+    _fields_ = [(n, vp) for n in ("x", "A1", "A2", "B", "C", "delta1", "delta2", "h", "y")] + \
+               [(n, C.c_long) for n in ("d1", "d2", "D", "M")]
+
+
+class ScanNDParams(C.Structure):
+    _fields_ = [("dims", lp), ("ndims", C.c_long), ("D", C.c_long), ("M", C.c_long)] + \
+               [(n, vp) for n in ("x", "A", "B", "C", "delta", "h", "y", "theta", "lambda_")]
+
+
+class ConvNDParams(C.Structure):
+    _fields_ = [(n, vp) for n in ("input", "kernel", "bias", "output", "dy", "dinput",
+                                  "dkernel", "dbias")] + \
+               [("dims", lp), ("ndims", C.c_long), ("D", C.c_long), ("K", C.c_long)]
+
+
+class Plan(C.Structure):
+    _fields_ = [("dims", lp), ("ndims", C.c_long), ("total_points", C.c_long),
+                ("max_level", C.c_long), ("max_level_size", C.c_long),
+                ("level_starts", lp), ("level_offsets", lp)]
+
+
+def _sig(lib, name, restype, argtypes):
+    if lib is None:
+        return None
+    fn = getattr(lib, name)
+    fn.restype = restype
+    fn.argtypes = argtypes
+    return fn
+
+
+for _lib in {orc, orc_fast}:
+    _sig(_lib, "orc_scan1d", None, [C.POINTER(ScanParams)])
+    _sig(_lib, "orc_scan1d_batched", None, [vp] * 8 + [C.c_long] * 7 + [C.c_int, C.c_int])
+    _sig(_lib, "orc_scan1d_backward", None, [C.POINTER(ScanBackwardParams)])
+    _sig(_lib, "orc_scan1d_backward_m1_shared_bc", None, [C.POINTER(ScanBackwardSharedParams)])
+    _sig(_lib, "orc_scan1d_batched_backward", None, [vp] * 13 + [C.c_long] * 7 + [C.c_int])
+    _sig(_lib, "orc_scan2d", None, [C.POINTER(Scan2DParams)])
+    _sig(_lib, "orc_scannd_ref", C.c_int, [C.POINTER(ScanNDParams), C.c_int])
+    _sig(_lib, "orc_scannd", C.c_int, [C.POINTER(ScanNDParams), C.c_int])
+    _sig(_lib, "orc_convnd_forward", None, [C.POINTER(ConvNDParams), C.c_int])
+    _sig(_lib, "orc_convnd_backward", None, [C.POINTER(ConvNDParams)])
+    _sig(_lib, "orc_plan_create", C.POINTER(Plan), [lp, C.c_long])
+    _sig(_lib, "orc_plan_free", None, [C.POINTER(Plan)])
+    _sig(_lib, "orc_wavefront_level_size", C.c_long, [lp, C.c_long, C.c_long])
+    _sig(_lib, "orc_wavefront_total_points", C.c_long, [lp, C.c_long])
+    _sig(_lib, "orc_wavefront_max_level", C.c_long, [lp, C.c_long])
+    _sig(_lib, "orc_wavefront_row_major_offset", C.c_long, [lp, lp, C.c_long])
+
+if ref is not None:
+    _sig(ref, "scannd_ref", C.c_int, [C.POINTER(ScanNDParams)])
+    _sig(ref, "convnd_forward_wavefront", None, [C.POINTER(ConvNDParams), C.POINTER(Plan)])
+    _sig(ref, "convnd_backward_wavefront", None, [C.POINTER(ConvNDParams), C.POINTER(Plan)])
+    _sig(ref, "scan1d_backward", None, [C.POINTER(ScanBackwardParams)])
+    _sig(ref, "scan1d_backward_m1_shared_bc", None, [C.POINTER(ScanBackwardSharedParams)])
+    _sig(ref, "km_wavefront_plan_create", C.POINTER(Plan), [lp, C.c_long])
+    _sig(ref, "km_wavefront_plan_free", None, [C.POINTER(Plan)])
+    _sig(ref, "wavefront_nd_level_size", C.c_long, [lp, C.c_long, C.c_long])
+    _sig(ref, "kmr_test_scan1d_ref", None, [vp] * 7 + [C.c_long] * 3)
+    _sig(ref, "kmr_test_scan1d_backward_forward_ref", None, [vp] * 7 + [C.c_long] * 3)
+
+
+# ---------------------------------------------------------------------------
+# Scan1D
+# ---------------------------------------------------------------------------
+def scan1d(x, A, B, Cm, delta, h):
+    """Reference scan1d (asm semantics): x, delta [L, D]; A [D, M];
+    B, C [L, D, M]; h [D, M] running state. Returns (y, h_final)."""
+    x, A, B, Cm, delta = map(f32, (x, A, B, Cm, delta))
+    h = f32(h).copy()
+    L, D = x.shape
+    M = A.shape[1]
+    y = np.zeros((L, D), np.float32)
+    p = ScanParams(P(x), P(A), P(B), P(Cm), P(delta), P(h), P(y), L, D, M)
+    orc.orc_scan1d(C.byref(p))
+    return y, h
+
+
+def scan1d_batched(x, delta, A, Bm, Cm, *, h0=None, bc_strides=None, clamp=True,
+                   hist=False, nthreads=1, fast=False):
+    """Batched scan: x, delta [B, L, D]; A [D, N]; B/C shared [B, L, N] by
+    default, or any buffer with strides bc_strides=(sb, st, sd).
+    Returns (y, h_final, h_hist or None)."""
+    x, delta, A, Bm, Cm = map(f32, (x, delta, A, Bm, Cm))
+    Bsz, L, D = x.shape
+    N = A.shape[1]
+    if bc_strides is None:
+        bc_strides = (L * N, N, 0)
+    h = np.zeros((Bsz, D, N), np.float32) if h0 is None else f32(h0).copy()
+    y = np.zeros((Bsz, L, D), np.float32)
+    hh = np.zeros((Bsz, L, D, N), np.float32) if hist else None
+    lib = orc_fast if fast else orc
+    lib.orc_scan1d_batched(P(x), P(delta), P(A), P(Bm), P(Cm), P(y), P(h), P(hh),
+                           Bsz, L, D, N, *bc_strides, int(clamp), int(nthreads))
+    return y, h, hh
+
+
+def scan1d_backward(x, A, B, Cm, delta, h, dy, h0=None, lib=None):
+    """Generic backward (cpu/scan1d_backward.c:297-306). Returns
+    (dx, dA, dB, dC, ddelta)."""
+    lib = lib or orc
+    x, A, B, Cm, delta, h, dy = map(f32, (x, A, B, Cm, delta, h, dy))
+    L, D = x.shape
+    M = A.shape[1]
+    out = dict(dx=np.zeros((L, D), np.float32), dA=np.zeros((D, M), np.float32),
+               dB=np.zeros((L, D, M), np.float32), dC=np.zeros((L, D, M), np.float32),
+               ddelta=np.zeros((L, D), np.float32))
+    h0 = None if h0 is None else f32(h0)
+    p = ScanBackwardParams(P(x), P(A), P(B), P(Cm), P(delta), P(h0), P(h), P(dy),
+                           P(out["dx"]), P(out["dA"]), P(out["dB"]), P(out["dC"]),
+                           P(out["ddelta"]), L, D, M)
+    if lib is orc:
+        orc.orc_scan1d_backward(C.byref(p))
+    else:
+        lib.scan1d_backward(C.byref(p))
+    return out["dx"], out["dA"], out["dB"], out["dC"], out["ddelta"]
+
+
+def scan1d_backward_m1_shared_bc(x, A, B, Cm, delta, h, dy, A_diag=None, h0=None, lib=None):
+    lib = lib or orc
+    x, A, B, Cm, delta, h, dy = map(f32, (x, A, B, Cm, delta, h, dy))
+    L, D = x.shape
+    A_diag = None if A_diag is None else f32(A_diag)
+    h0 = None if h0 is None else f32(h0)
+    out = dict(dx=np.zeros((L, D), np.float32), dA=np.zeros(D, np.float32),
+               dB=np.zeros(D, np.float32), dC=np.zeros(D, np.float32),
+               ddelta=np.zeros(L, np.float32))
+    p = ScanBackwardSharedParams(P(x), P(A), P(A_diag), P(B), P(Cm), P(delta), P(h0), P(h),
+                                 P(dy), P(out["dx"]), P(out["dA"]), P(out["dB"]), P(out["dC"]),
+                                 P(out["ddelta"]), L, D)
+    if lib is orc:
+        orc.orc_scan1d_backward_m1_shared_bc(C.byref(p))
+    else:
+        lib.scan1d_backward_m1_shared_bc(C.byref(p))
+    return out["dx"], out["dA"], out["dB"], out["dC"], out["ddelta"]
+
+
+def scan1d_batched_backward(x, delta, A, Bm, Cm, dy, h_hist, *, h0=None, bc_strides=None,
+                            nthreads=1, fast=False):
+    """Adjoint of scan1d_batched (no clamp). Returns dx, ddelta [B, L, D],
+    dA [D, N], dB, dC (shape of Bm: [B, L, N] when shared)."""
+    x, delta, A, Bm, Cm, dy, h_hist = map(f32, (x, delta, A, Bm, Cm, dy, h_hist))
+    Bsz, L, D = x.shape
+    N = A.shape[1]
+    if bc_strides is None:
+        bc_strides = (L * N, N, 0)
+    dx = np.zeros_like(x)
+    ddt = np.zeros_like(x)
+    dA = np.zeros((D, N), np.float32)
+    dB = np.zeros_like(Bm)
+    dC = np.zeros_like(Cm)
+    h0 = None if h0 is None else f32(h0)
+    lib = orc_fast if fast else orc
+    lib.orc_scan1d_batched_backward(P(x), P(delta), P(A), P(Bm), P(Cm), P(dy), P(h0), P(h_hist),
+                                    P(dx), P(ddt), P(dA), P(dB), P(dC),
+                                    Bsz, L, D, N, *bc_strides, int(nthreads))
+    return dx, ddt, dA, dB, dC
+
+
+# ---------------------------------------------------------------------------
+# Scan2D / ScanND
+# ---------------------------------------------------------------------------
+def scan2d(x, A1, A2, B, Cm, delta1, delta2, d1, d2):
+    x, A1, A2, B, Cm, delta1, delta2 = map(f32, (x, A1, A2, B, Cm, delta1, delta2))
+    D, M = A1.shape
+    h = np.zeros((d1 * d2, D, M), np.float32)
+    y = np.zeros((d1 * d2, D), np.float32)
+    p = Scan2DParams(P(x), P(A1), P(A2), P(B), P(Cm), P(delta1), P(delta2), P(h), P(y),
+                     d1, d2, D, M)
+    orc.orc_scan2d(C.byref(p))
+    return y, h
+
+
+def _nd_params(dims, x, A, B, Cm, delta, h, y):
+    dd = longs(dims)
+    D, M = A.shape[1], A.shape[2]
+    p = ScanNDParams(dd, len(dims), D, M, P(x), P(A), P(B), P(Cm), P(delta), P(h), P(y),
+                     None, None)
+    return p, dd
+
+
+def scannd_ref(dims, x, A, B, Cm, delta, *, nthreads=1, use_ref=False, fast=False):
+    """scannd_ref semantics: x [P, D]; A [nd, D, M]; B, C [P, D, M];
+    delta [nd, P, D]. Returns (y, h)."""
+    x, A, B, Cm, delta = map(f32, (x, A, B, Cm, delta))
+    Pn = int(np.prod(dims))
+    D, M = A.shape[1], A.shape[2]
+    h = np.zeros((Pn, D, M), np.float32)
+    y = np.zeros((Pn, D), np.float32)
+    p, _keep = _nd_params(dims, x, A, B, Cm, delta, h, y)
+    if use_ref:
+        rc = ref.scannd_ref(C.byref(p))
+    else:
+        rc = (orc_fast if fast else orc).orc_scannd_ref(C.byref(p), int(nthreads))
+    if rc != 0:
+        raise RuntimeError("scannd_ref failed")
+    return y, h
+
+
+def scannd(dims, x, A, B, Cm, delta, h=None, *, nthreads=1):
+    """CPU dispatch semantics of scannd (1D -> scan1d, 2D -> scan2d)."""
+    x, A, B, Cm, delta = map(f32, (x, A, B, Cm, delta))
+    Pn = int(np.prod(dims))
+    D, M = A.shape[1], A.shape[2]
+    if h is None:
+        h = np.zeros((Pn, D, M), np.float32)
+    h = f32(h).copy()
+    y = np.zeros((Pn, D), np.float32)
+    p, _keep = _nd_params(dims, x, A, B, Cm, delta, h, y)
+    if orc.orc_scannd(C.byref(p), int(nthreads)) != 0:
+        raise RuntimeError("scannd failed")
+    return y, h
+
+
+# ---------------------------------------------------------------------------
+# ConvND
+# ---------------------------------------------------------------------------
+def convnd_forward(dims, inp, kernel, bias, *, nthreads=1, use_ref=False, fast=False):
+    inp, kernel = f32(inp), f32(kernel)
+    bias = None if bias is None else f32(bias)
+    D = inp.shape[1]
+    K = int(round(kernel.shape[0] ** (1.0 / len(dims))))
+    out = np.zeros_like(inp)
+    dd = longs(dims)
+    p = ConvNDParams(P(inp), P(kernel), P(bias), P(out), None, None, None, None,
+                     dd, len(dims), D, K)
+    if use_ref:
+        plan = ref.km_wavefront_plan_create(dd, len(dims))
+        ref.convnd_forward_wavefront(C.byref(p), plan)
+        ref.km_wavefront_plan_free(plan)
+    else:
+        (orc_fast if fast else orc).orc_convnd_forward(C.byref(p), int(nthreads))
+    return out
+
+
+def convnd_backward(dims, inp, kernel, dy, *, with_bias=True, use_ref=False):
+    inp, kernel, dy = f32(inp), f32(kernel), f32(dy)
+    D = inp.shape[1]
+    K = int(round(kernel.shape[0] ** (1.0 / len(dims))))
+    dinp = np.zeros_like(inp)
+    dker = np.zeros_like(kernel)
+    dbias = np.zeros(D, np.float32) if with_bias else None
+    dd = longs(dims)
+    p = ConvNDParams(P(inp), P(kernel), None, None, P(dy), P(dinp), P(dker), P(dbias),
+                     dd, len(dims), D, K)
+    if use_ref:
+        plan = ref.km_wavefront_plan_create(dd, len(dims))
+        ref.convnd_backward_wavefront(C.byref(p), plan)
+        ref.km_wavefront_plan_free(plan)
+    else:
+        orc.orc_convnd_backward(C.byref(p))
+    return dinp, dker, dbias
+
+
+# ---------------------------------------------------------------------------
+# Wavefront plan
+# ---------------------------------------------------------------------------
+def plan_tables(dims, use_ref=False):
+    """(level_starts, level_offsets, max_level_size) as int64 arrays."""
+    dd = longs(dims)
+    lib = ref if use_ref else orc
+    create = lib.km_wavefront_plan_create if use_ref else lib.orc_plan_create
+    free = lib.km_wavefront_plan_free if use_ref else lib.orc_plan_free
+    pl = create(dd, len(dims))
+    if not pl:
+        return None
+    p = pl.contents
+    starts = np.ctypeslib.as_array(p.level_starts, shape=(p.max_level + 2,)).copy()
+    offs = np.ctypeslib.as_array(p.level_offsets, shape=(p.total_points,)).copy()
+    mls = p.max_level_size
+    free(pl)
+    return starts, offs, mls

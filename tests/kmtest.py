@@ -1,0 +1,94 @@
+"""Shared helpers for the test suite: seeded inputs of the benchmark
+configurations and the error metrics used for parity.
+
+Parity metric (pass/fail): condition-scaled relative error
+    max_i |got_i - ref_i| / max(|ref_i|, kappa_i)
+where kappa_i is the magnitude of the terms that produce element i: the same
+recurrence run on absolute values (|x|, |B|, |C|, |h0|; the decays are
+positive), so kappa_i has no cancellation. Tolerances: 1e-4 for fp32 I/O,
+2e-2 for bf16 I/O against the fp32 oracle of the unrounded inputs.
+
+Also reported: the floor metric max |got - ref| / max(|ref|, 1e-3*rms(ref)).
+It cannot be the criterion for outputs that are sums of signed terms: a
+float32 restatement of the reference with numpy's exp and summation order
+already scores 1.9e-4 on configs[0] under it (4.8e-7 condition-scaled).
+"""
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+
+TOL_F32 = 1e-4
+TOL_BF16 = 2e-2
+
+
+def rng_for(*key) -> np.random.Generator:
+    """Deterministic generator keyed by (config, tensor, seed)."""
+    h = hashlib.sha256(repr(key).encode()).digest()
+    return np.random.default_rng(int.from_bytes(h[:8], "little"))
+
+
+def softplus(v):
+    return np.log1p(np.exp(-np.abs(v))) + np.maximum(v, 0)
+
+
+def scan1d_inputs(Bsz, L, D, N, seed=0, tag="scan1d"):
+    """Inputs of the Scan1D configurations: x ~ N(0,1) [B,L,D];
+    delta = softplus(0.5*N(0,1) - 1) [B,L,D]; A[d,n] = -(n+1) [D,N];
+    B, C ~ N(0, 1/N) [B,L,N] (second argument read as variance)."""
+    g = rng_for(tag, Bsz, L, D, N, seed)
+    x = g.standard_normal((Bsz, L, D), dtype=np.float32)
+    dt = softplus(0.5 * g.standard_normal((Bsz, L, D), dtype=np.float32) - 1.0).astype(np.float32)
+    A = -np.tile(np.arange(1, N + 1, dtype=np.float32), (D, 1))
+    sd = np.float32(1.0 / np.sqrt(N))
+    Bm = (g.standard_normal((Bsz, L, N), dtype=np.float32) * sd).astype(np.float32)
+    Cm = (g.standard_normal((Bsz, L, N), dtype=np.float32) * sd).astype(np.float32)
+    return x, dt, A, Bm, Cm
+
+
+def rel_err(got, ref) -> float:
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    if ref.size == 0:
+        return 0.0
+    rms = float(np.sqrt(np.mean(ref * ref)))
+    floor = max(1e-3 * rms, 1e-30)
+    return float(np.max(np.abs(got - ref) / np.maximum(np.abs(ref), floor)))
+
+
+def rel_err_cond(got, ref, kappa) -> float:
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    if ref.size == 0:
+        return 0.0
+    den = np.maximum(np.abs(ref), np.asarray(kappa, dtype=np.float64))
+    den = np.maximum(den, 1e-30)
+    return float(np.max(np.abs(got - ref) / den))
+
+
+def assert_close(got, ref, tol, what="", kappa=None):
+    """Condition-scaled parity when kappa is given, else plain relative
+    error with the 1e-3*rms floor (for outputs without cancellation)."""
+    floor = rel_err(got, ref)
+    e = floor if kappa is None else rel_err_cond(got, ref, kappa)
+    assert e <= tol, f"{what}: max relative error {e:.3e} > {tol:.1e} (floor metric {floor:.2e})"
+    return e
+
+
+def scan1d_kappa(x, dt, A, Bm, Cm, *, h0=None, bc_strides=None):
+    """Cancellation-free magnitudes (kappa_y, kappa_h, kappa_hist) of a
+    Scan1D forward: the oracle on |x|, |B|, |C|, |h0| without clamp."""
+    import oracle as O
+    y, h, hh = O.scan1d_batched(np.abs(x), dt, A, np.abs(Bm), np.abs(Cm),
+                                h0=None if h0 is None else np.abs(h0), bc_strides=bc_strides,
+                                clamp=False, hist=True, nthreads=8, fast=True)
+    return y, h, hh
+
+
+def bf16_round(a):
+    """fp32 -> bf16 -> fp32 with round-to-nearest-even (numpy)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32)

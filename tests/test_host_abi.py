@@ -1,0 +1,261 @@
+"""CPU tests of libkmamba's host side: C-ABI exports, the wavefront plan /
+enumeration / topology code (bit-exact against the compiled reference and the
+oracle), and the behaviour of the compute entry points when no GPU is usable.
+"""
+import ctypes as C
+import os
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import kmamba as K
+import oracle as O
+
+ROOT = Path(__file__).resolve().parent.parent
+needs_ref = pytest.mark.skipif(O.ref is None, reason="oracle/_ref not built (reference tree absent)")
+
+
+def header_functions():
+    """Names of every function (and extern object) declared in include/*.h."""
+    names = set()
+    for h in sorted((ROOT / "include").glob("*.h")):
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        text = re.sub(r"^\s*#.*?(?<!\\)$", "", text, flags=re.M | re.S)
+        text = re.sub(r"typedef\s+(struct|enum)\s*\{.*?\}\s*\w+\s*;", "", text, flags=re.S)
+        text = re.sub(r"typedef[^;]*;", "", text)
+        text = text.replace('extern "C" {', "").replace("}", " ")
+        for stmt in text.split(";"):
+            stmt = " ".join(stmt.split())
+            if not stmt or "{" in stmt:
+                continue
+            m = re.match(r"^(?:extern\s+)?[\w\s\*]*?\b(\w+)\s*\(", stmt)
+            if m:
+                names.add(m.group(1))
+            elif stmt.startswith("extern "):
+                names.add(stmt.split()[-1].strip("*"))
+    return sorted(names)
+
+
+def test_headers_parse():
+    names = header_functions()
+    for must in ("scan1d", "om_scan1d_forward", "scannd", "km_wavefront_plan_create",
+                 "convnd", "kmamba_backend_preference", "km_scan1d_fwd"):
+        assert must in names, must
+
+
+@pytest.mark.xfail(reason="entry points still being implemented: the test lists the missing ones",
+                   strict=False)
+def test_library_exports_every_declared_symbol():
+    out = subprocess.run(["nm", "-D", "--defined-only", str(K.LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = [n for n in header_functions() if n not in exported]
+    assert not missing, f"declared in include/*.h but not exported: {missing}"
+
+
+# ---------------------------------------------------------------------------
+# Plan / wavefront / topology
+# ---------------------------------------------------------------------------
+def product_plan(dims):
+    dd = K.longs(dims)
+    pl = K.km_wavefront_plan_create(dd, len(dims))
+    if not pl:
+        return None
+    p = pl.contents
+    starts = np.ctypeslib.as_array(p.level_starts, shape=(p.max_level + 2,)).copy()
+    offs = np.ctypeslib.as_array(p.level_offsets, shape=(p.total_points,)).copy()
+    meta = (p.ndims, p.total_points, p.max_level, p.max_level_size,
+            list(np.ctypeslib.as_array(p.dims, shape=(p.ndims,))))
+    assert K.km_wavefront_plan_matches_dims(pl, dd, len(dims)) == 1
+    for lvl in (0, p.max_level // 2, p.max_level):
+        size = K.km_wavefront_plan_level_size(pl, lvl)
+        assert size == starts[lvl + 1] - starts[lvl]
+        lo = K.km_wavefront_plan_level_offsets(pl, lvl)
+        if size > 0:
+            np.testing.assert_array_equal(np.ctypeslib.as_array(lo, shape=(size,)),
+                                          offs[starts[lvl]:starts[lvl + 1]])
+    assert K.km_wavefront_plan_level_size(pl, -1) == -1
+    assert K.km_wavefront_plan_level_size(pl, p.max_level + 1) == -1
+    assert not K.km_wavefront_plan_level_offsets(pl, p.max_level + 1)
+    K.km_wavefront_plan_free(pl)
+    return starts, offs, meta
+
+
+PLAN_DIMS = [(1,), (7,), (3, 4), (2, 3, 2), (4, 1, 3), (2, 2, 2, 3), (16, 16), (5, 3, 2, 2, 2),
+             (1, 1, 1), (3, 1, 4, 1, 5, 1, 2, 2)]
+
+
+@pytest.mark.parametrize("dims", PLAN_DIMS)
+def test_plan_matches_oracle(dims):
+    starts, offs, meta = product_plan(dims)
+    o_starts, o_offs, o_mls = O.plan_tables(dims)
+    np.testing.assert_array_equal(starts, o_starts)
+    np.testing.assert_array_equal(offs, o_offs)
+    assert meta[3] == o_mls and meta[1] == int(np.prod(dims))
+
+
+@needs_ref
+@pytest.mark.parametrize("dims", PLAN_DIMS + [(256, 256), (64, 64, 64), (512, 512)])
+def test_plan_bit_exact_vs_reference(dims):
+    starts, offs, meta = product_plan(dims)
+    r_starts, r_offs, r_mls = O.plan_tables(dims, use_ref=True)
+    np.testing.assert_array_equal(starts, r_starts)
+    np.testing.assert_array_equal(offs, r_offs)
+    assert meta[3] == r_mls
+
+
+def test_plan_config_shapes():
+    # Shapes of the benchmark configurations.
+    for dims, maxl, mls in (((256, 256), 510, 256), ((64, 64, 64), 189, None), ((512, 512), 1022, 512)):
+        starts, offs, meta = product_plan(dims)
+        assert meta[2] == maxl
+        if mls:
+            assert meta[3] == mls
+        assert starts[-1] == int(np.prod(dims))
+    assert not K.km_wavefront_plan_create(K.longs((3, 0)), 2)
+    assert not K.km_wavefront_plan_create(K.longs((3,)), 0)
+
+
+def _visits(lib_fn, dims, level=None):
+    seen = []
+
+    @K.VisitFn
+    def cb(idx, nd, lvl, ordinal, user):
+        seen.append((tuple(idx[i] for i in range(nd)), lvl, ordinal))
+        return 0
+
+    dd = K.longs(dims)
+    rc = lib_fn(dd, len(dims), level, None, cb, None) if level is not None else \
+        lib_fn(dd, len(dims), None, cb, None)
+    return rc, seen
+
+
+@pytest.mark.parametrize("dims", [(3, 4), (2, 3, 2), (4, 1, 3), (5,), (2, 2, 3, 2)])
+def test_for_each_level_order_and_coverage(dims):
+    rc, seen = _visits(K.wavefront_nd_for_each_level, dims)
+    assert rc == 0
+    offs = [K.wavefront_nd_row_major_offset(K.longs(dims), K.longs(i), len(dims)) for i, _, _ in seen]
+    assert sorted(offs) == list(range(int(np.prod(dims))))
+    _, o_offs, _ = O.plan_tables(dims)
+    assert offs == list(o_offs)                       # level order, ascending offsets in a level
+    for i, lvl, _ in seen:
+        assert sum(i) == lvl
+    prev = None
+    for _, lvl, ordinal in seen:                      # ordinals restart at each level
+        assert ordinal == (0 if lvl != prev else last + 1)
+        prev, last = lvl, ordinal
+
+
+@needs_ref
+@pytest.mark.parametrize("dims", [(3, 4), (2, 3, 2), (4, 1, 3), (2, 2, 3, 2), (6, 5, 4)])
+def test_for_level_visits_equal_reference(dims):
+    O.ref.wavefront_nd_for_level.restype = C.c_int
+    O.ref.wavefront_nd_for_level.argtypes = [K.c_long_p, C.c_long, C.c_long, K.c_long_p, K.VisitFn,
+                                             C.c_void_p]
+    maxl = sum(d - 1 for d in dims)
+    for lvl in range(maxl + 1):
+        a = _visits(K.wavefront_nd_for_level, dims, lvl)
+        b = _visits(O.ref.wavefront_nd_for_level, dims, lvl)
+        assert a == b
+        assert K.wavefront_nd_level_size(K.longs(dims), len(dims), lvl) == \
+            O.ref.wavefront_nd_level_size(O.longs(dims), len(dims), lvl)
+
+
+def test_for_level_early_stop_and_invalid():
+    # tests/unit/test_wavefront_nd.c:212-248.
+    count = [0]
+
+    @K.VisitFn
+    def stop_after_two(idx, nd, lvl, ordinal, user):
+        count[0] += 1
+        return 77 if count[0] >= 2 else 0
+
+    assert K.wavefront_nd_for_level(K.longs((3, 4)), 2, 3, None, stop_after_two, None) == 77
+    assert count[0] == 2
+    bad = K.longs((3, 0))
+    assert K.wavefront_nd_validate_dims(bad, 2) == 0
+    assert K.wavefront_nd_total_points(bad, 2) == -1
+    assert K.wavefront_nd_max_level(bad, 2) == -1
+    assert K.wavefront_nd_for_each_level(bad, 2, None, stop_after_two, None) == -1
+    assert K.wavefront_nd_level_size(K.longs((3, 4)), 2, 6) == -1
+    assert K.wavefront_nd_row_major_offset(K.longs((2, 3, 2)), K.longs((1, 2, 1)), 3) == 11
+    assert K.wavefront_nd_row_major_offset(K.longs((2, 3, 2)), K.longs((1, 3, 1)), 3) == -1
+    big = K.longs((1 << 40, 1 << 40))
+    assert K.wavefront_nd_total_points(big, 2) == -1          # overflow detected
+    # Inclusion-exclusion: C(1502,2) - 3*C(502,2) points of [0,999]^3 sum to 1500.
+    assert K.wavefront_nd_level_size(K.longs((1000, 1000, 1000)), 3, 1500) == \
+        1502 * 1501 // 2 - 3 * (502 * 501 // 2)
+
+
+def test_topology_helpers():
+    dims = K.longs((2, 3, 4))
+    st = (C.c_long * 3)()
+    assert K.km_make_row_major_strides(dims, 3, st) == 1 and list(st) == [12, 4, 1]
+    co = (C.c_long * 3)()
+    K.km_unravel_index(17, dims, st, 3, co)
+    assert list(co) == [1, 1, 1]
+    assert K.km_ravel_index(co, dims, st, 3) == 17
+    co[1] = 3
+    assert K.km_ravel_index(co, dims, st, 3) == -1
+    assert K.km_power_long(0, 0) == 0 and K.km_power_long(3, 4) == 81 and K.km_power_long(2, -1) == 0
+    prod = C.c_size_t()
+    assert K.km_spatial_dims_product(dims, 3, C.byref(prod)) == 1 and prod.value == 24
+    nd = C.c_long(0)
+    sd = (C.c_long * 8)()
+    cn = C.c_long(0)
+    assert K.km_normalize_spatial_topology(C.byref(nd), sd, 12, 1, C.byref(cn), 3) == 0
+    assert nd.value == 1 and sd[0] == 12 and cn.value == 1
+    nd2 = C.c_long(2)
+    sd2 = (C.c_long * 8)(3, 5)
+    assert K.km_normalize_spatial_topology(C.byref(nd2), sd2, 12, 0, None, 0) == -1
+
+
+# ---------------------------------------------------------------------------
+# Backend selection and behaviour without a GPU
+# ---------------------------------------------------------------------------
+def _run_py(code, env_extra):
+    env = dict(os.environ, **env_extra)
+    return subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env,
+                          cwd=str(ROOT), timeout=120)
+
+
+def test_backend_env_parsing():
+    code = ("import sys; sys.path[:0]=['k-mamba_amd']; import kmamba as K; "
+            "K.kmamba_backend_init(); print(int(K.lib.kmamba_backend_preference if False else 0)); "
+            "import ctypes; v=ctypes.c_int.in_dll(K.lib,'kmamba_backend_preference'); print(v.value)")
+    for val, want in (("cpu", 1), ("GPU", 2), ("cuda", 2), ("auto", 0), ("weird", 0)):
+        out = _run_py(code, {"KMAMBA_BACKEND": val})
+        assert out.returncode == 0, out.stderr
+        assert out.stdout.split()[-1] == str(want), (val, out.stdout)
+
+
+def test_cpu_backend_request_fails_loudly():
+    # With KMAMBA_BACKEND=cpu the library refuses to compute (no CPU path)
+    # and leaves outputs untouched instead of producing something else.
+    code = ("import sys, ctypes as C, numpy as np; sys.path[:0]=['k-mamba_amd']; import kmamba as K\n"
+            "x=np.ones((4,3),np.float32); y=np.full((4,3),7,np.float32); A=-np.ones((3,2),np.float32)\n"
+            "B=np.ones((4,3,2),np.float32); h=np.zeros((3,2),np.float32)\n"
+            "p=K.ScanParams(K.ptr(x),K.ptr(A),K.ptr(B),K.ptr(B),K.ptr(x),K.ptr(h),K.ptr(y),4,3,2)\n"
+            "K.scan1d(C.byref(p)); print(K.km_last_error()); print(float(y.sum()))")
+    out = _run_py(code, {"KMAMBA_BACKEND": "cpu"})
+    assert out.returncode == 0, out.stderr
+    lines = out.stdout.strip().splitlines()
+    assert "no CPU compute path" in lines[-2]
+    assert lines[-1] == "84.0"
+
+
+@pytest.mark.skipif(K.kmamba_cuda_available() == 1, reason="a GPU is present")
+def test_no_gpu_reports_error():
+    assert K.kmamba_cuda_device_count() == 0
+    assert K.kmamba_backend_select() == K.KMAMBA_BACKEND_CPU
+    args = K.KMScan1DFwd()
+    args.B = args.L = args.D = args.N = 1
+    args.x = args.delta = args.A = args.Bm = args.Cm = args.y = 1
+    assert K.km_scan1d_fwd_c(C.byref(args), None) == -1
+    assert "HIP device" in K.km_last_error()

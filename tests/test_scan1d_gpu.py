@@ -1,0 +1,184 @@
+"""GPU parity of the Scan1D forward kernels (libkmamba, gfx950) against the
+CPU oracle on identical seeded inputs.
+
+Tolerances: condition-scaled max relative error (tests/kmtest.py) <= 1e-4
+for fp32 I/O and <= 2e-2 for bf16 I/O against the fp32 oracle of the
+unrounded inputs; the 1e-3*rms floor metric is printed beside it.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import kmamba as K
+import oracle as O
+from kmtest import (TOL_BF16, TOL_F32, assert_close, bf16_round, rel_err, rel_err_cond, rng_for,
+                    scan1d_inputs, scan1d_kappa)
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    torch.zeros(1, device=DEV)
+    assert K.kmamba_cuda_available() == 1, K.km_last_error()
+
+
+def T(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV, dtype)
+
+
+def run_km(x, dt, A, Bm, Cm, *, h0=None, hist=False, bc_strides=None, clamp=True, bf16=False):
+    Bsz, L, D = x.shape
+    N = A.shape[1]
+    io = torch.bfloat16 if bf16 else torch.float32
+    tx, tdt, tB, tC = T(x, io), T(dt, io), T(Bm, io), T(Cm, io)
+    tA = T(A)
+    y = torch.empty((Bsz, L, D), device=DEV, dtype=io)
+    th0 = None if h0 is None else T(h0)
+    hf = torch.empty((Bsz, D, N), device=DEV)
+    hh = torch.empty((Bsz, L, D, N), device=DEV) if hist else None
+    K.scan1d_fwd(tx, tdt, tA, tB, tC, y, h0=th0, h_final=hf, h_hist=hh, bc_strides=bc_strides,
+                 clamp=clamp)
+    torch.cuda.synchronize()
+    return (y.float().cpu().numpy(), hf.cpu().numpy(), None if hh is None else hh.cpu().numpy())
+
+
+def test_config0_fp32_parity():
+    # Scan1D fwd fp32, B=1, L=128, D=384, N=16.
+    x, dt, A, Bm, Cm = scan1d_inputs(1, 128, 384, 16, seed=0)
+    yr, hr, _ = O.scan1d_batched(x, dt, A, Bm, Cm)
+    assert np.abs(hr).max() < 1000          # clamp inactive on the config inputs
+    y, hf, _ = run_km(x, dt, A, Bm, Cm)
+    ky, kh, _ = scan1d_kappa(x, dt, A, Bm, Cm)
+    e_y = assert_close(y, yr, TOL_F32, "y", ky)
+    e_h = assert_close(hf, hr, TOL_F32, "h_final", kh)
+    print(f"config0 fp32: cond rel err y {e_y:.2e} h {e_h:.2e}; floor metric y {rel_err(y, yr):.2e} "
+          f"h {rel_err(hf, hr):.2e}")
+
+
+SHAPES = [
+    (2, 1, 32, 16), (1, 63, 33, 16), (3, 200, 70, 16), (2, 130, 64, 8), (1, 77, 100, 4),
+    (2, 65, 64, 2), (1, 300, 65, 1), (2, 50, 40, 3), (1, 40, 20, 32), (1, 1000, 32, 16),
+]
+
+
+@pytest.mark.parametrize("Bsz,L,D,N", SHAPES)
+@pytest.mark.parametrize("layout", ["shared", "per_channel"])
+def test_shapes_layouts_h0_hist(Bsz, L, D, N, layout):
+    x, dt, A, _, _ = scan1d_inputs(Bsz, L, D, N, seed=1)
+    g = rng_for("shapes", Bsz, L, D, N)
+    A = A * g.uniform(0.1, 1.0, size=A.shape).astype(np.float32)
+    h0 = g.standard_normal((Bsz, D, N)).astype(np.float32)
+    if layout == "shared":
+        Bm = (g.standard_normal((Bsz, L, N)) * 0.25).astype(np.float32)
+        Cm = (g.standard_normal((Bsz, L, N)) * 0.25).astype(np.float32)
+        strides = (L * N, N, 0)
+    else:
+        Bm = (g.standard_normal((Bsz, L, D, N)) * 0.25).astype(np.float32)
+        Cm = (g.standard_normal((Bsz, L, D, N)) * 0.25).astype(np.float32)
+        strides = (L * D * N, D * N, N)
+    yr, hr, hhr = O.scan1d_batched(x, dt, A, Bm, Cm, h0=h0, bc_strides=strides, hist=True)
+    y, hf, hh = run_km(x, dt, A, Bm, Cm, h0=h0, hist=True, bc_strides=strides)
+    ky, kh, khh = scan1d_kappa(x, dt, A, Bm, Cm, h0=h0, bc_strides=strides)
+    assert_close(y, yr, TOL_F32, "y", ky)
+    assert_close(hf, hr, TOL_F32, "h_final", kh)
+    assert_close(hh, hhr, TOL_F32, "h_hist", khh)
+
+
+def test_clamp_fallback_follows_per_step_clamp():
+    # Large drive: states leave [-1000, 1000]; the kernel must reproduce the
+    # reference's per-step clamp (cpu/scan1d.asm:136-140) exactly.
+    Bsz, L, D, N = 2, 300, 64, 16
+    x, dt, A, Bm, Cm = scan1d_inputs(Bsz, L, D, N, seed=2)
+    Bm = Bm * 800.0
+    A = A * 0.01
+    yr, hr, hhr = O.scan1d_batched(x, dt, A, Bm, Cm, hist=True)
+    assert np.abs(hhr).max() == 1000.0
+    y, hf, hh = run_km(x, dt, A, Bm, Cm, hist=True)
+    ky, kh, khh = scan1d_kappa(x, dt, A, Bm, Cm)
+    assert_close(y, yr, TOL_F32, "y", ky)
+    assert_close(hf, hr, TOL_F32, "h_final", np.minimum(kh, 1000.0))
+    assert np.abs(hh).max() == 1000.0
+    # Without the clamp flag the states run free.
+    y2, _, hh2 = run_km(x, dt, A, Bm, Cm, hist=True, clamp=False)
+    yu, _, hhu = O.scan1d_batched(x, dt, A, Bm, Cm, hist=True, clamp=False)
+    assert np.abs(hh2).max() > 1000.0
+    assert_close(hh2, hhu, TOL_F32, "unclamped h", khh)
+
+
+def test_bf16_io_against_fp32_oracle():
+    x, dt, A, Bm, Cm = scan1d_inputs(2, 512, 256, 16, seed=3)
+    yr, hr, _ = O.scan1d_batched(x, dt, A, Bm, Cm)
+    y, hf, _ = run_km(x, dt, A, Bm, Cm, bf16=True)
+    ky, _, _ = scan1d_kappa(x, dt, A, Bm, Cm)
+    e = assert_close(y, yr, TOL_BF16, "bf16 y", ky)
+    # And tighter against the oracle run on the bf16-rounded inputs.
+    yb, _, _ = O.scan1d_batched(*(bf16_round(a) for a in (x, dt)), A, bf16_round(Bm), bf16_round(Cm))
+    assert rel_err_cond(y, bf16_round(yb), ky) < 1e-2
+    print(f"bf16 y rel err vs fp32 oracle {e:.2e}")
+
+
+def test_om_scan1d_forward_reference_api():
+    # om_scan1d_forward: B, C, h are [L, D, M]; h receives the full history.
+    L, D, M = 150, 40, 16
+    x, A, B, Cm, dt = _api_inputs(L, D, M)
+    yr, _, hhr = O.scan1d_batched(x[None], dt[None], A, B[None], Cm[None],
+                                  bc_strides=(L * D * M, D * M, M), hist=True)
+    tx, tA, tB, tC, tdt = map(T, (x, A, B, Cm, dt))
+    y = torch.zeros((L, D), device=DEV)
+    h = torch.zeros((L, D, M), device=DEV)
+    K.om_scan1d_forward(K.ptr(tx), K.ptr(tA), K.ptr(tB), K.ptr(tC), K.ptr(tdt), K.ptr(y), K.ptr(h),
+                        L, D, M)
+    assert K.km_last_error() == ""
+    ky, _, khh = scan1d_kappa(x[None], dt[None], A, B[None], Cm[None], bc_strides=(L * D * M, D * M, M))
+    assert_close(y.cpu().numpy(), yr[0], TOL_F32, "y", ky[0])
+    assert_close(h.cpu().numpy(), hhr[0], TOL_F32, "h history", khh[0])
+
+
+def _api_inputs(L, D, M):
+    g = rng_for("api", L, D, M)
+    x = g.uniform(-1, 1, (L, D)).astype(np.float32)
+    A = g.uniform(-1, -0.01, (D, M)).astype(np.float32)
+    B = g.uniform(-0.5, 0.5, (L, D, M)).astype(np.float32)
+    Cm = g.uniform(-0.5, 0.5, (L, D, M)).astype(np.float32)
+    dt = g.uniform(0.01, 0.5, (L, D)).astype(np.float32)
+    return x, A, B, Cm, dt
+
+
+@pytest.mark.parametrize("L,D,M", [(4, 8, 1), (16, 16, 2), (64, 32, 1), (128, 48, 16)])
+def test_scan1d_host_pointer_api(L, D, M):
+    # scan1d(ScanParams*) on host memory, running [D, M] state in/out.
+    x, A, B, Cm, dt = _api_inputs(L, D, M)
+    h0 = rng_for("h0", L, D, M).uniform(-1, 1, (D, M)).astype(np.float32)
+    yr, hr = O.scan1d(x, A, B, Cm, dt, h0)
+    y = np.zeros((L, D), np.float32)
+    h = h0.copy()
+    p = K.ScanParams(K.ptr(x), K.ptr(A), K.ptr(B), K.ptr(Cm), K.ptr(dt), K.ptr(h), K.ptr(y), L, D, M)
+    K.mamba_scan1d_forward(C.byref(p))
+    assert K.km_last_error() == ""
+    ky, kh, _ = scan1d_kappa(x[None], dt[None], A, B[None], Cm[None], h0=h0[None],
+                             bc_strides=(L * D * M, D * M, M))
+    assert_close(y, yr, TOL_F32, "y", ky[0])
+    assert_close(h, hr, TOL_F32, "h", kh[0])
+
+
+def test_config1_full_size_sampled_parity():
+    # configs[1] shape (B=8, L=4096, D=1024, N=16) on the GPU, checked against
+    # the oracle on a sample of channels of the first and last batch element
+    # (channels are independent, so the sample is an exact sub-problem).
+    Bsz, L, D, N = 8, 4096, 1024, 16
+    x, dt, A, Bm, Cm = scan1d_inputs(Bsz, L, D, N, seed=0, tag="config1")
+    y, hf, _ = run_km(x, dt, A, Bm, Cm)
+    assert np.isfinite(y).all()
+    sel = np.sort(rng_for("sel").choice(D, 48, replace=False))
+    for b in (0, Bsz - 1):
+        args = (x[b:b + 1][:, :, sel], dt[b:b + 1][:, :, sel], A[sel], Bm[b:b + 1], Cm[b:b + 1])
+        yr, hr, _ = O.scan1d_batched(*args, nthreads=8, fast=True)
+        ky, kh, _ = scan1d_kappa(*args)
+        assert_close(y[b][:, sel], yr[0], TOL_F32, f"y[b={b}]", ky[0])
+        assert_close(hf[b][sel], hr[0], TOL_F32, f"h[b={b}]", kh[0])
