@@ -37,6 +37,41 @@ def scan1d_alg_bytes(Bsz, L, D, N, s):
     return 3 * Bsz * L * D * s + D * N * 4 + 2 * Bsz * L * N * s + Bsz * D * N * 4
 
 
+def scannd_alg_bytes(dims, D, M):
+    """Algorithmic bytes of one ScanND forward: x [P,D], delta [nd,P,D],
+    A [nd,D,M], B and C [P,D,M] read; h [P,D,M] and y [P,D] written (fp32)."""
+    nd = len(dims)
+    P = 1
+    for v in dims:
+        P *= v
+    return 4 * (P * D + nd * P * D + nd * D * M + 2 * P * D * M + P * D * M + P * D)
+
+
+def bench_scannd(torch, K, stream, dims, D, M, steps, warmup):
+    """configs[2] workload: x ~ N(0,1); delta = 1; A = log(U(0.05, 0.9/nd));
+    B, C ~ N(0, 1/16); scannd_ref semantics (h and y written)."""
+    nd = len(dims)
+    P = 1
+    for v in dims:
+        P *= v
+    g = torch.Generator(device="cuda").manual_seed(11)
+    x = torch.randn((P, D), device="cuda", generator=g)
+    A = torch.log(0.05 + (0.9 / nd - 0.05) * torch.rand((nd, D, M), device="cuda", generator=g))
+    B = torch.randn((P, D, M), device="cuda", generator=g) * 0.25
+    Cm = torch.randn((P, D, M), device="cuda", generator=g) * 0.25
+    dt = torch.ones((nd, P, D), device="cuda")
+    h = torch.empty((P, D, M), device="cuda")
+    y = torch.empty((P, D), device="cuda")
+    fn = lambda: K.scannd_fwd(dims, x, A, B, Cm, dt, h, y, stream=stream)  # noqa: E731
+    per, wall = time_launches(torch, stream, fn, steps, warmup)
+    ms = wall / steps
+    alg = scannd_alg_bytes(dims, D, M)
+    return {"ms": round(ms, 4), "elems_per_s": P * D / (ms * 1e-3),
+            "achieved_GBs": round(alg / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "alg_bytes": alg,
+            "launches_per_step": "one per tile band"}
+
+
 def make_inputs(torch, Bsz, L, D, N, dtype, seed=0):
     g = torch.Generator(device="cuda").manual_seed(seed)
     dev = "cuda"
@@ -97,7 +132,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["all", "scan1d", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "scan1d", "scannd", "copy"], default="all",
                     help="profiling modes: scan1d = the fp32 headline kernel only; copy = a plain "
                          "1 GiB device copy (calibrates rocprof FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -120,6 +155,12 @@ def main():
         ms = sum(per) / len(per)
         print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n, "ms": ms,
                           "GBs_read_plus_write": 8 * n / (ms * 1e-3) / 1e9}))
+        return
+    if args.only == "scannd":
+        with torch.cuda.stream(stream):
+            r2 = bench_scannd(torch, K, stream, (256, 256), 256, 16, args.steps, args.warmup)
+            r3 = bench_scannd(torch, K, stream, (64, 64, 64), 128, 16, args.steps, args.warmup)
+        print(json.dumps({"scan2d_256x256_D256_M16": r2, "scan3d_64cubed_D128_M16": r3}))
         return
     Bsz, L, D, N = 8, 4096, 1024, 16
     extra = {}
@@ -158,6 +199,13 @@ def main():
         extra["scan1d_fwd_bf16"] = {"ms": round(msb, 4), "elems_per_s": elems / (msb * 1e-3),
                                     "achieved_GBs": round(algb / (msb * 1e-3) / 1e9, 1),
                                     "frac_hbm": round(algb / (msb * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+    with torch.cuda.stream(stream):
+        del xb, dtb, Bb, Cb, yb
+        extra["scannd_2d_256x256_D256_M16_f32"] = bench_scannd(torch, K, stream, (256, 256), 256, 16,
+                                                                max(5, args.steps // 2), 2)
+        extra["scannd_3d_64cubed_D128_M16_f32"] = bench_scannd(torch, K, stream, (64, 64, 64), 128, 16,
+                                                                max(5, args.steps // 2), 2)
 
     traffic = None
     tf = ROOT / "profiles" / "scan1d_fwd_c1_traffic.json"

@@ -13,6 +13,8 @@
 
 #include <stddef.h>
 
+#include "scan_nd.h"
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -66,6 +68,12 @@ typedef struct {
 } KMScan1DFwd;
 
 int km_scan1d_fwd(const KMScan1DFwd *a, void *stream);
+
+/* ScanND forward on device pointers, enqueued on `stream` (NULL = default
+ * stream) without a host synchronisation. Same parameters and layout as
+ * om_scannd_forward (ref include/scan_nd.h:72, cuda/scan_nd.cu); theta
+ * and lambda must be NULL. Returns 0, or -1 with km_last_error() set. */
+int km_scannd_fwd(const ScanNDParams *p, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,648 @@
+// scannd.hip - ScanND / Scan2D selective-scan forward for gfx950.
+//
+// Recurrence (reference src/scan_nd.c:95-192, lambda == NULL branch):
+//   dt_bar(p,d) = (sum_axis delta(axis,p,d)) / ndims
+//   h(p,d,m)    = dt_bar * (B(p,d,m) * x(p,d))
+//               + sum_axis[idx_axis > 0] exp(delta(axis,p,d) * A(axis,d,m)) * h(p - e_axis, d, m)
+//   y(p,d)      = sum_m C(p,d,m) * h(p,d,m)
+// Scan2D (cpu/scan2d.asm:66-275) is the ndims = 2 case with separate A/delta
+// pointers per axis; it differs from scannd_ref only in the association of
+// the same products and sums.
+//
+// Layout and schedule (instead of one launch per wavefront level):
+//  * lanes: 64 consecutive flattened (d, m) pairs, so B, C and h rows are
+//    256-byte coalesced accesses and y is a reduction over the M lanes of a
+//    channel;
+//  * the grid is cut into tiles; tiles with equal coordinate sum (a tile band)
+//    are independent, so the host issues one launch per tile band (15 for a
+//    256x256 grid with 32x32 tiles instead of 511 per-level launches); the
+//    kernel boundary publishes every tile's h to the next band;
+//  * inside a tile the last two axes form planes; waves own column strips of
+//    a plane and walk its rows in a skewed pipeline (wave w handles row
+//    tau - w at step tau), handing the strip's last state to the next wave
+//    through LDS with one barrier per step; the row above lives in registers;
+//    leading axes iterate planes, reading the previous plane's states back
+//    from memory (same CU, just written).
+#include <cstdlib>
+
+#include "km_device.hpp"
+#include "../km_runtime.hpp"
+#include "kmamba_km.h"
+#include "scan.h"
+#include "scan_nd.h"
+#include "mamba_scan.h"
+#include "mamba_scan_cuda.h"
+
+namespace km {
+
+constexpr int kMaxNd = 8;
+
+struct ScanNDArgs {
+    const float *x;
+    const float *A[kMaxNd];      // per axis [D, M]
+    const float *dt[kMaxNd];     // per axis [P, D]
+    const float *B, *C;
+    float *h, *y;
+    int nd;
+    int dims[kMaxNd];
+    long pstride[kMaxNd];        // row-major point strides
+    int tile[kMaxNd];            // tile extent per axis
+    int ntile[kMaxNd];           // tiles per axis
+    int band;                    // tile band (sum of tile indices)
+    int D, M, DM;
+    int ncg;                     // channel groups of 64 (d, m) lanes
+};
+
+// Tile band b, ordinal o: the o-th tile (lexicographic) with index sum b.
+__device__ inline bool band_tile(const ScanNDArgs &p, int ordinal, int *ti) {
+    int cnt = 0;
+    int total = 1;
+    for (int a = 0; a < p.nd; ++a) total *= p.ntile[a];
+    for (int lin = 0; lin < total; ++lin) {
+        int rem = lin, s = 0;
+        for (int a = p.nd - 1; a >= 0; --a) {
+            ti[a] = rem % p.ntile[a];
+            rem /= p.ntile[a];
+            s += ti[a];
+        }
+        if (s == p.band) {
+            if (cnt == ordinal) return true;
+            ++cnt;
+        }
+    }
+    return false;
+}
+
+// DPP lane move within rows of 16 lanes (ctrl: row_ror, mirrors, quad_perm).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                  0xf, 0xf, false));
+}
+
+// Sum over the M consecutive lanes of a channel (M a power of two <= 64);
+// every lane of the group receives the sum. Within a 16-lane row the steps
+// are DPP VALU ops (no LDS round trip).
+template <int MM>
+__device__ __forceinline__ float sum_m_lanes(float v) {
+    if constexpr (MM == 2) {
+        v += dpp<0xB1>(v);                       // quad_perm [1,0,3,2]
+    } else if constexpr (MM == 4) {
+        v += dpp<0x4E>(v);                       // quad_perm [2,3,0,1]
+        v += dpp<0xB1>(v);
+    } else if constexpr (MM == 8) {
+        v += dpp<0x141>(v);                      // row_half_mirror
+        v += dpp<0x4E>(v);
+        v += dpp<0xB1>(v);
+    } else if constexpr (MM >= 16) {
+        v += dpp<0x128>(v);                      // row_ror:8
+        v += dpp<0x124>(v);                      // row_ror:4
+        v += dpp<0x122>(v);                      // row_ror:2
+        v += dpp<0x121>(v);                      // row_ror:1
+        if constexpr (MM >= 32) v += __shfl_xor(v, 16);
+        if constexpr (MM >= 64) v += __shfl_xor(v, 32);
+    }
+    return v;
+}
+
+// One wave per (tile, channel group). The wave walks its tile row by row
+// (rows along axis ND-2, leading axes outermost), each row along the last
+// axis, prefetching the next row's operands while the current row computes.
+// The row above is kept in registers; leading-axis neighbours and the tile's
+// top/left boundary are read from h (written earlier by this wave or by a
+// previous band's launch).
+template <int ND, int TW>
+struct NDRow {
+    float x[TW], b[TW], c[TW], dt[ND][TW], hn[ND - 1][TW];
+    float hleft;
+    int gi[ND];
+    long base;
+};
+
+template <int ND, int TW, int MM>
+__global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
+    const int lane = threadIdx.x;
+    const int cg = blockIdx.x % p.ncg;
+    const int ordinal = blockIdx.x / p.ncg;
+    int ti[kMaxNd];
+    if (!band_tile(p, ordinal, ti)) return;
+
+    constexpr int ar = ND - 2, ac = ND - 1;       // row / column axes
+    const int f = cg * 64 + lane;                 // flattened (d, m)
+    const int d = f / MM;
+    const int DM = p.DM;
+    const int D = p.D;
+    const bool y_lane = (lane % MM) == 0;
+
+    float Ap[ND];
+#pragma unroll
+    for (int a = 0; a < ND; ++a) Ap[a] = p.A[a][f] * kLog2e;
+
+    int lo[ND], ext[ND];
+#pragma unroll
+    for (int a = 0; a < ND; ++a) {
+        lo[a] = ti[a] * p.tile[a];
+        ext[a] = min(p.tile[a], p.dims[a] - lo[a]);
+    }
+    const int TC = ext[ac];
+    int nrows = 1;
+#pragma unroll
+    for (int a = 0; a < ac; ++a) nrows *= ext[a];
+
+    // Operands of one row, read through per-lane pointers that advance by
+    // a uniform stride per point (D for x/delta, D*M for B/C/h).
+    auto load_row = [&](int row, NDRow<ND, TW> &r) {
+        int rem = row;
+#pragma unroll
+        for (int a = ac - 1; a >= 0; --a) {
+            r.gi[a] = lo[a] + rem % ext[a];
+            rem /= ext[a];
+        }
+        r.gi[ac] = lo[ac];
+        long pb = lo[ac];
+#pragma unroll
+        for (int a = 0; a < ac; ++a) pb += static_cast<long>(r.gi[a]) * p.pstride[a];
+        r.base = pb;
+        const float *xp = p.x + pb * D + d;
+        const float *Bp = p.B + pb * DM + f;
+        const float *Cp = p.C + pb * DM + f;
+        const float *dp[ND];
+#pragma unroll
+        for (int a = 0; a < ND; ++a) dp[a] = p.dt[a] + pb * D + d;
+#pragma unroll
+        for (int c = 0; c < TW; ++c) {
+            r.x[c] = *xp;
+            r.b[c] = *Bp;
+            r.c[c] = *Cp;
+#pragma unroll
+            for (int a = 0; a < ND; ++a) r.dt[a][c] = *dp[a];
+            if (c + 1 < TC) {
+                xp += D;
+                Bp += DM;
+                Cp += DM;
+#pragma unroll
+                for (int a = 0; a < ND; ++a) dp[a] += D;
+            }
+        }
+        // Neighbours along leading axes, and along the row axis on the tile's
+        // first row of a plane (tile boundary); uniform conditions.
+        const float *hb = p.h + pb * DM + f;
+#pragma unroll
+        for (int a = 0; a < ND - 1; ++a) {
+            const bool need = (a < ar) ? (r.gi[a] > 0) : (r.gi[a] > 0 && r.gi[a] == lo[a]);
+            if (need) {
+                const float *np = hb - p.pstride[a] * DM;
+#pragma unroll
+                for (int c = 0; c < TW; ++c) {
+                    r.hn[a][c] = *np;
+                    if (c + 1 < TC) np += DM;
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < TW; ++c) r.hn[a][c] = 0.f;
+            }
+        }
+        r.hleft = (lo[ac] > 0) ? *(hb - DM) : 0.f;
+    };
+
+    float top[TW];
+#pragma unroll
+    for (int c = 0; c < TW; ++c) top[c] = 0.f;
+    // dt_bar = sum / ndims: 1/ndims is exact for ndims 2 and 4; for 3 the
+    // product differs from the reference's division by at most one ulp.
+    const float inv_nd = 1.0f / static_cast<float>(ND);
+
+    auto compute_row = [&](const NDRow<ND, TW> &r) {
+        const bool first_row_of_plane = (r.gi[ar] == lo[ar]);
+        float hleft = r.hleft;
+#pragma unroll
+        for (int c = 0; c < TW; ++c) {
+            if (c < TC) {
+                float dsum = 0.f;
+#pragma unroll
+                for (int a = 0; a < ND; ++a) dsum += r.dt[a][c];
+                float acc = (dsum * inv_nd) * (r.b[c] * r.x[c]);
+#pragma unroll
+                for (int a = 0; a < ar; ++a)
+                    if (r.gi[a] > 0) acc = fmaf(exp2_fast(r.dt[a][c] * Ap[a]), r.hn[a][c], acc);
+                if (r.gi[ar] > 0) {
+                    const float hu = first_row_of_plane ? r.hn[ar][c] : top[c];
+                    acc = fmaf(exp2_fast(r.dt[ar][c] * Ap[ar]), hu, acc);
+                }
+                if (lo[ac] + c > 0) acc = fmaf(exp2_fast(r.dt[ac][c] * Ap[ac]), hleft, acc);
+                p.h[(r.base + c) * DM + f] = acc;
+                top[c] = acc;
+                hleft = acc;
+                const float yv = sum_m_lanes<MM>(r.c[c] * acc);
+                if (y_lane) p.y[(r.base + c) * D + d] = yv;
+            }
+        }
+    };
+
+    NDRow<ND, TW> R0, R1;
+    load_row(0, R0);
+    for (int row = 0; row < nrows; row += 2) {
+        if (row + 1 < nrows) load_row(row + 1, R1);
+        compute_row(R0);
+        if (row + 1 < nrows) {
+            if (row + 2 < nrows) load_row(row + 2, R0);
+            compute_row(R1);
+        }
+    }
+}
+
+// General fallback (any D, M): one launch per wavefront level of the point
+// grid, one thread per (point, channel), reading the level's offsets from
+// the device copy of the plan.
+__global__ void __launch_bounds__(256) scannd_level_kernel(ScanNDArgs p, const long *offsets,
+                                                           long start, long count) {
+    const long gid = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid >= count * p.D) return;
+    const long off = offsets[start + gid / p.D];
+    const int d = static_cast<int>(gid % p.D);
+    int idx[kMaxNd];
+    {
+        long rem = off;
+        for (int a = p.nd - 1; a >= 0; --a) {
+            idx[a] = static_cast<int>(rem % p.dims[a]);
+            rem /= p.dims[a];
+        }
+    }
+    float dsum = 0.f;
+    for (int a = 0; a < p.nd; ++a) dsum += p.dt[a][off * p.D + d];
+    const float dtb = dsum / static_cast<float>(p.nd);
+    const float xv = p.x[off * p.D + d];
+    float y = 0.f;
+    for (int m = 0; m < p.M; ++m) {
+        const long q = off * p.DM + static_cast<long>(d) * p.M + m;
+        float acc = dtb * (p.B[q] * xv);
+        for (int a = 0; a < p.nd; ++a) {
+            if (idx[a] > 0) {
+                const float e = exp2_fast(p.dt[a][off * p.D + d] * p.A[a][d * p.M + m] * kLog2e);
+                acc = fmaf(e, p.h[q - p.pstride[a] * p.DM], acc);
+            }
+        }
+        p.h[q] = acc;
+        y = fmaf(p.C[q], acc, y);
+    }
+    p.y[off * p.D + d] = y;
+}
+
+// Device workspace for the fallback's plan offsets (grown on demand, kept
+// for the process).
+static long *g_plan_dev = nullptr;
+static size_t g_plan_cap = 0;
+
+static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s) {
+    const bool fast = (a.DM % 64 == 0) && (64 % a.M == 0) && a.nd >= 2 && a.nd <= 4;
+    if (fast) {
+        // Tiles: 2D 16 rows x 16 columns; 3D and up 8 per axis. One wave
+        // per (tile, channel group); one launch per tile band.
+        const int TWc = (a.nd == 2) ? 16 : 8;
+        const int Tlead = (a.nd == 2) ? 16 : 8;
+        int nbands = 1;
+        for (int ax = 0; ax < a.nd; ++ax) {
+            const int t = (ax == a.nd - 1) ? TWc : Tlead;
+            a.tile[ax] = (a.dims[ax] < t) ? a.dims[ax] : t;
+            a.ntile[ax] = (a.dims[ax] + a.tile[ax] - 1) / a.tile[ax];
+            nbands += a.ntile[ax] - 1;
+        }
+        a.ncg = a.DM / 64;
+        if (nbands > 4096) {
+            set_error("scannd: too many tile bands");
+            return -1;
+        }
+        // Tiles per band: distribution of tile-index sums.
+        static thread_local long cnt[4096], nxt[4096];
+        for (int i = 0; i < nbands; ++i) cnt[i] = 0;
+        cnt[0] = 1;
+        int reach = 0;
+        for (int ax = 0; ax < a.nd; ++ax) {
+            for (int i = 0; i <= reach + a.ntile[ax] - 1; ++i) nxt[i] = 0;
+            for (int sidx = 0; sidx <= reach; ++sidx)
+                for (int v = 0; v < a.ntile[ax]; ++v) nxt[sidx + v] += cnt[sidx];
+            reach += a.ntile[ax] - 1;
+            for (int sidx = 0; sidx <= reach; ++sidx) cnt[sidx] = nxt[sidx];
+        }
+        for (int b = 0; b < nbands; ++b) {
+            a.band = b;
+            const long grid = cnt[b] * a.ncg;
+            if (grid <= 0) continue;
+            const dim3 g(static_cast<unsigned>(grid)), blk(64);
+#define KM_ND_LAUNCH(NDv, TWv, MMv) hipLaunchKernelGGL((scannd_tile_kernel<NDv, TWv, MMv>), g, blk, 0, s, a)
+#define KM_ND_BY_M(NDv, TWv)                                  \
+            switch (a.M) {                                    \
+            case 1: KM_ND_LAUNCH(NDv, TWv, 1); break;         \
+            case 2: KM_ND_LAUNCH(NDv, TWv, 2); break;         \
+            case 4: KM_ND_LAUNCH(NDv, TWv, 4); break;         \
+            case 8: KM_ND_LAUNCH(NDv, TWv, 8); break;         \
+            case 16: KM_ND_LAUNCH(NDv, TWv, 16); break;       \
+            case 32: KM_ND_LAUNCH(NDv, TWv, 32); break;       \
+            default: KM_ND_LAUNCH(NDv, TWv, 64); break;       \
+            }
+            if (a.nd == 2) {
+                KM_ND_BY_M(2, 16)
+            } else if (a.nd == 3) {
+                KM_ND_BY_M(3, 8)
+            } else {
+                KM_ND_BY_M(4, 8)
+            }
+#undef KM_ND_BY_M
+#undef KM_ND_LAUNCH
+            KM_HIP_TRY(hipGetLastError());
+        }
+        return 0;
+    }
+    // Fallback: per-level launches over the plan.
+    long dims[kMaxNd];
+    for (int ax = 0; ax < a.nd; ++ax) dims[ax] = a.dims[ax];
+    KMWavefrontPlan *plan = km_wavefront_plan_create(dims, a.nd);
+    if (!plan) {
+        set_error("scannd: plan creation failed");
+        return -1;
+    }
+    const size_t bytes = sizeof(long) * P;
+    if (g_plan_cap < bytes) {
+        if (g_plan_dev) {
+            (void)hipStreamSynchronize(s);
+            (void)hipFree(g_plan_dev);
+        }
+        g_plan_dev = nullptr;
+        g_plan_cap = 0;
+        if (hipMalloc(&g_plan_dev, bytes) != hipSuccess) {
+            km_wavefront_plan_free(plan);
+            set_error("scannd: plan workspace allocation failed");
+            return -1;
+        }
+        g_plan_cap = bytes;
+    }
+    if (hipMemcpyAsync(g_plan_dev, plan->level_offsets, bytes, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess) {
+        km_wavefront_plan_free(plan);
+        set_error("scannd: plan upload failed");
+        return -1;
+    }
+    for (long lvl = 0; lvl <= plan->max_level; ++lvl) {
+        const long start = plan->level_starts[lvl];
+        const long count = plan->level_starts[lvl + 1] - start;
+        const long threads = count * a.D;
+        hipLaunchKernelGGL(scannd_level_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)),
+                           dim3(256), 0, s, a, g_plan_dev, start, count);
+    }
+    km_wavefront_plan_free(plan);
+    KM_HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+// Shared front end: device pointers, scannd_ref semantics for ndims >= 2.
+static int scannd_device(const float *x, const float *const *A, const float *const *dt,
+                         const float *B, const float *C, float *h, float *y, const long *dims,
+                         long nd, long D, long M, hipStream_t s) {
+    if (nd < 2 || nd > kMaxNd) {
+        set_error("scannd: ndims %ld outside [2, %d] for the band kernel", nd, kMaxNd);
+        return -1;
+    }
+    ScanNDArgs a{};
+    a.x = x;
+    a.B = B;
+    a.C = C;
+    a.h = h;
+    a.y = y;
+    a.nd = static_cast<int>(nd);
+    a.D = static_cast<int>(D);
+    a.M = static_cast<int>(M);
+    a.DM = static_cast<int>(D * M);
+    long P = 1;
+    for (int ax = 0; ax < nd; ++ax) {
+        if (dims[ax] <= 0 || dims[ax] > 0x7fffffff) {
+            set_error("scannd: invalid dims[%d] = %ld", ax, dims[ax]);
+            return -1;
+        }
+        a.dims[ax] = static_cast<int>(dims[ax]);
+        a.A[ax] = A[ax];
+        a.dt[ax] = dt[ax];
+        P *= dims[ax];
+    }
+    long st = 1;
+    for (int ax = static_cast<int>(nd) - 1; ax >= 0; --ax) {
+        a.pstride[ax] = st;
+        st *= dims[ax];
+    }
+    if (D * M > 0x7fffffffL || P * D * M > (1L << 46)) {
+        set_error("scannd: problem too large");
+        return -1;
+    }
+    return scannd_launch(a, P, s);
+}
+
+static bool scannd_params_ok(const ScanNDParams *p) {
+    if (!scannd_validate(p)) {
+        set_error("scannd: invalid parameters");
+        return false;
+    }
+    if (p->theta || p->lambda) {
+        set_error("scannd: the Mamba-3 theta/lambda extensions are not implemented by the GPU kernels");
+        return false;
+    }
+    return true;
+}
+
+int scannd_device_params(const ScanNDParams *p, hipStream_t s) {
+    if (!scannd_params_ok(p)) return -1;
+    if (!gpu_ready()) return -1;
+    const long P = wavefront_nd_total_points(p->dims, p->ndims);
+    const float *A[kMaxNd], *dt[kMaxNd];
+    for (long ax = 0; ax < p->ndims && ax < kMaxNd; ++ax) {
+        A[ax] = p->A + ax * p->D * p->M;
+        dt[ax] = p->delta + ax * P * p->D;
+    }
+    if (p->ndims == 1) {
+        // ndims == 1: the 1D recurrence with the full state written, no clamp.
+        KMScan1DFwd k{};
+        k.x = p->x; k.delta = p->delta; k.A = p->A; k.Bm = p->B; k.Cm = p->C; k.y = p->y;
+        k.h_hist = p->h;
+        k.B = 1; k.L = P; k.D = p->D; k.N = p->M;
+        k.bc_sb = P * p->D * p->M; k.bc_st = p->D * p->M; k.bc_sd = p->M;
+        k.dtype = KM_F32; k.clamp = 0;
+        return km_scan1d_fwd(&k, s);
+    }
+    return scannd_device(p->x, A, dt, p->B, p->C, p->h, p->y, p->dims, p->ndims, p->D, p->M, s);
+}
+
+// Host-pointer staging for the reference's host API: copies inputs to the
+// device (or uses them in place when they already are device memory), runs,
+// and copies h and y back.
+struct NDStage {
+    float *x, *A, *B, *C, *dt, *h, *y;
+};
+
+static int scannd_host(const ScanNDParams *p, bool scan1d_semantics) {
+    if (!scannd_params_ok(p)) return -1;
+    if (!gpu_ready()) return -1;
+    const long P = wavefront_nd_total_points(p->dims, p->ndims);
+    const long nd = p->ndims, D = p->D, M = p->M;
+    const size_t nx = P * D, nA = nd * D * M, nB = P * D * M, ndt = nd * P * D;
+    const size_t nh = scan1d_semantics ? static_cast<size_t>(D * M) : nB;
+    const bool dev = is_device_ptr(p->x) && is_device_ptr(p->A) && is_device_ptr(p->B) &&
+                     is_device_ptr(p->C) && is_device_ptr(p->delta) && is_device_ptr(p->h) &&
+                     is_device_ptr(p->y);
+    int rc = 0;
+    if (dev) {
+        if (scan1d_semantics) {
+            ScanParams sp{const_cast<float *>(p->x), const_cast<float *>(p->A), const_cast<float *>(p->B),
+                          const_cast<float *>(p->C), const_cast<float *>(p->delta), p->h, p->y,
+                          P, D, M};
+            scan1d(&sp);
+            return km_last_error()[0] ? -1 : 0;
+        }
+        rc = scannd_device_params(p, nullptr);
+        if (rc == 0 && hipStreamSynchronize(nullptr) != hipSuccess) {
+            set_error("scannd: %s", hipGetErrorString(hipGetLastError()));
+            rc = -1;
+        }
+        return rc;
+    }
+    if (scan1d_semantics) {
+        ScanParams sp{const_cast<float *>(p->x), const_cast<float *>(p->A), const_cast<float *>(p->B),
+                      const_cast<float *>(p->C), const_cast<float *>(p->delta), p->h, p->y, P, D, M};
+        scan1d(&sp);
+        return km_last_error()[0] ? -1 : 0;
+    }
+    Staging::lock();
+    const size_t bytes = sizeof(float) * (2 * nx + nA + 3 * nB + ndt) + 8 * 256;
+    void *base = Staging::reserve(bytes);
+    if (!base) {
+        Staging::unlock();
+        return -1;
+    }
+    Carver c(base);
+    NDStage st{c.take<float>(nx), c.take<float>(nA), c.take<float>(nB), c.take<float>(nB),
+               c.take<float>(ndt), c.take<float>(nh), c.take<float>(nx)};
+    const bool ok = hipMemcpy(st.x, p->x, nx * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                    hipMemcpy(st.A, p->A, nA * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                    hipMemcpy(st.B, p->B, nB * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                    hipMemcpy(st.C, p->C, nB * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                    hipMemcpy(st.dt, p->delta, ndt * 4, hipMemcpyHostToDevice) == hipSuccess;
+    if (!ok) {
+        set_error("scannd: host-to-device copy failed");
+        rc = -1;
+    } else {
+        ScanNDParams q = *p;
+        q.x = st.x; q.A = st.A; q.B = st.B; q.C = st.C; q.delta = st.dt; q.h = st.h; q.y = st.y;
+        rc = scannd_device_params(&q, nullptr);
+        if (rc == 0 && (hipMemcpy(p->h, st.h, nh * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+                        hipMemcpy(p->y, st.y, nx * 4, hipMemcpyDeviceToHost) != hipSuccess)) {
+            set_error("scannd: device-to-host copy failed");
+            rc = -1;
+        }
+    }
+    Staging::unlock();
+    return rc;
+}
+
+}  // namespace km
+
+extern "C" {
+
+int scannd_validate(const ScanNDParams *p) {
+    if (!p || !p->dims) return 0;
+    if (p->ndims <= 0 || p->D <= 0 || p->M <= 0) return 0;
+    if (!p->x || !p->A || !p->B || !p->C || !p->delta || !p->h || !p->y) return 0;
+    if (!wavefront_nd_validate_dims(p->dims, p->ndims)) return 0;
+    if (wavefront_nd_total_points(p->dims, p->ndims) <= 0) return 0;
+    return 1;
+}
+
+int km_scannd_fwd(const ScanNDParams *p, void *stream) {
+    km::clear_error();
+    return km::scannd_device_params(p, static_cast<hipStream_t>(stream));
+}
+
+int om_scannd_forward(ScanNDParams *p) {
+    km::clear_error();
+    if (km::scannd_device_params(p, nullptr) != 0) return -1;
+    if (hipStreamSynchronize(nullptr) != hipSuccess) {
+        km::set_error("om_scannd_forward: %s", hipGetErrorString(hipGetLastError()));
+        return -1;
+    }
+    return 0;
+}
+
+int mamba_scannd_cuda_forward(ScanNDParams *p) { return om_scannd_forward(p); }
+
+int scannd_ref(ScanNDParams *p) {
+    km::clear_error();
+    return km::scannd_host(p, false);
+}
+
+int scannd_ref_with_plan(ScanNDParams *p, const KMWavefrontPlan *plan) {
+    km::clear_error();
+    if (!p || !km_wavefront_plan_matches_dims(plan, p->dims, p->ndims)) {
+        km::set_error("scannd_ref_with_plan: plan does not match dims");
+        return -1;
+    }
+    return km::scannd_host(p, false);
+}
+
+int scannd(ScanNDParams *p) {
+    km::clear_error();
+    if (!scannd_validate(p)) {
+        km::set_error("scannd: invalid parameters");
+        return -1;
+    }
+    return km::scannd_host(p, p->ndims == 1);
+}
+
+void scan2d(Scan2DParams *p) {
+    km::clear_error();
+    if (!p || !p->x || !p->A1 || !p->A2 || !p->B || !p->C || !p->delta1 || !p->delta2 || !p->h ||
+        !p->y || p->d1 <= 0 || p->d2 <= 0 || p->D <= 0 || p->M <= 0) {
+        km::set_error("scan2d: invalid parameters");
+        return;
+    }
+    if (!km::gpu_ready()) return;
+    const long dims[2] = {p->d1, p->d2};
+    const long P = p->d1 * p->d2, D = p->D, M = p->M;
+    const size_t nx = P * D, nA = D * M, nB = P * D * M;
+    const bool dev = km::is_device_ptr(p->x) && km::is_device_ptr(p->A1) && km::is_device_ptr(p->A2) &&
+                     km::is_device_ptr(p->B) && km::is_device_ptr(p->C) &&
+                     km::is_device_ptr(p->delta1) && km::is_device_ptr(p->delta2) &&
+                     km::is_device_ptr(p->h) && km::is_device_ptr(p->y);
+    if (dev) {
+        const float *A[2] = {p->A1, p->A2}, *dt[2] = {p->delta1, p->delta2};
+        if (km::scannd_device(p->x, A, dt, p->B, p->C, p->h, p->y, dims, 2, D, M, nullptr) == 0 &&
+            hipStreamSynchronize(nullptr) != hipSuccess)
+            km::set_error("scan2d: %s", hipGetErrorString(hipGetLastError()));
+        return;
+    }
+    km::Staging::lock();
+    void *base = km::Staging::reserve(sizeof(float) * (4 * nx + 2 * nA + 3 * nB) + 10 * 256);
+    if (base) {
+        km::Carver c(base);
+        float *x = c.take<float>(nx), *A1 = c.take<float>(nA), *A2 = c.take<float>(nA);
+        float *B = c.take<float>(nB), *C = c.take<float>(nB), *d1 = c.take<float>(nx);
+        float *d2 = c.take<float>(nx), *h = c.take<float>(nB), *y = c.take<float>(nx);
+        const bool ok = hipMemcpy(x, p->x, nx * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                        hipMemcpy(A1, p->A1, nA * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                        hipMemcpy(A2, p->A2, nA * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                        hipMemcpy(B, p->B, nB * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                        hipMemcpy(C, p->C, nB * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                        hipMemcpy(d1, p->delta1, nx * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                        hipMemcpy(d2, p->delta2, nx * 4, hipMemcpyHostToDevice) == hipSuccess;
+        if (!ok) {
+            km::set_error("scan2d: host-to-device copy failed");
+        } else {
+            const float *A[2] = {A1, A2}, *dt[2] = {d1, d2};
+            if (km::scannd_device(x, A, dt, B, C, h, y, dims, 2, D, M, nullptr) == 0) {
+                if (hipMemcpy(p->h, h, nB * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+                    hipMemcpy(p->y, y, nx * 4, hipMemcpyDeviceToHost) != hipSuccess)
+                    km::set_error("scan2d: device-to-host copy failed");
+            }
+        }
+    }
+    km::Staging::unlock();
+}
+
+void mamba_scan2d_forward(MambaScan2DParams *p) { scan2d(p); }
+
+}  // extern "C"

@@ -196,3 +196,33 @@ def scan1d_fwd(x, delta, A, Bm, Cm, y, *, h0=None, h_final=None, h_hist=None,
     args = KMScan1DFwd(ptr(x), ptr(delta), ptr(A), ptr(Bm), ptr(Cm), ptr(y), ptr(h0),
                        ptr(h_final), ptr(h_hist), Bsz, L, D, N, *bc_strides, dt, int(clamp))
     check(km_scan1d_fwd_c(C.byref(args), C.c_void_p(stream_handle(stream))), "km_scan1d_fwd")
+
+
+# --- ScanND / Scan2D ----------------------------------------------------------
+scannd_validate = _decl("scannd_validate", C.c_int, [C.POINTER(ScanNDParams)])
+scannd_ref = _decl("scannd_ref", C.c_int, [C.POINTER(ScanNDParams)])
+scannd_ref_with_plan = _decl("scannd_ref_with_plan", C.c_int,
+                             [C.POINTER(ScanNDParams), C.POINTER(KMWavefrontPlan)])
+scannd = _decl("scannd", C.c_int, [C.POINTER(ScanNDParams)])
+om_scannd_forward = _decl("om_scannd_forward", C.c_int, [C.POINTER(ScanNDParams)])
+mamba_scannd_cuda_forward = _decl("mamba_scannd_cuda_forward", C.c_int, [C.POINTER(ScanNDParams)])
+km_scannd_fwd_c = _decl("km_scannd_fwd", C.c_int, [C.POINTER(ScanNDParams), C.c_void_p])
+scan2d = _decl("scan2d", None, [C.POINTER(Scan2DParams)])
+mamba_scan2d_forward = _decl("mamba_scan2d_forward", None, [C.POINTER(Scan2DParams)])
+
+
+def scannd_params(dims, x, A, B, Cm, delta, h, y):
+    """ScanNDParams over buffers (torch device tensors or numpy arrays).
+    Returns (params, keepalive)."""
+    dd = longs(dims)
+    D, M = A.shape[-2], A.shape[-1]
+    p = ScanNDParams(C.cast(dd, c_long_p), len(dims), D, M, ptr(x), ptr(A), ptr(B), ptr(Cm),
+                     ptr(delta), ptr(h), ptr(y), None, None)
+    return p, dd
+
+
+def scannd_fwd(dims, x, A, B, Cm, delta, h, y, stream=None):
+    """km_scannd_fwd (scannd_ref semantics) on torch device tensors."""
+    p, keep = scannd_params(dims, x, A, B, Cm, delta, h, y)
+    check(km_scannd_fwd_c(C.byref(p), C.c_void_p(stream_handle(stream))), "km_scannd_fwd")
+    return keep

@@ -121,6 +121,13 @@ if ref is not None:
     _sig(ref, "wavefront_nd_level_size", C.c_long, [lp, C.c_long, C.c_long])
     _sig(ref, "kmr_test_scan1d_ref", None, [vp] * 7 + [C.c_long] * 3)
     _sig(ref, "kmr_test_scan1d_backward_forward_ref", None, [vp] * 7 + [C.c_long] * 3)
+    # The reference's scannd_ref shares one idx[] scratch array between the
+    # OpenMP threads of its level loop (src/scan_nd.c:44 allocates it once,
+    # every thread writes it at :89), so it races with more than one thread.
+    # Its other loops are deterministic either way. Run the reference with a
+    # single OpenMP thread; the oracle's own loops name num_threads explicitly.
+    ref.omp_set_num_threads.argtypes = [C.c_int]
+    ref.omp_set_num_threads(1)
 
 
 # ---------------------------------------------------------------------------
