@@ -241,7 +241,8 @@ def main():
                    "B": Bsz, "L": L, "D": D, "N": N},
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "scan1d_fwd_chunked<f32,8,2,8,8,shared,B*u kept>", "alg_bytes": alg,
+                     "kernel": "km::scan1d_fwd_chunked (fp32, B/C shared over channels)",
+                     "alg_bytes": alg,
                      "avg_launch_ms": round(ms, 5)},
         "cpu_baseline": cpu,
         "extra": extra,
