@@ -37,6 +37,42 @@ def scan1d_alg_bytes(Bsz, L, D, N, s):
     return 3 * Bsz * L * D * s + D * N * 4 + 2 * Bsz * L * N * s + Bsz * D * N * 4
 
 
+def scan1d_bwd_alg_bytes(Bsz, L, D, N, s):
+    """Algorithmic bytes of one Scan1D backward with shared B/C: x, delta, dy
+    read and dx, ddelta written [B,L,D] at s bytes; B, C read and dB, dC
+    written [B,L,N] at s bytes; A read and dA written [D,N] fp32. Saved
+    checkpoints and recomputation are overhead, not algorithmic bytes."""
+    return 5 * Bsz * L * D * s + 4 * Bsz * L * N * s + 2 * D * N * 4
+
+
+def bench_scan1d_bwd(torch, K, stream, Bsz, L, D, N, dtype, steps, warmup):
+    """configs[1] backward: the forward writes 64-step state checkpoints (not
+    timed here), the backward recomputes states from them; dy ~ N(0,1)."""
+    x, dt, A, Bm, Cm = make_inputs(torch, Bsz, L, D, N, dtype, seed=3)
+    g = torch.Generator(device="cuda").manual_seed(4)
+    dy = torch.randn((Bsz, L, D), device="cuda", generator=g).to(x.dtype)
+    nck = (L + K.KM_SCAN1D_CKPT_STEPS - 1) // K.KM_SCAN1D_CKPT_STEPS
+    ck = torch.empty((Bsz, nck, D, N), device="cuda")
+    y = torch.empty_like(x)
+    dx, ddt = torch.empty_like(x), torch.empty_like(x)
+    dA = torch.empty((D, N), device="cuda")
+    dB, dC = torch.empty_like(Bm), torch.empty_like(Cm)
+    fwd = lambda: K.scan1d_fwd(x, dt, A, Bm, Cm, y, h_ckpt=ck, stream=stream)  # noqa: E731
+    bwd = lambda: K.scan1d_bwd(x, dt, A, Bm, Cm, dy, dx, ddt, dA, dB, dC,  # noqa: E731
+                               h_ckpt=ck, stream=stream)
+    fwd()
+    per, _ = time_launches(torch, stream, bwd, steps, warmup)
+    perf, _ = time_launches(torch, stream, fwd, steps, warmup)
+    ms = sum(per) / len(per)
+    msf = sum(perf) / len(perf)
+    alg = scan1d_bwd_alg_bytes(Bsz, L, D, N, 2 if dtype == "bf16" else 4)
+    return {"bwd_ms": round(ms, 4), "bwd_elems_per_s": Bsz * L * D / (ms * 1e-3),
+            "bwd_alg_bytes": alg, "bwd_achieved_GBs": round(alg / (ms * 1e-3) / 1e9, 1),
+            "bwd_frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "fwd_with_ckpt_ms": round(msf, 4),
+            "fwd_plus_bwd_elems_per_s": Bsz * L * D / ((ms + msf) * 1e-3)}
+
+
 def scannd_alg_bytes(dims, D, M):
     """Algorithmic bytes of one ScanND forward: x [P,D], delta [nd,P,D],
     A [nd,D,M], B and C [P,D,M] read; h [P,D,M] and y [P,D] written (fp32)."""
@@ -132,7 +168,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["all", "scan1d", "scannd", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "scan1d", "scan1d_bwd", "scannd", "copy"],
+                    default="all",
                     help="profiling modes: scan1d = the fp32 headline kernel only; copy = a plain "
                          "1 GiB device copy (calibrates rocprof FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -155,6 +192,13 @@ def main():
         ms = sum(per) / len(per)
         print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n, "ms": ms,
                           "GBs_read_plus_write": 8 * n / (ms * 1e-3) / 1e9}))
+        return
+    if args.only == "scan1d_bwd":
+        with torch.cuda.stream(stream):
+            r = bench_scan1d_bwd(torch, K, stream, 8, 4096, 1024, 16, "f32", args.steps, args.warmup)
+            rb = bench_scan1d_bwd(torch, K, stream, 8, 4096, 1024, 16, "bf16", args.steps,
+                                  args.warmup)
+        print(json.dumps({"scan1d_bwd_f32": r, "scan1d_bwd_bf16": rb}))
         return
     if args.only == "scannd":
         with torch.cuda.stream(stream):
@@ -202,6 +246,10 @@ def main():
 
     with torch.cuda.stream(stream):
         del xb, dtb, Bb, Cb, yb
+        extra["scan1d_bwd_f32"] = bench_scan1d_bwd(torch, K, stream, Bsz, L, D, N, "f32",
+                                                   max(5, args.steps // 2), 2)
+        extra["scan1d_bwd_bf16"] = bench_scan1d_bwd(torch, K, stream, Bsz, L, D, N, "bf16",
+                                                    max(5, args.steps // 2), 2)
         extra["scannd_2d_256x256_D256_M16_f32"] = bench_scannd(torch, K, stream, (256, 256), 256, 16,
                                                                 max(5, args.steps // 2), 2)
         extra["scannd_3d_64cubed_D128_M16_f32"] = bench_scannd(torch, K, stream, (64, 64, 64), 128, 16,

@@ -47,6 +47,10 @@ typedef enum {
  * h0          : [B, D, N] fp32 initial state, NULL for zero
  * h_final     : [B, D, N] fp32 final state, may be NULL (may alias h0)
  * h_hist      : [B, L, D, N] fp32 state after every step, may be NULL
+ * h_ckpt      : [B, ceil(L/64), D, N] fp32 state after every 64th step (and
+ *               after the last step), may be NULL: the checkpoints the
+ *               backward recomputes states from
+ * y may be NULL when only states are wanted.
  * The +-1000 clamp is not associative; the kernel runs the unclamped
  * chunked scan and re-runs any (b, channel group) whose state left
  * [-1000, 1000] with the sequential clamped recurrence, so results follow the
@@ -65,7 +69,57 @@ typedef struct {
     long bc_sb, bc_st, bc_sd;
     int  dtype;
     int  clamp;
+    float       *h_ckpt;
 } KMScan1DFwd;
+
+#define KM_SCAN1D_CKPT_STEPS 64
+
+/* Batched, strided Scan1D backward: the adjoint of km_scan1d_fwd, per batch
+ * element the reference scan1d_backward (cpu/scan1d_backward.c:248-295):
+ *   ah = adj + dy*C;  dC = dy*h_t;  dB = ah*delta*x;  dA += ah*delta*e*h_{t-1}
+ *   dx = sum_n ah*delta*B;  ddelta = sum_n ah*(A*e*h_{t-1} + B*x);  adj = ah*e
+ * The forward clamp is not differentiated (as in the reference).
+ * Forward states come from h_hist when given, else from h_ckpt (written by
+ * km_scan1d_fwd) when given, else the library first recomputes checkpoints
+ * into the workspace. Inputs as in KMScan1DFwd, plus:
+ *   dy          : [B, L, D] dtype
+ *   dx, ddelta  : [B, L, D] dtype (written)
+ *   dA          : [D, N] fp32, summed over batch and time (written)
+ *   dB, dC      : dtype. Shared over channels (bc_sd == 0): the sum over
+ *                 channels, written at b*bc_sb + t*bc_st + n. Otherwise per
+ *                 channel at the B/C strides. Strides must not alias over
+ *                 batch or time (bc_sb, bc_st > 0 when B, L > 1).
+ *   clamp       : the forward's clamp flag (used when states are recomputed)
+ *   workspace   : device scratch of km_scan1d_bwd_workspace_bytes() bytes, or
+ *                 NULL for the library's per-device scratch (calls that
+ *                 overlap on one device then race: pass a workspace each).
+ * dA and the shared dB/dC are sums formed with fp32 atomics: the order of
+ * their terms, and so their last bits, may vary between runs. */
+typedef struct {
+    const void  *x;
+    const void  *delta;
+    const float *A;
+    const void  *Bm;
+    const void  *Cm;
+    const void  *dy;
+    const float *h0;
+    const float *h_hist;
+    const float *h_ckpt;
+    void        *dx;
+    void        *ddelta;
+    float       *dA;
+    void        *dB;
+    void        *dC;
+    long B, L, D, N;
+    long bc_sb, bc_st, bc_sd;
+    int  dtype;
+    int  clamp;
+    void        *workspace;
+    size_t       workspace_bytes;
+} KMScan1DBwd;
+
+size_t km_scan1d_bwd_workspace_bytes(const KMScan1DBwd *a);
+int km_scan1d_bwd(const KMScan1DBwd *a, void *stream);
 
 int km_scan1d_fwd(const KMScan1DFwd *a, void *stream);
 

@@ -8,6 +8,10 @@ namespace km {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Steps between the forward-state checkpoints the Scan1D backward recomputes
+// from (KM_SCAN1D_CKPT_STEPS of the public header).
+constexpr int kCkptSteps = 64;
+
 // Element type tags. Storage is fp32 or bfloat16; arithmetic is always fp32.
 struct f32_t  { using storage = float; };
 struct bf16_t { using storage = uint16_t; };

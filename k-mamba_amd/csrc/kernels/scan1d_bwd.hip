@@ -1,0 +1,975 @@
+// scan1d_bwd.hip - Scan1D selective-scan backward for gfx950.
+//
+// Adjoint of the forward recurrence in reverse time (reference
+// cpu/scan1d_backward.c:248-295, per batch element):
+//   e  = exp(delta*A[d,n]);  hp = state before step t;  ht = state after it
+//   ah = adj + dy*C                         (dL/dh_t)
+//   dC = dy*ht;  dB = ah*delta*x;  dA += ah*delta*e*hp
+//   dx = sum_n ah*delta*B;  ddelta = sum_n ah*(A*e*hp + B*x)
+//   adj = ah*e                              (handed to step t-1)
+// The per-step clamp of the forward is not differentiated (as in the
+// reference, which consumes the clamped states).
+//
+// Design (same lane layout as the forward kernel):
+//  * A wave covers DL = 64/NS channels x NS groups of NPL states; a workgroup
+//    of W waves owns one (batch, channel group) and walks the sequence
+//    backwards in super-chunks of W*TC = 64 steps, one wave per TC steps.
+//  * Forward states of a super-chunk are either read from the history or
+//    recomputed from the 64-step checkpoint the forward wrote: local pass
+//    from zero, chunk maps through LDS, fold, replay (as the forward).
+//  * The adjoint is the same linear recurrence run backwards with the same
+//    decays: g -> P*g + a over a wave's steps, so the chunk maps fold in
+//    reverse order and each wave replays its steps from the exact incoming
+//    adjoint, producing every gradient term in registers.
+//  * dx and ddelta reduce over the states of a channel across lanes; dA
+//    accumulates per lane over the sequence. Shared B/C ([B, L, N], stride 0
+//    over channels) need dB, dC summed over channels: a reduce-scatter over
+//    the wave's lanes, then one fp32 atomic per (step, state) and wave into a
+//    workspace accumulator that a finalize kernel converts to the output.
+//  * States recomputed from checkpoints run unclamped; if any leaves
+//    [-1000, 1000] the super-chunk is recomputed with the sequential clamped
+//    recurrence, which matches the forward's clamp fallback.
+#include "km_device.hpp"
+#include "../km_runtime.hpp"
+#include "kmamba_km.h"
+#include "scan.h"
+#include "mamba_scan.h"
+#include "mamba_scan_cuda.h"
+
+namespace km {
+
+int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream);
+
+struct Scan1DBwdArgs {
+    const void *x, *dt, *dy;
+    const float *A;
+    const void *Bm, *Cm;
+    const float *h0;       // [B, D, N] or null
+    const float *hist;     // [B, L, D, N] state after each step, or null
+    const float *ckpt;     // [B, nck, D, N] state after each 64-step block, or null
+    long nck;
+    void *dx, *ddt;        // [B, L, D]
+    float *dA;             // [D, N] fp32 accumulator (zeroed by the launcher)
+    float *accB, *accC;    // shared B/C: [B, L, N] fp32 accumulators (zeroed)
+    void *dB, *dC;         // per-channel B/C: written at the B/C strides
+    long B, L, D, N, sb, st, sd;
+    int clamp;
+};
+
+// v from the lane whose id differs in bit MASK: ds_swizzle inside 32-lane
+// halves, ds_bpermute across them.
+template <int MASK>
+__device__ __forceinline__ float xor_lane(float v) {
+    if constexpr (MASK >= 32) return __shfl_xor(v, 32);
+    else return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (MASK << 10)));
+}
+
+// One exchange of the reduce-scatter below: while CNT values remain, keep
+// half of them and add the partner's copy of that half; then butterfly.
+template <int MASK, int CNT, int NV>
+__device__ __forceinline__ void rs_step(float (&cur)[NV], int lane) {
+    if constexpr (MASK >= 1) {
+        if constexpr (CNT > 1) {
+            constexpr int H = CNT / 2;
+            const bool hi = (lane & MASK) != 0;
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                const float keep = hi ? cur[H + i] : cur[i];
+                const float send = hi ? cur[i] : cur[H + i];
+                cur[i] = keep + xor_lane<MASK>(send);
+            }
+            rs_step<MASK / 2, H>(cur, lane);
+        } else {
+            cur[0] += xor_lane<MASK>(cur[0]);
+            rs_step<MASK / 2, 1>(cur, lane);
+        }
+    }
+}
+
+// Sums v[0..NV) over the DLN lanes of a lane's group (lanes sharing
+// lane / DLN). Lane l ends with the total of value index (l % DLN) / (DLN / NV).
+template <int NV, int DLN>
+__device__ __forceinline__ float reduce_scatter(const float (&v)[NV], int lane) {
+    static_assert(NV <= DLN && DLN <= 64, "reduce over at most 64 lanes");
+    float cur[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) cur[i] = v[i];
+    rs_step<DLN / 2, NV>(cur, lane);
+    return cur[0];
+}
+
+template <int NPL, int NS>
+__device__ __forceinline__ void pow_chain_b(float e1, int n0, float (&e)[NPL]) {
+    float pw = e1;
+    if constexpr (NS > 1) {
+        float sq = e1;
+#pragma unroll
+        for (int k = 1; k < NPL; k <<= 1) sq *= sq;
+#pragma unroll
+        for (int bit = NPL; bit < NPL * NS; bit <<= 1) {
+            pw *= (n0 & bit) ? sq : 1.0f;
+            sq *= sq;
+        }
+    }
+    e[0] = pw;
+#pragma unroll
+    for (int j = 1; j < NPL; ++j) e[j] = e[j - 1] * e1;
+}
+
+template <typename T, int NPL, int NS, int W, int TC, bool SHARED, bool HIN, int OCC>
+__global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs p) {
+    using IO = bio<T>;
+    constexpr int DL = 64 / NS;
+    constexpr int N = NPL * NS;
+    constexpr int SC = W * TC;
+    static_assert(SC == kCkptSteps, "backward super-chunks follow the forward checkpoints");
+    constexpr int TILE = SC * N;
+    constexpr int NT = 64 * W;
+    constexpr int TPT = (TILE + NT - 1) / NT;
+    constexpr int TS = IO::size;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int dl = lane % DL;
+    const int ns = lane / DL;
+    const int n0 = ns * NPL;
+    const long ngroups = (p.D + DL - 1) / DL;
+    const long b = blockIdx.x / ngroups;
+    const long d = (blockIdx.x - b * ngroups) * DL + dl;
+    const bool dvalid = d < p.D;
+    const int dc = static_cast<int>(dvalid ? d : p.D - 1);
+    const int L = static_cast<int>(p.L);
+    const int Dm = static_cast<int>(p.D);
+    const int nit = (L + SC - 1) / SC;
+    const bool own_x = dvalid && ns == 0;
+
+    // Per-batch-element windows, 32-bit byte offsets in the VGPR offset (the
+    // launcher keeps them below 1 GiB): rows past L load 0, stores drop.
+    const long xoff = b * p.L * p.D;
+    const long xbytes = p.L * p.D * TS;
+    const auto rx = make_rsrc(static_cast<const char *>(p.x) + xoff * TS, xbytes);
+    const auto rdt = make_rsrc(static_cast<const char *>(p.dt) + xoff * TS, xbytes);
+    const auto rdy = make_rsrc(static_cast<const char *>(p.dy) + xoff * TS, xbytes);
+    const auto rdx = make_rsrc(static_cast<char *>(p.dx) + xoff * TS, xbytes);
+    const auto rdd = make_rsrc(static_cast<char *>(p.ddt) + xoff * TS, xbytes);
+    const long bcbytes = p.L * p.st * TS;
+    const auto rB = make_rsrc(static_cast<const char *>(p.Bm) + b * p.sb * TS, bcbytes);
+    const auto rC = make_rsrc(static_cast<const char *>(p.Cm) + b * p.sb * TS, bcbytes);
+    const auto rdB = make_rsrc(SHARED ? nullptr : static_cast<char *>(p.dB) + b * p.sb * TS,
+                               SHARED ? 0 : bcbytes);
+    const auto rdC = make_rsrc(SHARED ? nullptr : static_cast<char *>(p.dC) + b * p.sb * TS,
+                               SHARED ? 0 : bcbytes);
+    const auto rh = make_rsrc(HIN ? p.hist + xoff * p.N : nullptr, HIN ? p.L * p.D * p.N * 4 : 0);
+    const int vx = dc * TS;
+    const int rowx = Dm * TS;
+    const int rowbc = static_cast<int>(p.st) * TS;
+    const int vbc = SHARED ? 0 : (dc * static_cast<int>(p.sd) + n0) * TS;
+    const int vh = (dc * N + n0) * 4;
+    const int rowh = Dm * N * 4;
+
+    __shared__ float sB[SHARED ? 3 : 1][SHARED ? TILE : 1];
+    __shared__ float sC[SHARED ? 3 : 1][SHARED ? TILE : 1];
+    __shared__ float aggP[W][NPL][64];
+    __shared__ float aggH[W][NPL][64];
+    __shared__ float pin[W][NPL][64];       // incoming forward state, then incoming adjoint
+    __shared__ float acar[2][NPL][64];      // adjoint carried between super-chunks
+
+    float Ap[NPL], Ar[NPL];
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+        Ar[j] = p.A[dc * N + n0 + j];
+        Ap[j] = Ar[j] * kLog2e;
+    }
+    const float A0p = p.A[dc * N] * kLog2e;
+    bool structured = (n0 == 0 || (n0 & (n0 - 1)) == 0);
+#pragma unroll
+    for (int j = 0; j < NPL; ++j)
+        structured = structured && (Ar[j] == static_cast<float>(n0 + j + 1) * p.A[dc * N]);
+    const bool fast = __builtin_amdgcn_readfirstlane(__syncthreads_and(structured)) != 0;
+
+    if (w == 0) {
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) acar[0][j][lane] = 0.f;
+    }
+
+    float rb[TPT], rc[TPT];
+    auto load_tile = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < TPT; ++i) {
+            const int e = tid + i * NT;
+            const int t = s * SC + e / N;
+            const int off = (e % N) * TS;
+            rb[i] = (e < TILE) ? IO::ld(rB, off + t * rowbc, 0) : 0.f;
+            rc[i] = (e < TILE) ? IO::ld(rC, off + t * rowbc, 0) : 0.f;
+        }
+    };
+    auto store_tile = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < TPT; ++i) {
+            const int e = tid + i * NT;
+            if (e < TILE) {
+                sB[slot][e] = rb[i];
+                sC[slot][e] = rc[i];
+            }
+        }
+    };
+    auto load_xd = [&](int s, float (&xo)[TC], float (&dto)[TC], float (&go)[TC]) {
+#pragma unroll
+        for (int k = 0; k < TC; ++k) {
+            const int so = (s * SC + w * TC + k) * rowx;
+            xo[k] = IO::ld(rx, vx + so, 0);
+            dto[k] = IO::ld(rdt, vx + so, 0);
+            go[k] = IO::ld(rdy, vx + so, 0);
+        }
+    };
+    // B or C row of step t (t relative to the super-chunk: r = t - s*SC).
+    auto bc_row = [&](const float (*tile)[SHARED ? TILE : 1], __amdgpu_buffer_rsrc_t r, int slot,
+                      int s, int rr, float (&out)[NPL]) {
+        if constexpr (SHARED) {
+            const float *row = &tile[slot][rr * N + n0];
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) out[j] = row[j];
+        } else {
+            const int so = (s * SC + rr) * rowbc;
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) out[j] = IO::ld(r, vbc + j * TS + so, 0);
+        }
+    };
+    // State entering super-chunk s, state j of this lane's group.
+    auto h_start = [&](int s, int j) -> float {
+        if (s == 0) return p.h0 ? p.h0[(b * Dm + dc) * N + n0 + j] : 0.f;
+        return p.ckpt[((b * p.nck + (s - 1)) * Dm + dc) * N + n0 + j];
+    };
+
+    if constexpr (SHARED) {
+        load_tile(nit - 1);
+        store_tile(0);
+        if (nit > 1) load_tile(nit - 2);
+    }
+    float X0[TC], D0[TC], G0[TC], X1[TC], D1[TC], G1[TC];
+    load_xd(nit - 1, X0, D0, G0);
+    __syncthreads();
+
+    float dAacc[NPL];
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) dAacc[j] = 0.f;
+
+    auto body = [&](int it, float (&xs)[TC], float (&ds)[TC], float (&gs)[TC],
+                    float (&xn)[TC], float (&dn)[TC], float (&gn)[TC]) {
+        const int s = nit - 1 - it;
+        const int cur = it & 1;
+        const int slot = it % 3;
+        if constexpr (SHARED) {
+            if (s >= 1) {                // tile s-1 -> LDS (slot last read in it-2)
+                store_tile((it + 1) % 3);
+                if (s >= 2) load_tile(s - 2);
+            }
+        }
+        if (s >= 1) load_xd(s - 1, xn, dn, gn);
+
+        // ---- forward states of this wave's steps ---------------------------
+        float e[TC][NPL];
+        float hs[TC][NPL];
+        float hin[NPL];
+        float dsum = 0.f;
+#pragma unroll
+        for (int k = 0; k < TC; ++k) {
+            dsum += ds[k];
+            if (fast) {
+                pow_chain_b<NPL, NS>(exp2_fast(ds[k] * A0p), n0, e[k]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) e[k][j] = exp2_fast(ds[k] * Ap[j]);
+            }
+        }
+        float P[NPL];
+        if (fast) {
+            pow_chain_b<NPL, NS>(exp2_fast(dsum * A0p), n0, P);
+        } else {
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) P[j] = exp2_fast(Ap[j] * dsum);
+        }
+        const int t0 = s * SC + w * TC;
+        if constexpr (HIN) {
+#pragma unroll
+            for (int k = 0; k < TC; ++k) {
+#pragma unroll
+                for (int j = 0; j < NPL; ++j)
+                    hs[k][j] = bio<f32_t>::ld(rh, vh + j * 4 + (t0 + k) * rowh, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) {
+                if (t0 > 0) hin[j] = bio<f32_t>::ld(rh, vh + j * 4 + (t0 - 1) * rowh, 0);
+                else hin[j] = p.h0 ? p.h0[(b * Dm + dc) * N + n0 + j] : 0.f;
+            }
+        } else {
+            // Local pass from a zero state, chunk maps, fold from the
+            // checkpoint, replay.
+            float hl[NPL];
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) hl[j] = 0.f;
+#pragma unroll
+            for (int k = 0; k < TC; ++k) {
+                float bv[NPL];
+                bc_row(sB, rB, slot, s, w * TC + k, bv);
+                const float u = ds[k] * xs[k];
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) hl[j] = fmaf(e[k][j], hl[j], bv[j] * u);
+            }
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) {
+                aggP[w][j][lane] = P[j];
+                aggH[w][j][lane] = hl[j];
+            }
+            __syncthreads();
+            for (int j = w; j < NPL; j += W) {
+                float run = h_start(s, j);
+#pragma unroll
+                for (int v = 0; v < W; ++v) {
+                    pin[v][j][lane] = run;
+                    run = fmaf(aggP[v][j][lane], run, aggH[v][j][lane]);
+                }
+            }
+            __syncthreads();
+            float hmax = 0.f;
+            bool nan_seen = false;
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) hin[j] = pin[w][j][lane];
+#pragma unroll
+            for (int k = 0; k < TC; ++k) {
+                float bv[NPL];
+                bc_row(sB, rB, slot, s, w * TC + k, bv);
+                const float u = ds[k] * xs[k];
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) {
+                    const float prev = (k == 0) ? hin[j] : hs[k - 1][j];
+                    hs[k][j] = fmaf(e[k][j], prev, bv[j] * u);
+                    hmax = fmaxf(hmax, fabsf(hs[k][j]));
+                    nan_seen |= (hs[k][j] != hs[k][j]);
+                }
+            }
+            const int bad = p.clamp && (nan_seen || hmax > 1000.f);
+            if (__syncthreads_or(bad)) {
+                // Sequential clamped recurrence from the checkpoint, in the
+                // forward fallback's arithmetic order.
+                float h[NPL];
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) h[j] = h_start(s, j);
+                for (int r = 0; r < w * TC; ++r) {
+                    const int so = (s * SC + r) * rowx;
+                    const float xv = IO::ld(rx, vx + so, 0), dv = IO::ld(rdt, vx + so, 0);
+                    float bv[NPL];
+                    bc_row(sB, rB, slot, s, r, bv);
+#pragma unroll
+                    for (int j = 0; j < NPL; ++j) {
+                        const float ee = exp2_fast(dv * Ap[j]);
+                        float hn = __fadd_rn(__fmul_rn(ee, h[j]), __fmul_rn(__fmul_rn(bv[j], dv), xv));
+                        hn = (hn < 1000.f) ? hn : 1000.f;
+                        h[j] = (hn > -1000.f) ? hn : -1000.f;
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) hin[j] = h[j];
+#pragma unroll
+                for (int k = 0; k < TC; ++k) {
+                    float bv[NPL];
+                    bc_row(sB, rB, slot, s, w * TC + k, bv);
+#pragma unroll
+                    for (int j = 0; j < NPL; ++j) {
+                        const float ee = exp2_fast(ds[k] * Ap[j]);
+                        float hn = __fadd_rn(__fmul_rn(ee, h[j]),
+                                             __fmul_rn(__fmul_rn(bv[j], ds[k]), xs[k]));
+                        hn = (hn < 1000.f) ? hn : 1000.f;
+                        h[j] = (hn > -1000.f) ? hn : -1000.f;
+                        hs[k][j] = h[j];
+                    }
+                }
+            }
+        }
+
+        // ---- adjoint: local reverse pass, fold, replay with gradients ------
+        float g[NPL];
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) g[j] = 0.f;
+#pragma unroll
+        for (int k = TC - 1; k >= 0; --k) {
+            float cv[NPL];
+            bc_row(sC, rC, slot, s, w * TC + k, cv);
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) g[j] = fmaf(gs[k], cv[j], g[j]) * e[k][j];
+        }
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+            if constexpr (HIN) aggP[w][j][lane] = P[j];
+            aggH[w][j][lane] = g[j];
+        }
+        __syncthreads();
+        for (int j = w; j < NPL; j += W) {
+            float run = acar[cur][j][lane];
+#pragma unroll
+            for (int v = W - 1; v >= 0; --v) {
+                pin[v][j][lane] = run;
+                run = fmaf(aggP[v][j][lane], run, aggH[v][j][lane]);
+            }
+            acar[cur ^ 1][j][lane] = run;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) g[j] = pin[w][j][lane];
+
+#pragma unroll
+        for (int k = TC - 1; k >= 0; --k) {
+            const int t = t0 + k;
+            float bv[NPL], cv[NPL];
+            bc_row(sB, rB, slot, s, w * TC + k, bv);
+            bc_row(sC, rC, slot, s, w * TC + k, cv);
+            const float dtk = ds[k], xk = xs[k], gk = gs[k];
+            const float u = dtk * xk;
+            float sa = 0.f, sbv = 0.f;
+            float dBv[NPL], dCv[NPL];
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) {
+                const float ah = fmaf(gk, cv[j], g[j]);
+                const float hp = (k == 0) ? hin[j] : hs[k - 1][j];
+                const float ae = ah * e[k][j];
+                const float q = ae * hp;
+                dAacc[j] = fmaf(dtk, q, dAacc[j]);
+                sa = fmaf(Ar[j], q, sa);
+                sbv = fmaf(ah, bv[j], sbv);
+                // Lanes past D (clamped to channel D-1) add nothing to the
+                // channel sums.
+                dBv[j] = dvalid ? ah * u : 0.f;
+                dCv[j] = dvalid ? gk * hs[k][j] : 0.f;
+                g[j] = ae;
+            }
+            // Sum the state groups of the channel (lanes dl + DL*ns).
+            if constexpr (NS >= 4) {
+                sa += __shfl_xor(sa, 16);
+                sbv += __shfl_xor(sbv, 16);
+            }
+            if constexpr (NS >= 2) {
+                sa += __shfl_xor(sa, 32);
+                sbv += __shfl_xor(sbv, 32);
+            }
+            if (own_x) {
+                IO::st(rdx, vx + t * rowx, 0, dtk * sbv);
+                IO::st(rdd, vx + t * rowx, 0, fmaf(xk, sbv, sa));
+            }
+            if constexpr (SHARED) {
+                // Sum over the wave's channels; lane l then holds state
+                // n0 + (l % DL) / (DL / NPL) of step t.
+                const float rbv = reduce_scatter<NPL, DL>(dBv, lane);
+                const float rcv = reduce_scatter<NPL, DL>(dCv, lane);
+                constexpr int GRP = DL / NPL;
+                if ((dl % GRP) == 0 && t < L) {
+                    const long o = (b * p.L + t) * N + n0 + dl / GRP;
+                    unsafeAtomicAdd(p.accB + o, rbv);
+                    unsafeAtomicAdd(p.accC + o, rcv);
+                }
+            } else {
+                if (dvalid) {
+#pragma unroll
+                    for (int j = 0; j < NPL; ++j) {
+                        IO::st(rdB, vbc + j * TS + t * rowbc, 0, dBv[j]);
+                        IO::st(rdC, vbc + j * TS + t * rowbc, 0, dCv[j]);
+                    }
+                }
+            }
+        }
+    };
+
+    for (int it = 0; it < nit; it += 2) {
+        body(it, X0, D0, G0, X1, D1, G1);
+        if (it + 1 < nit) body(it + 1, X1, D1, G1, X0, D0, G0);
+    }
+
+    if (dvalid) {
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) unsafeAtomicAdd(p.dA + dc * N + n0 + j, dAacc[j]);
+    }
+}
+
+// Any N <= 64 (and windows too large for 32-bit offsets): one thread per
+// (batch, channel), the reference's reverse step order, states from the
+// history.
+template <typename T>
+__global__ void __launch_bounds__(256) scan1d_bwd_serial(Scan1DBwdArgs p) {
+    using IO = io<T>;
+    const long gid = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid >= p.B * p.D) return;
+    const long b = gid / p.D, d = gid % p.D;
+    const long N = p.N;
+    const bool shared = (p.sd == 0);
+    float adj[64], dAl[64];
+    for (long m = 0; m < N; ++m) {
+        adj[m] = 0.f;
+        dAl[m] = 0.f;
+    }
+    for (long t = p.L - 1; t >= 0; --t) {
+        const long td = (b * p.L + t) * p.D + d;
+        const float dt = IO::ld(p.dt, td), xt = IO::ld(p.x, td), gy = IO::ld(p.dy, td);
+        const long bc = b * p.sb + t * p.st + d * p.sd;
+        float dxv = 0.f, ddt = 0.f;
+        for (long m = 0; m < N; ++m) {
+            const float a = p.A[d * N + m];
+            const float bb = IO::ld(p.Bm, bc + m), c = IO::ld(p.Cm, bc + m);
+            const float e = exp2_fast(dt * a * kLog2e);
+            float hp = 0.f;
+            if (t > 0) hp = p.hist[(td - p.D) * N + m];
+            else if (p.h0) hp = p.h0[(b * p.D + d) * N + m];
+            const float ah = adj[m] + gy * c;
+            const float dCv = gy * p.hist[td * N + m];
+            const float dBv = ah * dt * xt;
+            dAl[m] += ah * dt * e * hp;
+            dxv += ah * dt * bb;
+            ddt += ah * (a * e * hp + bb * xt);
+            adj[m] = ah * e;
+            if (shared) {
+                const long o = (b * p.L + t) * N + m;
+                unsafeAtomicAdd(p.accB + o, dBv);
+                unsafeAtomicAdd(p.accC + o, dCv);
+            } else {
+                IO::st(p.dB, bc + m, dBv);
+                IO::st(p.dC, bc + m, dCv);
+            }
+        }
+        IO::st(p.dx, td, dxv);
+        IO::st(p.ddt, td, ddt);
+    }
+    for (long m = 0; m < N; ++m) unsafeAtomicAdd(p.dA + d * N + m, dAl[m]);
+}
+
+__global__ void __launch_bounds__(256) fill_zero_kernel(float *p, long n) {
+    for (long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<long>(gridDim.x) * blockDim.x)
+        p[i] = 0.f;
+}
+
+// Shared B/C: accumulators [B, L, N] -> outputs at b*sb + t*st + n.
+template <typename T>
+__global__ void __launch_bounds__(256) scan1d_bwd_finalize(const float *accB, const float *accC,
+                                                           void *dB, void *dC, long B, long L,
+                                                           long N, long sb, long st) {
+    using IO = io<T>;
+    const long n_all = B * L * N;
+    for (long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_all;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        const long b = i / (L * N), r = i - b * L * N, t = r / N, n = r - t * N;
+        const long o = b * sb + t * st + n;
+        IO::st(dB, o, accB[i]);
+        IO::st(dC, o, accC[i]);
+    }
+}
+
+static int fill_zero(float *p, long n, hipStream_t s) {
+    if (n <= 0) return 0;
+    const long blocks = std::min<long>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, s, p, n);
+    KM_HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+struct BwdPlan {
+    bool shared, hist_in, need_ckpt, serial, need_hist;
+    size_t off_acc, off_ckpt, off_hist, bytes;
+};
+
+static BwdPlan bwd_plan(const KMScan1DBwd *k) {
+    BwdPlan pl{};
+    pl.shared = (k->bc_sd == 0);
+    const long es = (k->dtype == KM_BF16) ? 2 : 4;
+    const long lim = 0x3fffffffL;
+    const bool small_windows = k->L * k->D * es < lim && k->L * k->bc_st * es < lim &&
+                               (!k->h_hist || k->L * k->D * k->N * 4 < lim);
+    const bool chunk_n = (k->N == 16 || k->N == 8 || k->N == 4 || k->N == 2 || k->N == 1);
+    pl.serial = !(small_windows && chunk_n);
+    pl.hist_in = (k->h_hist != nullptr);
+    pl.need_hist = pl.serial && !pl.hist_in;
+    pl.need_ckpt = !pl.serial && !pl.hist_in && !k->h_ckpt;
+    size_t off = 0;
+    pl.off_acc = off;
+    if (pl.shared) off += align_up(sizeof(float) * 2 * k->B * k->L * k->N, 256);
+    pl.off_ckpt = off;
+    if (pl.need_ckpt)
+        off += align_up(sizeof(float) * k->B * ((k->L + kCkptSteps - 1) / kCkptSteps) * k->D * k->N, 256);
+    pl.off_hist = off;
+    if (pl.need_hist) off += align_up(sizeof(float) * k->B * k->L * k->D * k->N, 256);
+    pl.bytes = off;
+    return pl;
+}
+
+static bool bwd_args_ok(const KMScan1DBwd *k, const char *who) {
+    if (!k) { set_error("%s: NULL arguments", who); return false; }
+    if (!k->x || !k->delta || !k->A || !k->Bm || !k->Cm || !k->dy || !k->dx || !k->ddelta ||
+        !k->dA || !k->dB || !k->dC) {
+        set_error("%s: NULL tensor pointer", who);
+        return false;
+    }
+    if (k->B <= 0 || k->L < 0 || k->D <= 0 || k->N <= 0 || k->N > 64) {
+        set_error("%s: invalid sizes B=%ld L=%ld D=%ld N=%ld (need N <= 64)", who, k->B, k->L,
+                  k->D, k->N);
+        return false;
+    }
+    if (k->dtype != KM_F32 && k->dtype != KM_BF16) {
+        set_error("%s: unknown dtype %d", who, k->dtype);
+        return false;
+    }
+    if (k->bc_sb < 0 || k->bc_st < 0 || k->bc_sd < 0 ||
+        (k->B > 1 && k->bc_sb == 0) || (k->L > 1 && k->bc_st == 0)) {
+        set_error("%s: B/C strides must be non-negative and distinct over batch and time "
+                  "(sb=%ld st=%ld sd=%ld)", who, k->bc_sb, k->bc_st, k->bc_sd);
+        return false;
+    }
+    return true;
+}
+
+static int bwd_chunked_launch(const Scan1DBwdArgs &a, bool shared, bool hin, bool bf,
+                              hipStream_t s) {
+    constexpr int W = 8, TC = 8;
+    // Four states per lane keep the backward's per-lane working set (decays
+    // and states of 8 steps) within 256 VGPRs without spilling.
+    long DL = 64;
+    if (a.N == 16) DL = 16;
+    else if (a.N == 8) DL = 32;
+    const long grid = a.B * ((a.D + DL - 1) / DL);
+    if (grid <= 0 || grid > 0x7fffffffL) {
+        set_error("km_scan1d_bwd: grid of %ld workgroups out of range", grid);
+        return -1;
+    }
+    dim3 g(static_cast<unsigned>(grid)), blk(64 * W);
+#define KM_BWD_GO(TT, NPL, NS)                                                                    \
+    do {                                                                                          \
+        if (shared) {                                                                             \
+            if (hin) hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, W, TC, true, true, 1>), g, blk, 0, s, a);   \
+            else     hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, W, TC, true, false, 1>), g, blk, 0, s, a);  \
+        } else {                                                                                  \
+            if (hin) hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, W, TC, false, true, 1>), g, blk, 0, s, a);  \
+            else     hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, W, TC, false, false, 1>), g, blk, 0, s, a); \
+        }                                                                                         \
+    } while (0)
+    switch (a.N) {
+    case 16: if (bf) KM_BWD_GO(bf16_t, 4, 4); else KM_BWD_GO(f32_t, 4, 4); break;
+    case 8:  if (bf) KM_BWD_GO(bf16_t, 4, 2); else KM_BWD_GO(f32_t, 4, 2); break;
+    case 4:  if (bf) KM_BWD_GO(bf16_t, 4, 1); else KM_BWD_GO(f32_t, 4, 1); break;
+    case 2:  if (bf) KM_BWD_GO(bf16_t, 2, 1); else KM_BWD_GO(f32_t, 2, 1); break;
+    case 1:  if (bf) KM_BWD_GO(bf16_t, 1, 1); else KM_BWD_GO(f32_t, 1, 1); break;
+    default:
+        set_error("km_scan1d_bwd: no register-blocked kernel for N=%ld", a.N);
+        return -1;
+    }
+#undef KM_BWD_GO
+    KM_HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+size_t scan1d_bwd_workspace(const KMScan1DBwd *k) {
+    if (!bwd_args_ok(k, "km_scan1d_bwd_workspace_bytes")) return 0;
+    return bwd_plan(k).bytes;
+}
+
+int scan1d_bwd_launch(const KMScan1DBwd *k, hipStream_t stream) {
+    if (!bwd_args_ok(k, "km_scan1d_bwd")) return -1;
+    if (!gpu_ready()) return -1;
+    const BwdPlan pl = bwd_plan(k);
+    const bool bf = (k->dtype == KM_BF16);
+    if (fill_zero(k->dA, k->D * k->N, stream) != 0) return -1;
+    if (k->L == 0) return 0;
+    char *ws = nullptr;
+    if (pl.bytes > 0) {
+        if (k->workspace) {
+            if (k->workspace_bytes < pl.bytes) {
+                set_error("km_scan1d_bwd: workspace of %zu bytes, %zu needed", k->workspace_bytes,
+                          pl.bytes);
+                return -1;
+            }
+            ws = static_cast<char *>(k->workspace);
+        } else {
+            ws = static_cast<char *>(Workspace::reserve(pl.bytes));
+            if (!ws) return -1;
+        }
+    }
+    Scan1DBwdArgs a{};
+    a.x = k->x; a.dt = k->delta; a.dy = k->dy; a.A = k->A; a.Bm = k->Bm; a.Cm = k->Cm;
+    a.h0 = k->h0; a.hist = k->h_hist; a.ckpt = k->h_ckpt;
+    a.nck = (k->L + kCkptSteps - 1) / kCkptSteps;
+    a.dx = k->dx; a.ddt = k->ddelta; a.dA = k->dA; a.dB = k->dB; a.dC = k->dC;
+    a.B = k->B; a.L = k->L; a.D = k->D; a.N = k->N;
+    a.sb = k->bc_sb; a.st = k->bc_st; a.sd = k->bc_sd; a.clamp = k->clamp;
+    if (pl.shared) {
+        a.accB = reinterpret_cast<float *>(ws + pl.off_acc);
+        a.accC = a.accB + k->B * k->L * k->N;
+        if (fill_zero(a.accB, 2 * k->B * k->L * k->N, stream) != 0) return -1;
+    }
+    if (pl.need_ckpt || pl.need_hist) {
+        // Forward states from the same inputs (y not written).
+        KMScan1DFwd f{};
+        f.x = k->x; f.delta = k->delta; f.A = k->A; f.Bm = k->Bm; f.Cm = k->Cm; f.y = nullptr;
+        f.h0 = k->h0; f.B = k->B; f.L = k->L; f.D = k->D; f.N = k->N;
+        f.bc_sb = k->bc_sb; f.bc_st = k->bc_st; f.bc_sd = k->bc_sd;
+        f.dtype = k->dtype; f.clamp = k->clamp;
+        if (pl.need_ckpt) {
+            f.h_ckpt = reinterpret_cast<float *>(ws + pl.off_ckpt);
+            a.ckpt = f.h_ckpt;
+        } else {
+            f.h_hist = reinterpret_cast<float *>(ws + pl.off_hist);
+            a.hist = f.h_hist;
+        }
+        if (scan1d_fwd_launch(&f, stream) != 0) return -1;
+    }
+    if (pl.serial) {
+        const long threads = k->B * k->D;
+        const long grid = (threads + 255) / 256;
+        if (bf) hipLaunchKernelGGL(scan1d_bwd_serial<bf16_t>, dim3(grid), dim3(256), 0, stream, a);
+        else    hipLaunchKernelGGL(scan1d_bwd_serial<f32_t>, dim3(grid), dim3(256), 0, stream, a);
+        KM_HIP_TRY(hipGetLastError());
+    } else if (bwd_chunked_launch(a, pl.shared, a.hist != nullptr, bf, stream) != 0) {
+        return -1;
+    }
+    if (pl.shared) {
+        const long n = k->B * k->L * k->N;
+        const long blocks = std::min<long>((n + 255) / 256, 8192);
+        if (bf) hipLaunchKernelGGL(scan1d_bwd_finalize<bf16_t>, dim3(blocks), dim3(256), 0, stream,
+                                   a.accB, a.accC, k->dB, k->dC, k->B, k->L, k->N, k->bc_sb, k->bc_st);
+        else    hipLaunchKernelGGL(scan1d_bwd_finalize<f32_t>, dim3(blocks), dim3(256), 0, stream,
+                                   a.accB, a.accC, k->dB, k->dC, k->B, k->L, k->N, k->bc_sb, k->bc_st);
+        KM_HIP_TRY(hipGetLastError());
+    }
+    return 0;
+}
+
+}  // namespace km
+
+namespace km {
+
+struct M1Args {
+    const float *x, *A, *Adiag, *B, *C, *delta, *h0, *h, *dy;
+    float *dx, *dA, *dB, *dC, *ddelta;
+    long L, D;
+};
+
+// M = 1 with B, C shared over time ([D]) and delta shared over channels
+// ([L]) (reference cpu/scan1d_backward.c:23-70): one thread per channel in
+// reverse time; ddelta[t] sums the channels' terms (block sum, one atomic
+// per block and step).
+__global__ void __launch_bounds__(256) scan1d_bwd_m1_shared(M1Args p) {
+    __shared__ float part[4];
+    const int tid = threadIdx.x;
+    const long d = static_cast<long>(blockIdx.x) * 256 + tid;
+    const bool ok = d < p.D;
+    const long dc = ok ? d : p.D - 1;
+    const float a = p.A[dc], bb = p.B[dc], c = p.C[dc];
+    float adj = 0.f, dAl = 0.f, dBl = 0.f, dCl = 0.f;
+    for (long t = p.L - 1; t >= 0; --t) {
+        const long td = t * p.D + dc;
+        const float dt = p.delta[t];
+        const float xt = p.x[td], gy = p.dy[td];
+        const float e = p.Adiag ? p.Adiag[td] : exp2_fast(dt * a * kLog2e);
+        const float hp = (t > 0) ? p.h[td - p.D] : (p.h0 ? p.h0[dc] : 0.f);
+        const float ah = adj + gy * c;
+        dCl += gy * p.h[td];
+        dBl += ah * dt * xt;
+        dAl += ah * dt * e * hp;
+        if (ok) p.dx[td] = ah * dt * bb;
+        float term = ok ? ah * (a * e * hp + bb * xt) : 0.f;
+        adj = ah * e;
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) term += __shfl_xor(term, m);
+        if ((tid & 63) == 0) part[tid >> 6] = term;
+        __syncthreads();
+        if (tid == 0) unsafeAtomicAdd(p.ddelta + t, part[0] + part[1] + part[2] + part[3]);
+        __syncthreads();
+    }
+    if (ok) {
+        p.dA[d] = dAl;
+        p.dB[d] = dBl;
+        p.dC[d] = dCl;
+    }
+}
+
+static int m1_launch(const M1Args &a, hipStream_t s) {
+    if (fill_zero(a.ddelta, a.L, s) != 0) return -1;
+    const long grid = (a.D + 255) / 256;
+    hipLaunchKernelGGL(scan1d_bwd_m1_shared, dim3(grid), dim3(256), 0, s, a);
+    KM_HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+// Host-or-device buffers of one host-pointer call: device pointers pass
+// through, host buffers are staged (inputs copied in, outputs copied back).
+struct StagedCall {
+    struct Buf { const void *user; void *dev; size_t bytes; bool out; };
+    Buf bufs[24];
+    int n = 0;
+    bool all_dev = true;
+    void add(const void *user, size_t bytes, bool out) {
+        bufs[n++] = Buf{user, const_cast<void *>(user), bytes, out};
+        if (user && !is_device_ptr(user)) all_dev = false;
+    }
+    // Reserves staging and copies inputs; false on failure (error set).
+    bool stage_in(const char *who) {
+        if (all_dev) return true;
+        size_t total = 0;
+        for (int i = 0; i < n; ++i) if (bufs[i].user) total += align_up(bufs[i].bytes, 256);
+        void *base = Staging::reserve(total);
+        if (!base) return false;
+        Carver c(base);
+        for (int i = 0; i < n; ++i) {
+            if (!bufs[i].user) continue;
+            bufs[i].dev = c.take<char>(bufs[i].bytes);
+            if (!bufs[i].out &&
+                hipMemcpy(bufs[i].dev, bufs[i].user, bufs[i].bytes, hipMemcpyHostToDevice) != hipSuccess) {
+                set_error("%s: host-to-device copy failed", who);
+                return false;
+            }
+        }
+        return true;
+    }
+    bool stage_out(const char *who) {
+        if (hipStreamSynchronize(nullptr) != hipSuccess) {
+            set_error("%s: %s", who, hipGetErrorString(hipGetLastError()));
+            return false;
+        }
+        if (all_dev) return true;
+        for (int i = 0; i < n; ++i) {
+            if (!bufs[i].user || !bufs[i].out) continue;
+            if (hipMemcpy(const_cast<void *>(bufs[i].user), bufs[i].dev, bufs[i].bytes,
+                          hipMemcpyDeviceToHost) != hipSuccess) {
+                set_error("%s: device-to-host copy failed", who);
+                return false;
+            }
+        }
+        return true;
+    }
+    template <typename P> P *dev(int i) { return static_cast<P *>(bufs[i].dev); }
+};
+
+}  // namespace km
+
+extern "C" {
+
+size_t km_scan1d_bwd_workspace_bytes(const KMScan1DBwd *a) {
+    km::clear_error();
+    return km::scan1d_bwd_workspace(a);
+}
+
+int km_scan1d_bwd(const KMScan1DBwd *a, void *stream) {
+    km::clear_error();
+    return km::scan1d_bwd_launch(a, static_cast<hipStream_t>(stream));
+}
+
+// Reference cuda/scan1d_backward.cu:113-137: device pointers, B, C, h
+// [L, D, M] (h = forward state history), zero initial state; synchronous.
+void om_scan1d_backward(const float *d_dy, const float *d_x, const float *d_A, const float *d_B,
+                        const float *d_C, const float *d_dt, const float *d_h, float *d_dx,
+                        float *d_dA, float *d_dB, float *d_dC, float *d_ddt, int L, int D, int M) {
+    km::clear_error();
+    if (L < 0 || D <= 0 || M <= 0) {
+        km::set_error("om_scan1d_backward: invalid sizes L=%d D=%d M=%d", L, D, M);
+        return;
+    }
+    KMScan1DBwd a{};
+    a.x = d_x; a.delta = d_dt; a.A = d_A; a.Bm = d_B; a.Cm = d_C; a.dy = d_dy;
+    a.h_hist = d_h; a.dx = d_dx; a.ddelta = d_ddt; a.dA = d_dA; a.dB = d_dB; a.dC = d_dC;
+    a.B = 1; a.L = L; a.D = D; a.N = M;
+    a.bc_sb = static_cast<long>(L) * D * M; a.bc_st = static_cast<long>(D) * M; a.bc_sd = M;
+    a.dtype = KM_F32; a.clamp = 1;
+    if (km::scan1d_bwd_launch(&a, nullptr) != 0) return;
+    if (hipStreamSynchronize(nullptr) != hipSuccess)
+        km::set_error("om_scan1d_backward: %s", hipGetErrorString(hipGetLastError()));
+}
+
+void mamba_scan1d_cuda_backward(const float *d_dy, const float *d_x, const float *d_A,
+                                const float *d_B, const float *d_C, const float *d_dt,
+                                const float *d_h, float *d_dx, float *d_dA, float *d_dB,
+                                float *d_dC, float *d_ddt, int L, int D, int M) {
+    om_scan1d_backward(d_dy, d_x, d_A, d_B, d_C, d_dt, d_h, d_dx, d_dA, d_dB, d_dC, d_ddt, L, D, M);
+}
+
+// Reference scan1d_backward (cpu/scan1d_backward.c:297-306): host or device
+// pointers; B, C, h, dB, dC [L, D, M]; h = forward history; h0 [D, M] or
+// NULL; every output is overwritten.
+void scan1d_backward(ScanBackwardParams *p) {
+    km::clear_error();
+    if (!p || !p->x || !p->A || !p->B || !p->C || !p->delta || !p->h || !p->dy || !p->dx ||
+        !p->dA || !p->dB || !p->dC || !p->ddelta || p->L <= 0 || p->D <= 0 || p->M <= 0) {
+        km::set_error("scan1d_backward: invalid parameters");
+        return;
+    }
+    if (!km::gpu_ready()) return;
+    const size_t LD = p->L * p->D * 4, DM = p->D * p->M * 4, LDM = p->L * p->D * p->M * 4;
+    km::Staging::lock();
+    km::StagedCall sc;
+    sc.add(p->x, LD, false);      // 0
+    sc.add(p->A, DM, false);      // 1
+    sc.add(p->B, LDM, false);     // 2
+    sc.add(p->C, LDM, false);     // 3
+    sc.add(p->delta, LD, false);  // 4
+    sc.add(p->h0, DM, false);     // 5
+    sc.add(p->h, LDM, false);     // 6
+    sc.add(p->dy, LD, false);     // 7
+    sc.add(p->dx, LD, true);      // 8
+    sc.add(p->dA, DM, true);      // 9
+    sc.add(p->dB, LDM, true);     // 10
+    sc.add(p->dC, LDM, true);     // 11
+    sc.add(p->ddelta, LD, true);  // 12
+    if (sc.stage_in("scan1d_backward")) {
+        KMScan1DBwd a{};
+        a.x = sc.dev<float>(0); a.A = sc.dev<float>(1); a.Bm = sc.dev<float>(2);
+        a.Cm = sc.dev<float>(3); a.delta = sc.dev<float>(4); a.h0 = sc.dev<float>(5);
+        a.h_hist = sc.dev<float>(6); a.dy = sc.dev<float>(7); a.dx = sc.dev<float>(8);
+        a.dA = sc.dev<float>(9); a.dB = sc.dev<float>(10); a.dC = sc.dev<float>(11);
+        a.ddelta = sc.dev<float>(12);
+        a.B = 1; a.L = p->L; a.D = p->D; a.N = p->M;
+        a.bc_sb = p->L * p->D * p->M; a.bc_st = p->D * p->M; a.bc_sd = p->M;
+        a.dtype = KM_F32; a.clamp = 1;
+        if (km::scan1d_bwd_launch(&a, nullptr) == 0) sc.stage_out("scan1d_backward");
+    }
+    km::Staging::unlock();
+}
+
+void mamba_scan1d_backward(MambaScan1DBackwardParams *p) { scan1d_backward(p); }
+
+// Reference scan1d_backward_m1_shared_bc (cpu/scan1d_backward.c:17-191):
+// M = 1; B, C, dA, dB, dC [D]; delta, ddelta [L]; x, h, dy, dx [L, D];
+// A_diag [L, D] precomputed decays or NULL; h0 [D] or NULL.
+void scan1d_backward_m1_shared_bc(ScanBackwardSharedParams *p) {
+    km::clear_error();
+    if (!p || !p->x || !p->A || !p->B || !p->C || !p->delta || !p->h || !p->dy || !p->dx ||
+        !p->dA || !p->dB || !p->dC || !p->ddelta || p->L <= 0 || p->D <= 0) {
+        km::set_error("scan1d_backward_m1_shared_bc: invalid parameters");
+        return;
+    }
+    if (!km::gpu_ready()) return;
+    const size_t LD = p->L * p->D * 4, D4 = p->D * 4, L4 = p->L * 4;
+    km::Staging::lock();
+    km::StagedCall sc;
+    sc.add(p->x, LD, false);       // 0
+    sc.add(p->A, D4, false);       // 1
+    sc.add(p->A_diag, LD, false);  // 2
+    sc.add(p->B, D4, false);       // 3
+    sc.add(p->C, D4, false);       // 4
+    sc.add(p->delta, L4, false);   // 5
+    sc.add(p->h0, D4, false);      // 6
+    sc.add(p->h, LD, false);       // 7
+    sc.add(p->dy, LD, false);      // 8
+    sc.add(p->dx, LD, true);       // 9
+    sc.add(p->dA, D4, true);       // 10
+    sc.add(p->dB, D4, true);       // 11
+    sc.add(p->dC, D4, true);       // 12
+    sc.add(p->ddelta, L4, true);   // 13
+    if (sc.stage_in("scan1d_backward_m1_shared_bc")) {
+        km::M1Args a{sc.dev<float>(0), sc.dev<float>(1), sc.dev<float>(2), sc.dev<float>(3),
+                     sc.dev<float>(4), sc.dev<float>(5), sc.dev<float>(6), sc.dev<float>(7),
+                     sc.dev<float>(8), sc.dev<float>(9), sc.dev<float>(10), sc.dev<float>(11),
+                     sc.dev<float>(12), sc.dev<float>(13), p->L, p->D};
+        if (km::m1_launch(a, nullptr) == 0) sc.stage_out("scan1d_backward_m1_shared_bc");
+    }
+    km::Staging::unlock();
+}
+
+void mamba_scan1d_backward_m1_shared_bc(MambaScan1DBackwardM1Params *p) {
+    scan1d_backward_m1_shared_bc(p);
+}
+
+}  // extern "C"

@@ -45,6 +45,8 @@ struct Scan1DFwdArgs {
     const float *h0;
     float *hfin;
     float *hist;
+    float *ckpt;     // [B, nck, D, N] state after every kCkptSteps steps, or null
+    long nck;
     long B, L, D, N;
     long sb, st, sd;
     int clamp;
@@ -80,7 +82,12 @@ __device__ void scan1d_serial_wave(const Scan1DFwdArgs &p, long b, long d, bool 
         if (NS >= 4) yp += __shfl_xor(yp, 16);
         if (NS >= 2) yp += __shfl_xor(yp, 32);
         if (dvalid) {
-            if (n0 == 0) IO::st(p.y, xi, yp);
+            if (n0 == 0 && p.y) IO::st(p.y, xi, yp);
+            if (p.ckpt && ((t + 1) % kCkptSteps == 0 || t == p.L - 1)) {
+#pragma unroll
+                for (int j = 0; j < NPL; ++j)
+                    p.ckpt[((b * p.nck + t / kCkptSteps) * p.D + d) * N + n0 + j] = hs[j];
+            }
             if (HIST) {
 #pragma unroll
                 for (int j = 0; j < NPL; ++j) p.hist[xi * N + n0 + j] = hs[j];
@@ -151,7 +158,9 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     const long xoff = b * p.L * p.D;
     const auto rx = make_rsrc(static_cast<const char *>(p.x) + xoff * TS, p.L * p.D * TS);
     const auto rdt = make_rsrc(static_cast<const char *>(p.dt) + xoff * TS, p.L * p.D * TS);
-    const auto ry = make_rsrc(static_cast<char *>(p.y) + xoff * TS, p.L * p.D * TS);
+    // y may be null (checkpoint-only forward): a zero-sized window drops the stores.
+    const auto ry = make_rsrc(p.y ? static_cast<char *>(p.y) + xoff * TS : nullptr,
+                              p.y ? p.L * p.D * TS : 0);
     const auto rB = make_rsrc(static_cast<const char *>(p.Bm) + b * p.sb * TS, p.L * p.st * TS);
     const auto rC = make_rsrc(static_cast<const char *>(p.Cm) + b * p.sb * TS, p.L * p.st * TS);
     const auto rh = make_rsrc(p.hist ? p.hist + xoff * p.N : nullptr, HIST ? p.L * p.D * p.N * 4 : 0);
@@ -319,6 +328,9 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
                 run = fmaf(pv[v], run, hv[v]);
             }
             carry[cur ^ 1][j][lane] = run;
+            if constexpr (SC == kCkptSteps) {
+                if (p.ckpt && dvalid) p.ckpt[((b * p.nck + s) * Dm + d) * N + n0 + j] = run;
+            }
         }
         __syncthreads();
 #pragma unroll
@@ -409,9 +421,11 @@ __global__ void __launch_bounds__(256) scan1d_fwd_serial(Scan1DFwdArgs p) {
             }
             st[m] = hn;
             if (HIST) p.hist[xi * N + m] = hn;
+            if (p.ckpt && ((t + 1) % kCkptSteps == 0 || t == p.L - 1))
+                p.ckpt[((b * p.nck + t / kCkptSteps) * p.D + d) * N + m] = hn;
             y = __fadd_rn(y, __fmul_rn(IO::ld(p.Cm, bc + m), hn));
         }
-        IO::st(p.y, xi, y);
+        if (p.y) IO::st(p.y, xi, y);
     }
     if (p.hfin)
         for (long m = 0; m < N; ++m) p.hfin[(b * p.D + d) * N + m] = st[m];
@@ -453,6 +467,8 @@ static int scan1d_cfg16() {
 
 template <typename T>
 static int launch_n16(const Scan1DFwdArgs &a, bool shared, bool hist, hipStream_t s) {
+    // Checkpoints are written at super-chunk ends: keep 64-step super-chunks.
+    if (a.ckpt) return launch_chunked<T, 8, 2, 8, 8, true>(a, shared, hist, s);
     switch (scan1d_cfg16()) {
     case 0: return launch_chunked<T, 8, 2, 8, 8>(a, shared, hist, s);
     case 2: return launch_chunked<T, 4, 4, 8, 16>(a, shared, hist, s);
@@ -481,8 +497,12 @@ static int launch_serial(const Scan1DFwdArgs &a, bool hist, hipStream_t s) {
 
 int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream) {
     if (!k) { set_error("km_scan1d_fwd: NULL arguments"); return -1; }
-    if (!k->x || !k->delta || !k->A || !k->Bm || !k->Cm || !k->y) {
+    if (!k->x || !k->delta || !k->A || !k->Bm || !k->Cm) {
         set_error("km_scan1d_fwd: NULL tensor pointer");
+        return -1;
+    }
+    if (!k->y && !k->h_final && !k->h_hist && !k->h_ckpt) {
+        set_error("km_scan1d_fwd: no output requested");
         return -1;
     }
     if (k->B <= 0 || k->L < 0 || k->D <= 0 || k->N <= 0 || k->N > 64) {
@@ -495,7 +515,7 @@ int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream) {
         return -1;
     }
     if (!gpu_ready()) return -1;
-    if (k->L == 0) {   // no steps: the final state is the initial state
+    if (k->L == 0) {   // no steps: the final state is the initial state (no checkpoints)
         if (k->h_final && k->h_final != k->h0) {
             const size_t bytes = sizeof(float) * k->B * k->D * k->N;
             if (k->h0) KM_HIP_TRY(hipMemcpyAsync(k->h_final, k->h0, bytes, hipMemcpyDeviceToDevice, stream));
@@ -504,6 +524,7 @@ int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream) {
         return 0;
     }
     Scan1DFwdArgs a{k->x, k->delta, k->A, k->Bm, k->Cm, k->y, k->h0, k->h_final, k->h_hist,
+                    k->h_ckpt, (k->L + kCkptSteps - 1) / kCkptSteps,
                     k->B, k->L, k->D, k->N, k->bc_sb, k->bc_st, k->bc_sd, k->clamp};
     // The register-blocked kernel addresses each batch element's windows with
     // 32-bit byte offsets; larger problems take the sequential kernel.
@@ -528,10 +549,12 @@ int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream) {
         if (!bf) return launch_chunked<f32_t, 4, 1, 8, 8>(a, shared, hist, stream);
         break;
     case 2:
-        if (!bf) return launch_chunked<f32_t, 2, 1, 8, 16>(a, shared, hist, stream);
+        if (!bf) return k->h_ckpt ? launch_chunked<f32_t, 2, 1, 8, 8>(a, shared, hist, stream)
+                                  : launch_chunked<f32_t, 2, 1, 8, 16>(a, shared, hist, stream);
         break;
     case 1:
-        if (!bf) return launch_chunked<f32_t, 1, 1, 8, 16>(a, shared, hist, stream);
+        if (!bf) return k->h_ckpt ? launch_chunked<f32_t, 1, 1, 8, 8>(a, shared, hist, stream)
+                                  : launch_chunked<f32_t, 1, 1, 8, 16>(a, shared, hist, stream);
         break;
     default:
         break;

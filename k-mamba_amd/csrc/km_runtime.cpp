@@ -168,6 +168,38 @@ void *Staging::reserve(size_t bytes) {
     return p;
 }
 
+namespace {
+std::mutex g_ws_mu;
+void *g_ws_ptr[64] = {};
+size_t g_ws_size[64] = {};
+}  // namespace
+
+void *Workspace::reserve(size_t bytes) {
+    std::lock_guard<std::mutex> guard(g_ws_mu);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        set_error("workspace: no current HIP device");
+        return nullptr;
+    }
+    if (g_ws_size[dev] >= bytes && g_ws_ptr[dev]) return g_ws_ptr[dev];
+    if (g_ws_ptr[dev]) {
+        (void)hipDeviceSynchronize();   // earlier kernels may still use the old block
+        (void)hipFree(g_ws_ptr[dev]);
+        g_ws_ptr[dev] = nullptr;
+        g_ws_size[dev] = 0;
+    }
+    const size_t want = align_up(bytes, size_t(1) << 20);
+    void *p = nullptr;
+    if (hipMalloc(&p, want) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error("workspace: hipMalloc(%zu) failed", want);
+        return nullptr;
+    }
+    g_ws_ptr[dev] = p;
+    g_ws_size[dev] = want;
+    return p;
+}
+
 void Staging::lock() { g_stage_mu.lock(); }
 void Staging::unlock() { g_stage_mu.unlock(); }
 

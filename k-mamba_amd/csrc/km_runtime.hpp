@@ -32,6 +32,15 @@ struct Staging {
     static void unlock();
 };
 
+// Per-device scratch for kernels that need device memory beyond their
+// inputs and outputs (e.g. the Scan1D backward accumulators), used when the
+// caller passes no workspace. Grows on demand and is reused; calls that
+// overlap on one device with this shared scratch race, so concurrent callers
+// pass their own workspace.
+struct Workspace {
+    static void *reserve(size_t bytes);      // nullptr on failure (error set)
+};
+
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Bump allocator over a reserved staging block.

@@ -84,7 +84,18 @@ class KMScan1DFwd(C.Structure):           # include/kmamba_km.h
     _fields_ = [(n, C.c_void_p) for n in ("x", "delta", "A", "Bm", "Cm", "y", "h0",
                                           "h_final", "h_hist")] + \
                [(n, C.c_long) for n in ("B", "L", "D", "N", "bc_sb", "bc_st", "bc_sd")] + \
-               [("dtype", C.c_int), ("clamp", C.c_int)]
+               [("dtype", C.c_int), ("clamp", C.c_int), ("h_ckpt", C.c_void_p)]
+
+
+class KMScan1DBwd(C.Structure):           # include/kmamba_km.h
+    _fields_ = [(n, C.c_void_p) for n in ("x", "delta", "A", "Bm", "Cm", "dy", "h0", "h_hist",
+                                          "h_ckpt", "dx", "ddelta", "dA", "dB", "dC")] + \
+               [(n, C.c_long) for n in ("B", "L", "D", "N", "bc_sb", "bc_st", "bc_sd")] + \
+               [("dtype", C.c_int), ("clamp", C.c_int), ("workspace", C.c_void_p),
+                ("workspace_bytes", C.c_size_t)]
+
+
+KM_SCAN1D_CKPT_STEPS = 64
 
 
 VisitFn = C.CFUNCTYPE(C.c_int, c_long_p, C.c_long, C.c_long, C.c_long, C.c_void_p)
@@ -144,6 +155,18 @@ om_scan1d_forward = _decl("om_scan1d_forward", None,
 mamba_scan1d_cuda_forward = _decl("mamba_scan1d_cuda_forward", None,
                                   [C.c_void_p] * 7 + [C.c_int] * 3)
 km_scan1d_fwd_c = _decl("km_scan1d_fwd", C.c_int, [C.POINTER(KMScan1DFwd), C.c_void_p])
+scan1d_backward = _decl("scan1d_backward", None, [C.POINTER(ScanBackwardParams)])
+mamba_scan1d_backward = _decl("mamba_scan1d_backward", None, [C.POINTER(ScanBackwardParams)])
+scan1d_backward_m1_shared_bc = _decl("scan1d_backward_m1_shared_bc", None,
+                                     [C.POINTER(ScanBackwardSharedParams)])
+mamba_scan1d_backward_m1_shared_bc = _decl("mamba_scan1d_backward_m1_shared_bc", None,
+                                           [C.POINTER(ScanBackwardSharedParams)])
+om_scan1d_backward = _decl("om_scan1d_backward", None, [C.c_void_p] * 12 + [C.c_int] * 3)
+mamba_scan1d_cuda_backward = _decl("mamba_scan1d_cuda_backward", None,
+                                   [C.c_void_p] * 12 + [C.c_int] * 3)
+km_scan1d_bwd_c = _decl("km_scan1d_bwd", C.c_int, [C.POINTER(KMScan1DBwd), C.c_void_p])
+km_scan1d_bwd_workspace_bytes = _decl("km_scan1d_bwd_workspace_bytes", C.c_size_t,
+                                      [C.POINTER(KMScan1DBwd)])
 
 
 def km_last_error() -> str:
@@ -178,7 +201,7 @@ def stream_handle(stream=None):
     return s.cuda_stream
 
 
-def scan1d_fwd(x, delta, A, Bm, Cm, y, *, h0=None, h_final=None, h_hist=None,
+def scan1d_fwd(x, delta, A, Bm, Cm, y, *, h0=None, h_final=None, h_hist=None, h_ckpt=None,
                bc_strides=None, clamp=True, stream=None):
     """km_scan1d_fwd on torch device tensors.
 
@@ -194,8 +217,31 @@ def scan1d_fwd(x, delta, A, Bm, Cm, y, *, h0=None, h_final=None, h_hist=None,
         bc_strides = (L * N, N, 0)
     dt = KM_BF16 if x.dtype == torch.bfloat16 else KM_F32
     args = KMScan1DFwd(ptr(x), ptr(delta), ptr(A), ptr(Bm), ptr(Cm), ptr(y), ptr(h0),
-                       ptr(h_final), ptr(h_hist), Bsz, L, D, N, *bc_strides, dt, int(clamp))
+                       ptr(h_final), ptr(h_hist), Bsz, L, D, N, *bc_strides, dt, int(clamp),
+                       ptr(h_ckpt))
     check(km_scan1d_fwd_c(C.byref(args), C.c_void_p(stream_handle(stream))), "km_scan1d_fwd")
+
+
+def scan1d_bwd_args(x, delta, A, Bm, Cm, dy, dx, ddelta, dA, dB, dC, *, h0=None, h_hist=None,
+                    h_ckpt=None, bc_strides=None, clamp=True, workspace=None):
+    """KMScan1DBwd over torch device tensors (layouts as scan1d_fwd)."""
+    import torch
+    Bsz, L, D = x.shape
+    N = A.shape[1]
+    if bc_strides is None:
+        assert Bm.shape == (Bsz, L, N) and Bm.is_contiguous()
+        bc_strides = (L * N, N, 0)
+    dt = KM_BF16 if x.dtype == torch.bfloat16 else KM_F32
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    return KMScan1DBwd(ptr(x), ptr(delta), ptr(A), ptr(Bm), ptr(Cm), ptr(dy), ptr(h0), ptr(h_hist),
+                       ptr(h_ckpt), ptr(dx), ptr(ddelta), ptr(dA), ptr(dB), ptr(dC),
+                       Bsz, L, D, N, *bc_strides, dt, int(clamp), ptr(workspace), ws_bytes)
+
+
+def scan1d_bwd(x, delta, A, Bm, Cm, dy, dx, ddelta, dA, dB, dC, *, stream=None, **kw):
+    """km_scan1d_bwd on torch device tensors."""
+    args = scan1d_bwd_args(x, delta, A, Bm, Cm, dy, dx, ddelta, dA, dB, dC, **kw)
+    check(km_scan1d_bwd_c(C.byref(args), C.c_void_p(stream_handle(stream))), "km_scan1d_bwd")
 
 
 # --- ScanND / Scan2D ----------------------------------------------------------
