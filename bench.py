@@ -73,6 +73,39 @@ def bench_scan1d_bwd(torch, K, stream, Bsz, L, D, N, dtype, steps, warmup):
             "fwd_plus_bwd_elems_per_s": Bsz * L * D / ((ms + msf) * 1e-3)}
 
 
+def bench_convnd(torch, K, stream, dims, D, Kk, steps, warmup):
+    """configs[3] workload: input ~ N(0,1) [P,D]; kernel ~ N(0, 1/K^nd)
+    [K^nd,D]; bias ~ N(0, 0.01) [D]; causal zero padding, stride 1.
+    Forward algorithmic bytes: input read + output written (P*D*4 each) +
+    kernel + bias. Backward: input, dy read and dinput written (P*D*4
+    each) + kernel read + dkernel, dbias written."""
+    nd = len(dims)
+    P = 1
+    for v in dims:
+        P *= v
+    KV = Kk ** nd
+    g = torch.Generator(device="cuda").manual_seed(21)
+    inp = torch.randn((P, D), device="cuda", generator=g)
+    ker = torch.randn((KV, D), device="cuda", generator=g) / KV ** 0.5
+    bias = torch.randn((D,), device="cuda", generator=g) * 0.1
+    out = torch.empty_like(inp)
+    dy = torch.randn((P, D), device="cuda", generator=g)
+    din, dker, db = torch.empty_like(inp), torch.empty_like(ker), torch.empty_like(bias)
+    fwd = lambda: K.convnd_fwd(dims, inp, ker, bias, out, stream=stream)  # noqa: E731
+    bwd = lambda: K.convnd_bwd(dims, inp, ker, dy, din, dker, db, stream=stream)  # noqa: E731
+    per, _ = time_launches(torch, stream, fwd, steps, warmup)
+    perb, _ = time_launches(torch, stream, bwd, steps, warmup)
+    ms, msb = sum(per) / len(per), sum(perb) / len(perb)
+    alg = 2 * P * D * 4 + KV * D * 4 + D * 4
+    algb = 3 * P * D * 4 + 2 * KV * D * 4 + D * 4
+    return {"fwd_ms": round(ms, 4), "fwd_elems_per_s": P * D / (ms * 1e-3), "fwd_alg_bytes": alg,
+            "fwd_achieved_GBs": round(alg / (ms * 1e-3) / 1e9, 1),
+            "fwd_frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "bwd_ms": round(msb, 4), "bwd_alg_bytes": algb,
+            "bwd_achieved_GBs": round(algb / (msb * 1e-3) / 1e9, 1),
+            "bwd_frac_hbm": round(algb / (msb * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def scannd_alg_bytes(dims, D, M):
     """Algorithmic bytes of one ScanND forward: x [P,D], delta [nd,P,D],
     A [nd,D,M], B and C [P,D,M] read; h [P,D,M] and y [P,D] written (fp32)."""
@@ -168,7 +201,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["all", "scan1d", "scan1d_bwd", "scannd", "copy"],
+    ap.add_argument("--only", choices=["all", "scan1d", "scan1d_bwd", "scannd", "convnd", "copy"],
                     default="all",
                     help="profiling modes: scan1d = the fp32 headline kernel only; copy = a plain "
                          "1 GiB device copy (calibrates rocprof FETCH_SIZE/WRITE_SIZE)")
@@ -199,6 +232,12 @@ def main():
             rb = bench_scan1d_bwd(torch, K, stream, 8, 4096, 1024, 16, "bf16", args.steps,
                                   args.warmup)
         print(json.dumps({"scan1d_bwd_f32": r, "scan1d_bwd_bf16": rb}))
+        return
+    if args.only == "convnd":
+        with torch.cuda.stream(stream):
+            r2 = bench_convnd(torch, K, stream, (512, 512), 64, 3, args.steps, args.warmup)
+            r3 = bench_convnd(torch, K, stream, (64, 64, 64), 64, 3, args.steps, args.warmup)
+        print(json.dumps({"convnd_2d_512x512_D64_K3": r2, "convnd_3d_64cubed_D64_K3": r3}))
         return
     if args.only == "scannd":
         with torch.cuda.stream(stream):
@@ -252,6 +291,10 @@ def main():
                                                     max(5, args.steps // 2), 2)
         extra["scannd_2d_256x256_D256_M16_f32"] = bench_scannd(torch, K, stream, (256, 256), 256, 16,
                                                                 max(5, args.steps // 2), 2)
+        extra["convnd_2d_512x512_D64_K3_f32"] = bench_convnd(torch, K, stream, (512, 512), 64, 3,
+                                                             max(5, args.steps // 2), 2)
+        extra["convnd_3d_64cubed_D64_K3_f32"] = bench_convnd(torch, K, stream, (64, 64, 64), 64, 3,
+                                                             max(5, args.steps // 2), 2)
         extra["scannd_3d_64cubed_D128_M16_f32"] = bench_scannd(torch, K, stream, (64, 64, 64), 128, 16,
                                                                 max(5, args.steps // 2), 2)
 

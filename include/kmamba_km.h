@@ -5,8 +5,9 @@
  * All pointers are device pointers. Entry points are asynchronous on the
  * given stream (a hipStream_t passed as void*, NULL for the null stream) and
  * return 0 on success, -1 on invalid arguments or a launch failure; the
- * reason is available from km_last_error(). No entry point allocates device
- * memory on the hot path.
+ * reason is available from km_last_error(). The only device allocation is
+ * the library's per-device scratch, made on first use (and when a larger one
+ * is needed) by entry points that need scratch and were given none.
  */
 #ifndef KMAMBA_KM_H
 #define KMAMBA_KM_H
@@ -14,6 +15,7 @@
 #include <stddef.h>
 
 #include "scan_nd.h"
+#include "convnd.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -74,6 +76,8 @@ typedef struct {
 
 #define KM_SCAN1D_CKPT_STEPS 64
 
+int km_scan1d_fwd(const KMScan1DFwd *a, void *stream);
+
 /* Batched, strided Scan1D backward: the adjoint of km_scan1d_fwd, per batch
  * element the reference scan1d_backward (cpu/scan1d_backward.c:248-295):
  *   ah = adj + dy*C;  dC = dy*h_t;  dB = ah*delta*x;  dA += ah*delta*e*h_{t-1}
@@ -121,7 +125,17 @@ typedef struct {
 size_t km_scan1d_bwd_workspace_bytes(const KMScan1DBwd *a);
 int km_scan1d_bwd(const KMScan1DBwd *a, void *stream);
 
-int km_scan1d_fwd(const KMScan1DFwd *a, void *stream);
+/* ConvND forward / backward on device pointers over `batch` independent
+ * grids, enqueued on `stream` without a host synchronisation. Same
+ * ConvNDParams as om_convnd_forward / om_convnd_backward (ref
+ * include/convnd.h:10-51, cuda/convnd.cu:258-436), with input, output, dy and
+ * dinput holding [batch, prod(dims), D]; kernel and bias are shared by the
+ * batch, and dkernel / dbias sum over it. Backward overwrites dinput,
+ * dkernel and dbias (dbias may be NULL). dkernel and dbias are sums formed
+ * with fp32 atomics: their last bits may vary between runs.
+ * Returns 0, or -1 with km_last_error() set. */
+int km_convnd_fwd(const ConvNDParams *p, long batch, void *stream);
+int km_convnd_bwd(const ConvNDParams *p, long batch, void *stream);
 
 /* ScanND forward on device pointers, enqueued on `stream` (NULL = default
  * stream) without a host synchronisation. Same parameters and layout as

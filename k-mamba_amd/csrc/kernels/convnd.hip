@@ -1,0 +1,660 @@
+// convnd.hip - dense per-channel causal ND convolution for gfx950.
+//
+//   out[n, d] = bias[d] + sum_{k in [0,K)^N} in[n - (K-1-k), d] * W[k, d]
+// (reference src/convnd.c:83-126; taps below 0 on any axis are skipped,
+// summed in row-major kernel order). Backward (src/convnd.c:135-202):
+//   dinput[s, d]  = sum_k dy[s + (K-1-k), d] * W[k, d]   (taps past the end skipped)
+//   dkernel[k, d] = sum_n dy[n, d] * in[n - (K-1-k), d]
+//   dbias[d]      = sum_n dy[n, d]
+//
+// Design: the 64 lanes of a wave are 64 channels, so every point row of a
+// tensor is one coalesced 256-byte access. A wave sweeps a strip of points
+// along the last axis for one tuple of leading coordinates ("line"), keeping
+// a K-wide window of inputs for each of the K^(N-1) leading tap offsets in
+// registers: each step loads K^(N-1) new values instead of K^N. Lines that
+// share inputs (neighbours along the leading axes) are adjacent in the task
+// order, and workgroups are renumbered so that consecutive tasks run on the
+// same XCD and find each other's rows in that XCD's L2. The backward sweeps
+// the same strips with a trailing input window (for dkernel) and a leading
+// dy window (for dinput), reduces dkernel/dbias over the workgroup in LDS and
+// adds them with one fp32 atomic per (tap, channel) per workgroup.
+#include <algorithm>
+
+#include "km_device.hpp"
+#include "../km_runtime.hpp"
+#include "convnd.h"
+#include "wavefront_nd.h"
+#include "wavefront_plan.h"
+#include "kmamba_km.h"
+
+namespace km {
+
+constexpr int kConvMaxNd = 8;
+constexpr int ipow(int b, int e) { return e == 0 ? 1 : b * ipow(b, e - 1); }
+constexpr int kStrip = 64;        // points per wave along the last axis
+constexpr int kConvWaves = 4;     // waves per workgroup
+
+struct ConvArgs {
+    const float *in, *W, *bias;
+    float *out;
+    const float *dy;
+    float *din, *dW, *db;         // dW, db: fp32 accumulators zeroed by the launcher
+    long P;                        // points per batch element
+    long batch;
+    int nd, D, K, KV;
+    int dims[kConvMaxNd];
+    long stride[kConvMaxNd];
+    long lines, njb, groups, tasks;
+};
+
+// Workgroup id in an order where consecutive ids share an XCD: the hardware
+// deals workgroups to the 8 XCDs round-robin, so XCD x runs ids x, x+8, ...;
+// this maps them to one contiguous range of tasks per XCD.
+__device__ __forceinline__ long xcd_block(long b, long nb) {
+    const long q = nb / 8, r = nb % 8, x = b % 8;
+    return x * q + (x < r ? x : r) + b / 8;
+}
+
+struct TaskPos {
+    long batch, line, j0;
+    int d;
+    bool dvalid;
+    int lc[kConvMaxNd];            // leading coordinates of the line
+    long line_off;                 // point offset of (line, j = 0)
+};
+
+__device__ __forceinline__ bool task_pos(const ConvArgs &p, long task, TaskPos &t) {
+    if (task >= p.tasks) return false;
+    const long g = task % p.groups;
+    long rest = task / p.groups;
+    const long jb = rest % p.njb;
+    rest /= p.njb;
+    t.line = rest % p.lines;
+    t.batch = rest / p.lines;
+    t.j0 = jb * kStrip;
+    t.d = static_cast<int>(g * 64) + static_cast<int>(threadIdx.x & 63);
+    t.dvalid = t.d < p.D;
+    long rem = t.line, off = 0;
+    for (int a = p.nd - 2; a >= 0; --a) {
+        t.lc[a] = static_cast<int>(rem % p.dims[a]);
+        rem /= p.dims[a];
+        off += t.lc[a] * p.stride[a];
+    }
+    t.line_off = off;
+    return true;
+}
+
+// Point offsets (within the batch element) of the K^(N-1) leading tap rows
+// of a line, -1 where a tap leaves the grid. dir = -1: causal taps
+// (coordinate - (K-1-k)); dir = +1: anti-causal taps (coordinate + (K-1-k)).
+template <int ND, int K>
+__device__ __forceinline__ void lead_rows(const ConvArgs &p, const TaskPos &t, int dir,
+                                          long (&rows)[(ND > 1) ? ipow(K, ND - 1) : 1]) {
+    constexpr int KL = (ND > 1) ? ipow(K, ND - 1) : 1;
+#pragma unroll
+    for (int a = 0; a < KL; ++a) {
+        int rem = a;
+        long off = 0;
+        bool ok = true;
+#pragma unroll
+        for (int ax = ND - 2; ax >= 0; --ax) {
+            const int ka = rem % K;
+            rem /= K;
+            const int c = t.lc[ax] + dir * (K - 1 - ka);
+            ok = ok && c >= 0 && c < p.dims[ax];
+            off += static_cast<long>(c) * p.stride[ax];
+        }
+        rows[a] = ok ? off : -1;
+    }
+}
+
+template <int ND, int K>
+__global__ void __launch_bounds__(64 * kConvWaves) convnd_fwd_strip(ConvArgs p) {
+    constexpr int KL = (ND > 1) ? ipow(K, ND - 1) : 1;
+    constexpr int KV = KL * K;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const long blk = xcd_block(blockIdx.x, gridDim.x);
+    TaskPos t;
+    if (!task_pos(p, blk * kConvWaves + wave, t)) return;
+    const int dc = t.dvalid ? t.d : p.D - 1;
+    const int J = p.dims[ND - 1];
+    const long bbase = t.batch * p.P;
+    const float *in = p.in + bbase * p.D + dc;
+    float *out = p.out + bbase * p.D + dc;
+
+    float w[KV];
+#pragma unroll
+    for (int k = 0; k < KV; ++k) w[k] = p.W[static_cast<long>(k) * p.D + dc];
+    const float b0 = p.bias ? p.bias[dc] : 0.f;
+    long rows[KL];
+    lead_rows<ND, K>(p, t, -1, rows);
+
+    // win[a][c]: input of leading tap row a at column j - (K-1) + c.
+    float win[KL][K];
+#pragma unroll
+    for (int a = 0; a < KL; ++a) {
+#pragma unroll
+        for (int c = 0; c < K - 1; ++c) {
+            const long j = t.j0 - (K - 1) + c;
+            win[a][c + 1] = (rows[a] >= 0 && j >= 0) ? in[(rows[a] + j) * p.D] : 0.f;
+        }
+    }
+    const long jend = t.j0 + kStrip < J ? t.j0 + kStrip : J;
+    for (long j = t.j0; j < jend; ++j) {
+#pragma unroll
+        for (int a = 0; a < KL; ++a) {
+#pragma unroll
+            for (int c = 0; c < K - 1; ++c) win[a][c] = win[a][c + 1];
+            win[a][K - 1] = (rows[a] >= 0) ? in[(rows[a] + j) * p.D] : 0.f;
+        }
+        float s = b0;
+#pragma unroll
+        for (int kl = 0; kl < KV; ++kl) s += win[kl / K][kl % K] * w[kl];
+        if (t.dvalid) out[(t.line_off + j) * p.D] = s;
+    }
+}
+
+template <int ND, int K>
+__global__ void __launch_bounds__(64 * kConvWaves) convnd_bwd_strip(ConvArgs p) {
+    constexpr int KL = (ND > 1) ? ipow(K, ND - 1) : 1;
+    constexpr int KV = KL * K;
+    __shared__ float red[kConvWaves][KV + 1][64];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const long blk = xcd_block(blockIdx.x, gridDim.x);
+    TaskPos t;
+    const bool live = task_pos(p, blk * kConvWaves + wave, t);
+    float acc[KV + 1];
+#pragma unroll
+    for (int k = 0; k <= KV; ++k) acc[k] = 0.f;
+    int dc = 0;
+    if (live) {
+        dc = t.dvalid ? t.d : p.D - 1;
+        const int J = p.dims[ND - 1];
+        const long bbase = t.batch * p.P;
+        const float *in = p.in + bbase * p.D + dc;
+        const float *dy = p.dy + bbase * p.D + dc;
+        float *din = p.din + bbase * p.D + dc;
+        float w[KV];
+#pragma unroll
+        for (int k = 0; k < KV; ++k) w[k] = p.W[static_cast<long>(k) * p.D + dc];
+        long rin[KL], rdy[KL];
+        lead_rows<ND, K>(p, t, -1, rin);
+        lead_rows<ND, K>(p, t, +1, rdy);
+        // xin[a][c]: input at column j-(K-1)+c of causal row a.
+        // gdy[a][c]: dy at column j+c of anti-causal row a.
+        float xin[KL][K], gdy[KL][K];
+#pragma unroll
+        for (int a = 0; a < KL; ++a) {
+#pragma unroll
+            for (int c = 0; c < K - 1; ++c) {
+                const long ji = t.j0 - (K - 1) + c;
+                xin[a][c + 1] = (rin[a] >= 0 && ji >= 0) ? in[(rin[a] + ji) * p.D] : 0.f;
+                const long jd = t.j0 + c;
+                gdy[a][c] = (rdy[a] >= 0 && jd < J) ? dy[(rdy[a] + jd) * p.D] : 0.f;
+            }
+        }
+        // The anti-causal row with every leading tap at K-1 is the line itself.
+        constexpr int SELF = KL - 1;
+        const long jend = t.j0 + kStrip < J ? t.j0 + kStrip : J;
+        for (long j = t.j0; j < jend; ++j) {
+#pragma unroll
+            for (int a = 0; a < KL; ++a) {
+#pragma unroll
+                for (int c = 0; c < K - 1; ++c) xin[a][c] = xin[a][c + 1];
+                xin[a][K - 1] = (rin[a] >= 0) ? in[(rin[a] + j) * p.D] : 0.f;
+                const long jd = j + K - 1;
+                gdy[a][K - 1] = (rdy[a] >= 0 && jd < J) ? dy[(rdy[a] + jd) * p.D] : 0.f;
+            }
+            const float g = gdy[SELF][0];
+            float s = 0.f;
+#pragma unroll
+            for (int kl = 0; kl < KV; ++kl) {
+                const int a = kl / K, k = kl % K;
+                s += gdy[a][K - 1 - k] * w[kl];
+                acc[kl] = fmaf(g, xin[a][k], acc[kl]);
+            }
+            acc[KV] += g;
+            if (t.dvalid) din[(t.line_off + j) * p.D] = s;
+#pragma unroll
+            for (int a = 0; a < KL; ++a) {
+#pragma unroll
+                for (int c = 0; c < K - 1; ++c) gdy[a][c] = gdy[a][c + 1];
+            }
+        }
+        if (!t.dvalid) {
+#pragma unroll
+            for (int k = 0; k <= KV; ++k) acc[k] = 0.f;
+        }
+    }
+    // Workgroup sum per (tap, channel), then one atomic each. Waves of one
+    // workgroup share the channel group when groups divide the task order.
+#pragma unroll
+    for (int k = 0; k <= KV; ++k) red[wave][k][lane] = acc[k];
+    __syncthreads();
+    // Waves of a workgroup may belong to different channel groups: the first
+    // wave of each group adds the partials of the waves in that group.
+    if (live && t.dvalid) {
+        const long g = (blk * kConvWaves + wave) % p.groups;
+        bool first = true;
+        for (int v = 0; v < wave; ++v) {
+            const long tv = blk * kConvWaves + v;
+            if (tv < p.tasks && tv % p.groups == g) first = false;
+        }
+        if (first) {
+            for (int k = 0; k <= KV; ++k) {
+                float s = 0.f;
+                for (int v = 0; v < kConvWaves; ++v) {
+                    const long tv = blk * kConvWaves + v;
+                    if (tv < p.tasks && tv % p.groups == g) s += red[v][k][lane];
+                }
+                if (k < KV) unsafeAtomicAdd(p.dW + static_cast<long>(k) * p.D + dc, s);
+                else if (p.db) unsafeAtomicAdd(p.db + dc, s);
+            }
+        }
+    }
+}
+
+// Any ND <= 8 and K: one thread per (point, channel), taps from memory.
+__global__ void __launch_bounds__(256) convnd_fwd_generic(ConvArgs p) {
+    const long gid = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid >= p.batch * p.P * p.D) return;
+    const long d = gid % p.D, pt = (gid / p.D) % p.P, b = gid / (p.D * p.P);
+    int oc[kConvMaxNd];
+    long rem = pt;
+    for (int a = p.nd - 1; a >= 0; --a) {
+        oc[a] = static_cast<int>(rem % p.dims[a]);
+        rem /= p.dims[a];
+    }
+    const float *in = p.in + b * p.P * p.D;
+    float s = p.bias ? p.bias[d] : 0.f;
+    for (int kl = 0; kl < p.KV; ++kl) {
+        int tmp = kl;
+        long src = 0;
+        bool ok = true;
+        for (int a = p.nd - 1; a >= 0; --a) {
+            const int ka = tmp % p.K;
+            tmp /= p.K;
+            const int c = oc[a] - (p.K - 1 - ka);
+            ok = ok && c >= 0;
+            src += static_cast<long>(c) * p.stride[a];
+        }
+        if (ok) s += in[src * p.D + d] * p.W[static_cast<long>(kl) * p.D + d];
+    }
+    p.out[gid] = s;
+}
+
+__global__ void __launch_bounds__(256) convnd_bwd_input_generic(ConvArgs p) {
+    const long gid = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid >= p.batch * p.P * p.D) return;
+    const long d = gid % p.D, pt = (gid / p.D) % p.P, b = gid / (p.D * p.P);
+    int sc[kConvMaxNd];
+    long rem = pt;
+    for (int a = p.nd - 1; a >= 0; --a) {
+        sc[a] = static_cast<int>(rem % p.dims[a]);
+        rem /= p.dims[a];
+    }
+    const float *dy = p.dy + b * p.P * p.D;
+    float s = 0.f;
+    for (int kl = 0; kl < p.KV; ++kl) {
+        int tmp = kl;
+        long o = 0;
+        bool ok = true;
+        for (int a = p.nd - 1; a >= 0; --a) {
+            const int ka = tmp % p.K;
+            tmp /= p.K;
+            const int c = sc[a] + (p.K - 1 - ka);
+            ok = ok && c < p.dims[a];
+            o += static_cast<long>(c) * p.stride[a];
+        }
+        if (ok) s += dy[o * p.D + d] * p.W[static_cast<long>(kl) * p.D + d];
+    }
+    p.din[gid] = s;
+}
+
+// dkernel / dbias for any shape: block (tap, 64 channels, slice of points).
+__global__ void __launch_bounds__(256) convnd_bwd_kernel_generic(ConvArgs p, long pts_per_block) {
+    __shared__ float part[4][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int kl = blockIdx.y;              // KV = bias row
+    const long d = static_cast<long>(blockIdx.z) * 64 + lane;
+    const long total = p.batch * p.P;
+    const long lo = static_cast<long>(blockIdx.x) * pts_per_block;
+    const long hi = std::min(lo + pts_per_block, total);
+    float s = 0.f;
+    if (d < p.D) {
+        int kc[kConvMaxNd];
+        int tmp = kl;
+        for (int a = p.nd - 1; a >= 0; --a) {
+            kc[a] = tmp % p.K;
+            tmp /= p.K;
+        }
+        for (long n = lo + wv; n < hi; n += 4) {
+            const long pt = n % p.P, b = n / p.P;
+            const float g = p.dy[n * p.D + d];
+            if (kl == p.KV) { s += g; continue; }
+            long rem = pt, src = 0;
+            bool ok = true;
+            for (int a = p.nd - 1; a >= 0; --a) {
+                const int c = static_cast<int>(rem % p.dims[a]) - (p.K - 1 - kc[a]);
+                rem /= p.dims[a];
+                ok = ok && c >= 0;
+                src += static_cast<long>(c) * p.stride[a];
+            }
+            if (ok) s += g * p.in[(b * p.P + src) * p.D + d];
+        }
+    }
+    part[wv][lane] = s;
+    __syncthreads();
+    if (wv == 0 && d < p.D) {
+        const float t = part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane];
+        if (kl < p.KV) unsafeAtomicAdd(p.dW + static_cast<long>(kl) * p.D + d, t);
+        else if (p.db) unsafeAtomicAdd(p.db + d, t);
+    }
+}
+
+__global__ void __launch_bounds__(256) conv_zero(float *p, long n) {
+    for (long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<long>(gridDim.x) * blockDim.x)
+        p[i] = 0.f;
+}
+
+static int zero_dev(float *p, long n, hipStream_t s) {
+    if (!p || n <= 0) return 0;
+    hipLaunchKernelGGL(conv_zero, dim3(std::min<long>((n + 255) / 256, 4096)), dim3(256), 0, s, p, n);
+    KM_HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+static bool conv_args(const ConvNDParams *p, long batch, bool bwd, ConvArgs &a, const char *who) {
+    if (!p || !p->dims || p->ndims <= 0 || p->ndims > kConvMaxNd || p->D <= 0 || p->K <= 0 ||
+        !p->input || !p->kernel || batch <= 0) {
+        set_error("%s: invalid parameters", who);
+        return false;
+    }
+    if (bwd ? (!p->dy || !p->dinput || !p->dkernel) : !p->output) {
+        set_error("%s: missing %s buffers", who, bwd ? "backward" : "output");
+        return false;
+    }
+    if (!wavefront_nd_validate_dims(p->dims, p->ndims)) {
+        set_error("%s: invalid dims", who);
+        return false;
+    }
+    const long KV = convnd_kernel_volume(p->ndims, p->K);
+    if (KV <= 0 || KV > 65534 || p->D > 0x7fffffffL) {
+        set_error("%s: kernel volume %ld out of range", who, KV);
+        return false;
+    }
+    a = ConvArgs{};
+    a.in = p->input; a.W = p->kernel; a.bias = p->bias; a.out = p->output;
+    a.dy = p->dy; a.din = p->dinput; a.dW = p->dkernel; a.db = p->dbias;
+    a.nd = static_cast<int>(p->ndims); a.D = static_cast<int>(p->D);
+    a.K = static_cast<int>(p->K); a.KV = static_cast<int>(KV);
+    a.batch = batch;
+    long s = 1;
+    for (int ax = a.nd - 1; ax >= 0; --ax) {
+        if (p->dims[ax] > 0x7fffffffL) {
+            set_error("%s: dimension too large", who);
+            return false;
+        }
+        a.dims[ax] = static_cast<int>(p->dims[ax]);
+        a.stride[ax] = s;
+        s *= p->dims[ax];
+    }
+    a.P = s;
+    a.lines = s / a.dims[a.nd - 1];
+    a.njb = (a.dims[a.nd - 1] + kStrip - 1) / kStrip;
+    a.groups = (a.D + 63) / 64;
+    a.tasks = batch * a.lines * a.njb * a.groups;
+    return true;
+}
+
+#define KM_CONV_SHAPES(X) X(1, 2) X(1, 3) X(1, 4) X(2, 2) X(2, 3) X(2, 4) X(3, 2) X(3, 3)
+
+static int conv_fwd_launch(const ConvArgs &a, hipStream_t s) {
+    const long blocks = (a.tasks + kConvWaves - 1) / kConvWaves;
+    bool done = false;
+    if (blocks <= 0x7fffffffL) {
+#define KM_CONV_FWD(ND, KK)                                                                  \
+        if (!done && a.nd == ND && a.K == KK) {                                              \
+            hipLaunchKernelGGL((convnd_fwd_strip<ND, KK>), dim3(blocks), dim3(64 * kConvWaves), \
+                               0, s, a);                                                     \
+            done = true;                                                                     \
+        }
+        KM_CONV_SHAPES(KM_CONV_FWD)
+#undef KM_CONV_FWD
+    }
+    if (!done) {
+        const long n = a.batch * a.P * a.D;
+        hipLaunchKernelGGL(convnd_fwd_generic, dim3((n + 255) / 256), dim3(256), 0, s, a);
+    }
+    KM_HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+static int conv_bwd_launch(const ConvArgs &a, hipStream_t s) {
+    if (zero_dev(a.dW, static_cast<long>(a.KV) * a.D, s) != 0) return -1;
+    if (zero_dev(a.db, a.D, s) != 0) return -1;
+    const long blocks = (a.tasks + kConvWaves - 1) / kConvWaves;
+    bool done = false;
+    if (blocks <= 0x7fffffffL) {
+#define KM_CONV_BWD(ND, KK)                                                                  \
+        if (!done && a.nd == ND && a.K == KK) {                                              \
+            hipLaunchKernelGGL((convnd_bwd_strip<ND, KK>), dim3(blocks), dim3(64 * kConvWaves), \
+                               0, s, a);                                                     \
+            done = true;                                                                     \
+        }
+        KM_CONV_SHAPES(KM_CONV_BWD)
+#undef KM_CONV_BWD
+    }
+    if (!done) {
+        const long n = a.batch * a.P * a.D;
+        hipLaunchKernelGGL(convnd_bwd_input_generic, dim3((n + 255) / 256), dim3(256), 0, s, a);
+        const long per = 4096;
+        const long nb = (a.batch * a.P + per - 1) / per;
+        dim3 g(static_cast<unsigned>(nb), static_cast<unsigned>(a.KV + 1),
+               static_cast<unsigned>((a.D + 63) / 64));
+        hipLaunchKernelGGL(convnd_bwd_kernel_generic, g, dim3(256), 0, s, a, per);
+    }
+    KM_HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+int convnd_device(const ConvNDParams *p, long batch, bool fwd, bool bwd, hipStream_t s,
+                  const char *who) {
+    if (!gpu_ready()) return -1;
+    ConvArgs a;
+    if (fwd) {
+        if (!conv_args(p, batch, false, a, who)) return -1;
+        if (conv_fwd_launch(a, s) != 0) return -1;
+    }
+    if (bwd) {
+        if (!conv_args(p, batch, true, a, who)) return -1;
+        if (conv_bwd_launch(a, s) != 0) return -1;
+    }
+    return 0;
+}
+
+// Host-pointer path: stage every buffer the mode touches, run, copy back.
+static int convnd_host(ConvNDParams *p, bool fwd, bool bwd, const char *who) {
+    if (!gpu_ready()) return -1;
+    const long P = wavefront_nd_total_points(p->dims, p->ndims);
+    const long KV = convnd_kernel_volume(p->ndims, p->K);
+    if (P <= 0 || KV <= 0) {
+        set_error("%s: invalid dims", who);
+        return -1;
+    }
+    const size_t PD = sizeof(float) * P * p->D, KD = sizeof(float) * KV * p->D,
+                 D4 = sizeof(float) * p->D;
+    struct B { void *user; size_t bytes; bool in, out; void *dev; };
+    B bufs[] = {
+        {p->input, PD, true, false, nullptr},
+        {const_cast<float *>(p->kernel), KD, true, false, nullptr},
+        {const_cast<float *>(p->bias), D4, true, false, nullptr},
+        {fwd ? p->output : nullptr, PD, false, true, nullptr},
+        {bwd ? p->dy : nullptr, PD, true, false, nullptr},
+        {bwd ? p->dinput : nullptr, PD, false, true, nullptr},
+        {bwd ? p->dkernel : nullptr, KD, false, true, nullptr},
+        {bwd ? p->dbias : nullptr, D4, false, true, nullptr},
+    };
+    constexpr int NB = sizeof(bufs) / sizeof(bufs[0]);
+    bool all_dev = true;
+    for (auto &b : bufs)
+        if (b.user && !is_device_ptr(b.user)) all_dev = false;
+    ConvNDParams q = *p;
+    int rc = -1;
+    Staging::lock();
+    do {
+        if (!all_dev) {
+            size_t total = 0;
+            for (auto &b : bufs)
+                if (b.user) total += align_up(b.bytes, 256);
+            void *base = Staging::reserve(total);
+            if (!base) break;
+            Carver c(base);
+            bool ok = true;
+            for (auto &b : bufs) {
+                if (!b.user) continue;
+                b.dev = c.take<char>(b.bytes);
+                if (b.in && hipMemcpy(b.dev, b.user, b.bytes, hipMemcpyHostToDevice) != hipSuccess) ok = false;
+            }
+            if (!ok) {
+                set_error("%s: host-to-device copy failed", who);
+                break;
+            }
+        } else {
+            for (auto &b : bufs) b.dev = b.user;
+        }
+        q.input = static_cast<float *>(bufs[0].dev);
+        q.kernel = static_cast<const float *>(bufs[1].dev);
+        q.bias = static_cast<const float *>(bufs[2].dev);
+        q.output = static_cast<float *>(bufs[3].dev);
+        q.dy = static_cast<float *>(bufs[4].dev);
+        q.dinput = static_cast<float *>(bufs[5].dev);
+        q.dkernel = static_cast<float *>(bufs[6].dev);
+        q.dbias = static_cast<float *>(bufs[7].dev);
+        if (convnd_device(&q, 1, fwd, bwd, nullptr, who) != 0) break;
+        if (hipStreamSynchronize(nullptr) != hipSuccess) {
+            set_error("%s: %s", who, hipGetErrorString(hipGetLastError()));
+            break;
+        }
+        bool ok = true;
+        if (!all_dev) {
+            for (int i = 0; i < NB; ++i) {
+                if (!bufs[i].user || !bufs[i].out) continue;
+                if (hipMemcpy(bufs[i].user, bufs[i].dev, bufs[i].bytes, hipMemcpyDeviceToHost) != hipSuccess)
+                    ok = false;
+            }
+        }
+        if (!ok) {
+            set_error("%s: device-to-host copy failed", who);
+            break;
+        }
+        rc = 0;
+    } while (false);
+    Staging::unlock();
+    return rc;
+}
+
+}  // namespace km
+
+extern "C" {
+
+long convnd_kernel_volume(long ndims, long K) {
+    if (ndims <= 0 || K <= 0) return 0;
+    long v = 1;
+    for (long i = 0; i < ndims; ++i) {
+        if (v > 0x7fffffffffffffffL / K) return 0;
+        v *= K;
+    }
+    return v;
+}
+
+// Reference src/convnd.c:67-129: silently returns on invalid parameters or a
+// plan that does not match dims; host or device pointers.
+void convnd_forward_wavefront(ConvNDParams *p, const KMWavefrontPlan *plan) {
+    km::clear_error();
+    if (!p || !p->input || !p->kernel || !p->output || !p->dims || p->ndims <= 0 || p->D <= 0 ||
+        p->K <= 0) {
+        km::set_error("convnd_forward_wavefront: invalid parameters");
+        return;
+    }
+    if (!km_wavefront_plan_matches_dims(plan, p->dims, p->ndims)) {
+        km::set_error("convnd_forward_wavefront: plan does not match dims");
+        return;
+    }
+    km::convnd_host(p, true, false, "convnd_forward_wavefront");
+}
+
+// Reference src/convnd.c:135-202: dinput, dkernel, dbias overwritten.
+void convnd_backward_wavefront(ConvNDParams *p, const KMWavefrontPlan *plan) {
+    km::clear_error();
+    if (!p || !p->input || !p->kernel || !p->dy || !p->dinput || !p->dkernel || !p->dims ||
+        p->ndims <= 0 || p->D <= 0 || p->K <= 0) {
+        km::set_error("convnd_backward_wavefront: invalid parameters");
+        return;
+    }
+    if (!km_wavefront_plan_matches_dims(plan, p->dims, p->ndims)) {
+        km::set_error("convnd_backward_wavefront: plan does not match dims");
+        return;
+    }
+    km::convnd_host(p, false, true, "convnd_backward_wavefront");
+}
+
+// Reference src/convnd.c:208-244 (mode bits: 1 forward, 2 backward).
+void convnd(ConvNDParams *p, ConvNDMode mode) {
+    km::clear_error();
+    if (!p || !p->dims || p->ndims <= 0) {
+        km::set_error("convnd: invalid parameters");
+        return;
+    }
+    const bool fwd = (mode & CONVND_FORWARD) != 0, bwd = (mode & CONVND_BACKWARD) != 0;
+    if (fwd && (!p->input || !p->kernel || !p->output || p->D <= 0 || p->K <= 0)) {
+        km::set_error("convnd: invalid forward parameters");
+        return;
+    }
+    if (bwd && (!p->input || !p->kernel || !p->dy || !p->dinput || !p->dkernel || p->D <= 0 ||
+                p->K <= 0)) {
+        km::set_error("convnd: invalid backward parameters");
+        return;
+    }
+    if (!wavefront_nd_validate_dims(p->dims, p->ndims)) {
+        km::set_error("convnd: invalid dims");
+        return;
+    }
+    if (fwd || bwd) km::convnd_host(p, fwd, bwd, "convnd");
+}
+
+// Reference cuda/convnd.cu:258-436: device pointers (dims on the host),
+// synchronous, 0 ok / -1 error.
+int om_convnd_forward(ConvNDParams *p) {
+    km::clear_error();
+    if (km::convnd_device(p, 1, true, false, nullptr, "om_convnd_forward") != 0) return -1;
+    if (hipStreamSynchronize(nullptr) != hipSuccess) {
+        km::set_error("om_convnd_forward: %s", hipGetErrorString(hipGetLastError()));
+        return -1;
+    }
+    return 0;
+}
+
+int om_convnd_backward(ConvNDParams *p) {
+    km::clear_error();
+    if (km::convnd_device(p, 1, false, true, nullptr, "om_convnd_backward") != 0) return -1;
+    if (hipStreamSynchronize(nullptr) != hipSuccess) {
+        km::set_error("om_convnd_backward: %s", hipGetErrorString(hipGetLastError()));
+        return -1;
+    }
+    return 0;
+}
+
+int km_convnd_fwd(const ConvNDParams *p, long batch, void *stream) {
+    km::clear_error();
+    return km::convnd_device(p, batch, true, false, static_cast<hipStream_t>(stream), "km_convnd_fwd");
+}
+
+int km_convnd_bwd(const ConvNDParams *p, long batch, void *stream) {
+    km::clear_error();
+    return km::convnd_device(p, batch, false, true, static_cast<hipStream_t>(stream), "km_convnd_bwd");
+}
+
+}  // extern "C"

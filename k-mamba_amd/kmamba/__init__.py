@@ -244,6 +244,44 @@ def scan1d_bwd(x, delta, A, Bm, Cm, dy, dx, ddelta, dA, dB, dC, *, stream=None, 
     check(km_scan1d_bwd_c(C.byref(args), C.c_void_p(stream_handle(stream))), "km_scan1d_bwd")
 
 
+# --- ConvND -------------------------------------------------------------------
+convnd_kernel_volume = _decl("convnd_kernel_volume", C.c_long, [C.c_long, C.c_long])
+convnd_forward_wavefront = _decl("convnd_forward_wavefront", None,
+                                 [C.POINTER(ConvNDParams), C.POINTER(KMWavefrontPlan)])
+convnd_backward_wavefront = _decl("convnd_backward_wavefront", None,
+                                  [C.POINTER(ConvNDParams), C.POINTER(KMWavefrontPlan)])
+convnd = _decl("convnd", None, [C.POINTER(ConvNDParams), C.c_int])
+om_convnd_forward = _decl("om_convnd_forward", C.c_int, [C.POINTER(ConvNDParams)])
+om_convnd_backward = _decl("om_convnd_backward", C.c_int, [C.POINTER(ConvNDParams)])
+km_convnd_fwd_c = _decl("km_convnd_fwd", C.c_int, [C.POINTER(ConvNDParams), C.c_long, C.c_void_p])
+km_convnd_bwd_c = _decl("km_convnd_bwd", C.c_int, [C.POINTER(ConvNDParams), C.c_long, C.c_void_p])
+
+
+def convnd_params(dims, inp=None, kernel=None, bias=None, output=None, dy=None, dinput=None,
+                  dkernel=None, dbias=None, *, D, K):
+    """ConvNDParams over buffers (torch device tensors or numpy arrays);
+    returns (params, keepalive)."""
+    dd = longs(dims)
+    p = ConvNDParams(ptr(inp), ptr(kernel), ptr(bias), ptr(output), ptr(dy), ptr(dinput),
+                     ptr(dkernel), ptr(dbias), dd, len(dims), D, K)
+    return p, dd
+
+
+def convnd_fwd(dims, inp, kernel, bias, output, *, batch=1, stream=None):
+    """km_convnd_fwd: inp/output [batch, P, D] (or [P, D]); kernel [K^nd, D]."""
+    D = inp.shape[-1]
+    K = int(round(kernel.shape[0] ** (1.0 / len(dims))))
+    p, _keep = convnd_params(dims, inp, kernel, bias, output, D=D, K=K)
+    check(km_convnd_fwd_c(C.byref(p), batch, C.c_void_p(stream_handle(stream))), "km_convnd_fwd")
+
+
+def convnd_bwd(dims, inp, kernel, dy, dinput, dkernel, dbias, *, batch=1, stream=None):
+    D = inp.shape[-1]
+    K = int(round(kernel.shape[0] ** (1.0 / len(dims))))
+    p, _keep = convnd_params(dims, inp, kernel, None, None, dy, dinput, dkernel, dbias, D=D, K=K)
+    check(km_convnd_bwd_c(C.byref(p), batch, C.c_void_p(stream_handle(stream))), "km_convnd_bwd")
+
+
 # --- ScanND / Scan2D ----------------------------------------------------------
 scannd_validate = _decl("scannd_validate", C.c_int, [C.POINTER(ScanNDParams)])
 scannd_ref = _decl("scannd_ref", C.c_int, [C.POINTER(ScanNDParams)])

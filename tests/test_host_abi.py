@@ -49,8 +49,6 @@ def test_headers_parse():
         assert must in names, must
 
 
-@pytest.mark.xfail(reason="entry points still being implemented: the test lists the missing ones",
-                   strict=False)
 def test_library_exports_every_declared_symbol():
     out = subprocess.run(["nm", "-D", "--defined-only", str(K.LIB_PATH)],
                          capture_output=True, text=True, check=True).stdout
