@@ -106,6 +106,49 @@ def bench_convnd(torch, K, stream, dims, D, Kk, steps, warmup):
             "bwd_frac_hbm": round(algb / (msb * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def bench_mamba1_block(torch, K, stream, steps, warmup, Bsz=8, L=2048, dim=1024, di=2048, N=16,
+                       dconv=4, R=64):
+    """Mamba-1 block forward, bf16 weights/activations, fp32
+    state; weights ~ N(0, 0.02), A = -(1..N), x ~ N(0, 1). Reports tokens/s
+    for the whole block and, for the in/out projections (the MFMA GEMMs),
+    TFLOP/s against the 2.5 PFLOP/s dense bf16 peak."""
+    g = torch.Generator(device="cuda").manual_seed(31)
+    rn = lambda *s_, std=0.02: (torch.randn(s_, device="cuda", generator=g) * std)  # noqa: E731
+    w = {"W_in": rn(2 * di, dim).to(torch.bfloat16), "conv_w": rn(dconv, di, std=0.5),
+         "conv_b": rn(di, std=0.1), "W_x": rn(R + 2 * N, di).to(torch.bfloat16),
+         "W_dt": rn(di, R).to(torch.bfloat16), "dt_bias": rn(di, std=0.5) - 2.0,
+         "A": -torch.arange(1, N + 1, device="cuda", dtype=torch.float32).repeat(di, 1).contiguous(),
+         "Dskip": torch.ones(di, device="cuda"), "W_out": rn(dim, di).to(torch.bfloat16)}
+    x = torch.randn((Bsz, L, dim), device="cuda", generator=g).to(torch.bfloat16)
+    out = torch.empty_like(x)
+    ws = torch.empty(K.km_mamba1_block_workspace_bytes(K.C.byref(K.mamba1_weights(w)), Bsz, L),
+                     dtype=torch.uint8, device="cuda")
+    blk = lambda: K.mamba1_block_fwd(w, x, out, workspace=ws, stream=stream)  # noqa: E731
+    per, _ = time_launches(torch, stream, blk, steps, warmup)
+    ms = sum(per) / len(per)
+    T = Bsz * L
+    xi = torch.empty((T, di), device="cuda", dtype=torch.bfloat16)
+    y = torch.empty((T, di), device="cuda", dtype=torch.bfloat16)
+    o = torch.empty((T, dim), device="cuda", dtype=torch.bfloat16)
+    inp = lambda: K.gemm_bf16(x.view(T, dim), w["W_in"][:di], xi, stream=stream)  # noqa: E731
+    outp = lambda: K.gemm_bf16(y, w["W_out"], o, stream=stream)  # noqa: E731
+    pi, _ = time_launches(torch, stream, inp, steps, warmup)
+    po, _ = time_launches(torch, stream, outp, steps, warmup)
+    mi, mo = sum(pi) / len(pi), sum(po) / len(po)
+    fi, fo = 2.0 * T * di * dim, 2.0 * T * dim * di
+    return {"block_ms": round(ms, 4), "tokens_per_s": T / (ms * 1e-3),
+            "in_proj_half_ms": round(mi, 4),
+            "in_proj_TFLOPs": round(fi / (mi * 1e-3) / 1e12, 1),
+            "in_proj_frac_mfma_peak": round(fi / (mi * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "out_proj_ms": round(mo, 4), "out_proj_TFLOPs": round(fo / (mo * 1e-3) / 1e12, 1),
+            "out_proj_frac_mfma_peak": round(fo / (mo * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "config": {"B": Bsz, "L": L, "dim": dim, "d_inner": di, "d_state": N, "d_conv": dconv,
+                       "dt_rank": R}}
+
+
 def scannd_alg_bytes(dims, D, M):
     """Algorithmic bytes of one ScanND forward: x [P,D], delta [nd,P,D],
     A [nd,D,M], B and C [P,D,M] read; h [P,D,M] and y [P,D] written (fp32)."""
@@ -201,7 +244,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["all", "scan1d", "scan1d_bwd", "scannd", "convnd", "copy"],
+    ap.add_argument("--only", choices=["all", "scan1d", "scan1d_bwd", "scannd", "convnd", "block",
+                                       "copy"],
                     default="all",
                     help="profiling modes: scan1d = the fp32 headline kernel only; copy = a plain "
                          "1 GiB device copy (calibrates rocprof FETCH_SIZE/WRITE_SIZE)")
@@ -232,6 +276,11 @@ def main():
             rb = bench_scan1d_bwd(torch, K, stream, 8, 4096, 1024, 16, "bf16", args.steps,
                                   args.warmup)
         print(json.dumps({"scan1d_bwd_f32": r, "scan1d_bwd_bf16": rb}))
+        return
+    if args.only == "block":
+        with torch.cuda.stream(stream):
+            r = bench_mamba1_block(torch, K, stream, args.steps, args.warmup)
+        print(json.dumps({"mamba1_block_configs4": r}))
         return
     if args.only == "convnd":
         with torch.cuda.stream(stream):
@@ -295,6 +344,8 @@ def main():
                                                              max(5, args.steps // 2), 2)
         extra["convnd_3d_64cubed_D64_K3_f32"] = bench_convnd(torch, K, stream, (64, 64, 64), 64, 3,
                                                              max(5, args.steps // 2), 2)
+        extra["mamba1_block_configs4_bf16"] = bench_mamba1_block(torch, K, stream,
+                                                                  max(5, args.steps // 2), 2)
         extra["scannd_3d_64cubed_D128_M16_f32"] = bench_scannd(torch, K, stream, (64, 64, 64), 128, 16,
                                                                 max(5, args.steps // 2), 2)
 

@@ -53,6 +53,10 @@ typedef enum {
  *               after the last step), may be NULL: the checkpoints the
  *               backward recomputes states from
  * y may be NULL when only states are wanted.
+ * z           : [B, L, D] dtype gate, may be NULL; Dskip: [D] fp32, may be
+ *               NULL. When given, y = (sum_n C*h + Dskip*x) * SiLU(z) (the
+ *               Mamba-1 output gating, fused into the store; km_scan1d_bwd
+ *               does not differentiate it).
  * The +-1000 clamp is not associative; the kernel runs the unclamped
  * chunked scan and re-runs any (b, channel group) whose state left
  * [-1000, 1000] with the sequential clamped recurrence, so results follow the
@@ -72,6 +76,8 @@ typedef struct {
     int  dtype;
     int  clamp;
     float       *h_ckpt;
+    const void  *z;
+    const float *Dskip;
 } KMScan1DFwd;
 
 #define KM_SCAN1D_CKPT_STEPS 64
@@ -136,6 +142,65 @@ int km_scan1d_bwd(const KMScan1DBwd *a, void *stream);
  * Returns 0, or -1 with km_last_error() set. */
 int km_convnd_fwd(const ConvNDParams *p, long batch, void *stream);
 int km_convnd_bwd(const ConvNDParams *p, long batch, void *stream);
+
+/* bf16 GEMM on the matrix cores (no counterpart in the reference, whose
+ * kernels/gemm_f32.c:13-31 is a scalar fp32 triple loop):
+ *   C[M, N] = epilogue(A[M, K] . B[N, K]^T + bias[N])
+ * A, B: bf16 row-major with leading dimensions lda, ldb (B as [out, in]
+ * weights); C: c_dtype (KM_F32 or KM_BF16) with ldc; bias fp32 [N] or NULL.
+ * Accumulation in fp32. K, lda and ldb must be multiples of 8. */
+typedef enum {
+    KM_EPI_NONE = 0,
+    KM_EPI_SOFTPLUS = 1,   /* log(1 + e^v) (ref include/kmamba_kernels.h:47-49) */
+    KM_EPI_SILU = 2        /* v / (1 + e^-v) (ref include/kmamba_kernels.h:35-37) */
+} KMEpilogue;
+
+typedef struct {
+    const void  *A;
+    const void  *B;
+    void        *C;
+    const float *bias;
+    long M, N, K;
+    long lda, ldb, ldc;
+    int  c_dtype;
+    int  epilogue;
+} KMGemm;
+
+int km_gemm_bf16(const KMGemm *g, void *stream);
+
+/* Mamba-1 block forward (configs[4]; no single reference function, composed
+ * of the reference pieces: kernels/gemm_f32.c projections, the causal convnd
+ * in 1D, SiLU / softplus of include/kmamba_kernels.h:35-49 and the scan1d
+ * recurrence). With di = d_inner, N = d_state, R = dt_rank:
+ *   xi = x W_in[0:di]^T;  z = x W_in[di:2di]^T
+ *   u  = SiLU(causal_conv1d(xi, conv_w) + conv_b)
+ *   [dt_low | B | C] = u W_x^T
+ *   delta = softplus(dt_low W_dt^T + dt_bias)
+ *   y  = (scan(u, delta, A, B, C) + Dskip*u) * SiLU(z)
+ *   out = y W_out^T
+ * x, out: [B, L, dim] bf16. Weights: W_in [2*di, dim], W_x [R + 2N, di],
+ * W_dt [di, R], W_out [dim, di] bf16; conv_w [d_conv, di], conv_b [di] (may
+ * be NULL), dt_bias [di], A [di, N], Dskip [di] (may be NULL) fp32.
+ * clamp: the +-1000 state clamp of the reference scan (1) or none (0).
+ * workspace: km_mamba1_block_workspace_bytes() bytes of device memory, or
+ * NULL for the library's per-device scratch. */
+typedef struct {
+    long dim, d_inner, d_state, d_conv, dt_rank;
+    const void  *W_in;
+    const float *conv_w;
+    const float *conv_b;
+    const void  *W_x;
+    const void  *W_dt;
+    const float *dt_bias;
+    const float *A;
+    const float *Dskip;
+    const void  *W_out;
+    int clamp;
+} KMMamba1Weights;
+
+size_t km_mamba1_block_workspace_bytes(const KMMamba1Weights *w, long B, long L);
+int km_mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long B, long L,
+                        void *workspace, size_t workspace_bytes, void *stream);
 
 /* ScanND forward on device pointers, enqueued on `stream` (NULL = default
  * stream) without a host synchronisation. Same parameters and layout as

@@ -1,0 +1,219 @@
+// gemm_bf16.hip - bf16 GEMM on the gfx950 matrix cores (MFMA), fp32
+// accumulate, for the Mamba block projections:
+//   C[M, N] = epi(A[M, K] . B[N, K]^T + bias[N])
+// A and B are row-major bf16 with leading dimensions lda, ldb (B holds the
+// weights as [out, in], like a linear layer); C is fp32 or bf16 with ldc.
+//
+// Design: a 256-thread workgroup computes a 128 x 128 tile of C; each of its
+// 4 waves owns a 64 x 64 quarter as 2 x 2 v_mfma_f32_32x32x16_bf16 tiles
+// (64 fp32 accumulators per lane). K advances in steps of 64: the next
+// step's A and B tiles are loaded from global memory into registers while
+// the current step runs from LDS (double-buffered), so one barrier per step
+// separates the LDS write of step k+1 from the reads of step k. LDS rows are
+// 64 bf16 (eight 16-byte chunks) with chunk c of row r stored at c ^ (r & 7),
+// so the 32 rows a fragment read touches fall on different banks. Loads go
+// through raw buffer resources: rows past M (or N) read as zero, and the K
+// tail is masked per 16-byte chunk (K must be a multiple of 8).
+#include <algorithm>
+
+#include "km_device.hpp"
+#include "../km_runtime.hpp"
+#include "kmamba_km.h"
+
+namespace km {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+struct GemmArgs {
+    const uint16_t *A, *B;
+    void *C;
+    const float *bias;
+    long M, N, K, lda, ldb, ldc;
+    int c_bf16;
+    int epi;
+};
+
+constexpr int kBM = 128, kBN = 128, kBK = 64;
+
+__device__ __forceinline__ float softplus_ref(float v) {
+    // log(1 + e^v) (reference include/kmamba_kernels.h:47-49, which has no
+    // overflow guard: v > 88 gives inf there, v here).
+    return v > 20.f ? v : __logf(1.f + __expf(v));
+}
+
+template <int EPI>
+__device__ __forceinline__ float epilogue(float v) {
+    if constexpr (EPI == KM_EPI_SOFTPLUS) return softplus_ref(v);
+    else if constexpr (EPI == KM_EPI_SILU) return v / (1.f + __expf(-v));
+    else return v;
+}
+
+template <int EPI, bool CBF16>
+__global__ void __launch_bounds__(256, 2) gemm_bf16_mfma(GemmArgs p) {
+    __shared__ u32x4 sA[2][kBM * 8];
+    __shared__ u32x4 sB[2][kBN * 8];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = w >> 1, wn = w & 1;
+    const long m0 = static_cast<long>(blockIdx.y) * kBM;
+    const long n0 = static_cast<long>(blockIdx.x) * kBN;
+
+    // Windows over the rows this workgroup reads (offsets stay below 2 GiB:
+    // the launcher splits M so that a window fits).
+    const long arows = std::min<long>(kBM, p.M - m0), brows = std::min<long>(kBN, p.N - n0);
+    const auto rA = make_rsrc(p.A + m0 * p.lda, (arows - 1) * p.lda * 2 + p.K * 2);
+    const auto rB = make_rsrc(p.B + n0 * p.ldb, (brows - 1) * p.ldb * 2 + p.K * 2);
+
+    u32x4 ga[4], gb[4];
+    auto gload = [&](long k0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = tid + i * 256;
+            const int row = c >> 3, ch = c & 7;
+            const long k = k0 + ch * 8;
+            const bool kin = k < p.K;
+            const int offa = static_cast<int>((row * p.lda + k) * 2);
+            const int offb = static_cast<int>((row * p.ldb + k) * 2);
+            // rows past the window lie past the resource end and read 0
+            ga[i] = kin && row < arows ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rA, offa, 0, 0))
+                                       : u32x4{0, 0, 0, 0};
+            gb[i] = kin && row < brows ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rB, offb, 0, 0))
+                                       : u32x4{0, 0, 0, 0};
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = tid + i * 256;
+            const int row = c >> 3, ch = c & 7;
+            sA[buf][row * 8 + (ch ^ (row & 7))] = ga[i];
+            sB[buf][row * 8 + (ch ^ (row & 7))] = gb[i];
+        }
+    };
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const long nk = (p.K + kBK - 1) / kBK;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    const int fr = lane & 31;        // fragment row (A) / column (B) within a 32-tile
+    const int fk = lane >> 5;        // which 8-wide k group of a 16-wide step
+    for (long kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gload((kt + 1) * kBK);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const int ch = kk * 2 + fk;
+            bf16x8 af[2], bfr[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int ra = wm * 64 + i * 32 + fr;
+                af[i] = __builtin_bit_cast(bf16x8, sA[buf][ra * 8 + (ch ^ (ra & 7))]);
+                const int rb = wn * 64 + i * 32 + fr;
+                bfr[i] = __builtin_bit_cast(bf16x8, sB[buf][rb * 8 + (ch ^ (rb & 7))]);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) sstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Accumulator r of lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32
+    // of its 32 x 32 tile.
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const long col = n0 + wn * 64 + j * 32 + fr;
+            if (col >= p.N) continue;
+            const float bv = p.bias ? p.bias[col] : 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const long row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
+                if (row < p.M) {
+                    const float v = epilogue<EPI>(acc[i][j][r] + bv);
+                    if constexpr (CBF16)
+                        static_cast<uint16_t *>(p.C)[row * p.ldc + col] = f32_to_bf16(v);
+                    else
+                        static_cast<float *>(p.C)[row * p.ldc + col] = v;
+                }
+            }
+        }
+    }
+}
+
+template <int EPI>
+static void gemm_go(const GemmArgs &a, dim3 g, hipStream_t s) {
+    if (a.c_bf16) hipLaunchKernelGGL((gemm_bf16_mfma<EPI, true>), g, dim3(256), 0, s, a);
+    else          hipLaunchKernelGGL((gemm_bf16_mfma<EPI, false>), g, dim3(256), 0, s, a);
+}
+
+int gemm_bf16_launch(const KMGemm *g, hipStream_t s) {
+    if (!g || !g->A || !g->B || !g->C) { set_error("km_gemm_bf16: NULL pointer"); return -1; }
+    if (g->M < 0 || g->N < 0 || g->K <= 0 || g->K % 8 != 0 || g->lda < g->K || g->ldb < g->K ||
+        g->ldc < g->N || g->lda % 8 != 0 || g->ldb % 8 != 0) {
+        set_error("km_gemm_bf16: invalid shape M=%ld N=%ld K=%ld lda=%ld ldb=%ld ldc=%ld "
+                  "(K, lda, ldb must be multiples of 8)", g->M, g->N, g->K, g->lda, g->ldb, g->ldc);
+        return -1;
+    }
+    if (g->c_dtype != KM_F32 && g->c_dtype != KM_BF16) {
+        set_error("km_gemm_bf16: unknown C dtype %d", g->c_dtype);
+        return -1;
+    }
+    if (g->epilogue != KM_EPI_NONE && g->epilogue != KM_EPI_SOFTPLUS && g->epilogue != KM_EPI_SILU) {
+        set_error("km_gemm_bf16: unknown epilogue %d", g->epilogue);
+        return -1;
+    }
+    if (g->M == 0 || g->N == 0) return 0;
+    if (!gpu_ready()) return -1;
+    if (g->ldb * 2 * (kBN + 1) > 0x7fffffffL || g->lda * 2 * (kBM + 1) > 0x7fffffffL) {
+        set_error("km_gemm_bf16: leading dimension too large");
+        return -1;
+    }
+    const long nbn = (g->N + kBN - 1) / kBN;
+    const long nbm = (g->M + kBM - 1) / kBM;
+    if (nbn > 0x7fffffffL) { set_error("km_gemm_bf16: N too large"); return -1; }
+    // Row blocks per launch stay within the 65535 grid-y limit.
+    const long chunk = 65535;
+    for (long mb = 0; mb < nbm; mb += chunk) {
+        const long nb = std::min(chunk, nbm - mb);
+        GemmArgs a{};
+        a.A = static_cast<const uint16_t *>(g->A) + mb * kBM * g->lda;
+        a.B = static_cast<const uint16_t *>(g->B);
+        a.c_bf16 = (g->c_dtype == KM_BF16);
+        a.C = static_cast<char *>(g->C) + mb * kBM * g->ldc * (a.c_bf16 ? 2 : 4);
+        a.bias = g->bias;
+        a.M = std::min(g->M - mb * kBM, nb * kBM);
+        a.N = g->N; a.K = g->K; a.lda = g->lda; a.ldb = g->ldb; a.ldc = g->ldc;
+        a.epi = g->epilogue;
+        dim3 grid(static_cast<unsigned>(nbn), static_cast<unsigned>(nb));
+        switch (g->epilogue) {
+        case KM_EPI_SOFTPLUS: gemm_go<KM_EPI_SOFTPLUS>(a, grid, s); break;
+        case KM_EPI_SILU:     gemm_go<KM_EPI_SILU>(a, grid, s); break;
+        default:              gemm_go<KM_EPI_NONE>(a, grid, s); break;
+        }
+        KM_HIP_TRY(hipGetLastError());
+    }
+    return 0;
+}
+
+}  // namespace km
+
+extern "C" int km_gemm_bf16(const KMGemm *g, void *stream) {
+    km::clear_error();
+    return km::gemm_bf16_launch(g, static_cast<hipStream_t>(stream));
+}

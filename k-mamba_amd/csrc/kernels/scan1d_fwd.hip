@@ -47,10 +47,22 @@ struct Scan1DFwdArgs {
     float *hist;
     float *ckpt;     // [B, nck, D, N] state after every kCkptSteps steps, or null
     long nck;
+    const void *z;        // [B, L, D] gate: y *= SiLU(z), or null
+    const float *Dskip;   // [D] skip: y += Dskip * x, or null
     long B, L, D, N;
     long sb, st, sd;
     int clamp;
 };
+
+// Output of one step: the readout, plus Dskip*x and times SiLU(z) when
+// given (the Mamba gating, applied after the readout sum).
+template <typename T>
+__device__ __forceinline__ float gated(const Scan1DFwdArgs &p, float y, float xv, float dsk,
+                                       float zv) {
+    if (p.Dskip) y = fmaf(dsk, xv, y);
+    if (p.z) y *= zv / (1.f + __expf(-zv));
+    return y;
+}
 
 // Sequential clamped recurrence for the lanes of one wave (the clamp
 // fallback): the reference's step order, one (batch, channel, state group)
@@ -82,7 +94,10 @@ __device__ void scan1d_serial_wave(const Scan1DFwdArgs &p, long b, long d, bool 
         if (NS >= 4) yp += __shfl_xor(yp, 16);
         if (NS >= 2) yp += __shfl_xor(yp, 32);
         if (dvalid) {
-            if (n0 == 0 && p.y) IO::st(p.y, xi, yp);
+            if (n0 == 0 && p.y) {
+                const float zv = p.z ? IO::ld(p.z, xi) : 0.f;
+                IO::st(p.y, xi, gated<T>(p, yp, xv, p.Dskip ? p.Dskip[dc] : 0.f, zv));
+            }
             if (p.ckpt && ((t + 1) % kCkptSteps == 0 || t == p.L - 1)) {
 #pragma unroll
                 for (int j = 0; j < NPL; ++j)
@@ -150,6 +165,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     const int Dm = static_cast<int>(p.D);
     const int nit = (L + SC - 1) / SC;
     const bool store_y = dvalid && ns == 0;
+    const float dsk = p.Dskip ? p.Dskip[dvalid ? d : p.D - 1] : 0.f;
 
     // Per-batch-element windows addressed with 32-bit byte offsets (the
     // launcher keeps every window and offset below 1 GiB). Every variable
@@ -161,6 +177,8 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     // y may be null (checkpoint-only forward): a zero-sized window drops the stores.
     const auto ry = make_rsrc(p.y ? static_cast<char *>(p.y) + xoff * TS : nullptr,
                               p.y ? p.L * p.D * TS : 0);
+    const auto rz = make_rsrc(p.z ? static_cast<const char *>(p.z) + xoff * TS : nullptr,
+                              p.z ? p.L * p.D * TS : 0);
     const auto rB = make_rsrc(static_cast<const char *>(p.Bm) + b * p.sb * TS, p.L * p.st * TS);
     const auto rC = make_rsrc(static_cast<const char *>(p.Cm) + b * p.sb * TS, p.L * p.st * TS);
     const auto rh = make_rsrc(p.hist ? p.hist + xoff * p.N : nullptr, HIST ? p.L * p.D * p.N * 4 : 0);
@@ -367,7 +385,10 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             if constexpr (NS >= 4) yp += __shfl_xor(yp, 16);
             if constexpr (NS >= 2) yp += __shfl_xor(yp, 32);
             nan_seen |= (yp != yp);
-            if (store_y) IO::st(ry, vx + t * rowx, 0, yp);       // rows past L dropped
+            if (store_y) {                                          // rows past L dropped
+                const float zv = p.z ? IO::ld(rz, vx + t * rowx, 0) : 0.f;
+                IO::st(ry, vx + t * rowx, 0, gated<T>(p, yp, xs[k], dsk, zv));
+            }
             if constexpr (HIST) {
                 if (dvalid) {
 #pragma unroll
@@ -425,7 +446,10 @@ __global__ void __launch_bounds__(256) scan1d_fwd_serial(Scan1DFwdArgs p) {
                 p.ckpt[((b * p.nck + t / kCkptSteps) * p.D + d) * N + m] = hn;
             y = __fadd_rn(y, __fmul_rn(IO::ld(p.Cm, bc + m), hn));
         }
-        if (p.y) IO::st(p.y, xi, y);
+        if (p.y) {
+            const float zv = p.z ? IO::ld(p.z, xi) : 0.f;
+            IO::st(p.y, xi, gated<T>(p, y, xv, p.Dskip ? p.Dskip[d] : 0.f, zv));
+        }
     }
     if (p.hfin)
         for (long m = 0; m < N; ++m) p.hfin[(b * p.D + d) * N + m] = st[m];
@@ -524,7 +548,7 @@ int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream) {
         return 0;
     }
     Scan1DFwdArgs a{k->x, k->delta, k->A, k->Bm, k->Cm, k->y, k->h0, k->h_final, k->h_hist,
-                    k->h_ckpt, (k->L + kCkptSteps - 1) / kCkptSteps,
+                    k->h_ckpt, (k->L + kCkptSteps - 1) / kCkptSteps, k->z, k->Dskip,
                     k->B, k->L, k->D, k->N, k->bc_sb, k->bc_st, k->bc_sd, k->clamp};
     // The register-blocked kernel addresses each batch element's windows with
     // 32-bit byte offsets; larger problems take the sequential kernel.

@@ -84,7 +84,8 @@ class KMScan1DFwd(C.Structure):           # include/kmamba_km.h
     _fields_ = [(n, C.c_void_p) for n in ("x", "delta", "A", "Bm", "Cm", "y", "h0",
                                           "h_final", "h_hist")] + \
                [(n, C.c_long) for n in ("B", "L", "D", "N", "bc_sb", "bc_st", "bc_sd")] + \
-               [("dtype", C.c_int), ("clamp", C.c_int), ("h_ckpt", C.c_void_p)]
+               [("dtype", C.c_int), ("clamp", C.c_int), ("h_ckpt", C.c_void_p), ("z", C.c_void_p),
+                ("Dskip", C.c_void_p)]
 
 
 class KMScan1DBwd(C.Structure):           # include/kmamba_km.h
@@ -96,6 +97,19 @@ class KMScan1DBwd(C.Structure):           # include/kmamba_km.h
 
 
 KM_SCAN1D_CKPT_STEPS = 64
+KM_EPI_NONE, KM_EPI_SOFTPLUS, KM_EPI_SILU = 0, 1, 2
+
+
+class KMGemm(C.Structure):                # include/kmamba_km.h
+    _fields_ = [(n, C.c_void_p) for n in ("A", "B", "C", "bias")] + \
+               [(n, C.c_long) for n in ("M", "N", "K", "lda", "ldb", "ldc")] + \
+               [("c_dtype", C.c_int), ("epilogue", C.c_int)]
+
+
+class KMMamba1Weights(C.Structure):       # include/kmamba_km.h
+    _fields_ = [(n, C.c_long) for n in ("dim", "d_inner", "d_state", "d_conv", "dt_rank")] + \
+               [(n, C.c_void_p) for n in ("W_in", "conv_w", "conv_b", "W_x", "W_dt", "dt_bias",
+                                          "A", "Dskip", "W_out")] + [("clamp", C.c_int)]
 
 
 VisitFn = C.CFUNCTYPE(C.c_int, c_long_p, C.c_long, C.c_long, C.c_long, C.c_void_p)
@@ -202,7 +216,7 @@ def stream_handle(stream=None):
 
 
 def scan1d_fwd(x, delta, A, Bm, Cm, y, *, h0=None, h_final=None, h_hist=None, h_ckpt=None,
-               bc_strides=None, clamp=True, stream=None):
+               bc_strides=None, clamp=True, z=None, Dskip=None, stream=None):
     """km_scan1d_fwd on torch device tensors.
 
     x, delta, y: [B, L, D]; A: [D, N] fp32; Bm/Cm: [B, L, N] shared over
@@ -218,7 +232,7 @@ def scan1d_fwd(x, delta, A, Bm, Cm, y, *, h0=None, h_final=None, h_hist=None, h_
     dt = KM_BF16 if x.dtype == torch.bfloat16 else KM_F32
     args = KMScan1DFwd(ptr(x), ptr(delta), ptr(A), ptr(Bm), ptr(Cm), ptr(y), ptr(h0),
                        ptr(h_final), ptr(h_hist), Bsz, L, D, N, *bc_strides, dt, int(clamp),
-                       ptr(h_ckpt))
+                       ptr(h_ckpt), ptr(z), ptr(Dskip))
     check(km_scan1d_fwd_c(C.byref(args), C.c_void_p(stream_handle(stream))), "km_scan1d_fwd")
 
 
@@ -280,6 +294,50 @@ def convnd_bwd(dims, inp, kernel, dy, dinput, dkernel, dbias, *, batch=1, stream
     K = int(round(kernel.shape[0] ** (1.0 / len(dims))))
     p, _keep = convnd_params(dims, inp, kernel, None, None, dy, dinput, dkernel, dbias, D=D, K=K)
     check(km_convnd_bwd_c(C.byref(p), batch, C.c_void_p(stream_handle(stream))), "km_convnd_bwd")
+
+
+# --- bf16 GEMM and the Mamba-1 block -------------------------------------------
+km_gemm_bf16_c = _decl("km_gemm_bf16", C.c_int, [C.POINTER(KMGemm), C.c_void_p])
+km_mamba1_block_workspace_bytes = _decl("km_mamba1_block_workspace_bytes", C.c_size_t,
+                                        [C.POINTER(KMMamba1Weights), C.c_long, C.c_long])
+km_mamba1_block_fwd_c = _decl("km_mamba1_block_fwd", C.c_int,
+                              [C.POINTER(KMMamba1Weights), C.c_void_p, C.c_void_p, C.c_long,
+                               C.c_long, C.c_void_p, C.c_size_t, C.c_void_p])
+
+
+def gemm_bf16(A, B, Cout, *, bias=None, epilogue=KM_EPI_NONE, M=None, N=None, K=None, lda=None,
+              ldb=None, ldc=None, stream=None):
+    """km_gemm_bf16: Cout = epi(A . B^T + bias); A [M, K], B [N, K] bf16
+    (row strides lda, ldb), Cout [M, N] fp32 or bf16 (row stride ldc)."""
+    import torch
+    M = A.shape[0] if M is None else M
+    K = A.shape[1] if K is None else K
+    N = B.shape[0] if N is None else N
+    g = KMGemm(ptr(A), ptr(B), ptr(Cout), ptr(bias), M, N, K,
+               A.stride(0) if lda is None else lda, B.stride(0) if ldb is None else ldb,
+               Cout.stride(0) if ldc is None else ldc,
+               KM_BF16 if Cout.dtype == torch.bfloat16 else KM_F32, epilogue)
+    check(km_gemm_bf16_c(C.byref(g), C.c_void_p(stream_handle(stream))), "km_gemm_bf16")
+
+
+def mamba1_weights(w, clamp=True):
+    """KMMamba1Weights from a dict of torch device tensors (keys as the
+    struct fields; conv_b and Dskip optional)."""
+    di, dim = w["W_in"].shape[0] // 2, w["W_in"].shape[1]
+    N = w["A"].shape[1]
+    return KMMamba1Weights(dim, di, N, w["conv_w"].shape[0], w["W_dt"].shape[1],
+                           ptr(w["W_in"]), ptr(w["conv_w"]), ptr(w.get("conv_b")), ptr(w["W_x"]),
+                           ptr(w["W_dt"]), ptr(w["dt_bias"]), ptr(w["A"]), ptr(w.get("Dskip")),
+                           ptr(w["W_out"]), int(clamp))
+
+
+def mamba1_block_fwd(w, x, out, *, workspace=None, clamp=True, stream=None):
+    """km_mamba1_block_fwd: x, out [B, L, dim] bf16."""
+    Bsz, L, _ = x.shape
+    ws = mamba1_weights(w, clamp)
+    nb = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(km_mamba1_block_fwd_c(C.byref(ws), ptr(x), ptr(out), Bsz, L, ptr(workspace), nb,
+                                C.c_void_p(stream_handle(stream))), "km_mamba1_block_fwd")
 
 
 # --- ScanND / Scan2D ----------------------------------------------------------

@@ -111,3 +111,52 @@ def scan1d_bwd_kappa(x, dt, A, Bm, Cm, dy, *, h0=None, bc_strides=None, fast=Tru
     t2 = ax * kdx / np.asarray(dt, dtype=np.float32)
     kdd = np.maximum(2.0 * t2 - kdd, 0.0)
     return kdx, kdd, kdA, kdB, kdC
+
+
+def silu_ref(v):
+    """x / (1 + e^-x) in fp32 (reference include/kmamba_kernels.h:35-37)."""
+    v = np.asarray(v, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        return (v / (np.float32(1) + np.exp(-v))).astype(np.float32)
+
+
+def softplus_ref(v):
+    """log(1 + e^x) in fp32 (reference include/kmamba_kernels.h:47-49)."""
+    v = np.asarray(v, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        return np.log(np.float32(1) + np.exp(v)).astype(np.float32)
+
+
+def mamba1_block_ref(x, w, *, store_bf16=False, clamp=True):
+    """The configs[4] Mamba-1 block composed from the oracle pieces, fp32:
+    numpy projections, the oracle's causal convnd (1D) per batch element,
+    the reference activations and the oracle Scan1D. store_bf16 rounds the
+    activations to bf16 where the GPU path stores them. x [B, L, dim];
+    w: dict of numpy arrays (bf16-valued weights as fp32)."""
+    import oracle as O
+    rnd = bf16_round if store_bf16 else (lambda a: np.asarray(a, np.float32))
+    x = np.asarray(x, np.float32)
+    Bsz, L, dim = x.shape
+    W_in = w["W_in"]
+    di = W_in.shape[0] // 2
+    N = w["A"].shape[1]
+    R = w["W_dt"].shape[1]
+    T = Bsz * L
+    xf = x.reshape(T, dim)
+    xi = rnd(xf @ W_in[:di].T).reshape(Bsz, L, di)
+    z = rnd(xf @ W_in[di:].T).reshape(Bsz, L, di)
+    u = np.empty_like(xi)
+    for b in range(Bsz):
+        u[b] = silu_ref(O.convnd_forward((L,), xi[b], w["conv_w"], w.get("conv_b"), nthreads=8,
+                                         fast=True))
+    u = rnd(u)
+    xdbl = rnd(u.reshape(T, di) @ w["W_x"].T)
+    delta = rnd(softplus_ref(xdbl[:, :R] @ w["W_dt"].T + w["dt_bias"])).reshape(Bsz, L, di)
+    Bm = np.ascontiguousarray(xdbl[:, R:R + N].reshape(Bsz, L, N))
+    Cm = np.ascontiguousarray(xdbl[:, R + N:].reshape(Bsz, L, N))
+    ys, _, _ = O.scan1d_batched(u, delta, w["A"], Bm, Cm, clamp=clamp, nthreads=8, fast=True)
+    if w.get("Dskip") is not None:
+        ys = ys + w["Dskip"] * u
+    y = rnd(ys * silu_ref(z))
+    out = y.reshape(T, di) @ w["W_out"].T
+    return out.reshape(Bsz, L, dim).astype(np.float32)

@@ -1,0 +1,144 @@
+"""GPU parity of the bf16 MFMA GEMM and the configs[4] Mamba-1 block.
+
+GEMM: against a float64 product of the same bf16-valued operands,
+condition-scaled with kappa = |A| |B|^T + |bias| (tol 1e-4 for fp32 C, 2e-2
+for bf16 C).
+Block: no reference function exists for it; it is checked against the
+composition of the oracle pieces (tests/kmtest.py mamba1_block_ref) run in
+fp32 with the activations rounded to bf16 where the GPU stores them
+(normwise max error / max|ref| <= 1e-2), and against the plain fp32
+composition (<= 2e-2, the bf16 bound).
+"""
+import numpy as np
+import pytest
+
+import kmamba as K
+from kmtest import (TOL_BF16, TOL_F32, assert_close, bf16_round, mamba1_block_ref, rng_for,
+                    silu_ref, softplus_ref)
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    torch.zeros(1, device=DEV)
+    assert K.kmamba_cuda_available() == 1, K.km_last_error()
+
+
+def bf(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(DEV).to(torch.bfloat16)
+
+
+def f32(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(DEV)
+
+
+@pytest.mark.parametrize("M,N,Kd", [(128, 128, 64), (1, 1, 8), (130, 97, 72), (257, 300, 1024),
+                                    (1000, 96, 2048), (64, 2048, 64), (300, 33, 136)])
+@pytest.mark.parametrize("out_bf16", [False, True])
+def test_gemm_vs_float64(M, N, Kd, out_bf16):
+    g = rng_for("gemm", M, N, Kd)
+    A = bf16_round(g.standard_normal((M, Kd)).astype(np.float32))
+    B = bf16_round((g.standard_normal((N, Kd)) / np.sqrt(Kd)).astype(np.float32))
+    C = torch.full((M, N), float("nan"), device=DEV,
+                   dtype=torch.bfloat16 if out_bf16 else torch.float32)
+    K.gemm_bf16(bf(A), bf(B), C)
+    torch.cuda.synchronize()
+    ref = A.astype(np.float64) @ B.astype(np.float64).T
+    kap = np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64).T
+    assert_close(C.float().cpu().numpy(), ref, TOL_BF16 / 4 if out_bf16 else TOL_F32, "C", kap)
+
+
+@pytest.mark.parametrize("epi", [K.KM_EPI_NONE, K.KM_EPI_SOFTPLUS, K.KM_EPI_SILU])
+def test_gemm_strided_bias_epilogues(epi):
+    # A is a column slice of a wider buffer (lda > K), as dt_proj reads dt_low
+    # out of [dt_low | B | C]; C written into a wider buffer (ldc > N).
+    M, N, Kd, lda, ldc = 300, 200, 64, 96, 256
+    g = rng_for("gemm-epi", epi)
+    Abuf = bf16_round(g.standard_normal((M, lda)).astype(np.float32))
+    B = bf16_round((g.standard_normal((N, Kd)) / 8).astype(np.float32))
+    bias = g.standard_normal(N).astype(np.float32)
+    Cbuf = torch.full((M, ldc), 7.0, device=DEV)
+    K.gemm_bf16(bf(Abuf), bf(B), Cbuf, bias=f32(bias), epilogue=epi, M=M, N=N, K=Kd, lda=lda,
+                ldc=ldc)
+    torch.cuda.synchronize()
+    got = Cbuf.cpu().numpy()
+    assert (got[:, N:] == 7.0).all(), "wrote past N"
+    pre = Abuf[:, :Kd].astype(np.float64) @ B.astype(np.float64).T + bias
+    kap = np.abs(Abuf[:, :Kd]).astype(np.float64) @ np.abs(B).astype(np.float64).T + np.abs(bias)
+    if epi == K.KM_EPI_NONE:
+        assert_close(got[:, :N], pre, TOL_F32, "C", kap)
+    else:
+        fn = softplus_ref if epi == K.KM_EPI_SOFTPLUS else silu_ref
+        ref = fn(pre.astype(np.float32))
+        # the activation's own rounding dominates: compare with a 1e-5 floor
+        err = np.abs(got[:, :N] - ref) / np.maximum(np.abs(ref), 1e-2 * np.abs(ref).max())
+        assert err.max() < 1e-4, err.max()
+
+
+def test_gemm_rejects_bad_shapes():
+    A = torch.zeros((4, 12), device=DEV, dtype=torch.bfloat16)
+    B = torch.zeros((4, 12), device=DEV, dtype=torch.bfloat16)
+    C = torch.zeros((4, 4), device=DEV)
+    with pytest.raises(RuntimeError, match="multiples of 8"):
+        K.gemm_bf16(A, B, C)
+
+
+def block_weights(dim, di, N, dconv, R, seed=0, std=0.02):
+    g = rng_for("mamba1", dim, di, N, dconv, R, seed)
+    w = {
+        "W_in": bf16_round((g.standard_normal((2 * di, dim)) * std).astype(np.float32)),
+        "conv_w": (g.standard_normal((dconv, di)) * 0.5).astype(np.float32),
+        "conv_b": (g.standard_normal(di) * 0.1).astype(np.float32),
+        "W_x": bf16_round((g.standard_normal((R + 2 * N, di)) * std).astype(np.float32)),
+        "W_dt": bf16_round((g.standard_normal((di, R)) * std).astype(np.float32)),
+        "dt_bias": (g.standard_normal(di) * 0.5 - 2.0).astype(np.float32),
+        "A": -np.tile(np.arange(1, N + 1, dtype=np.float32), (di, 1)),
+        "Dskip": np.ones(di, np.float32),
+        "W_out": bf16_round((g.standard_normal((dim, di)) * std).astype(np.float32)),
+    }
+    return w
+
+
+def run_block(w, x):
+    tw = {k: (bf(v) if k.startswith("W_") else f32(v)) for k, v in w.items()}
+    out = torch.full(x.shape, float("nan"), device=DEV, dtype=torch.bfloat16)
+    K.mamba1_block_fwd(tw, bf(x), out)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def normwise(got, ref):
+    return float(np.abs(got - ref).max() / np.abs(ref).max())
+
+
+@pytest.mark.parametrize("Bsz,L,dim,di,N,dconv,R", [(2, 130, 64, 128, 16, 4, 8),
+                                                    (1, 64, 128, 256, 16, 3, 16),
+                                                    (3, 33, 64, 64, 8, 2, 8)])
+def test_block_vs_composed_oracle(Bsz, L, dim, di, N, dconv, R):
+    w = block_weights(dim, di, N, dconv, R, std=0.2)
+    x = bf16_round(rng_for("mx", Bsz, L, dim).standard_normal((Bsz, L, dim)).astype(np.float32))
+    got = run_block(w, x)
+    ref_b = mamba1_block_ref(x, w, store_bf16=True)
+    ref_f = mamba1_block_ref(x, w)
+    e_b, e_f = normwise(got, ref_b), normwise(got, ref_f)
+    assert e_b <= 1e-2, f"vs bf16-storage oracle {e_b:.3e}"
+    assert e_f <= TOL_BF16, f"vs fp32 oracle {e_f:.3e}"
+
+
+def test_config4_full_size_sampled():
+    # dim 1024, d_inner 2048, N 16, d_conv 4, dt_rank 64, B 8,
+    # L 2048, weights ~ N(0, 0.02), A = -(1..16), x ~ N(0, 1). The GPU runs
+    # the whole batch; batch element 0 is checked against the oracle.
+    Bsz, L, dim, di, N, dconv, R = 8, 2048, 1024, 2048, 16, 4, 64
+    w = block_weights(dim, di, N, dconv, R)
+    x = bf16_round(rng_for("mx4").standard_normal((Bsz, L, dim)).astype(np.float32))
+    got = run_block(w, x)
+    assert np.isfinite(got).all()
+    ref_b = mamba1_block_ref(x[:1], w, store_bf16=True)
+    e_b = normwise(got[:1], ref_b)
+    assert e_b <= 1e-2, f"vs bf16-storage oracle {e_b:.3e}"
