@@ -25,6 +25,8 @@
 //    from memory (same CU, just written).
 #include <cstdlib>
 
+#include <cstdio>
+
 #include "km_device.hpp"
 #include "../km_runtime.hpp"
 #include "kmamba_km.h"
@@ -53,24 +55,44 @@ struct ScanNDArgs {
     int ncg;                     // channel groups of 64 (d, m) lanes
 };
 
-// Tile band b, ordinal o: the o-th tile (lexicographic) with index sum b.
+// Number of pairs (u, v), 0 <= u < n1, 0 <= v < n2, with u + v = s.
+__device__ __forceinline__ int count2(int s, int n1, int n2) {
+    const int lo = max(0, s - (n2 - 1)), hi = min(s, n1 - 1);
+    return hi >= lo ? hi - lo + 1 : 0;
+}
+
+// Tile band b, ordinal o: the o-th tile, in lexicographic order of the tile
+// index tuple, whose indices sum to b (2 <= nd <= 4). Leading axes pick
+// their index by counting the tuples of the remaining axes; the last two
+// axes follow in closed form.
 __device__ inline bool band_tile(const ScanNDArgs &p, int ordinal, int *ti) {
-    int cnt = 0;
-    int total = 1;
-    for (int a = 0; a < p.nd; ++a) total *= p.ntile[a];
-    for (int lin = 0; lin < total; ++lin) {
-        int rem = lin, s = 0;
-        for (int a = p.nd - 1; a >= 0; --a) {
-            ti[a] = rem % p.ntile[a];
-            rem /= p.ntile[a];
-            s += ti[a];
+    int s = p.band, o = ordinal;
+    for (int a = 0; a + 2 < p.nd; ++a) {
+        bool found = false;
+        for (int v = 0; v < p.ntile[a] && v <= s; ++v) {
+            int c;
+            if (a + 3 == p.nd) {
+                c = count2(s - v, p.ntile[a + 1], p.ntile[a + 2]);
+            } else {
+                c = 0;
+                for (int w = 0; w < p.ntile[a + 1] && w <= s - v; ++w)
+                    c += count2(s - v - w, p.ntile[a + 2], p.ntile[a + 3]);
+            }
+            if (o < c) {
+                ti[a] = v;
+                s -= v;
+                found = true;
+                break;
+            }
+            o -= c;
         }
-        if (s == p.band) {
-            if (cnt == ordinal) return true;
-            ++cnt;
-        }
+        if (!found) return false;
     }
-    return false;
+    const int n1 = p.ntile[p.nd - 2], n2 = p.ntile[p.nd - 1];
+    if (o >= count2(s, n1, n2)) return false;
+    ti[p.nd - 2] = max(0, s - (n2 - 1)) + o;
+    ti[p.nd - 1] = s - ti[p.nd - 2];
+    return true;
 }
 
 // DPP lane move within rows of 16 lanes (ctrl: row_ror, mirrors, quad_perm).
@@ -122,8 +144,13 @@ struct NDRow {
 template <int ND, int TW, int MM>
 __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
     const int lane = threadIdx.x;
-    const int cg = blockIdx.x % p.ncg;
-    const int ordinal = blockIdx.x / p.ncg;
+    // Workgroups are dealt to the 8 XCDs round-robin; renumber them so that
+    // consecutive channel groups of a tile, which share x / delta cache
+    // lines (4 channels = 16 bytes of a row each), run on one XCD's L2.
+    const int nb = gridDim.x, q = nb / 8, r = nb % 8, xcd = blockIdx.x % 8;
+    const int lb = xcd * q + min(xcd, r) + static_cast<int>(blockIdx.x / 8);
+    const int cg = lb % p.ncg;
+    const int ordinal = lb / p.ncg;
     int ti[kMaxNd];
     if (!band_tile(p, ordinal, ti)) return;
 
@@ -185,7 +212,10 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
             }
         }
         // Neighbours along leading axes, and along the row axis on the tile's
-        // first row of a plane (tile boundary); uniform conditions.
+        // first row of a plane (tile boundary); uniform conditions. Rows are
+        // prefetched one row ahead, so a leading-axis neighbour inside the
+        // tile must lie at least two rows back: the launcher never builds a
+        // tile with a single row per plane below an in-tile leading axis.
         const float *hb = p.h + pb * DM + f;
 #pragma unroll
         for (int a = 0; a < ND - 1; ++a) {
@@ -293,16 +323,46 @@ __global__ void __launch_bounds__(256) scannd_level_kernel(ScanNDArgs p, const l
 static long *g_plan_dev = nullptr;
 static size_t g_plan_cap = 0;
 
+// Tuning knob (read once): KM_SCANND_T2 / KM_SCANND_T3 = "TW,TL" sets the
+// 2D / 3D tile to TW points along the last axis (4, 8 or 16 in 2D; 4 or 8 in
+// 3D) and TL along each leading axis.
+static void scannd_tile_shape(int nd, int &tw, int &tl) {
+    static int t2w = 0, t2l = 0, t3w = 0, t3l = 0;
+    static bool once = [] {
+        auto parse = [](const char *e, int &w, int &l) {
+            if (e && std::sscanf(e, "%d,%d", &w, &l) != 2) w = l = 0;
+        };
+        parse(std::getenv("KM_SCANND_T2"), t2w, t2l);
+        parse(std::getenv("KM_SCANND_T3"), t3w, t3l);
+        return true;
+    }();
+    (void)once;
+    if (nd == 2 && (t2w == 4 || t2w == 8 || t2w == 16) && t2l > 0 && t2l <= 64) { tw = t2w; tl = t2l; }
+    if (nd == 3 && (t3w == 4 || t3w == 8) && t3l > 0 && t3l <= 64) { tw = t3w; tl = t3l; }
+}
+
 static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s) {
     const bool fast = (a.DM % 64 == 0) && (64 % a.M == 0) && a.nd >= 2 && a.nd <= 4;
     if (fast) {
-        // Tiles: 2D 16 rows x 16 columns; 3D and up 8 per axis. One wave
-        // per (tile, channel group); one launch per tile band.
-        const int TWc = (a.nd == 2) ? 16 : 8;
-        const int Tlead = (a.nd == 2) ? 16 : 8;
+        // Tiles: rows of TWc points along the last axis, Tlead along each
+        // leading axis. One wave per (tile, channel group); one launch per
+        // tile band.
+        // Defaults measured fastest on MI355X at configs[2]: 2D rows of 8
+        // points x 6 rows; 3D and up rows of 4 points x 4 per leading axis.
+        int TWc = (a.nd == 2) ? 8 : 4;
+        int Tlead = (a.nd == 2) ? 6 : 4;
+        scannd_tile_shape(a.nd, TWc, Tlead);
+        // Rows are prefetched one ahead, so every tile needs at least two
+        // rows per plane below an in-tile leading axis: grow the row-axis
+        // tile while its last tile would hold one row, and use tiles of 1
+        // along the leading axes when the row axis has length 1.
+        const int rax = a.nd - 2;
+        int trow = (a.dims[rax] < Tlead) ? a.dims[rax] : Tlead;
+        while (trow < a.dims[rax] && a.dims[rax] % trow == 1) ++trow;
         int nbands = 1;
         for (int ax = 0; ax < a.nd; ++ax) {
-            const int t = (ax == a.nd - 1) ? TWc : Tlead;
+            int t = (ax == a.nd - 1) ? TWc : (ax == rax ? trow : Tlead);
+            if (ax < rax && a.dims[rax] == 1) t = 1;
             a.tile[ax] = (a.dims[ax] < t) ? a.dims[ax] : t;
             a.ntile[ax] = (a.dims[ax] + a.tile[ax] - 1) / a.tile[ax];
             nbands += a.ntile[ax] - 1;
@@ -341,11 +401,15 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s) {
             default: KM_ND_LAUNCH(NDv, TWv, 64); break;       \
             }
             if (a.nd == 2) {
-                KM_ND_BY_M(2, 16)
+                if (TWc == 4) { KM_ND_BY_M(2, 4) }
+                else if (TWc == 8) { KM_ND_BY_M(2, 8) }
+                else { KM_ND_BY_M(2, 16) }
             } else if (a.nd == 3) {
-                KM_ND_BY_M(3, 8)
+                if (TWc == 4) { KM_ND_BY_M(3, 4) }
+                else { KM_ND_BY_M(3, 8) }
             } else {
-                KM_ND_BY_M(4, 8)
+                if (TWc == 4) { KM_ND_BY_M(4, 4) }
+                else { KM_ND_BY_M(4, 8) }
             }
 #undef KM_ND_BY_M
 #undef KM_ND_LAUNCH

@@ -93,7 +93,11 @@ def test_known_answers_all_entry_points():
 
 CASES = [((7, 5), 3, 4), ((40, 70), 4, 16), ((33, 65), 8, 16), ((1, 90), 4, 16), ((90, 1), 4, 16),
          ((5, 18, 20), 4, 16), ((3, 4, 5, 6), 4, 16), ((6, 7, 9), 3, 3), ((17, 33), 2, 32),
-         ((100,), 4, 16), ((64, 64), 64, 1)]
+         ((100,), 4, 16), ((64, 64), 64, 1),
+         # ragged tiles with a single row per plane and length-1 row axes
+         # (the default 3D / 4D tiles are 4 per leading axis, 2D rows 6):
+         ((7, 5, 10), 4, 16), ((5, 1, 9), 4, 16), ((10, 9, 13), 4, 16), ((5, 5, 5, 9), 4, 16),
+         ((3, 1, 4, 5), 4, 16), ((13, 25), 4, 16), ((2, 1, 1, 6), 4, 16)]
 
 
 @pytest.mark.parametrize("dims,D,M", CASES)
