@@ -112,6 +112,28 @@ class KMMamba1Weights(C.Structure):       # include/kmamba_km.h
                                           "A", "Dskip", "W_out")] + [("clamp", C.c_int)]
 
 
+class MBMatrix(C.Structure):              # include/kmamba.h (ref include/kmamba.h:17-24)
+    _fields_ = [("data", C.POINTER(C.c_float)), ("rows", C.c_size_t), ("cols", C.c_size_t)]
+
+
+class MBConfig(C.Structure):              # ref include/kmamba.h:27-54
+    _fields_ = [(n, C.c_size_t) for n in ("dim", "state_size", "seq_len", "mimo_rank")] + \
+               [(n, C.c_float) for n in ("dt_scale", "dt_min", "dt_max")] + \
+               [("use_fp16", C.c_int), ("use_bf16", C.c_int), ("loss_scale", C.c_float),
+                ("spatial_ndims", C.c_long), ("spatial_dims", C.c_long * 8),
+                ("use_convnd", C.c_int), ("convnd_K", C.c_long), ("convnd_ndims", C.c_long)]
+
+
+class MambaBlock(C.Structure):            # ref include/kmamba.h:116-150
+    _fields_ = [("config", MBConfig)] + \
+               [(n, MBMatrix) for n in ("W_in", "W_out", "A_log", "W_B", "W_C", "delta_proj")] + \
+               [(n, C.POINTER(C.c_float)) for n in ("b_B", "b_C", "theta")] + \
+               [("lambda_proj", MBMatrix), ("wavefront_plan", C.c_void_p)] + \
+               [(n, C.POINTER(C.c_float)) for n in ("convnd_kernel", "convnd_bias", "hidden",
+                                                   "delta", "scan_B", "scan_C", "scan_delta",
+                                                   "scan_h")] + [("opt_state", C.c_void_p)]
+
+
 VisitFn = C.CFUNCTYPE(C.c_int, c_long_p, C.c_long, C.c_long, C.c_long, C.c_void_p)
 
 
@@ -338,6 +360,14 @@ def mamba1_block_fwd(w, x, out, *, workspace=None, clamp=True, stream=None):
     nb = 0 if workspace is None else workspace.numel() * workspace.element_size()
     check(km_mamba1_block_fwd_c(C.byref(ws), ptr(x), ptr(out), Bsz, L, ptr(workspace), nb,
                                 C.c_void_p(stream_handle(stream))), "km_mamba1_block_fwd")
+
+
+# --- Mamba-3 block -------------------------------------------------------------
+mamba_block_create = _decl("mamba_block_create", C.POINTER(MambaBlock), [C.POINTER(MBConfig)])
+mamba_block_free = _decl("mamba_block_free", None, [C.POINTER(MambaBlock)])
+mamba_block_init = _decl("mamba_block_init", None, [C.POINTER(MambaBlock)])
+mamba_block_forward = _decl("mamba_block_forward", None,
+                            [C.POINTER(MambaBlock), C.c_void_p, C.c_void_p, C.c_size_t])
 
 
 # --- ScanND / Scan2D ----------------------------------------------------------

@@ -644,3 +644,104 @@ void orc_convnd_backward(OrcConvNDParams *p) {
     }
     orc_plan_free(pl);
 }
+
+
+/* ======================================================================
+ * Mamba-3 block forward: src/mamba_block.c:89-120 (controller), :413-466
+ * (scan), :471-501 (forward). gemv rows sum j = 0..D-1 in order
+ * (kernels/gemm_f32.c:48-58); SiLU, softplus, sigmoid as
+ * include/kmamba_kernels.h:35-49.
+ * ====================================================================== */
+static void m3_gemv(const float *A, const float *x, float *y, long M, long N) {
+    for (long i = 0; i < M; i++) {                      /* gemm_f32.c:51-57 */
+        float sum = 0.0f;
+        for (long j = 0; j < N; j++) sum += A[i * N + j] * x[j];
+        y[i] = sum;
+    }
+}
+
+void orc_mamba3_forward(const OrcMamba3 *p, const float *input, float *output, long batch) {
+    if (!p || !input || !output) return;
+    long L = p->L, D = p->D, N = p->N, R = p->R > 1 ? p->R : 1, NR = N * R;
+    float *z = malloc((size_t)R * sizeof(float));
+    float *u = malloc((size_t)(L * R) * sizeof(float));
+    float *dl = malloc((size_t)L * sizeof(float));
+    float *lam = malloc((size_t)L * sizeof(float));
+    float *Bs = malloc((size_t)(L * NR) * sizeof(float));
+    float *Cs = malloc((size_t)(L * NR) * sizeof(float));
+    float *y = malloc((size_t)(L * R) * sizeof(float));
+    float *yp = malloc((size_t)D * sizeof(float));
+    float *h = malloc((size_t)N * sizeof(float));
+    float *hr = malloc((size_t)N * sizeof(float));
+    float *bu = malloc((size_t)N * sizeof(float));
+    float *pbu = malloc((size_t)N * sizeof(float));
+    if (!z || !u || !dl || !lam || !Bs || !Cs || !y || !yp || !h || !hr || !bu || !pbu) goto out;
+    for (long b = 0; b < batch; b++) {
+        const float *in = input + b * L * D;
+        float *o = output + b * L * D;
+        for (long t = 0; t < L; t++) {
+            const float *xt = in + t * D;
+            m3_gemv(p->W_in, xt, z, R, D);                               /* :98-99 */
+            for (long r = 0; r < R; r++) u[t * R + r] = z[r] / (1.0f + expf(-z[r]));
+            if (p->delta_proj) {                                         /* :102-108 */
+                float dv;
+                m3_gemv(p->delta_proj, xt, &dv, 1, D);
+                dv = logf(1.0f + expf(dv));
+                if (dv < p->dt_min) dv = p->dt_min;
+                if (dv > p->dt_max) dv = p->dt_max;
+                dl[t] = dv;
+            } else {
+                dl[t] = p->dt_scale;
+            }
+            if (p->lambda_proj) {                                        /* :112-118 */
+                float lr;
+                m3_gemv(p->lambda_proj, xt, &lr, 1, D);
+                lam[t] = 1.0f / (1.0f + expf(-lr));
+            } else {
+                lam[t] = 0.5f;
+            }
+            m3_gemv(p->W_B, xt, Bs + t * NR, NR, D);                     /* :488-493 */
+            m3_gemv(p->W_C, xt, Cs + t * NR, NR, D);
+            for (long i = 0; i < NR; i++) {
+                Bs[t * NR + i] += p->b_B[i];
+                Cs[t * NR + i] += p->b_C[i];
+            }
+        }
+        memset(h, 0, (size_t)N * sizeof(float));                        /* :422 */
+        memset(pbu, 0, (size_t)N * sizeof(float));
+        for (long t = 0; t < L; t++) {
+            float dt = dl[t], lt = lam[t];
+            const float *bt = Bs + t * NR, *ct = Cs + t * NR, *ut = u + t * R;
+            for (long i = 0; i + 1 < N; i += 2) {                        /* :431-437 */
+                float th = p->theta[i >> 1], cv = cosf(th), sv = sinf(th);
+                float h0 = h[i], h1 = h[i + 1];
+                hr[i] = cv * h0 - sv * h1;
+                hr[i + 1] = sv * h0 + cv * h1;
+            }
+            if (N & 1) hr[N - 1] = h[N - 1];
+            memset(bu, 0, (size_t)N * sizeof(float));                   /* :440-443 */
+            for (long r = 0; r < R; r++)
+                for (long n = 0; n < N; n++) bu[n] += bt[r * N + n] * ut[r];
+            for (long n = 0; n < N; n++) {                               /* :446-452 */
+                float a = p->A_log[n];
+                float alpha = expf(dt * a);
+                float beta = (1.0f - lt) * dt * alpha;
+                float gamma = lt * dt;
+                h[n] = alpha * hr[n] + beta * pbu[n] + gamma * bu[n];
+            }
+            for (long r = 0; r < R; r++) {                               /* :455-459 */
+                float yr = 0.0f;
+                for (long n = 0; n < N; n++) yr += ct[r * N + n] * h[n];
+                y[t * R + r] = yr;
+            }
+            memcpy(pbu, bu, (size_t)N * sizeof(float));                 /* :462 */
+        }
+        for (long t = 0; t < L; t++) {                                   /* :496-499 */
+            m3_gemv(p->W_out, y + t * R, yp, D, R);
+            for (long d = 0; d < D; d++) o[t * D + d] = in[t * D + d] + yp[d];
+        }
+    }
+out:
+    free(z); free(u); free(dl); free(lam); free(Bs); free(Cs); free(y); free(yp);
+    free(h); free(hr); free(bu); free(pbu);
+}

@@ -91,6 +91,22 @@ long orc_convnd_kernel_volume(long ndims, long K);
 void orc_convnd_forward(OrcConvNDParams *p, int nthreads);
 void orc_convnd_backward(OrcConvNDParams *p);
 
+/* ---- Mamba-3 block forward -------------------------------------------- */
+/* Parameters of one MambaBlock (ref include/kmamba.h:116-150) as plain
+ * arrays: W_in [R, D], W_out [D, R], A_log [N], W_B / W_C [N*R, D],
+ * delta_proj / lambda_proj [D] (NULL = absent), b_B / b_C [N*R],
+ * theta [N/2]. */
+typedef struct {
+    const float *W_in, *W_out, *A_log, *W_B, *W_C, *delta_proj, *lambda_proj;
+    const float *b_B, *b_C, *theta;
+    long L, D, N, R;
+    float dt_scale, dt_min, dt_max;
+} OrcMamba3;
+
+/* mamba_block_forward_ws (ref src/mamba_block.c:471-501) for input and
+ * output [batch, L, D]. */
+void orc_mamba3_forward(const OrcMamba3 *p, const float *input, float *output, long batch);
+
 /* ---- Wavefront / plan / topology -------------------------------------- */
 int  orc_wavefront_validate_dims(const long *dims, long ndims);
 long orc_wavefront_total_points(const long *dims, long ndims);

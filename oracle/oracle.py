@@ -340,3 +340,100 @@ def plan_tables(dims, use_ref=False):
     mls = p.max_level_size
     free(pl)
     return starts, offs, mls
+
+
+# ---------------------------------------------------------------------------
+# Mamba-3 block forward
+# ---------------------------------------------------------------------------
+class MBMatrix(C.Structure):              # ref include/kmamba.h:17-24
+    _fields_ = [("data", C.POINTER(C.c_float)), ("rows", C.c_size_t), ("cols", C.c_size_t)]
+
+
+class MBConfig(C.Structure):              # ref include/kmamba.h:27-54
+    _fields_ = [(n, C.c_size_t) for n in ("dim", "state_size", "seq_len", "mimo_rank")] + \
+               [(n, C.c_float) for n in ("dt_scale", "dt_min", "dt_max")] + \
+               [("use_fp16", C.c_int), ("use_bf16", C.c_int), ("loss_scale", C.c_float),
+                ("spatial_ndims", C.c_long), ("spatial_dims", C.c_long * 8),
+                ("use_convnd", C.c_int), ("convnd_K", C.c_long), ("convnd_ndims", C.c_long)]
+
+
+class MambaBlock(C.Structure):            # ref include/kmamba.h:116-150
+    _fields_ = [("config", MBConfig)] + \
+               [(n, MBMatrix) for n in ("W_in", "W_out", "A_log", "W_B", "W_C", "delta_proj")] + \
+               [(n, C.POINTER(C.c_float)) for n in ("b_B", "b_C", "theta")] + \
+               [("lambda_proj", MBMatrix), ("wavefront_plan", vp)] + \
+               [(n, C.POINTER(C.c_float)) for n in ("convnd_kernel", "convnd_bias", "hidden",
+                                                   "delta", "scan_B", "scan_C", "scan_delta",
+                                                   "scan_h")] + [("opt_state", vp)]
+
+
+class OrcMamba3(C.Structure):
+    _fields_ = [(n, vp) for n in ("W_in", "W_out", "A_log", "W_B", "W_C", "delta_proj",
+                                  "lambda_proj", "b_B", "b_C", "theta")] + \
+               [(n, C.c_long) for n in ("L", "D", "N", "R")] + \
+               [(n, C.c_float) for n in ("dt_scale", "dt_min", "dt_max")]
+
+
+MAMBA3_PARAMS = ("W_in", "W_out", "A_log", "W_B", "W_C", "delta_proj", "lambda_proj", "b_B", "b_C",
+                 "theta")
+
+_sig(orc, "orc_mamba3_forward", None, [C.POINTER(OrcMamba3), vp, vp, C.c_long])
+if ref is not None:
+    _sig(ref, "mamba_block_create", C.POINTER(MambaBlock), [C.POINTER(MBConfig)])
+    _sig(ref, "mamba_block_free", None, [C.POINTER(MambaBlock)])
+    _sig(ref, "mamba_block_init", None, [C.POINTER(MambaBlock)])
+    _sig(ref, "mamba_block_forward", None, [C.POINTER(MambaBlock), vp, vp, C.c_size_t])
+
+
+def mb_config(dim, N, L, R=1, dt_scale=0.1, dt_min=1e-3, dt_max=0.1):
+    cfg = MBConfig()
+    cfg.dim, cfg.state_size, cfg.seq_len, cfg.mimo_rank = dim, N, L, R
+    cfg.dt_scale, cfg.dt_min, cfg.dt_max = dt_scale, dt_min, dt_max
+    return cfg
+
+
+def block_params(blk):
+    """Copies of a MambaBlock's parameter arrays (numpy, fp32)."""
+    b = blk.contents
+    N, R = b.config.state_size, max(b.config.mimo_rank, 1)
+    out = {}
+    for name in ("W_in", "W_out", "A_log", "W_B", "W_C", "delta_proj", "lambda_proj"):
+        m = getattr(b, name)
+        out[name] = np.ctypeslib.as_array(m.data, shape=(m.rows * m.cols,)).reshape(m.rows, m.cols).copy()
+    out["b_B"] = np.ctypeslib.as_array(b.b_B, shape=(N * R,)).copy()
+    out["b_C"] = np.ctypeslib.as_array(b.b_C, shape=(N * R,)).copy()
+    out["theta"] = np.ctypeslib.as_array(b.theta, shape=(max(N // 2, 1),)).copy()
+    return out
+
+
+def set_block_params(blk, params):
+    """Writes parameter arrays into a MambaBlock's buffers."""
+    b = blk.contents
+    for name in ("W_in", "W_out", "A_log", "W_B", "W_C", "delta_proj", "lambda_proj"):
+        m = getattr(b, name)
+        dst = np.ctypeslib.as_array(m.data, shape=(m.rows * m.cols,))
+        dst[:] = f32(params[name]).ravel()
+    for name in ("b_B", "b_C", "theta"):
+        src = f32(params[name]).ravel()
+        np.ctypeslib.as_array(getattr(b, name), shape=(src.size,))[:] = src
+
+
+def mamba3_forward(params, x, *, dt_scale=0.1, dt_min=1e-3, dt_max=0.1, use_ref=False):
+    """Mamba-3 block forward (src/mamba_block.c:471-501): x [batch, L, D]."""
+    x = f32(x)
+    batch, L, D = x.shape
+    N = params["A_log"].size
+    R = params["W_in"].shape[0]
+    out = np.zeros_like(x)
+    if use_ref:
+        blk = ref.mamba_block_create(C.byref(mb_config(D, N, L, R, dt_scale, dt_min, dt_max)))
+        if not blk:
+            raise RuntimeError("reference mamba_block_create failed")
+        set_block_params(blk, params)
+        ref.mamba_block_forward(blk, P(out), P(x), batch)
+        ref.mamba_block_free(blk)
+        return out
+    keep = {k: f32(v) for k, v in params.items()}
+    p = OrcMamba3(*(P(keep[k]) for k in MAMBA3_PARAMS), L, D, N, R, dt_scale, dt_min, dt_max)
+    orc.orc_mamba3_forward(C.byref(p), P(x), P(out), batch)
+    return out

@@ -257,3 +257,56 @@ def test_no_gpu_reports_error():
     args.x = args.delta = args.A = args.Bm = args.Cm = args.y = 1
     assert K.km_scan1d_fwd_c(C.byref(args), None) == -1
     assert "HIP device" in K.km_last_error()
+
+
+# ---------------------------------------------------------------------------
+# Mamba-3 block: create / init / free (host side, no GPU needed)
+# ---------------------------------------------------------------------------
+def _mb_cfg(lib_cfg_cls, dim=12, N=6, L=10, R=2):
+    cfg = lib_cfg_cls()
+    cfg.dim, cfg.state_size, cfg.seq_len, cfg.mimo_rank = dim, N, L, R
+    cfg.dt_scale, cfg.dt_min, cfg.dt_max = 0.1, 1e-3, 0.1
+    return cfg
+
+
+def test_mamba_block_layout_matches_reference_header():
+    # MBConfig / MambaBlock field offsets (ref include/kmamba.h:27-54, :116-150).
+    assert C.sizeof(K.MBConfig) == C.sizeof(O.MBConfig) == 152
+    assert C.sizeof(K.MambaBlock) == C.sizeof(O.MambaBlock)
+    for name, _ in K.MambaBlock._fields_:
+        assert getattr(K.MambaBlock, name).offset == getattr(O.MambaBlock, name).offset, name
+
+
+@needs_ref
+@pytest.mark.parametrize("dim,N,L,R", [(12, 6, 10, 2), (8, 16, 4, 1), (5, 3, 7, 0)])
+def test_mamba_block_create_and_init_match_reference(dim, N, L, R):
+    libc = C.CDLL(None)
+    ours = K.mamba_block_create(C.byref(_mb_cfg(K.MBConfig, dim, N, L, R)))
+    theirs = O.ref.mamba_block_create(C.byref(_mb_cfg(O.MBConfig, dim, N, L, R)))
+    assert ours and theirs
+    a, b = ours.contents, theirs.contents
+    assert a.config.mimo_rank == b.config.mimo_rank == max(R, 1)
+    assert a.config.spatial_ndims == b.config.spatial_ndims == 1
+    assert a.config.spatial_dims[0] == b.config.spatial_dims[0] == L
+    for name in ("W_in", "W_out", "A_log", "W_B", "W_C", "delta_proj", "lambda_proj"):
+        ma, mb = getattr(a, name), getattr(b, name)
+        assert (ma.rows, ma.cols) == (mb.rows, mb.cols), name
+    # same rand() stream -> bit-identical initial parameters
+    libc.srand(1234)
+    K.mamba_block_init(ours)
+    libc.srand(1234)
+    O.ref.mamba_block_init(theirs)
+    pa, pb = O.block_params(C.cast(ours, C.POINTER(O.MambaBlock))), O.block_params(theirs)
+    for k in pa:
+        np.testing.assert_array_equal(pa[k], pb[k], err_msg=k)
+    K.mamba_block_free(ours)
+    O.ref.mamba_block_free(theirs)
+
+
+def test_mamba_block_create_rejects_bad_topology():
+    cfg = _mb_cfg(K.MBConfig, L=10)
+    cfg.spatial_ndims = 2
+    cfg.spatial_dims[0], cfg.spatial_dims[1] = 3, 4          # 12 != seq_len
+    assert not K.mamba_block_create(C.byref(cfg))
+    assert "topology" in K.km_last_error()
+    K.mamba_block_free(None)

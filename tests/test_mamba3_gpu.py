@@ -1,0 +1,96 @@
+"""GPU parity of the Mamba-3 block forward (mamba_block_forward, the
+reference src/mamba_block.c:471-501) against the oracle restatement, which
+is bit-exact to the compiled reference (test_oracle_pins.py).
+
+Metric: the block's contribution out - x (the residual is exact) compared
+normwise: max |got - ref| / max |ref| <= 1e-4 (fp32).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import kmamba as K
+import oracle as O
+from kmtest import rng_for
+from test_oracle_pins import mamba3_params
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    torch.zeros(1, device="cuda")
+    assert K.kmamba_cuda_available() == 1, K.km_last_error()
+
+
+def make_block(D, N, L, R, params, dt_min=0.01, dt_max=0.5):
+    cfg = K.MBConfig()
+    cfg.dim, cfg.state_size, cfg.seq_len, cfg.mimo_rank = D, N, L, R
+    cfg.dt_scale, cfg.dt_min, cfg.dt_max = 0.1, dt_min, dt_max
+    blk = K.mamba_block_create(C.byref(cfg))
+    assert blk, K.km_last_error()
+    O.set_block_params(C.cast(blk, C.POINTER(O.MambaBlock)), params)
+    return blk
+
+
+def check(got, want, x, tol=1e-4):
+    dg, dw = got - x, want - x
+    err = np.abs(dg - dw).max() / max(np.abs(dw).max(), 1e-30)
+    assert err <= tol, f"normwise error of out - x: {err:.3e}"
+    return err
+
+
+@pytest.mark.parametrize("D,N,L,R,batch", [(24, 8, 37, 2, 3), (16, 16, 64, 1, 2), (10, 7, 20, 1, 1),
+                                           (33, 4, 9, 3, 2), (8, 1, 5, 1, 1), (64, 16, 300, 1, 4)])
+def test_forward_host_pointers_vs_oracle(D, N, L, R, batch):
+    p = mamba3_params(D, N, R)
+    x = rng_for("m3x", D, N, L).standard_normal((batch, L, D)).astype(np.float32)
+    want = O.mamba3_forward(p, x, dt_min=0.01, dt_max=0.5)
+    blk = make_block(D, N, L, R, p)
+    out = np.full_like(x, np.nan)
+    K.mamba_block_forward(blk, K.ptr(out), K.ptr(x), batch)
+    assert K.km_last_error() == ""
+    check(out, want, x)
+    K.mamba_block_free(blk)
+
+
+def test_forward_device_pointers_and_reference_init():
+    # Parameters from mamba_block_init (the reference's rand() initialisation).
+    D, N, L, R, batch = 128, 16, 512, 1, 2
+    cfg = K.MBConfig()
+    cfg.dim, cfg.state_size, cfg.seq_len, cfg.mimo_rank = D, N, L, R
+    cfg.dt_scale, cfg.dt_min, cfg.dt_max = 0.1, 1e-3, 0.1
+    blk = K.mamba_block_create(C.byref(cfg))
+    C.CDLL(None).srand(7)
+    K.mamba_block_init(blk)
+    p = O.block_params(C.cast(blk, C.POINTER(O.MambaBlock)))
+    x = rng_for("m3dev").standard_normal((batch, L, D)).astype(np.float32)
+    want = O.mamba3_forward(p, x, dt_min=1e-3, dt_max=0.1)
+    tx = torch.from_numpy(x).cuda()
+    tout = torch.empty_like(tx)
+    K.mamba_block_forward(blk, K.ptr(tout), K.ptr(tx), batch)
+    assert K.km_last_error() == ""
+    check(tout.cpu().numpy(), want, x)
+    K.mamba_block_free(blk)
+
+
+def test_forward_rejects_invalid():
+    K.mamba_block_forward(None, None, None, 1)
+    assert "invalid" in K.km_last_error()
+
+
+def test_forward_larger_model_sampled():
+    # dim 1024, N 16, L 2048 (the configs[4] sequence and width), batch 2.
+    D, N, L, R, batch = 1024, 16, 2048, 1, 2
+    p = mamba3_params(D, N, R, seed=3)
+    x = rng_for("m3big").standard_normal((batch, L, D)).astype(np.float32)
+    blk = make_block(D, N, L, R, p)
+    out = np.empty_like(x)
+    K.mamba_block_forward(blk, K.ptr(out), K.ptr(x), batch)
+    assert K.km_last_error() == ""
+    want = O.mamba3_forward(p, x[:1], dt_min=0.01, dt_max=0.5)
+    check(out[:1], want, x[:1])
+    K.mamba_block_free(blk)

@@ -450,3 +450,63 @@ def test_plan_bit_exact_vs_reference(dims):
     np.testing.assert_array_equal(mine[0], theirs[0])
     np.testing.assert_array_equal(mine[1], theirs[1])
     assert mine[2] == theirs[2]
+
+
+def mamba3_params(D, N, R, seed=0):
+    g = rng_for("mamba3", D, N, R, seed)
+    s = np.float32(1.0 / np.sqrt(D))
+    return {"W_in": (g.standard_normal((R, D)) * s).astype(np.float32),
+            "W_out": (g.standard_normal((D, R)) * 0.3).astype(np.float32),
+            "A_log": -g.uniform(0.2, 2.0, N).astype(np.float32),
+            "W_B": (g.standard_normal((N * R, D)) * s).astype(np.float32),
+            "W_C": (g.standard_normal((N * R, D)) * s).astype(np.float32),
+            "delta_proj": (g.standard_normal((1, D)) * s).astype(np.float32),
+            "lambda_proj": (g.standard_normal((1, D)) * s).astype(np.float32),
+            "b_B": (g.standard_normal(N * R) * 0.1).astype(np.float32),
+            "b_C": (g.standard_normal(N * R) * 0.1).astype(np.float32),
+            "theta": g.uniform(0, 2 * np.pi / N, max(N // 2, 1)).astype(np.float32)}
+
+
+@needs_ref
+@pytest.mark.parametrize("D,N,L,R,batch", [(24, 8, 37, 2, 3), (16, 16, 64, 1, 2), (10, 7, 20, 1, 1),
+                                           (33, 4, 9, 3, 2), (8, 1, 5, 1, 1)])
+def test_mamba3_forward_bit_exact_vs_reference(D, N, L, R, batch):
+    # src/mamba_block.c:471-501 compiled in place; same parameters written
+    # into a block made by the reference's mamba_block_create.
+    p = mamba3_params(D, N, R)
+    x = rng_for("m3x", D, N, L).standard_normal((batch, L, D)).astype(np.float32)
+    got = O.mamba3_forward(p, x, dt_min=0.01, dt_max=0.5)
+    want = O.mamba3_forward(p, x, dt_min=0.01, dt_max=0.5, use_ref=True)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_mamba3_forward_closed_forms():
+    # With B = C = 0 (zero weights and biases) the state stays zero and the
+    # block is the identity (the residual); with theta = 0, lambda = 1 and a
+    # single constant input the state follows h_t = a h_{t-1} + dt*Bu.
+    D, N, L = 6, 4, 12
+    p = mamba3_params(D, N, 1)
+    for k in ("W_B", "W_C", "b_B", "b_C"):
+        p[k] = np.zeros_like(p[k])
+    x = rng_for("m3cf").standard_normal((2, L, D)).astype(np.float32)
+    np.testing.assert_array_equal(O.mamba3_forward(p, x), x)
+    # constant drive, no rotation: compare with the float64 recurrence
+    p = mamba3_params(D, N, 1, seed=1)
+    p["theta"][:] = 0
+    x1 = np.tile(rng_for("m3c").standard_normal(D).astype(np.float32), (1, L, 1))
+    out = O.mamba3_forward(p, x1, dt_min=1e-4, dt_max=10.0).astype(np.float64)
+    xt = x1[0, 0].astype(np.float64)
+    z = p["W_in"].astype(np.float64) @ xt
+    u = z / (1 + np.exp(-z))
+    dt = np.log1p(np.exp(p["delta_proj"].astype(np.float64) @ xt))[0]
+    lam = 1 / (1 + np.exp(-(p["lambda_proj"].astype(np.float64) @ xt)[0]))
+    Bt = p["W_B"].astype(np.float64) @ xt + p["b_B"]
+    Ct = p["W_C"].astype(np.float64) @ xt + p["b_C"]
+    bu = Bt * u[0]
+    alpha = np.exp(dt * p["A_log"].astype(np.float64))
+    h = np.zeros(N)
+    for t in range(L):
+        h = alpha * h + (1 - lam) * dt * alpha * (bu if t > 0 else 0) + lam * dt * bu
+        y = Ct @ h
+        want = xt + p["W_out"][:, 0] * y
+        np.testing.assert_allclose(out[0, t], want, rtol=2e-5, atol=2e-6)
