@@ -27,6 +27,7 @@
 //    its whole sequence with the sequential clamped recurrence, so results
 //    follow the per-step clamp exactly.
 #include <cstdlib>
+#include <type_traits>
 
 #include "km_device.hpp"
 #include "../km_runtime.hpp"
@@ -115,31 +116,28 @@ __device__ void scan1d_serial_wave(const Scan1DFwdArgs &p, long b, long d, bool 
     }
 }
 
-// Powers e1^(n0+1), ..., e1^(n0+NPL) of a lane's state group, n0 = ns*NPL:
-// the decays exp(delta*A[d,n]) when A[d,n] = (n+1)*A[d,0] (S4D-real
-// initialisation). Branch-free: the power e1^n0 is assembled from the
-// squarings e1^NPL, e1^(2*NPL), ... selected by the bits of n0.
+// Decays of a lane's states n = NS*j + ns (states interleaved over the NS
+// lane groups of a channel) when A[d, n] = (n+1) A[d, 0]: e1^(n+1) =
+// e1^(ns+1) * (e1^NS)^j, one multiply per state after the base.
 template <int NPL, int NS>
-__device__ __forceinline__ void pow_chain(float e1, int n0, float (&e)[NPL]) {
-    float pw = e1;
-    if constexpr (NS > 1) {
-        float sq = e1;
+__device__ __forceinline__ void pow_chain_il(float e1, int ns, float (&e)[NPL]) {
+    float pw[NS];
+    pw[0] = e1;
 #pragma unroll
-        for (int k = 1; k < NPL; k <<= 1) sq *= sq;          // e1^NPL
+    for (int i = 1; i < NS; ++i) pw[i] = pw[i - 1] * e1;
+    float base = pw[0];
 #pragma unroll
-        for (int bit = NPL; bit < NPL * NS; bit <<= 1) {
-            pw *= (n0 & bit) ? sq : 1.0f;
-            sq *= sq;
-        }
-    }
-    e[0] = pw;
+    for (int i = 1; i < NS; ++i) base = (ns == i) ? pw[i] : base;
+    const float step = pw[NS - 1];
+    e[0] = base;
 #pragma unroll
-    for (int j = 1; j < NPL; ++j) e[j] = e[j - 1] * e1;
+    for (int j = 1; j < NPL; ++j) e[j] = e[j - 1] * step;
 }
 
 // OCC: waves per SIMD the register allocation must allow (2 workgroups of
 // 8 waves per CU need 4).
-template <typename T, int NPL, int NS, int W, int TC, bool SHARED, bool HIST, bool STORE_BU, int OCC>
+template <typename T, int NPL, int NS, int W, int TC, bool SHARED, bool HIST, bool STORE_BU, int OCC,
+          bool GATE>
 __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs p) {
     using IO = bio<T>;
     constexpr int DL = 64 / NS;      // channels per wave
@@ -165,7 +163,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     const int Dm = static_cast<int>(p.D);
     const int nit = (L + SC - 1) / SC;
     const bool store_y = dvalid && ns == 0;
-    const float dsk = p.Dskip ? p.Dskip[dvalid ? d : p.D - 1] : 0.f;
+    const float dsk = (GATE && p.Dskip) ? p.Dskip[dvalid ? d : p.D - 1] : 0.f;
 
     // Per-batch-element windows addressed with 32-bit byte offsets (the
     // launcher keeps every window and offset below 1 GiB). Every variable
@@ -177,16 +175,16 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     // y may be null (checkpoint-only forward): a zero-sized window drops the stores.
     const auto ry = make_rsrc(p.y ? static_cast<char *>(p.y) + xoff * TS : nullptr,
                               p.y ? p.L * p.D * TS : 0);
-    const auto rz = make_rsrc(p.z ? static_cast<const char *>(p.z) + xoff * TS : nullptr,
-                              p.z ? p.L * p.D * TS : 0);
+    const auto rz = make_rsrc(GATE && p.z ? static_cast<const char *>(p.z) + xoff * TS : nullptr,
+                              GATE && p.z ? p.L * p.D * TS : 0);
     const auto rB = make_rsrc(static_cast<const char *>(p.Bm) + b * p.sb * TS, p.L * p.st * TS);
     const auto rC = make_rsrc(static_cast<const char *>(p.Cm) + b * p.sb * TS, p.L * p.st * TS);
     const auto rh = make_rsrc(p.hist ? p.hist + xoff * p.N : nullptr, HIST ? p.L * p.D * p.N * 4 : 0);
     const int vx = dc * TS;                             // lane byte offset in an x row
     const int rowx = Dm * TS;                           // bytes per x row
     const int rowbc = static_cast<int>(p.st) * TS;      // bytes per B/C row
-    const int vbc = SHARED ? 0 : (dc * static_cast<int>(p.sd) + n0) * TS;
-    const int vh = (dc * N + n0) * 4;
+    const int vbc = SHARED ? 0 : (dc * static_cast<int>(p.sd) + ns) * TS;
+    const int vh = (dc * N + ns) * 4;
 
     __shared__ float sB[SHARED ? 3 : 1][SHARED ? TILE : 1];
     __shared__ float sC[SHARED ? 3 : 1][SHARED ? TILE : 1];
@@ -198,22 +196,25 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     __shared__ float carry[2][NPL][64];
     __shared__ float pin[W][NPL][64];       // incoming state of each wave
 
+    // A lane holds the states n = NS*j + ns of its channel (interleaved over
+    // the lane groups), so the structured decays below form one chain.
     float Ap[NPL];
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) Ap[j] = p.A[dc * N + n0 + j] * kLog2e;
+    for (int j = 0; j < NPL; ++j) Ap[j] = p.A[dc * N + NS * j + ns] * kLog2e;
     const float A0p = p.A[dc * N] * kLog2e;
     // Structured decays (A[d,n] == (n+1)*A[d,0] for every state of every
     // channel of the workgroup) switch exp per state for a power chain.
-    bool structured = (n0 == 0 || (n0 & (n0 - 1)) == 0);
+    bool structured = true;
 #pragma unroll
     for (int j = 0; j < NPL; ++j)
-        structured = structured && (p.A[dc * N + n0 + j] == static_cast<float>(n0 + j + 1) * p.A[dc * N]);
+        structured = structured &&
+                     (p.A[dc * N + NS * j + ns] == static_cast<float>(NS * j + ns + 1) * p.A[dc * N]);
     const bool fast = __builtin_amdgcn_readfirstlane(__syncthreads_and(structured)) != 0;
 
     if (w == 0) {
 #pragma unroll
         for (int j = 0; j < NPL; ++j)
-            carry[0][j][lane] = p.h0 ? p.h0[(b * Dm + dc) * N + n0 + j] : 0.f;
+            carry[0][j][lane] = p.h0 ? p.h0[(b * Dm + dc) * N + NS * j + ns] : 0.f;
     }
 
     // B/C tile of super-chunk s: element e = (step, state) at row s*SC + e/N.
@@ -229,13 +230,17 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             rc[i] = (e < TILE) ? IO::ld(rC, off + so, 0) : 0.f;
         }
     };
+    // Tile element e = (step e/N, state n = e%N) is stored at
+    // step*N + (n%NS)*NPL + n/NS: a lane's interleaved states are contiguous.
     auto store_tile = [&](int slot) {
 #pragma unroll
         for (int i = 0; i < TPT; ++i) {
             const int e = tid + i * NT;
             if (e < TILE) {
-                sB[slot][e] = rb[i];
-                sC[slot][e] = rc[i];
+                const int n = e % N;
+                const int o = (e / N) * N + (n % NS) * NPL + n / NS;
+                sB[slot][o] = rb[i];
+                sC[slot][o] = rc[i];
             }
         }
     };
@@ -256,7 +261,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
         } else {
             const int so = (s * SC + w * TC + k) * rowbc;
 #pragma unroll
-            for (int j = 0; j < NPL; ++j) out[j] = IO::ld(r, vbc + j * TS + so, 0);
+            for (int j = 0; j < NPL; ++j) out[j] = IO::ld(r, vbc + j * NS * TS + so, 0);
         }
     };
 
@@ -303,7 +308,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             const float u = ds[k] * xs[k];
             dsum += ds[k];
             if (fast) {
-                pow_chain<NPL, NS>(exp2_fast(ds[k] * A0p), n0, e[k]);
+                pow_chain_il<NPL, NS>(exp2_fast(ds[k] * A0p), ns, e[k]);
             } else {
 #pragma unroll
                 for (int j = 0; j < NPL; ++j) e[k][j] = exp2_fast(ds[k] * Ap[j]);
@@ -317,7 +322,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
         }
         float P[NPL];
         if (fast) {
-            pow_chain<NPL, NS>(exp2_fast(dsum * A0p), n0, P);
+            pow_chain_il<NPL, NS>(exp2_fast(dsum * A0p), ns, P);
         } else {
 #pragma unroll
             for (int j = 0; j < NPL; ++j) P[j] = exp2_fast(Ap[j] * dsum);
@@ -347,7 +352,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             }
             carry[cur ^ 1][j][lane] = run;
             if constexpr (SC == kCkptSteps) {
-                if (p.ckpt && dvalid) p.ckpt[((b * p.nck + s) * Dm + d) * N + n0 + j] = run;
+                if (p.ckpt && dvalid) p.ckpt[((b * p.nck + s) * Dm + d) * N + NS * j + ns] = run;
             }
         }
         __syncthreads();
@@ -386,14 +391,18 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             if constexpr (NS >= 2) yp += __shfl_xor(yp, 32);
             nan_seen |= (yp != yp);
             if (store_y) {                                          // rows past L dropped
-                const float zv = p.z ? IO::ld(rz, vx + t * rowx, 0) : 0.f;
-                IO::st(ry, vx + t * rowx, 0, gated<T>(p, yp, xs[k], dsk, zv));
+                if constexpr (GATE) {
+                    const float zv = p.z ? IO::ld(rz, vx + t * rowx, 0) : 0.f;
+                    IO::st(ry, vx + t * rowx, 0, gated<T>(p, yp, xs[k], dsk, zv));
+                } else {
+                    IO::st(ry, vx + t * rowx, 0, yp);
+                }
             }
             if constexpr (HIST) {
                 if (dvalid) {
 #pragma unroll
                     for (int j = 0; j < NPL; ++j)
-                        bio<f32_t>::st(rh, vh + j * 4 + t * Dm * N * 4, 0, h[j]);
+                        bio<f32_t>::st(rh, vh + j * NS * 4 + t * Dm * N * 4, 0, h[j]);
                 }
             }
         }
@@ -406,12 +415,19 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
 
     const int bad = p.clamp && (nan_seen || hmax > 1000.f);
     if (__syncthreads_or(bad)) {
-        if (w == 0) scan1d_serial_wave<T, NPL, NS, SHARED, HIST>(p, b, d, dvalid, n0, Ap);
+        // The sequential pass keeps each lane's states contiguous
+        // (n = n0 + j) and writes every output itself.
+        if (w == 0) {
+            float Apc[NPL];
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) Apc[j] = p.A[dc * N + n0 + j] * kLog2e;
+            scan1d_serial_wave<T, NPL, NS, SHARED, HIST>(p, b, d, dvalid, n0, Apc);
+        }
         return;
     }
     if (w == W - 1 && p.hfin && dvalid) {
 #pragma unroll
-        for (int j = 0; j < NPL; ++j) p.hfin[(b * Dm + d) * N + n0 + j] = h[j];
+        for (int j = 0; j < NPL; ++j) p.hfin[(b * Dm + d) * N + NS * j + ns] = h[j];
     }
 }
 
@@ -464,13 +480,16 @@ static int launch_chunked(const Scan1DFwdArgs &a, bool shared, bool hist, hipStr
         return -1;
     }
     dim3 g(static_cast<unsigned>(grid)), blk(64 * W);
+    const bool gate = a.z || a.Dskip;
+#define KM_CH(SH, HI, GA) hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, W, TC, SH, HI, SBU, OCC, GA>), g, blk, 0, s, a)
     if (shared) {
-        if (hist) hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, W, TC, true, true, SBU, OCC>), g, blk, 0, s, a);
-        else      hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, W, TC, true, false, SBU, OCC>), g, blk, 0, s, a);
+        if (hist) { if (gate) KM_CH(true, true, true); else KM_CH(true, true, false); }
+        else      { if (gate) KM_CH(true, false, true); else KM_CH(true, false, false); }
     } else {
-        if (hist) hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, W, TC, false, true, SBU, OCC>), g, blk, 0, s, a);
-        else      hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, W, TC, false, false, SBU, OCC>), g, blk, 0, s, a);
+        if (hist) { if (gate) KM_CH(false, true, true); else KM_CH(false, true, false); }
+        else      { if (gate) KM_CH(false, false, true); else KM_CH(false, false, false); }
     }
+#undef KM_CH
     KM_HIP_TRY(hipGetLastError());
     return 0;
 }
