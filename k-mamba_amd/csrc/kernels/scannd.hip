@@ -138,7 +138,7 @@ struct NDRow {
     float x[TW], b[TW], c[TW], dt[ND][TW], hn[ND - 1][TW];
     float hleft;
     int gi[ND];
-    long base;
+    int base;                   // row offset from the tile origin, in points
 };
 
 template <int ND, int TW, int MM>
@@ -176,63 +176,76 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
 #pragma unroll
     for (int a = 0; a < ac; ++a) nrows *= ext[a];
 
-    // Operands of one row, read through per-lane pointers that advance by
-    // a uniform stride per point (D for x/delta, D*M for B/C/h).
+    // Addressing: buffer resources based at the tile origin (h one axis-0
+    // stride earlier, for the neighbours before the tile), so every offset
+    // below is a small non-negative 32-bit value. A point's lane offset
+    // within its row is fixed per tile (voffX / voffB, VGPRs); a row adds one
+    // scalar offset per array. Columns past the tile's edge repeat the last
+    // column's offsets and are never computed or stored.
+    long origin = lo[ac];
+#pragma unroll
+    for (int a = 0; a < ac; ++a) origin += static_cast<long>(lo[a]) * p.pstride[a];
+    const long P = static_cast<long>(p.dims[0]) * p.pstride[0];
+    const long hback = min(origin, p.pstride[0]);
+    auto win = [](long bytes) { return bytes < 0x7fffffffL ? bytes : 0x7fffffffL; };
+    const auto rx = make_rsrc(p.x + origin * D, win((P - origin) * D * 4));
+    __amdgpu_buffer_rsrc_t rdt[ND];
+#pragma unroll
+    for (int a = 0; a < ND; ++a) rdt[a] = make_rsrc(p.dt[a] + origin * D, win((P - origin) * D * 4));
+    const auto rB = make_rsrc(p.B + origin * DM, win((P - origin) * DM * 4));
+    const auto rC = make_rsrc(p.C + origin * DM, win((P - origin) * DM * 4));
+    const auto rh = make_rsrc(p.h + (origin - hback) * DM, win((P - origin + hback) * DM * 4));
+    const auto ry = make_rsrc(p.y + origin * D, win((P - origin) * D * 4));
+    int voffX[TW], voffB[TW];
+#pragma unroll
+    for (int c = 0; c < TW; ++c) {
+        const int cc = (c < TC) ? c : TC - 1;
+        voffX[c] = (cc * D + d) * 4;
+        voffB[c] = (cc * DM + f) * 4;
+    }
+    using F = bio<f32_t>;
+
+    // Operands of one row (tile-relative row offset in points: r.base).
     auto load_row = [&](int row, NDRow<ND, TW> &r) {
         int rem = row;
+        int roff = 0;
 #pragma unroll
         for (int a = ac - 1; a >= 0; --a) {
-            r.gi[a] = lo[a] + rem % ext[a];
+            const int ia = rem % ext[a];
             rem /= ext[a];
+            r.gi[a] = lo[a] + ia;
+            roff += ia * static_cast<int>(p.pstride[a]);
         }
         r.gi[ac] = lo[ac];
-        long pb = lo[ac];
-#pragma unroll
-        for (int a = 0; a < ac; ++a) pb += static_cast<long>(r.gi[a]) * p.pstride[a];
-        r.base = pb;
-        const float *xp = p.x + pb * D + d;
-        const float *Bp = p.B + pb * DM + f;
-        const float *Cp = p.C + pb * DM + f;
-        const float *dp[ND];
-#pragma unroll
-        for (int a = 0; a < ND; ++a) dp[a] = p.dt[a] + pb * D + d;
+        r.base = roff;
+        const int sx = roff * D * 4, sb = roff * DM * 4;
 #pragma unroll
         for (int c = 0; c < TW; ++c) {
-            r.x[c] = *xp;
-            r.b[c] = *Bp;
-            r.c[c] = *Cp;
+            r.x[c] = F::ld(rx, voffX[c], sx);
+            r.b[c] = F::ld(rB, voffB[c], sb);
+            r.c[c] = F::ld(rC, voffB[c], sb);
 #pragma unroll
-            for (int a = 0; a < ND; ++a) r.dt[a][c] = *dp[a];
-            if (c + 1 < TC) {
-                xp += D;
-                Bp += DM;
-                Cp += DM;
-#pragma unroll
-                for (int a = 0; a < ND; ++a) dp[a] += D;
-            }
+            for (int a = 0; a < ND; ++a) r.dt[a][c] = F::ld(rdt[a], voffX[c], sx);
         }
         // Neighbours along leading axes, and along the row axis on the tile's
         // first row of a plane (tile boundary); uniform conditions. Rows are
         // prefetched one row ahead, so a leading-axis neighbour inside the
         // tile must lie at least two rows back: the launcher never builds a
         // tile with a single row per plane below an in-tile leading axis.
-        const float *hb = p.h + pb * DM + f;
+        const int sh = (roff + static_cast<int>(hback)) * DM * 4;
 #pragma unroll
         for (int a = 0; a < ND - 1; ++a) {
             const bool need = (a < ar) ? (r.gi[a] > 0) : (r.gi[a] > 0 && r.gi[a] == lo[a]);
             if (need) {
-                const float *np = hb - p.pstride[a] * DM;
+                const int sn = sh - static_cast<int>(p.pstride[a]) * DM * 4;
 #pragma unroll
-                for (int c = 0; c < TW; ++c) {
-                    r.hn[a][c] = *np;
-                    if (c + 1 < TC) np += DM;
-                }
+                for (int c = 0; c < TW; ++c) r.hn[a][c] = F::ld(rh, voffB[c], sn);
             } else {
 #pragma unroll
                 for (int c = 0; c < TW; ++c) r.hn[a][c] = 0.f;
             }
         }
-        r.hleft = (lo[ac] > 0) ? *(hb - DM) : 0.f;
+        r.hleft = (lo[ac] > 0) ? F::ld(rh, voffB[0], sh - DM * 4) : 0.f;
     };
 
     float top[TW];
@@ -244,6 +257,8 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
 
     auto compute_row = [&](const NDRow<ND, TW> &r) {
         const bool first_row_of_plane = (r.gi[ar] == lo[ar]);
+        const int sh = (r.base + static_cast<int>(hback)) * DM * 4;
+        const int sx = r.base * D * 4;
         float hleft = r.hleft;
 #pragma unroll
         for (int c = 0; c < TW; ++c) {
@@ -260,11 +275,11 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
                     acc = fmaf(exp2_fast(r.dt[ar][c] * Ap[ar]), hu, acc);
                 }
                 if (lo[ac] + c > 0) acc = fmaf(exp2_fast(r.dt[ac][c] * Ap[ac]), hleft, acc);
-                p.h[(r.base + c) * DM + f] = acc;
+                F::st(rh, voffB[c], sh, acc);
                 top[c] = acc;
                 hleft = acc;
                 const float yv = sum_m_lanes<MM>(r.c[c] * acc);
-                if (y_lane) p.y[(r.base + c) * D + d] = yv;
+                if (y_lane) F::st(ry, voffX[c], sx, yv);
             }
         }
     };
@@ -342,15 +357,15 @@ static void scannd_tile_shape(int nd, int &tw, int &tl) {
 }
 
 static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s) {
-    const bool fast = (a.DM % 64 == 0) && (64 % a.M == 0) && a.nd >= 2 && a.nd <= 4;
+    bool fast = (a.DM % 64 == 0) && (64 % a.M == 0) && a.nd >= 2 && a.nd <= 4;
+    // Tiles: rows of TWc points along the last axis, Tlead along each
+    // leading axis. One wave per (tile, channel group); one launch per tile
+    // band. Defaults measured fastest on MI355X at configs[2]: 2D rows of 8
+    // points x 6 rows; 3D and up rows of 4 points x 4 per leading axis.
+    int TWc = (a.nd == 2) ? 8 : 4;
+    int Tlead = (a.nd == 2) ? 6 : 4;
+    int nbands = 1;
     if (fast) {
-        // Tiles: rows of TWc points along the last axis, Tlead along each
-        // leading axis. One wave per (tile, channel group); one launch per
-        // tile band.
-        // Defaults measured fastest on MI355X at configs[2]: 2D rows of 8
-        // points x 6 rows; 3D and up rows of 4 points x 4 per leading axis.
-        int TWc = (a.nd == 2) ? 8 : 4;
-        int Tlead = (a.nd == 2) ? 6 : 4;
         scannd_tile_shape(a.nd, TWc, Tlead);
         // Rows are prefetched one ahead, so every tile needs at least two
         // rows per plane below an in-tile leading axis: grow the row-axis
@@ -359,7 +374,6 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s) {
         const int rax = a.nd - 2;
         int trow = (a.dims[rax] < Tlead) ? a.dims[rax] : Tlead;
         while (trow < a.dims[rax] && a.dims[rax] % trow == 1) ++trow;
-        int nbands = 1;
         for (int ax = 0; ax < a.nd; ++ax) {
             int t = (ax == a.nd - 1) ? TWc : (ax == rax ? trow : Tlead);
             if (ax < rax && a.dims[rax] == 1) t = 1;
@@ -368,6 +382,13 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s) {
             nbands += a.ntile[ax] - 1;
         }
         a.ncg = a.DM / 64;
+        // The tile kernel addresses a tile (and the axis-0 plane before it)
+        // with 32-bit byte offsets.
+        long span = a.tile[a.nd - 1] + a.pstride[0];
+        for (int ax = 0; ax + 1 < a.nd; ++ax) span += static_cast<long>(a.tile[ax] - 1) * a.pstride[ax];
+        if (span * static_cast<long>(a.DM) * 4 >= 0x7fffffffL) fast = false;
+    }
+    if (fast) {
         if (nbands > 4096) {
             set_error("scannd: too many tile bands");
             return -1;
