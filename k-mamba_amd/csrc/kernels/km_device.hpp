@@ -48,6 +48,21 @@ template <> struct io<bf16_t> {
     }
 };
 
+// v(lane) + v(lane ^ 32) in every lane, on the VALU (gfx950
+// v_permlane32_swap: the upper half of one copy trades places with the lower
+// half of the other, so the two results hold each lane's value and its
+// partner's). Same sum, bit for bit, as v + __shfl_xor(v, 32), without the
+// LDS round trip of ds_bpermute.
+__device__ __forceinline__ float sum_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// v(lane) + v(lane ^ 16) (v_permlane16_swap trades odd and even 16-lane rows).
+__device__ __forceinline__ float sum_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // 2^x on the transcendental unit (v_exp_f32, ~1 ulp).
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -29,6 +29,8 @@
 //  * States recomputed from checkpoints run unclamped; if any leaves
 //    [-1000, 1000] the super-chunk is recomputed with the sequential clamped
 //    recurrence, which matches the forward's clamp fallback.
+#include <type_traits>
+
 #include "km_device.hpp"
 #include "../km_runtime.hpp"
 #include "kmamba_km.h"
@@ -167,6 +169,15 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
     const int vbc = SHARED ? 0 : (dc * static_cast<int>(p.sd) + n0) * TS;
     const int vh = (dc * N + n0) * 4;
     const int rowh = Dm * N * 4;
+    // Output offsets of lanes that own no output get bit 31 set: past every
+    // window, so the range check drops those stores without a branch.
+    constexpr unsigned kDrop = 0x80000000u;
+    constexpr int GRP = DL / NPL;   // lanes per reduced B/C gradient value
+    const unsigned vxs = own_x ? static_cast<unsigned>(vx) : kDrop;
+    const unsigned vbcs = dvalid ? static_cast<unsigned>(vbc) : kDrop;
+    const unsigned vacc = (dl % GRP) == 0 ? static_cast<unsigned>((n0 + dl / GRP) * 4) : kDrop;
+    const auto racB = make_rsrc(SHARED ? p.accB + b * p.L * N : nullptr, SHARED ? p.L * N * 4 : 0);
+    const auto racC = make_rsrc(SHARED ? p.accC + b * p.L * N : nullptr, SHARED ? p.L * N * 4 : 0);
 
     __shared__ float sB[SHARED ? 3 : 1][SHARED ? TILE : 1];
     __shared__ float sC[SHARED ? 3 : 1][SHARED ? TILE : 1];
@@ -200,8 +211,8 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
             const int e = tid + i * NT;
             const int t = s * SC + e / N;
             const int off = (e % N) * TS;
-            rb[i] = (e < TILE) ? IO::ld(rB, off + t * rowbc, 0) : 0.f;
-            rc[i] = (e < TILE) ? IO::ld(rC, off + t * rowbc, 0) : 0.f;
+            rb[i] = IO::ld(rB, off + t * rowbc, 0);   // e >= TILE: a row the store skips
+            rc[i] = IO::ld(rC, off + t * rowbc, 0);
         }
     };
     auto store_tile = [&](int slot) {
@@ -241,32 +252,57 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
         if (s == 0) return p.h0 ? p.h0[(b * Dm + dc) * N + n0 + j] : 0.f;
         return p.ckpt[((b * p.nck + (s - 1)) * Dm + dc) * N + n0 + j];
     };
+    // The same for the states j = w + i*W this thread folds, as loads that
+    // are prefetched with the super-chunk's x/delta/dy.
+    constexpr int NJ = (NPL + W - 1) / W;
+    const auto rck = make_rsrc(HIN ? nullptr : p.ckpt + b * p.nck * p.D * p.N,
+                               HIN ? 0 : p.nck * p.D * p.N * 4);
+    const auto rh0 = make_rsrc(p.h0 ? p.h0 + b * p.D * p.N : nullptr, p.h0 ? p.D * p.N * 4 : 0);
+    auto load_ck = [&](int s, float (&o)[NJ]) {
+#pragma unroll
+        for (int i = 0; i < NJ; ++i) {
+            const int j = min(w + i * W, NPL - 1);
+            const int vo = (dc * N + n0 + j) * 4;
+            const float hv = bio<f32_t>::ld(rh0, vo, 0);                           // 0 if no h0
+            const float cv = bio<f32_t>::ld(rck, vo + max(s - 1, 0) * Dm * N * 4, 0);
+            o[i] = (s == 0) ? hv : cv;
+        }
+    };
 
+    // Prefetches are issued unconditionally (clamped to super-chunk 0, or
+    // past the end where the range check reads 0): a load under a branch
+    // would make the compiler's wait-count merge at the join wait for it
+    // before the current data is used.
     if constexpr (SHARED) {
         load_tile(nit - 1);
         store_tile(0);
-        if (nit > 1) load_tile(nit - 2);
+        load_tile(max(nit - 2, 0));
     }
     float X0[TC], D0[TC], G0[TC], X1[TC], D1[TC], G1[TC];
+    float K0[NJ], K1[NJ];
     load_xd(nit - 1, X0, D0, G0);
+    load_ck(nit - 1, K0);
     __syncthreads();
 
     float dAacc[NPL];
 #pragma unroll
     for (int j = 0; j < NPL; ++j) dAacc[j] = 0.f;
 
-    auto body = [&](int it, float (&xs)[TC], float (&ds)[TC], float (&gs)[TC],
-                    float (&xn)[TC], float (&dn)[TC], float (&gn)[TC]) {
+    // FASTC selects the structured-decay form at compile time (straight-line
+    // bodies for the scheduler).
+    auto body = [&](auto fastc, int it, float (&xs)[TC], float (&ds)[TC], float (&gs)[TC],
+                    float (&ks)[NJ], float (&xn)[TC], float (&dn)[TC], float (&gn)[TC],
+                    float (&kn)[NJ]) __attribute__((always_inline)) {
+        constexpr bool FAST = decltype(fastc)::value;
         const int s = nit - 1 - it;
         const int cur = it & 1;
         const int slot = it % 3;
         if constexpr (SHARED) {
-            if (s >= 1) {                // tile s-1 -> LDS (slot last read in it-2)
-                store_tile((it + 1) % 3);
-                if (s >= 2) load_tile(s - 2);
-            }
+            store_tile((it + 1) % 3);    // tile s-1 -> LDS (slot last read in it-2)
+            load_tile(max(s - 2, 0));
         }
-        if (s >= 1) load_xd(s - 1, xn, dn, gn);
+        load_xd(max(s - 1, 0), xn, dn, gn);
+        load_ck(max(s - 1, 0), kn);
 
         // ---- forward states of this wave's steps ---------------------------
         float e[TC][NPL];
@@ -276,7 +312,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
 #pragma unroll
         for (int k = 0; k < TC; ++k) {
             dsum += ds[k];
-            if (fast) {
+            if constexpr (FAST) {
                 pow_chain_b<NPL, NS>(exp2_fast(ds[k] * A0p), n0, e[k]);
             } else {
 #pragma unroll
@@ -284,7 +320,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
             }
         }
         float P[NPL];
-        if (fast) {
+        if constexpr (FAST) {
             pow_chain_b<NPL, NS>(exp2_fast(dsum * A0p), n0, P);
         } else {
 #pragma unroll
@@ -323,8 +359,11 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
                 aggH[w][j][lane] = hl[j];
             }
             __syncthreads();
-            for (int j = w; j < NPL; j += W) {
-                float run = h_start(s, j);
+#pragma unroll
+            for (int i = 0; i < NJ; ++i) {
+                const int j = w + i * W;
+                if (j >= NPL) break;
+                float run = ks[i];
 #pragma unroll
                 for (int v = 0; v < W; ++v) {
                     pin[v][j][lane] = run;
@@ -445,44 +484,45 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
             }
             // Sum the state groups of the channel (lanes dl + DL*ns).
             if constexpr (NS >= 4) {
-                sa += __shfl_xor(sa, 16);
-                sbv += __shfl_xor(sbv, 16);
+                sa = sum_xor16(sa);
+                sbv = sum_xor16(sbv);
             }
             if constexpr (NS >= 2) {
-                sa += __shfl_xor(sa, 32);
-                sbv += __shfl_xor(sbv, 32);
+                sa = sum_xor32(sa);
+                sbv = sum_xor32(sbv);
             }
-            if (own_x) {
-                IO::st(rdx, vx + t * rowx, 0, dtk * sbv);
-                IO::st(rdd, vx + t * rowx, 0, fmaf(xk, sbv, sa));
-            }
+            // Rows past L and lanes without output are dropped by the range
+            // check, so none of the stores below needs a branch.
+            const int xo = static_cast<int>(vxs + static_cast<unsigned>(t * rowx));
+            IO::st(rdx, xo, 0, dtk * sbv);
+            IO::st(rdd, xo, 0, fmaf(xk, sbv, sa));
             if constexpr (SHARED) {
                 // Sum over the wave's channels; lane l then holds state
                 // n0 + (l % DL) / (DL / NPL) of step t.
                 const float rbv = reduce_scatter<NPL, DL>(dBv, lane);
                 const float rcv = reduce_scatter<NPL, DL>(dCv, lane);
-                constexpr int GRP = DL / NPL;
-                if ((dl % GRP) == 0 && t < L) {
-                    const long o = (b * p.L + t) * N + n0 + dl / GRP;
-                    unsafeAtomicAdd(p.accB + o, rbv);
-                    unsafeAtomicAdd(p.accC + o, rcv);
-                }
+                const int ao = static_cast<int>(vacc + static_cast<unsigned>(t * N * 4));
+                __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(rbv, racB, ao, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(rcv, racC, ao, 0, 0);
             } else {
-                if (dvalid) {
 #pragma unroll
-                    for (int j = 0; j < NPL; ++j) {
-                        IO::st(rdB, vbc + j * TS + t * rowbc, 0, dBv[j]);
-                        IO::st(rdC, vbc + j * TS + t * rowbc, 0, dCv[j]);
-                    }
+                for (int j = 0; j < NPL; ++j) {
+                    const int bo = static_cast<int>(vbcs + static_cast<unsigned>(j * TS + t * rowbc));
+                    IO::st(rdB, bo, 0, dBv[j]);
+                    IO::st(rdC, bo, 0, dCv[j]);
                 }
             }
         }
     };
 
-    for (int it = 0; it < nit; it += 2) {
-        body(it, X0, D0, G0, X1, D1, G1);
-        if (it + 1 < nit) body(it + 1, X1, D1, G1, X0, D0, G0);
-    }
+    auto run = [&](auto fastc) __attribute__((always_inline)) {
+        for (int it = 0; it < nit; it += 2) {
+            body(fastc, it, X0, D0, G0, K0, X1, D1, G1, K1);
+            if (it + 1 < nit) body(fastc, it + 1, X1, D1, G1, K1, X0, D0, G0, K0);
+        }
+    };
+    if (fast) run(std::true_type{});
+    else run(std::false_type{});
 
     if (dvalid) {
 #pragma unroll

@@ -185,6 +185,11 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     const int rowbc = static_cast<int>(p.st) * TS;      // bytes per B/C row
     const int vbc = SHARED ? 0 : (dc * static_cast<int>(p.sd) + ns) * TS;
     const int vh = (dc * N + ns) * 4;
+    // Lanes that own no output store at an offset with bit 31 set, past every
+    // window, which the range check drops: the stores need no branch.
+    constexpr unsigned kDrop = 0x80000000u;
+    const unsigned vy = store_y ? static_cast<unsigned>(vx) : kDrop;
+    const unsigned vhs = dvalid ? static_cast<unsigned>(vh) : kDrop;
 
     __shared__ float sB[SHARED ? 3 : 1][SHARED ? TILE : 1];
     __shared__ float sC[SHARED ? 3 : 1][SHARED ? TILE : 1];
@@ -226,8 +231,8 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             const int t = s * SC + e / N;
             const int off = (e % N) * TS;
             const int so = t * rowbc;
-            rb[i] = (e < TILE) ? IO::ld(rB, off + so, 0) : 0.f;
-            rc[i] = (e < TILE) ? IO::ld(rC, off + so, 0) : 0.f;
+            rb[i] = IO::ld(rB, off + so, 0);   // e >= TILE: a row the store skips
+            rc[i] = IO::ld(rC, off + so, 0);
         }
     };
     // Tile element e = (step e/N, state n = e%N) is stored at
@@ -244,12 +249,13 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             }
         }
     };
-    auto load_xd = [&](int s, float (&xo)[TC], float (&dto)[TC]) {
+    auto load_xd = [&](int s, float (&xo)[TC], float (&dto)[TC], float (&zo)[GATE ? TC : 1]) {
 #pragma unroll
         for (int k = 0; k < TC; ++k) {
             const int so = (s * SC + w * TC + k) * rowx;   // rows past L read as 0
             xo[k] = IO::ld(rx, vx + so, 0);
             dto[k] = IO::ld(rdt, vx + so, 0);
+            if constexpr (GATE) zo[k] = IO::ld(rz, vx + so, 0);   // 0 when z is null
         }
     };
     auto bc_row = [&](const float (*tile)[SHARED ? TILE : 1], __amdgpu_buffer_rsrc_t r, int slot,
@@ -265,29 +271,36 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
         }
     };
 
+    // Prefetches are issued unconditionally: rows past L read as 0 through
+    // the range check. A load under a branch would make the compiler's
+    // wait-count merge at the join wait for it before the current data is
+    // used, exposing one HBM latency per super-chunk.
     if constexpr (SHARED) {
         load_tile(0);
         store_tile(0);
-        if (nit > 1) load_tile(1);
+        load_tile(1);
     }
     float X0[TC], D0[TC], X1[TC], D1[TC];
-    load_xd(0, X0, D0);
+    float Z0[GATE ? TC : 1], Z1[GATE ? TC : 1];
+    load_xd(0, X0, D0, Z0);
     __syncthreads();
 
     float h[NPL];
     float hmax = 0.f;
     bool nan_seen = false;
 
-    auto body = [&](int s, float (&xs)[TC], float (&ds)[TC], float (&xn)[TC], float (&dn)[TC]) {
+    // FASTC selects the structured-decay form at compile time, so each body
+    // is straight-line code the scheduler can interleave across steps.
+    auto body = [&](auto fastc, int s, float (&xs)[TC], float (&ds)[TC], float (&zs)[GATE ? TC : 1],
+                    float (&xn)[TC], float (&dn)[TC], float (&zn)[GATE ? TC : 1]) __attribute__((always_inline)) {
+        constexpr bool FAST = decltype(fastc)::value;
         const int cur = s & 1;
         const int slot = s % 3;
         if constexpr (SHARED) {
-            if (s + 1 < nit) {           // tile s+1 -> LDS (slot last read in s-2)
-                store_tile((s + 1) % 3);
-                if (s + 2 < nit) load_tile(s + 2);
-            }
+            store_tile((s + 1) % 3);     // tile s+1 -> LDS (slot last read in s-2)
+            load_tile(s + 2);
         }
-        if (s + 1 < nit) load_xd(s + 1, xn, dn);
+        load_xd(s + 1, xn, dn, zn);
 
         // Local pass from a zero state; decays (and optionally B*u) kept for
         // the replay.
@@ -307,7 +320,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             if (k + 1 < TC) bc_row(sB, rB, slot, s, k + 1, bln);
             const float u = ds[k] * xs[k];
             dsum += ds[k];
-            if (fast) {
+            if constexpr (FAST) {
                 pow_chain_il<NPL, NS>(exp2_fast(ds[k] * A0p), ns, e[k]);
             } else {
 #pragma unroll
@@ -321,7 +334,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             }
         }
         float P[NPL];
-        if (fast) {
+        if constexpr (FAST) {
             pow_chain_il<NPL, NS>(exp2_fast(dsum * A0p), ns, P);
         } else {
 #pragma unroll
@@ -352,7 +365,8 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             }
             carry[cur ^ 1][j][lane] = run;
             if constexpr (SC == kCkptSteps) {
-                if (p.ckpt && dvalid) p.ckpt[((b * p.nck + s) * Dm + d) * N + NS * j + ns] = run;
+                if (p.ckpt && dvalid && s < nit)
+                    p.ckpt[((b * p.nck + s) * Dm + d) * N + NS * j + ns] = run;
             }
         }
         __syncthreads();
@@ -387,31 +401,30 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
                 hmax = fmaxf(hmax, fabsf(h[j]));
             }
             // Sum the state groups of this channel (lanes dl + DL*ns).
-            if constexpr (NS >= 4) yp += __shfl_xor(yp, 16);
-            if constexpr (NS >= 2) yp += __shfl_xor(yp, 32);
+            if constexpr (NS >= 4) yp = sum_xor16(yp);
+            if constexpr (NS >= 2) yp = sum_xor32(yp);
             nan_seen |= (yp != yp);
-            if (store_y) {                                          // rows past L dropped
-                if constexpr (GATE) {
-                    const float zv = p.z ? IO::ld(rz, vx + t * rowx, 0) : 0.f;
-                    IO::st(ry, vx + t * rowx, 0, gated<T>(p, yp, xs[k], dsk, zv));
-                } else {
-                    IO::st(ry, vx + t * rowx, 0, yp);
-                }
-            }
+            // Rows past L and lanes without output are dropped by the range check.
+            const int yo = static_cast<int>(vy + static_cast<unsigned>(t * rowx));
+            if constexpr (GATE) IO::st(ry, yo, 0, gated<T>(p, yp, xs[k], dsk, zs[k]));
+            else IO::st(ry, yo, 0, yp);
             if constexpr (HIST) {
-                if (dvalid) {
 #pragma unroll
-                    for (int j = 0; j < NPL; ++j)
-                        bio<f32_t>::st(rh, vh + j * NS * 4 + t * Dm * N * 4, 0, h[j]);
-                }
+                for (int j = 0; j < NPL; ++j)
+                    bio<f32_t>::st(rh, static_cast<int>(vhs + static_cast<unsigned>(j * NS * 4 + t * Dm * N * 4)),
+                                   0, h[j]);
             }
         }
     };
 
-    for (int s = 0; s < nit; s += 2) {
-        body(s, X0, D0, X1, D1);
-        if (s + 1 < nit) body(s + 1, X1, D1, X0, D0);
-    }
+    auto run = [&](auto fastc) __attribute__((always_inline)) {
+        for (int s = 0; s < nit; s += 2) {
+            body(fastc, s, X0, D0, Z0, X1, D1, Z1);
+            if (s + 1 < nit) body(fastc, s + 1, X1, D1, Z1, X0, D0, Z0);
+        }
+    };
+    if (fast) run(std::true_type{});
+    else run(std::false_type{});
 
     const int bad = p.clamp && (nan_seen || hmax > 1000.f);
     if (__syncthreads_or(bad)) {
@@ -481,7 +494,11 @@ static int launch_chunked(const Scan1DFwdArgs &a, bool shared, bool hist, hipStr
     }
     dim3 g(static_cast<unsigned>(grid)), blk(64 * W);
     const bool gate = a.z || a.Dskip;
-#define KM_CH(SH, HI, GA) hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, W, TC, SH, HI, SBU, OCC, GA>), g, blk, 0, s, a)
+    // B*u is kept in registers only without history stores or gating, whose
+    // extra registers would otherwise spill.
+#define KM_CH(SH, HI, GA) \
+    hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, W, TC, SH, HI, SBU && !HI && !GA, OCC, GA>), \
+                       g, blk, 0, s, a)
     if (shared) {
         if (hist) { if (gate) KM_CH(true, true, true); else KM_CH(true, true, false); }
         else      { if (gate) KM_CH(true, false, true); else KM_CH(true, false, false); }
@@ -495,11 +512,8 @@ static int launch_chunked(const Scan1DFwdArgs &a, bool shared, bool hist, hipStr
 }
 
 // Tuning knob for N = 16 (KM_SCAN1D_CFG, read once): 0 = 32 channels x 2
-// state halves, 8 waves, 8 steps per wave; 1 = 16 channels x 4 state
-// quarters, 8 waves, 8 steps, 4 waves/SIMD (two workgroups per CU); 2 = as 1
-// with 16 steps at 2 waves/SIMD; 3 = as 1 with B*u kept in registers; 4 = as
-// 1 at 3 waves/SIMD; 5 = 16x4, 4 waves, 16 steps, 2 waves/SIMD; 6 (default,
-// fastest measured on MI355X) = as 0 with B*u kept in registers.
+// state halves, 8 waves, 8 steps per wave, B*u recomputed in the replay;
+// any other value (default) = the same with B*u kept in registers.
 static int scan1d_cfg16() {
     static int cfg = [] {
         const char *e = std::getenv("KM_SCAN1D_CFG");
@@ -511,17 +525,8 @@ static int scan1d_cfg16() {
 template <typename T>
 static int launch_n16(const Scan1DFwdArgs &a, bool shared, bool hist, hipStream_t s) {
     // Checkpoints are written at super-chunk ends: keep 64-step super-chunks.
-    if (a.ckpt) return launch_chunked<T, 8, 2, 8, 8, true>(a, shared, hist, s);
-    switch (scan1d_cfg16()) {
-    case 0: return launch_chunked<T, 8, 2, 8, 8>(a, shared, hist, s);
-    case 2: return launch_chunked<T, 4, 4, 8, 16>(a, shared, hist, s);
-    case 3: return launch_chunked<T, 4, 4, 8, 8, true, 4>(a, shared, hist, s);
-    case 4: return launch_chunked<T, 4, 4, 8, 8, false, 3>(a, shared, hist, s);
-    case 5: return launch_chunked<T, 4, 4, 4, 16>(a, shared, hist, s);
-    case 1: return launch_chunked<T, 4, 4, 8, 8, false, 4>(a, shared, hist, s);
-    case 6:
-    default: return launch_chunked<T, 8, 2, 8, 8, true>(a, shared, hist, s);
-    }
+    if (!a.ckpt && scan1d_cfg16() == 0) return launch_chunked<T, 8, 2, 8, 8>(a, shared, hist, s);
+    return launch_chunked<T, 8, 2, 8, 8, true>(a, shared, hist, s);
 }
 
 template <typename T>

@@ -121,8 +121,8 @@ __device__ __forceinline__ float sum_m_lanes(float v) {
         v += dpp<0x124>(v);                      // row_ror:4
         v += dpp<0x122>(v);                      // row_ror:2
         v += dpp<0x121>(v);                      // row_ror:1
-        if constexpr (MM >= 32) v += __shfl_xor(v, 16);
-        if constexpr (MM >= 64) v += __shfl_xor(v, 32);
+        if constexpr (MM >= 32) v = sum_xor16(v);
+        if constexpr (MM >= 64) v = sum_xor32(v);
     }
     return v;
 }
