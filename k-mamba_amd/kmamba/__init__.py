@@ -14,7 +14,8 @@ import os
 from pathlib import Path
 
 PKG_ROOT = Path(__file__).resolve().parent.parent          # k-mamba_amd/
-LIB_PATH = PKG_ROOT / "lib" / "libkmamba.so"
+# KMAMBA_LIB names another build of the library (same ABI) to load instead.
+LIB_PATH = Path(os.environ.get("KMAMBA_LIB", PKG_ROOT / "lib" / "libkmamba.so"))
 INCLUDE_DIR = PKG_ROOT.parent / "include"
 
 if not LIB_PATH.exists():
