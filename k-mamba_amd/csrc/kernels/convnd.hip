@@ -108,10 +108,29 @@ __device__ __forceinline__ void lead_rows(const ConvArgs &p, const TaskPos &t, i
     }
 }
 
+// The strip kernels address one batch element through raw buffer resources
+// with 32-bit byte offsets (the launcher keeps P*D*4 below 2^31). Taps that
+// leave the grid along a leading axis use an offset with bit 31 set, past the
+// window, which loads 0; outputs of lanes past D or columns past the line end
+// are stored at such an offset and dropped. Every load and store is thus
+// unconditional and the strip loop has a fixed trip count: it is unrolled
+// and software-pipelined by hand in chunks of CU columns, the loads of chunk
+// c+1 issued before the arithmetic and stores of chunk c (the compiler does
+// not move loads above stores through buffer resources it cannot tell
+// apart).
+constexpr unsigned kConvDrop = 0x80000000u;
+// Columns per chunk: enough loads in flight per wave, few enough registers.
+constexpr int conv_chunk(int loads_per_column) { return loads_per_column <= 3 ? 8 : (loads_per_column <= 9 ? 4 : 2); }
+
+__device__ __forceinline__ int conv_off(unsigned base, int j, int rowbytes) {
+    return static_cast<int>(base + static_cast<unsigned>(j * rowbytes));
+}
+
 template <int ND, int K>
 __global__ void __launch_bounds__(64 * kConvWaves) convnd_fwd_strip(ConvArgs p) {
     constexpr int KL = (ND > 1) ? ipow(K, ND - 1) : 1;
     constexpr int KV = KL * K;
+    using F = bio<f32_t>;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const long blk = xcd_block(blockIdx.x, gridDim.x);
     TaskPos t;
@@ -119,8 +138,10 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_fwd_strip(ConvArgs p) 
     const int dc = t.dvalid ? t.d : p.D - 1;
     const int J = p.dims[ND - 1];
     const long bbase = t.batch * p.P;
-    const float *in = p.in + bbase * p.D + dc;
-    float *out = p.out + bbase * p.D + dc;
+    const auto rin = make_rsrc(p.in + bbase * p.D, p.P * p.D * 4);
+    const auto rout = make_rsrc(p.out + bbase * p.D, p.P * p.D * 4);
+    const int rb = p.D * 4;                          // bytes per point row
+    const int j0 = static_cast<int>(t.j0);
 
     float w[KV];
 #pragma unroll
@@ -128,29 +149,58 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_fwd_strip(ConvArgs p) 
     const float b0 = p.bias ? p.bias[dc] : 0.f;
     long rows[KL];
     lead_rows<ND, K>(p, t, -1, rows);
+    unsigned ro[KL];
+#pragma unroll
+    for (int a = 0; a < KL; ++a)
+        ro[a] = rows[a] >= 0 ? static_cast<unsigned>((rows[a] * p.D + dc) * 4) : kConvDrop;
+    const unsigned oo = t.dvalid ? static_cast<unsigned>((t.line_off * p.D + dc) * 4) : kConvDrop;
 
-    // win[a][c]: input of leading tap row a at column j - (K-1) + c.
+    // win[a][c]: input of leading tap row a at column j - (K-1) + c; columns
+    // before 0 are zero (the row offset would land in the previous line).
     float win[KL][K];
 #pragma unroll
     for (int a = 0; a < KL; ++a) {
 #pragma unroll
         for (int c = 0; c < K - 1; ++c) {
-            const long j = t.j0 - (K - 1) + c;
-            win[a][c + 1] = (rows[a] >= 0 && j >= 0) ? in[(rows[a] + j) * p.D] : 0.f;
+            const int j = j0 - (K - 1) + c;
+            const float v = F::ld(rin, conv_off(ro[a], j < 0 ? 0 : j, rb), 0);
+            win[a][c + 1] = j >= 0 ? v : 0.f;
         }
     }
-    const long jend = t.j0 + kStrip < J ? t.j0 + kStrip : J;
-    for (long j = t.j0; j < jend; ++j) {
+    constexpr int CU = conv_chunk(KL);
+    static_assert(kStrip % (2 * CU) == 0, "strip is whole chunk pairs");
+    float n0[CU][KL], n1[CU][KL];                    // chunk buffers
+    auto load_chunk = [&](int ch, float (&bx)[CU][KL]) {
 #pragma unroll
-        for (int a = 0; a < KL; ++a) {
+        for (int u = 0; u < CU; ++u)
 #pragma unroll
-            for (int c = 0; c < K - 1; ++c) win[a][c] = win[a][c + 1];
-            win[a][K - 1] = (rows[a] >= 0) ? in[(rows[a] + j) * p.D] : 0.f;
+            for (int a = 0; a < KL; ++a) bx[u][a] = F::ld(rin, conv_off(ro[a], j0 + ch * CU + u, rb), 0);
+    };
+    auto run_chunk = [&](int ch, const float (&bx)[CU][KL]) {
+#pragma unroll
+        for (int u = 0; u < CU; ++u) {
+            const int j = j0 + ch * CU + u;
+#pragma unroll
+            for (int a = 0; a < KL; ++a) {
+#pragma unroll
+                for (int c = 0; c < K - 1; ++c) win[a][c] = win[a][c + 1];
+                win[a][K - 1] = bx[u][a];
+            }
+            float s = b0;
+#pragma unroll
+            for (int kl = 0; kl < KV; ++kl) s += win[kl / K][kl % K] * w[kl];
+            F::st(rout, j < J ? conv_off(oo, j, rb) : static_cast<int>(kConvDrop), 0, s);
         }
-        float s = b0;
-#pragma unroll
-        for (int kl = 0; kl < KV; ++kl) s += win[kl / K][kl % K] * w[kl];
-        if (t.dvalid) out[(t.line_off + j) * p.D] = s;
+    };
+    // Past the strip the prefetch reads the next columns (in bounds or 0),
+    // unused.
+    load_chunk(0, n0);
+#pragma unroll 1
+    for (int ch = 0; ch < kStrip / CU; ch += 2) {
+        load_chunk(ch + 1, n1);
+        run_chunk(ch, n0);
+        load_chunk(ch + 2, n0);
+        run_chunk(ch + 1, n1);
     }
 }
 
@@ -158,6 +208,7 @@ template <int ND, int K>
 __global__ void __launch_bounds__(64 * kConvWaves) convnd_bwd_strip(ConvArgs p) {
     constexpr int KL = (ND > 1) ? ipow(K, ND - 1) : 1;
     constexpr int KV = KL * K;
+    using F = bio<f32_t>;
     __shared__ float red[kConvWaves][KV + 1][64];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -172,41 +223,67 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_bwd_strip(ConvArgs p) 
         dc = t.dvalid ? t.d : p.D - 1;
         const int J = p.dims[ND - 1];
         const long bbase = t.batch * p.P;
-        const float *in = p.in + bbase * p.D + dc;
-        const float *dy = p.dy + bbase * p.D + dc;
-        float *din = p.din + bbase * p.D + dc;
+        const auto rin = make_rsrc(p.in + bbase * p.D, p.P * p.D * 4);
+        const auto rdy = make_rsrc(p.dy + bbase * p.D, p.P * p.D * 4);
+        const auto rdin = make_rsrc(p.din + bbase * p.D, p.P * p.D * 4);
+        const int rb = p.D * 4;
+        const int j0 = static_cast<int>(t.j0);
         float w[KV];
 #pragma unroll
         for (int k = 0; k < KV; ++k) w[k] = p.W[static_cast<long>(k) * p.D + dc];
-        long rin[KL], rdy[KL];
-        lead_rows<ND, K>(p, t, -1, rin);
-        lead_rows<ND, K>(p, t, +1, rdy);
-        // xin[a][c]: input at column j-(K-1)+c of causal row a.
-        // gdy[a][c]: dy at column j+c of anti-causal row a.
+        long rin_[KL], rdy_[KL];
+        lead_rows<ND, K>(p, t, -1, rin_);
+        lead_rows<ND, K>(p, t, +1, rdy_);
+        unsigned oi[KL], og[KL];
+#pragma unroll
+        for (int a = 0; a < KL; ++a) {
+            oi[a] = rin_[a] >= 0 ? static_cast<unsigned>((rin_[a] * p.D + dc) * 4) : kConvDrop;
+            og[a] = rdy_[a] >= 0 ? static_cast<unsigned>((rdy_[a] * p.D + dc) * 4) : kConvDrop;
+        }
+        const unsigned od = t.dvalid ? static_cast<unsigned>((t.line_off * p.D + dc) * 4) : kConvDrop;
+        // xin[a][c]: input at column j-(K-1)+c of causal row a (0 before
+        // column 0). gdy[a][c]: dy at column j+c of anti-causal row a (0 past
+        // the line end, where the row offset would land in the next line).
         float xin[KL][K], gdy[KL][K];
 #pragma unroll
         for (int a = 0; a < KL; ++a) {
 #pragma unroll
             for (int c = 0; c < K - 1; ++c) {
-                const long ji = t.j0 - (K - 1) + c;
-                xin[a][c + 1] = (rin[a] >= 0 && ji >= 0) ? in[(rin[a] + ji) * p.D] : 0.f;
-                const long jd = t.j0 + c;
-                gdy[a][c] = (rdy[a] >= 0 && jd < J) ? dy[(rdy[a] + jd) * p.D] : 0.f;
+                const int ji = j0 - (K - 1) + c;
+                const float vi = F::ld(rin, conv_off(oi[a], ji < 0 ? 0 : ji, rb), 0);
+                xin[a][c + 1] = ji >= 0 ? vi : 0.f;
+                const int jd = j0 + c;
+                const float vd = F::ld(rdy, conv_off(og[a], jd, rb), 0);
+                gdy[a][c] = jd < J ? vd : 0.f;
             }
         }
         // The anti-causal row with every leading tap at K-1 is the line itself.
         constexpr int SELF = KL - 1;
-        const long jend = t.j0 + kStrip < J ? t.j0 + kStrip : J;
-        for (long j = t.j0; j < jend; ++j) {
+        constexpr int CU = conv_chunk(2 * KL);
+        static_assert(kStrip % (2 * CU) == 0, "strip is whole chunk pairs");
+        float i0[CU][KL], d0[CU][KL], i1[CU][KL], d1[CU][KL];   // chunk buffers
+        auto load_chunk = [&](int ch, float (&bi)[CU][KL], float (&bd)[CU][KL]) {
+#pragma unroll
+            for (int u = 0; u < CU; ++u)
+#pragma unroll
+                for (int a = 0; a < KL; ++a) {
+                    const int j = j0 + ch * CU + u;
+                    bi[u][a] = F::ld(rin, conv_off(oi[a], j, rb), 0);
+                    bd[u][a] = F::ld(rdy, conv_off(og[a], j + K - 1, rb), 0);
+                }
+        };
+        auto run_chunk = [&](int ch, const float (&bi)[CU][KL], const float (&bd)[CU][KL]) {
+#pragma unroll
+        for (int u = 0; u < CU; ++u) {
+            const int j = j0 + ch * CU + u;
 #pragma unroll
             for (int a = 0; a < KL; ++a) {
 #pragma unroll
                 for (int c = 0; c < K - 1; ++c) xin[a][c] = xin[a][c + 1];
-                xin[a][K - 1] = (rin[a] >= 0) ? in[(rin[a] + j) * p.D] : 0.f;
-                const long jd = j + K - 1;
-                gdy[a][K - 1] = (rdy[a] >= 0 && jd < J) ? dy[(rdy[a] + jd) * p.D] : 0.f;
+                xin[a][K - 1] = bi[u][a];
+                gdy[a][K - 1] = j + K - 1 < J ? bd[u][a] : 0.f;
             }
-            const float g = gdy[SELF][0];
+            const float g = gdy[SELF][0];            // 0 past the line end
             float s = 0.f;
 #pragma unroll
             for (int kl = 0; kl < KV; ++kl) {
@@ -215,12 +292,21 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_bwd_strip(ConvArgs p) 
                 acc[kl] = fmaf(g, xin[a][k], acc[kl]);
             }
             acc[KV] += g;
-            if (t.dvalid) din[(t.line_off + j) * p.D] = s;
+            F::st(rdin, j < J ? conv_off(od, j, rb) : static_cast<int>(kConvDrop), 0, s);
 #pragma unroll
             for (int a = 0; a < KL; ++a) {
 #pragma unroll
                 for (int c = 0; c < K - 1; ++c) gdy[a][c] = gdy[a][c + 1];
             }
+        }
+        };
+        load_chunk(0, i0, d0);
+#pragma unroll 1
+        for (int ch = 0; ch < kStrip / CU; ch += 2) {
+            load_chunk(ch + 1, i1, d1);
+            run_chunk(ch, i0, d0);
+            load_chunk(ch + 2, i0, d0);
+            run_chunk(ch + 1, i1, d1);
         }
         if (!t.dvalid) {
 #pragma unroll
@@ -409,12 +495,18 @@ static bool conv_args(const ConvNDParams *p, long batch, bool bwd, ConvArgs &a, 
     return true;
 }
 
+// The strip kernels' 32-bit offsets: one batch element, plus a strip's
+// overhang past the line end (kStrip + K rows), must stay below 2^31 bytes.
+static bool strip_fits(const ConvArgs &a) {
+    return (a.P + kStrip + a.K) * static_cast<long>(a.D) * 4 < 0x7fffffffL;
+}
+
 #define KM_CONV_SHAPES(X) X(1, 2) X(1, 3) X(1, 4) X(2, 2) X(2, 3) X(2, 4) X(3, 2) X(3, 3)
 
 static int conv_fwd_launch(const ConvArgs &a, hipStream_t s) {
     const long blocks = (a.tasks + kConvWaves - 1) / kConvWaves;
     bool done = false;
-    if (blocks <= 0x7fffffffL) {
+    if (blocks <= 0x7fffffffL && strip_fits(a)) {
 #define KM_CONV_FWD(ND, KK)                                                                  \
         if (!done && a.nd == ND && a.K == KK) {                                              \
             hipLaunchKernelGGL((convnd_fwd_strip<ND, KK>), dim3(blocks), dim3(64 * kConvWaves), \
@@ -437,7 +529,7 @@ static int conv_bwd_launch(const ConvArgs &a, hipStream_t s) {
     if (zero_dev(a.db, a.D, s) != 0) return -1;
     const long blocks = (a.tasks + kConvWaves - 1) / kConvWaves;
     bool done = false;
-    if (blocks <= 0x7fffffffL) {
+    if (blocks <= 0x7fffffffL && strip_fits(a)) {
 #define KM_CONV_BWD(ND, KK)                                                                  \
         if (!done && a.nd == ND && a.K == KK) {                                              \
             hipLaunchKernelGGL((convnd_bwd_strip<ND, KK>), dim3(blocks), dim3(64 * kConvWaves), \
