@@ -13,16 +13,14 @@
 //  * lanes: 64 consecutive flattened (d, m) pairs, so B, C and h rows are
 //    256-byte coalesced accesses and y is a reduction over the M lanes of a
 //    channel;
-//  * the grid is cut into tiles; tiles with equal coordinate sum (a tile band)
-//    are independent, so the host issues one launch per tile band (15 for a
-//    256x256 grid with 32x32 tiles instead of 511 per-level launches); the
-//    kernel boundary publishes every tile's h to the next band;
-//  * inside a tile the last two axes form planes; waves own column strips of
-//    a plane and walk its rows in a skewed pipeline (wave w handles row
-//    tau - w at step tau), handing the strip's last state to the next wave
-//    through LDS with one barrier per step; the row above lives in registers;
-//    leading axes iterate planes, reading the previous plane's states back
-//    from memory (same CU, just written).
+//  * the grid is cut into tiles; tiles with equal tile-index sum (a tile
+//    band) are independent, so the host issues one launch per tile band (74
+//    for a 256x256 grid with 6x8 tiles instead of 511 per-level launches);
+//    the kernel boundary publishes every tile's h to the next band;
+//  * one wave per (tile, channel group) walks its tile row by row (rows
+//    along the last axis), keeping the row above in registers and taking
+//    the left neighbour from the previous column; neighbours across the
+//    tile's boundary and along leading axes are read back from h.
 #include <cstdlib>
 
 #include <cstdio>
@@ -127,6 +125,42 @@ __device__ __forceinline__ float sum_m_lanes(float v) {
     return v;
 }
 
+// Readouts of a row of TW columns (v[c] = C*h of this lane's state), summed
+// over the 16 state lanes of each channel and scattered: lane l returns the
+// total of column (l % 16) / (16 / TW). Each step keeps half of the
+// remaining columns and adds the partner's copy of that half; partners
+// differ in one lane bit per step (xor 8 by row_ror:8, xor 7 by
+// row_half_mirror, xor 2 and xor 1 by quad_perm), so the four steps cover
+// all 16 lanes, as a butterfly does.
+template <int CTRL, int BIT, int CNT, int TW>
+__device__ __forceinline__ void readout_step(float (&cur)[TW], int l) {
+    if constexpr (CNT > 1) {
+        constexpr int H = CNT / 2;
+        const bool hi = (l & BIT) != 0;
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const float keep = hi ? cur[H + i] : cur[i];
+            const float send = hi ? cur[i] : cur[H + i];
+            cur[i] = keep + dpp<CTRL>(send);
+        }
+    } else {
+        cur[0] += dpp<CTRL>(cur[0]);
+    }
+}
+template <int TW>
+__device__ __forceinline__ float row_readout(const float (&yr)[TW]) {
+    static_assert(TW == 4 || TW == 8 || TW == 16, "16 / TW lanes per column");
+    const int l = threadIdx.x & 15;
+    float cur[TW];
+#pragma unroll
+    for (int i = 0; i < TW; ++i) cur[i] = yr[i];
+    readout_step<0x128, 8, TW>(cur, l);                         // row_ror:8 (l ^ 8)
+    readout_step<0x141, 4, (TW > 2 ? TW / 2 : 1)>(cur, l);      // row_half_mirror (l ^ 7)
+    readout_step<0x4E, 2, (TW > 4 ? TW / 4 : 1)>(cur, l);       // quad_perm [2,3,0,1] (l ^ 2)
+    readout_step<0xB1, 1, (TW > 8 ? TW / 8 : 1)>(cur, l);       // quad_perm [1,0,3,2] (l ^ 1)
+    return cur[0];
+}
+
 // One wave per (tile, channel group). The wave walks its tile row by row
 // (rows along axis ND-2, leading axes outermost), each row along the last
 // axis, prefetching the next row's operands while the current row computes.
@@ -206,6 +240,8 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
     using F = bio<f32_t>;
 
     // Operands of one row (tile-relative row offset in points: r.base).
+    // Every load is unconditional: a load under a branch makes the
+    // compiler's wait-count merge at the join wait for the whole prefetch.
     auto load_row = [&](int row, NDRow<ND, TW> &r) {
         int rem = row;
         int roff = 0;
@@ -228,24 +264,25 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
             for (int a = 0; a < ND; ++a) r.dt[a][c] = F::ld(rdt[a], voffX[c], sx);
         }
         // Neighbours along leading axes, and along the row axis on the tile's
-        // first row of a plane (tile boundary); uniform conditions. Rows are
-        // prefetched one row ahead, so a leading-axis neighbour inside the
-        // tile must lie at least two rows back: the launcher never builds a
-        // tile with a single row per plane below an in-tile leading axis.
+        // first row of a plane (tile boundary). An unneeded neighbour loads
+        // the row's B values again instead (cache hits; compute_row skips its
+        // term). Rows are prefetched one row ahead, so a leading-axis
+        // neighbour inside the tile must lie at least two rows back: the
+        // launcher never builds a tile with a single row per plane below an
+        // in-tile leading axis.
         const int sh = (roff + static_cast<int>(hback)) * DM * 4;
 #pragma unroll
         for (int a = 0; a < ND - 1; ++a) {
-            const bool need = (a < ar) ? (r.gi[a] > 0) : (r.gi[a] > 0 && r.gi[a] == lo[a]);
-            if (need) {
-                const int sn = sh - static_cast<int>(p.pstride[a]) * DM * 4;
+            // Wave-uniform (readfirstlane), so the resource choice is scalar.
+            const bool need = __builtin_amdgcn_readfirstlane(
+                                  (a < ar) ? (r.gi[a] > 0) : (r.gi[a] > 0 && r.gi[a] == lo[a])) != 0;
+            const auto rn = need ? rh : rB;
+            const int sn = need ? sh - static_cast<int>(p.pstride[a]) * DM * 4 : sb;
 #pragma unroll
-                for (int c = 0; c < TW; ++c) r.hn[a][c] = F::ld(rh, voffB[c], sn);
-            } else {
-#pragma unroll
-                for (int c = 0; c < TW; ++c) r.hn[a][c] = 0.f;
-            }
+            for (int c = 0; c < TW; ++c) r.hn[a][c] = F::ld(rn, voffB[c], sn);
         }
-        r.hleft = (lo[ac] > 0) ? F::ld(rh, voffB[0], sh - DM * 4) : 0.f;
+        const bool left = __builtin_amdgcn_readfirstlane(lo[ac] > 0) != 0;
+        r.hleft = F::ld(left ? rh : rB, voffB[0], left ? sh - DM * 4 : sb);
     };
 
     float top[TW];
@@ -255,44 +292,72 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
     // product differs from the reference's division by at most one ulp.
     const float inv_nd = 1.0f / static_cast<float>(ND);
 
-    auto compute_row = [&](const NDRow<ND, TW> &r) {
+    // Stores of columns past the tile's edge (c >= TC, computed on repeated
+    // operands) and of lanes that own no output go to an offset with bit 31
+    // set, past the window, and are dropped: no branch around any store.
+    constexpr unsigned kDrop = 0x80000000u;
+    int hoff[TW];
+#pragma unroll
+    for (int c = 0; c < TW; ++c) hoff[c] = static_cast<int>(c < TC ? static_cast<unsigned>(voffB[c]) : kDrop);
+    // M = 16 and TW | 16: the row's TW readouts are reduce-scattered over
+    // the 16 state lanes of a channel, leaving lane l with column
+    // (l % 16) / (16 / TW), and stored with one instruction per row.
+    constexpr bool kRowY = (MM == 16) && (16 % TW == 0);
+    constexpr int YG = kRowY ? 16 / TW : 1;
+    int yoff = 0;
+    if constexpr (kRowY) {
+        const int yc = (lane % 16) / YG;
+        yoff = static_cast<int>((lane % YG == 0 && yc < TC) ? static_cast<unsigned>((yc * D + d) * 4) : kDrop);
+    }
+
+    auto compute_row = [&](const NDRow<ND, TW> &r, bool live) {
         const bool first_row_of_plane = (r.gi[ar] == lo[ar]);
         const int sh = (r.base + static_cast<int>(hback)) * DM * 4;
         const int sx = r.base * D * 4;
         float hleft = r.hleft;
+        float yr[TW];
 #pragma unroll
         for (int c = 0; c < TW; ++c) {
-            if (c < TC) {
-                float dsum = 0.f;
+            float dsum = 0.f;
 #pragma unroll
-                for (int a = 0; a < ND; ++a) dsum += r.dt[a][c];
-                float acc = (dsum * inv_nd) * (r.b[c] * r.x[c]);
+            for (int a = 0; a < ND; ++a) dsum += r.dt[a][c];
+            float acc = (dsum * inv_nd) * (r.b[c] * r.x[c]);
 #pragma unroll
-                for (int a = 0; a < ar; ++a)
-                    if (r.gi[a] > 0) acc = fmaf(exp2_fast(r.dt[a][c] * Ap[a]), r.hn[a][c], acc);
-                if (r.gi[ar] > 0) {
-                    const float hu = first_row_of_plane ? r.hn[ar][c] : top[c];
-                    acc = fmaf(exp2_fast(r.dt[ar][c] * Ap[ar]), hu, acc);
-                }
-                if (lo[ac] + c > 0) acc = fmaf(exp2_fast(r.dt[ac][c] * Ap[ac]), hleft, acc);
-                F::st(rh, voffB[c], sh, acc);
-                top[c] = acc;
-                hleft = acc;
+            for (int a = 0; a < ar; ++a)
+                if (r.gi[a] > 0) acc = fmaf(exp2_fast(r.dt[a][c] * Ap[a]), r.hn[a][c], acc);
+            if (r.gi[ar] > 0) {
+                const float hu = first_row_of_plane ? r.hn[ar][c] : top[c];
+                acc = fmaf(exp2_fast(r.dt[ar][c] * Ap[ar]), hu, acc);
+            }
+            if (lo[ac] + c > 0) acc = fmaf(exp2_fast(r.dt[ac][c] * Ap[ac]), hleft, acc);
+            F::st(rh, live ? hoff[c] : static_cast<int>(kDrop), sh, acc);
+            top[c] = acc;
+            hleft = acc;
+            if constexpr (kRowY) {
+                yr[c] = r.c[c] * acc;
+            } else {
                 const float yv = sum_m_lanes<MM>(r.c[c] * acc);
-                if (y_lane) F::st(ry, voffX[c], sx, yv);
+                F::st(ry, static_cast<int>(live && y_lane && c < TC ? static_cast<unsigned>(voffX[c]) : kDrop),
+                      sx, yv);
             }
         }
+        if constexpr (kRowY) F::st(ry, live ? yoff : static_cast<int>(kDrop), sx, row_readout<TW>(yr));
     };
 
+    // Rows are prefetched one ahead and processed in pairs with no branch in
+    // the loop: past the last row the last row is reloaded (in bounds) and,
+    // for an odd row count, computed once more with its stores dropped. The
+    // scheduling barriers keep a row's prefetch ahead of the previous row's
+    // arithmetic, so the first wait of a row covers only the older loads.
     NDRow<ND, TW> R0, R1;
     load_row(0, R0);
     for (int row = 0; row < nrows; row += 2) {
-        if (row + 1 < nrows) load_row(row + 1, R1);
-        compute_row(R0);
-        if (row + 1 < nrows) {
-            if (row + 2 < nrows) load_row(row + 2, R0);
-            compute_row(R1);
-        }
+        load_row(min(row + 1, nrows - 1), R1);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_row(R0, true);
+        load_row(min(row + 2, nrows - 1), R0);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_row(R1, row + 1 < nrows);
     }
 }
 

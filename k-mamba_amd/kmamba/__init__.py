@@ -15,7 +15,7 @@ from pathlib import Path
 
 PKG_ROOT = Path(__file__).resolve().parent.parent          # k-mamba_amd/
 # KMAMBA_LIB names another build of the library (same ABI) to load instead.
-LIB_PATH = Path(os.environ.get("KMAMBA_LIB", PKG_ROOT / "lib" / "libkmamba.so"))
+LIB_PATH = Path(os.environ.get("KMAMBA_LIB") or PKG_ROOT / "lib" / "libkmamba.so")
 INCLUDE_DIR = PKG_ROOT.parent / "include"
 
 if not LIB_PATH.exists():
