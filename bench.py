@@ -159,6 +159,41 @@ def scannd_alg_bytes(dims, D, M):
     return 4 * (P * D + nd * P * D + nd * D * M + 2 * P * D * M + P * D * M + P * D)
 
 
+def bench_mamba3(torch, K, steps, warmup, Bsz=8, L=2048, dim=1024, N=16, R=1):
+    """The reference Mamba-3 block forward (mamba_block_forward: the API's
+    synchronous call, input and output resident on the device, parameters
+    from mamba_block_init), at the configs[4] width and sequence length. The
+    call uploads the block's host-side parameters each time, as the
+    reference layout keeps them on the host; wall clock per call."""
+    import ctypes
+    cfg = K.MBConfig()
+    cfg.dim, cfg.state_size, cfg.seq_len, cfg.mimo_rank = dim, N, L, R
+    cfg.dt_scale, cfg.dt_min, cfg.dt_max = 0.1, 1e-3, 0.1
+    blk = K.mamba_block_create(ctypes.byref(cfg))
+    ctypes.CDLL(None).srand(11)
+    K.mamba_block_init(blk)
+    g = torch.Generator(device="cuda").manual_seed(41)
+    x = torch.randn((Bsz, L, dim), device="cuda", generator=g)
+    out = torch.empty_like(x)
+    fn = lambda: K.mamba_block_forward(blk, K.ptr(out), K.ptr(x), Bsz)  # noqa: E731
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t) * 1e3 / steps
+    err = K.km_last_error()
+    K.mamba_block_free(blk)
+    if err:
+        raise RuntimeError(err)
+    T = Bsz * L
+    return {"ms": round(ms, 4), "tokens_per_s": T / (ms * 1e-3),
+            "config": {"B": Bsz, "L": L, "dim": dim, "state_size": N, "mimo_rank": R,
+                       "io": "device pointers"}}
+
+
 def bench_scannd(torch, K, stream, dims, D, M, steps, warmup):
     """configs[2] workload: x ~ N(0,1); delta = 1; A = log(U(0.05, 0.9/nd));
     B, C ~ N(0, 1/16); scannd_ref semantics (h and y written)."""
@@ -197,25 +232,22 @@ def make_inputs(torch, Bsz, L, D, N, dtype, seed=0):
 
 
 def time_launches(torch, stream, fn, steps, warmup):
-    """Per-launch durations (ms) from HIP events recorded on the launch
-    stream, plus the wall time of the whole timed region."""
+    """Average duration (ms) of one call of fn, from two HIP events recorded
+    on the launch stream around `steps` back-to-back calls (events between
+    the calls would add their own gaps), as a per-call list, plus the wall
+    time of the timed region."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0.record(stream)
-    for a, b in ev:
-        a.record(stream)
+    for _ in range(steps):
         fn()
-        b.record(stream)
     t1.record(stream)
     torch.cuda.synchronize()
-    per = [a.elapsed_time(b) for a, b in ev]
-    return per, t0.elapsed_time(t1)
+    wall = t0.elapsed_time(t1)
+    return [wall / steps] * steps, wall
 
 
 def cpu_baseline_scan1d(x, dt, A, Bm, Cm, budget_s=12.0):
@@ -247,7 +279,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", choices=["all", "scan1d", "scan1d_bwd", "scannd", "convnd", "block",
-                                       "copy"],
+                                       "mamba3", "copy"],
                     default="all",
                     help="profiling modes: scan1d = the fp32 headline kernel only; copy = a plain "
                          "1 GiB device copy (calibrates rocprof FETCH_SIZE/WRITE_SIZE)")
@@ -283,6 +315,9 @@ def main():
         with torch.cuda.stream(stream):
             r = bench_mamba1_block(torch, K, stream, args.steps, args.warmup)
         print(json.dumps({"mamba1_block_configs4": r}))
+        return
+    if args.only == "mamba3":
+        print(json.dumps({"mamba3_block_fwd": bench_mamba3(torch, K, args.steps, min(args.warmup, 20))}))
         return
     if args.only == "convnd":
         with torch.cuda.stream(stream):
@@ -350,6 +385,7 @@ def main():
                                                                   max(5, args.steps // 2), 2)
         extra["scannd_3d_64cubed_D128_M16_f32"] = bench_scannd(torch, K, stream, (64, 64, 64), 128, 16,
                                                                 max(5, args.steps // 2), 2)
+        extra["mamba3_block_fwd_f32"] = bench_mamba3(torch, K, max(5, args.steps // 10), 2)
 
     traffic = None
     tf = ROOT / "profiles" / "scan1d_fwd_c1_traffic.json"
