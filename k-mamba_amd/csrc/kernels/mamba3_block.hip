@@ -13,8 +13,9 @@
 //      at once (fp32 SGEMM, 64x64 register-blocked tiles through LDS).
 //   2. prep: per (t, n) the step's decay a_t = alpha and its drive
 //      c_t = beta Bu_{t-1} + gamma Bu_t, which do not depend on h.
-//   3. scan: h_t = a_t * R(theta) h_{t-1} + c_t, one lane per state pair,
-//      the only sequential part; operands prefetched a step ahead.
+//   3. scan: h_t = a_t * R(theta) h_{t-1} + c_t per state pair, a chunked
+//      scan of 2x2 maps: one wave per (batch element, pair), one lane per
+//      chunk of steps.
 //   4. readout: Y[t, r] = sum_n C_t[r, n] h_t[n].
 //   5. out: out = x + W_out Y.
 #include <algorithm>
@@ -49,48 +50,84 @@ struct M3Args {
 };
 
 // ---- 1. projections ------------------------------------------------------
-constexpr int kPT = 64, kPJ = 64, kPK = 16;
+// P[t, j] = sum_d x[t, d] Wcat[j, d]: a 256-thread workgroup owns 64 tokens x
+// 64 controller rows; each thread 4 x 4 outputs. K advances in stages of 32:
+// the next stage's x and Wcat tiles are loaded (float4, coalesced rows) into
+// registers while the current stage computes from LDS, where they are stored
+// k-major so a thread's 4 tokens / 4 rows are one 16-byte read.
+constexpr int kPT = 64, kPJ = 64, kPK = 32, kPPad = 4;
 
 __global__ void __launch_bounds__(256) m3_proj(M3Args p) {
-    __shared__ float sx[kPK][kPT + 4];
-    __shared__ float sw[kPK][kPJ + 4];
+    __shared__ float sx[2][kPK][kPT + kPPad];
+    __shared__ float sw[2][kPK][kPJ + kPPad];
     const int tid = threadIdx.x;
-    const int tr = tid / 16, tc = tid % 16;           // 16 x 16 threads, 4 x 4 outputs each
+    const int ty = tid / 16, tx = tid % 16;            // 4 tokens x 4 rows each
     const long t0 = static_cast<long>(blockIdx.x) * kPT;
     const long j0 = static_cast<long>(blockIdx.y) * kPJ;
-    float acc[4][4] = {};
-    for (long k0 = 0; k0 < p.D; k0 += kPK) {
-        // 64 rows x 16 k of X and of Wcat: 1024 values each, 4 per thread.
-        for (int i = tid; i < kPT * kPK; i += 256) {
-            const int r = i / kPK, kk = i % kPK;
-            const long t = t0 + r, k = k0 + kk;
-            sx[kk][r] = (t < p.T && k < p.D) ? p.x[t * p.D + k] : 0.f;
-            const long j = j0 + r;
-            sw[kk][r] = (j < p.J && k < p.D) ? p.Wcat[j * p.D + k] : 0.f;
-        }
-        __syncthreads();
+    const bool vec = (p.D % 4) == 0;
+    float4 gx[2], gw[2];
+    // Thread i loads rows i/8 and i/8 + 32, k quad i%8 of the stage.
+    auto gload = [&](long k0) {
 #pragma unroll
-        for (int kk = 0; kk < kPK; ++kk) {
-            float xv[4], wv[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                xv[i] = sx[kk][tr * 4 + i];
-                wv[i] = sw[kk][tc * 4 + i];
+        for (int h = 0; h < 2; ++h) {
+            const int r = tid / 8 + h * 32, kq = (tid % 8) * 4;
+            const long t = t0 + r, j = j0 + r, k = k0 + kq;
+            float4 vx = make_float4(0.f, 0.f, 0.f, 0.f), vw = vx;
+            if (vec && k + 3 < p.D) {
+                if (t < p.T) vx = *reinterpret_cast<const float4 *>(p.x + t * p.D + k);
+                if (j < p.J) vw = *reinterpret_cast<const float4 *>(p.Wcat + j * p.D + k);
+            } else {
+                float ex[4] = {0.f, 0.f, 0.f, 0.f}, ew[4] = {0.f, 0.f, 0.f, 0.f};
+                for (int c = 0; c < 4; ++c) {
+                    if (k + c >= p.D) break;
+                    if (t < p.T) ex[c] = p.x[t * p.D + k + c];
+                    if (j < p.J) ew[c] = p.Wcat[j * p.D + k + c];
+                }
+                vx = make_float4(ex[0], ex[1], ex[2], ex[3]);
+                vw = make_float4(ew[0], ew[1], ew[2], ew[3]);
             }
+            gx[h] = vx;
+            gw[h] = vw;
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = tid / 8 + h * 32, kq = (tid % 8) * 4;
+            sx[buf][kq + 0][r] = gx[h].x; sx[buf][kq + 1][r] = gx[h].y;
+            sx[buf][kq + 2][r] = gx[h].z; sx[buf][kq + 3][r] = gx[h].w;
+            sw[buf][kq + 0][r] = gw[h].x; sw[buf][kq + 1][r] = gw[h].y;
+            sw[buf][kq + 2][r] = gw[h].z; sw[buf][kq + 3][r] = gw[h].w;
+        }
+    };
+    float acc[4][4] = {};
+    const long nk = (p.D + kPK - 1) / kPK;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (long ks = 0; ks < nk; ++ks) {
+        const int buf = ks & 1;
+        if (ks + 1 < nk) gload((ks + 1) * kPK);
+#pragma unroll 8
+        for (int kk = 0; kk < kPK; ++kk) {
+            const float4 xv = *reinterpret_cast<const float4 *>(&sx[buf][kk][ty * 4]);
+            const float4 wv = *reinterpret_cast<const float4 *>(&sw[buf][kk][tx * 4]);
+            const float xa[4] = {xv.x, xv.y, xv.z, xv.w}, wa[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xv[i], wv[j], acc[i][j]);
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xa[i], wa[j], acc[i][j]);
         }
+        if (ks + 1 < nk) sstore(buf ^ 1);
         __syncthreads();
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const long t = t0 + tr * 4 + i;
+        const long t = t0 + ty * 4 + i;
         if (t >= p.T) continue;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const long jj = j0 + tc * 4 + j;
+            const long jj = j0 + tx * 4 + j;
             if (jj < p.J) p.P[t * p.J + jj] = acc[i][j];
         }
     }
@@ -135,44 +172,74 @@ __global__ void __launch_bounds__(256) m3_prep(M3Args p) {
 }
 
 // ---- 3. the recurrence ------------------------------------------------------
-// One lane per state pair (2i, 2i+1) of one batch element; an odd last state
-// has no partner and no rotation. Waves hold 64 pairs of consecutive batch
-// elements' flattened (b, pair) index.
+// Per state pair (2i, 2i+1) of one batch element, h_t = M_t h_{t-1} + c_t
+// with M_t = diag(a0_t, a1_t) R(theta): a linear recurrence of 2x2 maps, so
+// it runs as a chunked scan. One wave per (batch element, pair); lane k owns
+// the chunk of CH = ceil(L/64) consecutive steps. (1) Each lane composes its
+// chunk's map h -> P h + v from a zero state. (2) An inclusive scan of the 64
+// maps across the lanes (Hillis-Steele, lane shuffles) gives every chunk the
+// state entering it (the previous lane's v). (3) Each lane replays its steps
+// from that state with the sequential step formula, writing H. An odd last
+// state has no partner: M_t = diag(a0_t, 0) and no rotation.
+__device__ __forceinline__ void m3_step(float a0, float a1, float cs, float sn, bool pair,
+                                        float c0, float c1, float &h0, float &h1) {
+    if (pair) {
+        const float r0 = cs * h0 - sn * h1, r1 = sn * h0 + cs * h1;
+        h0 = fmaf(a0, r0, c0);
+        h1 = fmaf(a1, r1, c1);
+    } else {
+        h0 = fmaf(a0, h0, c0);
+    }
+}
+
 __global__ void __launch_bounds__(64) m3_scan(M3Args p, long npairs) {
-    const long gid = static_cast<long>(blockIdx.x) * 64 + threadIdx.x;
-    const long nb = p.T / p.L;
-    if (gid >= nb * npairs) return;
-    const long b = gid / npairs, pi = gid % npairs;
+    const int lane = threadIdx.x;
+    const long b = blockIdx.x / npairs, pi = blockIdx.x % npairs;
     const long n0 = 2 * pi, n1 = n0 + 1;
     const bool pair = n1 < p.N;
     const float th = pair ? p.theta[pi] : 0.f;
-    const float cv = pair ? cosf(th) : 1.f, sv = pair ? sinf(th) : 0.f;
-    const long base = b * p.L * p.N;
-    float h0 = 0.f, h1 = 0.f;
-    float a0n = p.a[base + n0], c0n = p.c[base + n0];
-    float a1n = pair ? p.a[base + n1] : 0.f, c1n = pair ? p.c[base + n1] : 0.f;
-    for (long l = 0; l < p.L; ++l) {
-        const float a0 = a0n, c0 = c0n, a1 = a1n, c1 = c1n;
-        if (l + 1 < p.L) {                               // next step's operands
-            const long o = base + (l + 1) * p.N;
-            a0n = p.a[o + n0];
-            c0n = p.c[o + n0];
-            if (pair) {
-                a1n = p.a[o + n1];
-                c1n = p.c[o + n1];
-            }
+    const float cs = pair ? cosf(th) : 1.f, sn = pair ? sinf(th) : 0.f;
+    const long L = p.L, N = p.N;
+    const long CH = (L + 63) / 64;
+    const long l0 = lane * CH, l1 = min(l0 + CH, L);
+    const float *ab = p.a + b * L * N, *cb = p.c + b * L * N;
+
+    // (1) chunk map: P (2x2) and v, composed step by step from identity / 0.
+    float P00 = 1.f, P01 = 0.f, P10 = 0.f, P11 = 1.f, v0 = 0.f, v1 = 0.f;
+    for (long l = l0; l < l1; ++l) {
+        const float a0 = ab[l * N + n0], c0 = cb[l * N + n0];
+        const float a1 = pair ? ab[l * N + n1] : 0.f, c1 = pair ? cb[l * N + n1] : 0.f;
+        const float m00 = pair ? a0 * cs : a0, m01 = pair ? -a0 * sn : 0.f;
+        const float m10 = a1 * sn, m11 = a1 * cs;
+        const float q00 = m00 * P00 + m01 * P10, q01 = m00 * P01 + m01 * P11;
+        const float q10 = m10 * P00 + m11 * P10, q11 = m10 * P01 + m11 * P11;
+        P00 = q00; P01 = q01; P10 = q10; P11 = q11;
+        m3_step(a0, a1, cs, sn, pair, c0, c1, v0, v1);
+    }
+    // (2) inclusive scan over lanes: (P, v) <- (P, v) o (P', v') of lane - d.
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const float e00 = __shfl_up(P00, d), e01 = __shfl_up(P01, d);
+        const float e10 = __shfl_up(P10, d), e11 = __shfl_up(P11, d);
+        const float w0 = __shfl_up(v0, d), w1 = __shfl_up(v1, d);
+        if (lane >= d) {
+            const float nv0 = P00 * w0 + P01 * w1 + v0, nv1 = P10 * w0 + P11 * w1 + v1;
+            const float q00 = P00 * e00 + P01 * e10, q01 = P00 * e01 + P01 * e11;
+            const float q10 = P10 * e00 + P11 * e10, q11 = P10 * e01 + P11 * e11;
+            P00 = q00; P01 = q01; P10 = q10; P11 = q11;
+            v0 = nv0; v1 = nv1;
         }
-        const long o = base + l * p.N;
-        if (pair) {
-            const float r0 = cv * h0 - sv * h1, r1 = sv * h0 + cv * h1;
-            h0 = fmaf(a0, r0, c0);
-            h1 = fmaf(a1, r1, c1);
-            p.H[o + n0] = h0;
-            p.H[o + n1] = h1;
-        } else {
-            h0 = fmaf(a0, h0, c0);
-            p.H[o + n0] = h0;
-        }
+    }
+    // (3) replay from the state after the previous chunk (zero for chunk 0).
+    float h0 = __shfl_up(v0, 1), h1 = __shfl_up(v1, 1);
+    if (lane == 0) h0 = h1 = 0.f;
+    float *Hb = p.H + b * L * N;
+    for (long l = l0; l < l1; ++l) {
+        const float a0 = ab[l * N + n0], c0 = cb[l * N + n0];
+        const float a1 = pair ? ab[l * N + n1] : 0.f, c1 = pair ? cb[l * N + n1] : 0.f;
+        m3_step(a0, a1, cs, sn, pair, c0, c1, h0, h1);
+        Hb[l * N + n0] = h0;
+        if (pair) Hb[l * N + n1] = h1;
     }
 }
 
@@ -213,8 +280,8 @@ int mamba3_launch(M3Args &a, hipStream_t s) {
     hipLaunchKernelGGL(m3_proj, gp, dim3(256), 0, s, a);
     hipLaunchKernelGGL(m3_prep, dim3(grid256(a.T * a.N)), dim3(256), 0, s, a);
     const long npairs = (a.N + 1) / 2;
-    const long lanes = (a.T / a.L) * npairs;
-    hipLaunchKernelGGL(m3_scan, dim3((lanes + 63) / 64), dim3(64), 0, s, a, npairs);
+    const long waves = (a.T / a.L) * npairs;          // one per (batch element, pair)
+    hipLaunchKernelGGL(m3_scan, dim3(static_cast<unsigned>(waves)), dim3(64), 0, s, a, npairs);
     hipLaunchKernelGGL(m3_readout, dim3(grid256(a.T * a.R)), dim3(256), 0, s, a);
     hipLaunchKernelGGL(m3_out, dim3(grid256(a.T * a.D)), dim3(256), 0, s, a);
     KM_HIP_TRY(hipGetLastError());
@@ -354,26 +421,33 @@ void mamba_block_forward(MambaBlock *b, float *output, const float *input, size_
         km::Carver cv(base);
         float *x = dev_io ? const_cast<float *>(input) : cv.take<float>(T * D);
         float *o = dev_io ? output : cv.take<float>(T * D);
-        float *Wcat = cv.take<float>(J * D);
-        float *Wout = cv.take<float>(D * R);
-        float *A = cv.take<float>(N);
-        float *bB = cv.take<float>(NR), *bC = cv.take<float>(NR);
-        float *th = cv.take<float>(TS);
-        bool ok = true;
-        auto h2d = [&](void *dst, const void *src, size_t n) {
-            ok = ok && hipMemcpy(dst, src, n, hipMemcpyHostToDevice) == hipSuccess;
+        // Parameters live in host memory (the reference layout): pack them
+        // into one pinned block and upload it with a single copy.
+        const size_t nW = static_cast<size_t>(J * D), nO = static_cast<size_t>(D * R);
+        const size_t nP = nW + nO + N + 2 * NR + TS;
+        float *dpar = cv.take<float>(nP);
+        float *hp = static_cast<float *>(km::PinnedStaging::reserve(sizeof(float) * nP));
+        if (!hp) break;
+        (void)hipStreamSynchronize(nullptr);   // no earlier copy still reads the pinned block
+        float *Wcat = dpar, *Wout = dpar + nW, *A = Wout + nO, *bB = A + N, *bC = bB + NR, *th = bC + NR;
+        auto put = [&](float *dst, const float *src, size_t n) {
+            std::memcpy(hp + (dst - dpar), src, sizeof(float) * n);
         };
-        if (!dev_io) h2d(x, input, sizeof(float) * T * D);
-        h2d(Wcat, b->W_in.data, sizeof(float) * R * D);
-        if (has_delta) h2d(Wcat + R * D, b->delta_proj.data, sizeof(float) * D);
-        if (has_lambda) h2d(Wcat + (R + 1) * D, b->lambda_proj.data, sizeof(float) * D);
-        h2d(Wcat + (R + 2) * D, b->W_B.data, sizeof(float) * NR * D);
-        h2d(Wcat + (R + 2 + NR) * D, b->W_C.data, sizeof(float) * NR * D);
-        h2d(Wout, b->W_out.data, sizeof(float) * D * R);
-        h2d(A, b->A_log.data, sizeof(float) * N);
-        h2d(bB, b->b_B, sizeof(float) * NR);
-        h2d(bC, b->b_C, sizeof(float) * NR);
-        h2d(th, b->theta, sizeof(float) * TS);
+        if (!has_delta) std::memset(hp + R * D, 0, sizeof(float) * D);
+        if (!has_lambda) std::memset(hp + (R + 1) * D, 0, sizeof(float) * D);
+        put(Wcat, b->W_in.data, R * D);
+        if (has_delta) put(Wcat + R * D, b->delta_proj.data, D);
+        if (has_lambda) put(Wcat + (R + 1) * D, b->lambda_proj.data, D);
+        put(Wcat + (R + 2) * D, b->W_B.data, NR * D);
+        put(Wcat + (R + 2 + NR) * D, b->W_C.data, NR * D);
+        put(Wout, b->W_out.data, D * R);
+        put(A, b->A_log.data, N);
+        put(bB, b->b_B, NR);
+        put(bC, b->b_C, NR);
+        put(th, b->theta, TS);
+        bool ok = hipMemcpyAsync(dpar, hp, sizeof(float) * nP, hipMemcpyHostToDevice, nullptr) == hipSuccess;
+        if (!dev_io)
+            ok = ok && hipMemcpyAsync(x, input, sizeof(float) * T * D, hipMemcpyHostToDevice, nullptr) == hipSuccess;
         if (!ok) {
             km::set_error("mamba_block_forward: host-to-device copy failed");
             break;

@@ -200,6 +200,31 @@ void *Workspace::reserve(size_t bytes) {
     return p;
 }
 
+namespace {
+void *g_pin_ptr = nullptr;
+size_t g_pin_size = 0;
+}  // namespace
+
+void *PinnedStaging::reserve(size_t bytes) {
+    if (g_pin_size >= bytes && g_pin_ptr) return g_pin_ptr;
+    if (g_pin_ptr) {
+        (void)hipDeviceSynchronize();   // a copy may still read the old block
+        (void)hipHostFree(g_pin_ptr);
+        g_pin_ptr = nullptr;
+        g_pin_size = 0;
+    }
+    const size_t want = align_up(bytes, size_t(1) << 20);
+    void *p = nullptr;
+    if (hipHostMalloc(&p, want, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error("pinned staging: hipHostMalloc(%zu) failed", want);
+        return nullptr;
+    }
+    g_pin_ptr = p;
+    g_pin_size = want;
+    return p;
+}
+
 void Staging::lock() { g_stage_mu.lock(); }
 void Staging::unlock() { g_stage_mu.unlock(); }
 

@@ -32,6 +32,13 @@ struct Staging {
     static void unlock();
 };
 
+// Pinned host staging buffer (hipHostMalloc, process-wide, grow-only) for
+// packing many small host arrays into one DMA. Use under Staging::lock(); the
+// buffer may be reused once the copy that read it has completed.
+struct PinnedStaging {
+    static void *reserve(size_t bytes);      // nullptr on failure (error set)
+};
+
 // Per-device scratch for kernels that need device memory beyond their
 // inputs and outputs (e.g. the Scan1D backward accumulators), used when the
 // caller passes no workspace. Grows on demand and is reused; calls that
