@@ -50,6 +50,70 @@ __device__ __forceinline__ float epilogue(float v) {
     else return v;
 }
 
+// Epilogue of one wave's TI x TJ grid of 32 x 32 MFMA tiles at (row0, col0)
+// of C: bias, activation and conversion, staged through the wave's 16 KB of
+// LDS (row-major, a few row tiles per pass) so that C is written with
+// 16-byte stores of whole row segments instead of one scalar store per
+// element. The accumulator r of lane l holds row 8*(r/4) + 4*(l/32) + r%4,
+// column l%32 of its tile. Chunks that cross the N edge, or a C whose rows
+// are not 16-byte aligned, are stored element by element.
+template <int EPI, bool CBF16, int TI, int TJ>
+__device__ __forceinline__ void store_wave_tile(const GemmArgs &p, const f32x16 (&acc)[TI][TJ],
+                                                long row0, long col0, char *lds, int lane) {
+    constexpr int ES = CBF16 ? 2 : 4;
+    constexpr int ROWB = TJ * 32 * ES;                 // LDS bytes per row
+    constexpr int RC = (16384 / ROWB) < TI * 32 ? (16384 / ROWB) : TI * 32;   // rows per pass
+    static_assert(RC % 32 == 0 && (TI * 32) % RC == 0, "whole row tiles per pass");
+    constexpr int CPR = ROWB / 16;                     // 16-byte chunks per row
+    constexpr int EPC = 16 / ES;                       // elements per chunk
+    const int fr = lane & 31, fk = lane >> 5;
+    const bool vec = ((p.ldc * ES) % 16 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15) == 0);
+    float bv[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const long col = col0 + j * 32 + fr;
+        bv[j] = (p.bias && col < p.N) ? p.bias[col] : 0.f;
+    }
+#pragma unroll
+    for (int pass = 0; pass < TI * 32 / RC; ++pass) {
+#pragma unroll
+        for (int ii = 0; ii < RC / 32; ++ii) {
+            const int i = pass * (RC / 32) + ii;
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int rr = ii * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
+                    const float v = epilogue<EPI>(acc[i][j][r] + bv[j]);
+                    char *dst = lds + rr * ROWB + (j * 32 + fr) * ES;
+                    if constexpr (CBF16) *reinterpret_cast<uint16_t *>(dst) = f32_to_bf16(v);
+                    else *reinterpret_cast<float *>(dst) = v;
+                }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);            // lgkmcnt(0): this wave's LDS writes done
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int q = 0; q < RC * CPR / 64; ++q) {
+            const int idx = q * 64 + lane;
+            const int rr = idx / CPR, cb = idx % CPR;
+            const long row = row0 + pass * RC + rr;
+            const long col = col0 + cb * EPC;
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(lds + rr * ROWB + cb * 16);
+            if (row >= p.M || col >= p.N) continue;
+            char *g = static_cast<char *>(p.C) + (row * p.ldc + col) * ES;
+            if (vec && col + EPC <= p.N) {
+                *reinterpret_cast<u32x4 *>(g) = v;
+            } else {
+                const char *src = reinterpret_cast<const char *>(&v);
+                for (int e = 0; e < EPC && col + e < p.N; ++e)
+                    for (int b = 0; b < ES; ++b) g[e * ES + b] = src[e * ES + b];
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);            // reads done before the next pass writes
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
 template <int EPI, bool CBF16>
 __global__ void __launch_bounds__(256, 2) gemm_bf16_mfma(GemmArgs p) {
     __shared__ u32x4 sA[2][kBM * 8];
@@ -111,6 +175,7 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_mfma(GemmArgs p) {
     for (long kt = 0; kt < nk; ++kt) {
         const int buf = kt & 1;
         if (kt + 1 < nk) gload((kt + 1) * kBK);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
             const int ch = kk * 2 + fk;
@@ -132,34 +197,133 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_mfma(GemmArgs p) {
         __syncthreads();
     }
 
-    // Accumulator r of lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32
-    // of its 32 x 32 tile.
+    // The loop ended with a barrier after every wave's last LDS read: each
+    // wave now stages its tile through 16 KB of the operand buffers.
+    char *lds = (w < 2 ? reinterpret_cast<char *>(&sA[0][0]) : reinterpret_cast<char *>(&sB[0][0])) +
+                (w & 1) * 16384;
+    store_wave_tile<EPI, CBF16, 2, 2>(p, acc, m0 + wm * 64, n0 + wn * 64, lds, lane);
+}
+
+// Large shapes: a 256-thread workgroup computes a 256 x 256 tile of C; each
+// of its 4 waves owns a 128 x 128 quarter as 4 x 4 MFMA tiles (256 fp32
+// accumulators per lane, one wave per SIMD). Per 16-wide k step a wave reads
+// 4 A and 4 B fragments (8 KB of LDS) for 16 MFMAs, half the LDS bytes per
+// MFMA of the 64 x 64 wave tile above, so the LDS keeps up with the matrix
+// cores. K advances in stages of 32, double-buffered as above; the K tail is
+// masked per 16-byte chunk through an out-of-range offset.
+constexpr int kGM = 256, kGN = 256, kGK = 32;
+
+template <int EPI, bool CBF16>
+__global__ void __launch_bounds__(256, 1) gemm_bf16_mfma_256(GemmArgs p) {
+    __shared__ u32x4 sA[2][kGM * 4];
+    __shared__ u32x4 sB[2][kGN * 4];
+    constexpr unsigned kDrop = 0x80000000u;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = w >> 1, wn = w & 1;
+    const long m0 = static_cast<long>(blockIdx.y) * kGM;
+    const long n0 = static_cast<long>(blockIdx.x) * kGN;
+    const long arows = std::min<long>(kGM, p.M - m0), brows = std::min<long>(kGN, p.N - n0);
+    // Rows past the window read 0 (range check); the launcher keeps offsets
+    // below 2 GiB.
+    const auto rA = make_rsrc(p.A + m0 * p.lda, (arows - 1) * p.lda * 2 + p.K * 2);
+    const auto rB = make_rsrc(p.B + n0 * p.ldb, (brows - 1) * p.ldb * 2 + p.K * 2);
+
+    // A stage is 256 rows x 32 k = 4 chunks of 16 B per row; thread i loads
+    // chunks i, i + 256, ... (row c >> 2, chunk c & 3) of A and of B.
+    u32x4 ga[4], gb[4];
+    auto gload = [&](long k0) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const long col = n0 + wn * 64 + j * 32 + fr;
-            if (col >= p.N) continue;
-            const float bv = p.bias ? p.bias[col] : 0.f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const long row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
-                if (row < p.M) {
-                    const float v = epilogue<EPI>(acc[i][j][r] + bv);
-                    if constexpr (CBF16)
-                        static_cast<uint16_t *>(p.C)[row * p.ldc + col] = f32_to_bf16(v);
-                    else
-                        static_cast<float *>(p.C)[row * p.ldc + col] = v;
-                }
-            }
+        for (int i = 0; i < 4; ++i) {
+            const int c = tid + i * 256;
+            const int row = c >> 2, ch = c & 3;
+            const long k = k0 + ch * 8;
+            const bool kin = k < p.K;
+            const int offa = static_cast<int>(kin ? static_cast<unsigned>((row * p.lda + k) * 2) : kDrop);
+            const int offb = static_cast<int>(kin ? static_cast<unsigned>((row * p.ldb + k) * 2) : kDrop);
+            ga[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rA, offa, 0, 0));
+            gb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rB, offb, 0, 0));
         }
+    };
+    // LDS rows of 4 chunks, chunk c of row r at c ^ ((r >> 1) & 3): the 32
+    // rows of a fragment read spread over the banks.
+    auto sw = [](int row, int ch) { return row * 4 + (ch ^ ((row >> 1) & 3)); };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = tid + i * 256;
+            const int row = c >> 2, ch = c & 3;
+            sA[buf][sw(row, ch)] = ga[i];
+            sB[buf][sw(row, ch)] = gb[i];
+        }
+    };
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const long nk = (p.K + kGK - 1) / kGK;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    const int fr = lane & 31;
+    const int fk = lane >> 5;
+    // Fragments of both 16-wide k steps of a stage are read before its
+    // MFMAs, and the next stage's global loads are issued first: the MFMAs
+    // of step 0 overlap the LDS reads of step 1 and the global loads.
+    auto frag = [&](int buf, int kk, bf16x8 (&af)[4], bf16x8 (&bfr)[4]) {
+        const int ch = kk * 2 + fk;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            af[i] = __builtin_bit_cast(bf16x8, sA[buf][sw(wm * 128 + i * 32 + fr, ch)]);
+            bfr[i] = __builtin_bit_cast(bf16x8, sB[buf][sw(wn * 128 + i * 32 + fr, ch)]);
+        }
+    };
+    for (long kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        gload((kt + 1) * kGK);           // past K: every chunk masked, unused
+        bf16x8 a0[4], b0[4], a1[4], b1[4];
+        frag(buf, 0, a0, b0);
+        frag(buf, 1, a1, b1);
+        // Keep the loads here, ahead of the MFMAs (the scheduler would
+        // otherwise sink the global loads to their LDS store and wait for
+        // them at once).
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[i], b0[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[i], b1[j], acc[i][j], 0, 0, 0);
+        // ... and the LDS store (which waits for the global loads) after them.
+        __builtin_amdgcn_sched_barrier(0);
+        sstore(buf ^ 1);
+        __syncthreads();
     }
+
+    char *lds = (w < 2 ? reinterpret_cast<char *>(&sA[0][0]) : reinterpret_cast<char *>(&sB[0][0])) +
+                (w & 1) * 16384;
+    store_wave_tile<EPI, CBF16, 4, 4>(p, acc, m0 + wm * 128, n0 + wn * 128, lds, lane);
 }
 
 template <int EPI>
-static void gemm_go(const GemmArgs &a, dim3 g, hipStream_t s) {
-    if (a.c_bf16) hipLaunchKernelGGL((gemm_bf16_mfma<EPI, true>), g, dim3(256), 0, s, a);
-    else          hipLaunchKernelGGL((gemm_bf16_mfma<EPI, false>), g, dim3(256), 0, s, a);
+static void gemm_go(const GemmArgs &a, dim3 g, bool big, hipStream_t s) {
+    if (big) {
+        if (a.c_bf16) hipLaunchKernelGGL((gemm_bf16_mfma_256<EPI, true>), g, dim3(256), 0, s, a);
+        else          hipLaunchKernelGGL((gemm_bf16_mfma_256<EPI, false>), g, dim3(256), 0, s, a);
+    } else {
+        if (a.c_bf16) hipLaunchKernelGGL((gemm_bf16_mfma<EPI, true>), g, dim3(256), 0, s, a);
+        else          hipLaunchKernelGGL((gemm_bf16_mfma<EPI, false>), g, dim3(256), 0, s, a);
+    }
 }
 
 int gemm_bf16_launch(const KMGemm *g, hipStream_t s) {
@@ -180,31 +344,36 @@ int gemm_bf16_launch(const KMGemm *g, hipStream_t s) {
     }
     if (g->M == 0 || g->N == 0) return 0;
     if (!gpu_ready()) return -1;
-    if (g->ldb * 2 * (kBN + 1) > 0x7fffffffL || g->lda * 2 * (kBM + 1) > 0x7fffffffL) {
+    // 256 x 256 tiles when both output dimensions fill them (and K spans
+    // at least a few stages); 128 x 128 otherwise.
+    const bool big = g->M >= kGM && g->N >= kGN && g->K >= 4 * kGK &&
+                     g->ldb * 2 * (kGN + 1) <= 0x7fffffffL && g->lda * 2 * (kGM + 1) <= 0x7fffffffL;
+    const long TM = big ? kGM : kBM, TN = big ? kGN : kBN;
+    if (g->ldb * 2 * (TN + 1) > 0x7fffffffL || g->lda * 2 * (TM + 1) > 0x7fffffffL) {
         set_error("km_gemm_bf16: leading dimension too large");
         return -1;
     }
-    const long nbn = (g->N + kBN - 1) / kBN;
-    const long nbm = (g->M + kBM - 1) / kBM;
+    const long nbn = (g->N + TN - 1) / TN;
+    const long nbm = (g->M + TM - 1) / TM;
     if (nbn > 0x7fffffffL) { set_error("km_gemm_bf16: N too large"); return -1; }
     // Row blocks per launch stay within the 65535 grid-y limit.
     const long chunk = 65535;
     for (long mb = 0; mb < nbm; mb += chunk) {
         const long nb = std::min(chunk, nbm - mb);
         GemmArgs a{};
-        a.A = static_cast<const uint16_t *>(g->A) + mb * kBM * g->lda;
+        a.A = static_cast<const uint16_t *>(g->A) + mb * TM * g->lda;
         a.B = static_cast<const uint16_t *>(g->B);
         a.c_bf16 = (g->c_dtype == KM_BF16);
-        a.C = static_cast<char *>(g->C) + mb * kBM * g->ldc * (a.c_bf16 ? 2 : 4);
+        a.C = static_cast<char *>(g->C) + mb * TM * g->ldc * (a.c_bf16 ? 2 : 4);
         a.bias = g->bias;
-        a.M = std::min(g->M - mb * kBM, nb * kBM);
+        a.M = std::min(g->M - mb * TM, nb * TM);
         a.N = g->N; a.K = g->K; a.lda = g->lda; a.ldb = g->ldb; a.ldc = g->ldc;
         a.epi = g->epilogue;
         dim3 grid(static_cast<unsigned>(nbn), static_cast<unsigned>(nb));
         switch (g->epilogue) {
-        case KM_EPI_SOFTPLUS: gemm_go<KM_EPI_SOFTPLUS>(a, grid, s); break;
-        case KM_EPI_SILU:     gemm_go<KM_EPI_SILU>(a, grid, s); break;
-        default:              gemm_go<KM_EPI_NONE>(a, grid, s); break;
+        case KM_EPI_SOFTPLUS: gemm_go<KM_EPI_SOFTPLUS>(a, grid, big, s); break;
+        case KM_EPI_SILU:     gemm_go<KM_EPI_SILU>(a, grid, big, s); break;
+        default:              gemm_go<KM_EPI_NONE>(a, grid, big, s); break;
         }
         KM_HIP_TRY(hipGetLastError());
     }
