@@ -209,14 +209,16 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_mfma(GemmArgs p) {
 // accumulators per lane, one wave per SIMD). Per 16-wide k step a wave reads
 // 4 A and 4 B fragments (8 KB of LDS) for 16 MFMAs, half the LDS bytes per
 // MFMA of the 64 x 64 wave tile above, so the LDS keeps up with the matrix
-// cores. K advances in stages of 32, double-buffered as above; the K tail is
-// masked per 16-byte chunk through an out-of-range offset.
-constexpr int kGM = 256, kGN = 256, kGK = 32;
+// cores. K advances in stages of 64, double-buffered; LDS rows are padded to
+// nine 16-byte chunks, so the 16 rows one quarter-wave reads fall on 16
+// different chunk slots of a 256-byte bank line. The K tail is masked per
+// 16-byte chunk through an out-of-range offset.
+constexpr int kGM = 256, kGN = 256, kGK = 64, kGRow = 9;   // chunks per LDS row (8 + 1 pad)
 
 template <int EPI, bool CBF16>
 __global__ void __launch_bounds__(256, 1) gemm_bf16_mfma_256(GemmArgs p) {
-    __shared__ u32x4 sA[2][kGM * 4];
-    __shared__ u32x4 sB[2][kGN * 4];
+    __shared__ u32x4 sA[2][kGM * kGRow];
+    __shared__ u32x4 sB[2][kGN * kGRow];
     constexpr unsigned kDrop = 0x80000000u;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -230,14 +232,14 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_mfma_256(GemmArgs p) {
     const auto rA = make_rsrc(p.A + m0 * p.lda, (arows - 1) * p.lda * 2 + p.K * 2);
     const auto rB = make_rsrc(p.B + n0 * p.ldb, (brows - 1) * p.ldb * 2 + p.K * 2);
 
-    // A stage is 256 rows x 32 k = 4 chunks of 16 B per row; thread i loads
-    // chunks i, i + 256, ... (row c >> 2, chunk c & 3) of A and of B.
-    u32x4 ga[4], gb[4];
+    // A stage is 256 rows x 64 k = 8 chunks of 16 B per row; thread i loads
+    // chunks i, i + 256, ... (row c >> 3, chunk c & 7) of A and of B.
+    u32x4 ga[8], gb[8];
     auto gload = [&](long k0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 8; ++i) {
             const int c = tid + i * 256;
-            const int row = c >> 2, ch = c & 3;
+            const int row = c >> 3, ch = c & 7;
             const long k = k0 + ch * 8;
             const bool kin = k < p.K;
             const int offa = static_cast<int>(kin ? static_cast<unsigned>((row * p.lda + k) * 2) : kDrop);
@@ -246,16 +248,13 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_mfma_256(GemmArgs p) {
             gb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rB, offb, 0, 0));
         }
     };
-    // LDS rows of 4 chunks, chunk c of row r at c ^ ((r >> 1) & 3): the 32
-    // rows of a fragment read spread over the banks.
-    auto sw = [](int row, int ch) { return row * 4 + (ch ^ ((row >> 1) & 3)); };
     auto sstore = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 8; ++i) {
             const int c = tid + i * 256;
-            const int row = c >> 2, ch = c & 3;
-            sA[buf][sw(row, ch)] = ga[i];
-            sB[buf][sw(row, ch)] = gb[i];
+            const int row = c >> 3, ch = c & 7;
+            sA[buf][row * kGRow + ch] = ga[i];
+            sB[buf][row * kGRow + ch] = gb[i];
         }
     };
 
@@ -273,37 +272,39 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_mfma_256(GemmArgs p) {
     __syncthreads();
     const int fr = lane & 31;
     const int fk = lane >> 5;
-    // Fragments of both 16-wide k steps of a stage are read before its
-    // MFMAs, and the next stage's global loads are issued first: the MFMAs
-    // of step 0 overlap the LDS reads of step 1 and the global loads.
     auto frag = [&](int buf, int kk, bf16x8 (&af)[4], bf16x8 (&bfr)[4]) {
         const int ch = kk * 2 + fk;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            af[i] = __builtin_bit_cast(bf16x8, sA[buf][sw(wm * 128 + i * 32 + fr, ch)]);
-            bfr[i] = __builtin_bit_cast(bf16x8, sB[buf][sw(wn * 128 + i * 32 + fr, ch)]);
+            af[i] = __builtin_bit_cast(bf16x8, sA[buf][(wm * 128 + i * 32 + fr) * kGRow + ch]);
+            bfr[i] = __builtin_bit_cast(bf16x8, sB[buf][(wn * 128 + i * 32 + fr) * kGRow + ch]);
         }
     };
     for (long kt = 0; kt < nk; ++kt) {
         const int buf = kt & 1;
         gload((kt + 1) * kGK);           // past K: every chunk masked, unused
+        // Fragments of the stage's first 16-wide k step, read with the global
+        // loads ahead of the MFMAs (the scheduler would otherwise sink the
+        // loads to their LDS store and wait for them at once); each later
+        // step's fragments are read while the previous step's MFMAs run.
         bf16x8 a0[4], b0[4], a1[4], b1[4];
         frag(buf, 0, a0, b0);
-        frag(buf, 1, a1, b1);
-        // Keep the loads here, ahead of the MFMAs (the scheduler would
-        // otherwise sink the global loads to their LDS store and wait for
-        // them at once).
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int kk = 0; kk < 4; kk += 2) {
+            frag(buf, kk + 1, a1, b1);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[i], b0[j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[i], b0[j], acc[i][j], 0, 0, 0);
+            if (kk + 2 < 4) frag(buf, kk + 2, a0, b0);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[i], b1[j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[i], b1[j], acc[i][j], 0, 0, 0);
+        }
         // ... and the LDS store (which waits for the global loads) after them.
         __builtin_amdgcn_sched_barrier(0);
         sstore(buf ^ 1);
