@@ -14,8 +14,8 @@
 //    256-byte coalesced accesses and y is a reduction over the M lanes of a
 //    channel;
 //  * the grid is cut into tiles; tiles with equal tile-index sum (a tile
-//    band) are independent, so the host issues one launch per tile band (74
-//    for a 256x256 grid with 6x8 tiles instead of 511 per-level launches);
+//    band) are independent, so the host issues one launch per tile band (47
+//    for a 256x256 grid with 16x8 tiles instead of 511 per-level launches);
 //    the kernel boundary publishes every tile's h to the next band;
 //  * one wave per (tile, channel group) walks its tile row by row (rows
 //    along the last axis), keeping the row above in registers and taking
@@ -426,9 +426,10 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s) {
     // Tiles: rows of TWc points along the last axis, Tlead along each
     // leading axis. One wave per (tile, channel group); one launch per tile
     // band. Defaults measured fastest on MI355X at configs[2]: 2D rows of 8
-    // points x 6 rows; 3D and up rows of 4 points x 4 per leading axis.
-    int TWc = (a.nd == 2) ? 8 : 4;
-    int Tlead = (a.nd == 2) ? 6 : 4;
+    // points x 16 rows; 3D rows of 8 points x 4 per leading axis; 4D rows of
+    // 4 x 4.
+    int TWc = (a.nd <= 3) ? 8 : 4;
+    int Tlead = (a.nd == 2) ? 16 : 4;
     int nbands = 1;
     if (fast) {
         scannd_tile_shape(a.nd, TWc, Tlead);
