@@ -269,10 +269,11 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
         // term). Rows are prefetched one row ahead, so a leading-axis
         // neighbour inside the tile must lie at least two rows back: the
         // launcher never builds a tile with a single row per plane below an
-        // in-tile leading axis.
+        // in-tile leading axis. In 2D the only such neighbour is the row above
+        // the tile, which the wave loads into `top` before its first row.
         const int sh = (roff + static_cast<int>(hback)) * DM * 4;
 #pragma unroll
-        for (int a = 0; a < ND - 1; ++a) {
+        for (int a = 0; a < (ND == 2 ? 0 : ND - 1); ++a) {
             // Wave-uniform (readfirstlane), so the resource choice is scalar.
             const bool need = __builtin_amdgcn_readfirstlane(
                                   (a < ar) ? (r.gi[a] > 0) : (r.gi[a] > 0 && r.gi[a] == lo[a])) != 0;
@@ -286,8 +287,17 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
     };
 
     float top[TW];
+    if constexpr (ND == 2) {
+        // The row above the tile (from the band before), or 0 on the grid's
+        // first row; h at the tile origin minus one row is the start of rh's
+        // window whenever that row exists (unneeded: B row, cache hit).
+        const bool up = __builtin_amdgcn_readfirstlane(lo[0] > 0) != 0;
 #pragma unroll
-    for (int c = 0; c < TW; ++c) top[c] = 0.f;
+        for (int c = 0; c < TW; ++c) top[c] = F::ld(up ? rh : rB, voffB[c], 0);
+    } else {
+#pragma unroll
+        for (int c = 0; c < TW; ++c) top[c] = 0.f;
+    }
     // dt_bar = sum / ndims: 1/ndims is exact for ndims 2 and 4; for 3 the
     // product differs from the reference's division by at most one ulp.
     const float inv_nd = 1.0f / static_cast<float>(ND);
@@ -326,7 +336,8 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
             for (int a = 0; a < ar; ++a)
                 if (r.gi[a] > 0) acc = fmaf(exp2_fast(r.dt[a][c] * Ap[a]), r.hn[a][c], acc);
             if (r.gi[ar] > 0) {
-                const float hu = first_row_of_plane ? r.hn[ar][c] : top[c];
+                float hu = top[c];
+                if constexpr (ND > 2) hu = first_row_of_plane ? r.hn[ar][c] : top[c];
                 acc = fmaf(exp2_fast(r.dt[ar][c] * Ap[ar]), hu, acc);
             }
             if (lo[ac] + c > 0) acc = fmaf(exp2_fast(r.dt[ac][c] * Ap[ac]), hleft, acc);
@@ -344,20 +355,42 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
         if constexpr (kRowY) F::st(ry, live ? yoff : static_cast<int>(kDrop), sx, row_readout<TW>(yr));
     };
 
-    // Rows are prefetched one ahead and processed in pairs with no branch in
-    // the loop: past the last row the last row is reloaded (in bounds) and,
-    // for an odd row count, computed once more with its stores dropped. The
-    // scheduling barriers keep a row's prefetch ahead of the previous row's
-    // arithmetic, so the first wait of a row covers only the older loads.
-    NDRow<ND, TW> R0, R1;
-    load_row(0, R0);
-    for (int row = 0; row < nrows; row += 2) {
-        load_row(min(row + 1, nrows - 1), R1);
-        __builtin_amdgcn_sched_barrier(0);
-        compute_row(R0, true);
-        load_row(min(row + 2, nrows - 1), R0);
-        __builtin_amdgcn_sched_barrier(0);
-        compute_row(R1, row + 1 < nrows);
+    // Rows are prefetched ahead and processed in groups with no branch in
+    // the loop: past the last row the last row is reloaded (in bounds) and
+    // computed with its stores dropped. The scheduling barriers keep a row's
+    // prefetch ahead of the previous row's arithmetic, so a row's first wait
+    // covers only older loads. 2D tiles hold one wave per SIMD in a band, so
+    // their rows are prefetched two ahead through a ring of four; deeper
+    // tiles have more waves per SIMD and prefetch one ahead.
+    if constexpr (ND == 2) {
+        NDRow<ND, TW> R0, R1, R2, R3;
+        load_row(0, R0);
+        load_row(min(1, nrows - 1), R1);
+        for (int row = 0; row < nrows; row += 4) {
+            load_row(min(row + 2, nrows - 1), R2);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_row(R0, true);
+            load_row(min(row + 3, nrows - 1), R3);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_row(R1, row + 1 < nrows);
+            load_row(min(row + 4, nrows - 1), R0);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_row(R2, row + 2 < nrows);
+            load_row(min(row + 5, nrows - 1), R1);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_row(R3, row + 3 < nrows);
+        }
+    } else {
+        NDRow<ND, TW> R0, R1;
+        load_row(0, R0);
+        for (int row = 0; row < nrows; row += 2) {
+            load_row(min(row + 1, nrows - 1), R1);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_row(R0, true);
+            load_row(min(row + 2, nrows - 1), R0);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_row(R1, row + 1 < nrows);
+        }
     }
 }
 
