@@ -45,7 +45,10 @@ struct ConvArgs {
     int dims[kConvMaxNd];
     long stride[kConvMaxNd];
     long lines, njb, groups, tasks;
+    long louter, ngrp, tasks_l;    // line-group tasks: tuples of axes < nd-2, groups along nd-2
 };
+
+constexpr int kConvR = 4;          // output lines per wave in the line-group kernel
 
 // Workgroup id in an order where consecutive ids share an XCD: the hardware
 // deals workgroups to the 8 XCDs round-robin, so XCD x runs ids x, x+8, ...;
@@ -341,6 +344,143 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_bwd_strip(ConvArgs p) 
     }
 }
 
+// Forward, ND >= 2: a wave computes kConvR consecutive lines along axis
+// nd-2 (same coordinates on the axes before it) over one 64-point strip.
+// Those lines share input rows: they need K^(nd-2) x (kConvR + K - 1)
+// distinct input rows instead of kConvR x K^(nd-1), each loaded once per
+// column and kept as a K-wide window. Taps are summed per output in
+// row-major kernel order, as the reference does.
+template <int ND, int K>
+__global__ void __launch_bounds__(64 * kConvWaves) convnd_fwd_lines(ConvArgs p) {
+    constexpr int R = kConvR;
+    constexpr int KO = ipow(K, ND - 2);              // tap combinations of axes < nd-2
+    constexpr int RS = R + K - 1;                     // input rows per combination
+    constexpr int NR = KO * RS;
+    constexpr int KV = ipow(K, ND);
+    constexpr int CU = NR <= 6 ? 4 : (NR <= 12 ? 2 : 1);   // columns per load chunk
+    static_assert(kStrip % (2 * CU) == 0, "strip is whole chunk pairs");
+    using F = bio<f32_t>;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const long task = xcd_block(blockIdx.x, gridDim.x) * kConvWaves + wave;
+    if (task >= p.tasks_l) return;
+    const long g = task % p.groups;
+    long rest = task / p.groups;
+    const int j0 = static_cast<int>((rest % p.njb) * kStrip);
+    rest /= p.njb;
+    const long lg = rest % (p.louter * p.ngrp);
+    const long batch = rest / (p.louter * p.ngrp);
+    const int i0 = static_cast<int>((lg % p.ngrp) * R);          // first line along nd-2
+    long outer = lg / p.ngrp;
+    int lc[ND];                                                   // coordinates of axes < nd-1
+    lc[ND - 2] = i0;
+#pragma unroll
+    for (int a = ND - 3; a >= 0; --a) {
+        lc[a] = static_cast<int>(outer % p.dims[a]);
+        outer /= p.dims[a];
+    }
+    const int d = static_cast<int>(g * 64) + static_cast<int>(threadIdx.x & 63);
+    const bool dvalid = d < p.D;
+    const int dc = dvalid ? d : p.D - 1;
+    const int J = p.dims[ND - 1];
+    const long bbase = batch * p.P;
+    const auto rin = make_rsrc(p.in + bbase * p.D, p.P * p.D * 4);
+    const auto rout = make_rsrc(p.out + bbase * p.D, p.P * p.D * 4);
+    const int rb = p.D * 4;
+
+    float w[KV];
+#pragma unroll
+    for (int k = 0; k < KV; ++k) w[k] = p.W[static_cast<long>(k) * p.D + dc];
+    const float b0 = p.bias ? p.bias[dc] : 0.f;
+    // Input rows: combination ko of the axes < nd-2 (row-major, taps
+    // coordinate - (K-1-k)) and s along nd-2 (coordinate i0 - (K-1) + s).
+    unsigned ro[NR];
+#pragma unroll
+    for (int ko = 0; ko < KO; ++ko) {
+        int rem = ko;
+        long off = 0;
+        bool ok = true;
+#pragma unroll
+        for (int a = ND - 3; a >= 0; --a) {
+            const int ka = rem % K;
+            rem /= K;
+            const int c = lc[a] - (K - 1 - ka);
+            ok = ok && c >= 0 && c < p.dims[a];
+            off += static_cast<long>(c) * p.stride[a];
+        }
+#pragma unroll
+        for (int sidx = 0; sidx < RS; ++sidx) {
+            const int c = i0 - (K - 1) + sidx;
+            const bool okr = ok && c >= 0 && c < p.dims[ND - 2];
+            ro[ko * RS + sidx] = okr ? static_cast<unsigned>(((off + static_cast<long>(c) * p.stride[ND - 2]) * p.D + dc) * 4)
+                                     : kConvDrop;
+        }
+    }
+    // Output lines r: stored only for lines inside the grid and lanes < D.
+    unsigned oo[R];
+    {
+        long off = 0;
+#pragma unroll
+        for (int a = 0; a < ND - 2; ++a) off += static_cast<long>(lc[a]) * p.stride[a];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const bool ok = dvalid && i0 + r < p.dims[ND - 2];
+            oo[r] = ok ? static_cast<unsigned>(((off + static_cast<long>(i0 + r) * p.stride[ND - 2]) * p.D + dc) * 4)
+                       : kConvDrop;
+        }
+    }
+
+    // win[q][c]: input row q at column j - (K-1) + c (0 before column 0).
+    float win[NR][K];
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+#pragma unroll
+        for (int c = 0; c < K - 1; ++c) {
+            const int j = j0 - (K - 1) + c;
+            const float v = F::ld(rin, conv_off(ro[q], j < 0 ? 0 : j, rb), 0);
+            win[q][c + 1] = j >= 0 ? v : 0.f;
+        }
+    }
+    float n0[CU][NR], n1[CU][NR];
+    auto load_chunk = [&](int ch, float (&bx)[CU][NR]) {
+#pragma unroll
+        for (int u = 0; u < CU; ++u)
+#pragma unroll
+            for (int q = 0; q < NR; ++q) bx[u][q] = F::ld(rin, conv_off(ro[q], j0 + ch * CU + u, rb), 0);
+    };
+    auto run_chunk = [&](int ch, const float (&bx)[CU][NR]) {
+#pragma unroll
+        for (int u = 0; u < CU; ++u) {
+            const int j = j0 + ch * CU + u;
+#pragma unroll
+            for (int q = 0; q < NR; ++q) {
+#pragma unroll
+                for (int c = 0; c < K - 1; ++c) win[q][c] = win[q][c + 1];
+                win[q][K - 1] = bx[u][q];
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float sacc = b0;
+#pragma unroll
+                for (int ko = 0; ko < KO; ++ko)
+#pragma unroll
+                    for (int ka = 0; ka < K; ++ka)
+#pragma unroll
+                        for (int kc = 0; kc < K; ++kc)
+                            sacc += win[ko * RS + r + ka][kc] * w[(ko * K + ka) * K + kc];
+                F::st(rout, j < J ? conv_off(oo[r], j, rb) : static_cast<int>(kConvDrop), 0, sacc);
+            }
+        }
+    };
+    load_chunk(0, n0);
+#pragma unroll 1
+    for (int ch = 0; ch < kStrip / CU; ch += 2) {
+        load_chunk(ch + 1, n1);
+        run_chunk(ch, n0);
+        load_chunk(ch + 2, n0);
+        run_chunk(ch + 1, n1);
+    }
+}
+
 // Any ND <= 8 and K: one thread per (point, channel), taps from memory.
 __global__ void __launch_bounds__(256) convnd_fwd_generic(ConvArgs p) {
     const long gid = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -492,6 +632,11 @@ static bool conv_args(const ConvNDParams *p, long batch, bool bwd, ConvArgs &a, 
     a.njb = (a.dims[a.nd - 1] + kStrip - 1) / kStrip;
     a.groups = (a.D + 63) / 64;
     a.tasks = batch * a.lines * a.njb * a.groups;
+    if (a.nd >= 2) {
+        a.louter = a.lines / a.dims[a.nd - 2];
+        a.ngrp = (a.dims[a.nd - 2] + kConvR - 1) / kConvR;
+        a.tasks_l = batch * a.louter * a.ngrp * a.njb * a.groups;
+    }
     return true;
 }
 
@@ -504,9 +649,20 @@ static bool strip_fits(const ConvArgs &a) {
 #define KM_CONV_SHAPES(X) X(1, 2) X(1, 3) X(1, 4) X(2, 2) X(2, 3) X(2, 4) X(3, 2) X(3, 3)
 
 static int conv_fwd_launch(const ConvArgs &a, hipStream_t s) {
-    const long blocks = (a.tasks + kConvWaves - 1) / kConvWaves;
     bool done = false;
-    if (blocks <= 0x7fffffffL && strip_fits(a)) {
+    const long lblocks = (a.tasks_l + kConvWaves - 1) / kConvWaves;
+    if (a.nd >= 2 && lblocks > 0 && lblocks <= 0x7fffffffL && strip_fits(a)) {
+#define KM_CONV_FWDL(ND, KK)                                                                 \
+        if (!done && a.nd == ND && a.K == KK) {                                              \
+            hipLaunchKernelGGL((convnd_fwd_lines<ND, KK>), dim3(lblocks), dim3(64 * kConvWaves), \
+                               0, s, a);                                                     \
+            done = true;                                                                     \
+        }
+        KM_CONV_FWDL(2, 2) KM_CONV_FWDL(2, 3) KM_CONV_FWDL(2, 4) KM_CONV_FWDL(3, 2) KM_CONV_FWDL(3, 3)
+#undef KM_CONV_FWDL
+    }
+    const long blocks = (a.tasks + kConvWaves - 1) / kConvWaves;
+    if (!done && blocks <= 0x7fffffffL && strip_fits(a)) {
 #define KM_CONV_FWD(ND, KK)                                                                  \
         if (!done && a.nd == ND && a.K == KK) {                                              \
             hipLaunchKernelGGL((convnd_fwd_strip<ND, KK>), dim3(blocks), dim3(64 * kConvWaves), \

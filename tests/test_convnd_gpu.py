@@ -68,7 +68,8 @@ def gpu_bwd(dims, inp, ker, dy, with_bias):
 
 CASES = [((7,), 3, 2), ((9,), 70, 3), ((33,), 64, 4), ((5, 6), 5, 2), ((8, 9), 64, 3),
          ((70, 3), 130, 3), ((4, 5), 3, 4), ((3, 4, 5), 64, 3), ((5, 4, 3), 7, 2),
-         ((2, 3, 2, 3), 5, 3), ((6, 7), 4, 5), ((1, 1, 4), 65, 3), ((9,), 2, 1)]
+         ((2, 3, 2, 3), 5, 3), ((6, 7), 4, 5), ((1, 1, 4), 65, 3), ((9,), 2, 1),
+         ((4, 7, 9), 70, 3), ((10, 11), 65, 4), ((3, 6, 70), 3, 2)]
 
 
 @pytest.mark.parametrize("dims,D,Kk", CASES)
