@@ -129,6 +129,35 @@ __device__ __forceinline__ int conv_off(unsigned base, int j, int rowbytes) {
     return static_cast<int>(base + static_cast<unsigned>(j * rowbytes));
 }
 
+// Workgroup sum of the per-wave dkernel / dbias partials acc[0..KV], then one
+// atomic per (tap, channel). Waves of one workgroup may belong to different
+// channel groups (task % groups): the first wave of each group adds the
+// partials of the waves in that group. Every wave of the workgroup calls
+// this (it holds a barrier); ntasks bounds the task ids of the launch.
+template <int KV>
+__device__ __forceinline__ void conv_wg_reduce(const ConvArgs &p, float (&red)[kConvWaves][KV + 1][64],
+                                               const float (&acc)[KV + 1], int wave, int lane, long blk,
+                                               long ntasks, bool active, int dc) {
+#pragma unroll
+    for (int k = 0; k <= KV; ++k) red[wave][k][lane] = active ? acc[k] : 0.f;
+    __syncthreads();
+    if (!active) return;
+    const long g = (blk * kConvWaves + wave) % p.groups;
+    for (int v = 0; v < wave; ++v) {
+        const long tv = blk * kConvWaves + v;
+        if (tv < ntasks && tv % p.groups == g) return;
+    }
+    for (int k = 0; k <= KV; ++k) {
+        float s = 0.f;
+        for (int v = 0; v < kConvWaves; ++v) {
+            const long tv = blk * kConvWaves + v;
+            if (tv < ntasks && tv % p.groups == g) s += red[v][k][lane];
+        }
+        if (k < KV) unsafeAtomicAdd(p.dW + static_cast<long>(k) * p.D + dc, s);
+        else if (p.db) unsafeAtomicAdd(p.db + dc, s);
+    }
+}
+
 template <int ND, int K>
 __global__ void __launch_bounds__(64 * kConvWaves) convnd_fwd_strip(ConvArgs p) {
     constexpr int KL = (ND > 1) ? ipow(K, ND - 1) : 1;
@@ -316,45 +345,101 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_bwd_strip(ConvArgs p) 
             for (int k = 0; k <= KV; ++k) acc[k] = 0.f;
         }
     }
-    // Workgroup sum per (tap, channel), then one atomic each. Waves of one
-    // workgroup share the channel group when groups divide the task order.
+    conv_wg_reduce<KV>(p, red, acc, wave, lane, blk, p.tasks, live && t.dvalid, dc);
+}
+
+// Line-group kernels, ND >= 2: a wave covers kConvR consecutive lines along
+// axis nd-2 (same coordinates on the axes before it) over one 64-point strip.
+// Those lines share their tap rows: K^(nd-2) x (kConvR + K - 1) distinct rows
+// instead of kConvR x K^(nd-1), each loaded once per column and kept as a
+// K-wide window.
+struct LineTask {
+    long batch;
+    int j0, i0, d, dc;
+    bool dvalid;
+    int lc[kConvMaxNd];            // coordinates of axes < nd-2; lc[nd-2] = i0
+};
+
+template <int ND>
+__device__ __forceinline__ LineTask line_task(const ConvArgs &p, long task) {
+    LineTask t;
+    const long g = task % p.groups;
+    long rest = task / p.groups;
+    t.j0 = static_cast<int>((rest % p.njb) * kStrip);
+    rest /= p.njb;
+    const long lg = rest % (p.louter * p.ngrp);
+    t.batch = rest / (p.louter * p.ngrp);
+    t.i0 = static_cast<int>((lg % p.ngrp) * kConvR);
+    long outer = lg / p.ngrp;
+    t.lc[ND - 2] = t.i0;
 #pragma unroll
-    for (int k = 0; k <= KV; ++k) red[wave][k][lane] = acc[k];
-    __syncthreads();
-    // Waves of a workgroup may belong to different channel groups: the first
-    // wave of each group adds the partials of the waves in that group.
-    if (live && t.dvalid) {
-        const long g = (blk * kConvWaves + wave) % p.groups;
-        bool first = true;
-        for (int v = 0; v < wave; ++v) {
-            const long tv = blk * kConvWaves + v;
-            if (tv < p.tasks && tv % p.groups == g) first = false;
+    for (int a = ND - 3; a >= 0; --a) {
+        t.lc[a] = static_cast<int>(outer % p.dims[a]);
+        outer /= p.dims[a];
+    }
+    t.d = static_cast<int>(g * 64) + static_cast<int>(threadIdx.x & 63);
+    t.dvalid = t.d < p.D;
+    t.dc = t.dvalid ? t.d : p.D - 1;
+    return t;
+}
+
+// Byte offsets of the tap rows of a line group: combination ko of the axes
+// < nd-2 (row-major over taps k, coordinate c -/+ (K-1-k)) and s along nd-2,
+// coordinate i0 - (K-1) + s (causal) or i0 + s (anti-causal).
+template <int ND, int K, bool ANTI>
+__device__ __forceinline__ void group_rows(const ConvArgs &p, const LineTask &t,
+                                           unsigned (&ro)[ipow(K, ND - 2) * (kConvR + K - 1)]) {
+    constexpr int RS = kConvR + K - 1;
+#pragma unroll
+    for (int ko = 0; ko < ipow(K, ND - 2); ++ko) {
+        int rem = ko;
+        long off = 0;
+        bool ok = true;
+#pragma unroll
+        for (int a = ND - 3; a >= 0; --a) {
+            const int ka = rem % K;
+            rem /= K;
+            const int c = ANTI ? t.lc[a] + (K - 1 - ka) : t.lc[a] - (K - 1 - ka);
+            ok = ok && c >= 0 && c < p.dims[a];
+            off += static_cast<long>(c) * p.stride[a];
         }
-        if (first) {
-            for (int k = 0; k <= KV; ++k) {
-                float s = 0.f;
-                for (int v = 0; v < kConvWaves; ++v) {
-                    const long tv = blk * kConvWaves + v;
-                    if (tv < p.tasks && tv % p.groups == g) s += red[v][k][lane];
-                }
-                if (k < KV) unsafeAtomicAdd(p.dW + static_cast<long>(k) * p.D + dc, s);
-                else if (p.db) unsafeAtomicAdd(p.db + dc, s);
-            }
+#pragma unroll
+        for (int s = 0; s < RS; ++s) {
+            const int c = ANTI ? t.i0 + s : t.i0 - (K - 1) + s;
+            const bool okr = ok && c >= 0 && c < p.dims[ND - 2];
+            ro[ko * RS + s] =
+                okr ? static_cast<unsigned>(((off + static_cast<long>(c) * p.stride[ND - 2]) * p.D + t.dc) * 4)
+                    : kConvDrop;
         }
     }
 }
 
-// Forward, ND >= 2: a wave computes kConvR consecutive lines along axis
-// nd-2 (same coordinates on the axes before it) over one 64-point strip.
-// Those lines share input rows: they need K^(nd-2) x (kConvR + K - 1)
-// distinct input rows instead of kConvR x K^(nd-1), each loaded once per
-// column and kept as a K-wide window. Taps are summed per output in
-// row-major kernel order, as the reference does.
-template <int ND, int K>
-__global__ void __launch_bounds__(64 * kConvWaves) convnd_fwd_lines(ConvArgs p) {
+// Byte offsets of the kConvR lines of the group themselves, dropped for
+// lines past the grid and lanes past D.
+template <int ND>
+__device__ __forceinline__ void group_lines(const ConvArgs &p, const LineTask &t, unsigned (&oo)[kConvR]) {
+    long off = 0;
+#pragma unroll
+    for (int a = 0; a < ND - 2; ++a) off += static_cast<long>(t.lc[a]) * p.stride[a];
+#pragma unroll
+    for (int r = 0; r < kConvR; ++r) {
+        const bool ok = t.dvalid && t.i0 + r < p.dims[ND - 2];
+        oo[r] = ok ? static_cast<unsigned>(((off + static_cast<long>(t.i0 + r) * p.stride[ND - 2]) * p.D + t.dc) * 4)
+                   : kConvDrop;
+    }
+}
+
+// ANTI = false: the forward, out = bias + causal taps of in.
+// ANTI = true: dinput = anti-causal taps of dy (no bias).
+// Taps are summed per output in row-major kernel order, as the reference.
+// The causal window holds columns j-(K-1)..j (0 before column 0); the
+// anti-causal one columns j..j+K-1 (0 past the line end, where the offset
+// would land in the next line).
+template <int ND, int K, bool ANTI>
+__global__ void __launch_bounds__(64 * kConvWaves) convnd_lines(ConvArgs p) {
     constexpr int R = kConvR;
-    constexpr int KO = ipow(K, ND - 2);              // tap combinations of axes < nd-2
-    constexpr int RS = R + K - 1;                     // input rows per combination
+    constexpr int KO = ipow(K, ND - 2);
+    constexpr int RS = R + K - 1;
     constexpr int NR = KO * RS;
     constexpr int KV = ipow(K, ND);
     constexpr int CU = NR <= 6 ? 4 : (NR <= 12 ? 2 : 1);   // columns per load chunk
@@ -363,81 +448,31 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_fwd_lines(ConvArgs p) 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const long task = xcd_block(blockIdx.x, gridDim.x) * kConvWaves + wave;
     if (task >= p.tasks_l) return;
-    const long g = task % p.groups;
-    long rest = task / p.groups;
-    const int j0 = static_cast<int>((rest % p.njb) * kStrip);
-    rest /= p.njb;
-    const long lg = rest % (p.louter * p.ngrp);
-    const long batch = rest / (p.louter * p.ngrp);
-    const int i0 = static_cast<int>((lg % p.ngrp) * R);          // first line along nd-2
-    long outer = lg / p.ngrp;
-    int lc[ND];                                                   // coordinates of axes < nd-1
-    lc[ND - 2] = i0;
-#pragma unroll
-    for (int a = ND - 3; a >= 0; --a) {
-        lc[a] = static_cast<int>(outer % p.dims[a]);
-        outer /= p.dims[a];
-    }
-    const int d = static_cast<int>(g * 64) + static_cast<int>(threadIdx.x & 63);
-    const bool dvalid = d < p.D;
-    const int dc = dvalid ? d : p.D - 1;
+    const LineTask t = line_task<ND>(p, task);
     const int J = p.dims[ND - 1];
-    const long bbase = batch * p.P;
-    const auto rin = make_rsrc(p.in + bbase * p.D, p.P * p.D * 4);
-    const auto rout = make_rsrc(p.out + bbase * p.D, p.P * p.D * 4);
+    const long bbase = t.batch * p.P;
+    const auto rin = make_rsrc((ANTI ? p.dy : p.in) + bbase * p.D, p.P * p.D * 4);
+    const auto rout = make_rsrc((ANTI ? p.din : p.out) + bbase * p.D, p.P * p.D * 4);
     const int rb = p.D * 4;
+    const int j0 = t.j0;
 
     float w[KV];
 #pragma unroll
-    for (int k = 0; k < KV; ++k) w[k] = p.W[static_cast<long>(k) * p.D + dc];
-    const float b0 = p.bias ? p.bias[dc] : 0.f;
-    // Input rows: combination ko of the axes < nd-2 (row-major, taps
-    // coordinate - (K-1-k)) and s along nd-2 (coordinate i0 - (K-1) + s).
-    unsigned ro[NR];
-#pragma unroll
-    for (int ko = 0; ko < KO; ++ko) {
-        int rem = ko;
-        long off = 0;
-        bool ok = true;
-#pragma unroll
-        for (int a = ND - 3; a >= 0; --a) {
-            const int ka = rem % K;
-            rem /= K;
-            const int c = lc[a] - (K - 1 - ka);
-            ok = ok && c >= 0 && c < p.dims[a];
-            off += static_cast<long>(c) * p.stride[a];
-        }
-#pragma unroll
-        for (int sidx = 0; sidx < RS; ++sidx) {
-            const int c = i0 - (K - 1) + sidx;
-            const bool okr = ok && c >= 0 && c < p.dims[ND - 2];
-            ro[ko * RS + sidx] = okr ? static_cast<unsigned>(((off + static_cast<long>(c) * p.stride[ND - 2]) * p.D + dc) * 4)
-                                     : kConvDrop;
-        }
-    }
-    // Output lines r: stored only for lines inside the grid and lanes < D.
-    unsigned oo[R];
-    {
-        long off = 0;
-#pragma unroll
-        for (int a = 0; a < ND - 2; ++a) off += static_cast<long>(lc[a]) * p.stride[a];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const bool ok = dvalid && i0 + r < p.dims[ND - 2];
-            oo[r] = ok ? static_cast<unsigned>(((off + static_cast<long>(i0 + r) * p.stride[ND - 2]) * p.D + dc) * 4)
-                       : kConvDrop;
-        }
-    }
-
-    // win[q][c]: input row q at column j - (K-1) + c (0 before column 0).
+    for (int k = 0; k < KV; ++k) w[k] = p.W[static_cast<long>(k) * p.D + t.dc];
+    const float b0 = (!ANTI && p.bias) ? p.bias[t.dc] : 0.f;
+    unsigned ro[NR], oo[R];
+    group_rows<ND, K, ANTI>(p, t, ro);
+    group_lines<ND>(p, t, oo);
+    // Column loaded at step j, and the one the window starts with.
+    constexpr int LEAD = ANTI ? K - 1 : 0;
     float win[NR][K];
 #pragma unroll
     for (int q = 0; q < NR; ++q) {
 #pragma unroll
         for (int c = 0; c < K - 1; ++c) {
-            const int j = j0 - (K - 1) + c;
+            const int j = j0 - (K - 1) + LEAD + c;
             const float v = F::ld(rin, conv_off(ro[q], j < 0 ? 0 : j, rb), 0);
-            win[q][c + 1] = j >= 0 ? v : 0.f;
+            win[q][c + 1] = (j >= 0 && j < J) ? v : 0.f;
         }
     }
     float n0[CU][NR], n1[CU][NR];
@@ -445,29 +480,33 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_fwd_lines(ConvArgs p) 
 #pragma unroll
         for (int u = 0; u < CU; ++u)
 #pragma unroll
-            for (int q = 0; q < NR; ++q) bx[u][q] = F::ld(rin, conv_off(ro[q], j0 + ch * CU + u, rb), 0);
+            for (int q = 0; q < NR; ++q) bx[u][q] = F::ld(rin, conv_off(ro[q], j0 + ch * CU + u + LEAD, rb), 0);
     };
     auto run_chunk = [&](int ch, const float (&bx)[CU][NR]) {
 #pragma unroll
         for (int u = 0; u < CU; ++u) {
             const int j = j0 + ch * CU + u;
+            const bool in_line = !ANTI || j + LEAD < J;
 #pragma unroll
             for (int q = 0; q < NR; ++q) {
 #pragma unroll
                 for (int c = 0; c < K - 1; ++c) win[q][c] = win[q][c + 1];
-                win[q][K - 1] = bx[u][q];
+                win[q][K - 1] = in_line ? bx[u][q] : 0.f;
             }
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                float sacc = b0;
+                float s = b0;
 #pragma unroll
                 for (int ko = 0; ko < KO; ++ko)
 #pragma unroll
                     for (int ka = 0; ka < K; ++ka)
 #pragma unroll
-                        for (int kc = 0; kc < K; ++kc)
-                            sacc += win[ko * RS + r + ka][kc] * w[(ko * K + ka) * K + kc];
-                F::st(rout, j < J ? conv_off(oo[r], j, rb) : static_cast<int>(kConvDrop), 0, sacc);
+                        for (int kc = 0; kc < K; ++kc) {
+                            const float x = ANTI ? win[ko * RS + r + (K - 1 - ka)][K - 1 - kc]
+                                                 : win[ko * RS + r + ka][kc];
+                            s += x * w[(ko * K + ka) * K + kc];
+                        }
+                F::st(rout, j < J ? conv_off(oo[r], j, rb) : static_cast<int>(kConvDrop), 0, s);
             }
         }
     };
@@ -479,6 +518,99 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_fwd_lines(ConvArgs p) 
         load_chunk(ch + 2, n0);
         run_chunk(ch + 1, n1);
     }
+}
+
+// dkernel / dbias over line groups: acc[k] += dy[line r, j] * in[causal tap
+// k of (r, j)], acc[KV] += dy, then the workgroup reduction and one atomic
+// per (tap, channel) per workgroup.
+template <int ND, int K>
+__global__ void __launch_bounds__(64 * kConvWaves) convnd_dw_lines(ConvArgs p) {
+    constexpr int R = kConvR;
+    constexpr int KO = ipow(K, ND - 2);
+    constexpr int RS = R + K - 1;
+    constexpr int NR = KO * RS;
+    constexpr int KV = ipow(K, ND);
+    constexpr int CU = NR + R <= 8 ? 4 : (NR + R <= 14 ? 2 : 1);
+    static_assert(kStrip % (2 * CU) == 0, "strip is whole chunk pairs");
+    using F = bio<f32_t>;
+    __shared__ float red[kConvWaves][KV + 1][64];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const long blk = xcd_block(blockIdx.x, gridDim.x);
+    const long task = blk * kConvWaves + wave;
+    const bool live = task < p.tasks_l;
+    float acc[KV + 1];
+#pragma unroll
+    for (int k = 0; k <= KV; ++k) acc[k] = 0.f;
+    LineTask t{};
+    if (live) {
+        t = line_task<ND>(p, task);
+        const int J = p.dims[ND - 1];
+        const long bbase = t.batch * p.P;
+        const auto rin = make_rsrc(p.in + bbase * p.D, p.P * p.D * 4);
+        const auto rdy = make_rsrc(p.dy + bbase * p.D, p.P * p.D * 4);
+        const int rb = p.D * 4;
+        const int j0 = t.j0;
+        unsigned ro[NR], og[R];
+        group_rows<ND, K, false>(p, t, ro);
+        group_lines<ND>(p, t, og);        // dy of lanes past D and lines past the grid: 0
+        float win[NR][K];
+#pragma unroll
+        for (int q = 0; q < NR; ++q) {
+#pragma unroll
+            for (int c = 0; c < K - 1; ++c) {
+                const int j = j0 - (K - 1) + c;
+                const float v = F::ld(rin, conv_off(ro[q], j < 0 ? 0 : j, rb), 0);
+                win[q][c + 1] = j >= 0 ? v : 0.f;
+            }
+        }
+        float x0[CU][NR], g0[CU][R], x1[CU][NR], g1[CU][R];
+        auto load_chunk = [&](int ch, float (&bx)[CU][NR], float (&bg)[CU][R]) {
+#pragma unroll
+            for (int u = 0; u < CU; ++u) {
+                const int j = j0 + ch * CU + u;
+#pragma unroll
+                for (int q = 0; q < NR; ++q) bx[u][q] = F::ld(rin, conv_off(ro[q], j, rb), 0);
+#pragma unroll
+                for (int r = 0; r < R; ++r) bg[u][r] = F::ld(rdy, conv_off(og[r], j, rb), 0);
+            }
+        };
+        auto run_chunk = [&](int ch, const float (&bx)[CU][NR], const float (&bg)[CU][R]) {
+#pragma unroll
+            for (int u = 0; u < CU; ++u) {
+                const int j = j0 + ch * CU + u;
+#pragma unroll
+                for (int q = 0; q < NR; ++q) {
+#pragma unroll
+                    for (int c = 0; c < K - 1; ++c) win[q][c] = win[q][c + 1];
+                    win[q][K - 1] = bx[u][q];
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const float g = j < J ? bg[u][r] : 0.f;
+#pragma unroll
+                    for (int ko = 0; ko < KO; ++ko)
+#pragma unroll
+                        for (int ka = 0; ka < K; ++ka)
+#pragma unroll
+                            for (int kc = 0; kc < K; ++kc) {
+                                const int k = (ko * K + ka) * K + kc;
+                                acc[k] = fmaf(g, win[ko * RS + r + ka][kc], acc[k]);
+                            }
+                    acc[KV] += g;
+                }
+            }
+        };
+        load_chunk(0, x0, g0);
+#pragma unroll 1
+        for (int ch = 0; ch < kStrip / CU; ch += 2) {
+            load_chunk(ch + 1, x1, g1);
+            run_chunk(ch, x0, g0);
+            load_chunk(ch + 2, x0, g0);
+            run_chunk(ch + 1, x1, g1);
+        }
+    }
+    conv_wg_reduce<KV>(p, red, acc, wave, lane, blk, p.tasks_l, live && t.dvalid, t.dc);
 }
 
 // Any ND <= 8 and K: one thread per (point, channel), taps from memory.
@@ -654,7 +786,7 @@ static int conv_fwd_launch(const ConvArgs &a, hipStream_t s) {
     if (a.nd >= 2 && lblocks > 0 && lblocks <= 0x7fffffffL && strip_fits(a)) {
 #define KM_CONV_FWDL(ND, KK)                                                                 \
         if (!done && a.nd == ND && a.K == KK) {                                              \
-            hipLaunchKernelGGL((convnd_fwd_lines<ND, KK>), dim3(lblocks), dim3(64 * kConvWaves), \
+            hipLaunchKernelGGL((convnd_lines<ND, KK, false>), dim3(lblocks), dim3(64 * kConvWaves), \
                                0, s, a);                                                     \
             done = true;                                                                     \
         }
@@ -683,9 +815,22 @@ static int conv_fwd_launch(const ConvArgs &a, hipStream_t s) {
 static int conv_bwd_launch(const ConvArgs &a, hipStream_t s) {
     if (zero_dev(a.dW, static_cast<long>(a.KV) * a.D, s) != 0) return -1;
     if (zero_dev(a.db, a.D, s) != 0) return -1;
-    const long blocks = (a.tasks + kConvWaves - 1) / kConvWaves;
     bool done = false;
-    if (blocks <= 0x7fffffffL && strip_fits(a)) {
+    const long lblocks = (a.tasks_l + kConvWaves - 1) / kConvWaves;
+    if (a.nd >= 2 && lblocks > 0 && lblocks <= 0x7fffffffL && strip_fits(a)) {
+#define KM_CONV_BWDL(ND, KK)                                                                 \
+        if (!done && a.nd == ND && a.K == KK) {                                              \
+            hipLaunchKernelGGL((convnd_lines<ND, KK, true>), dim3(lblocks), dim3(64 * kConvWaves), \
+                               0, s, a);                                                     \
+            hipLaunchKernelGGL((convnd_dw_lines<ND, KK>), dim3(lblocks), dim3(64 * kConvWaves), \
+                               0, s, a);                                                     \
+            done = true;                                                                     \
+        }
+        KM_CONV_BWDL(2, 2) KM_CONV_BWDL(2, 3) KM_CONV_BWDL(2, 4) KM_CONV_BWDL(3, 2) KM_CONV_BWDL(3, 3)
+#undef KM_CONV_BWDL
+    }
+    const long blocks = (a.tasks + kConvWaves - 1) / kConvWaves;
+    if (!done && blocks <= 0x7fffffffL && strip_fits(a)) {
 #define KM_CONV_BWD(ND, KK)                                                                  \
         if (!done && a.nd == ND && a.K == KK) {                                              \
             hipLaunchKernelGGL((convnd_bwd_strip<ND, KK>), dim3(blocks), dim3(64 * kConvWaves), \
