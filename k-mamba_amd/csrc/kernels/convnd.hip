@@ -9,15 +9,21 @@
 //
 // Design: the 64 lanes of a wave are 64 channels, so every point row of a
 // tensor is one coalesced 256-byte access. A wave sweeps a strip of points
-// along the last axis for one tuple of leading coordinates ("line"), keeping
-// a K-wide window of inputs for each of the K^(N-1) leading tap offsets in
-// registers: each step loads K^(N-1) new values instead of K^N. Lines that
-// share inputs (neighbours along the leading axes) are adjacent in the task
-// order, and workgroups are renumbered so that consecutive tasks run on the
-// same XCD and find each other's rows in that XCD's L2. The backward sweeps
-// the same strips with a trailing input window (for dkernel) and a leading
-// dy window (for dinput), reduces dkernel/dbias over the workgroup in LDS and
-// adds them with one fp32 atomic per (tap, channel) per workgroup.
+// along the last axis and keeps, for each tap row it reads, a K-wide window
+// in registers: each step loads one new value per row instead of K.
+//  - 2D and 3D (K <= 4 / K <= 3), the line-group kernels: a wave covers four
+//    adjacent lines along axis N-2, which share their tap rows
+//    (K^(N-2) x (K+3) rows for four lines instead of 4 x K^(N-1)). The
+//    forward and dinput (anti-causal taps of dy) are one kernel; dkernel /
+//    dbias accumulate per wave, are summed per workgroup in LDS and stored to
+//    one slot per workgroup in the library workspace, and a second kernel
+//    adds the slots in a fixed order (no atomics, run-to-run identical).
+//  - Other shapes with N <= 3: one line per wave; the backward fuses dinput
+//    and dkernel and adds dkernel per workgroup with fp32 atomics.
+//  - Anything else: one thread per (point, channel), taps from memory.
+// Lines that share inputs are adjacent in the task order, and workgroups are
+// renumbered so that consecutive tasks run on the same XCD and find each
+// other's rows in that XCD's L2.
 #include <algorithm>
 
 #include "km_device.hpp"
@@ -45,7 +51,9 @@ struct ConvArgs {
     int dims[kConvMaxNd];
     long stride[kConvMaxNd];
     long lines, njb, groups, tasks;
-    long louter, ngrp, tasks_l;    // line-group tasks: tuples of axes < nd-2, groups along nd-2
+    long louter, ngrp;             // line groups: tuples of axes < nd-2, groups along nd-2
+    int strip_l;                   // strip length of the line-group kernels (16, 32 or 64)
+    long njb_l, tasks_l;
 };
 
 constexpr int kConvR = 4;          // output lines per wave in the line-group kernel
@@ -349,7 +357,9 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_bwd_strip(ConvArgs p) 
 }
 
 // Line-group kernels, ND >= 2: a wave covers kConvR consecutive lines along
-// axis nd-2 (same coordinates on the axes before it) over one 64-point strip.
+// axis nd-2 (same coordinates on the axes before it) over one strip of S
+// points (S = 64, or 32 / 16 where longer strips would leave fewer than two
+// waves per SIMD).
 // Those lines share their tap rows: K^(nd-2) x (kConvR + K - 1) distinct rows
 // instead of kConvR x K^(nd-1), each loaded once per column and kept as a
 // K-wide window.
@@ -360,13 +370,14 @@ struct LineTask {
     int lc[kConvMaxNd];            // coordinates of axes < nd-2; lc[nd-2] = i0
 };
 
-template <int ND>
-__device__ __forceinline__ LineTask line_task(const ConvArgs &p, long task) {
+// Task tl of channel group g: tl = ((batch * louter + outer) * ngrp + group)
+// * njb_l + strip.
+template <int ND, int S>
+__device__ __forceinline__ LineTask line_task(const ConvArgs &p, long g, long tl) {
     LineTask t;
-    const long g = task % p.groups;
-    long rest = task / p.groups;
-    t.j0 = static_cast<int>((rest % p.njb) * kStrip);
-    rest /= p.njb;
+    long rest = tl;
+    t.j0 = static_cast<int>((rest % p.njb_l) * S);
+    rest /= p.njb_l;
     const long lg = rest % (p.louter * p.ngrp);
     t.batch = rest / (p.louter * p.ngrp);
     t.i0 = static_cast<int>((lg % p.ngrp) * kConvR);
@@ -429,26 +440,77 @@ __device__ __forceinline__ void group_lines(const ConvArgs &p, const LineTask &t
     }
 }
 
+// dkernel[k, d] (k < KV) or dbias[d] (k = KV) of channel group g: the sum of
+// the nslot per-workgroup slots that convnd_dw_lines stored. Wave w of the
+// workgroup adds slots w, w + 4, ... (32 independent loads per round), then
+// wave 0 adds the four partials: a fixed order, so the result does not
+// depend on timing.
+__device__ __forceinline__ void dw_finalize(const ConvArgs &p, const float *part, int nslot, int k, long g,
+                                            int wave, int lane, float (&red)[kConvWaves][64]) {
+    using F = bio<f32_t>;
+    const int KV = p.KV;
+    const long per_slot = static_cast<long>(KV + 1) * 64;
+    const auto rp = make_rsrc(part + g * nslot * per_slot, nslot * per_slot * 4);
+    float s = 0.f;
+#pragma unroll 1
+    for (int b0 = 0; b0 < nslot; b0 += 32 * kConvWaves) {
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const int b = b0 + i * kConvWaves + wave;
+            v[i] = F::ld(rp, b < nslot ? static_cast<int>(((b * (KV + 1) + k) * 64 + lane) * 4)
+                                       : static_cast<int>(kConvDrop), 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) s += v[i];
+    }
+    red[wave][lane] = s;
+    __syncthreads();
+    if (wave != 0) return;
+    float sum = 0.f;
+#pragma unroll
+    for (int v = 0; v < kConvWaves; ++v) sum += red[v][lane];
+    const long d = g * 64 + lane;
+    if (d >= p.D) return;
+    if (k < KV) p.dW[k * static_cast<long>(p.D) + d] = sum;
+    else if (p.db) p.db[d] = sum;
+}
+
 // ANTI = false: the forward, out = bias + causal taps of in.
-// ANTI = true: dinput = anti-causal taps of dy (no bias).
+// ANTI = true: dinput = anti-causal taps of dy (no bias). With part set, the
+// first (KV + 1) * groups workgroups instead finish dkernel / dbias from the
+// slots of convnd_dw_lines (launched before on the stream), alongside.
 // Taps are summed per output in row-major kernel order, as the reference.
 // The causal window holds columns j-(K-1)..j (0 before column 0); the
 // anti-causal one columns j..j+K-1 (0 past the line end, where the offset
 // would land in the next line).
-template <int ND, int K, bool ANTI>
-__global__ void __launch_bounds__(64 * kConvWaves) convnd_lines(ConvArgs p) {
+template <int ND, int K, bool ANTI, int S>
+__global__ void __launch_bounds__(64 * kConvWaves) convnd_lines(ConvArgs p, const float *part, int nslot) {
     constexpr int R = kConvR;
     constexpr int KO = ipow(K, ND - 2);
     constexpr int RS = R + K - 1;
     constexpr int NR = KO * RS;
     constexpr int KV = ipow(K, ND);
     constexpr int CU = NR <= 6 ? 4 : (NR <= 12 ? 2 : 1);   // columns per load chunk
-    static_assert(kStrip % (2 * CU) == 0, "strip is whole chunk pairs");
+    constexpr int NCH = S / CU;                      // chunks per strip
+    static_assert(NCH >= 2 && NCH % 2 == 0, "strip is whole chunk pairs");
     using F = bio<f32_t>;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const long task = xcd_block(blockIdx.x, gridDim.x) * kConvWaves + wave;
+    long blk = blockIdx.x, nblk = gridDim.x;
+    if (ANTI && part) {
+        const long nfin = static_cast<long>(KV + 1) * p.groups;
+        if (blk < nfin) {
+            __shared__ float red[kConvWaves][64];
+            dw_finalize(p, part, nslot, static_cast<int>(blk % (KV + 1)), blk / (KV + 1), wave,
+                        threadIdx.x & 63, red);
+            return;
+        }
+        blk -= nfin;
+        nblk -= nfin;
+    }
+    const long task = xcd_block(blk, nblk) * kConvWaves + wave;
     if (task >= p.tasks_l) return;
-    const LineTask t = line_task<ND>(p, task);
+    const LineTask t = line_task<ND, S>(p, task % p.groups, task / p.groups);
     const int J = p.dims[ND - 1];
     const long bbase = t.batch * p.P;
     const auto rin = make_rsrc((ANTI ? p.dy : p.in) + bbase * p.D, p.P * p.D * 4);
@@ -512,39 +574,48 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_lines(ConvArgs p) {
     };
     load_chunk(0, n0);
 #pragma unroll 1
-    for (int ch = 0; ch < kStrip / CU; ch += 2) {
+    for (int ch = 0; ch < NCH - 2; ch += 2) {
         load_chunk(ch + 1, n1);
         run_chunk(ch, n0);
         load_chunk(ch + 2, n0);
         run_chunk(ch + 1, n1);
     }
+    load_chunk(NCH - 1, n1);
+    run_chunk(NCH - 2, n0);
+    run_chunk(NCH - 1, n1);
 }
 
 // dkernel / dbias over line groups: acc[k] += dy[line r, j] * in[causal tap
-// k of (r, j)], acc[KV] += dy, then the workgroup reduction and one atomic
-// per (tap, channel) per workgroup.
-template <int ND, int K>
-__global__ void __launch_bounds__(64 * kConvWaves) convnd_dw_lines(ConvArgs p) {
+// k of (r, j)], acc[KV] += dy. blockIdx.y is the channel group; workgroup x
+// of it takes the tasks quads [x * per, (x + 1) * per) of that group (wave w
+// the task 4q + w of quad q), sums its waves' partials in LDS and stores them
+// to its slot part[(y * gridDim.x + x) * (KV + 1) * 64 ...]: no atomics, and
+// dw_finalize adds the slots in a fixed order.
+template <int ND, int K, int S>
+__global__ void __launch_bounds__(64 * kConvWaves) convnd_dw_lines(ConvArgs p, float *part, long per) {
     constexpr int R = kConvR;
     constexpr int KO = ipow(K, ND - 2);
     constexpr int RS = R + K - 1;
     constexpr int NR = KO * RS;
     constexpr int KV = ipow(K, ND);
     constexpr int CU = NR + R <= 8 ? 4 : (NR + R <= 14 ? 2 : 1);
-    static_assert(kStrip % (2 * CU) == 0, "strip is whole chunk pairs");
+    constexpr int NCH = S / CU;                      // chunks per strip
+    static_assert(NCH >= 2 && NCH % 2 == 0, "strip is whole chunk pairs");
     using F = bio<f32_t>;
     __shared__ float red[kConvWaves][KV + 1][64];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const long blk = xcd_block(blockIdx.x, gridDim.x);
-    const long task = blk * kConvWaves + wave;
-    const bool live = task < p.tasks_l;
+    const long g = blockIdx.y;
+    const long T = p.tasks_l / p.groups;             // tasks per channel group
+    const long q0 = xcd_block(blockIdx.x, gridDim.x) * per;   // neighbours on one XCD
     float acc[KV + 1];
 #pragma unroll
     for (int k = 0; k <= KV; ++k) acc[k] = 0.f;
-    LineTask t{};
-    if (live) {
-        t = line_task<ND>(p, task);
+#pragma unroll 1
+    for (long q = q0; q < q0 + per; ++q) {
+        const long tl = q * kConvWaves + wave;
+        if (tl >= T) break;
+        const LineTask t = line_task<ND, S>(p, g, tl);
         const int J = p.dims[ND - 1];
         const long bbase = t.batch * p.P;
         const auto rin = make_rsrc(p.in + bbase * p.D, p.P * p.D * 4);
@@ -556,12 +627,12 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_dw_lines(ConvArgs p) {
         group_lines<ND>(p, t, og);        // dy of lanes past D and lines past the grid: 0
         float win[NR][K];
 #pragma unroll
-        for (int q = 0; q < NR; ++q) {
+        for (int qq = 0; qq < NR; ++qq) {
 #pragma unroll
             for (int c = 0; c < K - 1; ++c) {
                 const int j = j0 - (K - 1) + c;
-                const float v = F::ld(rin, conv_off(ro[q], j < 0 ? 0 : j, rb), 0);
-                win[q][c + 1] = j >= 0 ? v : 0.f;
+                const float v = F::ld(rin, conv_off(ro[qq], j < 0 ? 0 : j, rb), 0);
+                win[qq][c + 1] = j >= 0 ? v : 0.f;
             }
         }
         float x0[CU][NR], g0[CU][R], x1[CU][NR], g1[CU][R];
@@ -570,7 +641,7 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_dw_lines(ConvArgs p) {
             for (int u = 0; u < CU; ++u) {
                 const int j = j0 + ch * CU + u;
 #pragma unroll
-                for (int q = 0; q < NR; ++q) bx[u][q] = F::ld(rin, conv_off(ro[q], j, rb), 0);
+                for (int qq = 0; qq < NR; ++qq) bx[u][qq] = F::ld(rin, conv_off(ro[qq], j, rb), 0);
 #pragma unroll
                 for (int r = 0; r < R; ++r) bg[u][r] = F::ld(rdy, conv_off(og[r], j, rb), 0);
             }
@@ -580,14 +651,14 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_dw_lines(ConvArgs p) {
             for (int u = 0; u < CU; ++u) {
                 const int j = j0 + ch * CU + u;
 #pragma unroll
-                for (int q = 0; q < NR; ++q) {
+                for (int qq = 0; qq < NR; ++qq) {
 #pragma unroll
-                    for (int c = 0; c < K - 1; ++c) win[q][c] = win[q][c + 1];
-                    win[q][K - 1] = bx[u][q];
+                    for (int c = 0; c < K - 1; ++c) win[qq][c] = win[qq][c + 1];
+                    win[qq][K - 1] = bx[u][qq];
                 }
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const float g = j < J ? bg[u][r] : 0.f;
+                    const float gy = j < J ? bg[u][r] : 0.f;
 #pragma unroll
                     for (int ko = 0; ko < KO; ++ko)
 #pragma unroll
@@ -595,22 +666,34 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_dw_lines(ConvArgs p) {
 #pragma unroll
                             for (int kc = 0; kc < K; ++kc) {
                                 const int k = (ko * K + ka) * K + kc;
-                                acc[k] = fmaf(g, win[ko * RS + r + ka][kc], acc[k]);
+                                acc[k] = fmaf(gy, win[ko * RS + r + ka][kc], acc[k]);
                             }
-                    acc[KV] += g;
+                    acc[KV] += gy;
                 }
             }
         };
         load_chunk(0, x0, g0);
 #pragma unroll 1
-        for (int ch = 0; ch < kStrip / CU; ch += 2) {
+        for (int ch = 0; ch < NCH - 2; ch += 2) {
             load_chunk(ch + 1, x1, g1);
             run_chunk(ch, x0, g0);
             load_chunk(ch + 2, x0, g0);
             run_chunk(ch + 1, x1, g1);
         }
+        load_chunk(NCH - 1, x1, g1);
+        run_chunk(NCH - 2, x0, g0);
+        run_chunk(NCH - 1, x1, g1);
     }
-    conv_wg_reduce<KV>(p, red, acc, wave, lane, blk, p.tasks_l, live && t.dvalid, t.dc);
+#pragma unroll
+    for (int k = 0; k <= KV; ++k) red[wave][k][lane] = acc[k];
+    __syncthreads();
+    float *slot = part + (g * gridDim.x + blockIdx.x) * static_cast<long>(KV + 1) * 64;
+    for (int i = threadIdx.x; i < (KV + 1) * 64; i += 64 * kConvWaves) {
+        float sum = 0.f;
+#pragma unroll
+        for (int v = 0; v < kConvWaves; ++v) sum += red[v][i / 64][i % 64];
+        slot[i] = sum;
+    }
 }
 
 // Any ND <= 8 and K: one thread per (point, channel), taps from memory.
@@ -767,7 +850,14 @@ static bool conv_args(const ConvNDParams *p, long batch, bool bwd, ConvArgs &a, 
     if (a.nd >= 2) {
         a.louter = a.lines / a.dims[a.nd - 2];
         a.ngrp = (a.dims[a.nd - 2] + kConvR - 1) / kConvR;
-        a.tasks_l = batch * a.louter * a.ngrp * a.njb * a.groups;
+        // Longest strip that still gives two waves per SIMD (256 CUs).
+        const int J = a.dims[a.nd - 1];
+        for (a.strip_l = 64; a.strip_l > 16; a.strip_l /= 2) {
+            const long njb = (J + a.strip_l - 1) / a.strip_l;
+            if (batch * a.louter * a.ngrp * njb * a.groups >= 2048) break;
+        }
+        a.njb_l = (J + a.strip_l - 1) / a.strip_l;
+        a.tasks_l = batch * a.louter * a.ngrp * a.njb_l * a.groups;
     }
     return true;
 }
@@ -780,14 +870,22 @@ static bool strip_fits(const ConvArgs &a) {
 
 #define KM_CONV_SHAPES(X) X(1, 2) X(1, 3) X(1, 4) X(2, 2) X(2, 3) X(2, 4) X(3, 2) X(3, 3)
 
+// Shapes with line-group kernels (the KM_CONV_FWDL / KM_CONV_BWDL lists).
+static bool line_shape(const ConvArgs &a) {
+    return (a.nd == 2 && a.K >= 2 && a.K <= 4) || (a.nd == 3 && (a.K == 2 || a.K == 3));
+}
+
 static int conv_fwd_launch(const ConvArgs &a, hipStream_t s) {
     bool done = false;
     const long lblocks = (a.tasks_l + kConvWaves - 1) / kConvWaves;
-    if (a.nd >= 2 && lblocks > 0 && lblocks <= 0x7fffffffL && strip_fits(a)) {
+    if (line_shape(a) && lblocks > 0 && lblocks <= 0x7fffffffL && strip_fits(a)) {
 #define KM_CONV_FWDL(ND, KK)                                                                 \
         if (!done && a.nd == ND && a.K == KK) {                                              \
-            hipLaunchKernelGGL((convnd_lines<ND, KK, false>), dim3(lblocks), dim3(64 * kConvWaves), \
-                               0, s, a);                                                     \
+            const auto kern = a.strip_l == 64 ? convnd_lines<ND, KK, false, 64>                 \
+                              : a.strip_l == 32 ? convnd_lines<ND, KK, false, 32>               \
+                                                : convnd_lines<ND, KK, false, 16>;              \
+            hipLaunchKernelGGL(kern, dim3(lblocks), dim3(64 * kConvWaves), 0, s, a,          \
+                               static_cast<const float *>(nullptr), 0);                      \
             done = true;                                                                     \
         }
         KM_CONV_FWDL(2, 2) KM_CONV_FWDL(2, 3) KM_CONV_FWDL(2, 4) KM_CONV_FWDL(3, 2) KM_CONV_FWDL(3, 3)
@@ -813,22 +911,38 @@ static int conv_fwd_launch(const ConvArgs &a, hipStream_t s) {
 }
 
 static int conv_bwd_launch(const ConvArgs &a, hipStream_t s) {
-    if (zero_dev(a.dW, static_cast<long>(a.KV) * a.D, s) != 0) return -1;
-    if (zero_dev(a.db, a.D, s) != 0) return -1;
     bool done = false;
     const long lblocks = (a.tasks_l + kConvWaves - 1) / kConvWaves;
-    if (a.nd >= 2 && lblocks > 0 && lblocks <= 0x7fffffffL && strip_fits(a)) {
+    // dkernel slots: about two workgroups per CU over all channel groups.
+    const long quads = (a.tasks_l / std::max(a.groups, 1L) + kConvWaves - 1) / kConvWaves;
+    const long nslot = std::max(1L, std::min(quads, 512L / std::max(a.groups, 1L)));
+    const long per = (quads + nslot - 1) / std::max(nslot, 1L);
+    float *part = nullptr;
+    if (line_shape(a) && lblocks > 0 && lblocks + (a.KV + 1) * a.groups <= 0x7fffffffL && a.groups <= 65535 &&
+        strip_fits(a)) {
+        part = static_cast<float *>(
+            Workspace::reserve(sizeof(float) * a.groups * nslot * (a.KV + 1) * 64));
+        if (!part) return -1;
+    }
+    if (part) {
 #define KM_CONV_BWDL(ND, KK)                                                                 \
         if (!done && a.nd == ND && a.K == KK) {                                              \
-            hipLaunchKernelGGL((convnd_lines<ND, KK, true>), dim3(lblocks), dim3(64 * kConvWaves), \
-                               0, s, a);                                                     \
-            hipLaunchKernelGGL((convnd_dw_lines<ND, KK>), dim3(lblocks), dim3(64 * kConvWaves), \
-                               0, s, a);                                                     \
+            const auto kdin = a.strip_l == 64 ? convnd_lines<ND, KK, true, 64>                 \
+                              : a.strip_l == 32 ? convnd_lines<ND, KK, true, 32>               \
+                                                : convnd_lines<ND, KK, true, 16>;              \
+            const auto kdw = a.strip_l == 64 ? convnd_dw_lines<ND, KK, 64>                      \
+                             : a.strip_l == 32 ? convnd_dw_lines<ND, KK, 32>                    \
+                                               : convnd_dw_lines<ND, KK, 16>;                   \
+            hipLaunchKernelGGL(kdw, dim3(nslot, a.groups), dim3(64 * kConvWaves), 0, s, a, part, per); \
+            hipLaunchKernelGGL(kdin, dim3(lblocks + (a.KV + 1) * a.groups), dim3(64 * kConvWaves), 0, \
+                               s, a, static_cast<const float *>(part), static_cast<int>(nslot)); \
             done = true;                                                                     \
         }
         KM_CONV_BWDL(2, 2) KM_CONV_BWDL(2, 3) KM_CONV_BWDL(2, 4) KM_CONV_BWDL(3, 2) KM_CONV_BWDL(3, 3)
 #undef KM_CONV_BWDL
     }
+    if (!done && (zero_dev(a.dW, static_cast<long>(a.KV) * a.D, s) != 0 || zero_dev(a.db, a.D, s) != 0))
+        return -1;
     const long blocks = (a.tasks + kConvWaves - 1) / kConvWaves;
     if (!done && blocks <= 0x7fffffffL && strip_fits(a)) {
 #define KM_CONV_BWD(ND, KK)                                                                  \

@@ -130,6 +130,35 @@ def test_batched_equals_per_grid():
     assert_close(db.cpu().numpy(), sb, TOL_F32, "dbias (sum over batch)", kb)
 
 
+def test_backward_many_tasks_deterministic():
+    # 2 x (2048, 48) grids, D = 100 (two channel groups): 32-point strips, and
+    # each dkernel workgroup sums two quads of line tasks into its slot. The
+    # slots are added in a fixed order, so two runs agree bit for bit.
+    dims, D, Kk, nb = (2048, 48), 100, 3, 2
+    parts = [conv_inputs(dims, D, Kk, seed=20 + i) for i in range(nb)]
+    ker = parts[0][1]
+    inp = np.stack([p[0] for p in parts])
+    dy = np.stack([p[3] for p in parts])
+    runs = []
+    for _ in range(2):
+        din = torch.full(inp.shape, float("nan"), device=DEV)
+        dker = torch.full(ker.shape, float("nan"), device=DEV)
+        db = torch.full((D,), float("nan"), device=DEV)
+        K.convnd_bwd(dims, T(inp), T(ker), T(dy), din, dker, db, batch=nb)
+        torch.cuda.synchronize()
+        runs.append((din.cpu().numpy(), dker.cpu().numpy(), db.cpu().numpy()))
+    for a, b in zip(runs[0], runs[1]):
+        assert np.array_equal(a, b)
+    sk, sb, kk, kb = 0, 0, 0, 0
+    for i in range(nb):
+        rdi, rdk, rdb = O.convnd_backward(dims, inp[i], ker, dy[i])
+        kdi, kdk, kdb = bwd_kappa(dims, inp[i], ker, dy[i], True)
+        assert_close(runs[0][0][i], rdi, TOL_F32, f"dinput[{i}]", kdi)
+        sk, sb, kk, kb = sk + rdk, sb + rdb, kk + kdk, kb + kdb
+    assert_close(runs[0][1], sk, TOL_F32, "dkernel (sum over batch)", kk)
+    assert_close(runs[0][2], sb, TOL_F32, "dbias (sum over batch)", kb)
+
+
 def test_reference_entry_points_host_and_device():
     dims, D, Kk = (9, 10), 20, 3
     inp, ker, b, dy = conv_inputs(dims, D, Kk, seed=3)
