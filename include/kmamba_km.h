@@ -137,8 +137,11 @@ int km_scan1d_bwd(const KMScan1DBwd *a, void *stream);
  * include/convnd.h:10-51, cuda/convnd.cu:258-436), with input, output, dy and
  * dinput holding [batch, prod(dims), D]; kernel and bias are shared by the
  * batch, and dkernel / dbias sum over it. Backward overwrites dinput,
- * dkernel and dbias (dbias may be NULL). dkernel and dbias are sums formed
- * with fp32 atomics: their last bits may vary between runs.
+ * dkernel and dbias (dbias may be NULL). For 2D (K <= 4) and 3D (K <= 3)
+ * grids dkernel and dbias are summed in a fixed order through the library's
+ * per-device workspace (identical run to run; backward calls that overlap
+ * on one device then race); other shapes sum them with fp32 atomics, whose
+ * last bits may vary between runs.
  * Returns 0, or -1 with km_last_error() set. */
 int km_convnd_fwd(const ConvNDParams *p, long batch, void *stream);
 int km_convnd_bwd(const ConvNDParams *p, long batch, void *stream);
