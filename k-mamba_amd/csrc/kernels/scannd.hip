@@ -175,8 +175,13 @@ struct NDRow {
     int base;                   // row offset from the tile origin, in points
 };
 
-template <int ND, int TW, int MM>
+// PL > 0 (3D, tiles of PL rows along axis 1): the wave also keeps the
+// previous plane's PL rows in registers, so only the tile's first plane reads
+// its axis-0 neighbours from h.
+template <int ND, int TW, int MM, int PL>
 __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
+    constexpr bool RING = (ND == 3 && PL > 0);
+    static_assert(PL % 2 == 0, "planes of whole row pairs");
     const int lane = threadIdx.x;
     // Workgroups are dealt to the 8 XCDs round-robin; renumber them so that
     // consecutive channel groups of a tile, which share x / delta cache
@@ -276,7 +281,7 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
         for (int a = 0; a < (ND == 2 ? 0 : ND - 1); ++a) {
             // Wave-uniform (readfirstlane), so the resource choice is scalar.
             const bool need = __builtin_amdgcn_readfirstlane(
-                                  (a < ar) ? (r.gi[a] > 0) : (r.gi[a] > 0 && r.gi[a] == lo[a])) != 0;
+                                  (a < ar && !(RING && a == 0)) ? (r.gi[a] > 0) : (r.gi[a] > 0 && r.gi[a] == lo[a])) != 0;
             const auto rn = need ? rh : rB;
             const int sn = need ? sh - static_cast<int>(p.pstride[a]) * DM * 4 : sb;
 #pragma unroll
@@ -320,7 +325,9 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
         yoff = static_cast<int>((lane % YG == 0 && yc < TC) ? static_cast<unsigned>((yc * D + d) * 4) : kDrop);
     }
 
-    auto compute_row = [&](const NDRow<ND, TW> &r, bool live) {
+    // ring0 / from_ring: the axis-0 neighbour row kept in registers (PL > 0,
+    // rows past the tile's first plane) instead of r.hn[0].
+    auto compute_row = [&](const NDRow<ND, TW> &r, bool live, const float (&ring0)[TW], bool from_ring) {
         const bool first_row_of_plane = (r.gi[ar] == lo[ar]);
         const int sh = (r.base + static_cast<int>(hback)) * DM * 4;
         const int sx = r.base * D * 4;
@@ -333,8 +340,10 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
             for (int a = 0; a < ND; ++a) dsum += r.dt[a][c];
             float acc = (dsum * inv_nd) * (r.b[c] * r.x[c]);
 #pragma unroll
-            for (int a = 0; a < ar; ++a)
-                if (r.gi[a] > 0) acc = fmaf(exp2_fast(r.dt[a][c] * Ap[a]), r.hn[a][c], acc);
+            for (int a = 0; a < ar; ++a) {
+                const float hn = (RING && a == 0 && from_ring) ? ring0[c] : r.hn[a][c];
+                if (r.gi[a] > 0) acc = fmaf(exp2_fast(r.dt[a][c] * Ap[a]), hn, acc);
+            }
             if (r.gi[ar] > 0) {
                 float hu = top[c];
                 if constexpr (ND > 2) hu = first_row_of_plane ? r.hn[ar][c] : top[c];
@@ -362,6 +371,9 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
     // covers only older loads. 2D tiles hold one wave per SIMD in a band, so
     // their rows are prefetched two ahead through a ring of four; deeper
     // tiles have more waves per SIMD and prefetch one ahead.
+    float none[TW];
+#pragma unroll
+    for (int c = 0; c < TW; ++c) none[c] = 0.f;
     if constexpr (ND == 2) {
         NDRow<ND, TW> R0, R1, R2, R3;
         load_row(0, R0);
@@ -369,16 +381,45 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
         for (int row = 0; row < nrows; row += 4) {
             load_row(min(row + 2, nrows - 1), R2);
             __builtin_amdgcn_sched_barrier(0);
-            compute_row(R0, true);
+            compute_row(R0, true, none, false);
             load_row(min(row + 3, nrows - 1), R3);
             __builtin_amdgcn_sched_barrier(0);
-            compute_row(R1, row + 1 < nrows);
+            compute_row(R1, row + 1 < nrows, none, false);
             load_row(min(row + 4, nrows - 1), R0);
             __builtin_amdgcn_sched_barrier(0);
-            compute_row(R2, row + 2 < nrows);
+            compute_row(R2, row + 2 < nrows, none, false);
             load_row(min(row + 5, nrows - 1), R1);
             __builtin_amdgcn_sched_barrier(0);
-            compute_row(R3, row + 3 < nrows);
+            compute_row(R3, row + 3 < nrows, none, false);
+        }
+    } else if constexpr (RING) {
+        // Planes of PL rows (i1 = 0..PL-1; rows past ext[1] are recomputed
+        // on the last row's operands with their stores dropped), row pairs
+        // prefetched one row ahead. ring[i1] holds h of row (i0 - 1, i1).
+        const int e0 = ext[0], e1 = ext[1];
+        auto row_at = [&](int i0, int i1) { return min(i0, e0 - 1) * e1 + min(i1, e1 - 1); };
+        float ring[PL][TW];
+#pragma unroll
+        for (int i = 0; i < PL; ++i)
+#pragma unroll
+            for (int c = 0; c < TW; ++c) ring[i][c] = 0.f;
+        NDRow<ND, TW> R0, R1;
+        load_row(0, R0);
+        for (int i0 = 0; i0 < e0; ++i0) {
+            const bool inner = i0 > 0;
+#pragma unroll
+            for (int i1 = 0; i1 < PL; i1 += 2) {
+                load_row(row_at(i0, i1 + 1), R1);
+                __builtin_amdgcn_sched_barrier(0);
+                compute_row(R0, i1 < e1, ring[i1], inner);
+#pragma unroll
+                for (int c = 0; c < TW; ++c) ring[i1][c] = top[c];
+                load_row(i1 + 2 < PL ? row_at(i0, i1 + 2) : row_at(i0 + 1, 0), R0);
+                __builtin_amdgcn_sched_barrier(0);
+                compute_row(R1, i1 + 1 < e1, ring[i1 + 1], inner);
+#pragma unroll
+                for (int c = 0; c < TW; ++c) ring[i1 + 1][c] = top[c];
+            }
         }
     } else {
         NDRow<ND, TW> R0, R1;
@@ -386,10 +427,10 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
         for (int row = 0; row < nrows; row += 2) {
             load_row(min(row + 1, nrows - 1), R1);
             __builtin_amdgcn_sched_barrier(0);
-            compute_row(R0, true);
+            compute_row(R0, true, none, false);
             load_row(min(row + 2, nrows - 1), R0);
             __builtin_amdgcn_sched_barrier(0);
-            compute_row(R1, row + 1 < nrows);
+            compute_row(R1, row + 1 < nrows, none, false);
         }
     }
 }
@@ -454,6 +495,17 @@ static void scannd_tile_shape(int nd, int &tw, int &tl) {
     if (nd == 3 && (t3w == 4 || t3w == 8) && t3l > 0 && t3l <= 64) { tw = t3w; tl = t3l; }
 }
 
+template <int ND, int TW, int MM>
+static void launch_tile(dim3 g, const ScanNDArgs &a, bool ring, hipStream_t s) {
+    if constexpr (ND == 3) {
+        if (ring) {
+            hipLaunchKernelGGL((scannd_tile_kernel<ND, TW, MM, 4>), g, dim3(64), 0, s, a);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((scannd_tile_kernel<ND, TW, MM, 0>), g, dim3(64), 0, s, a);
+}
+
 static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s) {
     bool fast = (a.DM % 64 == 0) && (64 % a.M == 0) && a.nd >= 2 && a.nd <= 4;
     // Tiles: rows of TWc points along the last axis, Tlead along each
@@ -504,12 +556,14 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s) {
             reach += a.ntile[ax] - 1;
             for (int sidx = 0; sidx <= reach; ++sidx) cnt[sidx] = nxt[sidx];
         }
+        // 3D tiles of 4 rows along axis 1 keep the previous plane in registers.
+        const bool ring = a.nd == 3 && a.tile[1] == 4;
         for (int b = 0; b < nbands; ++b) {
             a.band = b;
             const long grid = cnt[b] * a.ncg;
             if (grid <= 0) continue;
-            const dim3 g(static_cast<unsigned>(grid)), blk(64);
-#define KM_ND_LAUNCH(NDv, TWv, MMv) hipLaunchKernelGGL((scannd_tile_kernel<NDv, TWv, MMv>), g, blk, 0, s, a)
+            const dim3 g(static_cast<unsigned>(grid));
+#define KM_ND_LAUNCH(NDv, TWv, MMv) launch_tile<NDv, TWv, MMv>(g, a, ring, s)
 #define KM_ND_BY_M(NDv, TWv)                                  \
             switch (a.M) {                                    \
             case 1: KM_ND_LAUNCH(NDv, TWv, 1); break;         \

@@ -97,7 +97,10 @@ CASES = [((7, 5), 3, 4), ((40, 70), 4, 16), ((33, 65), 8, 16), ((1, 90), 4, 16),
          # ragged tiles with a single row per plane and length-1 row axes
          # (the default 3D / 4D tiles are 4 per leading axis, 2D rows 6):
          ((7, 5, 10), 4, 16), ((5, 1, 9), 4, 16), ((10, 9, 13), 4, 16), ((5, 5, 5, 9), 4, 16),
-         ((3, 1, 4, 5), 4, 16), ((13, 25), 4, 16), ((2, 1, 1, 6), 4, 16)]
+         ((3, 1, 4, 5), 4, 16), ((13, 25), 4, 16), ((2, 1, 1, 6), 4, 16),
+         # 3D tiles of 4 rows along axis 1 (previous plane kept in registers),
+         # ragged along every axis:
+         ((9, 6, 11), 4, 16), ((6, 4, 17), 8, 8)]
 
 
 @pytest.mark.parametrize("dims,D,M", CASES)
