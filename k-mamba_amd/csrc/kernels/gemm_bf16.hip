@@ -37,16 +37,12 @@ struct GemmArgs {
 
 constexpr int kBM = 128, kBN = 128, kBK = 64;
 
-__device__ __forceinline__ float softplus_ref(float v) {
-    // log(1 + e^v) (reference include/kmamba_kernels.h:47-49, which has no
-    // overflow guard: v > 88 gives inf there, v here).
-    return v > 20.f ? v : __logf(1.f + __expf(v));
-}
-
 template <int EPI>
 __device__ __forceinline__ float epilogue(float v) {
-    if constexpr (EPI == KM_EPI_SOFTPLUS) return softplus_ref(v);
-    else if constexpr (EPI == KM_EPI_SILU) return v / (1.f + __expf(-v));
+    // softplus: log(1 + e^v) as in reference include/kmamba_kernels.h:47-49
+    // (which has no overflow guard: v > 88 gives inf there, v here).
+    if constexpr (EPI == KM_EPI_SOFTPLUS) return softplus_fast(v);
+    else if constexpr (EPI == KM_EPI_SILU) return silu_fast(v);
     else return v;
 }
 
@@ -316,6 +312,103 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_mfma_256(GemmArgs p) {
     store_wave_tile<EPI, CBF16, 4, 4>(p, acc, m0 + wm * 128, n0 + wn * 128, lds, lane);
 }
 
+
+// Skinny shapes (N <= 128 with a long K, or K <= 64): MFMA operands come
+// from global memory straight into registers, with no LDS staging and no
+// barrier in the K loop. K runs in blocks of 16*CPB: lane l < 32 holds row
+// l's first half of the block and lane l + 32 its second half, CPB
+// contiguous 16-byte chunks each, and MFMA step s of a block takes chunk s
+// of both halves: the order of the terms of a dot product is free, and A
+// and B use the same one. A wave computes a 32 x 32*TN block of C.
+// KSPLIT = 1 (K <= 64, one block of 64): the 4 waves of a workgroup take 4
+// consecutive row blocks (workgroup tile 128 x 32*TN). KSPLIT = 4 (blocks of
+// 32, two in flight per wave): the waves take the same row block and the k
+// blocks w, w + 4, ..., and wave 0 adds the other waves' partial sums from
+// LDS in wave order. Chunks past K load as zero (out-of-range offset).
+template <int EPI, bool CBF16, int TN, int KSPLIT>
+__global__ void __launch_bounds__(256) gemm_bf16_direct(GemmArgs p) {
+    constexpr int ES = CBF16 ? 2 : 4;
+    constexpr int CPB = KSPLIT > 1 ? 2 : 4;            // 16-byte chunks per lane per block
+    constexpr int KB = 16 * CPB;                       // k per block
+    constexpr int SW = KSPLIT > 1 ? 1 : 4;             // waves that store
+    __shared__ float red[KSPLIT > 1 ? KSPLIT - 1 : 1][KSPLIT > 1 ? TN * 16 : 1][64];
+    __shared__ __attribute__((aligned(16))) char stage[SW][32 * TN * 32 * ES];
+    constexpr unsigned kDrop = 0x80000000u;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int fr = lane & 31, fh = lane >> 5;
+    const long m0 = static_cast<long>(blockIdx.y) * (KSPLIT > 1 ? 32 : 128) + (KSPLIT > 1 ? 0 : w * 32);
+    const long n0 = static_cast<long>(blockIdx.x) * (32 * TN);
+    const long arows = std::min<long>(32, p.M - m0), brows = std::min<long>(32 * TN, p.N - n0);
+    const auto rA = make_rsrc(p.A + (arows > 0 ? m0 : 0) * p.lda,
+                              arows > 0 ? (arows - 1) * p.lda * 2 + p.K * 2 : 0);
+    const auto rB = make_rsrc(p.B + n0 * p.ldb, brows > 0 ? (brows - 1) * p.ldb * 2 + p.K * 2 : 0);
+    const int aoff = fr * static_cast<int>(p.lda) * 2;
+    int boff[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) boff[j] = (j * 32 + fr) * static_cast<int>(p.ldb) * 2;
+
+    auto ld = [&](__amdgpu_buffer_rsrc_t r, int rowoff, long kb, int c) {
+        const long k = kb * KB + (KB / 2) * fh + 8 * c;
+        const int off = static_cast<int>(k < p.K ? static_cast<unsigned>(rowoff + k * 2) : kDrop);
+        return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    };
+    auto load_blk = [&](long kb, bf16x8 (&a)[CPB], bf16x8 (&b)[TN][CPB]) {
+#pragma unroll
+        for (int c = 0; c < CPB; ++c) a[c] = ld(rA, aoff, kb, c);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int c = 0; c < CPB; ++c) b[j][c] = ld(rB, boff[j], kb, c);
+    };
+    f32x16 acc[1][TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[0][j][r] = 0.f;
+    auto mfma_blk = [&](const bf16x8 (&a)[CPB], const bf16x8 (&b)[TN][CPB]) {
+#pragma unroll
+        for (int c = 0; c < CPB; ++c)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c], b[j][c], acc[0][j], 0, 0, 0);
+    };
+    bf16x8 a0[CPB], b0[TN][CPB];
+    if constexpr (KSPLIT == 1) {
+        load_blk(0, a0, b0);
+        mfma_blk(a0, b0);
+    } else {
+        bf16x8 a1[CPB], b1[TN][CPB];
+        const long nkb = (p.K + KB - 1) / KB;
+        long kb = w;
+        load_blk(kb, a0, b0);
+        for (; kb < nkb; kb += 2 * KSPLIT) {
+            load_blk(kb + KSPLIT, a1, b1);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_blk(a0, b0);
+            load_blk(kb + 2 * KSPLIT, a0, b0);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_blk(a1, b1);
+        }
+        if (w > 0) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) red[w - 1][j * 16 + r][lane] = acc[0][j][r];
+        }
+        __syncthreads();
+        if (w != 0) return;
+#pragma unroll 1
+        for (int v = 0; v < KSPLIT - 1; ++v)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[0][j][r] += red[v][j * 16 + r][lane];
+    }
+    store_wave_tile<EPI, CBF16, 1, TN>(p, acc, m0, n0, stage[KSPLIT > 1 ? 0 : w], lane);
+}
+
 template <int EPI>
 static void gemm_go(const GemmArgs &a, dim3 g, bool big, hipStream_t s) {
     if (big) {
@@ -325,6 +418,63 @@ static void gemm_go(const GemmArgs &a, dim3 g, bool big, hipStream_t s) {
         if (a.c_bf16) hipLaunchKernelGGL((gemm_bf16_mfma<EPI, true>), g, dim3(256), 0, s, a);
         else          hipLaunchKernelGGL((gemm_bf16_mfma<EPI, false>), g, dim3(256), 0, s, a);
     }
+}
+
+template <int EPI, int TN, int KSPLIT>
+static void direct_go(const GemmArgs &a, dim3 g, hipStream_t s) {
+    if (a.c_bf16) hipLaunchKernelGGL((gemm_bf16_direct<EPI, true, TN, KSPLIT>), g, dim3(256), 0, s, a);
+    else          hipLaunchKernelGGL((gemm_bf16_direct<EPI, false, TN, KSPLIT>), g, dim3(256), 0, s, a);
+}
+
+template <int EPI>
+static void direct_by_shape(const GemmArgs &a, dim3 g, int tn, int ksplit, hipStream_t s) {
+    if (ksplit == 1) { direct_go<EPI, 4, 1>(a, g, s); return; }
+    switch (tn) {
+    case 1: direct_go<EPI, 1, 4>(a, g, s); break;
+    case 2: direct_go<EPI, 2, 4>(a, g, s); break;
+    case 3: direct_go<EPI, 3, 4>(a, g, s); break;
+    default: direct_go<EPI, 4, 4>(a, g, s); break;
+    }
+}
+
+// Skinny shapes on gemm_bf16_direct: N <= 128 with K >= 512 (the 4 waves of
+// a workgroup split K), or K <= 64 (one k block). Returns 1 when launched,
+// 0 when the shape is not one of these, -1 on a launch error.
+static int direct_launch(const KMGemm *g, hipStream_t s) {
+    const bool narrow = g->N <= 128 && g->K >= 512;
+    const bool shallow = g->K <= 64;
+    if (!narrow && !shallow) return 0;
+    const int ksplit = narrow ? 4 : 1;
+    const int tn = narrow ? static_cast<int>((g->N + 31) / 32) : 4;
+    const long TM = ksplit > 1 ? 32 : 128, TN = 32L * tn;
+    if (g->ldb * 2 * (TN + 1) > 0x7fffffffL || g->lda * 2 * (TM + 1) > 0x7fffffffL) return 0;
+    const long nbn = (g->N + TN - 1) / TN, nbm = (g->M + TM - 1) / TM;
+    if (nbn > 0x7fffffffL) return 0;
+    const long chunk = 65535;
+    for (long mb = 0; mb < nbm; mb += chunk) {
+        const long nb = std::min(chunk, nbm - mb);
+        GemmArgs a{};
+        a.A = static_cast<const uint16_t *>(g->A) + mb * TM * g->lda;
+        a.B = static_cast<const uint16_t *>(g->B);
+        a.c_bf16 = (g->c_dtype == KM_BF16);
+        a.C = static_cast<char *>(g->C) + mb * TM * g->ldc * (a.c_bf16 ? 2 : 4);
+        a.bias = g->bias;
+        a.M = std::min(g->M - mb * TM, nb * TM);
+        a.N = g->N; a.K = g->K; a.lda = g->lda; a.ldb = g->ldb; a.ldc = g->ldc;
+        a.epi = g->epilogue;
+        const dim3 grid(static_cast<unsigned>(nbn), static_cast<unsigned>(nb));
+        switch (g->epilogue) {
+        case KM_EPI_SOFTPLUS: direct_by_shape<KM_EPI_SOFTPLUS>(a, grid, tn, ksplit, s); break;
+        case KM_EPI_SILU:     direct_by_shape<KM_EPI_SILU>(a, grid, tn, ksplit, s); break;
+        default:              direct_by_shape<KM_EPI_NONE>(a, grid, tn, ksplit, s); break;
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) {
+            set_error("km_gemm_bf16: launch failed: %s", hipGetErrorString(e));
+            return -1;
+        }
+    }
+    return 1;
 }
 
 int gemm_bf16_launch(const KMGemm *g, hipStream_t s) {
@@ -345,6 +495,7 @@ int gemm_bf16_launch(const KMGemm *g, hipStream_t s) {
     }
     if (g->M == 0 || g->N == 0) return 0;
     if (!gpu_ready()) return -1;
+    if (const int d = direct_launch(g, s)) return d > 0 ? 0 : -1;
     // 256 x 256 tiles when both output dimensions fill them (and K spans
     // at least a few stages); 128 x 128 otherwise.
     const bool big = g->M >= kGM && g->N >= kGN && g->K >= 4 * kGK &&

@@ -66,6 +66,21 @@ __device__ __forceinline__ float sum_xor16(float v) {
 // 2^x on the transcendental unit (v_exp_f32, ~1 ulp).
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// SiLU v * sigmoid(v) = v / (1 + e^-v) on the hardware exp2 and reciprocal
+// (about 1 ulp each) instead of the library exp and the IEEE division
+// sequence; e^-v = inf gives rcp = 0, the limit.
+__device__ __forceinline__ float silu_fast(float v) {
+    return v * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-v * kLog2e));
+}
+
+// softplus log(1 + e^v) on the hardware exp2 / log2 (5 instructions instead
+// of the library exp and log with their range reduction); v > 20 returns v,
+// where log(1 + e^v) rounds to v in fp32 anyway.
+constexpr float kLn2 = 0.6931471805599453f;
+__device__ __forceinline__ float softplus_fast(float v) {
+    return v > 20.f ? v : kLn2 * __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(v * kLog2e));
+}
+
 // Raw buffer resource over [base, base + bytes): loads past the end return 0
 // and stores past the end are dropped by the hardware range check. Word 3 is
 // the gfx9 raw-buffer format (no swizzle, 32-bit data).

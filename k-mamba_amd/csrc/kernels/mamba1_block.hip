@@ -28,6 +28,9 @@ constexpr int kConvStrip = 64;
 // u[b,t,d] = SiLU(bias[d] + sum_k x[b, t-(KC-1-k), d] * w[k, d]), taps before
 // t = 0 skipped (the causal convnd in 1D). One thread per channel pair and
 // strip of kConvStrip steps; 64 lanes read 256 contiguous bytes per step.
+// The strip's inputs are all loaded before the arithmetic (one memory
+// latency per strip); rows past L read 0 and their stores are dropped by the
+// buffer range check.
 template <int KC>
 __global__ void __launch_bounds__(256) conv1d_silu_bf16(const uint32_t *x, const float *w,
                                                         const float *bias, uint32_t *u, long L,
@@ -37,10 +40,14 @@ __global__ void __launch_bounds__(256) conv1d_silu_bf16(const uint32_t *x, const
     const long D2 = D / 2;
     if (c >= D2) return;
     const long b = blockIdx.z;
-    const long t0 = static_cast<long>(blockIdx.y) * kConvStrip;
-    const long t1 = std::min<long>(t0 + kConvStrip, L);
-    const uint32_t *xb = x + b * L * D2 + c;
-    uint32_t *ub = u + b * L * D2 + c;
+    const int t0 = static_cast<int>(blockIdx.y) * kConvStrip;
+    const auto rx = make_rsrc(x + b * L * D2, L * D2 * 4);
+    const auto ru = make_rsrc(u + b * L * D2, L * D2 * 4);
+    const int row = static_cast<int>(D2) * 4, lane_off = static_cast<int>(c) * 4;
+    uint32_t xv[kConvStrip];
+#pragma unroll
+    for (int i = 0; i < kConvStrip; ++i)
+        xv[i] = __builtin_amdgcn_raw_buffer_load_b32(rx, lane_off + (t0 + i) * row, 0, 0);
     float w0[8], w1[8];
     for (int k = 0; k < K; ++k) {
         w0[k] = w[k * D + 2 * c];
@@ -49,27 +56,29 @@ __global__ void __launch_bounds__(256) conv1d_silu_bf16(const uint32_t *x, const
     const float b0 = bias ? bias[2 * c] : 0.f, b1 = bias ? bias[2 * c + 1] : 0.f;
     float h0[8], h1[8];                      // inputs at t-(K-1) .. t
     for (int k = 0; k < K - 1; ++k) {
-        const long t = t0 - (K - 1) + k;
-        const uint32_t v = t >= 0 ? xb[t * D2] : 0u;
+        const int t = t0 - (K - 1) + k;
+        const uint32_t v = t >= 0 ? __builtin_amdgcn_raw_buffer_load_b32(rx, lane_off + t * row, 0, 0) : 0u;
         h0[k + 1] = bf16_to_f32(static_cast<uint16_t>(v & 0xffff));
         h1[k + 1] = bf16_to_f32(static_cast<uint16_t>(v >> 16));
     }
-    for (long t = t0; t < t1; ++t) {
+#pragma unroll
+    for (int i = 0; i < kConvStrip; ++i) {
         for (int k = 0; k < K - 1; ++k) {
             h0[k] = h0[k + 1];
             h1[k] = h1[k + 1];
         }
-        const uint32_t v = xb[t * D2];
-        h0[K - 1] = bf16_to_f32(static_cast<uint16_t>(v & 0xffff));
-        h1[K - 1] = bf16_to_f32(static_cast<uint16_t>(v >> 16));
+        h0[K - 1] = bf16_to_f32(static_cast<uint16_t>(xv[i] & 0xffff));
+        h1[K - 1] = bf16_to_f32(static_cast<uint16_t>(xv[i] >> 16));
         float s0 = b0, s1 = b1;
         for (int k = 0; k < K; ++k) {
             s0 += h0[k] * w0[k];
             s1 += h1[k] * w1[k];
         }
-        s0 = s0 / (1.f + __expf(-s0));
-        s1 = s1 / (1.f + __expf(-s1));
-        ub[t * D2] = static_cast<uint32_t>(f32_to_bf16(s0)) | (static_cast<uint32_t>(f32_to_bf16(s1)) << 16);
+        s0 = silu_fast(s0);
+        s1 = silu_fast(s1);
+        __builtin_amdgcn_raw_buffer_store_b32(
+            static_cast<uint32_t>(f32_to_bf16(s0)) | (static_cast<uint32_t>(f32_to_bf16(s1)) << 16), ru,
+            lane_off + (t0 + i) * row, 0, 0);
     }
 }
 
@@ -147,7 +156,9 @@ int mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long B,
     {
         dim3 grid(static_cast<unsigned>((di / 2 + 255) / 256),
                   static_cast<unsigned>((L + kConvStrip - 1) / kConvStrip), static_cast<unsigned>(B));
-        if (grid.y > 65535 || grid.z > 65535) {
+        // The conv kernel addresses one sequence (plus a strip past its end)
+        // with 32-bit byte offsets.
+        if (grid.y > 65535 || grid.z > 65535 || (L + kConvStrip) * di * 2 > 0x7fffffffL) {
             set_error("km_mamba1_block_fwd: sequence or batch too large");
             return -1;
         }

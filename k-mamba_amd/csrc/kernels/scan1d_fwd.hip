@@ -61,7 +61,7 @@ template <typename T>
 __device__ __forceinline__ float gated(const Scan1DFwdArgs &p, float y, float xv, float dsk,
                                        float zv) {
     if (p.Dskip) y = fmaf(dsk, xv, y);
-    if (p.z) y *= zv / (1.f + __expf(-zv));
+    if (p.z) y *= silu_fast(zv);
     return y;
 }
 

@@ -38,7 +38,11 @@ def f32(a):
 
 
 @pytest.mark.parametrize("M,N,Kd", [(128, 128, 64), (1, 1, 8), (130, 97, 72), (257, 300, 1024),
-                                    (1000, 96, 2048), (64, 2048, 64), (300, 33, 136)])
+                                    (1000, 96, 2048), (64, 2048, 64), (300, 33, 136),
+                                    # direct-operand kernel: N <= 128 with K >= 512 (k split
+                                    # over 4 waves, ragged M and K), and K <= 64
+                                    (517, 128, 512), (33, 64, 1000), (77, 20, 4104), (1, 128, 512),
+                                    (200, 300, 24), (259, 129, 40)])
 @pytest.mark.parametrize("out_bf16", [False, True])
 def test_gemm_vs_float64(M, N, Kd, out_bf16):
     g = rng_for("gemm", M, N, Kd)
@@ -76,6 +80,32 @@ def test_gemm_strided_bias_epilogues(epi):
         fn = softplus_ref if epi == K.KM_EPI_SOFTPLUS else silu_ref
         ref = fn(pre.astype(np.float32))
         # the activation's own rounding dominates: compare with a 1e-5 floor
+        err = np.abs(got[:, :N] - ref) / np.maximum(np.abs(ref), 1e-2 * np.abs(ref).max())
+        assert err.max() < 1e-4, err.max()
+
+
+@pytest.mark.parametrize("epi", [K.KM_EPI_NONE, K.KM_EPI_SOFTPLUS, K.KM_EPI_SILU])
+def test_gemm_narrow_strided_bias_epilogues(epi):
+    # N <= 128 with a long K (the x_proj shape class): A a column slice of a
+    # wider buffer, C inside a wider one.
+    M, N, Kd, lda, ldc = 300, 100, 1032, 1104, 128
+    g = rng_for("gemm-narrow", epi)
+    Abuf = bf16_round(g.standard_normal((M, lda)).astype(np.float32))
+    B = bf16_round((g.standard_normal((N, Kd)) / 32).astype(np.float32))
+    bias = g.standard_normal(N).astype(np.float32)
+    Cbuf = torch.full((M, ldc), 7.0, device=DEV)
+    K.gemm_bf16(bf(Abuf), bf(B), Cbuf, bias=f32(bias), epilogue=epi, M=M, N=N, K=Kd, lda=lda,
+                ldc=ldc)
+    torch.cuda.synchronize()
+    got = Cbuf.cpu().numpy()
+    assert (got[:, N:] == 7.0).all(), "wrote past N"
+    pre = Abuf[:, :Kd].astype(np.float64) @ B.astype(np.float64).T + bias
+    kap = np.abs(Abuf[:, :Kd]).astype(np.float64) @ np.abs(B).astype(np.float64).T + np.abs(bias)
+    if epi == K.KM_EPI_NONE:
+        assert_close(got[:, :N], pre, TOL_F32, "C", kap)
+    else:
+        fn = softplus_ref if epi == K.KM_EPI_SOFTPLUS else silu_ref
+        ref = fn(pre.astype(np.float32))
         err = np.abs(got[:, :N] - ref) / np.maximum(np.abs(ref), 1e-2 * np.abs(ref).max())
         assert err.max() < 1e-4, err.max()
 
