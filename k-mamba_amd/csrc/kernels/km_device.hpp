@@ -20,12 +20,18 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t v) {
     return __uint_as_float(static_cast<uint32_t>(v) << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16; NaN stays NaN (quiet bit forced).
+// Round-to-nearest-even fp32 -> bf16 on the gfx950 converter
+// (v_cvt_pk_bf16_f32): the same bits as (u + 0x7fff + ((u >> 16) & 1)) >> 16
+// for every non-NaN input, NaN kept NaN with its quiet bit set.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+// Two values in one instruction: a in the low half, b in the high half.
+typedef __bf16 km_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float km_f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((km_f32x2{a, b}), km_bf16x2));
 }
 
 template <typename T> struct io;

@@ -76,9 +76,7 @@ __global__ void __launch_bounds__(256) conv1d_silu_bf16(const uint32_t *x, const
         }
         s0 = silu_fast(s0);
         s1 = silu_fast(s1);
-        __builtin_amdgcn_raw_buffer_store_b32(
-            static_cast<uint32_t>(f32_to_bf16(s0)) | (static_cast<uint32_t>(f32_to_bf16(s1)) << 16), ru,
-            lane_off + (t0 + i) * row, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(f32x2_to_bf16x2(s0, s1), ru, lane_off + (t0 + i) * row, 0, 0);
     }
 }
 
