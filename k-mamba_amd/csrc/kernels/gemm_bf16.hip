@@ -118,8 +118,10 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_mfma(GemmArgs p) {
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = w >> 1, wn = w & 1;
-    const long m0 = static_cast<long>(blockIdx.y) * kBM;
-    const long n0 = static_cast<long>(blockIdx.x) * kBN;
+    long mb, nb;
+    xcd_tile(mb, nb);                  // tiles of one row block share an XCD's L2
+    const long m0 = mb * kBM;
+    const long n0 = nb * kBN;
 
     // Windows over the rows this workgroup reads (offsets stay below 2 GiB:
     // the launcher splits M so that a window fits).
@@ -220,8 +222,10 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_mfma_256(GemmArgs p) {
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = w >> 1, wn = w & 1;
-    const long m0 = static_cast<long>(blockIdx.y) * kGM;
-    const long n0 = static_cast<long>(blockIdx.x) * kGN;
+    long mb, nb;
+    xcd_tile(mb, nb);                  // tiles of one row block share an XCD's L2
+    const long m0 = mb * kGM;
+    const long n0 = nb * kGN;
     const long arows = std::min<long>(kGM, p.M - m0), brows = std::min<long>(kGN, p.N - n0);
     // Rows past the window read 0 (range check); the launcher keeps offsets
     // below 2 GiB.
@@ -338,8 +342,10 @@ __global__ void __launch_bounds__(256) gemm_bf16_direct(GemmArgs p) {
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int fr = lane & 31, fh = lane >> 5;
-    const long m0 = static_cast<long>(blockIdx.y) * (KSPLIT > 1 ? 32 : 128) + (KSPLIT > 1 ? 0 : w * 32);
-    const long n0 = static_cast<long>(blockIdx.x) * (32 * TN);
+    long mb, nb;
+    xcd_tile(mb, nb);
+    const long m0 = mb * (KSPLIT > 1 ? 32 : 128) + (KSPLIT > 1 ? 0 : w * 32);
+    const long n0 = nb * (32 * TN);
     const long arows = std::min<long>(32, p.M - m0), brows = std::min<long>(32 * TN, p.N - n0);
     const auto rA = make_rsrc(p.A + (arows > 0 ? m0 : 0) * p.lda,
                               arows > 0 ? (arows - 1) * p.lda * 2 + p.K * 2 : 0);

@@ -72,6 +72,24 @@ __device__ __forceinline__ float sum_xor16(float v) {
 // 2^x on the transcendental unit (v_exp_f32, ~1 ulp).
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Workgroup id in an order where consecutive ids share an XCD: the hardware
+// deals workgroups to the 8 XCDs round-robin (XCD x runs ids x, x + 8, ...);
+// this maps XCD x's ids to one contiguous range, so neighbouring tiles (which
+// share operands) meet in one L2.
+__device__ __forceinline__ long xcd_remap(long b, long nb) {
+    const long q = nb / 8, r = nb % 8, x = b % 8;
+    return x * q + (x < r ? x : r) + b / 8;
+}
+
+// (row block, column block) of a 2D grid of gx column blocks, numbered
+// row-major in XCD order.
+__device__ __forceinline__ void xcd_tile(long &mb, long &nb) {
+    const long gx = gridDim.x, lin = static_cast<long>(blockIdx.y) * gx + blockIdx.x;
+    const long t = xcd_remap(lin, gx * gridDim.y);
+    mb = t / gx;
+    nb = t % gx;
+}
+
 // SiLU v * sigmoid(v) = v / (1 + e^-v) on the hardware exp2 and reciprocal
 // (about 1 ulp each) instead of the library exp and the IEEE division
 // sequence; e^-v = inf gives rcp = 0, the limit.
