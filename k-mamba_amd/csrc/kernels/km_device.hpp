@@ -72,6 +72,48 @@ __device__ __forceinline__ float sum_xor16(float v) {
 // 2^x on the transcendental unit (v_exp_f32, ~1 ulp).
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// DPP lane move within rows of 16 lanes (ctrl: row_ror, mirrors, quad_perm).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                  0xf, 0xf, false));
+}
+
+// Reduce-scatter over the 16 lanes of each row, on DPP VALU operands only:
+// lane l contributes yr[0..TW) and returns the row's total of value
+// (l % 16) / (16 / TW). Each step keeps half of the remaining values and
+// adds the partner's copy of that half; partners differ in one lane bit per
+// step (xor 8 by row_ror:8, xor 7 by row_half_mirror, xor 2 and xor 1 by
+// quad_perm), so the four steps cover all 16 lanes, as a butterfly does.
+template <int CTRL, int BIT, int CNT, int TW>
+__device__ __forceinline__ void readout_step(float (&cur)[TW], int l) {
+    if constexpr (CNT > 1) {
+        constexpr int H = CNT / 2;
+        const bool hi = (l & BIT) != 0;
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const float keep = hi ? cur[H + i] : cur[i];
+            const float send = hi ? cur[i] : cur[H + i];
+            cur[i] = keep + dpp<CTRL>(send);
+        }
+    } else {
+        cur[0] += dpp<CTRL>(cur[0]);
+    }
+}
+template <int TW>
+__device__ __forceinline__ float row_readout(const float (&yr)[TW]) {
+    static_assert(TW == 4 || TW == 8 || TW == 16, "16 / TW lanes per column");
+    const int l = threadIdx.x & 15;
+    float cur[TW];
+#pragma unroll
+    for (int i = 0; i < TW; ++i) cur[i] = yr[i];
+    readout_step<0x128, 8, TW>(cur, l);                         // row_ror:8 (l ^ 8)
+    readout_step<0x141, 4, (TW > 2 ? TW / 2 : 1)>(cur, l);      // row_half_mirror (l ^ 7)
+    readout_step<0x4E, 2, (TW > 4 ? TW / 4 : 1)>(cur, l);       // quad_perm [2,3,0,1] (l ^ 2)
+    readout_step<0xB1, 1, (TW > 8 ? TW / 8 : 1)>(cur, l);       // quad_perm [1,0,3,2] (l ^ 1)
+    return cur[0];
+}
+
 // Workgroup id in an order where consecutive ids share an XCD: the hardware
 // deals workgroups to the 8 XCDs round-robin (XCD x runs ids x, x + 8, ...);
 // this maps XCD x's ids to one contiguous range, so neighbouring tiles (which

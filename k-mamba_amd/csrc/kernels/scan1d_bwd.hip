@@ -93,6 +93,7 @@ __device__ __forceinline__ void rs_step(float (&cur)[NV], int lane) {
 template <int NV, int DLN>
 __device__ __forceinline__ float reduce_scatter(const float (&v)[NV], int lane) {
     static_assert(NV <= DLN && DLN <= 64, "reduce over at most 64 lanes");
+    if constexpr (DLN == 16 && NV == 4) return row_readout<4>(v);   // DPP, no LDS swizzles
     float cur[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) cur[i] = v[i];
@@ -174,6 +175,10 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
     constexpr unsigned kDrop = 0x80000000u;
     constexpr int GRP = DL / NPL;   // lanes per reduced B/C gradient value
     const unsigned vxs = own_x ? static_cast<unsigned>(vx) : kDrop;
+    // x and dy of lanes past D load as 0: their dB / dC terms (ah*delta*x,
+    // dy*h) vanish without a select, and every other output of such a lane
+    // is dropped.
+    const int vxz = static_cast<int>(dvalid ? static_cast<unsigned>(vx) : kDrop);
     const unsigned vbcs = dvalid ? static_cast<unsigned>(vbc) : kDrop;
     const unsigned vacc = (dl % GRP) == 0 ? static_cast<unsigned>((n0 + dl / GRP) * 4) : kDrop;
     const auto racB = make_rsrc(SHARED ? p.accB + b * p.L * N : nullptr, SHARED ? p.L * N * 4 : 0);
@@ -229,9 +234,9 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
 #pragma unroll
         for (int k = 0; k < TC; ++k) {
             const int so = (s * SC + w * TC + k) * rowx;
-            xo[k] = IO::ld(rx, vx + so, 0);
+            xo[k] = IO::ld(rx, vxz + so, 0);
             dto[k] = IO::ld(rdt, vx + so, 0);
-            go[k] = IO::ld(rdy, vx + so, 0);
+            go[k] = IO::ld(rdy, vxz + so, 0);
         }
     };
     // B or C row of step t (t relative to the super-chunk: r = t - s*SC).
@@ -476,10 +481,10 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
                 dAacc[j] = fmaf(dtk, q, dAacc[j]);
                 sa = fmaf(Ar[j], q, sa);
                 sbv = fmaf(ah, bv[j], sbv);
-                // Lanes past D (clamped to channel D-1) add nothing to the
-                // channel sums.
-                dBv[j] = dvalid ? ah * u : 0.f;
-                dCv[j] = dvalid ? gk * hs[k][j] : 0.f;
+                // Lanes past D have x = dy = 0 (so u = gk = 0 and ah = 0): they
+                // add nothing to the channel sums.
+                dBv[j] = ah * u;
+                dCv[j] = gk * hs[k][j];
                 g[j] = ae;
             }
             // Sum the state groups of the channel (lanes dl + DL*ns).
