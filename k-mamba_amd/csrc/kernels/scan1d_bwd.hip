@@ -487,14 +487,20 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
                 dCv[j] = gk * hs[k][j];
                 g[j] = ae;
             }
-            // Sum the state groups of the channel (lanes dl + DL*ns).
-            if constexpr (NS >= 4) {
-                sa = sum_xor16(sa);
-                sbv = sum_xor16(sbv);
-            }
+            // Sum the state groups of the channel (lanes dl + DL*ns), both
+            // values at once: a 32-lane swap of (sa, sbv) leaves partial sums
+            // of sa in lanes 0-31 and of sbv in lanes 32-63, a 16-lane swap
+            // completes them (NS = 4), and a last 32-lane swap hands every
+            // lane both totals.
             if constexpr (NS >= 2) {
-                sa = sum_xor32(sa);
-                sbv = sum_xor32(sbv);
+                const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(sa), __float_as_uint(sbv),
+                                                                false, false);
+                float z = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+                if constexpr (NS >= 4) z = sum_xor16(z);
+                const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(z), __float_as_uint(z),
+                                                                false, false);
+                sa = __uint_as_float(q[0]);
+                sbv = __uint_as_float(q[1]);
             }
             // Rows past L and lanes without output are dropped by the range
             // check, so none of the stores below needs a branch.
