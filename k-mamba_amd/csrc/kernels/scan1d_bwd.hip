@@ -591,10 +591,16 @@ __global__ void __launch_bounds__(256) scan1d_bwd_serial(Scan1DBwdArgs p) {
     for (long m = 0; m < N; ++m) unsafeAtomicAdd(p.dA + d * N + m, dAl[m]);
 }
 
-__global__ void __launch_bounds__(256) fill_zero_kernel(float *p, long n) {
-    for (long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-         i += static_cast<long>(gridDim.x) * blockDim.x)
-        p[i] = 0.f;
+// Zeroes p[0, n) and q[0, m) in one launch; q (the workspace accumulators)
+// with 16-byte stores when it is 16-byte aligned.
+__global__ void __launch_bounds__(256) fill_zero_kernel(float *p, long n, float *q, long m) {
+    const long i0 = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const long stride = static_cast<long>(gridDim.x) * blockDim.x;
+    for (long i = i0; i < n; i += stride) p[i] = 0.f;
+    const long m4 = (reinterpret_cast<uintptr_t>(q) & 15) == 0 ? m / 4 : 0;
+    float4 *q4 = reinterpret_cast<float4 *>(q);
+    for (long i = i0; i < m4; i += stride) q4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (long i = m4 * 4 + i0; i < m; i += stride) q[i] = 0.f;
 }
 
 // Shared B/C: accumulators [B, L, N] -> outputs at b*sb + t*st + n.
@@ -613,10 +619,11 @@ __global__ void __launch_bounds__(256) scan1d_bwd_finalize(const float *accB, co
     }
 }
 
-static int fill_zero(float *p, long n, hipStream_t s) {
-    if (n <= 0) return 0;
-    const long blocks = std::min<long>((n + 255) / 256, 4096);
-    hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, s, p, n);
+static int fill_zero(float *p, long n, hipStream_t s, float *q = nullptr, long m = 0) {
+    if (n <= 0 && m <= 0) return 0;
+    const long blocks = std::min<long>((std::max(n, m / 4) + 255) / 256, 4096);
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, s, p, std::max(n, 0L), q,
+                       q ? std::max(m, 0L) : 0L);
     KM_HIP_TRY(hipGetLastError());
     return 0;
 }
@@ -724,8 +731,7 @@ int scan1d_bwd_launch(const KMScan1DBwd *k, hipStream_t stream) {
     if (!gpu_ready()) return -1;
     const BwdPlan pl = bwd_plan(k);
     const bool bf = (k->dtype == KM_BF16);
-    if (fill_zero(k->dA, k->D * k->N, stream) != 0) return -1;
-    if (k->L == 0) return 0;
+    if (k->L == 0) return fill_zero(k->dA, k->D * k->N, stream);
     char *ws = nullptr;
     if (pl.bytes > 0) {
         if (k->workspace) {
@@ -750,8 +756,10 @@ int scan1d_bwd_launch(const KMScan1DBwd *k, hipStream_t stream) {
     if (pl.shared) {
         a.accB = reinterpret_cast<float *>(ws + pl.off_acc);
         a.accC = a.accB + k->B * k->L * k->N;
-        if (fill_zero(a.accB, 2 * k->B * k->L * k->N, stream) != 0) return -1;
     }
+    // dA, and the shared dB / dC accumulators, start at zero (one launch).
+    if (fill_zero(k->dA, k->D * k->N, stream, a.accB, pl.shared ? 2 * k->B * k->L * k->N : 0) != 0)
+        return -1;
     if (pl.need_ckpt || pl.need_hist) {
         // Forward states from the same inputs (y not written).
         KMScan1DFwd f{};
