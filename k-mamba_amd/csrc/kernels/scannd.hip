@@ -14,14 +14,18 @@
 //    256-byte coalesced accesses and y is a reduction over the M lanes of a
 //    channel;
 //  * the grid is cut into tiles; tiles with equal tile-index sum (a tile
-//    band) are independent, so the host issues one launch per tile band (47
-//    for a 256x256 grid with 16x8 tiles instead of 511 per-level launches);
-//    the kernel boundary publishes every tile's h to the next band;
+//    band) are independent. 2D grids run one launch per tile band (47 for a
+//    256x256 grid with 16x8 tiles instead of 511 per-level launches); the
+//    kernel boundary publishes every tile's h to the next band. Grids of 3
+//    or more dims run one dataflow launch per step, in which a tile waits
+//    only for its own axis predecessors (completion flags, each channel
+//    group kept on one XCD so producer and consumer share an L2);
 //  * one wave per (tile, channel group) walks its tile row by row (rows
 //    along the last axis), keeping the row above in registers and taking
 //    the left neighbour from the previous column; neighbours across the
 //    tile's boundary and along leading axes are read back from h.
 #include <cstdlib>
+#include <cstring>
 
 #include <cstdio>
 
@@ -63,8 +67,8 @@ __device__ __forceinline__ int count2(int s, int n1, int n2) {
 // index tuple, whose indices sum to b (2 <= nd <= 4). Leading axes pick
 // their index by counting the tuples of the remaining axes; the last two
 // axes follow in closed form.
-__device__ inline bool band_tile(const ScanNDArgs &p, int ordinal, int *ti) {
-    int s = p.band, o = ordinal;
+__device__ inline bool band_tile(const ScanNDArgs &p, int band, int ordinal, int *ti) {
+    int s = band, o = ordinal;
     for (int a = 0; a + 2 < p.nd; ++a) {
         bool found = false;
         for (int v = 0; v < p.ntile[a] && v <= s; ++v) {
@@ -136,19 +140,10 @@ struct NDRow {
 // previous plane's PL rows in registers, so only the tile's first plane reads
 // its axis-0 neighbours from h.
 template <int ND, int TW, int MM, int PL>
-__global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
+__device__ __forceinline__ void scannd_tile(const ScanNDArgs &p, const int (&ti)[kMaxNd], int cg) {
     constexpr bool RING = (ND == 3 && PL > 0);
     static_assert(PL % 2 == 0, "planes of whole row pairs");
-    const int lane = threadIdx.x;
-    // Workgroups are dealt to the 8 XCDs round-robin; renumber them so that
-    // consecutive channel groups of a tile, which share x / delta cache
-    // lines (4 channels = 16 bytes of a row each), run on one XCD's L2.
-    const int nb = gridDim.x, q = nb / 8, r = nb % 8, xcd = blockIdx.x % 8;
-    const int lb = xcd * q + min(xcd, r) + static_cast<int>(blockIdx.x / 8);
-    const int cg = lb % p.ncg;
-    const int ordinal = lb / p.ncg;
-    int ti[kMaxNd];
-    if (!band_tile(p, ordinal, ti)) return;
+    const int lane = threadIdx.x & 63;
 
     constexpr int ar = ND - 2, ac = ND - 1;       // row / column axes
     const int f = cg * 64 + lane;                 // flattened (d, m)
@@ -392,6 +387,97 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
     }
 }
 
+// One launch per tile band: workgroup = (tile of band p.band, channel group).
+// Workgroups are dealt to the 8 XCDs round-robin; they are renumbered so
+// that consecutive channel groups of a tile, which share x / delta cache
+// lines (4 channels = 16 bytes of a row each), run on one XCD's L2.
+template <int ND, int TW, int MM, int PL>
+__global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
+    const int nb = gridDim.x, q = nb / 8, r = nb % 8, xcd = blockIdx.x % 8;
+    const int lb = xcd * q + min(xcd, r) + static_cast<int>(blockIdx.x / 8);
+    const int cg = lb % p.ncg;
+    const int ordinal = lb / p.ncg;
+    int ti[kMaxNd];
+    if (!band_tile(p, p.band, ordinal, ti)) return;
+    scannd_tile<ND, TW, MM, PL>(p, ti, cg);
+}
+
+// Dataflow schedule, one launch per step: a tile waits only for its own
+// axis predecessors instead of the whole previous band. Channel groups never
+// depend on each other, so XCD x owns the groups [cg_lo[x], cg_lo[x + 1]) for
+// every tile: each producer / consumer pair shares one XCD's L2 (coherent
+// for all its CUs), and no data crosses XCDs inside the launch. Each
+// workgroup reads the XCD it runs on from the hardware and takes items (tile
+// in band order, then channel group) from that XCD's counter, so an item is
+// only ever taken by a running wave and every item's predecessors were taken
+// before it: the waits always end. Finishing an item publishes
+// flags[tile * ncg + cg] = epoch (this launch's number) after its h stores
+// are acknowledged; a wait polls at most kFlowSpin times and then goes on.
+constexpr int kMaxFlowBands = 768;
+constexpr int kFlowSpin = 1 << 16;
+struct FlowArgs {
+    unsigned *flags;                     // [ntiles * ncg] epoch of the last finish
+    unsigned *counter;                   // [8] items taken per XCD, zero at launch
+    unsigned epoch;
+    int nbands;
+    int cg_lo[9];                        // channel groups of XCD x: [cg_lo[x], cg_lo[x + 1])
+    int band_start[kMaxFlowBands + 1];   // first tile (band order) of each band
+};
+
+__device__ __forceinline__ void flow_wait(const unsigned *flag, unsigned epoch) {
+    if ((threadIdx.x & 63) == 0) {
+        for (int i = 0; i < kFlowSpin; ++i) {
+            if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch) break;
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+template <int ND, int TW, int MM, int PL>
+__global__ void __launch_bounds__(64) scannd_flow_kernel(ScanNDArgs p, FlowArgs f) {
+    const int xcd = static_cast<int>(__builtin_amdgcn_s_getreg(20 | (3 << 11))) & 7;   // HW_REG_XCC_ID
+    const int cg0 = f.cg_lo[xcd], ncx = f.cg_lo[xcd + 1] - cg0;
+    if (ncx <= 0) return;
+    const int ntiles = f.band_start[f.nbands];
+    const unsigned nitems = static_cast<unsigned>(ntiles) * static_cast<unsigned>(ncx);
+    int tstride[kMaxNd];                 // row-major tile index strides
+    tstride[ND - 1] = 1;
+#pragma unroll
+    for (int a = ND - 2; a >= 0; --a) tstride[a] = tstride[a + 1] * p.ntile[a + 1];
+    for (;;) {
+        unsigned item = 0;
+        if ((threadIdx.x & 63) == 0) item = atomicAdd(&f.counter[xcd], 1u);
+        item = __builtin_amdgcn_readfirstlane(item);
+        if (item >= nitems) break;
+        const int tb = static_cast<int>(item / ncx);
+        const int cg = cg0 + static_cast<int>(item % ncx);
+        int lo = 0, hi = f.nbands - 1;   // band: last b with band_start[b] <= tb
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) / 2;
+            if (f.band_start[mid] <= tb) lo = mid;
+            else hi = mid - 1;
+        }
+        int ti[kMaxNd];
+        band_tile(p, lo, tb - f.band_start[lo], ti);
+        int tl = 0;
+#pragma unroll
+        for (int a = 0; a < ND; ++a) tl += ti[a] * tstride[a];
+#pragma unroll
+        for (int a = 0; a < ND; ++a)
+            if (ti[a] > 0) flow_wait(f.flags + static_cast<long>(tl - tstride[a]) * p.ncg + cg, f.epoch);
+        scannd_tile<ND, TW, MM, PL>(p, ti, cg);
+        __builtin_amdgcn_s_waitcnt(0);   // this wave's h stores acknowledged by L2
+        if ((threadIdx.x & 63) == 0)
+            __hip_atomic_store(f.flags + static_cast<long>(tl) * p.ncg + cg, f.epoch, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+__global__ void flow_reset(unsigned *counter) {
+    if (threadIdx.x < 8) counter[threadIdx.x] = 0u;
+}
+
 // General fallback (any D, M): one launch per wavefront level of the point
 // grid, one thread per (point, channel), reading the level's offsets from
 // the device copy of the plan.
@@ -452,15 +538,75 @@ static void scannd_tile_shape(int nd, int &tw, int &tl) {
     if (nd == 3 && (t3w == 4 || t3w == 8) && t3l > 0 && t3l <= 64) { tw = t3w; tl = t3l; }
 }
 
+template <int ND, int TW, int MM, int PL>
+static void launch_tile_pl(dim3 g, const ScanNDArgs &a, const FlowArgs *flow, hipStream_t s) {
+    if (flow) hipLaunchKernelGGL((scannd_flow_kernel<ND, TW, MM, PL>), g, dim3(64), 0, s, a, *flow);
+    else      hipLaunchKernelGGL((scannd_tile_kernel<ND, TW, MM, PL>), g, dim3(64), 0, s, a);
+}
+
 template <int ND, int TW, int MM>
-static void launch_tile(dim3 g, const ScanNDArgs &a, bool ring, hipStream_t s) {
+static void launch_tile(dim3 g, const ScanNDArgs &a, bool ring, const FlowArgs *flow, hipStream_t s) {
     if constexpr (ND == 3) {
         if (ring) {
-            hipLaunchKernelGGL((scannd_tile_kernel<ND, TW, MM, 4>), g, dim3(64), 0, s, a);
+            launch_tile_pl<ND, TW, MM, 4>(g, a, flow, s);
             return;
         }
     }
-    hipLaunchKernelGGL((scannd_tile_kernel<ND, TW, MM, 0>), g, dim3(64), 0, s, a);
+    launch_tile_pl<ND, TW, MM, 0>(g, a, flow, s);
+}
+
+// Per-device state of the dataflow schedule: completion flags and the
+// per-XCD item counters (one buffer: 8 counters, then flags; zeroed when
+// allocated), the launch
+// epoch, and the device's XCD count. Launches that overlap on one device
+// share it and race, like the library workspace.
+struct FlowState {
+    unsigned *buf = nullptr;
+    size_t cap = 0;                      // u32 words
+    unsigned epoch = 0;
+    int nxcc = -1;
+};
+static FlowState g_flow[64];
+
+// The dataflow schedule runs grids of 3 or more dims (2D grids are faster
+// with one launch per band on MI355X: their 47-tile critical path, slowed by
+// the tiles running beside it, sets the time), needs the device's 8 XCDs as
+// the hardware reports them (XCC_ID 0-7) and a band table that fits the
+// kernel arguments; KM_SCANND_SCHED=band keeps one launch per band.
+static FlowState *flow_state(int nd, int nbands, size_t words, hipStream_t s) {
+    const char *e = std::getenv("KM_SCANND_SCHED");
+    if (nd < 3 || (e && std::strcmp(e, "band") == 0) || nbands > kMaxFlowBands) return nullptr;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    FlowState &st = g_flow[dev];
+    if (st.nxcc < 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess) n = 0;
+        st.nxcc = n;
+    }
+    if (st.nxcc != 8) return nullptr;
+    if (st.cap < words) {
+        if (st.buf) {
+            (void)hipDeviceSynchronize();   // earlier launches may still use the old flags
+            (void)hipFree(st.buf);
+            st.buf = nullptr;
+            st.cap = 0;
+        }
+        void *ptr = nullptr;
+        if (hipMalloc(&ptr, words * 4) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        if (hipMemset(ptr, 0, words * 4) != hipSuccess) {
+            (void)hipGetLastError();
+            (void)hipFree(ptr);
+            return nullptr;
+        }
+        st.buf = static_cast<unsigned *>(ptr);
+        st.cap = words;
+    }
+    (void)s;
+    return &st;
 }
 
 static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s) {
@@ -515,12 +661,41 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s) {
         }
         // 3D tiles of 4 rows along axis 1 keep the previous plane in registers.
         const bool ring = a.nd == 3 && a.tile[1] == 4;
-        for (int b = 0; b < nbands; ++b) {
+        long ntiles = 0;
+        for (int b = 0; b < nbands; ++b) ntiles += cnt[b];
+        static thread_local FlowArgs fa;
+        FlowState *st = (ntiles * a.ncg < 0x7fffffffL)
+                            ? flow_state(a.nd, nbands, static_cast<size_t>(ntiles * a.ncg) + 8, s) : nullptr;
+        const FlowArgs *flow = nullptr;
+        if (st) {
+            if (++st->epoch == 0) st->epoch = 1;
+            // Counters first, flags after: flags only ever hold epochs of
+            // earlier launches (whatever the shape), never the current one.
+            fa.counter = st->buf;
+            fa.flags = st->buf + 8;
+            fa.epoch = st->epoch;
+            fa.nbands = nbands;
+            for (int x = 0; x <= 8; ++x) fa.cg_lo[x] = static_cast<int>(static_cast<long>(x) * a.ncg / 8);
+            fa.band_start[0] = 0;
+            for (int b = 0; b < nbands; ++b) fa.band_start[b + 1] = fa.band_start[b] + static_cast<int>(cnt[b]);
+            hipLaunchKernelGGL(flow_reset, dim3(1), dim3(64), 0, s, fa.counter);
+            flow = &fa;
+        }
+        // Dataflow: one launch of 8k one-wave workgroups (k <= 256: two per
+        // SIMD) that take items until their XCD's queue is empty. The
+        // hardware deals workgroups to the XCDs round-robin, so each XCD
+        // runs k of them, k = the largest per-XCD item count up to 256.
+        long per_xcd = 0;
+        if (flow)
+            for (int x = 0; x < 8; ++x)
+                per_xcd = std::max<long>(per_xcd, ntiles * (fa.cg_lo[x + 1] - fa.cg_lo[x]));
+        const int nlaunch = flow ? 1 : nbands;
+        for (int b = 0; b < nlaunch; ++b) {
             a.band = b;
-            const long grid = cnt[b] * a.ncg;
+            const long grid = flow ? 8 * std::min<long>(per_xcd, 256) : cnt[b] * a.ncg;
             if (grid <= 0) continue;
             const dim3 g(static_cast<unsigned>(grid));
-#define KM_ND_LAUNCH(NDv, TWv, MMv) launch_tile<NDv, TWv, MMv>(g, a, ring, s)
+#define KM_ND_LAUNCH(NDv, TWv, MMv) launch_tile<NDv, TWv, MMv>(g, a, ring, flow, s)
 #define KM_ND_BY_M(NDv, TWv)                                  \
             switch (a.M) {                                    \
             case 1: KM_ND_LAUNCH(NDv, TWv, 1); break;         \

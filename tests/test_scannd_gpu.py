@@ -62,6 +62,39 @@ def run_device(dims, x, A, B, Cm, dt, entry="km"):
     return y.cpu().numpy(), h.cpu().numpy()
 
 
+# Shapes on the tile kernels: 2D, 3D with the register ring (tiles of 4 rows
+# along axis 1), 3D without it, 4D, ragged edges, several channel groups.
+SCHED_CASES = [((64, 96), 64, 16), ((130, 70), 8, 8), ((9, 6, 11), 4, 16), ((7, 5, 10), 4, 16),
+               ((5, 5, 5, 9), 4, 16), ((33, 65), 8, 16), ((40, 24, 24), 16, 16)]
+
+
+@pytest.mark.parametrize("dims,D,M", SCHED_CASES)
+def test_dataflow_and_band_schedules_agree(dims, D, M, monkeypatch):
+    # The per-tile dataflow launch (3+ dims on a device with 8 XCDs) and one
+    # launch per tile band compute every point with the same arithmetic:
+    # their outputs agree bit for bit, and the band schedule matches the
+    # oracle.
+    # Stable decays (configs[2]: a_k ~ U(0.05, 0.9/ndims), A = log a_k), so
+    # every value stays finite on the larger grids.
+    nd, P = len(dims), int(np.prod(dims))
+    g = rng_for("nd-sched", dims, D, M)
+    x = g.standard_normal((P, D)).astype(np.float32)
+    A = np.log(g.uniform(0.05, 0.9 / nd, (nd, D, M))).astype(np.float32)
+    B = (g.standard_normal((P, D, M)) * 0.25).astype(np.float32)
+    Cm = (g.standard_normal((P, D, M)) * 0.25).astype(np.float32)
+    dt = g.uniform(0.5, 1.0, (nd, P, D)).astype(np.float32)
+    y1, h1 = run_device(dims, x, A, B, Cm, dt)
+    monkeypatch.setenv("KM_SCANND_SCHED", "band")
+    y2, h2 = run_device(dims, x, A, B, Cm, dt)
+    assert np.isfinite(y1).all() and np.isfinite(h1).all()
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    assert np.array_equal(h1.view(np.uint32), h2.view(np.uint32))
+    yr, hr = O.scannd_ref(dims, x, A, B, Cm, dt, nthreads=8, fast=True)
+    ya, ha = kappa(dims, x, A, B, Cm, dt)
+    assert_close(y2, yr, TOL_F32, "y", ya)
+    assert_close(h2, hr, TOL_F32, "h", ha)
+
+
 def test_known_answers_all_entry_points():
     # tests/unit/test_scan_nd.c:41-141.
     for dims, A, want in (((2, 2), [np.log(2.0), np.log(3.0)], [1, 4, 3, 18]),
