@@ -44,7 +44,9 @@ def check(got, want, x, tol=1e-4):
 
 
 @pytest.mark.parametrize("D,N,L,R,batch", [(24, 8, 37, 2, 3), (16, 16, 64, 1, 2), (10, 7, 20, 1, 1),
-                                           (33, 4, 9, 3, 2), (8, 1, 5, 1, 1), (64, 16, 300, 1, 4)])
+                                           (33, 4, 9, 3, 2), (8, 1, 5, 1, 1), (64, 16, 300, 1, 4),
+                                           # 101 controller rows: two row groups of 64
+                                           (32, 16, 40, 3, 2)])
 def test_forward_host_pointers_vs_oracle(D, N, L, R, batch):
     p = mamba3_params(D, N, R)
     x = rng_for("m3x", D, N, L).standard_normal((batch, L, D)).astype(np.float32)
