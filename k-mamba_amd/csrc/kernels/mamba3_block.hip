@@ -135,16 +135,17 @@ __global__ void __launch_bounds__(256) m3_proj(M3Args p) {
 
 // The same projections on the fp32 matrix cores (v_mfma_f32_16x16x4_f32),
 // for D a multiple of 4: a wave computes 16 tokens x 16*TJ rows over every
-// fourth 16-wide k block (the 4 waves of a workgroup split K; wave 0 adds
+// kM3Split-th 16-wide k block (the waves of a workgroup split K; wave 0 adds
 // the other waves' partials from LDS in wave order). Lane l supplies token /
 // row l % 16 and, for k block b, the 16 contiguous bytes k = 16b + 4(l/16)
 // .. +3, one element per MFMA step: the k order within a dot product is
 // free, and both operands use the same one. Operands come from global memory
 // straight into registers, one block ahead; rows past T or J read 0.
 using f32x4v = float __attribute__((ext_vector_type(4)));
+constexpr int kM3Split = 8;
 template <int TJ>
-__global__ void __launch_bounds__(256) m3_proj_mfma(M3Args p) {
-    __shared__ float red[3][TJ * 4][64];
+__global__ void __launch_bounds__(64 * kM3Split) m3_proj_mfma(M3Args p) {
+    __shared__ float red[kM3Split - 1][TJ * 4][64];
     constexpr unsigned kDrop = 0x80000000u;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -178,11 +179,11 @@ __global__ void __launch_bounds__(256) m3_proj_mfma(M3Args p) {
     const long nkb = (p.D + 15) / 16;
     long kb = w;
     load_blk(kb, a0, b0);
-    for (; kb < nkb; kb += 8) {
-        load_blk(kb + 4, a1, b1);        // past K: zeros, added harmlessly
+    for (; kb < nkb; kb += 2 * kM3Split) {
+        load_blk(kb + kM3Split, a1, b1);        // past K: zeros, added harmlessly
         __builtin_amdgcn_sched_barrier(0);
         mfma_blk(a0, b0);
-        load_blk(kb + 8, a0, b0);
+        load_blk(kb + 2 * kM3Split, a0, b0);
         __builtin_amdgcn_sched_barrier(0);
         mfma_blk(a1, b1);
     }
@@ -195,7 +196,7 @@ __global__ void __launch_bounds__(256) m3_proj_mfma(M3Args p) {
     __syncthreads();
     if (w != 0) return;
 #pragma unroll 1
-    for (int v = 0; v < 3; ++v)
+    for (int v = 0; v < kM3Split - 1; ++v)
 #pragma unroll
         for (int j = 0; j < TJ; ++j)
 #pragma unroll
@@ -343,6 +344,26 @@ __global__ void __launch_bounds__(256) m3_out(M3Args p) {
     p.out[i] = p.x[i] + s;
 }
 
+// The same for D a multiple of 4 and 16-byte aligned x / out: thread (t, q)
+// handles channels 4q .. 4q+3 of token t with 16-byte loads and stores (no
+// per-element index division).
+__global__ void __launch_bounds__(256) m3_out4(M3Args p) {
+    const long q = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    if (4 * q >= p.D) return;
+    for (long t = blockIdx.y; t < p.T; t += gridDim.y) {
+        const long i = t * p.D + 4 * q;
+        float4 v = *reinterpret_cast<const float4 *>(p.x + i);
+        for (long r = 0; r < p.R; ++r) {
+            const float y = p.Y[t * p.R + r];
+            v.x = fmaf(p.W_out[(4 * q + 0) * p.R + r], y, v.x);
+            v.y = fmaf(p.W_out[(4 * q + 1) * p.R + r], y, v.y);
+            v.z = fmaf(p.W_out[(4 * q + 2) * p.R + r], y, v.z);
+            v.w = fmaf(p.W_out[(4 * q + 3) * p.R + r], y, v.w);
+        }
+        *reinterpret_cast<float4 *>(p.out + i) = v;
+    }
+}
+
 static long grid256(long n) { return (n + 255) / 256; }
 
 int mamba3_launch(M3Args &a, hipStream_t s) {
@@ -364,10 +385,10 @@ int mamba3_launch(M3Args &a, hipStream_t s) {
             return -1;
         }
         switch (tj) {
-        case 1: hipLaunchKernelGGL(m3_proj_mfma<1>, gm, dim3(256), 0, s, a); break;
-        case 2: hipLaunchKernelGGL(m3_proj_mfma<2>, gm, dim3(256), 0, s, a); break;
-        case 3: hipLaunchKernelGGL(m3_proj_mfma<3>, gm, dim3(256), 0, s, a); break;
-        default: hipLaunchKernelGGL(m3_proj_mfma<4>, gm, dim3(256), 0, s, a); break;
+        case 1: hipLaunchKernelGGL(m3_proj_mfma<1>, gm, dim3(64 * kM3Split), 0, s, a); break;
+        case 2: hipLaunchKernelGGL(m3_proj_mfma<2>, gm, dim3(64 * kM3Split), 0, s, a); break;
+        case 3: hipLaunchKernelGGL(m3_proj_mfma<3>, gm, dim3(64 * kM3Split), 0, s, a); break;
+        default: hipLaunchKernelGGL(m3_proj_mfma<4>, gm, dim3(64 * kM3Split), 0, s, a); break;
         }
     } else {
         hipLaunchKernelGGL(m3_proj, gp, dim3(256), 0, s, a);
@@ -377,7 +398,13 @@ int mamba3_launch(M3Args &a, hipStream_t s) {
     const long waves = (a.T / a.L) * npairs;          // one per (batch element, pair)
     hipLaunchKernelGGL(m3_scan, dim3(static_cast<unsigned>(waves)), dim3(64), 0, s, a, npairs);
     hipLaunchKernelGGL(m3_readout, dim3(grid256(a.T * a.R)), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(m3_out, dim3(grid256(a.T * a.D)), dim3(256), 0, s, a);
+    const bool al16 = ((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.out)) & 15) == 0;
+    if (a.D % 4 == 0 && al16) {
+        const dim3 go(static_cast<unsigned>(grid256(a.D / 4)), static_cast<unsigned>(std::min<long>(a.T, 65535)));
+        hipLaunchKernelGGL(m3_out4, go, dim3(256), 0, s, a);
+    } else {
+        hipLaunchKernelGGL(m3_out, dim3(grid256(a.T * a.D)), dim3(256), 0, s, a);
+    }
     KM_HIP_TRY(hipGetLastError());
     return 0;
 }
