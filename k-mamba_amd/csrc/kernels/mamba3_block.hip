@@ -134,7 +134,8 @@ __global__ void __launch_bounds__(256) m3_proj(M3Args p) {
 }
 
 // The same projections on the fp32 matrix cores (v_mfma_f32_16x16x4_f32),
-// for D a multiple of 4: a wave computes 16 tokens x 16*TJ rows over every
+// for D a multiple of 4: a wave computes 16*kM3TM tokens x 16*TJ rows (each
+// W fragment serves kM3TM token tiles) over every
 // kM3Split-th 16-wide k block (the waves of a workgroup split K; wave 0 adds
 // the other waves' partials from LDS in wave order). Lane l supplies token /
 // row l % 16 and, for k block b, the 16 contiguous bytes k = 16b + 4(l/16)
@@ -142,17 +143,18 @@ __global__ void __launch_bounds__(256) m3_proj(M3Args p) {
 // free, and both operands use the same one. Operands come from global memory
 // straight into registers, one block ahead; rows past T or J read 0.
 using f32x4v = float __attribute__((ext_vector_type(4)));
-constexpr int kM3Split = 8;
+constexpr int kM3Split = 8, kM3TM = 2;
 template <int TJ>
 __global__ void __launch_bounds__(64 * kM3Split) m3_proj_mfma(M3Args p) {
-    __shared__ float red[kM3Split - 1][TJ * 4][64];
+    constexpr int TM = kM3TM;
+    __shared__ float red[kM3Split - 1][TM * TJ * 4][64];
     constexpr unsigned kDrop = 0x80000000u;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int fr = lane & 15, fg = lane >> 4;
-    const long t0 = static_cast<long>(blockIdx.x) * 16;
+    const long t0 = static_cast<long>(blockIdx.x) * 16 * TM;
     const long j0 = static_cast<long>(blockIdx.y) * 16 * TJ;
-    const long trows = std::min<long>(16, p.T - t0), jrows = std::min<long>(16 * TJ, p.J - j0);
+    const long trows = std::min<long>(16 * TM, p.T - t0), jrows = std::min<long>(16 * TJ, p.J - j0);
     const auto rx = make_rsrc(p.x + t0 * p.D, trows > 0 ? trows * p.D * 4 : 0);
     const auto rw = make_rsrc(p.Wcat + j0 * p.D, jrows > 0 ? jrows * p.D * 4 : 0);
     const int D4 = static_cast<int>(p.D) * 4;
@@ -161,20 +163,26 @@ __global__ void __launch_bounds__(64 * kM3Split) m3_proj_mfma(M3Args p) {
         const int off = static_cast<int>(k < p.D ? static_cast<unsigned>(row * D4 + k * 4) : kDrop);
         return __builtin_bit_cast(f32x4v, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
     };
-    f32x4v acc[TJ];
+    f32x4v acc[TM][TJ];
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) acc[j] = f32x4v{0.f, 0.f, 0.f, 0.f};
-    f32x4v a0, a1, b0[TJ], b1[TJ];
-    auto load_blk = [&](long kb, f32x4v &a, f32x4v (&b)[TJ]) {
-        a = ld(rx, fr, kb);
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    f32x4v a0[TM], a1[TM], b0[TJ], b1[TJ];
+    auto load_blk = [&](long kb, f32x4v (&a)[TM], f32x4v (&b)[TJ]) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) a[i] = ld(rx, i * 16 + fr, kb);
 #pragma unroll
         for (int j = 0; j < TJ; ++j) b[j] = ld(rw, j * 16 + fr, kb);
     };
-    auto mfma_blk = [&](const f32x4v &a, const f32x4v (&b)[TJ]) {
+    auto mfma_blk = [&](const f32x4v (&a)[TM], const f32x4v (&b)[TJ]) {
 #pragma unroll
         for (int st = 0; st < 4; ++st)
 #pragma unroll
-            for (int j = 0; j < TJ; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st], b[j][st], acc[j], 0, 0, 0);
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][st], b[j][st], acc[i][j], 0, 0, 0);
     };
     const long nkb = (p.D + 15) / 16;
     long kb = w;
@@ -189,28 +197,34 @@ __global__ void __launch_bounds__(64 * kM3Split) m3_proj_mfma(M3Args p) {
     }
     if (w > 0) {
 #pragma unroll
-        for (int j = 0; j < TJ; ++j)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) red[w - 1][j * 4 + r][lane] = acc[j][r];
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) red[w - 1][(i * TJ + j) * 4 + r][lane] = acc[i][j][r];
     }
     __syncthreads();
     if (w != 0) return;
 #pragma unroll 1
     for (int v = 0; v < kM3Split - 1; ++v)
 #pragma unroll
-        for (int j = 0; j < TJ; ++j)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[j][r] += red[v][j * 4 + r][lane];
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[i][j][r] += red[v][(i * TJ + j) * 4 + r][lane];
     // Accumulator r of lane l: token 4(l/16) + r, row l % 16 of its tile.
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-        const long jj = j0 + j * 16 + fr;
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const long t = t0 + 4 * fg + r;
-            if (t < p.T && jj < p.J) p.P[t * p.J + jj] = acc[j][r];
+        for (int j = 0; j < TJ; ++j) {
+            const long jj = j0 + j * 16 + fr;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const long t = t0 + i * 16 + 4 * fg + r;
+                if (t < p.T && jj < p.J) p.P[t * p.J + jj] = acc[i][j][r];
+            }
         }
-    }
 }
 
 // ---- 2. per-step decay and drive --------------------------------------------
@@ -377,9 +391,10 @@ int mamba3_launch(M3Args &a, hipStream_t s) {
         set_error("mamba_block_forward: too many projection rows");
         return -1;
     }
-    if (a.D % 4 == 0 && a.D * 16 * 4 < 0x7fffffffL && a.D * 64 * 4 < 0x7fffffffL) {
+    if (a.D % 4 == 0 && a.D * 16 * kM3TM * 4 < 0x7fffffffL && a.D * 64 * 4 < 0x7fffffffL) {
         const int tj = static_cast<int>(std::min<long>(4, (a.J + 15) / 16));
-        const dim3 gm(static_cast<unsigned>((a.T + 15) / 16), static_cast<unsigned>((a.J + 16 * tj - 1) / (16 * tj)));
+        const dim3 gm(static_cast<unsigned>((a.T + 16 * kM3TM - 1) / (16 * kM3TM)),
+                      static_cast<unsigned>((a.J + 16 * tj - 1) / (16 * tj)));
         if (gm.y > 65535) {
             set_error("mamba_block_forward: too many projection rows");
             return -1;
