@@ -143,7 +143,7 @@ __global__ void __launch_bounds__(256) m3_proj(M3Args p) {
 // free, and both operands use the same one. Operands come from global memory
 // straight into registers, one block ahead; rows past T or J read 0.
 using f32x4v = float __attribute__((ext_vector_type(4)));
-constexpr int kM3Split = 8, kM3TM = 2;
+constexpr int kM3Split = 8, kM3TM = 4;
 template <int TJ>
 __global__ void __launch_bounds__(64 * kM3Split) m3_proj_mfma(M3Args p) {
     constexpr int TM = kM3TM;
