@@ -268,13 +268,16 @@ __global__ void __launch_bounds__(256) m3_prep(M3Args p) {
 // ---- 3. the recurrence ------------------------------------------------------
 // Per state pair (2i, 2i+1) of one batch element, h_t = M_t h_{t-1} + c_t
 // with M_t = diag(a0_t, a1_t) R(theta): a linear recurrence of 2x2 maps, so
-// it runs as a chunked scan. One wave per (batch element, pair); lane k owns
-// the chunk of CH = ceil(L/64) consecutive steps. (1) Each lane composes its
-// chunk's map h -> P h + v from a zero state. (2) An inclusive scan of the 64
-// maps across the lanes (Hillis-Steele, lane shuffles) gives every chunk the
-// state entering it (the previous lane's v). (3) Each lane replays its steps
-// from that state with the sequential step formula, writing H. An odd last
-// state has no partner: M_t = diag(a0_t, 0) and no rotation.
+// it runs as a chunked scan. One workgroup of kM3ScanW waves per (batch
+// element, pair); thread k owns the chunk of CH = ceil(L / (64 kM3ScanW))
+// consecutive steps. (1) Each thread composes its chunk's map h -> P h + v
+// from a zero state. (2) An inclusive scan of the maps across the lanes of
+// each wave (Hillis-Steele, lane shuffles), then the waves' total maps
+// through LDS, give every chunk the state entering it. (3) Each thread
+// replays its steps from that state with the sequential step formula,
+// writing H. An odd last state has no partner: M_t = diag(a0_t, 0) and no
+// rotation.
+constexpr int kM3ScanW = 4;
 __device__ __forceinline__ void m3_step(float a0, float a1, float cs, float sn, bool pair,
                                         float c0, float c1, float &h0, float &h1) {
     if (pair) {
@@ -286,16 +289,17 @@ __device__ __forceinline__ void m3_step(float a0, float a1, float cs, float sn, 
     }
 }
 
-__global__ void __launch_bounds__(64) m3_scan(M3Args p, long npairs) {
-    const int lane = threadIdx.x;
+__global__ void __launch_bounds__(64 * kM3ScanW) m3_scan(M3Args p, long npairs) {
+    __shared__ float wmap[kM3ScanW][6];          // each wave's total map (P, v)
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const long b = blockIdx.x / npairs, pi = blockIdx.x % npairs;
     const long n0 = 2 * pi, n1 = n0 + 1;
     const bool pair = n1 < p.N;
     const float th = pair ? p.theta[pi] : 0.f;
     const float cs = pair ? cosf(th) : 1.f, sn = pair ? sinf(th) : 0.f;
     const long L = p.L, N = p.N;
-    const long CH = (L + 63) / 64;
-    const long l0 = lane * CH, l1 = min(l0 + CH, L);
+    const long CH = (L + 64 * kM3ScanW - 1) / (64 * kM3ScanW);
+    const long l0 = tid * CH, l1 = min(l0 + CH, L);
     const float *ab = p.a + b * L * N, *cb = p.c + b * L * N;
 
     // (1) chunk map: P (2x2) and v, composed step by step from identity / 0.
@@ -310,7 +314,8 @@ __global__ void __launch_bounds__(64) m3_scan(M3Args p, long npairs) {
         P00 = q00; P01 = q01; P10 = q10; P11 = q11;
         m3_step(a0, a1, cs, sn, pair, c0, c1, v0, v1);
     }
-    // (2) inclusive scan over lanes: (P, v) <- (P, v) o (P', v') of lane - d.
+    // (2) inclusive scan over the wave's lanes: (P, v) <- (P, v) o (P', v')
+    // of lane - d; then the waves' totals.
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
         const float e00 = __shfl_up(P00, d), e01 = __shfl_up(P01, d);
@@ -324,9 +329,29 @@ __global__ void __launch_bounds__(64) m3_scan(M3Args p, long npairs) {
             v0 = nv0; v1 = nv1;
         }
     }
-    // (3) replay from the state after the previous chunk (zero for chunk 0).
-    float h0 = __shfl_up(v0, 1), h1 = __shfl_up(v1, 1);
-    if (lane == 0) h0 = h1 = 0.f;
+    if (lane == 63) {
+        wmap[w][0] = P00; wmap[w][1] = P01; wmap[w][2] = P10; wmap[w][3] = P11;
+        wmap[w][4] = v0; wmap[w][5] = v1;
+    }
+    __syncthreads();
+    // State entering this wave: the earlier waves' maps applied in order to 0.
+    float V0 = 0.f, V1 = 0.f;
+    for (int u = 0; u < w; ++u) {
+        const float n0v = wmap[u][0] * V0 + wmap[u][1] * V1 + wmap[u][4];
+        const float n1v = wmap[u][2] * V0 + wmap[u][3] * V1 + wmap[u][5];
+        V0 = n0v;
+        V1 = n1v;
+    }
+    // (3) replay from the state after the previous chunk: lane k > 0 of the
+    // wave starts from lane k-1's inclusive map applied to V.
+    const float e00 = __shfl_up(P00, 1), e01 = __shfl_up(P01, 1);
+    const float e10 = __shfl_up(P10, 1), e11 = __shfl_up(P11, 1);
+    const float w0 = __shfl_up(v0, 1), w1 = __shfl_up(v1, 1);
+    float h0 = V0, h1 = V1;
+    if (lane > 0) {
+        h0 = e00 * V0 + e01 * V1 + w0;
+        h1 = e10 * V0 + e11 * V1 + w1;
+    }
     float *Hb = p.H + b * L * N;
     for (long l = l0; l < l1; ++l) {
         const float a0 = ab[l * N + n0], c0 = cb[l * N + n0];
@@ -410,8 +435,8 @@ int mamba3_launch(M3Args &a, hipStream_t s) {
     }
     hipLaunchKernelGGL(m3_prep, dim3(grid256(a.T * a.N)), dim3(256), 0, s, a);
     const long npairs = (a.N + 1) / 2;
-    const long waves = (a.T / a.L) * npairs;          // one per (batch element, pair)
-    hipLaunchKernelGGL(m3_scan, dim3(static_cast<unsigned>(waves)), dim3(64), 0, s, a, npairs);
+    const long waves = (a.T / a.L) * npairs;          // workgroups: one per (batch element, pair)
+    hipLaunchKernelGGL(m3_scan, dim3(static_cast<unsigned>(waves)), dim3(64 * kM3ScanW), 0, s, a, npairs);
     hipLaunchKernelGGL(m3_readout, dim3(grid256(a.T * a.R)), dim3(256), 0, s, a);
     const bool al16 = ((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.out)) & 15) == 0;
     if (a.D % 4 == 0 && al16) {
