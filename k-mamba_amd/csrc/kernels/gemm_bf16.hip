@@ -15,6 +15,7 @@
 // through raw buffer resources: rows past M (or N) read as zero, and the K
 // tail is masked per 16-byte chunk (K must be a multiple of 8).
 #include <algorithm>
+#include <cstdlib>
 
 #include "km_device.hpp"
 #include "../km_runtime.hpp"
@@ -207,115 +208,8 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_mfma(GemmArgs p) {
 // accumulators per lane, one wave per SIMD). Per 16-wide k step a wave reads
 // 4 A and 4 B fragments (8 KB of LDS) for 16 MFMAs, half the LDS bytes per
 // MFMA of the 64 x 64 wave tile above, so the LDS keeps up with the matrix
-// cores. K advances in stages of 64, double-buffered; LDS rows are padded to
-// nine 16-byte chunks, so the 16 rows one quarter-wave reads fall on 16
-// different chunk slots of a 256-byte bank line. The K tail is masked per
-// 16-byte chunk through an out-of-range offset.
-constexpr int kGM = 256, kGN = 256, kGK = 64, kGRow = 9;   // chunks per LDS row (8 + 1 pad)
-
-template <int EPI, bool CBF16>
-__global__ void __launch_bounds__(256, 1) gemm_bf16_mfma_256(GemmArgs p) {
-    __shared__ u32x4 sA[2][kGM * kGRow];
-    __shared__ u32x4 sB[2][kGN * kGRow];
-    constexpr unsigned kDrop = 0x80000000u;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = w >> 1, wn = w & 1;
-    long mb, nb;
-    xcd_tile(mb, nb);                  // tiles of one row block share an XCD's L2
-    const long m0 = mb * kGM;
-    const long n0 = nb * kGN;
-    const long arows = std::min<long>(kGM, p.M - m0), brows = std::min<long>(kGN, p.N - n0);
-    // Rows past the window read 0 (range check); the launcher keeps offsets
-    // below 2 GiB.
-    const auto rA = make_rsrc(p.A + m0 * p.lda, (arows - 1) * p.lda * 2 + p.K * 2);
-    const auto rB = make_rsrc(p.B + n0 * p.ldb, (brows - 1) * p.ldb * 2 + p.K * 2);
-
-    // A stage is 256 rows x 64 k = 8 chunks of 16 B per row; thread i loads
-    // chunks i, i + 256, ... (row c >> 3, chunk c & 7) of A and of B.
-    u32x4 ga[8], gb[8];
-    auto gload = [&](long k0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int c = tid + i * 256;
-            const int row = c >> 3, ch = c & 7;
-            const long k = k0 + ch * 8;
-            const bool kin = k < p.K;
-            const int offa = static_cast<int>(kin ? static_cast<unsigned>((row * p.lda + k) * 2) : kDrop);
-            const int offb = static_cast<int>(kin ? static_cast<unsigned>((row * p.ldb + k) * 2) : kDrop);
-            ga[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rA, offa, 0, 0));
-            gb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rB, offb, 0, 0));
-        }
-    };
-    auto sstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int c = tid + i * 256;
-            const int row = c >> 3, ch = c & 7;
-            sA[buf][row * kGRow + ch] = ga[i];
-            sB[buf][row * kGRow + ch] = gb[i];
-        }
-    };
-
-    f32x16 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-    const long nk = (p.K + kGK - 1) / kGK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    const int fr = lane & 31;
-    const int fk = lane >> 5;
-    auto frag = [&](int buf, int kk, bf16x8 (&af)[4], bf16x8 (&bfr)[4]) {
-        const int ch = kk * 2 + fk;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            af[i] = __builtin_bit_cast(bf16x8, sA[buf][(wm * 128 + i * 32 + fr) * kGRow + ch]);
-            bfr[i] = __builtin_bit_cast(bf16x8, sB[buf][(wn * 128 + i * 32 + fr) * kGRow + ch]);
-        }
-    };
-    for (long kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        gload((kt + 1) * kGK);           // past K: every chunk masked, unused
-        // Fragments of the stage's first 16-wide k step, read with the global
-        // loads ahead of the MFMAs (the scheduler would otherwise sink the
-        // loads to their LDS store and wait for them at once); each later
-        // step's fragments are read while the previous step's MFMAs run.
-        bf16x8 a0[4], b0[4], a1[4], b1[4];
-        frag(buf, 0, a0, b0);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int kk = 0; kk < 4; kk += 2) {
-            frag(buf, kk + 1, a1, b1);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[i], b0[j], acc[i][j], 0, 0, 0);
-            if (kk + 2 < 4) frag(buf, kk + 2, a0, b0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[i], b1[j], acc[i][j], 0, 0, 0);
-        }
-        // ... and the LDS store (which waits for the global loads) after them.
-        __builtin_amdgcn_sched_barrier(0);
-        sstore(buf ^ 1);
-        __syncthreads();
-    }
-
-    char *lds = (w < 2 ? reinterpret_cast<char *>(&sA[0][0]) : reinterpret_cast<char *>(&sB[0][0])) +
-                (w & 1) * 16384;
-    store_wave_tile<EPI, CBF16, 4, 4>(p, acc, m0 + wm * 128, n0 + wn * 128, lds, lane);
-}
-
+// cores.
+constexpr int kGM = 256, kGN = 256, kGK = 32;   // rows, columns, k per stage
 
 // Skinny shapes (N <= 128 with a long K, or K <= 64): MFMA operands come
 // from global memory straight into registers, with no LDS staging and no
@@ -415,11 +309,120 @@ __global__ void __launch_bounds__(256) gemm_bf16_direct(GemmArgs p) {
     store_wave_tile<EPI, CBF16, 1, TN>(p, acc, m0, n0, stage[KSPLIT > 1 ? 0 : w], lane);
 }
 
+// The 256x256 tile with operands loaded straight into LDS (gfx950
+// buffer_load_dwordx4 ... lds): no staging registers, so stages of 32 k run
+// three ahead through four LDS buffers (separate arrays, which lets the
+// compiler's wait counts track each buffer's loads apart). A stage of A (or
+// B) is 256 rows x 4 chunks of 16 B; load instruction i of wave w fills LDS
+// slots [64 (4w + i), +64), lane l slot 64 (4w + i) + l = row * 4 + pc,
+// holding chunk c = pc ^ ((row >> 2) & 3) of its row: the 16 rows a
+// quarter-wave's fragment read touches land on 16 distinct 16-byte bank
+// slots. Per stage each wave waits for its own loads of the stage, then one
+// barrier makes every wave's loads visible and frees the buffer read two
+// stages back for the next load.
+template <int EPI, bool CBF16>
+__global__ void __launch_bounds__(256, 1) gemm_bf16_mfma_256d(GemmArgs p) {
+    __shared__ u32x4 sA0[kGM * 4], sA1[kGM * 4], sA2[kGM * 4], sA3[kGM * 4];
+    __shared__ u32x4 sB0[kGN * 4], sB1[kGN * 4], sB2[kGN * 4], sB3[kGN * 4];
+    constexpr unsigned kDrop = 0x80000000u;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = w >> 1, wn = w & 1;
+    long mb, nb;
+    xcd_tile(mb, nb);                  // tiles of one row block share an XCD's L2
+    const long m0 = mb * kGM;
+    const long n0 = nb * kGN;
+    const long arows = std::min<long>(kGM, p.M - m0), brows = std::min<long>(kGN, p.N - n0);
+    const auto rA = make_rsrc(p.A + m0 * p.lda, (arows - 1) * p.lda * 2 + p.K * 2);
+    const auto rB = make_rsrc(p.B + n0 * p.ldb, (brows - 1) * p.ldb * 2 + p.K * 2);
+    // Row and chunk of this lane in each of its 4 load instructions.
+    int arow_off[4], brow_off[4], chk[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int slot = (w * 4 + i) * 64 + lane;
+        const int row = slot >> 2, pc = slot & 3;
+        chk[i] = pc ^ ((row >> 2) & 3);
+        arow_off[i] = static_cast<int>(row * p.lda * 2);
+        brow_off[i] = static_cast<int>(row * p.ldb * 2);
+    }
+    using lds_t = __attribute__((address_space(3))) void *;
+    auto dma = [&](long kt, u32x4 *dA, u32x4 *dB) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const long k = kt * kGK + chk[i] * 8;
+            const bool kin = k < p.K;
+            const unsigned oa = kin ? static_cast<unsigned>(arow_off[i] + k * 2) : kDrop;
+            const unsigned ob = kin ? static_cast<unsigned>(brow_off[i] + k * 2) : kDrop;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_t)(dA + (w * 4 + i) * 64), 16, oa, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_t)(dB + (w * 4 + i) * 64), 16, ob, 0, 0, 0);
+        }
+    };
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    const int fr = lane & 31, fk = lane >> 5;
+    auto frag = [&](const u32x4 *bA, const u32x4 *bB, int kk, bf16x8 (&af)[4], bf16x8 (&bfr)[4])
+        __attribute__((always_inline)) {
+        const int c = kk * 2 + fk;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ra = wm * 128 + i * 32 + fr, rb = wn * 128 + i * 32 + fr;
+            af[i] = __builtin_bit_cast(bf16x8, bA[ra * 4 + (c ^ ((ra >> 2) & 3))]);
+            bfr[i] = __builtin_bit_cast(bf16x8, bB[rb * 4 + (c ^ ((rb >> 2) & 3))]);
+        }
+    };
+    // Stage kt from (bA, bB); the loads of stage kt + 3 go to (nA, nB).
+    auto stage = [&](long kt, const u32x4 *bA, const u32x4 *bB, u32x4 *nA, u32x4 *nB)
+        __attribute__((always_inline)) {
+        __builtin_amdgcn_s_waitcnt(0x4F70 | 0x0000);   // vmcnt(16): this wave's loads of stage kt done
+        __builtin_amdgcn_s_barrier();                    // ... and every wave's
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        __builtin_amdgcn_sched_barrier(0);
+        dma(kt + 3, nA, nB);
+        bf16x8 a0[4], b0[4], a1[4], b1[4];
+        frag(bA, bB, 0, a0, b0);
+        frag(bA, bB, 1, a1, b1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[i], b0[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[i], b1[j], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    const long nk = (p.K + kGK - 1) / kGK;
+    dma(0, sA0, sB0);
+    dma(1, sA1, sB1);
+    dma(2, sA2, sB2);
+    // Groups of four stages with no branch inside (a branch would make the
+    // compiler's wait-count merge wait for every load in flight): stages past
+    // K load zeros and add nothing.
+    for (long kt = 0; kt < nk; kt += 4) {
+        stage(kt, sA0, sB0, sA3, sB3);
+        stage(kt + 1, sA1, sB1, sA0, sB0);
+        stage(kt + 2, sA2, sB2, sA1, sB1);
+        stage(kt + 3, sA3, sB3, sA2, sB2);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    char *lds = reinterpret_cast<char *>(w == 0 ? sA0 : w == 1 ? sA1 : w == 2 ? sA2 : sA3);
+    store_wave_tile<EPI, CBF16, 4, 4>(p, acc, m0 + wm * 128, n0 + wn * 128, lds, lane);
+}
+
 template <int EPI>
 static void gemm_go(const GemmArgs &a, dim3 g, bool big, hipStream_t s) {
     if (big) {
-        if (a.c_bf16) hipLaunchKernelGGL((gemm_bf16_mfma_256<EPI, true>), g, dim3(256), 0, s, a);
-        else          hipLaunchKernelGGL((gemm_bf16_mfma_256<EPI, false>), g, dim3(256), 0, s, a);
+        if (a.c_bf16) hipLaunchKernelGGL((gemm_bf16_mfma_256d<EPI, true>), g, dim3(256), 0, s, a);
+        else          hipLaunchKernelGGL((gemm_bf16_mfma_256d<EPI, false>), g, dim3(256), 0, s, a);
     } else {
         if (a.c_bf16) hipLaunchKernelGGL((gemm_bf16_mfma<EPI, true>), g, dim3(256), 0, s, a);
         else          hipLaunchKernelGGL((gemm_bf16_mfma<EPI, false>), g, dim3(256), 0, s, a);

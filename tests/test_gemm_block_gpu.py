@@ -42,7 +42,9 @@ def f32(a):
                                     # direct-operand kernel: N <= 128 with K >= 512 (k split
                                     # over 4 waves, ragged M and K), and K <= 64
                                     (517, 128, 512), (33, 64, 1000), (77, 20, 4104), (1, 128, 512),
-                                    (200, 300, 24), (259, 129, 40)])
+                                    (200, 300, 24), (259, 129, 40),
+                                    # 256x256 tiles with a K tail inside a 32-k stage
+                                    (300, 260, 136), (512, 257, 1000)])
 @pytest.mark.parametrize("out_bf16", [False, True])
 def test_gemm_vs_float64(M, N, Kd, out_bf16):
     g = rng_for("gemm", M, N, Kd)
