@@ -317,9 +317,9 @@ __global__ void __launch_bounds__(256) gemm_bf16_direct(GemmArgs p) {
 // slots [64 (4w + i), +64), lane l slot 64 (4w + i) + l = row * 4 + pc,
 // holding chunk c = pc ^ ((row >> 2) & 3) of its row: the 16 rows a
 // quarter-wave's fragment read touches land on 16 distinct 16-byte bank
-// slots. Per stage each wave waits for its own loads of the stage, then one
-// barrier makes every wave's loads visible and frees the buffer read two
-// stages back for the next load.
+// slots. Per stage each wave waits for its own loads of the next stage, then
+// one barrier makes every wave's loads visible and frees the buffer read in
+// the previous stage for the next load.
 template <int EPI, bool CBF16>
 __global__ void __launch_bounds__(256, 1) gemm_bf16_mfma_256d(GemmArgs p) {
     __shared__ u32x4 sA0[kGM * 4], sA1[kGM * 4], sA2[kGM * 4], sA3[kGM * 4];
@@ -376,22 +376,26 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_mfma_256d(GemmArgs p) {
             bfr[i] = __builtin_bit_cast(bf16x8, bB[rb * 4 + (c ^ ((rb >> 2) & 3))]);
         }
     };
-    // Stage kt from (bA, bB); the loads of stage kt + 3 go to (nA, nB).
-    auto stage = [&](long kt, const u32x4 *bA, const u32x4 *bB, u32x4 *nA, u32x4 *nB)
-        __attribute__((always_inline)) {
-        __builtin_amdgcn_s_waitcnt(0x4F70 | 0x0000);   // vmcnt(16): this wave's loads of stage kt done
+    // Stage kt from (bA, bB) while its loads of stage kt + 3 go to (nA, nB).
+    // Its barrier covers stage kt + 1's loads, so the first fragments of
+    // stage kt + 1 (xA, xB) are read while stage kt's MFMAs run; (ra0, rb0)
+    // carry them across. Loads run two to three stages ahead.
+    bf16x8 ra0[4], rb0[4];
+    auto stage_ra = [&](long kt, const u32x4 *bA, const u32x4 *bB, const u32x4 *xA, const u32x4 *xB,
+                        u32x4 *nA, u32x4 *nB) __attribute__((always_inline)) {
+        __builtin_amdgcn_s_waitcnt(0x0F78);              // vmcnt(8): this wave's loads of stage kt + 1 done
         __builtin_amdgcn_s_barrier();                    // ... and every wave's
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         __builtin_amdgcn_sched_barrier(0);
         dma(kt + 3, nA, nB);
-        bf16x8 a0[4], b0[4], a1[4], b1[4];
-        frag(bA, bB, 0, a0, b0);
+        bf16x8 a1[4], b1[4];
         frag(bA, bB, 1, a1, b1);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[i], b0[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ra0[i], rb0[j], acc[i][j], 0, 0, 0);
+        frag(xA, xB, 0, ra0, rb0);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -406,11 +410,15 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_mfma_256d(GemmArgs p) {
     // Groups of four stages with no branch inside (a branch would make the
     // compiler's wait-count merge wait for every load in flight): stages past
     // K load zeros and add nothing.
+    __builtin_amdgcn_s_waitcnt(0x4F70);                  // vmcnt(16): stage 0 loaded
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    frag(sA0, sB0, 0, ra0, rb0);
     for (long kt = 0; kt < nk; kt += 4) {
-        stage(kt, sA0, sB0, sA3, sB3);
-        stage(kt + 1, sA1, sB1, sA0, sB0);
-        stage(kt + 2, sA2, sB2, sA1, sB1);
-        stage(kt + 3, sA3, sB3, sA2, sB2);
+        stage_ra(kt, sA0, sB0, sA1, sB1, sA3, sB3);
+        stage_ra(kt + 1, sA1, sB1, sA2, sB2, sA0, sB0);
+        stage_ra(kt + 2, sA2, sB2, sA3, sB3, sA1, sB1);
+        stage_ra(kt + 3, sA3, sB3, sA0, sB0, sA2, sB2);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
