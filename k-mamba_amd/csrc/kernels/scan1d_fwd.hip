@@ -164,6 +164,12 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     const int nit = (L + SC - 1) / SC;
     const bool store_y = dvalid && ns == 0;
     const float dsk = (GATE && p.Dskip) ? p.Dskip[dvalid ? d : p.D - 1] : 0.f;
+    // Gated output with two state halves per channel: both halves hold the
+    // step's full readout, so they gate alternate steps (half ns takes steps
+    // 2i + ns) and each loads only its own steps' z: one SiLU per two steps
+    // and one 64-lane store per step pair.
+    constexpr bool PAIRG = GATE && NS == 2 && TC % 2 == 0;
+    constexpr int ZC = GATE ? (PAIRG ? TC / 2 : TC) : 1;
 
     // Per-batch-element windows addressed with 32-bit byte offsets (the
     // launcher keeps every window and offset below 1 GiB). Every variable
@@ -189,6 +195,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     // window, which the range check drops: the stores need no branch.
     constexpr unsigned kDrop = 0x80000000u;
     const unsigned vy = store_y ? static_cast<unsigned>(vx) : kDrop;
+    const unsigned vy2 = dvalid ? static_cast<unsigned>(vx + ns * Dm * TS) : kDrop;   // paired gating
     const unsigned vhs = dvalid ? static_cast<unsigned>(vh) : kDrop;
 
     __shared__ float sB[SHARED ? 3 : 1][SHARED ? TILE : 1];
@@ -249,13 +256,18 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             }
         }
     };
-    auto load_xd = [&](int s, float (&xo)[TC], float (&dto)[TC], float (&zo)[GATE ? TC : 1]) {
+    auto load_xd = [&](int s, float (&xo)[TC], float (&dto)[TC], float (&zo)[ZC]) {
 #pragma unroll
         for (int k = 0; k < TC; ++k) {
             const int so = (s * SC + w * TC + k) * rowx;   // rows past L read as 0
             xo[k] = IO::ld(rx, vx + so, 0);
             dto[k] = IO::ld(rdt, vx + so, 0);
-            if constexpr (GATE) zo[k] = IO::ld(rz, vx + so, 0);   // 0 when z is null
+            // z is 0 when null; with paired gating, step 2i + ns of this half.
+            if constexpr (PAIRG) {
+                if (k % 2 == 0) zo[k / 2] = IO::ld(rz, vx + ns * rowx + so, 0);
+            } else if constexpr (GATE) {
+                zo[k] = IO::ld(rz, vx + so, 0);
+            }
         }
     };
     auto bc_row = [&](const float (*tile)[SHARED ? TILE : 1], __amdgpu_buffer_rsrc_t r, int slot,
@@ -281,7 +293,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
         load_tile(1);
     }
     float X0[TC], D0[TC], X1[TC], D1[TC];
-    float Z0[GATE ? TC : 1], Z1[GATE ? TC : 1];
+    float Z0[ZC], Z1[ZC];
     load_xd(0, X0, D0, Z0);
     __syncthreads();
 
@@ -291,8 +303,8 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
 
     // FASTC selects the structured-decay form at compile time, so each body
     // is straight-line code the scheduler can interleave across steps.
-    auto body = [&](auto fastc, int s, float (&xs)[TC], float (&ds)[TC], float (&zs)[GATE ? TC : 1],
-                    float (&xn)[TC], float (&dn)[TC], float (&zn)[GATE ? TC : 1]) __attribute__((always_inline)) {
+    auto body = [&](auto fastc, int s, float (&xs)[TC], float (&ds)[TC], float (&zs)[ZC],
+                    float (&xn)[TC], float (&dn)[TC], float (&zn)[ZC]) __attribute__((always_inline)) {
         constexpr bool FAST = decltype(fastc)::value;
         const int cur = s & 1;
         const int slot = s % 3;
@@ -376,6 +388,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
         // Replay from the exact incoming state; B/C rows of step k+1 are read
         // while step k computes.
         float bvn[NPL], cvn[NPL];
+        float yprev = 0.f;
         if constexpr (!STORE_BU) bc_row(sB, rB, slot, s, 0, bvn);
         bc_row(sC, rC, slot, s, 0, cvn);
 #pragma unroll
@@ -405,9 +418,20 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             if constexpr (NS >= 2) yp = sum_xor32(yp);
             nan_seen |= (yp != yp);
             // Rows past L and lanes without output are dropped by the range check.
-            const int yo = static_cast<int>(vy + static_cast<unsigned>(t * rowx));
-            if constexpr (GATE) IO::st(ry, yo, 0, gated<T>(p, yp, xs[k], dsk, zs[k]));
-            else IO::st(ry, yo, 0, yp);
+            if constexpr (PAIRG) {
+                if (k % 2 == 0) {
+                    yprev = yp;
+                } else {
+                    const float yv = ns ? yp : yprev;
+                    const float xv = ns ? xs[k] : xs[k - 1];
+                    const int yo = static_cast<int>(vy2 + static_cast<unsigned>((t - 1) * rowx));
+                    IO::st(ry, yo, 0, gated<T>(p, yv, xv, dsk, zs[k / 2]));
+                }
+            } else {
+                const int yo = static_cast<int>(vy + static_cast<unsigned>(t * rowx));
+                if constexpr (GATE) IO::st(ry, yo, 0, gated<T>(p, yp, xs[k], dsk, zs[k]));
+                else IO::st(ry, yo, 0, yp);
+            }
             if constexpr (HIST) {
 #pragma unroll
                 for (int j = 0; j < NPL; ++j)

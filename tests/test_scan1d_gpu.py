@@ -13,7 +13,7 @@ import pytest
 import kmamba as K
 import oracle as O
 from kmtest import (TOL_BF16, TOL_F32, assert_close, bf16_round, rel_err, rel_err_cond, rng_for,
-                    scan1d_inputs, scan1d_kappa)
+                    scan1d_inputs, scan1d_kappa, silu_ref)
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -32,7 +32,8 @@ def T(a, dtype=torch.float32):
     return torch.from_numpy(np.ascontiguousarray(a)).to(DEV, dtype)
 
 
-def run_km(x, dt, A, Bm, Cm, *, h0=None, hist=False, bc_strides=None, clamp=True, bf16=False):
+def run_km(x, dt, A, Bm, Cm, *, h0=None, hist=False, bc_strides=None, clamp=True, bf16=False,
+           z=None, Dskip=None):
     Bsz, L, D = x.shape
     N = A.shape[1]
     io = torch.bfloat16 if bf16 else torch.float32
@@ -42,8 +43,10 @@ def run_km(x, dt, A, Bm, Cm, *, h0=None, hist=False, bc_strides=None, clamp=True
     th0 = None if h0 is None else T(h0)
     hf = torch.empty((Bsz, D, N), device=DEV)
     hh = torch.empty((Bsz, L, D, N), device=DEV) if hist else None
+    tz = None if z is None else T(z, io)
+    tD = None if Dskip is None else T(Dskip)
     K.scan1d_fwd(tx, tdt, tA, tB, tC, y, h0=th0, h_final=hf, h_hist=hh, bc_strides=bc_strides,
-                 clamp=clamp)
+                 clamp=clamp, z=tz, Dskip=tD)
     torch.cuda.synchronize()
     return (y.float().cpu().numpy(), hf.cpu().numpy(), None if hh is None else hh.cpu().numpy())
 
@@ -109,6 +112,40 @@ def test_clamp_fallback_follows_per_step_clamp():
     yu, _, hhu = O.scan1d_batched(x, dt, A, Bm, Cm, hist=True, clamp=False)
     assert np.abs(hh2).max() > 1000.0
     assert_close(hh2, hhu, TOL_F32, "unclamped h", khh)
+
+
+GATED = [(2, 1, 32, 16), (1, 63, 33, 16), (2, 131, 70, 16), (1, 77, 100, 8), (2, 65, 64, 4),
+         (1, 200, 96, 2)]
+
+
+@pytest.mark.parametrize("Bsz,L,D,N", GATED)
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+@pytest.mark.parametrize("parts", ["z+Dskip", "z", "Dskip"])
+def test_gated_output(Bsz, L, D, N, bf16, parts):
+    # y = (sum_n C*h + Dskip*x) * SiLU(z), the Mamba-1 output gating fused into
+    # the store. Odd L leaves a step pair across the end of the sequence;
+    # D not a multiple of 32 leaves lanes without a channel.
+    x, dt, A, Bm, Cm = scan1d_inputs(Bsz, L, D, N, seed=7)
+    g = rng_for("gated", Bsz, L, D, N)
+    z = (2.0 * g.standard_normal((Bsz, L, D))).astype(np.float32) if "z" in parts else None
+    Dsk = g.uniform(0.5, 1.5, D).astype(np.float32) if "Dskip" in parts else None
+    rnd = bf16_round if bf16 else (lambda a: a)
+    xr, dtr, Br, Cr = rnd(x), rnd(dt), rnd(Bm), rnd(Cm)
+    yr, hr, _ = O.scan1d_batched(xr, dtr, A, Br, Cr)
+    ky, kh, _ = scan1d_kappa(xr, dtr, A, Br, Cr)
+    ref, kap = yr.copy(), ky.copy()
+    if Dsk is not None:
+        ref = ref + Dsk * xr
+        kap = kap + np.abs(Dsk * xr)
+    if z is not None:
+        sz = silu_ref(rnd(z))
+        ref, kap = ref * sz, kap * np.abs(sz)
+    y, hf, _ = run_km(x, dt, A, Bm, Cm, bf16=bf16, z=z, Dskip=Dsk)
+    if bf16:
+        assert rel_err_cond(y, bf16_round(ref), kap) < 1e-2
+    else:
+        assert_close(y, ref, TOL_F32, "gated y", kap)
+    assert_close(hf, hr, TOL_BF16 if bf16 else TOL_F32, "h_final", kh)
 
 
 def test_bf16_io_against_fp32_oracle():
