@@ -152,6 +152,30 @@ def bench_mamba1_block(torch, K, stream, steps, warmup, Bsz=8, L=2048, dim=1024,
                        "dt_rank": R}}
 
 
+def bench_gemm_vs_library(torch, K, stream, steps, warmup):
+    """The block's two projection shapes (in_proj half: 16384 x 2048 x 1024,
+    out_proj: 16384 x 1024 x 2048) on km_gemm_bf16 and on torch.matmul
+    (hipBLASLt on ROCm), same bf16 operands (N(0,1) activations, N(0, 0.02)
+    weights: matrix-core throughput depends on the operand bits), bf16 out."""
+    g = torch.Generator(device="cuda").manual_seed(11)
+    out = {}
+    for name, (M, N, Kd) in {"in_proj_half": (16384, 2048, 1024),
+                             "out_proj": (16384, 1024, 2048)}.items():
+        A = torch.randn((M, Kd), device="cuda", generator=g).to(torch.bfloat16)
+        B = (torch.randn((N, Kd), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        C = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+        Bt = B.t()
+        pk, _ = time_launches(torch, stream, lambda: K.gemm_bf16(A, B, C, stream=stream), steps, warmup)
+        pl, _ = time_launches(torch, stream, lambda: torch.matmul(A, Bt, out=C), steps, warmup)
+        fl = 2.0 * M * N * Kd
+        mk, ml = sum(pk) / len(pk), sum(pl) / len(pl)
+        out[name] = {"M": M, "N": N, "K": Kd,
+                     "km_ms": round(mk, 4), "km_TFLOPs": round(fl / (mk * 1e-3) / 1e12, 1),
+                     "torch_matmul_ms": round(ml, 4),
+                     "torch_matmul_TFLOPs": round(fl / (ml * 1e-3) / 1e12, 1)}
+    return out
+
+
 def scannd_alg_bytes(dims, D, M):
     """Algorithmic bytes of one ScanND forward: x [P,D], delta [nd,P,D],
     A [nd,D,M], B and C [P,D,M] read; h [P,D,M] and y [P,D] written (fp32)."""
@@ -282,7 +306,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", choices=["all", "scan1d", "scan1d_bwd", "scannd", "convnd", "block",
-                                       "mamba3", "copy"],
+                                       "mamba3", "gemm", "copy"],
                     default="all",
                     help="profiling modes: scan1d = the fp32 headline kernel only; copy = a plain "
                          "1 GiB device copy (calibrates rocprof FETCH_SIZE/WRITE_SIZE)")
@@ -318,6 +342,11 @@ def main():
         with torch.cuda.stream(stream):
             r = bench_mamba1_block(torch, K, stream, args.steps, args.warmup)
         print(json.dumps({"mamba1_block_configs4": r}))
+        return
+    if args.only == "gemm":
+        with torch.cuda.stream(stream):
+            r = bench_gemm_vs_library(torch, K, stream, args.steps, min(args.warmup, 200))
+        print(json.dumps({"gemm_bf16_vs_torch_matmul": r}))
         return
     if args.only == "mamba3":
         print(json.dumps({"mamba3_block_fwd": bench_mamba3(torch, K, args.steps, min(args.warmup, 20))}))
