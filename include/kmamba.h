@@ -96,6 +96,98 @@ void mamba_block_init(MambaBlock *block);
  * km_last_error(). */
 void mamba_block_forward(MambaBlock *block, float *output, const float *input, size_t batch_size);
 
+/* ------------------------------------------------------------------------
+ * The stacked model (ref include/kmamba.h:159-223, src/kmamba.c): token
+ * embedding, n_layers Mamba-3 blocks, output head. Layouts are those of the
+ * reference's CPU build (no KMAMBA_BUILD_CUDA member). Parameters live in
+ * host memory as in the reference; the forward runs on the GPU. Training
+ * (kmamba_enable_training, kmamba_train_*) is not part of this library.
+ * ---------------------------------------------------------------------- */
+
+/* Optimizer settings (ref include/kmamba_kernels.h:78-85); kept for the
+ * KMamba layout. */
+typedef struct {
+    float lr;
+    float mu;
+    float beta2;
+    float eps;
+    float clip_norm;
+    float weight_decay;
+} MBOptimConfig;
+
+typedef struct {
+    size_t vocab_size;
+    size_t dim;
+    size_t state_size;
+    size_t seq_len;
+    size_t n_layers;
+    size_t mimo_rank;             /* 0 or 1: SISO */
+    float dt_scale;
+    float dt_min;
+    float dt_max;
+    long spatial_ndims;           /* 0: the implicit 1D shape [seq_len] */
+    long spatial_dims[KMAMBA_MAX_NDIMS];
+    int use_convnd;
+    long convnd_K;
+    long convnd_ndims;
+    int weight_tying;             /* 1: head shares the embedding's memory */
+} KMambaConfig;                               /* ref include/kmamba.h:159-183 */
+
+typedef struct {
+    KMambaConfig cfg;
+    float *embedding;             /* [vocab_size, dim] row-major */
+    float *head;                  /* [dim, vocab_size] row-major (the embedding when tied) */
+    MambaBlock **layers;          /* [n_layers] */
+    int for_training;
+    MBOptimConfig opt_blocks;
+    float lr_embed_head;
+    float weight_decay;
+    float *m_embedding;
+    float *v_embedding;
+    float *m_head;
+    float *v_head;
+    size_t step_embed_head;
+    float last_grad_norm;
+    float last_grad_over_clip;
+    int last_grad_would_clip;
+} KMamba;                                     /* ref include/kmamba.h:185-223 */
+
+/* Allocates a model (ref src/kmamba.c:102-152): NULL when vocab_size, dim,
+ * seq_len or n_layers is 0, the spatial topology is invalid, or memory
+ * runs out. Parameters start at zero. */
+KMamba *kmamba_create(const KMambaConfig *cfg);
+
+/* Frees a model and its blocks (ref src/kmamba.c:154-175). */
+void kmamba_free(KMamba *m);
+
+/* srand(seed), then Xavier-uniform embedding and (untied) head and the
+ * blocks' initialisation, in the reference's rand() order
+ * (ref src/kmamba.c:177-188). Returns 0, or -1 for NULL. */
+int kmamba_init(KMamba *m, uint32_t seed);
+
+/* Checkpoint version 4 (ref src/kmamba.c:216-294): an 80-byte header
+ * ("KMAMBA", version, sizes, dt range), the embedding, the head, then per
+ * layer W_in, W_out, A_log, W_B, W_C, b_B, b_C, delta_proj, lambda_proj,
+ * theta as raw fp32. Returns 0, or -1 (error in km_last_error()). */
+int kmamba_save(const KMamba *m, const char *path);
+
+/* Reads a checkpoint written by kmamba_save (versions <= 4; versions below
+ * 4 load as mimo_rank 1) into a new untied model (ref src/kmamba.c:296-342).
+ * for_training must be 0: training is not part of this library (NULL with
+ * an error otherwise); opt_blocks, lr_embed_head and weight_decay are then
+ * unused. NULL on a missing file, a bad header or a short read. */
+KMamba *kmamba_load(const char *path, int for_training, const MBOptimConfig *opt_blocks,
+                    float lr_embed_head, float weight_decay);
+
+/* Inference on one sequence (ref src/kmamba.c:344-372): tokens [seq_len]
+ * (ids >= vocab_size embed as zeros), logits_out [seq_len, vocab_size], both
+ * host memory; logits = h . head with h the last block's output. Clears the
+ * blocks' hidden and scan_h as the reference does. Runs on the GPU: the
+ * head is uploaded on every call, as the parameters are host-owned. Calls
+ * that overlap on one device race on the library's device workspace.
+ * Returns 0, or -1 (error in km_last_error()). */
+int kmamba_forward(KMamba *m, const uint32_t *tokens, float *logits_out);
+
 #ifdef __cplusplus
 }
 #endif

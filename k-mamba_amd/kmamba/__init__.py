@@ -135,6 +135,30 @@ class MambaBlock(C.Structure):            # ref include/kmamba.h:116-150
                                                    "scan_h")] + [("opt_state", C.c_void_p)]
 
 
+class KMambaConfig(C.Structure):          # ref include/kmamba.h:159-183
+    _fields_ = [(n, C.c_size_t) for n in ("vocab_size", "dim", "state_size", "seq_len",
+                                          "n_layers", "mimo_rank")] + \
+               [(n, C.c_float) for n in ("dt_scale", "dt_min", "dt_max")] + \
+               [("spatial_ndims", C.c_long), ("spatial_dims", C.c_long * 8),
+                ("use_convnd", C.c_int), ("convnd_K", C.c_long), ("convnd_ndims", C.c_long),
+                ("weight_tying", C.c_int)]
+
+
+class MBOptimConfig(C.Structure):         # ref include/kmamba_kernels.h:78-85
+    _fields_ = [(n, C.c_float) for n in ("lr", "mu", "beta2", "eps", "clip_norm", "weight_decay")]
+
+
+class KMamba(C.Structure):                # ref include/kmamba.h:185-223 (CPU build)
+    _fields_ = [("cfg", KMambaConfig), ("embedding", C.POINTER(C.c_float)),
+                ("head", C.POINTER(C.c_float)), ("layers", C.POINTER(C.POINTER(MambaBlock))),
+                ("for_training", C.c_int), ("opt_blocks", MBOptimConfig),
+                ("lr_embed_head", C.c_float), ("weight_decay", C.c_float)] + \
+               [(n, C.POINTER(C.c_float)) for n in ("m_embedding", "v_embedding", "m_head",
+                                                   "v_head")] + \
+               [("step_embed_head", C.c_size_t), ("last_grad_norm", C.c_float),
+                ("last_grad_over_clip", C.c_float), ("last_grad_would_clip", C.c_int)]
+
+
 VisitFn = C.CFUNCTYPE(C.c_int, c_long_p, C.c_long, C.c_long, C.c_long, C.c_void_p)
 
 
@@ -369,6 +393,16 @@ mamba_block_free = _decl("mamba_block_free", None, [C.POINTER(MambaBlock)])
 mamba_block_init = _decl("mamba_block_init", None, [C.POINTER(MambaBlock)])
 mamba_block_forward = _decl("mamba_block_forward", None,
                             [C.POINTER(MambaBlock), C.c_void_p, C.c_void_p, C.c_size_t])
+
+
+# --- The stacked model ----------------------------------------------------------
+kmamba_create = _decl("kmamba_create", C.POINTER(KMamba), [C.POINTER(KMambaConfig)])
+kmamba_free = _decl("kmamba_free", None, [C.POINTER(KMamba)])
+kmamba_init = _decl("kmamba_init", C.c_int, [C.POINTER(KMamba), C.c_uint32])
+kmamba_save = _decl("kmamba_save", C.c_int, [C.POINTER(KMamba), C.c_char_p])
+kmamba_load = _decl("kmamba_load", C.POINTER(KMamba),
+                    [C.c_char_p, C.c_int, C.POINTER(MBOptimConfig), C.c_float, C.c_float])
+kmamba_forward = _decl("kmamba_forward", C.c_int, [C.POINTER(KMamba), C.c_void_p, C.c_void_p])
 
 
 # --- ScanND / Scan2D ----------------------------------------------------------

@@ -745,3 +745,18 @@ out:
     free(z); free(u); free(dl); free(lam); free(Bs); free(Cs); free(y); free(yp);
     free(h); free(hr); free(bu); free(pbu);
 }
+
+/* ref kernels/gemm_f32.c:13-31; see kmoracle.h. */
+void orc_gemm_f32(const float *A, const float *B, float *C, long M, long K, long N) {
+    if (!A || !B || !C || M <= 0 || N <= 0) return;
+    #pragma omp parallel for schedule(static)
+    for (long i = 0; i < M; i++) {
+        float *c = C + i * N;
+        for (long j = 0; j < N; j++) c[j] = 0.0f;
+        for (long k = 0; k < K; k++) {
+            const float a = A[i * K + k];
+            const float *b = B + k * N;
+            for (long j = 0; j < N; j++) c[j] = c[j] + a * b[j];
+        }
+    }
+}

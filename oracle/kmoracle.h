@@ -107,6 +107,12 @@ typedef struct {
  * output [batch, L, D]. */
 void orc_mamba3_forward(const OrcMamba3 *p, const float *input, float *output, long batch);
 
+/* The reference's gemm_f32 (kernels/gemm_f32.c:13-31): C[M,N] = A[M,K] B[K,N]
+ * row-major, C zeroed, then C[i,j] += A[i,k] * B[k,j] with k ascending per
+ * element (two roundings per term, as the reference built without FMA
+ * contraction). Rows run in parallel; each element's order is fixed. */
+void orc_gemm_f32(const float *A, const float *B, float *C, long M, long K, long N);
+
 /* ---- Wavefront / plan / topology -------------------------------------- */
 int  orc_wavefront_validate_dims(const long *dims, long ndims);
 long orc_wavefront_total_points(const long *dims, long ndims);

@@ -385,6 +385,89 @@ if ref is not None:
     _sig(ref, "mamba_block_forward", None, [C.POINTER(MambaBlock), vp, vp, C.c_size_t])
 
 
+# ---------------------------------------------------------------------------
+# The stacked model: embedding, Mamba-3 blocks, head (src/kmamba.c)
+# ---------------------------------------------------------------------------
+class KMambaConfig(C.Structure):          # ref include/kmamba.h:159-183
+    _fields_ = [(n, C.c_size_t) for n in ("vocab_size", "dim", "state_size", "seq_len",
+                                          "n_layers", "mimo_rank")] + \
+               [(n, C.c_float) for n in ("dt_scale", "dt_min", "dt_max")] + \
+               [("spatial_ndims", C.c_long), ("spatial_dims", C.c_long * 8),
+                ("use_convnd", C.c_int), ("convnd_K", C.c_long), ("convnd_ndims", C.c_long),
+                ("weight_tying", C.c_int)]
+
+
+class MBOptimConfig(C.Structure):         # ref include/kmamba_kernels.h:78-85
+    _fields_ = [(n, C.c_float) for n in ("lr", "mu", "beta2", "eps", "clip_norm", "weight_decay")]
+
+
+class KMamba(C.Structure):                # ref include/kmamba.h:185-223 (CPU build)
+    _fields_ = [("cfg", KMambaConfig), ("embedding", C.POINTER(C.c_float)),
+                ("head", C.POINTER(C.c_float)), ("layers", C.POINTER(C.POINTER(MambaBlock))),
+                ("for_training", C.c_int), ("opt_blocks", MBOptimConfig),
+                ("lr_embed_head", C.c_float), ("weight_decay", C.c_float)] + \
+               [(n, C.POINTER(C.c_float)) for n in ("m_embedding", "v_embedding", "m_head",
+                                                   "v_head")] + \
+               [("step_embed_head", C.c_size_t), ("last_grad_norm", C.c_float),
+                ("last_grad_over_clip", C.c_float), ("last_grad_would_clip", C.c_int)]
+
+
+_sig(orc, "orc_gemm_f32", None, [vp, vp, vp, C.c_long, C.c_long, C.c_long])
+if ref is not None:
+    _sig(ref, "kmamba_create", C.POINTER(KMamba), [C.POINTER(KMambaConfig)])
+    _sig(ref, "kmamba_free", None, [C.POINTER(KMamba)])
+    _sig(ref, "kmamba_init", C.c_int, [C.POINTER(KMamba), C.c_uint32])
+    _sig(ref, "kmamba_forward", C.c_int, [C.POINTER(KMamba), vp, vp])
+    _sig(ref, "kmamba_save", C.c_int, [C.POINTER(KMamba), C.c_char_p])
+    _sig(ref, "kmamba_load", C.POINTER(KMamba), [C.c_char_p, C.c_int, vp, C.c_float, C.c_float])
+
+
+def kmamba_config(vocab, dim, N, L, n_layers, R=1, dt_scale=0.1, dt_min=1e-3, dt_max=0.1,
+                  weight_tying=0, cls=KMambaConfig):
+    cfg = cls()
+    cfg.vocab_size, cfg.dim, cfg.state_size, cfg.seq_len = vocab, dim, N, L
+    cfg.n_layers, cfg.mimo_rank = n_layers, R
+    cfg.dt_scale, cfg.dt_min, cfg.dt_max = dt_scale, dt_min, dt_max
+    cfg.weight_tying = weight_tying
+    return cfg
+
+
+def model_params(m):
+    """Copies of a KMamba's parameters: embedding [V, D], head [D, V] and one
+    block_params dict per layer (works on any library's KMamba pointer)."""
+    c = m.contents.cfg
+    V, D = c.vocab_size, c.dim
+    emb = np.ctypeslib.as_array(m.contents.embedding, shape=(V * D,)).reshape(V, D).copy()
+    head = np.ctypeslib.as_array(m.contents.head, shape=(D * V,)).reshape(D, V).copy()
+    layers = [block_params(C.cast(m.contents.layers[i], C.POINTER(MambaBlock)))
+              for i in range(c.n_layers)]
+    return emb, head, layers
+
+
+def gemm_f32(A, B):
+    """C = A . B in the reference gemm_f32's order (kernels/gemm_f32.c:13-31)."""
+    A, B = f32(A), f32(B)
+    M, K = A.shape
+    N = B.shape[1]
+    out = np.empty((M, N), np.float32)
+    orc.orc_gemm_f32(P(A), P(B), P(out), M, K, N)
+    return out
+
+
+def kmamba_forward(emb, head, layers, tokens, *, dt_scale=0.1, dt_min=1e-3, dt_max=0.1):
+    """The model forward of src/kmamba.c:344-372: embedding rows (ids past the
+    vocabulary embed as zeros, :85-98), the blocks in order, then h . head."""
+    emb, head = f32(emb), f32(head)
+    V = emb.shape[0]
+    tokens = np.asarray(tokens, dtype=np.int64)
+    x = np.zeros((1, tokens.size, emb.shape[1]), np.float32)
+    ok = tokens < V
+    x[0, ok] = emb[tokens[ok]]
+    for p in layers:
+        x = mamba3_forward(p, x, dt_scale=dt_scale, dt_min=dt_min, dt_max=dt_max)
+    return gemm_f32(x[0], head)
+
+
 def mb_config(dim, N, L, R=1, dt_scale=0.1, dt_min=1e-3, dt_max=0.1):
     cfg = MBConfig()
     cfg.dim, cfg.state_size, cfg.seq_len, cfg.mimo_rank = dim, N, L, R

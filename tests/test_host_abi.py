@@ -310,3 +310,119 @@ def test_mamba_block_create_rejects_bad_topology():
     assert not K.mamba_block_create(C.byref(cfg))
     assert "topology" in K.km_last_error()
     K.mamba_block_free(None)
+
+
+# ---------------------------------------------------------------------------
+# The stacked model: layout, create / init / save / load (host side)
+# ---------------------------------------------------------------------------
+REF_INC = Path("/root/reference/include")
+MODEL_STRUCTS = ("KMambaConfig", "MBOptimConfig", "KMamba")
+
+
+@pytest.mark.skipif(not (REF_INC / "kmamba.h").exists(), reason="reference headers absent")
+def test_kmamba_layout_matches_reference_header(tmp_path):
+    # Sizes and field offsets as gcc lays out the reference's own header
+    # (include/kmamba.h:159-223, include/kmamba_kernels.h:78-85, CPU build).
+    src = ['#include <stdio.h>', '#include <stddef.h>', '#include "kmamba.h"', 'int main(void) {']
+    for cls in MODEL_STRUCTS:
+        src.append(f'printf("{cls} %zu\\n", sizeof({cls}));')
+        for name, _ in getattr(K, cls)._fields_:
+            src.append(f'printf("{cls}.{name} %zu\\n", offsetof({cls}, {name}));')
+    src.append("return 0; }")
+    (tmp_path / "lay.c").write_text("\n".join(src) + "\n")
+    subprocess.run(["gcc", "-w", f"-I{REF_INC}", f"-I{REF_INC.parent / 'cpu' / 'include'}",
+                    str(tmp_path / "lay.c"), "-o", str(tmp_path / "lay")], check=True)
+    got = dict(line.rsplit(" ", 1) for line in
+               subprocess.run([str(tmp_path / "lay")], capture_output=True, text=True,
+                              check=True).stdout.split("\n") if line)
+    for cls in MODEL_STRUCTS:
+        ct = getattr(K, cls)
+        assert int(got[cls]) == C.sizeof(ct), cls
+        for name, _ in ct._fields_:
+            assert int(got[f"{cls}.{name}"]) == getattr(ct, name).offset, (cls, name)
+
+
+def _model_arrays(m):
+    return O.model_params(C.cast(m, C.POINTER(O.KMamba)))
+
+
+def _assert_same_params(pa, pb):
+    np.testing.assert_array_equal(pa[0], pb[0], err_msg="embedding")
+    np.testing.assert_array_equal(pa[1], pb[1], err_msg="head")
+    assert len(pa[2]) == len(pb[2])
+    for la, lb in zip(pa[2], pb[2]):
+        for k in la:
+            np.testing.assert_array_equal(la[k], lb[k], err_msg=k)
+
+
+@needs_ref
+@pytest.mark.parametrize("tying,R", [(0, 1), (1, 2), (0, 0)])
+def test_kmamba_checkpoint_matches_reference(tmp_path, tying, R):
+    # Same seed -> the same parameters (the reference's rand() order,
+    # src/kmamba.c:177-188) and byte-identical version-4 files
+    # (src/kmamba.c:241-294); each library reads the other's file.
+    args = (37, 12, 6, 9, 2)                       # vocab, dim, N, seq_len, layers
+    ours = K.kmamba_create(C.byref(O.kmamba_config(*args, R=R, weight_tying=tying,
+                                                   cls=K.KMambaConfig)))
+    theirs = O.ref.kmamba_create(C.byref(O.kmamba_config(*args, R=R, weight_tying=tying)))
+    assert ours and theirs
+    assert bool(tying) == (C.addressof(ours.contents.head.contents)
+                           == C.addressof(ours.contents.embedding.contents))
+    assert K.kmamba_init(ours, 77) == 0 and O.ref.kmamba_init(theirs, 77) == 0
+    _assert_same_params(_model_arrays(ours), O.model_params(theirs))
+    fa, fb = tmp_path / "ours.kmamba", tmp_path / "theirs.kmamba"
+    assert K.kmamba_save(ours, str(fa).encode()) == 0
+    assert O.ref.kmamba_save(theirs, str(fb).encode()) == 0
+    assert fa.read_bytes() == fb.read_bytes()
+    la = K.kmamba_load(str(fb).encode(), 0, None, 0.0, 0.0)
+    lb = O.ref.kmamba_load(str(fa).encode(), 0, None, 0.0, 0.0)
+    assert la and lb
+    assert la.contents.cfg.mimo_rank == lb.contents.cfg.mimo_rank == max(R, 1)
+    assert la.contents.cfg.weight_tying == lb.contents.cfg.weight_tying == 0
+    _assert_same_params(_model_arrays(la), O.model_params(lb))
+    _assert_same_params(_model_arrays(la), _model_arrays(ours))
+    for m in (ours, la):
+        K.kmamba_free(m)
+    for m in (theirs, lb):
+        O.ref.kmamba_free(m)
+
+
+def test_kmamba_create_and_load_errors(tmp_path):
+    zero = O.kmamba_config(0, 8, 4, 6, 1, cls=K.KMambaConfig)
+    assert not K.kmamba_create(C.byref(zero))
+    assert "non-zero" in K.km_last_error()
+    topo = O.kmamba_config(11, 8, 4, 6, 1, cls=K.KMambaConfig)
+    topo.spatial_ndims = 2
+    topo.spatial_dims[0], topo.spatial_dims[1] = 2, 2          # 4 != seq_len
+    assert not K.kmamba_create(C.byref(topo))
+    assert K.kmamba_init(None, 1) == -1
+    K.kmamba_free(None)
+    m = K.kmamba_create(C.byref(O.kmamba_config(11, 8, 4, 6, 2, R=2, cls=K.KMambaConfig)))
+    assert m and K.kmamba_init(m, 5) == 0
+    good = tmp_path / "m.kmamba"
+    assert K.kmamba_save(m, str(good).encode()) == 0
+    raw = good.read_bytes()
+    assert raw[:8] == b"KMAMBA\0\0" and int.from_bytes(raw[8:12], "little") == 4
+    assert not K.kmamba_load(str(tmp_path / "missing").encode(), 0, None, 0.0, 0.0)
+    cases = {"magic": b"KMAMBX" + raw[6:], "version5": raw[:8] + (5).to_bytes(4, "little") + raw[12:],
+             "truncated": raw[:-4], "header_only": raw[:80]}
+    for name, data in cases.items():
+        (tmp_path / name).write_bytes(data)
+        assert not K.kmamba_load(str(tmp_path / name).encode(), 0, None, 0.0, 0.0), name
+        assert K.km_last_error(), name
+    # Below version 4 the header's rank is ignored: the file loads as
+    # mimo_rank 1, reading rank-1 arrays and leaving the rest unread, as the
+    # reference does (src/kmamba.c:313, no trailing-data check).
+    v3 = tmp_path / "v3"
+    v3.write_bytes(raw[:8] + (3).to_bytes(4, "little") + raw[12:])
+    old = K.kmamba_load(str(v3).encode(), 0, None, 0.0, 0.0)
+    assert old and old.contents.cfg.mimo_rank == 1
+    K.kmamba_free(old)
+    opt = K.MBOptimConfig()
+    assert not K.kmamba_load(str(good).encode(), 1, C.byref(opt), 1e-3, 0.0)
+    assert "training" in K.km_last_error()
+    loaded = K.kmamba_load(str(good).encode(), 0, None, 0.0, 0.0)
+    assert loaded
+    _assert_same_params(_model_arrays(loaded), _model_arrays(m))
+    K.kmamba_free(loaded)
+    K.kmamba_free(m)

@@ -96,3 +96,67 @@ def test_forward_larger_model_sampled():
     want = O.mamba3_forward(p, x[:1], dt_min=0.01, dt_max=0.5)
     check(out[:1], want, x[:1])
     K.mamba_block_free(blk)
+
+
+# ---------------------------------------------------------------------------
+# The stacked model (kmamba_forward, ref src/kmamba.c:344-372)
+# ---------------------------------------------------------------------------
+def model_forward(m, toks):
+    c = m.contents.cfg
+    logits = np.full((c.seq_len, c.vocab_size), np.nan, np.float32)
+    assert K.kmamba_forward(m, toks.ctypes.data, logits.ctypes.data) == 0, K.km_last_error()
+    return logits
+
+
+@pytest.mark.parametrize("V,D,N,L,layers,R,tying", [
+    (37, 12, 6, 9, 2, 1, 0),          # ragged everything, below one head tile
+    (97, 64, 16, 130, 2, 1, 1),       # tied head, M spans three row tiles
+    (300, 40, 8, 77, 3, 2, 0),        # MIMO rank 2, N spans five column tiles
+    (4096, 256, 16, 512, 2, 1, 0),    # 16 K steps, 64 x 8 head tiles
+])
+def test_kmamba_forward_vs_oracle(V, D, N, L, layers, R, tying):
+    # Logits against the oracle's model forward (bit-exact to the compiled
+    # reference) on this model's own parameters. Metric: condition-scaled,
+    # max |got - ref| / (|h| . |head|) <= 1e-4 with h the oracle's last
+    # block output (the head's sums carry no cancellation in that scale).
+    m = K.kmamba_create(C.byref(O.kmamba_config(V, D, N, L, layers, R=R, weight_tying=tying,
+                                                cls=K.KMambaConfig)))
+    assert m, K.km_last_error()
+    assert K.kmamba_init(m, 11) == 0
+    toks = rng_for("kmgpu", V, L).integers(0, V + 3, L).astype(np.uint32)
+    got = model_forward(m, toks)
+    emb, head, blocks = O.model_params(C.cast(m, C.POINTER(O.KMamba)))
+    want = O.kmamba_forward(emb, head, blocks, toks)
+    x = np.zeros((1, L, D), np.float32)
+    ok = toks < V
+    x[0, ok] = emb[toks[ok]]
+    for p in blocks:
+        x = O.mamba3_forward(p, x)
+    kappa = np.abs(x[0]).astype(np.float64) @ np.abs(head).astype(np.float64)
+    err = float(np.max(np.abs(got.astype(np.float64) - want) / np.maximum(kappa, 1e-30)))
+    K.kmamba_free(m)
+    assert np.isfinite(got).all()
+    assert err <= 1e-4, f"condition-scaled logits error {err:.3e}"
+
+
+def test_kmamba_checkpoint_roundtrip_forward(tmp_path):
+    # A saved and reloaded model (untied on load) gives the same logits.
+    V, D, N, L = 200, 32, 8, 50
+    m = K.kmamba_create(C.byref(O.kmamba_config(V, D, N, L, 2, weight_tying=1, cls=K.KMambaConfig)))
+    assert m and K.kmamba_init(m, 4) == 0
+    toks = rng_for("kmrt", V, L).integers(0, V, L).astype(np.uint32)
+    a = model_forward(m, toks)
+    path = str(tmp_path / "m.kmamba").encode()
+    assert K.kmamba_save(m, path) == 0
+    m2 = K.kmamba_load(path, 0, None, 0.0, 0.0)
+    assert m2, K.km_last_error()
+    assert m2.contents.cfg.weight_tying == 0
+    b = model_forward(m2, toks)
+    np.testing.assert_array_equal(a, b)
+    # The blocks' hidden / scan_h are cleared by the forward (src/kmamba.c:351-354).
+    blk = m2.contents.layers[0].contents
+    assert not np.any(np.ctypeslib.as_array(blk.hidden, shape=(N,)))
+    assert K.kmamba_forward(m2, None, a.ctypes.data) == -1
+    assert "NULL" in K.km_last_error()
+    K.kmamba_free(m)
+    K.kmamba_free(m2)

@@ -480,6 +480,49 @@ def test_mamba3_forward_bit_exact_vs_reference(D, N, L, R, batch):
     np.testing.assert_array_equal(got, want)
 
 
+@needs_ref
+@pytest.mark.parametrize("V,D,N,L,layers,R,tying", [(37, 12, 6, 9, 2, 1, 0), (50, 16, 8, 20, 3, 2, 1),
+                                                    (10, 8, 4, 7, 1, 1, 0)])
+def test_kmamba_forward_bit_exact_vs_reference(V, D, N, L, layers, R, tying):
+    # src/kmamba.c:344-372 compiled in place, the reference initialising the
+    # model (kmamba_init); the oracle composes the embedding rows, its
+    # Mamba-3 blocks and its gemm_f32 on the same parameters. The reference
+    # runs on one OpenMP thread: its gemm_f32 updates a row of C from
+    # several threads at once (kernels/gemm_f32.c:22-29).
+    import ctypes as C
+    m = O.ref.kmamba_create(C.byref(O.kmamba_config(V, D, N, L, layers, R=R, weight_tying=tying)))
+    assert m and O.ref.kmamba_init(m, 3) == 0
+    toks = rng_for("kmtok", V, L).integers(0, V + 5, L).astype(np.uint32)   # a few past the vocabulary
+    assert (toks >= V).any() or L < 10
+    want = np.zeros((L, V), np.float32)
+    gomp = C.CDLL("libgomp.so.1")
+    prev = gomp.omp_get_max_threads()
+    gomp.omp_set_num_threads(1)
+    try:
+        assert O.ref.kmamba_forward(m, toks.ctypes.data, want.ctypes.data) == 0
+    finally:
+        gomp.omp_set_num_threads(prev)
+    emb, head, blocks = O.model_params(m)
+    got = O.kmamba_forward(emb, head, blocks, toks)
+    O.ref.kmamba_free(m)
+    np.testing.assert_array_equal(got, want)
+    assert np.abs(want).max() > 0
+
+
+def test_gemm_f32_matches_float64():
+    # The restated gemm_f32 against float64 products (k-ordered fp32 sums
+    # carry at most K roundings of the partial sums).
+    g = rng_for("gemmf32")
+    A = g.standard_normal((13, 40)).astype(np.float32)
+    B = g.standard_normal((40, 29)).astype(np.float32)
+    got = O.gemm_f32(A, B)
+    want = A.astype(np.float64) @ B.astype(np.float64)
+    scale = np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64)
+    assert np.max(np.abs(got - want) / scale) < 40 * 2.0 ** -24
+    # one nonzero term per element: exact
+    np.testing.assert_array_equal(O.gemm_f32(np.eye(5, dtype=np.float32), B[:5]), B[:5])
+
+
 def test_mamba3_forward_closed_forms():
     # With B = C = 0 (zero weights and biases) the state stays zero and the
     # block is the identity (the residual); with theta = 0, lambda = 1 and a
