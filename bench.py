@@ -176,6 +176,41 @@ def bench_gemm_vs_library(torch, K, stream, steps, warmup):
     return out
 
 
+def bench_model(K, steps, warmup, V=32768, D=1024, N=16, L=2048, n_layers=4):
+    """The stacked model's forward (kmamba_forward: embedding rows, n_layers
+    Mamba-3 blocks, head product; host tokens in, host logits out, the
+    head uploaded per call as its parameters are host-owned), wall clock per
+    call. Reports the head product's fp32 FLOP rate bound as well."""
+    import ctypes
+    import numpy as np
+    cfg = K.KMambaConfig()
+    cfg.vocab_size, cfg.dim, cfg.state_size, cfg.seq_len, cfg.n_layers = V, D, N, L, n_layers
+    cfg.mimo_rank, cfg.dt_scale, cfg.dt_min, cfg.dt_max = 1, 0.1, 1e-3, 0.1
+    m = K.kmamba_create(ctypes.byref(cfg))
+    if not m:
+        raise RuntimeError(K.km_last_error())
+    K.kmamba_init(m, 7)
+    toks = np.random.default_rng(7).integers(0, V, L).astype(np.uint32)
+    logits = np.empty((L, V), np.float32)
+    fn = lambda: K.kmamba_forward(m, toks.ctypes.data, logits.ctypes.data)  # noqa: E731
+    for _ in range(warmup):
+        fn()
+    t = time.perf_counter()
+    for _ in range(steps):
+        rc = fn()
+    ms = (time.perf_counter() - t) * 1e3 / steps
+    err = K.km_last_error() if rc else ""
+    K.kmamba_free(m)
+    if err:
+        raise RuntimeError(err)
+    return {"ms": round(ms, 3), "tokens_per_s": L / (ms * 1e-3),
+            "head_GFLOP": round(2.0 * L * D * V / 1e9, 1),
+            "host_bytes_per_call": {"head_up": 4 * D * V, "logits_down": 4 * L * V,
+                                    "embedding_rows_up": 4 * L * D},
+            "config": {"vocab": V, "dim": D, "state_size": N, "seq_len": L, "n_layers": n_layers,
+                       "io": "host tokens and logits"}}
+
+
 def scannd_alg_bytes(dims, D, M):
     """Algorithmic bytes of one ScanND forward: x [P,D], delta [nd,P,D],
     A [nd,D,M], B and C [P,D,M] read; h [P,D,M] and y [P,D] written (fp32)."""
@@ -306,7 +341,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", choices=["all", "scan1d", "scan1d_bwd", "scannd", "convnd", "block",
-                                       "mamba3", "gemm", "copy"],
+                                       "mamba3", "gemm", "model", "copy"],
                     default="all",
                     help="profiling modes: scan1d = the fp32 headline kernel only; copy = a plain "
                          "1 GiB device copy (calibrates rocprof FETCH_SIZE/WRITE_SIZE)")
@@ -342,6 +377,9 @@ def main():
         with torch.cuda.stream(stream):
             r = bench_mamba1_block(torch, K, stream, args.steps, args.warmup)
         print(json.dumps({"mamba1_block_configs4": r}))
+        return
+    if args.only == "model":
+        print(json.dumps({"kmamba_forward": bench_model(K, args.steps, min(args.warmup, 3))}))
         return
     if args.only == "gemm":
         with torch.cuda.stream(stream):
