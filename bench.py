@@ -278,7 +278,49 @@ def bench_scannd(torch, K, stream, dims, D, M, steps, warmup):
     return {"ms": round(ms, 4), "elems_per_s": P * D / (ms * 1e-3),
             "achieved_GBs": round(alg / (ms * 1e-3) / 1e9, 1),
             "frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "alg_bytes": alg,
-            "launches_per_step": "one per tile band"}
+            "launches_per_step": "one per tile band" if nd < 3 else "one dataflow launch"}
+
+
+def scannd_bwd_alg_bytes(dims, D, M):
+    """Algorithmic bytes of one ScanND backward: x, dy [P,D], delta [nd,P,D],
+    A [nd,D,M], B, C, h [P,D,M] read; dx [P,D], ddelta [nd,P,D], dA
+    [nd,D,M], dB, dC [P,D,M] written (fp32)."""
+    nd = len(dims)
+    P = 1
+    for v in dims:
+        P *= v
+    reads = 2 * P * D + nd * P * D + nd * D * M + 3 * P * D * M
+    writes = P * D + nd * P * D + nd * D * M + 2 * P * D * M
+    return 4 * (reads + writes)
+
+
+def bench_scannd_bwd(torch, K, stream, dims, D, M, steps, warmup):
+    """The ScanND backward on the configs[2] grids and inputs (h from the
+    forward, dy ~ N(0, 1)): one launch per anti-diagonal level for the
+    adjoint state, then the gradient and dA launches."""
+    nd = len(dims)
+    P = 1
+    for v in dims:
+        P *= v
+    g = torch.Generator(device="cuda").manual_seed(12)
+    x = torch.randn((P, D), device="cuda", generator=g)
+    A = torch.log(0.05 + (0.9 / nd - 0.05) * torch.rand((nd, D, M), device="cuda", generator=g))
+    B = torch.randn((P, D, M), device="cuda", generator=g) * 0.25
+    Cm = torch.randn((P, D, M), device="cuda", generator=g) * 0.25
+    dt = torch.ones((nd, P, D), device="cuda")
+    h = torch.empty((P, D, M), device="cuda")
+    y = torch.empty((P, D), device="cuda")
+    K.scannd_fwd(dims, x, A, B, Cm, dt, h, y, stream=stream)
+    dy = torch.randn((P, D), device="cuda", generator=g)
+    dx, ddt = torch.empty_like(x), torch.empty_like(dt)
+    dA, dB, dC = torch.empty_like(A), torch.empty_like(B), torch.empty_like(Cm)
+    fn = lambda: K.scannd_bwd(dims, x, A, B, Cm, dt, h, dy, dx, ddt, dA, dB, dC, stream=stream)  # noqa: E731
+    per, wall = time_launches(torch, stream, fn, steps, warmup)
+    ms = wall / steps
+    alg = scannd_bwd_alg_bytes(dims, D, M)
+    return {"ms": round(ms, 4), "elems_per_s": P * D / (ms * 1e-3),
+            "achieved_GBs": round(alg / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "alg_bytes": alg}
 
 
 def make_inputs(torch, Bsz, L, D, N, dtype, seed=0):
@@ -341,7 +383,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", choices=["all", "scan1d", "scan1d_bwd", "scannd", "convnd", "block",
-                                       "mamba3", "gemm", "model", "copy"],
+                                       "mamba3", "gemm", "model", "scannd_bwd", "copy"],
                     default="all",
                     help="profiling modes: scan1d = the fp32 headline kernel only; copy = a plain "
                          "1 GiB device copy (calibrates rocprof FETCH_SIZE/WRITE_SIZE)")
@@ -377,6 +419,12 @@ def main():
         with torch.cuda.stream(stream):
             r = bench_mamba1_block(torch, K, stream, args.steps, args.warmup)
         print(json.dumps({"mamba1_block_configs4": r}))
+        return
+    if args.only == "scannd_bwd":
+        with torch.cuda.stream(stream):
+            r2 = bench_scannd_bwd(torch, K, stream, (256, 256), 256, 16, args.steps, min(args.warmup, 10))
+            r3 = bench_scannd_bwd(torch, K, stream, (64, 64, 64), 128, 16, args.steps, min(args.warmup, 10))
+        print(json.dumps({"scannd_bwd_2d_256x256_D256_M16": r2, "scannd_bwd_3d_64cubed_D128_M16": r3}))
         return
     if args.only == "model":
         print(json.dumps({"kmamba_forward": bench_model(K, args.steps, min(args.warmup, 3))}))

@@ -211,6 +211,44 @@ int km_mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long
  * and lambda must be NULL. Returns 0, or -1 with km_last_error() set. */
 int km_scannd_fwd(const ScanNDParams *p, void *stream);
 
+/* ScanND backward (no counterpart in the reference, which has no ScanND
+ * adjoint; the adjoint of scannd_ref, src/scan_nd.c:74-192, for the loss
+ * L = sum dy . y). With e_a[p] = exp(delta_a[p] A_a), dtbar = sum_a
+ * delta_a / ndims and h the forward's states:
+ *   g[p]     = dy[p] C[p] + sum_a [i_a < dims_a - 1] e_a[p + s_a] g[p + s_a]
+ *   dC = dy h;  dB = g dtbar x;  dx = sum_m g dtbar B
+ *   ddelta_a = sum_m g B x / ndims + [i_a > 0] sum_m g A_a e_a h[p - s_a]
+ *   dA_a     = sum_p [i_a > 0] g delta_a e_a h[p - s_a]
+ * Layouts as ScanNDParams (dims a host pointer): x, dy, dx [P, D];
+ * delta, ddelta [ndims, P, D]; A, dA [ndims, D, M]; B, C, h, dB, dC
+ * [P, D, M] (h: the states km_scannd_fwd wrote). All outputs are
+ * overwritten; dA is summed in a fixed order (identical run to run).
+ * Needs ndims * M <= 128. workspace: km_scannd_bwd_workspace_bytes()
+ * bytes of device memory, or NULL for the library's per-device scratch
+ * (calls that overlap on one device then race). The adjoint state runs one
+ * launch per anti-diagonal level of the grid, last to first. */
+typedef struct {
+    const long  *dims;
+    long ndims, D, M;
+    const float *x;
+    const float *A;
+    const float *B;
+    const float *C;
+    const float *delta;
+    const float *h;
+    const float *dy;
+    float *dx;
+    float *ddelta;
+    float *dA;
+    float *dB;
+    float *dC;
+    void  *workspace;
+    size_t workspace_bytes;
+} KMScanNDBwd;
+
+size_t km_scannd_bwd_workspace_bytes(const KMScanNDBwd *a);
+int km_scannd_bwd(const KMScanNDBwd *a, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,397 @@
+// scannd_bwd.hip - ScanND backward (km_scannd_bwd): the adjoint of the
+// ScanND forward (reference src/scan_nd.c:74-192, non-lambda branch) for
+// L = sum dy . y. The reference has no ScanND backward; the oracle's C
+// restatement (orc_scannd_backward) is pinned by float64 finite differences
+// and, in 1D, by the reference's scan1d_backward.
+//
+// Three launches kinds, no atomics:
+//  1. The adjoint state g[p] = dy[p] C[p] + sum_a e_a[p+s_a] g[p+s_a] flows
+//     against the forward's wavefront: one launch per anti-diagonal level,
+//     last level first, one thread per (point, channel-state); g is kept in
+//     dB's memory (no P x D x M scratch).
+//  2. Gradients, parallel over points, writing dC, dx, ddelta and dB (over
+//     g, in place) and per-workgroup dA partials. With M a power of two
+//     <= 64, lanes own consecutive channel-states (coalesced) and sum over
+//     a channel's states with xor shuffles; otherwise a thread owns one
+//     channel, loops over its states and keeps its dA terms in its own LDS
+//     slots.
+//  3. dA = the workgroups' partials summed in workgroup order.
+#include <algorithm>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+
+#include "km_device.hpp"
+#include "../km_runtime.hpp"
+#include "kmamba_km.h"
+#include "scan_nd.h"
+#include "wavefront_nd.h"
+#include "wavefront_plan.h"
+
+namespace km {
+
+constexpr int kNdBwdMaxAcc = 64;   // ndims * M: per-thread dA slots in LDS (64 KB)
+
+struct NdBwdArgs {
+    const float *x, *A, *B, *C, *delta, *h, *dy;
+    float *dx, *ddelta, *dB, *dC;
+    float *part;            // [nbx][nd][D][M] dA partials
+    const long *offs;       // level offsets of the wavefront plan (device)
+    const uint16_t *nbr;    // per point: bit a = has a successor on axis a, bit 8 + a = a predecessor
+    long P, D, M;
+    long dims[8], strides[8];
+};
+
+// One level of the adjoint state: workgroup (x, y) = channel-states
+// [256 x, +256) of the level's point s0 + y.
+template <int ND>
+__global__ void __launch_bounds__(256) nd_adjoint_level(NdBwdArgs a, long s0) {
+    const long DM = a.D * a.M;
+    const long c = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    if (c >= DM) return;
+    const long d = c / a.M;
+    const long q = a.offs[s0 + blockIdx.y];
+    const unsigned nb = a.nbr[q];
+    float g = a.dy[q * a.D + d] * a.C[q * DM + c];
+#pragma unroll
+    for (int ax = 0; ax < ND; ++ax) {
+        if (nb & (1u << ax)) {
+            const long nx = q + a.strides[ax];
+            const float e = exp2_fast(a.delta[(ax * a.P + nx) * a.D + d] * a.A[ax * DM + c] * kLog2e);
+            g = fmaf(e, a.dB[nx * DM + c], g);
+        }
+    }
+    a.dB[q * DM + c] = g;
+}
+
+// Block: 256 threads = qlanes point lanes x db channels (db a power of two);
+// the workgroup covers channels [blockIdx.y * db, +db) and points
+// [blockIdx.x * qc, +qc).
+template <int ND>
+__global__ void __launch_bounds__(256) nd_adjoint_grads(NdBwdArgs a, long qc, int db) {
+    extern __shared__ float acc[];                 // [ND * M][256]
+    const int tid = threadIdx.x;
+    const int qlanes = 256 / db;
+    const int ql = tid / db, dl = tid - ql * db;
+    const long d = static_cast<long>(blockIdx.y) * db + dl;
+    const long q0 = static_cast<long>(blockIdx.x) * qc;
+    const long q1 = std::min<long>(a.P, q0 + qc);
+    const long M = a.M, DM = a.D * M;
+    const int nacc = ND * static_cast<int>(M);
+    for (int k = 0; k < nacc; ++k) acc[k * 256 + tid] = 0.f;
+    if (d < a.D) {
+        for (long q = q0 + ql; q < q1; q += qlanes) {
+            const float xv = a.x[q * a.D + d], dyv = a.dy[q * a.D + d];
+            float dl_[ND];
+            long prev[ND];
+            bool has[ND];
+            float dtb = 0.f;
+#pragma unroll
+            for (int ax = 0; ax < ND; ++ax) {
+                dl_[ax] = a.delta[(ax * a.P + q) * a.D + d];
+                dtb += dl_[ax];
+                has[ax] = (a.nbr[q] >> (8 + ax)) & 1u;
+                prev[ax] = has[ax] ? q - a.strides[ax] : q;
+            }
+            dtb /= static_cast<float>(ND);
+            float sx = 0.f, sbx = 0.f, sdel[ND];
+#pragma unroll
+            for (int ax = 0; ax < ND; ++ax) sdel[ax] = 0.f;
+            const long base = q * DM + d * M;
+            for (long m = 0; m < M; ++m) {
+                const float gv = a.dB[base + m], bv = a.B[base + m];
+                a.dC[base + m] = dyv * a.h[base + m];
+                sx += gv * dtb * bv;
+                sbx += gv * bv * xv;
+#pragma unroll
+                for (int ax = 0; ax < ND; ++ax) {
+                    if (has[ax]) {
+                        const float av = a.A[(ax * a.D + d) * M + m];
+                        const float e = exp2_fast(dl_[ax] * av * kLog2e);
+                        const float gh = gv * e * a.h[prev[ax] * DM + d * M + m];
+                        sdel[ax] += gh * av;
+                        acc[(ax * M + m) * 256 + tid] += gh * dl_[ax];
+                    }
+                }
+                a.dB[base + m] = gv * dtb * xv;
+            }
+            a.dx[q * a.D + d] = sx;
+#pragma unroll
+            for (int ax = 0; ax < ND; ++ax)
+                a.ddelta[(ax * a.P + q) * a.D + d] = sbx / static_cast<float>(ND) + sdel[ax];
+        }
+    }
+    __syncthreads();
+    if (ql == 0 && d < a.D) {
+        for (int k = 0; k < nacc; ++k) {
+            float s = 0.f;
+            for (int l = 0; l < qlanes; ++l) s += acc[k * 256 + l * db + dl];
+            const long ax = k / M, m = k - ax * M;
+            a.part[((static_cast<long>(blockIdx.x) * ND + ax) * a.D + d) * M + m] = s;
+        }
+    }
+}
+
+// Gradients with M a power of two <= 64: lane order follows memory (thread
+// t of workgroup (x, y) owns channel-state c = 256 y + t, so every load and
+// store of a point is one contiguous run), the M lanes of a channel sum
+// their dx / ddelta terms with xor shuffles (groups of M lanes are aligned
+// since M divides 64), and each lane keeps its own dA terms in registers
+// over the workgroup's points. Workgroup x covers points [x qc, +qc).
+template <int ND>
+__global__ void __launch_bounds__(256) nd_adjoint_grads_lanes(NdBwdArgs a, long qc) {
+    const long M = a.M, DM = a.D * M;
+    const long c0 = static_cast<long>(blockIdx.y) * 256 + threadIdx.x;
+    const bool active = c0 < DM;
+    const long c = active ? c0 : 0;                 // idle lanes still join the shuffles
+    const long d = c / M;
+    const int m = static_cast<int>(c - d * M);
+    const long q0 = static_cast<long>(blockIdx.x) * qc;
+    const long q1 = std::min<long>(a.P, q0 + qc);
+    float av[ND], dAacc[ND];
+#pragma unroll
+    for (int ax = 0; ax < ND; ++ax) {
+        av[ax] = a.A[ax * DM + c];
+        dAacc[ax] = 0.f;
+    }
+    for (long q = q0; q < q1; ++q) {
+        const float xv = a.x[q * a.D + d], dyv = a.dy[q * a.D + d];
+        float dl_[ND];
+        float dtb = 0.f;
+#pragma unroll
+        for (int ax = 0; ax < ND; ++ax) {
+            dl_[ax] = a.delta[(ax * a.P + q) * a.D + d];
+            dtb += dl_[ax];
+        }
+        dtb /= static_cast<float>(ND);
+        const long pc = q * DM + c;
+        const unsigned nb = a.nbr[q];
+        const float gv = a.dB[pc], bv = a.B[pc];
+        float tx = gv * dtb * bv, tbx = gv * bv * xv, td[ND];
+#pragma unroll
+        for (int ax = 0; ax < ND; ++ax) {
+            td[ax] = 0.f;
+            if ((nb >> (8 + ax)) & 1u) {
+                const float e = exp2_fast(dl_[ax] * av[ax] * kLog2e);
+                const float gh = gv * e * a.h[pc - a.strides[ax] * DM];
+                td[ax] = gh * av[ax];
+                dAacc[ax] += gh * dl_[ax];
+            }
+        }
+        for (int k = 1; k < M; k <<= 1) {
+            tx += __shfl_xor(tx, k);
+            tbx += __shfl_xor(tbx, k);
+#pragma unroll
+            for (int ax = 0; ax < ND; ++ax) td[ax] += __shfl_xor(td[ax], k);
+        }
+        if (active) {
+            a.dC[pc] = dyv * a.h[pc];
+            a.dB[pc] = gv * dtb * xv;
+            if (m == 0) {
+                a.dx[q * a.D + d] = tx;
+#pragma unroll
+                for (int ax = 0; ax < ND; ++ax)
+                    a.ddelta[(ax * a.P + q) * a.D + d] = tbx / static_cast<float>(ND) + td[ax];
+            }
+        }
+    }
+    if (active) {
+#pragma unroll
+        for (int ax = 0; ax < ND; ++ax) a.part[(static_cast<long>(blockIdx.x) * ND + ax) * DM + c] = dAacc[ax];
+    }
+}
+
+__global__ void __launch_bounds__(256) nd_adjoint_dA(const float *part, float *dA, long nbx, long n) {
+    const long k = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    if (k >= n) return;
+    float s = 0.f;
+    for (long b = 0; b < nbx; ++b) s += part[b * n + k];
+    dA[k] = s;
+}
+
+struct NdBwdShape {
+    long P, nd, D, M;
+    bool lanes;          // M a power of two <= 64: nd_adjoint_grads_lanes
+    int db;
+    long qc, nbx, nby;
+    size_t offs_bytes, nbr_bytes, part_bytes;
+};
+
+static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
+    if (!a || !a->dims || a->ndims < 1 || a->ndims > 8 || a->D <= 0 || a->M <= 0) {
+        set_error("km_scannd_bwd: invalid ndims / D / M");
+        return false;
+    }
+    if (!wavefront_nd_validate_dims(a->dims, a->ndims)) {
+        set_error("km_scannd_bwd: invalid dims");
+        return false;
+    }
+    if (a->ndims * a->M > kNdBwdMaxAcc) {
+        set_error("km_scannd_bwd: ndims * M = %ld exceeds %d", a->ndims * a->M, kNdBwdMaxAcc);
+        return false;
+    }
+    s.P = wavefront_nd_total_points(a->dims, a->ndims);
+    if (s.P <= 0) {
+        set_error("km_scannd_bwd: empty grid");
+        return false;
+    }
+    s.nd = a->ndims;
+    s.D = a->D;
+    s.M = a->M;
+    s.lanes = s.M <= 64 && (s.M & (s.M - 1)) == 0;
+    int db = 1;
+    while (db < 256 && db < s.D) db *= 2;
+    s.db = db;
+    if (s.lanes) {
+        s.nby = (s.D * s.M + 255) / 256;
+        const long want = std::max<long>(1, 2048 / s.nby);    // ~2048 workgroups
+        s.qc = std::max<long>(1, (s.P + want - 1) / want);
+    } else {
+        s.nby = (s.D + db - 1) / db;
+        const long want = std::max<long>(1, 1024 / s.nby);    // ~1024 workgroups
+        s.qc = std::max<long>(256 / db, (s.P + want - 1) / want);
+    }
+    s.nbx = (s.P + s.qc - 1) / s.qc;
+    s.offs_bytes = align_up(sizeof(long) * s.P, 256);
+    s.nbr_bytes = align_up(sizeof(uint16_t) * s.P, 256);
+    s.part_bytes = sizeof(float) * s.nbx * s.nd * s.D * s.M;
+    return true;
+}
+
+template <int ND>
+static void nd_bwd_launch(const NdBwdArgs &args, const NdBwdShape &s, const KMWavefrontPlan *plan,
+                          float *dA, hipStream_t st) {
+    const long DM = s.D * s.M;
+    const unsigned bx = static_cast<unsigned>((DM + 255) / 256);
+    for (long lvl = plan->max_level; lvl >= 0; --lvl) {
+        // Levels of more than 65535 points go in several launches.
+        for (long s0 = plan->level_starts[lvl]; s0 < plan->level_starts[lvl + 1]; s0 += 65535) {
+            const long n = std::min<long>(65535, plan->level_starts[lvl + 1] - s0);
+            hipLaunchKernelGGL(nd_adjoint_level<ND>, dim3(bx, static_cast<unsigned>(n)), dim3(256), 0, st,
+                               args, s0);
+        }
+    }
+    if (s.lanes) {
+        hipLaunchKernelGGL(nd_adjoint_grads_lanes<ND>,
+                           dim3(static_cast<unsigned>(s.nbx), static_cast<unsigned>(s.nby)), dim3(256), 0, st,
+                           args, s.qc);
+    } else {
+        const size_t lds = sizeof(float) * ND * s.M * 256;
+        hipLaunchKernelGGL(nd_adjoint_grads<ND>,
+                           dim3(static_cast<unsigned>(s.nbx), static_cast<unsigned>(s.nby)), dim3(256), lds, st,
+                           args, s.qc, s.db);
+    }
+    const long n = s.nd * DM;
+    hipLaunchKernelGGL(nd_adjoint_dA, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st,
+                       args.part, dA, s.nbx, n);
+}
+
+}  // namespace km
+
+extern "C" {
+
+size_t km_scannd_bwd_workspace_bytes(const KMScanNDBwd *a) {
+    km::clear_error();
+    km::NdBwdShape s;
+    if (!km::nd_bwd_shape(a, s)) return 0;
+    return s.offs_bytes + s.nbr_bytes + s.part_bytes;
+}
+
+int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
+    km::clear_error();
+    km::NdBwdShape s;
+    if (!km::nd_bwd_shape(a, s)) return -1;
+    if (!a->x || !a->A || !a->B || !a->C || !a->delta || !a->h || !a->dy || !a->dx || !a->ddelta ||
+        !a->dA || !a->dB || !a->dC) {
+        km::set_error("km_scannd_bwd: NULL tensor pointer");
+        return -1;
+    }
+    if (s.nbx > 0x7fffffffL || s.nby > 65535 || s.nd * s.D * s.M > 0x7fffffffL * 256L) {
+        km::set_error("km_scannd_bwd: grid out of range");
+        return -1;
+    }
+    if (!km::gpu_ready()) return -1;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const size_t need = s.offs_bytes + s.nbr_bytes + s.part_bytes;
+    char *ws = static_cast<char *>(a->workspace);
+    if (ws) {
+        if (a->workspace_bytes < need) {
+            km::set_error("km_scannd_bwd: workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
+            return -1;
+        }
+    } else {
+        ws = static_cast<char *>(km::Workspace::reserve(need));
+        if (!ws) return -1;
+    }
+    KMWavefrontPlan *plan = km_wavefront_plan_create(a->dims, a->ndims);
+    if (!plan) {
+        km::set_error("km_scannd_bwd: wavefront plan could not be built");
+        return -1;
+    }
+    km::NdBwdArgs args{};
+    args.x = a->x; args.A = a->A; args.B = a->B; args.C = a->C; args.delta = a->delta;
+    args.h = a->h; args.dy = a->dy; args.dx = a->dx; args.ddelta = a->ddelta; args.dB = a->dB;
+    args.dC = a->dC;
+    args.offs = reinterpret_cast<const long *>(ws);
+    args.nbr = reinterpret_cast<const uint16_t *>(ws + s.offs_bytes);
+    args.part = reinterpret_cast<float *>(ws + s.offs_bytes + s.nbr_bytes);
+    args.P = s.P; args.D = s.D; args.M = s.M;
+    long stride = 1;
+    for (long ax = s.nd - 1; ax >= 0; --ax) {
+        args.dims[ax] = a->dims[ax];
+        args.strides[ax] = stride;
+        stride *= a->dims[ax];
+    }
+    // Neighbour flags of every point, by an odometer over the row-major
+    // coordinates (no divisions).
+    uint16_t *nbr = static_cast<uint16_t *>(malloc(sizeof(uint16_t) * s.P));
+    if (!nbr) {
+        km_wavefront_plan_free(plan);
+        km::set_error("km_scannd_bwd: out of host memory");
+        return -1;
+    }
+    {
+        long idx[8] = {0};
+        for (long q = 0; q < s.P; ++q) {
+            unsigned f = 0;
+            for (long ax = 0; ax < s.nd; ++ax) {
+                if (idx[ax] + 1 < a->dims[ax]) f |= 1u << ax;
+                if (idx[ax] > 0) f |= 1u << (8 + ax);
+            }
+            nbr[q] = static_cast<uint16_t>(f);
+            for (long ax = s.nd - 1; ax >= 0; --ax) {
+                if (++idx[ax] < a->dims[ax]) break;
+                idx[ax] = 0;
+            }
+        }
+    }
+    int rc = 0;
+    // The host tables must outlive the copies: wait for them.
+    if (hipMemcpyAsync(ws, plan->level_offsets, sizeof(long) * s.P, hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipMemcpyAsync(ws + s.offs_bytes, nbr, sizeof(uint16_t) * s.P, hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess) {
+        km::set_error("km_scannd_bwd: plan upload failed");
+        rc = -1;
+    } else {
+        switch (s.nd) {
+        case 1: km::nd_bwd_launch<1>(args, s, plan, a->dA, st); break;
+        case 2: km::nd_bwd_launch<2>(args, s, plan, a->dA, st); break;
+        case 3: km::nd_bwd_launch<3>(args, s, plan, a->dA, st); break;
+        case 4: km::nd_bwd_launch<4>(args, s, plan, a->dA, st); break;
+        case 5: km::nd_bwd_launch<5>(args, s, plan, a->dA, st); break;
+        case 6: km::nd_bwd_launch<6>(args, s, plan, a->dA, st); break;
+        case 7: km::nd_bwd_launch<7>(args, s, plan, a->dA, st); break;
+        default: km::nd_bwd_launch<8>(args, s, plan, a->dA, st); break;
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) {
+            km::set_error("km_scannd_bwd: launch failed: %s", hipGetErrorString(e));
+            rc = -1;
+        }
+    }
+    km_wavefront_plan_free(plan);
+    free(nbr);
+    return rc;
+}
+
+}  // extern "C"

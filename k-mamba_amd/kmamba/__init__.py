@@ -428,6 +428,30 @@ def scannd_params(dims, x, A, B, Cm, delta, h, y):
     return p, dd
 
 
+class KMScanNDBwd(C.Structure):           # include/kmamba_km.h (no reference counterpart)
+    _fields_ = [("dims", c_long_p), ("ndims", C.c_long), ("D", C.c_long), ("M", C.c_long)] + \
+               [(n, C.c_void_p) for n in ("x", "A", "B", "C", "delta", "h", "dy", "dx", "ddelta",
+                                          "dA", "dB", "dC", "workspace")] + \
+               [("workspace_bytes", C.c_size_t)]
+
+
+km_scannd_bwd_workspace_bytes = _decl("km_scannd_bwd_workspace_bytes", C.c_size_t,
+                                      [C.POINTER(KMScanNDBwd)])
+km_scannd_bwd_c = _decl("km_scannd_bwd", C.c_int, [C.POINTER(KMScanNDBwd), C.c_void_p])
+
+
+def scannd_bwd(dims, x, A, B, Cm, delta, h, dy, dx, ddelta, dA, dB, dC, *, workspace=None,
+               stream=None):
+    """km_scannd_bwd on torch device tensors (layouts as scannd_fwd)."""
+    dd = longs(dims)
+    nd, D, M = A.shape
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    args = KMScanNDBwd(dd, len(dims), D, M, ptr(x), ptr(A), ptr(B), ptr(Cm), ptr(delta), ptr(h),
+                       ptr(dy), ptr(dx), ptr(ddelta), ptr(dA), ptr(dB), ptr(dC), ptr(workspace),
+                       ws_bytes)
+    check(km_scannd_bwd_c(C.byref(args), C.c_void_p(stream_handle(stream))), "km_scannd_bwd")
+
+
 def scannd_fwd(dims, x, A, B, Cm, delta, h, y, stream=None):
     """km_scannd_fwd (scannd_ref semantics) on torch device tensors."""
     p, keep = scannd_params(dims, x, A, B, Cm, delta, h, y)

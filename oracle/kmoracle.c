@@ -532,6 +532,71 @@ int orc_scannd_ref(OrcScanNDParams *p, int nthreads) {        /* :235-247 */
     return rc;
 }
 
+/* Adjoint of scannd_ref; see kmoracle.h. */
+int orc_scannd_backward(const OrcScanNDParams *p, const float *dy, float *dx, float *ddelta,
+                        float *dA, float *dB, float *dC) {
+    if (!p || !p->dims || p->ndims <= 0 || p->ndims > 8 || p->D <= 0 || p->M <= 0) return -1;
+    if (!p->x || !p->A || !p->B || !p->C || !p->delta || !p->h || !dy) return -1;
+    if (!dx || !ddelta || !dA || !dB || !dC) return -1;
+    if (!orc_wavefront_validate_dims(p->dims, p->ndims)) return -1;
+    long strides[8], idx[8];
+    if (!orc_make_row_major_strides(p->dims, p->ndims, strides)) return -1;
+    const long nd = p->ndims, D = p->D, M = p->M;
+    const long P = orc_wavefront_total_points(p->dims, nd);
+    float *g = dB;
+    for (long q = P - 1; q >= 0; q--) {
+        orc_unravel_index(q, p->dims, strides, nd, idx);
+        for (long d = 0; d < D; d++) {
+            const float dyv = dy[q * D + d];
+            for (long m = 0; m < M; m++) {
+                const long dm = d * M + m;
+                float gv = dyv * p->C[q * D * M + dm];
+                for (long a = 0; a < nd; a++) {
+                    if (idx[a] + 1 < p->dims[a]) {
+                        const long nx = q + strides[a];
+                        const float e = expf(p->delta[(a * P + nx) * D + d] * p->A[(a * D + d) * M + m]);
+                        gv += e * g[nx * D * M + dm];
+                    }
+                }
+                g[q * D * M + dm] = gv;
+            }
+        }
+    }
+    for (long i = 0; i < nd * D * M; i++) dA[i] = 0.0f;
+    for (long q = 0; q < P; q++) {
+        orc_unravel_index(q, p->dims, strides, nd, idx);
+        for (long d = 0; d < D; d++) {
+            const float xv = p->x[q * D + d], dyv = dy[q * D + d];
+            float dtb = 0.0f;
+            for (long a = 0; a < nd; a++) dtb += p->delta[(a * P + q) * D + d];
+            dtb /= (float)nd;
+            float sx = 0.0f, sbx = 0.0f, sdel[8];
+            for (long a = 0; a < nd; a++) sdel[a] = 0.0f;
+            for (long m = 0; m < M; m++) {
+                const long dm = d * M + m, pdm = q * D * M + dm;
+                const float gv = g[pdm], bv = p->B[pdm];
+                dC[pdm] = dyv * p->h[pdm];
+                sx += gv * dtb * bv;
+                sbx += gv * bv * xv;
+                for (long a = 0; a < nd; a++) {
+                    if (idx[a] > 0) {
+                        const float dta = p->delta[(a * P + q) * D + d];
+                        const float av = p->A[(a * D + d) * M + m];
+                        const float e = expf(dta * av);
+                        const float gh = gv * e * p->h[(q - strides[a]) * D * M + dm];
+                        sdel[a] += gh * av;
+                        dA[(a * D + d) * M + m] += gh * dta;
+                    }
+                }
+                dB[pdm] = gv * dtb * xv;
+            }
+            dx[q * D + d] = sx;
+            for (long a = 0; a < nd; a++) ddelta[(a * P + q) * D + d] = sbx / (float)nd + sdel[a];
+        }
+    }
+    return 0;
+}
+
 /* CPU dispatch of scannd (src/scan_nd.c:265-307): 1D -> scan1d with h as a
  * running [D, M] state, 2D -> scan2d, otherwise scannd_ref. */
 int orc_scannd(OrcScanNDParams *p, int nthreads) {

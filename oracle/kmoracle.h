@@ -86,6 +86,20 @@ int  orc_scannd_ref_with_plan(OrcScanNDParams *p, const OrcPlan *plan, int nthre
 int  orc_scannd_ref(OrcScanNDParams *p, int nthreads);
 int  orc_scannd(OrcScanNDParams *p, int nthreads);
 
+/* Adjoint of scannd_ref (no counterpart in the reference, which has no
+ * ScanND backward): for L = sum dy . y with h the forward's states (p->h),
+ *   g[p]     = dy[p] C[p] + sum_a [i_a < dims_a - 1] exp(delta_a[p+s_a] A_a) g[p+s_a]
+ *   dC[p]    = dy[p] h[p];  dB[p] = g[p] dtbar[p] x[p]
+ *   dx[p]    = sum_m g dtbar B
+ *   ddelta_a = sum_m g B x / ndims + [i_a > 0] sum_m g A_a e_a[p] h[p-s_a]
+ *   dA_a     = sum_p [i_a > 0] g delta_a[p] e_a[p] h[p-s_a]
+ * with e_a[p] = exp(delta_a[p] A_a) and dtbar = sum_a delta_a / ndims as the
+ * forward forms them (src/scan_nd.c:105-108, :174-188). g runs in reverse
+ * row-major order (every p + s_a precedes p); g is kept in dB's memory until
+ * dB is formed. Sums over m and over p run in ascending order. */
+int  orc_scannd_backward(const OrcScanNDParams *p, const float *dy, float *dx, float *ddelta,
+                         float *dA, float *dB, float *dC);
+
 /* ---- ConvND ----------------------------------------------------------- */
 long orc_convnd_kernel_volume(long ndims, long K);
 void orc_convnd_forward(OrcConvNDParams *p, int nthreads);

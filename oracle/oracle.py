@@ -101,6 +101,7 @@ for _lib in {orc, orc_fast}:
     _sig(_lib, "orc_scan2d", None, [C.POINTER(Scan2DParams)])
     _sig(_lib, "orc_scannd_ref", C.c_int, [C.POINTER(ScanNDParams), C.c_int])
     _sig(_lib, "orc_scannd", C.c_int, [C.POINTER(ScanNDParams), C.c_int])
+    _sig(_lib, "orc_scannd_backward", C.c_int, [C.POINTER(ScanNDParams), vp, vp, vp, vp, vp, vp])
     _sig(_lib, "orc_convnd_forward", None, [C.POINTER(ConvNDParams), C.c_int])
     _sig(_lib, "orc_convnd_backward", None, [C.POINTER(ConvNDParams)])
     _sig(_lib, "orc_plan_create", C.POINTER(Plan), [lp, C.c_long])
@@ -265,6 +266,25 @@ def scannd_ref(dims, x, A, B, Cm, delta, *, nthreads=1, use_ref=False, fast=Fals
     if rc != 0:
         raise RuntimeError("scannd_ref failed")
     return y, h
+
+
+def scannd_backward(dims, x, A, B, Cm, delta, h, dy, *, fast=False):
+    """Adjoint of scannd_ref for L = sum dy . y (restated in kmoracle.c; the
+    reference has no ScanND backward): h is the forward's states [P, D, M].
+    Returns dict dx [P, D], ddelta [nd, P, D], dA [nd, D, M], dB, dC [P, D, M]."""
+    x, A, B, Cm, delta, h, dy = map(f32, (x, A, B, Cm, delta, h, dy))
+    Pn = int(np.prod(dims))
+    nd, D, M = A.shape
+    out = {"dx": np.zeros((Pn, D), np.float32), "ddelta": np.zeros((nd, Pn, D), np.float32),
+           "dA": np.zeros((nd, D, M), np.float32), "dB": np.zeros((Pn, D, M), np.float32),
+           "dC": np.zeros((Pn, D, M), np.float32)}
+    y = np.zeros((Pn, D), np.float32)
+    p, _keep = _nd_params(dims, x, A, B, Cm, delta, h, y)
+    rc = (orc_fast if fast else orc).orc_scannd_backward(
+        C.byref(p), P(dy), P(out["dx"]), P(out["ddelta"]), P(out["dA"]), P(out["dB"]), P(out["dC"]))
+    if rc != 0:
+        raise RuntimeError("orc_scannd_backward failed")
+    return out
 
 
 def scannd(dims, x, A, B, Cm, delta, h=None, *, nthreads=1):

@@ -553,3 +553,78 @@ def test_mamba3_forward_closed_forms():
         y = Ct @ h
         want = xt + p["W_out"][:, 0] * y
         np.testing.assert_allclose(out[0, t], want, rtol=2e-5, atol=2e-6)
+
+
+# ---------------------------------------------------------------------------
+# ScanND adjoint (no reference function: pinned by float64 finite
+# differences and by its 1D case, which is the reference's scan1d_backward)
+# ---------------------------------------------------------------------------
+def _scannd_f64(dims, x, A, B, Cm, delta):
+    """Brute-force float64 forward of scannd_ref (src/scan_nd.c:74-192,
+    non-lambda branch) for tiny grids: y [P, D]."""
+    nd = len(dims)
+    Pn = int(np.prod(dims))
+    strides = [int(np.prod(dims[a + 1:])) for a in range(nd)]
+    h = np.zeros(B.shape)
+    y = np.zeros(x.shape)
+    for q in range(Pn):
+        idx = [(q // strides[a]) % dims[a] for a in range(nd)]
+        dtb = delta[:, q, :].sum(0) / nd                      # [D]
+        hq = (dtb * x[q])[:, None] * B[q]
+        for a in range(nd):
+            if idx[a] > 0:
+                hq = hq + np.exp(delta[a, q][:, None] * A[a]) * h[q - strides[a]]
+        h[q] = hq
+        y[q] = (Cm[q] * hq).sum(-1)
+    return y
+
+
+def _nd_case(dims, D, M, seed):
+    g = rng_for("ndadj", dims, D, M, seed)
+    Pn, nd = int(np.prod(dims)), len(dims)
+    return dict(x=g.standard_normal((Pn, D)), A=-g.uniform(0.2, 1.5, (nd, D, M)),
+                B=g.standard_normal((Pn, D, M)) * 0.5, Cm=g.standard_normal((Pn, D, M)) * 0.5,
+                delta=g.uniform(0.05, 0.6, (nd, Pn, D)), dy=g.standard_normal((Pn, D)))
+
+
+@pytest.mark.parametrize("dims,D,M", [((5,), 2, 3), ((3, 4), 2, 3), ((2, 3, 2), 1, 2), ((2, 2, 2, 2), 1, 1)])
+def test_scannd_backward_vs_finite_differences(dims, D, M):
+    # Central differences of L = sum dy . y on the float64 forward; the
+    # oracle runs in fp32 on the same (fp32-representable) inputs.
+    c = {k: v.astype(np.float32).astype(np.float64) for k, v in _nd_case(dims, D, M, 0).items()}
+    y32, h32 = O.scannd_ref(dims, c["x"], c["A"], c["B"], c["Cm"], c["delta"])
+    got = O.scannd_backward(dims, c["x"], c["A"], c["B"], c["Cm"], c["delta"], h32, c["dy"])
+    names = {"x": "dx", "A": "dA", "B": "dB", "Cm": "dC", "delta": "ddelta"}
+
+    def loss(**kw):
+        args = {k: kw.get(k, c[k]) for k in ("x", "A", "B", "Cm", "delta")}
+        return float((c["dy"] * _scannd_f64(dims, **args)).sum())
+    for name, gname in names.items():
+        base = c[name]
+        fd = np.zeros_like(base)
+        eps = 1e-6
+        for i in np.ndindex(base.shape):
+            up, dn = base.copy(), base.copy()
+            up[i] += eps
+            dn[i] -= eps
+            fd[i] = (loss(**{name: up}) - loss(**{name: dn})) / (2 * eps)
+        err = np.abs(got[gname] - fd).max() / max(np.abs(fd).max(), 1e-12)
+        assert err < 2e-5, f"{gname}: max error {err:.2e} relative to max |grad|"
+
+
+@needs_ref
+@pytest.mark.parametrize("L,D,M", [(9, 3, 4), (40, 8, 16)])
+def test_scannd_backward_1d_equals_reference_scan1d_backward(L, D, M):
+    # With ndims = 1, dtbar = delta and the ScanND recurrence is Scan1D's
+    # without the clamp, so the adjoint is cpu/scan1d_backward.c:248-295
+    # (h0 = 0; B, C per channel [L, D, M], the layout both use).
+    c = _nd_case((L,), D, M, 1)
+    c = {k: v.astype(np.float32) for k, v in c.items()}
+    y, h = O.scannd_ref((L,), c["x"], c["A"], c["B"], c["Cm"], c["delta"])
+    got = O.scannd_backward((L,), c["x"], c["A"], c["B"], c["Cm"], c["delta"], h, c["dy"])
+    dx, dA, dB, dC, dd = O.scan1d_backward(c["x"], c["A"][0], c["B"], c["Cm"], c["delta"][0], h,
+                                           c["dy"], lib=O.ref)
+    for name, want, have in (("dx", dx, got["dx"]), ("dA", dA, got["dA"][0]), ("dB", dB, got["dB"]),
+                             ("dC", dC, got["dC"]), ("ddelta", dd, got["ddelta"][0])):
+        scale = max(np.abs(want).max(), 1e-30)
+        assert np.abs(have - want).max() / scale < 1e-5, name

@@ -210,3 +210,87 @@ def test_config2_full_size_sampled(dims, D, M, nsel):
     ya, ha = kappa(dims, *args)
     assert_close(y[:, sel], yr, TOL_F32, "y", ya)
     assert_close(h[:, sel], hr, TOL_F32, "h", ha)
+
+
+# ---------------------------------------------------------------------------
+# ScanND backward (km_scannd_bwd; the oracle's adjoint is pinned in
+# test_oracle_pins.py by float64 finite differences and by the reference's
+# scan1d_backward in 1D). Metric: normwise per output, max |got - ref| /
+# max |ref| <= 1e-4 (fp32; dA and ddelta are sums of signed terms).
+# ---------------------------------------------------------------------------
+BWD_CASES = [((50,), 8, 4), ((17, 23), 8, 16), ((64, 64), 32, 16), ((5, 6, 7), 4, 8),
+             ((16, 16, 16), 16, 16), ((3, 4, 2, 5), 3, 5), ((9, 11), 5, 32), ((256, 256), 16, 16),
+             ((64, 64, 64), 8, 16)]
+
+
+def bwd_inputs(dims, D, M, seed):
+    # Decays whose sum over the axes stays <= 0.9 (A = log U(0.05, 0.9/nd),
+    # delta in [1, 2]), as the configs[2] inputs: the adjoint, like the
+    # forward, sums over every lattice path and overflows fp32 on large grids
+    # when that sum nears 1.
+    x, A, B, Cm, dt = nd_inputs(dims, D, M, seed)
+    g = rng_for("ndbwd", dims, D, M, seed)
+    nd = len(dims)
+    A = np.log(g.uniform(0.05, 0.9 / nd, A.shape)).astype(np.float32)
+    dt = g.uniform(1.0, 2.0, dt.shape).astype(np.float32)
+    dy = g.standard_normal((int(np.prod(dims)), D)).astype(np.float32)
+    _, h = O.scannd_ref(dims, x, A, B, Cm, dt, nthreads=8, fast=True)
+    return x, A, B, Cm, dt, h, dy
+
+
+def run_bwd(dims, x, A, B, Cm, dt, h, dy):
+    Pn, D = x.shape
+    nd, _, M = A.shape
+    out = {"dx": torch.full((Pn, D), float("nan"), device="cuda"),
+           "ddelta": torch.full((nd, Pn, D), float("nan"), device="cuda"),
+           "dA": torch.full((nd, D, M), float("nan"), device="cuda"),
+           "dB": torch.full((Pn, D, M), float("nan"), device="cuda"),
+           "dC": torch.full((Pn, D, M), float("nan"), device="cuda")}
+    K.scannd_bwd(dims, T(x), T(A), T(B), T(Cm), T(dt), T(h), T(dy), out["dx"], out["ddelta"],
+                 out["dA"], out["dB"], out["dC"])
+    torch.cuda.synchronize()
+    return {k: v.cpu().numpy() for k, v in out.items()}
+
+
+@pytest.mark.parametrize("dims,D,M", BWD_CASES)
+def test_backward_vs_oracle(dims, D, M):
+    x, A, B, Cm, dt, h, dy = bwd_inputs(dims, D, M, 0)
+    want = O.scannd_backward(dims, x, A, B, Cm, dt, h, dy, fast=True)
+    got = run_bwd(dims, x, A, B, Cm, dt, h, dy)
+    for k in want:
+        assert np.isfinite(got[k]).all(), k
+        err = np.abs(got[k] - want[k]).max() / max(np.abs(want[k]).max(), 1e-30)
+        assert err <= 1e-4, f"{k}: normwise error {err:.2e}"
+
+
+def test_backward_deterministic_and_workspace():
+    dims, D, M = (33, 40), 8, 16
+    x, A, B, Cm, dt, h, dy = bwd_inputs(dims, D, M, 1)
+    a = run_bwd(dims, x, A, B, Cm, dt, h, dy)
+    b = run_bwd(dims, x, A, B, Cm, dt, h, dy)
+    for k in a:
+        assert np.array_equal(a[k].view(np.uint32), b[k].view(np.uint32)), k
+    # An explicit workspace of the queried size gives the same result.
+    args = K.KMScanNDBwd(K.longs(dims), 2, D, M)
+    need = K.km_scannd_bwd_workspace_bytes(C.byref(args))
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    Pn = int(np.prod(dims))
+    out = [torch.empty(s, device="cuda") for s in ((Pn, D), (2, Pn, D), (2, D, M), (Pn, D, M), (Pn, D, M))]
+    K.scannd_bwd(dims, T(x), T(A), T(B), T(Cm), T(dt), T(h), T(dy), *out, workspace=ws)
+    torch.cuda.synchronize()
+    for k, t in zip(("dx", "ddelta", "dA", "dB", "dC"), out):
+        assert np.array_equal(t.cpu().numpy().view(np.uint32), a[k].view(np.uint32)), k
+    small = torch.empty(need - 256, dtype=torch.uint8, device="cuda")
+    with pytest.raises(RuntimeError, match="workspace"):
+        K.scannd_bwd(dims, T(x), T(A), T(B), T(Cm), T(dt), T(h), T(dy), *out, workspace=small)
+
+
+def test_backward_rejects_invalid():
+    dims, D, M = (4, 4), 2, 33                 # ndims * M = 66 > 64
+    args = K.KMScanNDBwd(K.longs(dims), 2, D, M)
+    assert K.km_scannd_bwd_workspace_bytes(C.byref(args)) == 0
+    assert "exceeds" in K.km_last_error()
+    assert K.km_scannd_bwd_c(C.byref(args), None) == -1
+    args = K.KMScanNDBwd(K.longs((4, 0)), 2, 2, 4)
+    assert K.km_scannd_bwd_c(C.byref(args), None) == -1
