@@ -4,11 +4,12 @@
 // restatement (orc_scannd_backward) is pinned by float64 finite differences
 // and, in 1D, by the reference's scan1d_backward.
 //
-// Three launches kinds, no atomics:
+// Three kinds of launches, no atomics:
 //  1. The adjoint state g[p] = dy[p] C[p] + sum_a e_a[p+s_a] g[p+s_a] flows
-//     against the forward's wavefront: one launch per anti-diagonal level,
-//     last level first, one thread per (point, channel-state); g is kept in
-//     dB's memory (no P x D x M scratch).
+//     against the forward's wavefront, g kept in dB's memory (no P x D x M
+//     scratch): 2D grids with D*M a multiple of 64 by tile bands (one launch
+//     per band, last first), other grids one launch per anti-diagonal level,
+//     last level first, one thread per (point, channel-state).
 //  2. Gradients, parallel over points, writing dC, dx, ddelta and dB (over
 //     g, in place) and per-workgroup dA partials. With M a power of two
 //     <= 64, lanes own consecutive channel-states (coalesced) and sum over
@@ -62,6 +63,77 @@ __global__ void __launch_bounds__(256) nd_adjoint_level(NdBwdArgs a, long s0) {
         }
     }
     a.dB[q * DM + c] = g;
+}
+
+// 2D grids with D*M a multiple of 64: the adjoint state by tile bands. The
+// grid is cut into TR x TW tiles; tiles with equal tile-index sum (a band)
+// are independent, and bands run last to first, one launch each. One wave
+// per (tile, group of 64 channel-states) walks its tile's rows bottom-up,
+// each row right to left, keeping the row below (its g and axis-0 delta) in
+// registers and the right neighbour from the previous step; successors
+// across the tile's bottom and right edges were written by the previous
+// launch (the next band).
+template <int TR, int TW>
+__global__ void __launch_bounds__(64) nd_adjoint_tile2d(NdBwdArgs a, int band, int nt1, int ncg) {
+    const int lane = threadIdx.x;
+    const int o = static_cast<int>(blockIdx.x) / ncg, cg = static_cast<int>(blockIdx.x) - o * ncg;
+    const int ti0 = (band > nt1 - 1 ? band - (nt1 - 1) : 0) + o, ti1 = band - ti0;
+    const long n0 = a.dims[0], n1 = a.dims[1];
+    const long r0 = static_cast<long>(ti0) * TR, r1 = std::min<long>(n0, r0 + TR);
+    const long j0 = static_cast<long>(ti1) * TW, j1 = std::min<long>(n1, j0 + TW);
+    const long DM = a.D * a.M, P = a.P;
+    const long c = static_cast<long>(cg) * 64 + lane;
+    const long d = c / a.M;
+    const float A0 = a.A[c] * kLog2e, A1 = a.A[DM + c] * kLog2e;
+    // A row's operands (dy . C, both deltas) and right-edge successor,
+    // loaded before the row computes (its g stores would otherwise order
+    // every later load); columns past j1 load column j1 - 1 and go unused.
+    struct Row {
+        float dyc[TW], d0[TW], d1[TW];
+        float gr, dr1;
+    };
+    auto load_row = [&](long r, Row &w) __attribute__((always_inline)) {
+#pragma unroll
+        for (int jj = 0; jj < TW; ++jj) {
+            const long q = r * n1 + std::min<long>(j0 + jj, j1 - 1);
+            w.dyc[jj] = a.dy[q * a.D + d] * a.C[q * DM + c];
+            w.d0[jj] = a.delta[q * a.D + d];
+            w.d1[jj] = a.delta[(P + q) * a.D + d];
+        }
+        const long qr = r * n1 + std::min<long>(j1, n1 - 1);
+        w.gr = a.dB[qr * DM + c];
+        w.dr1 = a.delta[(P + qr) * a.D + d];
+    };
+    float gb[TW], db0[TW];
+#pragma unroll
+    for (int jj = 0; jj < TW; ++jj) {
+        const long q = std::min<long>(r1, n0 - 1) * n1 + std::min<long>(j0 + jj, j1 - 1);
+        gb[jj] = a.dB[q * DM + c];
+        db0[jj] = a.delta[q * a.D + d];
+    }
+    Row cur, nxt;
+    load_row(r1 - 1, cur);
+    for (long r = r1 - 1; r >= r0; --r) {
+        load_row(r > 0 ? r - 1 : 0, nxt);
+        const bool below = r + 1 < n0;
+        float gr = cur.gr, dr1 = cur.dr1;
+        bool right = j1 < n1;
+#pragma unroll
+        for (int jj = TW - 1; jj >= 0; --jj) {
+            if (j0 + jj < j1) {
+                float g = cur.dyc[jj];
+                if (below) g = fmaf(exp2_fast(db0[jj] * A0), gb[jj], g);
+                if (right) g = fmaf(exp2_fast(dr1 * A1), gr, g);
+                a.dB[(r * n1 + j0 + jj) * DM + c] = g;
+                gb[jj] = g;
+                db0[jj] = cur.d0[jj];
+                gr = g;
+                dr1 = cur.d1[jj];
+                right = true;
+            }
+        }
+        cur = nxt;
+    }
 }
 
 // Block: 256 threads = qlanes point lanes x db channels (db a power of two);
@@ -258,11 +330,25 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
     return true;
 }
 
+constexpr int kAdjTR = 16, kAdjTW = 8;
+
 template <int ND>
 static void nd_bwd_launch(const NdBwdArgs &args, const NdBwdShape &s, const KMWavefrontPlan *plan,
                           float *dA, hipStream_t st) {
     const long DM = s.D * s.M;
     const unsigned bx = static_cast<unsigned>((DM + 255) / 256);
+    if (ND == 2 && DM % 64 == 0) {
+        const int nt0 = static_cast<int>((args.dims[0] + kAdjTR - 1) / kAdjTR);
+        const int nt1 = static_cast<int>((args.dims[1] + kAdjTW - 1) / kAdjTW);
+        const int ncg = static_cast<int>(DM / 64);
+        for (int band = nt0 + nt1 - 2; band >= 0; --band) {
+            const int lo = band > nt1 - 1 ? band - (nt1 - 1) : 0;
+            const int hi = band < nt0 - 1 ? band : nt0 - 1;
+            const long tiles = hi - lo + 1;
+            hipLaunchKernelGGL((nd_adjoint_tile2d<kAdjTR, kAdjTW>),
+                               dim3(static_cast<unsigned>(tiles * ncg)), dim3(64), 0, st, args, band, nt1, ncg);
+        }
+    } else {
     for (long lvl = plan->max_level; lvl >= 0; --lvl) {
         // Levels of more than 65535 points go in several launches.
         for (long s0 = plan->level_starts[lvl]; s0 < plan->level_starts[lvl + 1]; s0 += 65535) {
@@ -270,6 +356,7 @@ static void nd_bwd_launch(const NdBwdArgs &args, const NdBwdShape &s, const KMWa
             hipLaunchKernelGGL(nd_adjoint_level<ND>, dim3(bx, static_cast<unsigned>(n)), dim3(256), 0, st,
                                args, s0);
         }
+    }
     }
     if (s.lanes) {
         hipLaunchKernelGGL(nd_adjoint_grads_lanes<ND>,
