@@ -7,9 +7,9 @@
 // Three kinds of launches, no atomics:
 //  1. The adjoint state g[p] = dy[p] C[p] + sum_a e_a[p+s_a] g[p+s_a] flows
 //     against the forward's wavefront, g kept in dB's memory (no P x D x M
-//     scratch): 2D grids with D*M a multiple of 64 by tile bands (one launch
-//     per band, last first), other grids one launch per anti-diagonal level,
-//     last level first, one thread per (point, channel-state).
+//     scratch): 2D and 3D grids with D*M a multiple of 64 by tile bands (one
+//     launch per band, last first), other grids one launch per anti-diagonal
+//     level, last level first, one thread per (point, channel-state).
 //  2. Gradients, parallel over points, writing dC, dx, ddelta and dB (over
 //     g, in place) and per-workgroup dA partials. With M a power of two
 //     <= 64, lanes own consecutive channel-states (coalesced) and sum over
@@ -18,6 +18,7 @@
 //     slots.
 //  3. dA = the workgroups' partials summed in workgroup order.
 #include <algorithm>
+#include <vector>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
@@ -32,6 +33,7 @@
 namespace km {
 
 constexpr int kNdBwdMaxAcc = 64;   // ndims * M: per-thread dA slots in LDS (64 KB)
+constexpr int kAdj3P = 4, kAdj3R = 4, kAdj3W = 8;   // 3D adjoint tiles (axis 0, 1, 2)
 
 struct NdBwdArgs {
     const float *x, *A, *B, *C, *delta, *h, *dy;
@@ -133,6 +135,95 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile2d(NdBwdArgs a, int band, i
             }
         }
         cur = nxt;
+    }
+}
+
+// 3D grids with D*M a multiple of 64: the same by TP x TR x TW tiles (axis
+// 0, 1, 2). tiles[] lists each band's tiles (host-built, bands contiguous);
+// a wave walks its tile's planes, rows and points in reverse, keeping the
+// plane below (g and axis-0 delta of every (row, column) of the tile) and
+// the row below in registers (loops fully unrolled: no dynamic indexing).
+template <int TP, int TR, int TW>
+__global__ void __launch_bounds__(64) nd_adjoint_tile3d(NdBwdArgs a, const int *tiles, int ncg) {
+    const int lane = threadIdx.x;
+    const int o = static_cast<int>(blockIdx.x) / ncg, cg = static_cast<int>(blockIdx.x) - o * ncg;
+    const long n0 = a.dims[0], n1 = a.dims[1], n2 = a.dims[2];
+    const long p0 = static_cast<long>(tiles[3 * o]) * TP, p1 = std::min<long>(n0, p0 + TP);
+    const long r0 = static_cast<long>(tiles[3 * o + 1]) * TR, r1 = std::min<long>(n1, r0 + TR);
+    const long j0 = static_cast<long>(tiles[3 * o + 2]) * TW, j1 = std::min<long>(n2, j0 + TW);
+    const long DM = a.D * a.M, P = a.P, s0 = n1 * n2;
+    const long c = static_cast<long>(cg) * 64 + lane;
+    const long d = c / a.M;
+    const float A0 = a.A[c] * kLog2e, A1 = a.A[DM + c] * kLog2e, A2 = a.A[2 * DM + c] * kLog2e;
+    struct Row {
+        float dyc[TW], d0[TW], d1[TW], d2[TW];
+        float gr, dr2;
+    };
+    auto qof = [&](long pp, long rr, long jj) { return pp * s0 + rr * n2 + jj; };
+    auto load_row = [&](long pp, long rr, Row &w) __attribute__((always_inline)) {
+#pragma unroll
+        for (int jj = 0; jj < TW; ++jj) {
+            const long q = qof(pp, rr, std::min<long>(j0 + jj, j1 - 1));
+            w.dyc[jj] = a.dy[q * a.D + d] * a.C[q * DM + c];
+            w.d0[jj] = a.delta[q * a.D + d];
+            w.d1[jj] = a.delta[(P + q) * a.D + d];
+            w.d2[jj] = a.delta[(2 * P + q) * a.D + d];
+        }
+        const long qr = qof(pp, rr, std::min<long>(j1, n2 - 1));
+        w.gr = a.dB[qr * DM + c];
+        w.dr2 = a.delta[(2 * P + qr) * a.D + d];
+    };
+    // Plane below: successors along axis 0 of every (row, column).
+    float gp[TR][TW], dp0[TR][TW];
+#pragma unroll
+    for (int ri = 0; ri < TR; ++ri)
+#pragma unroll
+        for (int jj = 0; jj < TW; ++jj) {
+            const long q = qof(std::min<long>(p1, n0 - 1), std::min<long>(r0 + ri, r1 - 1),
+                               std::min<long>(j0 + jj, j1 - 1));
+            gp[ri][jj] = a.dB[q * DM + c];
+            dp0[ri][jj] = a.delta[q * a.D + d];
+        }
+    for (long pp = p1 - 1; pp >= p0; --pp) {
+        const bool pbelow = pp + 1 < n0;
+        // Row below the tile's last row: successors along axis 1.
+        float gb[TW], db1[TW];
+#pragma unroll
+        for (int jj = 0; jj < TW; ++jj) {
+            const long q = qof(pp, std::min<long>(r1, n1 - 1), std::min<long>(j0 + jj, j1 - 1));
+            gb[jj] = a.dB[q * DM + c];
+            db1[jj] = a.delta[(P + q) * a.D + d];
+        }
+        Row cur, nxt;
+        load_row(pp, r1 - 1, cur);
+#pragma unroll
+        for (int ri = TR - 1; ri >= 0; --ri) {
+            const long r = r0 + ri;
+            if (r < r1) {
+                load_row(pp, r > r0 ? r - 1 : r, nxt);
+                const bool rbelow = r + 1 < n1;
+                float gr = cur.gr, dr2 = cur.dr2;
+                bool right = j1 < n2;
+#pragma unroll
+                for (int jj = TW - 1; jj >= 0; --jj) {
+                    if (j0 + jj < j1) {
+                        float g = cur.dyc[jj];
+                        if (pbelow) g = fmaf(exp2_fast(dp0[ri][jj] * A0), gp[ri][jj], g);
+                        if (rbelow) g = fmaf(exp2_fast(db1[jj] * A1), gb[jj], g);
+                        if (right) g = fmaf(exp2_fast(dr2 * A2), gr, g);
+                        a.dB[qof(pp, r, j0 + jj) * DM + c] = g;
+                        gp[ri][jj] = g;
+                        dp0[ri][jj] = cur.d0[jj];
+                        gb[jj] = g;
+                        db1[jj] = cur.d1[jj];
+                        gr = g;
+                        dr2 = cur.d2[jj];
+                        right = true;
+                    }
+                }
+                cur = nxt;
+            }
+        }
     }
 }
 
@@ -286,7 +377,7 @@ struct NdBwdShape {
     bool lanes;          // M a power of two <= 64: nd_adjoint_grads_lanes
     int db;
     long qc, nbx, nby;
-    size_t offs_bytes, nbr_bytes, part_bytes;
+    size_t offs_bytes, nbr_bytes, part_bytes, tile_bytes;
 };
 
 static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
@@ -326,6 +417,13 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
     s.nbx = (s.P + s.qc - 1) / s.qc;
     s.offs_bytes = align_up(sizeof(long) * s.P, 256);
     s.nbr_bytes = align_up(sizeof(uint16_t) * s.P, 256);
+    s.tile_bytes = 0;
+    if (s.nd == 3 && (s.D * s.M) % 64 == 0) {
+        long nt = 1;
+        const long tdim[3] = {kAdj3P, kAdj3R, kAdj3W};
+        for (int ax = 0; ax < 3; ++ax) nt *= (a->dims[ax] + tdim[ax] - 1) / tdim[ax];
+        s.tile_bytes = align_up(sizeof(int) * 3 * nt, 256);
+    }
     s.part_bytes = sizeof(float) * s.nbx * s.nd * s.D * s.M;
     return true;
 }
@@ -334,10 +432,19 @@ constexpr int kAdjTR = 16, kAdjTW = 8;
 
 template <int ND>
 static void nd_bwd_launch(const NdBwdArgs &args, const NdBwdShape &s, const KMWavefrontPlan *plan,
-                          float *dA, hipStream_t st) {
+                          float *dA, const int *dtiles, const std::vector<long> &bstart, hipStream_t st) {
     const long DM = s.D * s.M;
     const unsigned bx = static_cast<unsigned>((DM + 255) / 256);
-    if (ND == 2 && DM % 64 == 0) {
+    if (ND == 3 && s.tile_bytes) {
+        const int ncg = static_cast<int>(DM / 64);
+        for (long b = static_cast<long>(bstart.size()) - 2; b >= 0; --b) {
+            const long n = bstart[b + 1] - bstart[b];
+            if (n > 0)
+                hipLaunchKernelGGL((nd_adjoint_tile3d<kAdj3P, kAdj3R, kAdj3W>),
+                                   dim3(static_cast<unsigned>(n * ncg)), dim3(64), 0, st, args,
+                                   dtiles + 3 * bstart[b], ncg);
+        }
+    } else if (ND == 2 && DM % 64 == 0) {
         const int nt0 = static_cast<int>((args.dims[0] + kAdjTR - 1) / kAdjTR);
         const int nt1 = static_cast<int>((args.dims[1] + kAdjTW - 1) / kAdjTW);
         const int ncg = static_cast<int>(DM / 64);
@@ -381,7 +488,7 @@ size_t km_scannd_bwd_workspace_bytes(const KMScanNDBwd *a) {
     km::clear_error();
     km::NdBwdShape s;
     if (!km::nd_bwd_shape(a, s)) return 0;
-    return s.offs_bytes + s.nbr_bytes + s.part_bytes;
+    return s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes;
 }
 
 int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
@@ -399,7 +506,7 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
     }
     if (!km::gpu_ready()) return -1;
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    const size_t need = s.offs_bytes + s.nbr_bytes + s.part_bytes;
+    const size_t need = s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes;
     char *ws = static_cast<char *>(a->workspace);
     if (ws) {
         if (a->workspace_bytes < need) {
@@ -452,23 +559,48 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
             }
         }
     }
+    // 3D tile bands: each band's tiles (tile-index sum b), bands contiguous.
+    std::vector<int> tl;
+    std::vector<long> bstart;
+    if (s.tile_bytes) {
+        const long nt0 = (a->dims[0] + km::kAdj3P - 1) / km::kAdj3P;
+        const long nt1 = (a->dims[1] + km::kAdj3R - 1) / km::kAdj3R;
+        const long nt2 = (a->dims[2] + km::kAdj3W - 1) / km::kAdj3W;
+        for (long b = 0; b <= nt0 + nt1 + nt2 - 3; ++b) {
+            bstart.push_back(static_cast<long>(tl.size() / 3));
+            for (long t0 = 0; t0 < nt0; ++t0)
+                for (long t1 = 0; t1 < nt1; ++t1) {
+                    const long t2 = b - t0 - t1;
+                    if (t2 >= 0 && t2 < nt2) {
+                        tl.push_back(static_cast<int>(t0));
+                        tl.push_back(static_cast<int>(t1));
+                        tl.push_back(static_cast<int>(t2));
+                    }
+                }
+        }
+        bstart.push_back(static_cast<long>(tl.size() / 3));
+    }
+    char *tile_ws = ws + s.offs_bytes + s.nbr_bytes + s.part_bytes;
     int rc = 0;
     // The host tables must outlive the copies: wait for them.
     if (hipMemcpyAsync(ws, plan->level_offsets, sizeof(long) * s.P, hipMemcpyHostToDevice, st) != hipSuccess ||
         hipMemcpyAsync(ws + s.offs_bytes, nbr, sizeof(uint16_t) * s.P, hipMemcpyHostToDevice, st) != hipSuccess ||
+        (!tl.empty() && hipMemcpyAsync(tile_ws, tl.data(), sizeof(int) * tl.size(), hipMemcpyHostToDevice,
+                                       st) != hipSuccess) ||
         hipStreamSynchronize(st) != hipSuccess) {
         km::set_error("km_scannd_bwd: plan upload failed");
         rc = -1;
     } else {
+        const int *dtiles = reinterpret_cast<const int *>(tile_ws);
         switch (s.nd) {
-        case 1: km::nd_bwd_launch<1>(args, s, plan, a->dA, st); break;
-        case 2: km::nd_bwd_launch<2>(args, s, plan, a->dA, st); break;
-        case 3: km::nd_bwd_launch<3>(args, s, plan, a->dA, st); break;
-        case 4: km::nd_bwd_launch<4>(args, s, plan, a->dA, st); break;
-        case 5: km::nd_bwd_launch<5>(args, s, plan, a->dA, st); break;
-        case 6: km::nd_bwd_launch<6>(args, s, plan, a->dA, st); break;
-        case 7: km::nd_bwd_launch<7>(args, s, plan, a->dA, st); break;
-        default: km::nd_bwd_launch<8>(args, s, plan, a->dA, st); break;
+        case 1: km::nd_bwd_launch<1>(args, s, plan, a->dA, dtiles, bstart, st); break;
+        case 2: km::nd_bwd_launch<2>(args, s, plan, a->dA, dtiles, bstart, st); break;
+        case 3: km::nd_bwd_launch<3>(args, s, plan, a->dA, dtiles, bstart, st); break;
+        case 4: km::nd_bwd_launch<4>(args, s, plan, a->dA, dtiles, bstart, st); break;
+        case 5: km::nd_bwd_launch<5>(args, s, plan, a->dA, dtiles, bstart, st); break;
+        case 6: km::nd_bwd_launch<6>(args, s, plan, a->dA, dtiles, bstart, st); break;
+        case 7: km::nd_bwd_launch<7>(args, s, plan, a->dA, dtiles, bstart, st); break;
+        default: km::nd_bwd_launch<8>(args, s, plan, a->dA, dtiles, bstart, st); break;
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) {
