@@ -504,6 +504,11 @@ def main():
         extra["scannd_3d_64cubed_D128_M16_f32"] = bench_scannd(torch, K, stream, (64, 64, 64), 128, 16,
                                                                 max(5, args.steps // 2), 2)
         extra["mamba3_block_fwd_f32"] = bench_mamba3(torch, K, max(5, args.steps // 10), 2)
+        extra["scannd_bwd_2d_256x256_D256_M16_f32"] = bench_scannd_bwd(
+            torch, K, stream, (256, 256), 256, 16, max(5, args.steps // 10), 2)
+        extra["scannd_bwd_3d_64cubed_D128_M16_f32"] = bench_scannd_bwd(
+            torch, K, stream, (64, 64, 64), 128, 16, max(5, args.steps // 10), 2)
+    extra["kmamba_forward_f32"] = bench_model(K, 3, 1)
 
     traffic = None
     tf = ROOT / "profiles" / "scan1d_fwd_c1_traffic.json"
