@@ -294,3 +294,35 @@ def test_backward_rejects_invalid():
     assert K.km_scannd_bwd_c(C.byref(args), None) == -1
     args = K.KMScanNDBwd(K.longs((4, 0)), 2, 2, 4)
     assert K.km_scannd_bwd_c(C.byref(args), None) == -1
+
+
+@pytest.mark.parametrize("dims,D,M", [((256, 256), 256, 16), ((64, 64, 64), 128, 16)])
+def test_backward_full_size_adjoint_identities(dims, D, M):
+    # configs[2] sizes, checked through what the recurrence fixes at any
+    # size: y is linear in x, in B and in C separately (h is linear in B x),
+    # so sum dx.x = sum dB.B = sum dC.C = sum dy.y exactly in real
+    # arithmetic. The forward's y and h come from km_scannd_fwd.
+    nd = len(dims)
+    Pn = int(np.prod(dims))
+    g = torch.Generator(device="cuda").manual_seed(21)
+    x = torch.randn((Pn, D), device="cuda", generator=g)
+    A = torch.log(0.05 + (0.9 / nd - 0.05) * torch.rand((nd, D, M), device="cuda", generator=g))
+    B = torch.randn((Pn, D, M), device="cuda", generator=g) * 0.25
+    Cm = torch.randn((Pn, D, M), device="cuda", generator=g) * 0.25
+    dt = 1.0 + torch.rand((nd, Pn, D), device="cuda", generator=g)
+    h = torch.empty((Pn, D, M), device="cuda")
+    y = torch.empty((Pn, D), device="cuda")
+    K.scannd_fwd(dims, x, A, B, Cm, dt, h, y)
+    dy = torch.randn((Pn, D), device="cuda", generator=g)
+    dx, ddt = torch.empty_like(x), torch.empty_like(dt)
+    dA, dB, dC = torch.empty_like(A), torch.empty_like(B), torch.empty_like(Cm)
+    K.scannd_bwd(dims, x, A, B, Cm, dt, h, dy, dx, ddt, dA, dB, dC)
+    torch.cuda.synchronize()
+    ref = (dy.double() * y.double()).sum().item()
+    scale = (dy.double().abs() * y.double().abs()).sum().item()
+    for name, grad, val in (("dx", dx, x), ("dB", dB, B), ("dC", dC, Cm)):
+        assert torch.isfinite(grad).all(), name
+        got = (grad.double() * val.double()).sum().item()
+        assert abs(got - ref) <= 1e-5 * scale, f"{name}: <grad, input> {got:.6e} vs <dy, y> {ref:.6e}"
+    for t in (dA, ddt):
+        assert torch.isfinite(t).all()
