@@ -45,6 +45,20 @@ struct NdBwdArgs {
     long dims[8], strides[8];
 };
 
+// Neighbour flags of every point: bit a = a successor on axis a, bit 8 + a
+// = a predecessor.
+__global__ void __launch_bounds__(256) nd_adjoint_flags(NdBwdArgs a, long nd, uint16_t *nbr) {
+    const long q = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    if (q >= a.P) return;
+    unsigned f = 0;
+    for (long ax = 0; ax < nd; ++ax) {
+        const long i = (q / a.strides[ax]) % a.dims[ax];
+        if (i + 1 < a.dims[ax]) f |= 1u << ax;
+        if (i > 0) f |= 1u << (8 + ax);
+    }
+    nbr[q] = static_cast<uint16_t>(f);
+}
+
 // One level of the adjoint state: workgroup (x, y) = channel-states
 // [256 x, +256) of the level's point s0 + y.
 template <int ND>
@@ -517,8 +531,12 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
         ws = static_cast<char *>(km::Workspace::reserve(need));
         if (!ws) return -1;
     }
-    KMWavefrontPlan *plan = km_wavefront_plan_create(a->dims, a->ndims);
-    if (!plan) {
+    // The per-level path reads the plan's level offsets; the tile-band paths
+    // (2D and 3D with D*M a multiple of 64) need no plan.
+    const bool tiles2d = s.nd == 2 && (s.D * s.M) % 64 == 0;
+    const bool levels = !tiles2d && !s.tile_bytes;
+    KMWavefrontPlan *plan = nullptr;
+    if (levels && !(plan = km_wavefront_plan_create(a->dims, a->ndims))) {
         km::set_error("km_scannd_bwd: wavefront plan could not be built");
         return -1;
     }
@@ -535,29 +553,6 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
         args.dims[ax] = a->dims[ax];
         args.strides[ax] = stride;
         stride *= a->dims[ax];
-    }
-    // Neighbour flags of every point, by an odometer over the row-major
-    // coordinates (no divisions).
-    uint16_t *nbr = static_cast<uint16_t *>(malloc(sizeof(uint16_t) * s.P));
-    if (!nbr) {
-        km_wavefront_plan_free(plan);
-        km::set_error("km_scannd_bwd: out of host memory");
-        return -1;
-    }
-    {
-        long idx[8] = {0};
-        for (long q = 0; q < s.P; ++q) {
-            unsigned f = 0;
-            for (long ax = 0; ax < s.nd; ++ax) {
-                if (idx[ax] + 1 < a->dims[ax]) f |= 1u << ax;
-                if (idx[ax] > 0) f |= 1u << (8 + ax);
-            }
-            nbr[q] = static_cast<uint16_t>(f);
-            for (long ax = s.nd - 1; ax >= 0; --ax) {
-                if (++idx[ax] < a->dims[ax]) break;
-                idx[ax] = 0;
-            }
-        }
     }
     // 3D tile bands: each band's tiles (tile-index sum b), bands contiguous.
     std::vector<int> tl;
@@ -582,12 +577,14 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
     }
     char *tile_ws = ws + s.offs_bytes + s.nbr_bytes + s.part_bytes;
     int rc = 0;
-    // The host tables must outlive the copies: wait for them.
-    if (hipMemcpyAsync(ws, plan->level_offsets, sizeof(long) * s.P, hipMemcpyHostToDevice, st) != hipSuccess ||
-        hipMemcpyAsync(ws + s.offs_bytes, nbr, sizeof(uint16_t) * s.P, hipMemcpyHostToDevice, st) != hipSuccess ||
+    hipLaunchKernelGGL(km::nd_adjoint_flags, dim3(static_cast<unsigned>((s.P + 255) / 256)), dim3(256), 0, st,
+                       args, s.nd, reinterpret_cast<uint16_t *>(ws + s.offs_bytes));
+    // The host tables must outlive their copies: wait for them.
+    if ((plan && hipMemcpyAsync(ws, plan->level_offsets, sizeof(long) * s.P, hipMemcpyHostToDevice, st) !=
+                     hipSuccess) ||
         (!tl.empty() && hipMemcpyAsync(tile_ws, tl.data(), sizeof(int) * tl.size(), hipMemcpyHostToDevice,
                                        st) != hipSuccess) ||
-        hipStreamSynchronize(st) != hipSuccess) {
+        ((plan || !tl.empty()) && hipStreamSynchronize(st) != hipSuccess)) {
         km::set_error("km_scannd_bwd: plan upload failed");
         rc = -1;
     } else {
@@ -608,8 +605,7 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
             rc = -1;
         }
     }
-    km_wavefront_plan_free(plan);
-    free(nbr);
+    if (plan) km_wavefront_plan_free(plan);
     return rc;
 }
 
