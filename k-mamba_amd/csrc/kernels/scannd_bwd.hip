@@ -4,7 +4,9 @@
 // restatement (orc_scannd_backward) is pinned by float64 finite differences
 // and, in 1D, by the reference's scan1d_backward.
 //
-// Three kinds of launches, no atomics:
+// Launches, no atomics:
+//  0. Neighbour flags of every point (successor / predecessor per axis), so
+//     the sweeps below do no index division.
 //  1. The adjoint state g[p] = dy[p] C[p] + sum_a e_a[p+s_a] g[p+s_a] flows
 //     against the forward's wavefront, g kept in dB's memory (no P x D x M
 //     scratch): 2D and 3D grids with D*M a multiple of 64 by tile bands (one
