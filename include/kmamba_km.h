@@ -223,7 +223,7 @@ int km_scannd_fwd(const ScanNDParams *p, void *stream);
  * delta, ddelta [ndims, P, D]; A, dA [ndims, D, M]; B, C, h, dB, dC
  * [P, D, M] (h: the states km_scannd_fwd wrote). All outputs are
  * overwritten; dA is summed in a fixed order (identical run to run).
- * Needs ndims * M <= 128. workspace: km_scannd_bwd_workspace_bytes()
+ * M a power of two <= 64, or ndims * M <= 64. workspace: km_scannd_bwd_workspace_bytes()
  * bytes of device memory, or NULL for the library's per-device scratch
  * (calls that overlap on one device then race). The adjoint state runs one
  * launch per anti-diagonal level of the grid, last to first. */

@@ -405,8 +405,11 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
         set_error("km_scannd_bwd: invalid dims");
         return false;
     }
-    if (a->ndims * a->M > kNdBwdMaxAcc) {
-        set_error("km_scannd_bwd: ndims * M = %ld exceeds %d", a->ndims * a->M, kNdBwdMaxAcc);
+    // The per-channel path keeps ndims * M dA terms per thread in LDS.
+    const bool pow2 = a->M <= 64 && (a->M & (a->M - 1)) == 0;
+    if (!pow2 && a->ndims * a->M > kNdBwdMaxAcc) {
+        set_error("km_scannd_bwd: ndims * M = %ld exceeds %d (M not a power of two <= 64)",
+                  a->ndims * a->M, kNdBwdMaxAcc);
         return false;
     }
     s.P = wavefront_nd_total_points(a->dims, a->ndims);

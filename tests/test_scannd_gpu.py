@@ -219,6 +219,7 @@ def test_config2_full_size_sampled(dims, D, M, nsel):
 # max |ref| <= 1e-4 (fp32; dA and ddelta are sums of signed terms).
 # ---------------------------------------------------------------------------
 BWD_CASES = [((50,), 8, 4), ((17, 23), 8, 16), ((64, 64), 32, 16), ((5, 6, 7), 4, 8),
+             ((3, 2, 3, 2, 2), 2, 16),     # ndims * M = 80: the shuffle path needs no LDS
              ((16, 16, 16), 16, 16), ((3, 4, 2, 5), 3, 5), ((9, 11), 5, 32), ((256, 256), 16, 16),
              ((64, 64, 64), 8, 16)]
 
@@ -287,7 +288,7 @@ def test_backward_deterministic_and_workspace():
 
 
 def test_backward_rejects_invalid():
-    dims, D, M = (4, 4), 2, 33                 # ndims * M = 66 > 64
+    dims, D, M = (4, 4), 2, 33                 # M not a power of two and ndims * M = 66 > 64
     args = K.KMScanNDBwd(K.longs(dims), 2, D, M)
     assert K.km_scannd_bwd_workspace_bytes(C.byref(args)) == 0
     assert "exceeds" in K.km_last_error()
