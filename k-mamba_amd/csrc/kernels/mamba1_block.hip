@@ -22,6 +22,11 @@ namespace km {
 
 int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream);
 int gemm_bf16_launch(const KMGemm *g, hipStream_t s);
+int lib_gemm_bf16(const void *A, const void *B, void *C, long M, long N, long K, long lda, long ldb,
+                  long ldc, void *ws, size_t ws_bytes, hipStream_t s);
+
+// Workspace of the library GEMM (in_proj / out_proj) inside the block's.
+constexpr size_t kLibGemmWs = size_t(32) << 20;
 
 constexpr int kConvStrip = 64;
 
@@ -81,7 +86,7 @@ __global__ void __launch_bounds__(256) conv1d_silu_bf16(const uint32_t *x, const
 }
 
 struct BlockLayout {
-    size_t xi, z, u, xdbl, delta, y, bytes;
+    size_t xi, z, u, xdbl, delta, y, gws, bytes;
 };
 
 static BlockLayout block_layout(const KMMamba1Weights *w, long B, long L) {
@@ -95,6 +100,7 @@ static BlockLayout block_layout(const KMMamba1Weights *w, long B, long L) {
     l.delta = off; off += act;
     l.y = off; off += act;
     l.xdbl = off; off += align_up(T * (w->dt_rank + 2 * w->d_state) * 2, 256);
+    l.gws = off; off += kLibGemmWs;
     l.bytes = off;
     return l;
 }
@@ -142,14 +148,21 @@ int mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long B,
          *delta = ws + lay.delta, *y = ws + lay.y;
     const uint16_t *Win = static_cast<const uint16_t *>(w->W_in);
 
+    // Plain GEMMs (in_proj, out_proj) go to the library GEMM, the rest to
+    // the hand-written kernels.
+    auto plain = [&](const KMGemm &g) {
+        const int r = lib_gemm_bf16(g.A, g.B, g.C, g.M, g.N, g.K, g.lda, g.ldb, g.ldc, ws + lay.gws,
+                                    kLibGemmWs, s);
+        return r < 0 ? -1 : r > 0 ? 0 : gemm_bf16_launch(&g, s);
+    };
     KMGemm g{};
     g.c_dtype = KM_BF16;
     // in_proj, x and z halves
     g.A = x; g.B = Win; g.C = xi; g.M = T; g.N = di; g.K = w->dim;
     g.lda = w->dim; g.ldb = w->dim; g.ldc = di; g.epilogue = KM_EPI_NONE;
-    if (gemm_bf16_launch(&g, s) != 0) return -1;
+    if (plain(g) != 0) return -1;
     g.B = Win + di * w->dim; g.C = z;
-    if (gemm_bf16_launch(&g, s) != 0) return -1;
+    if (plain(g) != 0) return -1;
     // causal depthwise conv1d + SiLU
     {
         dim3 grid(static_cast<unsigned>((di / 2 + 255) / 256),
@@ -193,7 +206,7 @@ int mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long B,
     KMGemm o{};
     o.A = y; o.B = w->W_out; o.C = out; o.M = T; o.N = w->dim; o.K = di;
     o.lda = di; o.ldb = di; o.ldc = w->dim; o.c_dtype = KM_BF16; o.epilogue = KM_EPI_NONE;
-    return gemm_bf16_launch(&o, s);
+    return plain(o);
 }
 
 }  // namespace km
