@@ -25,7 +25,7 @@ int gemm_bf16_launch(const KMGemm *g, hipStream_t s);
 int lib_gemm_bf16(const void *A, const void *B, void *C, long M, long N, long K, long lda, long ldb,
                   long ldc, void *ws, size_t ws_bytes, hipStream_t s);
 
-// Workspace of the library GEMM (in_proj / out_proj) inside the block's.
+// Workspace of the library GEMM (in_proj / x_proj / out_proj) inside the block's.
 constexpr size_t kLibGemmWs = size_t(32) << 20;
 
 constexpr int kConvStrip = 64;
@@ -148,7 +148,7 @@ int mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long B,
          *delta = ws + lay.delta, *y = ws + lay.y;
     const uint16_t *Win = static_cast<const uint16_t *>(w->W_in);
 
-    // Plain GEMMs (in_proj, out_proj) go to the library GEMM, the rest to
+    // Plain GEMMs (in_proj, x_proj, out_proj) go to the library GEMM, the rest to
     // the hand-written kernels.
     auto plain = [&](const KMGemm &g) {
         const int r = lib_gemm_bf16(g.A, g.B, g.C, g.M, g.N, g.K, g.lda, g.ldb, g.ldc, ws + lay.gws,
@@ -187,7 +187,7 @@ int mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long B,
     // x_proj -> [dt_low | B | C]
     g.A = u; g.B = w->W_x; g.C = xdbl; g.M = T; g.N = NX; g.K = di;
     g.lda = di; g.ldb = di; g.ldc = NX;
-    if (gemm_bf16_launch(&g, s) != 0) return -1;
+    if (plain(g) != 0) return -1;
     // dt_proj + bias + softplus
     g.A = xdbl; g.B = w->W_dt; g.C = delta; g.M = T; g.N = di; g.K = R;
     g.lda = NX; g.ldb = R; g.ldc = di; g.bias = w->dt_bias; g.epilogue = KM_EPI_SOFTPLUS;
