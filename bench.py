@@ -392,7 +392,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; multi-GPU sharding is design-only "
-              "(see DESIGN.md), so --gpus must be 1", file=sys.stderr)
+              "(the kernels shard over batch and channels with no exchange), so --gpus must be 1", file=sys.stderr)
         sys.exit(2)
 
     import torch

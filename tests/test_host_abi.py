@@ -109,7 +109,7 @@ def test_plan_bit_exact_vs_reference(dims):
 
 
 def test_plan_config_shapes():
-    # Shapes of the benchmark configurations.
+    # Plan shapes of the benchmark grids: 256^2 (Scan2D), 64^3 (ScanND 3D), 512^2 (ConvND 2D).
     for dims, maxl, mls in (((256, 256), 510, 256), ((64, 64, 64), 189, None), ((512, 512), 1022, 512)):
         starts, offs, meta = product_plan(dims)
         assert meta[2] == maxl

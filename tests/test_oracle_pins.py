@@ -291,7 +291,7 @@ def test_scannd_ref_bit_exact_vs_reference(dims, D, M):
 @pytest.mark.parametrize("dims,D,M", [((7, 5), 3, 4), ((6, 6), 4, 16), ((1, 9), 2, 2)])
 def test_scan2d_agrees_with_scannd_ref(dims, D, M):
     # scan2d (asm order) and scannd_ref differ only in association of
-    # dt_bar*B*x and the decay sum (SURVEY Appendix A.3 note).
+    # dt_bar*B*x and the decay sum (cpu/scan2d.asm against src/scan_nd.c).
     x, A, B, Cm, dt = _nd_inputs(dims, D, M, 1)
     Pn = int(np.prod(dims))
     y2, h2 = O.scan2d(x, A[0], A[1], B, Cm, dt[0], dt[1], *dims)
