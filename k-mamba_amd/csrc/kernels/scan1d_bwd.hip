@@ -659,8 +659,10 @@ static BwdPlan bwd_plan(const KMScan1DBwd *k) {
 
 static bool bwd_args_ok(const KMScan1DBwd *k, const char *who) {
     if (!k) { set_error("%s: NULL arguments", who); return false; }
-    if (!k->x || !k->delta || !k->A || !k->Bm || !k->Cm || !k->dy || !k->dx || !k->ddelta ||
-        !k->dA || !k->dB || !k->dC) {
+    // With no steps (L = 0) only A and dA (zeroed) take part.
+    if (!k->A || !k->dA ||
+        (k->L > 0 && (!k->x || !k->delta || !k->Bm || !k->Cm || !k->dy || !k->dx || !k->ddelta ||
+                      !k->dB || !k->dC))) {
         set_error("%s: NULL tensor pointer", who);
         return false;
     }
@@ -674,7 +676,7 @@ static bool bwd_args_ok(const KMScan1DBwd *k, const char *who) {
         return false;
     }
     if (k->bc_sb < 0 || k->bc_st < 0 || k->bc_sd < 0 ||
-        (k->B > 1 && k->bc_sb == 0) || (k->L > 1 && k->bc_st == 0)) {
+        (k->B > 1 && k->L > 0 && k->bc_sb == 0) || (k->L > 1 && k->bc_st == 0)) {
         set_error("%s: B/C strides must be non-negative and distinct over batch and time "
                   "(sb=%ld st=%ld sd=%ld)", who, k->bc_sb, k->bc_st, k->bc_sd);
         return false;

@@ -569,7 +569,8 @@ static int launch_serial(const Scan1DFwdArgs &a, bool hist, hipStream_t s) {
 
 int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream) {
     if (!k) { set_error("km_scan1d_fwd: NULL arguments"); return -1; }
-    if (!k->x || !k->delta || !k->A || !k->Bm || !k->Cm) {
+    // With no steps (L = 0) only A, h0 and h_final take part.
+    if (!k->A || (k->L > 0 && (!k->x || !k->delta || !k->Bm || !k->Cm))) {
         set_error("km_scan1d_fwd: NULL tensor pointer");
         return -1;
     }
