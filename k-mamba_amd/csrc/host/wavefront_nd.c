@@ -14,33 +14,18 @@
 #include <limits.h>
 #include <stdlib.h>
 
+#include "km_shape.h"
 
-static int add_ok(long a, long b, long *out) {
-    if ((b > 0 && a > LONG_MAX - b) || (b < 0 && a < LONG_MIN - b)) return 0;
-    *out = a + b;
-    return 1;
-}
-
-static int mul_ok(long a, long b, long *out) {
-    if (a < 0 || b < 0) return 0;
-    if (a == 0 || b == 0) { *out = 0; return 1; }
-    if (a > LONG_MAX / b) return 0;
-    *out = a * b;
-    return 1;
-}
 
 int wavefront_nd_validate_dims(const long *dims, long ndims) {
-    if (!dims || ndims <= 0) return 0;
-    for (long a = 0; a < ndims; a++)
-        if (dims[a] <= 0) return 0;
-    return 1;
+    return km_shape_valid(dims, ndims, 0);
 }
 
 long wavefront_nd_total_points(const long *dims, long ndims) {
     long total = 1;
     if (!wavefront_nd_validate_dims(dims, ndims)) return -1;
     for (long a = 0; a < ndims; a++)
-        if (!mul_ok(total, dims[a], &total)) return -1;
+        if (!km_mul_ok(total, dims[a], &total)) return -1;
     return total;
 }
 
@@ -48,7 +33,7 @@ long wavefront_nd_max_level(const long *dims, long ndims) {
     long lvl = 0;
     if (!wavefront_nd_validate_dims(dims, ndims)) return -1;
     for (long a = 0; a < ndims; a++)
-        if (!add_ok(lvl, dims[a] - 1, &lvl)) return -1;
+        if (!km_add_ok(lvl, dims[a] - 1, &lvl)) return -1;
     return lvl;
 }
 
@@ -57,8 +42,8 @@ long wavefront_nd_row_major_offset(const long *dims, const long *idx, long ndims
     if (!wavefront_nd_validate_dims(dims, ndims) || !idx) return -1;
     for (long a = 0; a < ndims; a++) {
         if (idx[a] < 0 || idx[a] >= dims[a]) return -1;
-        if (!mul_ok(off, dims[a], &off)) return -1;
-        if (!add_ok(off, idx[a], &off)) return -1;
+        if (!km_mul_ok(off, dims[a], &off)) return -1;
+        if (!km_add_ok(off, idx[a], &off)) return -1;
     }
     return off;
 }
@@ -79,7 +64,7 @@ long wavefront_nd_level_size(const long *dims, long ndims, long level) {
         if (nreach > level) nreach = level;
         long window = 0;
         for (long s = 0; s <= nreach; s++) {
-            if (s <= reach && !add_ok(window, cnt[s], &window)) { free(cnt); free(nxt); return -1; }
+            if (s <= reach && !km_add_ok(window, cnt[s], &window)) { free(cnt); free(nxt); return -1; }
             long drop = s - dims[a];
             if (drop >= 0 && drop <= reach) window -= cnt[drop];
             nxt[s] = window;
@@ -142,7 +127,7 @@ static int build_caps(const long *dims, long ndims, long *cap) {
     long s = 0;
     for (long a = ndims - 1; a >= 0; a--) {
         cap[a] = s;
-        if (!add_ok(s, dims[a] - 1, &s)) return 0;
+        if (!km_add_ok(s, dims[a] - 1, &s)) return 0;
     }
     return 1;
 }

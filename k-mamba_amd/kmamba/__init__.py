@@ -262,21 +262,91 @@ def stream_handle(stream=None):
     return s.cuda_stream
 
 
+def _need(t, name, *, shape=None, dtype=None, optional=False):
+    """Checks a torch tensor argument before its address goes to the C ABI:
+    contiguous, and of the given shape and dtype (the device is checked by
+    _on_gpu once every argument passed these checks). Raises ValueError
+    naming the argument otherwise (a wrong dtype or stride would make the
+    kernel read or write past the tensor)."""
+    import torch
+    if t is None:
+        if optional:
+            return
+        raise ValueError(f"{name} is required")
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a torch tensor")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} has dtype {t.dtype}, expected {dtype}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _on_gpu(**tensors):
+    """Every given (non-None) tensor must live on the GPU."""
+    for name, t in tensors.items():
+        if t is not None and t.device.type != "cuda":
+            raise ValueError(f"{name} must be a GPU tensor")
+
+
+def _scan1d_io(x, A, Bm, Cm, bc_strides):
+    """Validates the operands common to the Scan1D forward and backward and
+    returns (B, L, D, N, io dtype, KMDtype, bc_strides)."""
+    import torch
+    _need(x, "x")
+    if x.dim() != 3:
+        raise ValueError(f"x must be [B, L, D], got shape {tuple(x.shape)}")
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"x has dtype {x.dtype}; fp32 or bf16 expected")
+    Bsz, L, D = x.shape
+    _need(A, "A", dtype=torch.float32)
+    if A.dim() != 2 or A.shape[0] != D:
+        raise ValueError(f"A must be [D={D}, N], got shape {tuple(A.shape)}")
+    N = A.shape[1]
+    io = x.dtype
+    if bc_strides is None:
+        _need(Bm, "Bm", shape=(Bsz, L, N), dtype=io)
+        _need(Cm, "Cm", shape=(Bsz, L, N), dtype=io)
+        bc_strides = (L * N, N, 0)
+    else:
+        sb, st, sd = (int(v) for v in bc_strides)
+        if min(sb, st, sd) < 0:
+            raise ValueError("bc_strides must be non-negative")
+        need = 0 if L == 0 else (Bsz - 1) * sb + (L - 1) * st + (D - 1) * sd + N
+        for t, name in ((Bm, "Bm"), (Cm, "Cm")):
+            _need(t, name, dtype=io)
+            if t.numel() < need:
+                raise ValueError(f"{name} holds {t.numel()} elements; bc_strides address {need}")
+        if Bm.shape != Cm.shape:
+            raise ValueError(f"Cm shape {tuple(Cm.shape)} differs from Bm {tuple(Bm.shape)}")
+    return Bsz, L, D, N, io, (KM_BF16 if io == torch.bfloat16 else KM_F32), bc_strides
+
+
 def scan1d_fwd(x, delta, A, Bm, Cm, y, *, h0=None, h_final=None, h_hist=None, h_ckpt=None,
                bc_strides=None, clamp=True, z=None, Dskip=None, stream=None):
     """km_scan1d_fwd on torch device tensors.
 
-    x, delta, y: [B, L, D]; A: [D, N] fp32; Bm/Cm: [B, L, N] shared over
-    channels (default strides) or any layout described by bc_strides =
-    (sb, st, sd) in elements with N contiguous.
+    x, delta, y: [B, L, D] (one dtype: fp32 or bf16); A: [D, N] fp32;
+    Bm/Cm: [B, L, N] shared over channels (default strides) or any layout
+    described by bc_strides = (sb, st, sd) in elements with N contiguous;
+    h0 / h_final [B, D, N], h_hist [B, L, D, N], h_ckpt [B, ceil(L/64), D, N]
+    fp32; z [B, L, D] as x; Dskip [D] fp32. Every tensor must be contiguous
+    and on the GPU (ValueError otherwise).
     """
     import torch
-    Bsz, L, D = x.shape
-    N = A.shape[1]
-    if bc_strides is None:
-        assert Bm.shape == (Bsz, L, N) and Bm.is_contiguous()
-        bc_strides = (L * N, N, 0)
-    dt = KM_BF16 if x.dtype == torch.bfloat16 else KM_F32
+    Bsz, L, D, N, io, dt, bc_strides = _scan1d_io(x, A, Bm, Cm, bc_strides)
+    _need(delta, "delta", shape=x.shape, dtype=io)
+    _need(y, "y", shape=x.shape, dtype=io, optional=True)
+    _need(z, "z", shape=x.shape, dtype=io, optional=True)
+    _need(Dskip, "Dskip", shape=(D,), dtype=torch.float32, optional=True)
+    _need(h0, "h0", shape=(Bsz, D, N), dtype=torch.float32, optional=True)
+    _need(h_final, "h_final", shape=(Bsz, D, N), dtype=torch.float32, optional=True)
+    _need(h_hist, "h_hist", shape=(Bsz, L, D, N), dtype=torch.float32, optional=True)
+    nck = (L + KM_SCAN1D_CKPT_STEPS - 1) // KM_SCAN1D_CKPT_STEPS
+    _need(h_ckpt, "h_ckpt", shape=(Bsz, nck, D, N), dtype=torch.float32, optional=True)
+    _on_gpu(x=x, delta=delta, A=A, Bm=Bm, Cm=Cm, y=y, z=z, Dskip=Dskip, h0=h0, h_final=h_final,
+            h_hist=h_hist, h_ckpt=h_ckpt)
     args = KMScan1DFwd(ptr(x), ptr(delta), ptr(A), ptr(Bm), ptr(Cm), ptr(y), ptr(h0),
                        ptr(h_final), ptr(h_hist), Bsz, L, D, N, *bc_strides, dt, int(clamp),
                        ptr(h_ckpt), ptr(z), ptr(Dskip))
@@ -285,14 +355,26 @@ def scan1d_fwd(x, delta, A, Bm, Cm, y, *, h0=None, h_final=None, h_hist=None, h_
 
 def scan1d_bwd_args(x, delta, A, Bm, Cm, dy, dx, ddelta, dA, dB, dC, *, h0=None, h_hist=None,
                     h_ckpt=None, bc_strides=None, clamp=True, workspace=None):
-    """KMScan1DBwd over torch device tensors (layouts as scan1d_fwd)."""
+    """KMScan1DBwd over torch device tensors (layouts as scan1d_fwd; dx,
+    ddelta, dy as x; dA [D, N] fp32; dB, dC [B, L, N] when B/C are shared
+    over channels, else the shape of Bm). Raises ValueError on a tensor of
+    the wrong device, dtype, shape or layout."""
     import torch
-    Bsz, L, D = x.shape
-    N = A.shape[1]
-    if bc_strides is None:
-        assert Bm.shape == (Bsz, L, N) and Bm.is_contiguous()
-        bc_strides = (L * N, N, 0)
-    dt = KM_BF16 if x.dtype == torch.bfloat16 else KM_F32
+    Bsz, L, D, N, io, dt, bc_strides = _scan1d_io(x, A, Bm, Cm, bc_strides)
+    for t, name in ((delta, "delta"), (dy, "dy"), (dx, "dx"), (ddelta, "ddelta")):
+        _need(t, name, shape=x.shape, dtype=io)
+    _need(dA, "dA", shape=(D, N), dtype=torch.float32)
+    gshape = (Bsz, L, N) if bc_strides[2] == 0 else tuple(Bm.shape)
+    _need(dB, "dB", shape=gshape, dtype=io)
+    _need(dC, "dC", shape=gshape, dtype=io)
+    _need(h0, "h0", shape=(Bsz, D, N), dtype=torch.float32, optional=True)
+    _need(h_hist, "h_hist", shape=(Bsz, L, D, N), dtype=torch.float32, optional=True)
+    nck = (L + KM_SCAN1D_CKPT_STEPS - 1) // KM_SCAN1D_CKPT_STEPS
+    _need(h_ckpt, "h_ckpt", shape=(Bsz, nck, D, N), dtype=torch.float32, optional=True)
+    if workspace is not None:
+        _need(workspace, "workspace")
+    _on_gpu(x=x, delta=delta, A=A, Bm=Bm, Cm=Cm, dy=dy, dx=dx, ddelta=ddelta, dA=dA, dB=dB, dC=dC,
+            h0=h0, h_hist=h_hist, h_ckpt=h_ckpt, workspace=workspace)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     return KMScan1DBwd(ptr(x), ptr(delta), ptr(A), ptr(Bm), ptr(Cm), ptr(dy), ptr(h0), ptr(h_hist),
                        ptr(h_ckpt), ptr(dx), ptr(ddelta), ptr(dA), ptr(dB), ptr(dC),

@@ -825,3 +825,21 @@ void orc_gemm_f32(const float *A, const float *B, float *C, long M, long K, long
         }
     }
 }
+
+/* SiLU and softplus of the reference (include/kmamba_kernels.h:35-37 and
+ * :47-49, applied elementwise by kernels/activations_f32.c:7-29):
+ * x / (1 + expf(-x)) and logf(1 + expf(x)), fp32, glibc expf/logf, no
+ * overflow guard (softplus of x > ~88.7 is +inf, SiLU of x < ~-88.7 is -0). */
+void orc_silu_f32(const float *x, float *y, long n) {
+    for (long i = 0; i < n; i++) {
+        const float den = 1.0f + expf(-x[i]);
+        y[i] = x[i] / den;
+    }
+}
+
+void orc_softplus_f32(const float *x, float *y, long n) {
+    for (long i = 0; i < n; i++) {
+        const float arg = 1.0f + expf(x[i]);
+        y[i] = logf(arg);
+    }
+}

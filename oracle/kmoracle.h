@@ -127,6 +127,12 @@ void orc_mamba3_forward(const OrcMamba3 *p, const float *input, float *output, l
  * contraction). Rows run in parallel; each element's order is fixed. */
 void orc_gemm_f32(const float *A, const float *B, float *C, long M, long K, long N);
 
+/* The reference activations (include/kmamba_kernels.h:35-49 through
+ * kernels/activations_f32.c:7-29): y[i] = x[i] / (1 + expf(-x[i])) and
+ * y[i] = logf(1 + expf(x[i])), fp32. */
+void orc_silu_f32(const float *x, float *y, long n);
+void orc_softplus_f32(const float *x, float *y, long n);
+
 /* ---- Wavefront / plan / topology -------------------------------------- */
 int  orc_wavefront_validate_dims(const long *dims, long ndims);
 long orc_wavefront_total_points(const long *dims, long ndims);

@@ -1,10 +1,13 @@
 """ctypes binding of the CPU oracle (test infrastructure only).
 
 Loads oracle/liboracle.so (the C restatement of the reference CPU path,
-kmoracle.c) and, when it was built in this container from /root/reference,
-oracle/_ref/libkmref.so (the reference's own C compiled in place). Only the
-tests, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
-module; the product never does.
+kmoracle.c). oracle/_ref/libkmref.so (the reference's own C compiled in
+place, built only where the reference tree exists) is loaded lazily, on the
+first access to `ref` or a use_ref=True call: only the CPU pin tests do that,
+so GPU test processes never load the compiled reference. REF_AVAILABLE says
+whether it was built, without loading it. Only the tests,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg import this module;
+the product never does.
 
 All wrappers take and return numpy float32 / int64 arrays.
 """
@@ -25,7 +28,9 @@ if not ORACLE_SO.exists():
 
 orc = C.CDLL(str(ORACLE_SO))
 orc_fast = C.CDLL(str(ORACLE_FAST_SO)) if ORACLE_FAST_SO.exists() else orc
-ref = C.CDLL(str(REF_SO)) if REF_SO.exists() else None
+REF_AVAILABLE = REF_SO.exists()
+_ref_lib = None
+_REF_SIGS = []   # signature setters run when the compiled reference is loaded
 
 vp = C.c_void_p
 lp = C.POINTER(C.c_long)
@@ -110,8 +115,17 @@ for _lib in {orc, orc_fast}:
     _sig(_lib, "orc_wavefront_total_points", C.c_long, [lp, C.c_long])
     _sig(_lib, "orc_wavefront_max_level", C.c_long, [lp, C.c_long])
     _sig(_lib, "orc_wavefront_row_major_offset", C.c_long, [lp, lp, C.c_long])
+    _sig(_lib, "orc_silu_f32", None, [vp, vp, C.c_long])
+    _sig(_lib, "orc_softplus_f32", None, [vp, vp, C.c_long])
 
-if ref is not None:
+def _load_ref():
+    """The compiled reference (oracle/_ref/libkmref.so), loaded on first use."""
+    global _ref_lib
+    if _ref_lib is not None:
+        return _ref_lib
+    if not REF_AVAILABLE:
+        raise RuntimeError(f"{REF_SO} not built (the reference tree is absent)")
+    ref = C.CDLL(str(REF_SO))
     _sig(ref, "scannd_ref", C.c_int, [C.POINTER(ScanNDParams)])
     _sig(ref, "convnd_forward_wavefront", None, [C.POINTER(ConvNDParams), C.POINTER(Plan)])
     _sig(ref, "convnd_backward_wavefront", None, [C.POINTER(ConvNDParams), C.POINTER(Plan)])
@@ -122,6 +136,8 @@ if ref is not None:
     _sig(ref, "wavefront_nd_level_size", C.c_long, [lp, C.c_long, C.c_long])
     _sig(ref, "kmr_test_scan1d_ref", None, [vp] * 7 + [C.c_long] * 3)
     _sig(ref, "kmr_test_scan1d_backward_forward_ref", None, [vp] * 7 + [C.c_long] * 3)
+    _sig(ref, "silu_f32", None, [vp, vp, C.c_long])
+    _sig(ref, "softplus_f32", None, [vp, vp, C.c_long])
     # The reference's scannd_ref shares one idx[] scratch array between the
     # OpenMP threads of its level loop (src/scan_nd.c:44 allocates it once,
     # every thread writes it at :89), so it races with more than one thread.
@@ -129,6 +145,17 @@ if ref is not None:
     # single OpenMP thread; the oracle's own loops name num_threads explicitly.
     ref.omp_set_num_threads.argtypes = [C.c_int]
     ref.omp_set_num_threads(1)
+    for setter in _REF_SIGS:
+        setter(ref)
+    _ref_lib = ref
+    return ref
+
+
+def __getattr__(name):
+    # `oracle.ref` is the compiled reference, loaded on first access.
+    if name == "ref":
+        return _load_ref()
+    raise AttributeError(f"module 'oracle' has no attribute {name!r}")
 
 
 # ---------------------------------------------------------------------------
@@ -260,7 +287,7 @@ def scannd_ref(dims, x, A, B, Cm, delta, *, nthreads=1, use_ref=False, fast=Fals
     y = np.zeros((Pn, D), np.float32)
     p, _keep = _nd_params(dims, x, A, B, Cm, delta, h, y)
     if use_ref:
-        rc = ref.scannd_ref(C.byref(p))
+        rc = _load_ref().scannd_ref(C.byref(p))
     else:
         rc = (orc_fast if fast else orc).orc_scannd_ref(C.byref(p), int(nthreads))
     if rc != 0:
@@ -315,6 +342,7 @@ def convnd_forward(dims, inp, kernel, bias, *, nthreads=1, use_ref=False, fast=F
     p = ConvNDParams(P(inp), P(kernel), P(bias), P(out), None, None, None, None,
                      dd, len(dims), D, K)
     if use_ref:
+        ref = _load_ref()
         plan = ref.km_wavefront_plan_create(dd, len(dims))
         ref.convnd_forward_wavefront(C.byref(p), plan)
         ref.km_wavefront_plan_free(plan)
@@ -334,6 +362,7 @@ def convnd_backward(dims, inp, kernel, dy, *, with_bias=True, use_ref=False):
     p = ConvNDParams(P(inp), P(kernel), None, None, P(dy), P(dinp), P(dker), P(dbias),
                      dd, len(dims), D, K)
     if use_ref:
+        ref = _load_ref()
         plan = ref.km_wavefront_plan_create(dd, len(dims))
         ref.convnd_backward_wavefront(C.byref(p), plan)
         ref.km_wavefront_plan_free(plan)
@@ -348,7 +377,7 @@ def convnd_backward(dims, inp, kernel, dy, *, with_bias=True, use_ref=False):
 def plan_tables(dims, use_ref=False):
     """(level_starts, level_offsets, max_level_size) as int64 arrays."""
     dd = longs(dims)
-    lib = ref if use_ref else orc
+    lib = _load_ref() if use_ref else orc
     create = lib.km_wavefront_plan_create if use_ref else lib.orc_plan_create
     free = lib.km_wavefront_plan_free if use_ref else lib.orc_plan_free
     pl = create(dd, len(dims))
@@ -398,7 +427,10 @@ MAMBA3_PARAMS = ("W_in", "W_out", "A_log", "W_B", "W_C", "delta_proj", "lambda_p
                  "theta")
 
 _sig(orc, "orc_mamba3_forward", None, [C.POINTER(OrcMamba3), vp, vp, C.c_long])
-if ref is not None:
+
+
+@_REF_SIGS.append
+def _ref_block_sigs(ref):
     _sig(ref, "mamba_block_create", C.POINTER(MambaBlock), [C.POINTER(MBConfig)])
     _sig(ref, "mamba_block_free", None, [C.POINTER(MambaBlock)])
     _sig(ref, "mamba_block_init", None, [C.POINTER(MambaBlock)])
@@ -433,7 +465,10 @@ class KMamba(C.Structure):                # ref include/kmamba.h:185-223 (CPU bu
 
 
 _sig(orc, "orc_gemm_f32", None, [vp, vp, vp, C.c_long, C.c_long, C.c_long])
-if ref is not None:
+
+
+@_REF_SIGS.append
+def _ref_model_sigs(ref):
     _sig(ref, "kmamba_create", C.POINTER(KMamba), [C.POINTER(KMambaConfig)])
     _sig(ref, "kmamba_free", None, [C.POINTER(KMamba)])
     _sig(ref, "kmamba_init", C.c_int, [C.POINTER(KMamba), C.c_uint32])
@@ -462,6 +497,28 @@ def model_params(m):
     layers = [block_params(C.cast(m.contents.layers[i], C.POINTER(MambaBlock)))
               for i in range(c.n_layers)]
     return emb, head, layers
+
+
+def silu(v, *, use_ref=False):
+    """The reference SiLU x / (1 + expf(-x)) (include/kmamba_kernels.h:35-37),
+    elementwise in fp32: the oracle's restatement, or with use_ref the
+    compiled reference's silu_f32 (kernels/activations_f32.c:7-11)."""
+    v = f32(v)
+    out = np.empty_like(v)
+    fn = _load_ref().silu_f32 if use_ref else orc.orc_silu_f32
+    fn(P(v), P(out), v.size)
+    return out
+
+
+def softplus(v, *, use_ref=False):
+    """The reference softplus logf(1 + expf(x)) (include/kmamba_kernels.h:47-49),
+    elementwise in fp32: the oracle's restatement, or with use_ref the
+    compiled reference's softplus_f32 (kernels/activations_f32.c:25-29)."""
+    v = f32(v)
+    out = np.empty_like(v)
+    fn = _load_ref().softplus_f32 if use_ref else orc.orc_softplus_f32
+    fn(P(v), P(out), v.size)
+    return out
 
 
 def gemm_f32(A, B):
@@ -529,6 +586,7 @@ def mamba3_forward(params, x, *, dt_scale=0.1, dt_min=1e-3, dt_max=0.1, use_ref=
     R = params["W_in"].shape[0]
     out = np.zeros_like(x)
     if use_ref:
+        ref = _load_ref()
         blk = ref.mamba_block_create(C.byref(mb_config(D, N, L, R, dt_scale, dt_min, dt_max)))
         if not blk:
             raise RuntimeError("reference mamba_block_create failed")

@@ -114,25 +114,28 @@ def scan1d_bwd_kappa(x, dt, A, Bm, Cm, dy, *, h0=None, bc_strides=None, fast=Tru
 
 
 def silu_ref(v):
-    """x / (1 + e^-x) in fp32 (reference include/kmamba_kernels.h:35-37)."""
-    v = np.asarray(v, dtype=np.float32)
-    with np.errstate(over="ignore"):
-        return (v / (np.float32(1) + np.exp(-v))).astype(np.float32)
+    """x / (1 + e^-x) in fp32 (reference include/kmamba_kernels.h:35-37):
+    the oracle's C restatement, pinned bit-exact against the compiled
+    reference's silu_f32 in test_mamba1_oracle_pins.py."""
+    import oracle as O
+    return O.silu(v)
 
 
 def softplus_ref(v):
-    """log(1 + e^x) in fp32 (reference include/kmamba_kernels.h:47-49)."""
-    v = np.asarray(v, dtype=np.float32)
-    with np.errstate(over="ignore"):
-        return np.log(np.float32(1) + np.exp(v)).astype(np.float32)
+    """log(1 + e^x) in fp32 (reference include/kmamba_kernels.h:47-49): the
+    oracle's C restatement, pinned bit-exact against the compiled
+    reference's softplus_f32 in test_mamba1_oracle_pins.py."""
+    import oracle as O
+    return O.softplus(v)
 
 
-def mamba1_block_ref(x, w, *, store_bf16=False, clamp=True):
+def mamba1_block_ref(x, w, *, store_bf16=False, clamp=True, parts=False):
     """The configs[4] Mamba-1 block composed from the oracle pieces, fp32:
     numpy projections, the oracle's causal convnd (1D) per batch element,
     the reference activations and the oracle Scan1D. store_bf16 rounds the
     activations to bf16 where the GPU path stores them. x [B, L, dim];
-    w: dict of numpy arrays (bf16-valued weights as fp32)."""
+    w: dict of numpy arrays (bf16-valued weights as fp32). With parts=True
+    the intermediates (xi, z, u, delta, B, C, scan, y) are returned too."""
     import oracle as O
     rnd = bf16_round if store_bf16 else (lambda a: np.asarray(a, np.float32))
     x = np.asarray(x, np.float32)
@@ -155,8 +158,11 @@ def mamba1_block_ref(x, w, *, store_bf16=False, clamp=True):
     Bm = np.ascontiguousarray(xdbl[:, R:R + N].reshape(Bsz, L, N))
     Cm = np.ascontiguousarray(xdbl[:, R + N:].reshape(Bsz, L, N))
     ys, _, _ = O.scan1d_batched(u, delta, w["A"], Bm, Cm, clamp=clamp, nthreads=8, fast=True)
+    yg = ys
     if w.get("Dskip") is not None:
-        ys = ys + w["Dskip"] * u
-    y = rnd(ys * silu_ref(z))
-    out = y.reshape(T, di) @ w["W_out"].T
-    return out.reshape(Bsz, L, dim).astype(np.float32)
+        yg = ys + w["Dskip"] * u
+    y = rnd(yg * silu_ref(z))
+    out = (y.reshape(T, di) @ w["W_out"].T).reshape(Bsz, L, dim).astype(np.float32)
+    if parts:
+        return out, dict(xi=xi, z=z, u=u, delta=delta, B=Bm, C=Cm, scan=ys, y=y)
+    return out

@@ -16,7 +16,7 @@ import kmamba as K
 import oracle as O
 
 ROOT = Path(__file__).resolve().parent.parent
-needs_ref = pytest.mark.skipif(O.ref is None, reason="oracle/_ref not built (reference tree absent)")
+needs_ref = pytest.mark.skipif(not O.REF_AVAILABLE, reason="oracle/_ref not built (reference tree absent)")
 
 
 def header_functions():
@@ -426,3 +426,100 @@ def test_kmamba_create_and_load_errors(tmp_path):
     _assert_same_params(_model_arrays(loaded), _model_arrays(m))
     K.kmamba_free(loaded)
     K.kmamba_free(m)
+
+
+def test_scan1d_wrappers_reject_mismatched_tensors():
+    # The Python mirror checks dtype, shape and layout before an address goes
+    # to the C ABI (a bf16 y beside an fp32 x would make the kernel write past
+    # y). These errors are raised before any device check, so they run here.
+    torch = pytest.importorskip("torch")
+    Bsz, L, D, N = 2, 8, 4, 8
+    x = torch.zeros((Bsz, L, D))
+    dt = torch.zeros((Bsz, L, D))
+    A = torch.zeros((D, N))
+    Bm = torch.zeros((Bsz, L, N))
+    Cm = torch.zeros((Bsz, L, N))
+    y = torch.zeros((Bsz, L, D))
+    with pytest.raises(ValueError, match="y has dtype"):
+        K.scan1d_fwd(x, dt, A, Bm, Cm, y.bfloat16())
+    with pytest.raises(ValueError, match="delta has shape"):
+        K.scan1d_fwd(x, dt[:, :4], A, Bm, Cm, y)
+    with pytest.raises(ValueError, match="x must be contiguous"):
+        K.scan1d_fwd(x.transpose(1, 2).contiguous().transpose(1, 2), dt, A, Bm, Cm, y)
+    with pytest.raises(ValueError, match="Cm has shape"):
+        K.scan1d_fwd(x, dt, A, Bm, Cm[:, :, :2], y)
+    with pytest.raises(ValueError, match="A has dtype"):
+        K.scan1d_fwd(x, dt, A.double(), Bm, Cm, y)
+    with pytest.raises(ValueError, match="h_final has shape"):
+        K.scan1d_fwd(x, dt, A, Bm, Cm, y, h_final=torch.zeros((Bsz, N, D)))
+    with pytest.raises(ValueError, match="Bm holds"):
+        K.scan1d_fwd(x, dt, A, Bm, Cm, y, bc_strides=(L * D * N, D * N, N))
+    with pytest.raises(ValueError, match="must be a GPU tensor"):
+        K.scan1d_fwd(x, dt, A, Bm, Cm, y)
+    g = torch.zeros((Bsz, L, D))
+    with pytest.raises(ValueError, match="dA has shape"):
+        K.scan1d_bwd_args(x, dt, A, Bm, Cm, g, g, g, torch.zeros((N, D)), Bm, Cm)
+    with pytest.raises(ValueError, match="dB has dtype"):
+        K.scan1d_bwd_args(x, dt, A, Bm, Cm, g, g, g, torch.zeros((D, N)), Bm.bfloat16(), Cm)
+
+
+@needs_ref
+def test_topology_bit_exact_vs_reference():
+    # Every topology helper against the compiled reference on random and
+    # edge-case inputs: wrapping products, invalid ranks, zero/negative
+    # extents, out-of-range coordinates, the implicit 1D topology.
+    ref = O.ref
+    lp = C.POINTER(C.c_long)
+    for lib in (ref, K.lib):
+        lib.km_power_long.restype = C.c_long
+        lib.km_power_long.argtypes = [C.c_long, C.c_long]
+        lib.km_make_row_major_strides.restype = C.c_int
+        lib.km_make_row_major_strides.argtypes = [lp, C.c_long, lp]
+        lib.km_ravel_index.restype = C.c_long
+        lib.km_ravel_index.argtypes = [lp, lp, lp, C.c_long]
+        lib.km_unravel_index.restype = None
+        lib.km_unravel_index.argtypes = [C.c_long, lp, lp, C.c_long, lp]
+        lib.km_spatial_dims_product.restype = C.c_int
+        lib.km_spatial_dims_product.argtypes = [lp, C.c_long, C.POINTER(C.c_size_t)]
+        lib.km_normalize_spatial_topology.restype = C.c_int
+        lib.km_normalize_spatial_topology.argtypes = [lp, lp, C.c_size_t, C.c_int, lp, C.c_long]
+    g = np.random.default_rng(11)
+    for base in (-7, -2, -1, 0, 1, 2, 3, 10, 1 << 20, (1 << 62) + 3):
+        for e in (-3, -1, 0, 1, 2, 5, 31, 63, 64, 65, 200):
+            assert K.lib.km_power_long(base, e) == ref.km_power_long(base, e), (base, e)
+    shapes = [(3,), (2, 3, 4), (1, 1, 1, 1), (7, 5), (1 << 20, 1 << 20, 1 << 20, 1 << 10),
+              (2,) * 8, (2,) * 9, (4, 0, 2), (4, -1), ()]
+    for dims in shapes:
+        n = len(dims)
+        dd = K.longs(dims) if n else (C.c_long * 1)()
+        s1, s2 = (C.c_long * 9)(), (C.c_long * 9)()
+        r1 = K.lib.km_make_row_major_strides(dd, n, s1)
+        r2 = ref.km_make_row_major_strides(dd, n, s2)
+        assert r1 == r2 and list(s1) == list(s2), dims
+        p1, p2 = C.c_size_t(77), C.c_size_t(77)
+        assert (K.lib.km_spatial_dims_product(dd, n, C.byref(p1)) ==
+                ref.km_spatial_dims_product(dd, n, C.byref(p2))) and p1.value == p2.value, dims
+        if r1 != 1:
+            continue
+        for _ in range(50):
+            co = (C.c_long * 9)(*[int(g.integers(-1, d + 1)) for d in dims])
+            assert K.lib.km_ravel_index(co, dd, s1, n) == ref.km_ravel_index(co, dd, s2, n)
+            lin = int(g.integers(-2, 1 << 40))
+            c1, c2 = (C.c_long * 9)(*([5] * 9)), (C.c_long * 9)(*([5] * 9))
+            K.lib.km_unravel_index(lin, dd, s1, n, c1)
+            ref.km_unravel_index(lin, dd, s2, n, c2)
+            assert list(c1) == list(c2), (dims, lin)
+    for nd0, dims, seq, conv, cnd in [(0, (), 12, 1, 0), (0, (), 12, 0, 0), (2, (3, 4), 12, 1, 0),
+                                      (2, (3, 4), 12, 1, 3), (2, (3, 4), 13, 0, 0),
+                                      (3, (2, 2, 3), 12, 1, 3), (1, (12,), 12, 1, -1),
+                                      (9, (1,) * 9, 1, 0, 0), (0, (), 0, 0, 0)]:
+        outs = []
+        for lib in (K.lib, ref):
+            nd = C.c_long(nd0)
+            sd = (C.c_long * 8)(*([9] * 8))
+            for i, v in enumerate(dims[:8]):
+                sd[i] = v
+            cn = C.c_long(cnd)
+            rc = lib.km_normalize_spatial_topology(C.byref(nd), sd, seq, conv, C.byref(cn), 3)
+            outs.append((rc, nd.value, list(sd), cn.value))
+        assert outs[0] == outs[1], (nd0, dims, seq, conv, cnd, outs)

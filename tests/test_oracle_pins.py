@@ -23,7 +23,7 @@ import oracle as O
 from kmtest import rng_for, rel_err
 
 ROOT = Path(__file__).resolve().parent.parent
-needs_ref = pytest.mark.skipif(O.ref is None, reason="oracle/_ref not built (reference tree absent)")
+needs_ref = pytest.mark.skipif(not O.REF_AVAILABLE, reason="oracle/_ref not built (reference tree absent)")
 
 
 def uniform(g, shape, lo, hi):

@@ -291,3 +291,31 @@ def test_config1_full_size_sampled():
     kap0 = scan1d_bwd_kappa(*args0)
     assert_close(got[3][:1], ref0[3], TOL_F32, "dB[b=0]", kap0[3])
     assert_close(got[4][:1], ref0[4], TOL_F32, "dC[b=0]", kap0[4])
+
+
+def test_config1_bf16_full_size_sampled():
+    # configs[1] backward with bf16 I/O (x, delta, B, C, dy and dx, ddelta,
+    # dB, dC bf16; A, dA and the states fp32) at full size, B=8 L=4096 D=1024
+    # N=16, states from the forward's checkpoints. Against the fp32 oracle of
+    # the unrounded inputs at the bf16 tolerance: dx, ddelta, dA on a sample
+    # of channels over every batch element (exact sub-problems per channel),
+    # dB, dC (sums over every channel) on batch elements 0 and 7 in full.
+    Bsz, L, D, N = 8, 4096, 1024, 16
+    x, dt, A, Bm, Cm = scan1d_inputs(Bsz, L, D, N, seed=0, tag="config1")
+    dy = dy_for(Bsz, L, D, seed=0)
+    got = run_bwd(x, dt, A, Bm, Cm, dy, mode="ckpt", bf16=True)
+    for gg in got:
+        assert np.isfinite(gg).all()
+    sel = np.sort(rng_for("bsel-bf16").choice(D, 24, replace=False))
+    args = (x[:, :, sel], dt[:, :, sel], A[sel], Bm, Cm, dy[:, :, sel])
+    ref, _ = oracle_bwd(*args)
+    kap = scan1d_bwd_kappa(*args)
+    assert_close(got[0][:, :, sel], ref[0], TOL_BF16, "bf16 dx", kap[0])
+    assert_close(got[1][:, :, sel], ref[1], TOL_BF16, "bf16 ddelta", kap[1])
+    assert_close(got[2][sel], ref[2], TOL_BF16, "bf16 dA", kap[2])
+    for b in (0, Bsz - 1):
+        argsb = (x[b:b + 1], dt[b:b + 1], A, Bm[b:b + 1], Cm[b:b + 1], dy[b:b + 1])
+        refb, _ = oracle_bwd(*argsb)
+        kapb = scan1d_bwd_kappa(*argsb)
+        assert_close(got[3][b:b + 1], refb[3], TOL_BF16, f"bf16 dB[b={b}]", kapb[3])
+        assert_close(got[4][b:b + 1], refb[4], TOL_BF16, f"bf16 dC[b={b}]", kapb[4])
