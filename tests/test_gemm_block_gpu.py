@@ -160,7 +160,12 @@ def test_block_vs_composed_oracle(Bsz, L, dim, di, N, dconv, R):
     e_b, e_f = normwise(got, ref_b), normwise(got, ref_f)
     assert e_b <= 1e-2, f"vs bf16-storage oracle {e_b:.3e}"
     assert e_f <= TOL_BF16, f"vs fp32 oracle {e_f:.3e}"
-    assert_close(got, ref_f, TOL_BF16, "block out vs fp32 oracle", _block_kappa(parts, w))
+    # Weights of std 0.2 drive |y| to ~1e4 and delta to ~15: rounding the
+    # activations to bf16 alone then moves single outputs by up to ~5 % of
+    # |y| |W_out| (the bf16-storage oracle scores 4.7e-2 against the fp32
+    # oracle here), so elementwise the GPU is held to the oracle that rounds
+    # where it stores.
+    assert_close(got, ref_b, TOL_BF16, "block out vs bf16-storage oracle", _block_kappa(parts, w))
 
 
 def _block_kappa(parts, w):
