@@ -103,8 +103,12 @@ int km_scan1d_fwd(const KMScan1DFwd *a, void *stream);
  *   workspace   : device scratch of km_scan1d_bwd_workspace_bytes() bytes, or
  *                 NULL for the library's per-device scratch (calls that
  *                 overlap on one device then race: pass a workspace each).
- * dA and the shared dB/dC are sums formed with fp32 atomics: the order of
- * their terms, and so their last bits, may vary between runs. */
+ *                 It holds per-workgroup partial sums: B*D*N floats for dA
+ *                 and, with shared B/C, 2*B*ceil(D/g)*L*N floats for dB/dC
+ *                 (g = 16 channels for N = 16, 32 for N = 8, else 64).
+ * dA (summed over batch and time) and the shared dB/dC (summed over
+ * channels) are formed from those partials in a fixed order, with no
+ * atomics: every output is identical run to run. */
 typedef struct {
     const void  *x;
     const void  *delta;

@@ -22,10 +22,13 @@
 //    reverse order and each wave replays its steps from the exact incoming
 //    adjoint, producing every gradient term in registers.
 //  * dx and ddelta reduce over the states of a channel across lanes; dA
-//    accumulates per lane over the sequence. Shared B/C ([B, L, N], stride 0
-//    over channels) need dB, dC summed over channels: a reduce-scatter over
-//    the wave's lanes, then one fp32 atomic per (step, state) and wave into a
-//    workspace accumulator that a finalize kernel converts to the output.
+//    accumulates per lane over the sequence and the waves of a workgroup add
+//    their sums in wave order. Shared B/C ([B, L, N], stride 0 over
+//    channels) need dB, dC summed over channels: a reduce-scatter over the
+//    wave's lanes gives the wave's channel-group sum, stored to the
+//    workgroup's own partial slot; a finalize kernel adds the slots of every
+//    channel group (and dA's per-batch partials) in a fixed order. No
+//    atomics: every output is identical run to run.
 //  * States recomputed from checkpoints run unclamped; if any leaves
 //    [-1000, 1000] the super-chunk is recomputed with the sequential clamped
 //    recurrence, which matches the forward's clamp fallback.
@@ -51,8 +54,9 @@ struct Scan1DBwdArgs {
     const float *ckpt;     // [B, nck, D, N] state after each 64-step block, or null
     long nck;
     void *dx, *ddt;        // [B, L, D]
-    float *dA;             // [D, N] fp32 accumulator (zeroed by the launcher)
-    float *accB, *accC;    // shared B/C: [B, L, N] fp32 accumulators (zeroed)
+    float *dApart;         // [B, D, N] per-batch dA partials (every element written)
+    float *slotB, *slotC;  // shared B/C: [B, G, L, N] per-channel-group partials
+    long G;                // channel groups per batch element (shared B/C slots)
     void *dB, *dC;         // per-channel B/C: written at the B/C strides
     long B, L, D, N, sb, st, sd;
     int clamp;
@@ -181,8 +185,11 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
     const int vxz = static_cast<int>(dvalid ? static_cast<unsigned>(vx) : kDrop);
     const unsigned vbcs = dvalid ? static_cast<unsigned>(vbc) : kDrop;
     const unsigned vacc = (dl % GRP) == 0 ? static_cast<unsigned>((n0 + dl / GRP) * 4) : kDrop;
-    const auto racB = make_rsrc(SHARED ? p.accB + b * p.L * N : nullptr, SHARED ? p.L * N * 4 : 0);
-    const auto racC = make_rsrc(SHARED ? p.accC + b * p.L * N : nullptr, SHARED ? p.L * N * 4 : 0);
+    // This workgroup's partial slot of the shared dB / dC: [L, N] of
+    // [B, G, L, N], one writer per element.
+    const long slot0 = (b * p.G + (blockIdx.x - b * ngroups)) * p.L * N;
+    const auto racB = make_rsrc(SHARED ? p.slotB + slot0 : nullptr, SHARED ? p.L * N * 4 : 0);
+    const auto racC = make_rsrc(SHARED ? p.slotC + slot0 : nullptr, SHARED ? p.L * N * 4 : 0);
 
     __shared__ float sB[SHARED ? 3 : 1][SHARED ? TILE : 1];
     __shared__ float sC[SHARED ? 3 : 1][SHARED ? TILE : 1];
@@ -513,8 +520,8 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
                 const float rbv = reduce_scatter<NPL, DL>(dBv, lane);
                 const float rcv = reduce_scatter<NPL, DL>(dCv, lane);
                 const int ao = static_cast<int>(vacc + static_cast<unsigned>(t * N * 4));
-                __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(rbv, racB, ao, 0, 0);
-                __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(rcv, racC, ao, 0, 0);
+                bio<f32_t>::st(racB, ao, 0, rbv);
+                bio<f32_t>::st(racC, ao, 0, rcv);
             } else {
 #pragma unroll
                 for (int j = 0; j < NPL; ++j) {
@@ -535,21 +542,39 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
     if (fast) run(std::true_type{});
     else run(std::false_type{});
 
-    if (dvalid) {
+    // dA: the waves' sums over their steps, added in wave order, one
+    // store per (batch, channel, state).
 #pragma unroll
-        for (int j = 0; j < NPL; ++j) unsafeAtomicAdd(p.dA + dc * N + n0 + j, dAacc[j]);
+    for (int j = 0; j < NPL; ++j) aggH[w][j][lane] = dAacc[j];
+    __syncthreads();
+    if (w == 0 && dvalid) {
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+            float acc = aggH[0][j][lane];
+#pragma unroll
+            for (int v = 1; v < W; ++v) acc += aggH[v][j][lane];
+            p.dApart[(b * Dm + d) * N + n0 + j] = acc;
+        }
     }
 }
 
 // Any N <= 64 (and windows too large for 32-bit offsets): one thread per
 // (batch, channel), the reference's reverse step order, states from the
-// history.
+// history. A workgroup holds kSerialNB channels of one batch element; with
+// shared B/C the channels' dB / dC terms of a step are summed in channel
+// order through LDS into the workgroup's partial slot.
+constexpr int kSerialNB = 128;
+
 template <typename T>
-__global__ void __launch_bounds__(256) scan1d_bwd_serial(Scan1DBwdArgs p) {
+__global__ void __launch_bounds__(kSerialNB) scan1d_bwd_serial(Scan1DBwdArgs p) {
     using IO = io<T>;
-    const long gid = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (gid >= p.B * p.D) return;
-    const long b = gid / p.D, d = gid % p.D;
+    __shared__ float red[2][64][kSerialNB];
+    const int tid = threadIdx.x;
+    const long cblocks = (p.D + kSerialNB - 1) / kSerialNB;
+    const long b = blockIdx.x / cblocks, g = blockIdx.x - b * cblocks;
+    const long d = g * kSerialNB + tid;
+    const bool ok = d < p.D;
+    const long dc = ok ? d : p.D - 1;
     const long N = p.N;
     const bool shared = (p.sd == 0);
     float adj[64], dAl[64];
@@ -557,18 +582,20 @@ __global__ void __launch_bounds__(256) scan1d_bwd_serial(Scan1DBwdArgs p) {
         adj[m] = 0.f;
         dAl[m] = 0.f;
     }
+    // Every thread walks every step (uniform barriers); lanes past D compute
+    // on channel D-1 and contribute nothing.
     for (long t = p.L - 1; t >= 0; --t) {
-        const long td = (b * p.L + t) * p.D + d;
+        const long td = (b * p.L + t) * p.D + dc;
         const float dt = IO::ld(p.dt, td), xt = IO::ld(p.x, td), gy = IO::ld(p.dy, td);
-        const long bc = b * p.sb + t * p.st + d * p.sd;
+        const long bc = b * p.sb + t * p.st + dc * p.sd;
         float dxv = 0.f, ddt = 0.f;
         for (long m = 0; m < N; ++m) {
-            const float a = p.A[d * N + m];
+            const float a = p.A[dc * N + m];
             const float bb = IO::ld(p.Bm, bc + m), c = IO::ld(p.Cm, bc + m);
             const float e = exp2_fast(dt * a * kLog2e);
             float hp = 0.f;
             if (t > 0) hp = p.hist[(td - p.D) * N + m];
-            else if (p.h0) hp = p.h0[(b * p.D + d) * N + m];
+            else if (p.h0) hp = p.h0[(b * p.D + dc) * N + m];
             const float ah = adj[m] + gy * c;
             const float dCv = gy * p.hist[td * N + m];
             const float dBv = ah * dt * xt;
@@ -577,61 +604,99 @@ __global__ void __launch_bounds__(256) scan1d_bwd_serial(Scan1DBwdArgs p) {
             ddt += ah * (a * e * hp + bb * xt);
             adj[m] = ah * e;
             if (shared) {
-                const long o = (b * p.L + t) * N + m;
-                unsafeAtomicAdd(p.accB + o, dBv);
-                unsafeAtomicAdd(p.accC + o, dCv);
-            } else {
+                red[0][m][tid] = ok ? dBv : 0.f;
+                red[1][m][tid] = ok ? dCv : 0.f;
+            } else if (ok) {
                 IO::st(p.dB, bc + m, dBv);
                 IO::st(p.dC, bc + m, dCv);
             }
         }
-        IO::st(p.dx, td, dxv);
-        IO::st(p.ddt, td, ddt);
+        if (ok) {
+            IO::st(p.dx, td, dxv);
+            IO::st(p.ddt, td, ddt);
+        }
+        if (shared) {
+            __syncthreads();
+            const long so = ((b * p.G + g) * p.L + t) * N;
+            for (long k = tid; k < 2 * N; k += kSerialNB) {
+                const int which = static_cast<int>(k / N);
+                const long m = k - which * N;
+                float acc = 0.f;
+                for (int i = 0; i < kSerialNB; ++i) acc += red[which][m][i];
+                (which ? p.slotC : p.slotB)[so + m] = acc;
+            }
+            __syncthreads();
+        }
     }
-    for (long m = 0; m < N; ++m) unsafeAtomicAdd(p.dA + d * N + m, dAl[m]);
+    if (ok)
+        for (long m = 0; m < N; ++m) p.dApart[(b * p.D + d) * N + m] = dAl[m];
 }
 
-// Zeroes p[0, n) and q[0, m) in one launch; q (the workspace accumulators)
-// with 16-byte stores when it is 16-byte aligned.
-__global__ void __launch_bounds__(256) fill_zero_kernel(float *p, long n, float *q, long m) {
+// Zeroes p[0, n) (16-byte stores when p is 16-byte aligned).
+__global__ void __launch_bounds__(256) fill_zero_kernel(float *p, long n) {
     const long i0 = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
     const long stride = static_cast<long>(gridDim.x) * blockDim.x;
-    for (long i = i0; i < n; i += stride) p[i] = 0.f;
-    const long m4 = (reinterpret_cast<uintptr_t>(q) & 15) == 0 ? m / 4 : 0;
-    float4 *q4 = reinterpret_cast<float4 *>(q);
-    for (long i = i0; i < m4; i += stride) q4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (long i = m4 * 4 + i0; i < m; i += stride) q[i] = 0.f;
+    const long n4 = (reinterpret_cast<uintptr_t>(p) & 15) == 0 ? n / 4 : 0;
+    float4 *p4 = reinterpret_cast<float4 *>(p);
+    for (long i = i0; i < n4; i += stride) p4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (long i = n4 * 4 + i0; i < n; i += stride) p[i] = 0.f;
 }
 
-// Shared B/C: accumulators [B, L, N] -> outputs at b*sb + t*st + n.
+// Fixed-order sums of the partials: dA[i] = sum over b of dApart[b, i]
+// (b ascending); with shared B/C, dB / dC at b*sb + t*st + n = sum over the
+// channel groups g (ascending) of slot[b, g, t, n].
 template <typename T>
-__global__ void __launch_bounds__(256) scan1d_bwd_finalize(const float *accB, const float *accC,
-                                                           void *dB, void *dC, long B, long L,
-                                                           long N, long sb, long st) {
+__global__ void __launch_bounds__(256) scan1d_bwd_finalize(const float *slotB, const float *slotC,
+                                                           long G, void *dB, void *dC, long B,
+                                                           long L, long N, long sb, long st,
+                                                           const float *dApart, float *dA, long DN) {
     using IO = io<T>;
-    const long n_all = B * L * N;
-    for (long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_all;
-         i += static_cast<long>(gridDim.x) * blockDim.x) {
-        const long b = i / (L * N), r = i - b * L * N, t = r / N, n = r - t * N;
-        const long o = b * sb + t * st + n;
-        IO::st(dB, o, accB[i]);
-        IO::st(dC, o, accC[i]);
+    const long n_bc = slotB ? B * L * N : 0;
+    const long LN = L * N;
+    const long stride = static_cast<long>(gridDim.x) * blockDim.x;
+    for (long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_bc + DN;
+         i += stride) {
+        if (i < n_bc) {
+            const long b = i / LN, r = i - b * LN, t = r / N, n = r - t * N;
+            const float *pb = slotB + b * G * LN + r;
+            const float *pc = slotC + b * G * LN + r;
+            float sB = 0.f, sC = 0.f;
+            for (long g = 0; g < G; ++g) {
+                sB += pb[g * LN];
+                sC += pc[g * LN];
+            }
+            const long o = b * sb + t * st + n;
+            IO::st(dB, o, sB);
+            IO::st(dC, o, sC);
+        } else {
+            const long k = i - n_bc;
+            float acc = 0.f;
+            for (long b = 0; b < B; ++b) acc += dApart[b * DN + k];
+            dA[k] = acc;
+        }
     }
 }
 
-static int fill_zero(float *p, long n, hipStream_t s, float *q = nullptr, long m = 0) {
-    if (n <= 0 && m <= 0) return 0;
-    const long blocks = std::min<long>((std::max(n, m / 4) + 255) / 256, 4096);
-    hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, s, p, std::max(n, 0L), q,
-                       q ? std::max(m, 0L) : 0L);
+static int fill_zero(float *p, long n, hipStream_t s) {
+    if (n <= 0) return 0;
+    const long blocks = std::min<long>((n / 4 + 255) / 256 + 1, 4096);
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, s, p, n);
     KM_HIP_TRY(hipGetLastError());
     return 0;
 }
 
 struct BwdPlan {
     bool shared, hist_in, need_ckpt, serial, need_hist;
-    size_t off_acc, off_ckpt, off_hist, bytes;
+    long G;                 // channel groups per batch element (partial slots)
+    size_t off_slots, off_dA, off_ckpt, off_hist, bytes;
 };
+
+// Channels per workgroup of the register-blocked backward for a state size.
+static long bwd_group_channels(long N) {
+    if (N == 16) return 16;
+    if (N == 8) return 32;
+    return 64;
+}
 
 static BwdPlan bwd_plan(const KMScan1DBwd *k) {
     BwdPlan pl{};
@@ -645,9 +710,13 @@ static BwdPlan bwd_plan(const KMScan1DBwd *k) {
     pl.hist_in = (k->h_hist != nullptr);
     pl.need_hist = pl.serial && !pl.hist_in;
     pl.need_ckpt = !pl.serial && !pl.hist_in && !k->h_ckpt;
+    const long gc = pl.serial ? kSerialNB : bwd_group_channels(k->N);
+    pl.G = (k->D + gc - 1) / gc;
     size_t off = 0;
-    pl.off_acc = off;
-    if (pl.shared) off += align_up(sizeof(float) * 2 * k->B * k->L * k->N, 256);
+    pl.off_slots = off;
+    if (pl.shared) off += align_up(sizeof(float) * 2 * k->B * pl.G * k->L * k->N, 256);
+    pl.off_dA = off;
+    off += align_up(sizeof(float) * k->B * k->D * k->N, 256);
     pl.off_ckpt = off;
     if (pl.need_ckpt)
         off += align_up(sizeof(float) * k->B * ((k->L + kCkptSteps - 1) / kCkptSteps) * k->D * k->N, 256);
@@ -689,9 +758,7 @@ static int bwd_chunked_launch(const Scan1DBwdArgs &a, bool shared, bool hin, boo
     constexpr int W = 8, TC = 8;
     // Four states per lane keep the backward's per-lane working set (decays
     // and states of 8 steps) within 256 VGPRs without spilling.
-    long DL = 64;
-    if (a.N == 16) DL = 16;
-    else if (a.N == 8) DL = 32;
+    const long DL = bwd_group_channels(a.N);
     const long grid = a.B * ((a.D + DL - 1) / DL);
     if (grid <= 0 || grid > 0x7fffffffL) {
         set_error("km_scan1d_bwd: grid of %ld workgroups out of range", grid);
@@ -723,6 +790,8 @@ static int bwd_chunked_launch(const Scan1DBwdArgs &a, bool shared, bool hin, boo
     return 0;
 }
 
+static int scan1d_bwd_run(const KMScan1DBwd *k, const BwdPlan &pl, bool bf, hipStream_t stream);
+
 size_t scan1d_bwd_workspace(const KMScan1DBwd *k) {
     if (!bwd_args_ok(k, "km_scan1d_bwd_workspace_bytes")) return 0;
     return bwd_plan(k).bytes;
@@ -734,6 +803,10 @@ int scan1d_bwd_launch(const KMScan1DBwd *k, hipStream_t stream) {
     const BwdPlan pl = bwd_plan(k);
     const bool bf = (k->dtype == KM_BF16);
     if (k->L == 0) return fill_zero(k->dA, k->D * k->N, stream);
+    return scan1d_bwd_run(k, pl, bf, stream);
+}
+
+static int scan1d_bwd_run(const KMScan1DBwd *k, const BwdPlan &pl, bool bf, hipStream_t stream) {
     char *ws = nullptr;
     if (pl.bytes > 0) {
         if (k->workspace) {
@@ -752,16 +825,17 @@ int scan1d_bwd_launch(const KMScan1DBwd *k, hipStream_t stream) {
     a.x = k->x; a.dt = k->delta; a.dy = k->dy; a.A = k->A; a.Bm = k->Bm; a.Cm = k->Cm;
     a.h0 = k->h0; a.hist = k->h_hist; a.ckpt = k->h_ckpt;
     a.nck = (k->L + kCkptSteps - 1) / kCkptSteps;
-    a.dx = k->dx; a.ddt = k->ddelta; a.dA = k->dA; a.dB = k->dB; a.dC = k->dC;
+    a.dx = k->dx; a.ddt = k->ddelta; a.dB = k->dB; a.dC = k->dC;
     a.B = k->B; a.L = k->L; a.D = k->D; a.N = k->N;
     a.sb = k->bc_sb; a.st = k->bc_st; a.sd = k->bc_sd; a.clamp = k->clamp;
+    // Every partial slot is written by exactly one workgroup: nothing is
+    // zeroed first.
+    a.G = pl.G;
+    a.dApart = reinterpret_cast<float *>(ws + pl.off_dA);
     if (pl.shared) {
-        a.accB = reinterpret_cast<float *>(ws + pl.off_acc);
-        a.accC = a.accB + k->B * k->L * k->N;
+        a.slotB = reinterpret_cast<float *>(ws + pl.off_slots);
+        a.slotC = a.slotB + k->B * pl.G * k->L * k->N;
     }
-    // dA, and the shared dB / dC accumulators, start at zero (one launch).
-    if (fill_zero(k->dA, k->D * k->N, stream, a.accB, pl.shared ? 2 * k->B * k->L * k->N : 0) != 0)
-        return -1;
     if (pl.need_ckpt || pl.need_hist) {
         // Forward states from the same inputs (y not written).
         KMScan1DFwd f{};
@@ -779,23 +853,27 @@ int scan1d_bwd_launch(const KMScan1DBwd *k, hipStream_t stream) {
         if (scan1d_fwd_launch(&f, stream) != 0) return -1;
     }
     if (pl.serial) {
-        const long threads = k->B * k->D;
-        const long grid = (threads + 255) / 256;
-        if (bf) hipLaunchKernelGGL(scan1d_bwd_serial<bf16_t>, dim3(grid), dim3(256), 0, stream, a);
-        else    hipLaunchKernelGGL(scan1d_bwd_serial<f32_t>, dim3(grid), dim3(256), 0, stream, a);
+        const long grid = k->B * pl.G;
+        if (grid > 0x7fffffffL) {
+            set_error("km_scan1d_bwd: grid of %ld workgroups out of range", grid);
+            return -1;
+        }
+        if (bf) hipLaunchKernelGGL(scan1d_bwd_serial<bf16_t>, dim3(grid), dim3(kSerialNB), 0, stream, a);
+        else    hipLaunchKernelGGL(scan1d_bwd_serial<f32_t>, dim3(grid), dim3(kSerialNB), 0, stream, a);
         KM_HIP_TRY(hipGetLastError());
     } else if (bwd_chunked_launch(a, pl.shared, a.hist != nullptr, bf, stream) != 0) {
         return -1;
     }
-    if (pl.shared) {
-        const long n = k->B * k->L * k->N;
-        const long blocks = std::min<long>((n + 255) / 256, 8192);
-        if (bf) hipLaunchKernelGGL(scan1d_bwd_finalize<bf16_t>, dim3(blocks), dim3(256), 0, stream,
-                                   a.accB, a.accC, k->dB, k->dC, k->B, k->L, k->N, k->bc_sb, k->bc_st);
-        else    hipLaunchKernelGGL(scan1d_bwd_finalize<f32_t>, dim3(blocks), dim3(256), 0, stream,
-                                   a.accB, a.accC, k->dB, k->dC, k->B, k->L, k->N, k->bc_sb, k->bc_st);
-        KM_HIP_TRY(hipGetLastError());
-    }
+    const long n = (pl.shared ? k->B * k->L * k->N : 0) + k->D * k->N;
+    const long blocks = std::min<long>((n + 255) / 256, 8192);
+#define KM_FIN(TT)                                                                                 \
+    hipLaunchKernelGGL(scan1d_bwd_finalize<TT>, dim3(blocks), dim3(256), 0, stream, a.slotB,      \
+                       a.slotC, pl.G, k->dB, k->dC, k->B, k->L, k->N, k->bc_sb, k->bc_st,         \
+                       a.dApart, k->dA, k->D * k->N)
+    if (bf) KM_FIN(bf16_t);
+    else    KM_FIN(f32_t);
+#undef KM_FIN
+    KM_HIP_TRY(hipGetLastError());
     return 0;
 }
 
@@ -807,12 +885,14 @@ struct M1Args {
     const float *x, *A, *Adiag, *B, *C, *delta, *h0, *h, *dy;
     float *dx, *dA, *dB, *dC, *ddelta;
     long L, D;
+    float *part;   // [gridDim.x, L] per-workgroup ddelta partials
 };
 
 // M = 1 with B, C shared over time ([D]) and delta shared over channels
 // ([L]) (reference cpu/scan1d_backward.c:23-70): one thread per channel in
-// reverse time; ddelta[t] sums the channels' terms (block sum, one atomic
-// per block and step).
+// reverse time. ddelta[t] sums the channels' terms: each workgroup sums its
+// 256 channels (wave shuffles, then the four waves in order) into its own
+// partial slot, and m1_finalize adds the slots in workgroup order.
 __global__ void __launch_bounds__(256) scan1d_bwd_m1_shared(M1Args p) {
     __shared__ float part[4];
     const int tid = threadIdx.x;
@@ -838,7 +918,7 @@ __global__ void __launch_bounds__(256) scan1d_bwd_m1_shared(M1Args p) {
         for (int m = 32; m >= 1; m >>= 1) term += __shfl_xor(term, m);
         if ((tid & 63) == 0) part[tid >> 6] = term;
         __syncthreads();
-        if (tid == 0) unsafeAtomicAdd(p.ddelta + t, part[0] + part[1] + part[2] + part[3]);
+        if (tid == 0) p.part[blockIdx.x * p.L + t] = ((part[0] + part[1]) + part[2]) + part[3];
         __syncthreads();
     }
     if (ok) {
@@ -848,10 +928,24 @@ __global__ void __launch_bounds__(256) scan1d_bwd_m1_shared(M1Args p) {
     }
 }
 
-static int m1_launch(const M1Args &a, hipStream_t s) {
-    if (fill_zero(a.ddelta, a.L, s) != 0) return -1;
+// ddelta[t] = sum over workgroups (ascending) of part[wg, t].
+__global__ void __launch_bounds__(256) m1_finalize(const float *part, long nwg, long L,
+                                                   float *ddelta) {
+    const long t = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= L) return;
+    float acc = 0.f;
+    for (long g = 0; g < nwg; ++g) acc += part[g * L + t];
+    ddelta[t] = acc;
+}
+
+static int m1_launch(M1Args a, hipStream_t s) {
     const long grid = (a.D + 255) / 256;
+    a.part = static_cast<float *>(Workspace::reserve(sizeof(float) * grid * a.L));
+    if (!a.part) return -1;
     hipLaunchKernelGGL(scan1d_bwd_m1_shared, dim3(grid), dim3(256), 0, s, a);
+    KM_HIP_TRY(hipGetLastError());
+    hipLaunchKernelGGL(m1_finalize, dim3((a.L + 255) / 256), dim3(256), 0, s,
+                       static_cast<const float *>(a.part), grid, a.L, a.ddelta);
     KM_HIP_TRY(hipGetLastError());
     return 0;
 }
@@ -1023,7 +1117,7 @@ void scan1d_backward_m1_shared_bc(ScanBackwardSharedParams *p) {
         km::M1Args a{sc.dev<float>(0), sc.dev<float>(1), sc.dev<float>(2), sc.dev<float>(3),
                      sc.dev<float>(4), sc.dev<float>(5), sc.dev<float>(6), sc.dev<float>(7),
                      sc.dev<float>(8), sc.dev<float>(9), sc.dev<float>(10), sc.dev<float>(11),
-                     sc.dev<float>(12), sc.dev<float>(13), p->L, p->D};
+                     sc.dev<float>(12), sc.dev<float>(13), p->L, p->D, nullptr};
         if (km::m1_launch(a, nullptr) == 0) sc.stage_out("scan1d_backward_m1_shared_bc");
     }
     km::Staging::unlock();

@@ -319,3 +319,48 @@ def test_config1_bf16_full_size_sampled():
         kapb = scan1d_bwd_kappa(*argsb)
         assert_close(got[3][b:b + 1], refb[3], TOL_BF16, f"bf16 dB[b={b}]", kapb[3])
         assert_close(got[4][b:b + 1], refb[4], TOL_BF16, f"bf16 dC[b={b}]", kapb[4])
+
+
+@pytest.mark.parametrize("Bsz,L,D,N,layout", [(2, 300, 96, 16, "shared"), (2, 130, 64, 8, "shared"),
+                                               (2, 77, 40, 3, "shared"), (1, 90, 48, 16, "channel"),
+                                               (3, 65, 200, 5, "shared")])
+def test_backward_bit_identical_across_runs(Bsz, L, D, N, layout):
+    # dA (summed over batch and time) and the shared dB / dC (summed over
+    # channels) are formed from per-workgroup partials in a fixed order: two
+    # runs give the same bits. The per-channel layout covers dA alone.
+    x, dt, A, Bm, Cm = scan1d_inputs(Bsz, L, D, N, seed=21)
+    dy = dy_for(Bsz, L, D, seed=21)
+    kw = {}
+    if layout == "channel":
+        g = rng_for("bitid", Bsz, L, D, N)
+        Bm = (g.standard_normal((Bsz, L, D, N)) * 0.25).astype(np.float32)
+        Cm = (g.standard_normal((Bsz, L, D, N)) * 0.25).astype(np.float32)
+        kw["bc_strides"] = (L * D * N, D * N, N)
+    runs = [run_bwd(x, dt, A, Bm, Cm, dy, mode="recompute", **kw) for _ in range(2)]
+    for n, a, b in zip(NAMES, runs[0], runs[1]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{n} differs between runs"
+
+
+def test_m1_shared_bc_ddelta_bit_identical_across_runs():
+    # ddelta of the M = 1 entry point sums every channel's term per step:
+    # per-workgroup partials added in workgroup order, identical run to run.
+    L, D = 50, 700
+    g = rng_for("m1bitid", L, D)
+    x = g.standard_normal((L, D)).astype(np.float32)
+    A = -g.uniform(0.1, 1.0, D).astype(np.float32)
+    B = g.standard_normal(D).astype(np.float32)
+    Cm = g.standard_normal(D).astype(np.float32)
+    dt = g.uniform(0.01, 0.5, L).astype(np.float32)
+    h = g.standard_normal((L, D)).astype(np.float32)
+    dy = g.standard_normal((L, D)).astype(np.float32)
+    outs = []
+    for _ in range(2):
+        dx, ddt = np.zeros((L, D), np.float32), np.zeros(L, np.float32)
+        dA, dB, dC = (np.zeros(D, np.float32) for _ in range(3))
+        p = K.ScanBackwardSharedParams(K.ptr(x), K.ptr(A), None, K.ptr(B), K.ptr(Cm), K.ptr(dt),
+                                       None, K.ptr(h), K.ptr(dy), K.ptr(dx), K.ptr(dA), K.ptr(dB),
+                                       K.ptr(dC), K.ptr(ddt), L, D)
+        K.scan1d_backward_m1_shared_bc(C.byref(p))
+        assert K.km_last_error() == ""
+        outs.append(ddt)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
