@@ -921,7 +921,7 @@ static int conv_bwd_launch(const ConvArgs &a, hipStream_t s) {
     if (line_shape(a) && lblocks > 0 && lblocks + (a.KV + 1) * a.groups <= 0x7fffffffL && a.groups <= 65535 &&
         strip_fits(a)) {
         part = static_cast<float *>(
-            Workspace::reserve(sizeof(float) * a.groups * nslot * (a.KV + 1) * 64));
+            Workspace::reserve(sizeof(float) * a.groups * nslot * (a.KV + 1) * 64, s));
         if (!part) return -1;
     }
     if (part) {

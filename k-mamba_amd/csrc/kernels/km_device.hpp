@@ -168,6 +168,11 @@ template <> struct bio<f32_t> {
     static __device__ __forceinline__ void st(__amdgpu_buffer_rsrc_t r, int voff, int soff, float v) {
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, voff, soff, 0);
     }
+    // Agent-coherent load (cache policy sc1): misses the CU's L1 and reads
+    // the XCD's L2, so it sees stores another CU of the same XCD completed.
+    static __device__ __forceinline__ float ld_agent(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 16));
+    }
 };
 template <> struct bio<bf16_t> {
     static constexpr int size = 2;

@@ -140,7 +140,7 @@ int mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long B,
             return -1;
         }
     } else {
-        ws = static_cast<char *>(Workspace::reserve(lay.bytes));
+        ws = static_cast<char *>(Workspace::reserve(lay.bytes, s));
         if (!ws) return -1;
     }
     const long T = B * L, di = w->d_inner, N = w->d_state, R = w->dt_rank, NX = R + 2 * N;

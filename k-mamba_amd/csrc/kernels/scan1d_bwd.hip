@@ -817,7 +817,7 @@ static int scan1d_bwd_run(const KMScan1DBwd *k, const BwdPlan &pl, bool bf, hipS
             }
             ws = static_cast<char *>(k->workspace);
         } else {
-            ws = static_cast<char *>(Workspace::reserve(pl.bytes));
+            ws = static_cast<char *>(Workspace::reserve(pl.bytes, stream));
             if (!ws) return -1;
         }
     }
@@ -940,7 +940,7 @@ __global__ void __launch_bounds__(256) m1_finalize(const float *part, long nwg, 
 
 static int m1_launch(M1Args a, hipStream_t s) {
     const long grid = (a.D + 255) / 256;
-    a.part = static_cast<float *>(Workspace::reserve(sizeof(float) * grid * a.L));
+    a.part = static_cast<float *>(Workspace::reserve(sizeof(float) * grid * a.L, s));
     if (!a.part) return -1;
     hipLaunchKernelGGL(scan1d_bwd_m1_shared, dim3(grid), dim3(256), 0, s, a);
     KM_HIP_TRY(hipGetLastError());

@@ -25,6 +25,7 @@
 //    the left neighbour from the previous column; neighbours across the
 //    tile's boundary and along leading axes are read back from h.
 #include <cstdlib>
+#include <mutex>
 #include <cstring>
 
 #include <cstdio>
@@ -138,8 +139,10 @@ struct NDRow {
 
 // PL > 0 (3D, tiles of PL rows along axis 1): the wave also keeps the
 // previous plane's PL rows in registers, so only the tile's first plane reads
-// its axis-0 neighbours from h.
-template <int ND, int TW, int MM, int PL>
+// its axis-0 neighbours from h. COH: states written by other workgroups of
+// the same launch (the dataflow schedule) are read with agent-coherent loads
+// that bypass the CU's L1.
+template <int ND, int TW, int MM, int PL, bool COH = false>
 __device__ __forceinline__ void scannd_tile(const ScanNDArgs &p, const int (&ti)[kMaxNd], int cg) {
     constexpr bool RING = (ND == 3 && PL > 0);
     static_assert(PL % 2 == 0, "planes of whole row pairs");
@@ -195,6 +198,11 @@ __device__ __forceinline__ void scannd_tile(const ScanNDArgs &p, const int (&ti)
         voffB[c] = (cc * DM + f) * 4;
     }
     using F = bio<f32_t>;
+    // Neighbour states: L1-bypassing loads when other workgroups of this
+    // launch may have written them.
+    auto hld = [](__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+        return COH ? F::ld_agent(r, voff, soff) : F::ld(r, voff, soff);
+    };
 
     // Operands of one row (tile-relative row offset in points: r.base).
     // Every load is unconditional: a load under a branch makes the
@@ -237,10 +245,10 @@ __device__ __forceinline__ void scannd_tile(const ScanNDArgs &p, const int (&ti)
             const auto rn = need ? rh : rB;
             const int sn = need ? sh - static_cast<int>(p.pstride[a]) * DM * 4 : sb;
 #pragma unroll
-            for (int c = 0; c < TW; ++c) r.hn[a][c] = F::ld(rn, voffB[c], sn);
+            for (int c = 0; c < TW; ++c) r.hn[a][c] = hld(rn, voffB[c], sn);
         }
         const bool left = __builtin_amdgcn_readfirstlane(lo[ac] > 0) != 0;
-        r.hleft = F::ld(left ? rh : rB, voffB[0], left ? sh - DM * 4 : sb);
+        r.hleft = hld(left ? rh : rB, voffB[0], left ? sh - DM * 4 : sb);
     };
 
     float top[TW];
@@ -250,7 +258,7 @@ __device__ __forceinline__ void scannd_tile(const ScanNDArgs &p, const int (&ti)
         // window whenever that row exists (unneeded: B row, cache hit).
         const bool up = __builtin_amdgcn_readfirstlane(lo[0] > 0) != 0;
 #pragma unroll
-        for (int c = 0; c < TW; ++c) top[c] = F::ld(up ? rh : rB, voffB[c], 0);
+        for (int c = 0; c < TW; ++c) top[c] = hld(up ? rh : rB, voffB[c], 0);
     } else {
 #pragma unroll
         for (int c = 0; c < TW; ++c) top[c] = 0.f;
@@ -410,28 +418,75 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
 // workgroup reads the XCD it runs on from the hardware and takes items (tile
 // in band order, then channel group) from that XCD's counter, so an item is
 // only ever taken by a running wave and every item's predecessors were taken
-// before it: the waits always end. Finishing an item publishes
-// flags[tile * ncg + cg] = epoch (this launch's number) after its h stores
-// are acknowledged; a wait polls at most kFlowSpin times and then goes on.
+// before it: the waits always end.
+//
+// Hand-off: the producer waits until its h stores are acknowledged by the
+// L2 (vmcnt 0), then publishes flags[tile * ncg + cg] = epoch (this launch's
+// number) with an agent-scope store; the consumer polls the flag with
+// agent-scope loads and reads the predecessor's states with agent-coherent
+// loads (sc1: past its own L1, from the shared L2). A wait polls at most
+// `spin` times. If it runs out, the wave does not compute its tile: it
+// writes NaN into the tile's states and outputs, so every tile that depends
+// on it (reading those states) turns NaN too and no output is silently
+// wrong, and it sets the launch's status word, which the synchronous entry
+// points read to re-run the call on the band schedule.
 constexpr int kMaxFlowBands = 768;
-constexpr int kFlowSpin = 1 << 16;
+constexpr unsigned kFlowSpinDefault = 1u << 20;
 struct FlowArgs {
     unsigned *flags;                     // [ntiles * ncg] epoch of the last finish
     unsigned *counter;                   // [8] items taken per XCD, zero at launch
+    unsigned *status;                    // nonzero when a wait ran out (zero at launch)
     unsigned epoch;
+    unsigned spin;                       // polls per wait before giving up
     int nbands;
     int cg_lo[9];                        // channel groups of XCD x: [cg_lo[x], cg_lo[x + 1])
     int band_start[kMaxFlowBands + 1];   // first tile (band order) of each band
 };
 
-__device__ __forceinline__ void flow_wait(const unsigned *flag, unsigned epoch) {
+// True once the predecessor published this launch's epoch; false when the
+// budget ran out first. Lane 0 polls; the result is wave-uniform.
+__device__ __forceinline__ bool flow_wait(const unsigned *flag, unsigned epoch, unsigned spin) {
+    int done = 0;
     if ((threadIdx.x & 63) == 0) {
-        for (int i = 0; i < kFlowSpin; ++i) {
-            if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch) break;
+        for (unsigned i = 0; i < spin; ++i) {
+            if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch) {
+                done = 1;
+                break;
+            }
             __builtin_amdgcn_s_sleep(2);
         }
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    return __builtin_amdgcn_readfirstlane(done) != 0;
+}
+
+// NaN into the states and outputs of one (tile, channel group): the wave's
+// 64 (channel, state) lanes at every point of the tile.
+template <int ND>
+__device__ void scannd_tile_poison(const ScanNDArgs &p, const int (&ti)[kMaxNd], int cg) {
+    const int lane = threadIdx.x & 63;
+    const int f = cg * 64 + lane;
+    const int MM = p.M;
+    const int d = f / MM;
+    const float qnan = __builtin_nanf("");
+    int lo[ND], ext[ND];
+    long npts = 1;
+#pragma unroll
+    for (int a = 0; a < ND; ++a) {
+        lo[a] = ti[a] * p.tile[a];
+        ext[a] = min(p.tile[a], p.dims[a] - lo[a]);
+        npts *= ext[a];
+    }
+    for (long q = 0; q < npts; ++q) {
+        long rem = q, off = 0;
+#pragma unroll
+        for (int a = ND - 1; a >= 0; --a) {
+            const long ia = rem % ext[a];
+            rem /= ext[a];
+            off += (lo[a] + ia) * p.pstride[a];
+        }
+        p.h[off * p.DM + f] = qnan;
+        if (lane % MM == 0) p.y[off * p.D + d] = qnan;
+    }
 }
 
 template <int ND, int TW, int MM, int PL>
@@ -463,10 +518,19 @@ __global__ void __launch_bounds__(64) scannd_flow_kernel(ScanNDArgs p, FlowArgs 
         int tl = 0;
 #pragma unroll
         for (int a = 0; a < ND; ++a) tl += ti[a] * tstride[a];
+        bool ready = true;
 #pragma unroll
         for (int a = 0; a < ND; ++a)
-            if (ti[a] > 0) flow_wait(f.flags + static_cast<long>(tl - tstride[a]) * p.ncg + cg, f.epoch);
-        scannd_tile<ND, TW, MM, PL>(p, ti, cg);
+            if (ti[a] > 0)
+                ready = flow_wait(f.flags + static_cast<long>(tl - tstride[a]) * p.ncg + cg, f.epoch,
+                                  f.spin) && ready;
+        if (ready) {
+            scannd_tile<ND, TW, MM, PL, true>(p, ti, cg);
+        } else {
+            scannd_tile_poison<ND>(p, ti, cg);
+            if ((threadIdx.x & 63) == 0)
+                __hip_atomic_store(f.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         __builtin_amdgcn_s_waitcnt(0);   // this wave's h stores acknowledged by L2
         if ((threadIdx.x & 63) == 0)
             __hip_atomic_store(f.flags + static_cast<long>(tl) * p.ncg + cg, f.epoch, __ATOMIC_RELAXED,
@@ -474,8 +538,10 @@ __global__ void __launch_bounds__(64) scannd_flow_kernel(ScanNDArgs p, FlowArgs 
     }
 }
 
-__global__ void flow_reset(unsigned *counter) {
+// Zeroes the per-XCD item counters and the status word before a launch.
+__global__ void flow_reset(unsigned *counter, unsigned *status) {
     if (threadIdx.x < 8) counter[threadIdx.x] = 0u;
+    if (threadIdx.x == 8) *status = 0u;
 }
 
 // General fallback (any D, M): one launch per wavefront level of the point
@@ -555,42 +621,70 @@ static void launch_tile(dim3 g, const ScanNDArgs &a, bool ring, const FlowArgs *
     launch_tile_pl<ND, TW, MM, 0>(g, a, flow, s);
 }
 
-// Per-device state of the dataflow schedule: completion flags and the
-// per-XCD item counters (one buffer: 8 counters, then flags; zeroed when
-// allocated), the launch
-// epoch, and the device's XCD count. Launches that overlap on one device
-// share it and race, like the library workspace.
+// State of the dataflow schedule, one per (device, stream): the per-XCD
+// item counters (words 0-7), the status word (8), then the completion flags
+// (from word 16; zeroed when allocated), the launch epoch and the device's
+// XCD count. Launches on one stream run in order, so they may share it;
+// launches on different streams use different states.
+constexpr size_t kFlowHead = 16;
 struct FlowState {
+    int dev = -1;
+    hipStream_t stream = nullptr;
     unsigned *buf = nullptr;
     size_t cap = 0;                      // u32 words
     unsigned epoch = 0;
     int nxcc = -1;
 };
-static FlowState g_flow[64];
+constexpr int kMaxFlowStates = 64;
+static FlowState g_flow[kMaxFlowStates];
+static int g_flow_n = 0;
+static std::mutex g_flow_mu;
+
+// Polls per dataflow wait (KM_SCANND_FLOW_SPIN, read once): the safety
+// budget after which a wait gives up (see scannd_flow_kernel).
+static unsigned flow_spin() {
+    static unsigned spin = [] {
+        const char *e = std::getenv("KM_SCANND_FLOW_SPIN");
+        if (!e || !*e) return kFlowSpinDefault;
+        return static_cast<unsigned>(std::strtoul(e, nullptr, 10));
+    }();
+    return spin;
+}
 
 // The dataflow schedule runs grids of 3 or more dims (2D grids are faster
 // with one launch per band on MI355X: their 47-tile critical path, slowed by
 // the tiles running beside it, sets the time), needs the device's 8 XCDs as
 // the hardware reports them (XCC_ID 0-7) and a band table that fits the
-// kernel arguments; KM_SCANND_SCHED=band keeps one launch per band.
-static FlowState *flow_state(int nd, int nbands, size_t words, hipStream_t s) {
+// kernel arguments; KM_SCANND_SCHED=band keeps one launch per band. Returns
+// the stream's state with a fresh epoch (under the lock), or null.
+static FlowState *flow_state(int nd, int nbands, size_t words, hipStream_t s, unsigned *epoch) {
     const char *e = std::getenv("KM_SCANND_SCHED");
     if (nd < 3 || (e && std::strcmp(e, "band") == 0) || nbands > kMaxFlowBands) return nullptr;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    FlowState &st = g_flow[dev];
-    if (st.nxcc < 0) {
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return nullptr;
+    std::lock_guard<std::mutex> guard(g_flow_mu);
+    FlowState *st = nullptr;
+    for (int i = 0; i < g_flow_n; ++i)
+        if (g_flow[i].dev == dev && g_flow[i].stream == s) st = &g_flow[i];
+    if (!st) {
+        if (g_flow_n == kMaxFlowStates) return nullptr;   // band schedule instead
+        st = &g_flow[g_flow_n++];
+        st->dev = dev;
+        st->stream = s;
+    }
+    if (st->nxcc < 0) {
         int n = 0;
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess) n = 0;
-        st.nxcc = n;
+        st->nxcc = n;
     }
-    if (st.nxcc != 8) return nullptr;
-    if (st.cap < words) {
-        if (st.buf) {
-            (void)hipDeviceSynchronize();   // earlier launches may still use the old flags
-            (void)hipFree(st.buf);
-            st.buf = nullptr;
-            st.cap = 0;
+    if (st->nxcc != 8) return nullptr;
+    words += kFlowHead;
+    if (st->cap < words) {
+        if (st->buf) {
+            (void)hipStreamSynchronize(s);   // earlier launches on this stream may still use it
+            (void)hipFree(st->buf);
+            st->buf = nullptr;
+            st->cap = 0;
         }
         void *ptr = nullptr;
         if (hipMalloc(&ptr, words * 4) != hipSuccess) {
@@ -602,14 +696,21 @@ static FlowState *flow_state(int nd, int nbands, size_t words, hipStream_t s) {
             (void)hipFree(ptr);
             return nullptr;
         }
-        st.buf = static_cast<unsigned *>(ptr);
-        st.cap = words;
+        st->buf = static_cast<unsigned *>(ptr);
+        st->cap = words;
     }
-    (void)s;
-    return &st;
+    if (++st->epoch == 0) st->epoch = 1;
+    *epoch = st->epoch;
+    return st;
 }
 
-static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s) {
+// Launches the forward on stream s. With allow_flow, grids of 3+ dims may
+// use the dataflow schedule; *status then points at that launch's status
+// word (device memory; nonzero after the launch when a wait gave up), else
+// it is null.
+static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
+                         const unsigned **status) {
+    if (status) *status = nullptr;
     bool fast = (a.DM % 64 == 0) && (64 % a.M == 0) && a.nd >= 2 && a.nd <= 4;
     // Tiles: rows of TWc points along the last axis, Tlead along each
     // leading axis. One wave per (tile, channel group); one launch per tile
@@ -664,22 +765,27 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s) {
         long ntiles = 0;
         for (int b = 0; b < nbands; ++b) ntiles += cnt[b];
         static thread_local FlowArgs fa;
-        FlowState *st = (ntiles * a.ncg < 0x7fffffffL)
-                            ? flow_state(a.nd, nbands, static_cast<size_t>(ntiles * a.ncg) + 8, s) : nullptr;
+        unsigned epoch = 0;
+        FlowState *st = (allow_flow && ntiles * a.ncg < 0x7fffffffL)
+                            ? flow_state(a.nd, nbands, static_cast<size_t>(ntiles * a.ncg), s, &epoch)
+                            : nullptr;
         const FlowArgs *flow = nullptr;
         if (st) {
-            if (++st->epoch == 0) st->epoch = 1;
-            // Counters first, flags after: flags only ever hold epochs of
-            // earlier launches (whatever the shape), never the current one.
+            // Counters and status first, flags after: flags only ever hold
+            // epochs of earlier launches (whatever the shape), never the
+            // current one.
             fa.counter = st->buf;
-            fa.flags = st->buf + 8;
-            fa.epoch = st->epoch;
+            fa.status = st->buf + 8;
+            fa.flags = st->buf + kFlowHead;
+            fa.epoch = epoch;
+            fa.spin = flow_spin();
             fa.nbands = nbands;
             for (int x = 0; x <= 8; ++x) fa.cg_lo[x] = static_cast<int>(static_cast<long>(x) * a.ncg / 8);
             fa.band_start[0] = 0;
             for (int b = 0; b < nbands; ++b) fa.band_start[b + 1] = fa.band_start[b] + static_cast<int>(cnt[b]);
-            hipLaunchKernelGGL(flow_reset, dim3(1), dim3(64), 0, s, fa.counter);
+            hipLaunchKernelGGL(flow_reset, dim3(1), dim3(64), 0, s, fa.counter, fa.status);
             flow = &fa;
+            if (status) *status = fa.status;
         }
         // Dataflow: one launch of 8k one-wave workgroups (k <= 256: two per
         // SIMD) that take items until their XCD's queue is empty. The
@@ -765,9 +871,12 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s) {
 }
 
 // Shared front end: device pointers, scannd_ref semantics for ndims >= 2.
+// sync: wait for the result; if a dataflow wait gave up, run the call again
+// on the band schedule, so the synchronous entry points always return the
+// exact result.
 static int scannd_device(const float *x, const float *const *A, const float *const *dt,
                          const float *B, const float *C, float *h, float *y, const long *dims,
-                         long nd, long D, long M, hipStream_t s) {
+                         long nd, long D, long M, hipStream_t s, bool sync) {
     if (nd < 2 || nd > kMaxNd) {
         set_error("scannd: ndims %ld outside [2, %d] for the band kernel", nd, kMaxNd);
         return -1;
@@ -802,7 +911,28 @@ static int scannd_device(const float *x, const float *const *A, const float *con
         set_error("scannd: problem too large");
         return -1;
     }
-    return scannd_launch(a, P, s);
+    const unsigned *status = nullptr;
+    if (scannd_launch(a, P, s, true, sync ? &status : nullptr) != 0) return -1;
+    if (!sync) return 0;
+    if (hipStreamSynchronize(s) != hipSuccess) {
+        set_error("scannd: %s", hipGetErrorString(hipGetLastError()));
+        return -1;
+    }
+    if (!status) return 0;
+    unsigned failed = 0;
+    if (hipMemcpy(&failed, status, sizeof failed, hipMemcpyDeviceToHost) != hipSuccess) {
+        set_error("scannd: status read failed");
+        return -1;
+    }
+    if (!failed) return 0;
+    // A dataflow wait ran out of budget (its tiles hold NaN): once more on
+    // the band schedule, whose launches order the tiles.
+    if (scannd_launch(a, P, s, false, nullptr) != 0) return -1;
+    if (hipStreamSynchronize(s) != hipSuccess) {
+        set_error("scannd: %s", hipGetErrorString(hipGetLastError()));
+        return -1;
+    }
+    return 0;
 }
 
 static bool scannd_params_ok(const ScanNDParams *p) {
@@ -817,7 +947,7 @@ static bool scannd_params_ok(const ScanNDParams *p) {
     return true;
 }
 
-int scannd_device_params(const ScanNDParams *p, hipStream_t s) {
+int scannd_device_params(const ScanNDParams *p, hipStream_t s, bool sync) {
     if (!scannd_params_ok(p)) return -1;
     if (!gpu_ready()) return -1;
     const long P = wavefront_nd_total_points(p->dims, p->ndims);
@@ -834,9 +964,14 @@ int scannd_device_params(const ScanNDParams *p, hipStream_t s) {
         k.B = 1; k.L = P; k.D = p->D; k.N = p->M;
         k.bc_sb = P * p->D * p->M; k.bc_st = p->D * p->M; k.bc_sd = p->M;
         k.dtype = KM_F32; k.clamp = 0;
-        return km_scan1d_fwd(&k, s);
+        if (km_scan1d_fwd(&k, s) != 0) return -1;
+        if (sync && hipStreamSynchronize(s) != hipSuccess) {
+            set_error("scannd: %s", hipGetErrorString(hipGetLastError()));
+            return -1;
+        }
+        return 0;
     }
-    return scannd_device(p->x, A, dt, p->B, p->C, p->h, p->y, p->dims, p->ndims, p->D, p->M, s);
+    return scannd_device(p->x, A, dt, p->B, p->C, p->h, p->y, p->dims, p->ndims, p->D, p->M, s, sync);
 }
 
 // Host-pointer staging for the reference's host API: copies inputs to the
@@ -865,12 +1000,7 @@ static int scannd_host(const ScanNDParams *p, bool scan1d_semantics) {
             scan1d(&sp);
             return km_last_error()[0] ? -1 : 0;
         }
-        rc = scannd_device_params(p, nullptr);
-        if (rc == 0 && hipStreamSynchronize(nullptr) != hipSuccess) {
-            set_error("scannd: %s", hipGetErrorString(hipGetLastError()));
-            rc = -1;
-        }
-        return rc;
+        return scannd_device_params(p, nullptr, true);
     }
     if (scan1d_semantics) {
         ScanParams sp{const_cast<float *>(p->x), const_cast<float *>(p->A), const_cast<float *>(p->B),
@@ -899,7 +1029,7 @@ static int scannd_host(const ScanNDParams *p, bool scan1d_semantics) {
     } else {
         ScanNDParams q = *p;
         q.x = st.x; q.A = st.A; q.B = st.B; q.C = st.C; q.delta = st.dt; q.h = st.h; q.y = st.y;
-        rc = scannd_device_params(&q, nullptr);
+        rc = scannd_device_params(&q, nullptr, true);
         if (rc == 0 && (hipMemcpy(p->h, st.h, nh * 4, hipMemcpyDeviceToHost) != hipSuccess ||
                         hipMemcpy(p->y, st.y, nx * 4, hipMemcpyDeviceToHost) != hipSuccess)) {
             set_error("scannd: device-to-host copy failed");
@@ -925,17 +1055,12 @@ int scannd_validate(const ScanNDParams *p) {
 
 int km_scannd_fwd(const ScanNDParams *p, void *stream) {
     km::clear_error();
-    return km::scannd_device_params(p, static_cast<hipStream_t>(stream));
+    return km::scannd_device_params(p, static_cast<hipStream_t>(stream), false);
 }
 
 int om_scannd_forward(ScanNDParams *p) {
     km::clear_error();
-    if (km::scannd_device_params(p, nullptr) != 0) return -1;
-    if (hipStreamSynchronize(nullptr) != hipSuccess) {
-        km::set_error("om_scannd_forward: %s", hipGetErrorString(hipGetLastError()));
-        return -1;
-    }
-    return 0;
+    return km::scannd_device_params(p, nullptr, true);
 }
 
 int mamba_scannd_cuda_forward(ScanNDParams *p) { return om_scannd_forward(p); }
@@ -980,9 +1105,7 @@ void scan2d(Scan2DParams *p) {
                      km::is_device_ptr(p->h) && km::is_device_ptr(p->y);
     if (dev) {
         const float *A[2] = {p->A1, p->A2}, *dt[2] = {p->delta1, p->delta2};
-        if (km::scannd_device(p->x, A, dt, p->B, p->C, p->h, p->y, dims, 2, D, M, nullptr) == 0 &&
-            hipStreamSynchronize(nullptr) != hipSuccess)
-            km::set_error("scan2d: %s", hipGetErrorString(hipGetLastError()));
+        (void)km::scannd_device(p->x, A, dt, p->B, p->C, p->h, p->y, dims, 2, D, M, nullptr, true);
         return;
     }
     km::Staging::lock();
@@ -1003,7 +1126,7 @@ void scan2d(Scan2DParams *p) {
             km::set_error("scan2d: host-to-device copy failed");
         } else {
             const float *A[2] = {A1, A2}, *dt[2] = {d1, d2};
-            if (km::scannd_device(x, A, dt, B, C, h, y, dims, 2, D, M, nullptr) == 0) {
+            if (km::scannd_device(x, A, dt, B, C, h, y, dims, 2, D, M, nullptr, true) == 0) {
                 if (hipMemcpy(p->h, h, nB * 4, hipMemcpyDeviceToHost) != hipSuccess ||
                     hipMemcpy(p->y, y, nx * 4, hipMemcpyDeviceToHost) != hipSuccess)
                     km::set_error("scan2d: device-to-host copy failed");

@@ -533,7 +533,7 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
             return -1;
         }
     } else {
-        ws = static_cast<char *>(km::Workspace::reserve(need));
+        ws = static_cast<char *>(km::Workspace::reserve(need, st));
         if (!ws) return -1;
     }
     // The per-level path reads the plan's level offsets; the tile-band paths

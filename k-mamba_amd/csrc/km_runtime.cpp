@@ -169,24 +169,45 @@ void *Staging::reserve(size_t bytes) {
 }
 
 namespace {
+// Workspaces keyed by (device, stream): launches on different streams never
+// share one, and a block is only freed (to grow it) after its own stream
+// has drained.
+struct WsEntry {
+    int dev;
+    hipStream_t stream;
+    void *ptr;
+    size_t size;
+};
+constexpr int kMaxWs = 64;
 std::mutex g_ws_mu;
-void *g_ws_ptr[64] = {};
-size_t g_ws_size[64] = {};
+WsEntry g_ws[kMaxWs];
+int g_ws_n = 0;
 }  // namespace
 
-void *Workspace::reserve(size_t bytes) {
+void *Workspace::reserve(size_t bytes, hipStream_t stream) {
     std::lock_guard<std::mutex> guard(g_ws_mu);
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
         set_error("workspace: no current HIP device");
         return nullptr;
     }
-    if (g_ws_size[dev] >= bytes && g_ws_ptr[dev]) return g_ws_ptr[dev];
-    if (g_ws_ptr[dev]) {
-        (void)hipDeviceSynchronize();   // earlier kernels may still use the old block
-        (void)hipFree(g_ws_ptr[dev]);
-        g_ws_ptr[dev] = nullptr;
-        g_ws_size[dev] = 0;
+    WsEntry *e = nullptr;
+    for (int i = 0; i < g_ws_n; ++i)
+        if (g_ws[i].dev == dev && g_ws[i].stream == stream) e = &g_ws[i];
+    if (!e) {
+        if (g_ws_n == kMaxWs) {
+            set_error("workspace: more than %d (device, stream) pairs; pass a workspace", kMaxWs);
+            return nullptr;
+        }
+        e = &g_ws[g_ws_n++];
+        *e = WsEntry{dev, stream, nullptr, 0};
+    }
+    if (e->size >= bytes && e->ptr) return e->ptr;
+    if (e->ptr) {
+        (void)hipStreamSynchronize(stream);   // earlier kernels on this stream may use the old block
+        (void)hipFree(e->ptr);
+        e->ptr = nullptr;
+        e->size = 0;
     }
     const size_t want = align_up(bytes, size_t(1) << 20);
     void *p = nullptr;
@@ -195,8 +216,8 @@ void *Workspace::reserve(size_t bytes) {
         set_error("workspace: hipMalloc(%zu) failed", want);
         return nullptr;
     }
-    g_ws_ptr[dev] = p;
-    g_ws_size[dev] = want;
+    e->ptr = p;
+    e->size = want;
     return p;
 }
 

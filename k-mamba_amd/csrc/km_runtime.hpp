@@ -39,13 +39,14 @@ struct PinnedStaging {
     static void *reserve(size_t bytes);      // nullptr on failure (error set)
 };
 
-// Per-device scratch for kernels that need device memory beyond their
-// inputs and outputs (e.g. the Scan1D backward accumulators), used when the
-// caller passes no workspace. Grows on demand and is reused; calls that
-// overlap on one device with this shared scratch race, so concurrent callers
-// pass their own workspace.
+// Scratch for kernels that need device memory beyond their inputs and
+// outputs (e.g. the Scan1D backward's partial sums), used when the caller
+// passes no workspace. One block per (device, stream): grows on demand
+// (after draining that stream) and is reused by later calls on the same
+// stream, so calls on different streams never share it. Host threads that
+// enqueue on one stream concurrently must serialise their calls.
 struct Workspace {
-    static void *reserve(size_t bytes);      // nullptr on failure (error set)
+    static void *reserve(size_t bytes, hipStream_t stream);   // nullptr on failure (error set)
 };
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }

@@ -95,6 +95,101 @@ def test_dataflow_and_band_schedules_agree(dims, D, M, monkeypatch):
     assert_close(h2, hr, TOL_F32, "h", ha)
 
 
+def _stable_nd_inputs(dims, D, M, tag):
+    nd, P = len(dims), int(np.prod(dims))
+    g = rng_for(tag, dims, D, M)
+    x = g.standard_normal((P, D)).astype(np.float32)
+    A = np.log(g.uniform(0.05, 0.9 / nd, (nd, D, M))).astype(np.float32)
+    B = (g.standard_normal((P, D, M)) * 0.25).astype(np.float32)
+    Cm = (g.standard_normal((P, D, M)) * 0.25).astype(np.float32)
+    dt = g.uniform(0.5, 1.0, (nd, P, D)).astype(np.float32)
+    return x, A, B, Cm, dt
+
+
+_BUDGET0 = r"""
+import ctypes as C, sys
+import numpy as np, torch
+sys.path[:0] = [sys.argv[2], sys.argv[3]]
+import kmamba as K
+d = np.load(sys.argv[1])
+dims = tuple(int(v) for v in d["dims"])
+t = [torch.from_numpy(d[k]).cuda() for k in ("x", "A", "B", "C", "dt")]
+P, D, M = int(np.prod(dims)), t[1].shape[1], t[1].shape[2]
+out = {}
+# Asynchronous entry point: every dataflow wait gives up at once.
+h = torch.zeros((P, D, M), device="cuda"); y = torch.zeros((P, D), device="cuda")
+K.scannd_fwd(dims, *t, h, y)
+torch.cuda.synchronize()
+out["y_async"] = y.cpu().numpy()
+# Synchronous entry point: the same failure, then the band schedule.
+h = torch.zeros((P, D, M), device="cuda"); y = torch.zeros((P, D), device="cuda")
+p, keep = K.scannd_params(dims, *t, h, y)
+rc = K.om_scannd_forward(C.byref(p))
+out["rc"] = np.int64(rc); out["y_sync"] = y.cpu().numpy(); out["h_sync"] = h.cpu().numpy()
+np.savez(sys.argv[4], **out)
+print("budget0 done", flush=True)
+"""
+
+
+def test_dataflow_wait_budget_exhausted_fails_loudly_and_sync_api_recovers(tmp_path):
+    # KM_SCANND_FLOW_SPIN=0 (read once per process, so a child process) makes
+    # every dataflow wait give up without polling; every kernel still exits
+    # normally. The waves then write NaN into their tiles instead of
+    # computing, so the asynchronous km_scannd_fwd returns NaN wherever a
+    # tile had a predecessor (never a silently wrong value), and the
+    # synchronous om_scannd_forward sees the status word and re-runs the
+    # call on the band schedule: exact result.
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parent.parent
+    dims, D, M = (9, 6, 11), 4, 16
+    x, A, B, Cm, dt = _stable_nd_inputs(dims, D, M, "nd-budget0")
+    src, dst = tmp_path / "in.npz", tmp_path / "out.npz"
+    np.savez(src, dims=np.array(dims), x=x, A=A, B=B, C=Cm, dt=dt)
+    env = dict(__import__("os").environ, KM_SCANND_FLOW_SPIN="0")
+    r = subprocess.run([sys.executable, "-c", _BUDGET0, str(src), str(root / "k-mamba_amd"),
+                        str(root / "oracle"), str(dst)], env=env, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    out = np.load(dst)
+    yr, hr = O.scannd_ref(dims, x, A, B, Cm, dt, nthreads=8, fast=True)
+    ya, ha = kappa(dims, x, A, B, Cm, dt)
+    assert int(out["rc"]) == 0
+    assert_close(out["y_sync"], yr, TOL_F32, "y after re-run", ya)
+    assert_close(out["h_sync"], hr, TOL_F32, "h after re-run", ha)
+    ya_ = out["y_async"].reshape(dims + (D,))
+    assert np.isnan(ya_).any(), "a failed wait must not leave finite outputs behind"
+    assert np.isfinite(ya_[0, 0, 0]).all()           # the first tile has no predecessor
+    assert np.isnan(ya_[-1, -1, -1]).all()           # the last one depends on everything
+    fin = np.isfinite(out["y_async"])
+    np.testing.assert_allclose(out["y_async"][fin], yr[fin], rtol=0, atol=1e-4 * float(np.abs(ya).max()))
+
+
+def test_dataflow_on_two_streams_concurrently():
+    # Each (device, stream) pair has its own dataflow flags and counters:
+    # launches on two streams back to back, with no synchronisation between
+    # them, both match the oracle.
+    dims, D, M = (40, 24, 24), 16, 16
+    P = int(np.prod(dims))
+    sets = [_stable_nd_inputs(dims, D, M, f"nd-streams{i}") for i in range(2)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = []
+    for arrs in sets:
+        t = [T(a) for a in arrs]
+        outs.append((t, torch.zeros((P, D, M), device=DEV), torch.zeros((P, D), device=DEV)))
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for (t, h, y), st in zip(outs, streams):
+            K.scannd_fwd(dims, *t, h, y, stream=st)
+    torch.cuda.synchronize()
+    for arrs, (t, h, y) in zip(sets, outs):
+        yr, hr = O.scannd_ref(dims, *arrs, nthreads=8, fast=True)
+        ya, ha = kappa(dims, *arrs)
+        assert_close(y.cpu().numpy(), yr, TOL_F32, "y", ya)
+        assert_close(h.cpu().numpy(), hr, TOL_F32, "h", ha)
+
+
 def test_known_answers_all_entry_points():
     # tests/unit/test_scan_nd.c:41-141.
     for dims, A, want in (((2, 2), [np.log(2.0), np.log(3.0)], [1, 4, 3, 18]),
