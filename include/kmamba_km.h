@@ -219,6 +219,19 @@ int km_mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long
  * and lambda must be NULL. Returns 0, or -1 with km_last_error() set. */
 int km_scannd_fwd(const ScanNDParams *p, void *stream);
 
+/* km_scannd_fwd without any allocation. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * parameters, semantics and results as km_scannd_fwd. The dataflow schedule
+ * of 3- and 4-dimensional grids keeps its counters and completion flags in a
+ * fixed 1 MiB array in each GPU's memory (held until the process ends)
+ * instead of a per-stream allocation; grids needing more than 262,128
+ * (tile, channel group) flags, and shapes outside the tile kernels (D*M not
+ * a multiple of 64, or M not dividing 64), are rejected with -1 and
+ * km_last_error(). Every call on one GPU shares that array: calls that
+ * overlap on one GPU (other streams, other threads) race. */
+int km_scannd_fwd_noalloc(const ScanNDParams *p, void *stream);
+
 /* ScanND backward (no counterpart in the reference, which has no ScanND
  * adjoint; the adjoint of scannd_ref, src/scan_nd.c:74-192, for the loss
  * L = sum dy . y). With e_a[p] = exp(delta_a[p] A_a), dtbar = sum_a

@@ -704,12 +704,31 @@ static FlowState *flow_state(int nd, int nbands, size_t words, hipStream_t s, un
     return st;
 }
 
+// Dataflow state supplied by the caller instead of the per-stream state
+// (the allocation-free entry point): a device buffer of `cap` words laid
+// out like FlowState's, the host-side epoch counter of that buffer and the
+// device's XCD count.
+struct FlowBuf {
+    unsigned *buf;
+    size_t cap;
+    unsigned *epoch;
+    int nxcc;
+};
+
+__global__ void __launch_bounds__(256) flow_clear(unsigned *p, long n) {
+    for (long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<long>(gridDim.x) * 256)
+        p[i] = 0u;
+}
+
 // Launches the forward on stream s. With allow_flow, grids of 3+ dims may
 // use the dataflow schedule; *status then points at that launch's status
 // word (device memory; nonzero after the launch when a wait gave up), else
-// it is null.
+// it is null. With ext, the dataflow state lives in ext's buffer and
+// nothing is allocated: shapes that need the per-level fallback's plan
+// buffer, or more flags than ext holds, fail with an error.
 static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
-                         const unsigned **status) {
+                         const unsigned **status, FlowBuf *ext = nullptr) {
     if (status) *status = nullptr;
     bool fast = (a.DM % 64 == 0) && (64 % a.M == 0) && a.nd >= 2 && a.nd <= 4;
     // Tiles: rows of TWc points along the last axis, Tlead along each
@@ -766,17 +785,40 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
         for (int b = 0; b < nbands; ++b) ntiles += cnt[b];
         static thread_local FlowArgs fa;
         unsigned epoch = 0;
-        FlowState *st = (allow_flow && ntiles * a.ncg < 0x7fffffffL)
-                            ? flow_state(a.nd, nbands, static_cast<size_t>(ntiles * a.ncg), s, &epoch)
-                            : nullptr;
+        unsigned *fbuf = nullptr;
+        if (ext) {
+            const char *e = std::getenv("KM_SCANND_SCHED");
+            if (allow_flow && a.nd >= 3 && !(e && std::strcmp(e, "band") == 0) &&
+                nbands <= kMaxFlowBands && ext->nxcc == 8) {
+                const size_t words = kFlowHead + static_cast<size_t>(ntiles * a.ncg);
+                if (words > ext->cap) {
+                    set_error("scannd: the dataflow schedule needs %zu flag words, the scratch holds %zu",
+                              words, ext->cap);
+                    return -1;
+                }
+                if (++*ext->epoch == 0) {
+                    // Epochs wrapped: no flag may hold the new one.
+                    hipLaunchKernelGGL(flow_clear, dim3(256), dim3(256), 0, s, ext->buf,
+                                       static_cast<long>(ext->cap));
+                    *ext->epoch = 1;
+                }
+                epoch = *ext->epoch;
+                fbuf = ext->buf;
+            }
+        } else {
+            FlowState *st = (allow_flow && ntiles * a.ncg < 0x7fffffffL)
+                                ? flow_state(a.nd, nbands, static_cast<size_t>(ntiles * a.ncg), s, &epoch)
+                                : nullptr;
+            if (st) fbuf = st->buf;
+        }
         const FlowArgs *flow = nullptr;
-        if (st) {
+        if (fbuf) {
             // Counters and status first, flags after: flags only ever hold
             // epochs of earlier launches (whatever the shape), never the
             // current one.
-            fa.counter = st->buf;
-            fa.status = st->buf + 8;
-            fa.flags = st->buf + kFlowHead;
+            fa.counter = fbuf;
+            fa.status = fbuf + 8;
+            fa.flags = fbuf + kFlowHead;
             fa.epoch = epoch;
             fa.spin = flow_spin();
             fa.nbands = nbands;
@@ -830,6 +872,11 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
         return 0;
     }
     // Fallback: per-level launches over the plan.
+    if (ext) {
+        set_error("scannd: this shape needs the per-level schedule, whose plan buffer is "
+                  "allocated; use km_scannd_fwd");
+        return -1;
+    }
     long dims[kMaxNd];
     for (int ax = 0; ax < a.nd; ++ax) dims[ax] = a.dims[ax];
     KMWavefrontPlan *plan = km_wavefront_plan_create(dims, a.nd);
@@ -876,7 +923,8 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
 // exact result.
 static int scannd_device(const float *x, const float *const *A, const float *const *dt,
                          const float *B, const float *C, float *h, float *y, const long *dims,
-                         long nd, long D, long M, hipStream_t s, bool sync) {
+                         long nd, long D, long M, hipStream_t s, bool sync,
+                         FlowBuf *ext = nullptr) {
     if (nd < 2 || nd > kMaxNd) {
         set_error("scannd: ndims %ld outside [2, %d] for the band kernel", nd, kMaxNd);
         return -1;
@@ -912,7 +960,7 @@ static int scannd_device(const float *x, const float *const *A, const float *con
         return -1;
     }
     const unsigned *status = nullptr;
-    if (scannd_launch(a, P, s, true, sync ? &status : nullptr) != 0) return -1;
+    if (scannd_launch(a, P, s, true, sync ? &status : nullptr, ext) != 0) return -1;
     if (!sync) return 0;
     if (hipStreamSynchronize(s) != hipSuccess) {
         set_error("scannd: %s", hipGetErrorString(hipGetLastError()));
@@ -947,7 +995,7 @@ static bool scannd_params_ok(const ScanNDParams *p) {
     return true;
 }
 
-int scannd_device_params(const ScanNDParams *p, hipStream_t s, bool sync) {
+int scannd_device_params(const ScanNDParams *p, hipStream_t s, bool sync, FlowBuf *ext = nullptr) {
     if (!scannd_params_ok(p)) return -1;
     if (!gpu_ready()) return -1;
     const long P = wavefront_nd_total_points(p->dims, p->ndims);
@@ -971,7 +1019,54 @@ int scannd_device_params(const ScanNDParams *p, hipStream_t s, bool sync) {
         }
         return 0;
     }
-    return scannd_device(p->x, A, dt, p->B, p->C, p->h, p->y, p->dims, p->ndims, p->D, p->M, s, sync);
+    return scannd_device(p->x, A, dt, p->B, p->C, p->h, p->y, p->dims, p->ndims, p->D, p->M, s, sync,
+                         ext);
+}
+
+// The allocation-free variant's dataflow state: a file-scope device array
+// (each GPU holds its own copy for the life of the process), 16 words of
+// counters and status and then the completion flags of up to
+// kScratchWords - 16 (tile, channel group) items. Its device address is
+// looked up once per device with hipGetSymbolAddress; host code uses that
+// address, never the array's name (which on the host is only a stand-in).
+constexpr size_t kScratchWords = size_t(1) << 18;   // 1 MiB
+static __device__ __align__(256) unsigned scratch[kScratchWords];
+
+struct NoAllocDevice {
+    bool ready = false;
+    unsigned *ptr = nullptr;
+    unsigned epoch = 0;
+    int nxcc = 0;
+};
+constexpr int kMaxDevices = 64;
+static NoAllocDevice g_noalloc[kMaxDevices];
+static std::mutex g_noalloc_mu;
+
+int scannd_fwd_noalloc(const ScanNDParams *p, hipStream_t s) {
+    if (!scannd_params_ok(p)) return -1;
+    if (!gpu_ready()) return -1;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_error("km_scannd_fwd_noalloc: no current HIP device below %d", kMaxDevices);
+        return -1;
+    }
+    std::lock_guard<std::mutex> guard(g_noalloc_mu);
+    NoAllocDevice &nd = g_noalloc[dev];
+    if (!nd.ready) {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            set_error("km_scannd_fwd_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+            return -1;
+        }
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess) n = 0;
+        nd.ptr = static_cast<unsigned *>(ptr);
+        nd.nxcc = n;
+        nd.ready = true;
+    }
+    FlowBuf fb{nd.ptr, kScratchWords, &nd.epoch, nd.nxcc};
+    return scannd_device_params(p, s, false, &fb);
 }
 
 // Host-pointer staging for the reference's host API: copies inputs to the
@@ -1056,6 +1151,13 @@ int scannd_validate(const ScanNDParams *p) {
 int km_scannd_fwd(const ScanNDParams *p, void *stream) {
     km::clear_error();
     return km::scannd_device_params(p, static_cast<hipStream_t>(stream), false);
+}
+
+// No counterpart in the reference: km_scannd_fwd for callers that cannot
+// allocate (see kmamba_km.h).
+int km_scannd_fwd_noalloc(const ScanNDParams *p, void *stream) {
+    km::clear_error();
+    return km::scannd_fwd_noalloc(p, static_cast<hipStream_t>(stream));
 }
 
 int om_scannd_forward(ScanNDParams *p) {

@@ -496,6 +496,8 @@ scannd = _decl("scannd", C.c_int, [C.POINTER(ScanNDParams)])
 om_scannd_forward = _decl("om_scannd_forward", C.c_int, [C.POINTER(ScanNDParams)])
 mamba_scannd_cuda_forward = _decl("mamba_scannd_cuda_forward", C.c_int, [C.POINTER(ScanNDParams)])
 km_scannd_fwd_c = _decl("km_scannd_fwd", C.c_int, [C.POINTER(ScanNDParams), C.c_void_p])
+km_scannd_fwd_noalloc_c = _decl("km_scannd_fwd_noalloc", C.c_int,
+                                  [C.POINTER(ScanNDParams), C.c_void_p])
 scan2d = _decl("scan2d", None, [C.POINTER(Scan2DParams)])
 mamba_scan2d_forward = _decl("mamba_scan2d_forward", None, [C.POINTER(Scan2DParams)])
 
@@ -538,4 +540,13 @@ def scannd_fwd(dims, x, A, B, Cm, delta, h, y, stream=None):
     """km_scannd_fwd (scannd_ref semantics) on torch device tensors."""
     p, keep = scannd_params(dims, x, A, B, Cm, delta, h, y)
     check(km_scannd_fwd_c(C.byref(p), C.c_void_p(stream_handle(stream))), "km_scannd_fwd")
+    return keep
+
+
+def scannd_fwd_noalloc(dims, x, A, B, Cm, delta, h, y, stream=None):
+    """km_scannd_fwd_noalloc: km_scannd_fwd with its dataflow state in the
+    library's fixed device array (no allocation)."""
+    p, keep = scannd_params(dims, x, A, B, Cm, delta, h, y)
+    check(km_scannd_fwd_noalloc_c(C.byref(p), C.c_void_p(stream_handle(stream))),
+          "km_scannd_fwd_noalloc")
     return keep
