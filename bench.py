@@ -143,8 +143,8 @@ def bench_mamba1_block(torch, K, stream, steps, warmup, Bsz=8, L=2048, dim=1024,
     mi, mo = sum(pi) / len(pi), sum(po) / len(po)
     fi, fo = 2.0 * T * di * dim, 2.0 * T * dim * di
     return {"block_ms": round(ms, 4), "tokens_per_s": T / (ms * 1e-3),
-            "projections": "in_proj / x_proj / out_proj on hipBLASLt (KM_BLOCK_GEMM=km: km_gemm_bf16); "
-                           "the figures below time km_gemm_bf16 alone on those shapes",
+            "projections": "every projection on km_gemm_bf16 (hand-written bf16 MFMA); the figures "
+                           "below time the in_proj half and out_proj shapes alone",
             "in_proj_half_ms": round(mi, 4),
             "in_proj_TFLOPs": round(fi / (mi * 1e-3) / 1e12, 1),
             "in_proj_frac_mfma_peak": round(fi / (mi * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),

@@ -190,11 +190,8 @@ int km_gemm_bf16(const KMGemm *g, void *stream);
  * be NULL), dt_bias [di], A [di, N], Dskip [di] (may be NULL) fp32.
  * clamp: the +-1000 state clamp of the reference scan (1) or none (0).
  * workspace: km_mamba1_block_workspace_bytes() bytes of device memory, or
- * NULL for the library's per-device scratch. The plain projections
- * (in_proj, x_proj, out_proj) run on hipBLASLt (32 MB of the workspace is its
- * scratch), the other GEMMs on km_gemm_bf16's kernels; with the environment
- * variable KM_BLOCK_GEMM=km, or when hipBLASLt has no algorithm for a shape,
- * they run on km_gemm_bf16 too. */
+ * NULL for the library's scratch of this (device, stream). Every projection
+ * runs on km_gemm_bf16's bf16 MFMA kernels. */
 typedef struct {
     long dim, d_inner, d_state, d_conv, dt_rank;
     const void  *W_in;

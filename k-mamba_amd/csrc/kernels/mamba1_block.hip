@@ -22,11 +22,6 @@ namespace km {
 
 int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream);
 int gemm_bf16_launch(const KMGemm *g, hipStream_t s);
-int lib_gemm_bf16(const void *A, const void *B, void *C, long M, long N, long K, long lda, long ldb,
-                  long ldc, void *ws, size_t ws_bytes, hipStream_t s);
-
-// Workspace of the library GEMM (in_proj / x_proj / out_proj) inside the block's.
-constexpr size_t kLibGemmWs = size_t(32) << 20;
 
 constexpr int kConvStrip = 64;
 
@@ -86,7 +81,7 @@ __global__ void __launch_bounds__(256) conv1d_silu_bf16(const uint32_t *x, const
 }
 
 struct BlockLayout {
-    size_t xi, z, u, xdbl, delta, y, gws, bytes;
+    size_t xi, z, u, xdbl, delta, y, bytes;
 };
 
 static BlockLayout block_layout(const KMMamba1Weights *w, long B, long L) {
@@ -100,7 +95,6 @@ static BlockLayout block_layout(const KMMamba1Weights *w, long B, long L) {
     l.delta = off; off += act;
     l.y = off; off += act;
     l.xdbl = off; off += align_up(T * (w->dt_rank + 2 * w->d_state) * 2, 256);
-    l.gws = off; off += kLibGemmWs;
     l.bytes = off;
     return l;
 }
@@ -148,13 +142,8 @@ int mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long B,
          *delta = ws + lay.delta, *y = ws + lay.y;
     const uint16_t *Win = static_cast<const uint16_t *>(w->W_in);
 
-    // Plain GEMMs (in_proj, x_proj, out_proj) go to the library GEMM, the rest to
-    // the hand-written kernels.
-    auto plain = [&](const KMGemm &g) {
-        const int r = lib_gemm_bf16(g.A, g.B, g.C, g.M, g.N, g.K, g.lda, g.ldb, g.ldc, ws + lay.gws,
-                                    kLibGemmWs, s);
-        return r < 0 ? -1 : r > 0 ? 0 : gemm_bf16_launch(&g, s);
-    };
+    // Every projection runs on the hand-written bf16 MFMA GEMM (km_gemm_bf16).
+    auto plain = [&](const KMGemm &g) { return gemm_bf16_launch(&g, s); };
     KMGemm g{};
     g.c_dtype = KM_BF16;
     // in_proj, x and z halves

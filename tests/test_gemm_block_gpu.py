@@ -59,6 +59,28 @@ def test_gemm_vs_float64(M, N, Kd, out_bf16):
     assert_close(C.float().cpu().numpy(), ref, TOL_BF16 / 4 if out_bf16 else TOL_F32, "C", kap)
 
 
+@pytest.mark.parametrize("M,N,Kd", [(16384, 2048, 1024), (16384, 1024, 2048), (16384, 4096, 1024),
+                                    (16384, 96, 2048)])
+def test_gemm_block_shapes_sampled_rows(M, N, Kd):
+    # The configs[4] projection shapes at full size (in_proj half and whole,
+    # out_proj, x_proj): hundreds of 256 x 256 tiles in the XCD-ordered tile
+    # order. Operands like the block's (N(0, 1) activations, N(0, 0.02)
+    # weights), bf16 output; every column of 1024 rows spread over the whole
+    # M range is checked (rows are independent: an exact sub-problem).
+    g = rng_for("gemm-block", M, N, Kd)
+    A = bf16_round(g.standard_normal((M, Kd)).astype(np.float32))
+    B = bf16_round((g.standard_normal((N, Kd)) * 0.02).astype(np.float32))
+    C = torch.full((M, N), float("nan"), device=DEV, dtype=torch.bfloat16)
+    K.gemm_bf16(bf(A), bf(B), C)
+    torch.cuda.synchronize()
+    got = C.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    rows = np.unique(np.concatenate([np.arange(0, M, 16), [M - 1]]))
+    ref = A[rows].astype(np.float64) @ B.astype(np.float64).T
+    kap = np.abs(A[rows]).astype(np.float64) @ np.abs(B).astype(np.float64).T
+    assert_close(got[rows], ref, TOL_BF16 / 4, "C rows", kap)
+
+
 @pytest.mark.parametrize("epi", [K.KM_EPI_NONE, K.KM_EPI_SOFTPLUS, K.KM_EPI_SILU])
 def test_gemm_strided_bias_epilogues(epi):
     # A is a column slice of a wider buffer (lda > K), as dt_proj reads dt_low
