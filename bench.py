@@ -356,33 +356,109 @@ def time_launches(torch, stream, fn, steps, warmup):
     return [wall / steps] * steps, wall
 
 
-def cpu_baseline_scan1d(x, dt, A, Bm, Cm, budget_s=12.0):
-    """Oracle restatement of the reference scan1d (cpu/scan1d.asm, single
-    thread like the asm) on whole batch elements of the workload until the
-    time budget is used; returns elems/s."""
+def host_info():
+    """CPU model, glibc and thread settings of the host the CPU legs run on."""
+    model = platform.processor() or platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu": model, "glibc": "-".join(platform.libc_ver()), "nproc": os.cpu_count(),
+            "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")}
+
+
+def cpu_threads():
+    """Threads of the all-cores legs: OMP_NUM_THREADS when set (the GPU
+    boxes set it to the box's CPU share), else every core, at most 16."""
+    try:
+        n = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        n = 0
+    return max(1, min(n if n > 0 else (os.cpu_count() or 1), 16))
+
+
+def cpu_baseline_scan1d(x, dt, A, Bm, Cm, nthreads=1, budget_s=3.0):
+    """Oracle restatement of the reference scan1d (cpu/scan1d.asm) on whole
+    batch elements of the workload, repeated until the time budget is used: one
+    thread (the asm is single-threaded), or nthreads over (batch, channel)
+    as the reference's batch threading (src/kmamba.c:512-531). Returns
+    (elems/s, batch elements done, seconds)."""
     import numpy as np
     import oracle as O
     Bsz, L, D = x.shape
-    done = 0
-    t_total = 0.0
-    b = 0
-    while t_total < budget_s and b < Bsz:
-        xs, dts, Bs, Cs = (np.ascontiguousarray(a[b:b + 1]) for a in (x, dt, Bm, Cm))
+    done, t_total, b = 0, 0.0, 0
+    per = 1 if nthreads == 1 else Bsz
+    while t_total < budget_s:            # whole batch elements, repeated up to the budget
+        nb = min(per, Bsz - b % Bsz)
+        i0 = b % Bsz
+        xs, dts, Bs, Cs = (np.ascontiguousarray(a[i0:i0 + nb]) for a in (x, dt, Bm, Cm))
         t = time.perf_counter()
-        O.scan1d_batched(xs, dts, A, Bs, Cs, nthreads=1, fast=True)
+        O.scan1d_batched(xs, dts, A, Bs, Cs, nthreads=nthreads, fast=True)
         t_total += time.perf_counter() - t
-        done += L * D
-        b += 1
+        done += nb * L * D
+        b += nb
     return done / t_total, b, t_total
+
+
+def cpu_baseline_scan2d(nthreads, dims=(256, 256), D=256, M=16, dsample=16, budget_s=3.0):
+    """The oracle's scannd_ref (src/scan_nd.c, OpenMP over the points of each
+    wavefront level as src/scan_nd.c:86) on configs[2]'s 256x256 grid with
+    dsample of the D channels (channels are independent, so this is an exact
+    sub-problem; the state arrays of all 256 channels would take 3 GB of host
+    memory), repeated until the time budget is used. Returns (y elems/s,
+    seconds)."""
+    import numpy as np
+    import oracle as O
+    g = np.random.default_rng(7)
+    P, nd = int(np.prod(dims)), len(dims)
+    x = g.standard_normal((P, dsample)).astype(np.float32)
+    A = np.log(g.uniform(0.05, 0.9 / nd, (nd, dsample, M))).astype(np.float32)
+    B = (g.standard_normal((P, dsample, M)) * 0.25).astype(np.float32)
+    C = (g.standard_normal((P, dsample, M)) * 0.25).astype(np.float32)
+    dt = np.ones((nd, P, dsample), np.float32)
+    secs, runs = 0.0, 0
+    while secs < budget_s:
+        t = time.perf_counter()
+        O.scannd_ref(dims, x, A, B, C, dt, nthreads=nthreads, fast=True)
+        secs += time.perf_counter() - t
+        runs += 1
+    return runs * P * dsample / secs, secs
+
+
+def cpu_baselines(x, dt, A, Bm, Cm):
+    """The CPU legs (the oracle's optimised build; a reported baseline, not
+    the target), timed on this host before the GPU work."""
+    nt = cpu_threads()
+    r1, nb1, s1 = cpu_baseline_scan1d(x, dt, A, Bm, Cm, nthreads=1)
+    rn, nbn, sn = cpu_baseline_scan1d(x, dt, A, Bm, Cm, nthreads=nt)
+    r2, s2 = cpu_baseline_scan2d(1)
+    r2n, s2n = cpu_baseline_scan2d(nt)
+    Bsz, L, D = x.shape
+    return {"value": r1, "unit": "elems/s", "cores": 1, "kind": "port",
+            "sample": f"{nb1} batch elements (of {Bsz}, cycled) of the headline workload (L={L}, D={D}, "
+                      f"N={A.shape[1]}), the oracle's restatement of cpu/scan1d.asm, one thread as "
+                      f"the asm, {s1:.1f} s",
+            "all_cores": {"value": rn, "unit": "elems/s", "cores": nt,
+                          "sample": f"{nbn} batch elements, OpenMP over (batch, channel), {sn:.1f} s"},
+            "scan2d_256x256": {"value": r2, "unit": "elems/s", "cores": 1,
+                               "all_cores_value": r2n, "all_cores": nt,
+                               "sample": f"scannd_ref restatement, 16 of 256 channels (independent), "
+                                         f"N=16; {s2:.1f} s on one thread, {s2n:.1f} s on {nt} "
+                                         f"(OpenMP per wavefront level)"},
+            "host": host_info()}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    # The GPU needs ~0.1 s of load before its clocks settle: fewer warm-up
-    # launches time the ramp, not the kernel.
-    ap.add_argument("--warmup", type=int, default=500)
+    # The headline runs after every other reported workload, so its clocks
+    # have settled; --only modes time the ramp unless the warm-up is long
+    # (the GPU needs ~0.1 s of load after idle).
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", choices=["all", "scan1d", "scan1d_bwd", "scannd", "convnd", "block",
                                        "mamba3", "gemm", "model", "scannd_bwd", "copy"],
@@ -445,86 +521,102 @@ def main():
             r3 = bench_convnd(torch, K, stream, (64, 64, 64), 64, 3, args.steps, args.warmup)
         print(json.dumps({"convnd_2d_512x512_D64_K3": r2, "convnd_3d_64cubed_D64_K3": r3}))
         return
+    if args.only == "scan1d":
+        Bsz, L, D, N = 8, 4096, 1024, 16
+        with torch.cuda.stream(stream):
+            x, dt, A, Bm, Cm = make_inputs(torch, Bsz, L, D, N, "f32")
+            y = torch.empty_like(x)
+            hf = torch.empty((Bsz, D, N), device="cuda")
+            fn = lambda: K.scan1d_fwd(x, dt, A, Bm, Cm, y, h_final=hf, stream=stream)  # noqa: E731
+            per, _ = time_launches(torch, stream, fn, args.steps, args.warmup)
+        ms = sum(per) / len(per)
+        print(json.dumps({"scan1d_f32_ms": ms, "GBs": scan1d_alg_bytes(Bsz, L, D, N, 4) / (ms * 1e-3) / 1e9}))
+        return
     if args.only == "scannd":
         with torch.cuda.stream(stream):
             r2 = bench_scannd(torch, K, stream, (256, 256), 256, 16, args.steps, args.warmup)
             r3 = bench_scannd(torch, K, stream, (64, 64, 64), 128, 16, args.steps, args.warmup)
         print(json.dumps({"scan2d_256x256_D256_M16": r2, "scan3d_64cubed_D128_M16": r3}))
         return
+    # Order: the CPU legs first (the GPU idles), then every reported GPU
+    # workload, then the headline's W warm-up and K timed steps, which thus
+    # run on a GPU whose clocks have settled under load (~0.1 s of load
+    # after idle; W = 5 alone would time the ramp).
     Bsz, L, D, N = 8, 4096, 1024, 16
     extra = {}
     with torch.cuda.stream(stream):
         x, dt, A, Bm, Cm = make_inputs(torch, Bsz, L, D, N, "f32")
+    torch.cuda.synchronize()
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baselines(*(t.float().cpu().numpy() for t in (x, dt, A, Bm, Cm)))
+    elems = Bsz * L * D
+    alg = scan1d_alg_bytes(Bsz, L, D, N, 4)
+    extra["kmamba_forward_f32"] = bench_model(K, 3, 1)
+    with torch.cuda.stream(stream):
+        # Untimed: ~0.2 s of forward launches so the reported workloads below
+        # start on settled clocks.
         y = torch.empty_like(x)
         hf = torch.empty((Bsz, D, N), device="cuda")
-        fn = lambda: K.scan1d_fwd(x, dt, A, Bm, Cm, y, h_final=hf, stream=stream)  # noqa: E731
-        per, wall = time_launches(torch, stream, fn, args.steps, args.warmup)
-        ms = sum(per) / len(per)
-        elems = Bsz * L * D
-        alg = scan1d_alg_bytes(Bsz, L, D, N, 4)
-        ach = alg / (ms * 1e-3) / 1e9
-        # Generic decays: the same workload with A perturbed off the S4D-real
-        # structure, which disables the power-chain path (one exp per state).
-        Ag = A * (1.0 + 0.01 * torch.rand(A.shape, device="cuda", generator=torch.Generator(
-            device="cuda").manual_seed(7)))
-        fng = lambda: K.scan1d_fwd(x, dt, Ag, Bm, Cm, y, h_final=hf, stream=stream)  # noqa: E731
-        perg, _ = time_launches(torch, stream, fng, args.steps, args.warmup)
-        msg = sum(perg) / len(perg)
-        extra["scan1d_fwd_f32_generic_A"] = {
-            "ms": round(msg, 4), "elems_per_s": elems / (msg * 1e-3),
-            "achieved_GBs": round(alg / (msg * 1e-3) / 1e9, 1),
-            "frac_hbm": round(alg / (msg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-        if args.only == "scan1d":
-            print(json.dumps({"scan1d_f32_ms": ms, "GBs": ach, **extra}))
-            return
-
-        # bf16 I/O variant (reported, not the headline)
-        xb, dtb, Ab, Bb, Cb = make_inputs(torch, Bsz, L, D, N, "bf16")
-        yb = torch.empty_like(xb)
-        fnb = lambda: K.scan1d_fwd(xb, dtb, Ab, Bb, Cb, yb, h_final=hf, stream=stream)  # noqa: E731
-        perb, _ = time_launches(torch, stream, fnb, args.steps, args.warmup)
-        msb = sum(perb) / len(perb)
-        algb = scan1d_alg_bytes(Bsz, L, D, N, 2)
-        extra["scan1d_fwd_bf16"] = {"ms": round(msb, 4), "elems_per_s": elems / (msb * 1e-3),
-                                    "achieved_GBs": round(algb / (msb * 1e-3) / 1e9, 1),
-                                    "frac_hbm": round(algb / (msb * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-
-    with torch.cuda.stream(stream):
-        del xb, dtb, Bb, Cb, yb
+        t_end = time.perf_counter() + 0.2
+        while time.perf_counter() < t_end:
+            for _ in range(50):
+                K.scan1d_fwd(x, dt, A, Bm, Cm, y, h_final=hf, stream=stream)
+            torch.cuda.synchronize()
         extra["scan1d_bwd_f32"] = bench_scan1d_bwd(torch, K, stream, Bsz, L, D, N, "f32",
-                                                   max(5, args.steps // 2), 2)
+                                                   max(5, args.steps // 2), 5)
         extra["scan1d_bwd_bf16"] = bench_scan1d_bwd(torch, K, stream, Bsz, L, D, N, "bf16",
-                                                    max(5, args.steps // 2), 2)
+                                                    max(5, args.steps // 2), 5)
         extra["scannd_2d_256x256_D256_M16_f32"] = bench_scannd(torch, K, stream, (256, 256), 256, 16,
-                                                                max(5, args.steps // 2), 2)
+                                                                max(5, args.steps // 2), 5)
         extra["convnd_2d_512x512_D64_K3_f32"] = bench_convnd(torch, K, stream, (512, 512), 64, 3,
-                                                             max(5, args.steps // 2), 2)
+                                                             max(5, args.steps // 2), 5)
         extra["convnd_3d_64cubed_D64_K3_f32"] = bench_convnd(torch, K, stream, (64, 64, 64), 64, 3,
-                                                             max(5, args.steps // 2), 2)
+                                                             max(5, args.steps // 2), 5)
         extra["mamba1_block_configs4_bf16"] = bench_mamba1_block(torch, K, stream,
-                                                                  max(5, args.steps // 2), 2)
+                                                                  max(5, args.steps // 2), 5)
         extra["scannd_3d_64cubed_D128_M16_f32"] = bench_scannd(torch, K, stream, (64, 64, 64), 128, 16,
-                                                                max(5, args.steps // 2), 2)
+                                                                max(5, args.steps // 2), 5)
         extra["mamba3_block_fwd_f32"] = bench_mamba3(torch, K, max(5, args.steps // 10), 2)
         extra["scannd_bwd_2d_256x256_D256_M16_f32"] = bench_scannd_bwd(
             torch, K, stream, (256, 256), 256, 16, max(5, args.steps // 10), 2)
         extra["scannd_bwd_3d_64cubed_D128_M16_f32"] = bench_scannd_bwd(
             torch, K, stream, (64, 64, 64), 128, 16, max(5, args.steps // 10), 2)
-    extra["kmamba_forward_f32"] = bench_model(K, 3, 1)
+
+        # bf16 I/O forward (reported, not the headline)
+        xb, dtb, Ab, Bb, Cb = make_inputs(torch, Bsz, L, D, N, "bf16")
+        yb = torch.empty_like(xb)
+        fnb = lambda: K.scan1d_fwd(xb, dtb, Ab, Bb, Cb, yb, h_final=hf, stream=stream)  # noqa: E731
+        perb, _ = time_launches(torch, stream, fnb, args.steps, 20)
+        msb = sum(perb) / len(perb)
+        algb = scan1d_alg_bytes(Bsz, L, D, N, 2)
+        extra["scan1d_fwd_bf16"] = {"ms": round(msb, 4), "elems_per_s": elems / (msb * 1e-3),
+                                    "achieved_GBs": round(algb / (msb * 1e-3) / 1e9, 1),
+                                    "frac_hbm": round(algb / (msb * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del xb, dtb, Bb, Cb, yb
+
+        # Generic decays: the same workload with A perturbed off the S4D-real
+        # structure, which disables the power-chain path (one exp per state).
+        Ag = A * (1.0 + 0.01 * torch.rand(A.shape, device="cuda", generator=torch.Generator(
+            device="cuda").manual_seed(7)))
+        fng = lambda: K.scan1d_fwd(x, dt, Ag, Bm, Cm, y, h_final=hf, stream=stream)  # noqa: E731
+        perg, _ = time_launches(torch, stream, fng, args.steps, 20)
+        msg = sum(perg) / len(perg)
+        extra["scan1d_fwd_f32_generic_A"] = {
+            "ms": round(msg, 4), "elems_per_s": elems / (msg * 1e-3),
+            "achieved_GBs": round(alg / (msg * 1e-3) / 1e9, 1),
+            "frac_hbm": round(alg / (msg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+        # The headline: W warm-up steps, then exactly K timed steps.
+        fn = lambda: K.scan1d_fwd(x, dt, A, Bm, Cm, y, h_final=hf, stream=stream)  # noqa: E731
+        per, wall = time_launches(torch, stream, fn, args.steps, args.warmup)
+        ms = sum(per) / len(per)
+        ach = alg / (ms * 1e-3) / 1e9
 
     traffic = None
     tf = ROOT / "profiles" / "scan1d_fwd_c1_traffic.json"
     if tf.exists():
         traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
-
-    cpu = None
-    if not args.no_cpu:
-        xh, dth, Ah, Bh, Ch = (t.float().cpu().numpy() for t in (x, dt, A, Bm, Cm))
-        rate, nb, secs = cpu_baseline_scan1d(xh, dth, Ah, Bh, Ch)
-        cpu = {"value": rate, "unit": "elems/s", "cores": 1, "kind": "port",
-               "sample": f"{nb} of {Bsz} batch elements of the same workload (L={L}, D={D}, N={N}), "
-                         f"oracle restatement of cpu/scan1d.asm, single thread, {secs:.1f} s",
-               "host": platform.processor() or platform.machine(), "nproc": os.cpu_count()}
 
     line = {
         "metric": METRIC,
@@ -546,6 +638,8 @@ def main():
                    "B": Bsz, "L": L, "D": D, "N": N},
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": "profiles/scan1d_fwd_c1_traffic.json: rocprofv3 FETCH_SIZE and "
+                                       "WRITE_SIZE of this kernel, scaled by a copy calibration",
                      "kernel": "km::scan1d_fwd_chunked (fp32, B/C shared over channels)",
                      "alg_bytes": alg,
                      "avg_launch_ms": round(ms, 5)},

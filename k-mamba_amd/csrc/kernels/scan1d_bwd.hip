@@ -323,7 +323,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
         float dsum = 0.f;
 #pragma unroll
         for (int k = 0; k < TC; ++k) {
-            dsum += ds[k];
+            dsum = (k == 0) ? ds[0] : dsum + ds[k];
             if constexpr (FAST) {
                 pow_chain_b<NPL, NS>(exp2_fast(ds[k] * A0p), n0, e[k]);
             } else {
@@ -356,14 +356,12 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
             // checkpoint, replay.
             float hl[NPL];
 #pragma unroll
-            for (int j = 0; j < NPL; ++j) hl[j] = 0.f;
-#pragma unroll
             for (int k = 0; k < TC; ++k) {
                 float bv[NPL];
                 bc_row(sB, rB, slot, s, w * TC + k, bv);
                 const float u = ds[k] * xs[k];
 #pragma unroll
-                for (int j = 0; j < NPL; ++j) hl[j] = fmaf(e[k][j], hl[j], bv[j] * u);
+                for (int j = 0; j < NPL; ++j) hl[j] = (k == 0) ? bv[j] * u : fmaf(e[k][j], hl[j], bv[j] * u);
             }
 #pragma unroll
             for (int j = 0; j < NPL; ++j) {

@@ -318,9 +318,10 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
         // the replay.
         float e[TC][NPL];
         float bus[STORE_BU ? TC : 1][NPL];
+        // The first step starts from zero: hl = B*u and dsum = delta, with no
+        // fma(e, 0, .) (which the compiler may not fold: e*0 is NaN for e
+        // inf or NaN).
         float hl[NPL];
-#pragma unroll
-        for (int j = 0; j < NPL; ++j) hl[j] = 0.f;
         float dsum = 0.f;
         float bln[NPL];
         bc_row(sB, rB, slot, s, 0, bln);
@@ -331,7 +332,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             for (int j = 0; j < NPL; ++j) bv[j] = bln[j];
             if (k + 1 < TC) bc_row(sB, rB, slot, s, k + 1, bln);
             const float u = ds[k] * xs[k];
-            dsum += ds[k];
+            dsum = (k == 0) ? ds[0] : dsum + ds[k];
             if constexpr (FAST) {
                 pow_chain_il<NPL, NS>(exp2_fast(ds[k] * A0p), ns, e[k]);
             } else {
@@ -342,7 +343,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             for (int j = 0; j < NPL; ++j) {
                 const float bu = bv[j] * u;
                 if constexpr (STORE_BU) bus[k][j] = bu;
-                hl[j] = fmaf(e[k][j], hl[j], bu);
+                hl[j] = (k == 0) ? bu : fmaf(e[k][j], hl[j], bu);
             }
         }
         float P[NPL];

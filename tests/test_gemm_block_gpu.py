@@ -59,6 +59,37 @@ def test_gemm_vs_float64(M, N, Kd, out_bf16):
     assert_close(C.float().cpu().numpy(), ref, TOL_BF16 / 4 if out_bf16 else TOL_F32, "C", kap)
 
 
+@pytest.mark.parametrize("M,N,Kd,epi,bias", [(300, 264, 256, K.KM_EPI_NONE, False),
+                                              (1000, 520, 384, K.KM_EPI_SILU, True),
+                                              (8192, 2304, 128, K.KM_EPI_NONE, False),
+                                              (600, 512, 256, K.KM_EPI_SOFTPLUS, True),
+                                              (257, 256, 1152, K.KM_EPI_NONE, True)])
+def test_gemm_256_tiles_edges_and_epilogues(M, N, Kd, epi, bias):
+    # The 256 x 256 kernel with bf16 C: ragged M and N edges (nothing written
+    # past them), more tiles than CUs, bias and activation epilogues. C sits
+    # inside a wider buffer to catch stores past N.
+    g = rng_for("gemm-pers", M, N, Kd, epi)
+    A = bf16_round(g.standard_normal((M, Kd)).astype(np.float32))
+    B = bf16_round((g.standard_normal((N, Kd)) / np.sqrt(Kd)).astype(np.float32))
+    bv = g.standard_normal(N).astype(np.float32) if bias else None
+    ldc = N + 8
+    Cbuf = torch.full((M, ldc), 7.0, device=DEV, dtype=torch.bfloat16)
+    K.gemm_bf16(bf(A), bf(B), Cbuf, bias=None if bv is None else f32(bv), epilogue=epi, M=M, N=N,
+                K=Kd, ldc=ldc)
+    torch.cuda.synchronize()
+    got = Cbuf.float().cpu().numpy()
+    assert (got[:, N:] == 7.0).all(), "wrote past N"
+    pre = A.astype(np.float64) @ B.astype(np.float64).T + (0 if bv is None else bv)
+    kap = np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64).T + (0 if bv is None else np.abs(bv))
+    if epi == K.KM_EPI_NONE:
+        assert_close(got[:, :N], pre, TOL_BF16 / 4, "C", kap)
+    else:
+        fn = softplus_ref if epi == K.KM_EPI_SOFTPLUS else silu_ref
+        ref = fn(pre.astype(np.float32)).astype(np.float64)
+        err = np.abs(got[:, :N] - ref) / np.maximum(np.abs(ref), 1e-2 * np.abs(ref).max())
+        assert err.max() < 1e-2, err.max()
+
+
 @pytest.mark.parametrize("M,N,Kd", [(16384, 2048, 1024), (16384, 1024, 2048), (16384, 4096, 1024),
                                     (16384, 96, 2048)])
 def test_gemm_block_shapes_sampled_rows(M, N, Kd):
