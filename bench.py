@@ -73,6 +73,29 @@ def bench_scan1d_bwd(torch, K, stream, Bsz, L, D, N, dtype, steps, warmup):
             "fwd_plus_bwd_elems_per_s": Bsz * L * D / ((ms + msf) * 1e-3)}
 
 
+def bench_scan1d_shape(torch, K, stream, Bsz, L, D, N, dtype, steps, warmup):
+    """Scan1D forward at one shape (make_inputs' distributions, B/C shared
+    over channels, y and h_final written), called through the C-ABI with a
+    prebuilt argument struct so that small shapes time the GPU, not the
+    Python wrapper."""
+    import ctypes as C
+    x, dt, A, Bm, Cm = make_inputs(torch, Bsz, L, D, N, dtype)
+    y = torch.empty_like(x)
+    hf = torch.empty((Bsz, D, N), device="cuda")
+    args = K.scan1d_fwd_args(x, dt, A, Bm, Cm, y, h_final=hf)
+    ref, st = C.byref(args), C.c_void_p(stream.cuda_stream)
+
+    def fn():
+        if K.km_scan1d_fwd_c(ref, st) != 0:
+            raise RuntimeError(K.km_last_error())
+    per, _ = time_launches(torch, stream, fn, steps, warmup)
+    ms = sum(per) / len(per)
+    alg = scan1d_alg_bytes(Bsz, L, D, N, 2 if dtype == "bf16" else 4)
+    return {"ms": round(ms, 5), "elems_per_s": Bsz * L * D / (ms * 1e-3),
+            "achieved_GBs": round(alg / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def bench_convnd(torch, K, stream, dims, D, Kk, steps, warmup):
     """configs[3] workload: input ~ N(0,1) [P,D]; kernel ~ N(0, 1/K^nd)
     [K^nd,D]; bias ~ N(0, 0.01) [D]; causal zero padding, stride 1.
@@ -460,11 +483,15 @@ def main():
     # (the GPU needs ~0.1 s of load after idle).
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["all", "scan1d", "scan1d_bwd", "scannd", "convnd", "block",
-                                       "mamba3", "gemm", "model", "scannd_bwd", "copy"],
+    ap.add_argument("--only", choices=["all", "scan1d", "scan1d_shapes", "scan1d_bwd", "scannd",
+                                       "convnd", "block", "mamba3", "gemm", "model", "scannd_bwd",
+                                       "copy"],
                     default="all",
-                    help="profiling modes: scan1d = the fp32 headline kernel only; copy = a plain "
-                         "1 GiB device copy (calibrates rocprof FETCH_SIZE/WRITE_SIZE)")
+                    help="profiling modes: scan1d = the fp32 headline kernel only; scan1d_shapes = "
+                         "the forward at each --shapes entry; copy = a plain 1 GiB device copy "
+                         "(calibrates rocprof FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--shapes", nargs="+", default=["1,128,384"],
+                    help="B,L,D[,dtype] entries for --only scan1d_shapes (N = 16; dtype f32 or bf16)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; multi-GPU sharding is design-only "
@@ -532,6 +559,17 @@ def main():
         ms = sum(per) / len(per)
         print(json.dumps({"scan1d_f32_ms": ms, "GBs": scan1d_alg_bytes(Bsz, L, D, N, 4) / (ms * 1e-3) / 1e9}))
         return
+    if args.only == "scan1d_shapes":
+        out = {}
+        with torch.cuda.stream(stream):
+            for e in args.shapes:
+                f = e.split(",")
+                Bsz, L, D = (int(v) for v in f[:3])
+                dtype = f[3] if len(f) > 3 else "f32"
+                out[f"B{Bsz}_L{L}_D{D}_{dtype}"] = bench_scan1d_shape(torch, K, stream, Bsz, L, D, 16,
+                                                                      dtype, args.steps, args.warmup)
+        print(json.dumps(out))
+        return
     if args.only == "scannd":
         with torch.cuda.stream(stream):
             r2 = bench_scannd(torch, K, stream, (256, 256), 256, 16, args.steps, args.warmup)
@@ -582,6 +620,13 @@ def main():
             torch, K, stream, (256, 256), 256, 16, max(5, args.steps // 10), 2)
         extra["scannd_bwd_3d_64cubed_D128_M16_f32"] = bench_scannd_bwd(
             torch, K, stream, (64, 64, 64), 128, 16, max(5, args.steps // 10), 2)
+        # configs[0] (the reference's CPU-runnable case: 12 workgroups, one
+        # per (batch, 32-channel group)) and a few-pairs long sequence that
+        # the launcher splits over 256 workgroups (8 segments of 1024 steps).
+        extra["scan1d_fwd_configs0_B1_L128_D384_f32"] = bench_scan1d_shape(
+            torch, K, stream, 1, 128, 384, 16, "f32", max(20, args.steps), 10)
+        extra["scan1d_fwd_split_B1_L8192_D1024_f32"] = bench_scan1d_shape(
+            torch, K, stream, 1, 8192, 1024, 16, "f32", max(20, args.steps), 10)
 
         # bf16 I/O forward (reported, not the headline)
         xb, dtb, Ab, Bb, Cb = make_inputs(torch, Bsz, L, D, N, "bf16")

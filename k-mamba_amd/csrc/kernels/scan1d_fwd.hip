@@ -26,6 +26,7 @@
 //    unclamped and tracks max|h| and NaN; a workgroup that saw either re-runs
 //    its whole sequence with the sequential clamped recurrence, so results
 //    follow the per-step clamp exactly.
+#include <algorithm>
 #include <cstdlib>
 #include <type_traits>
 
@@ -53,6 +54,14 @@ struct Scan1DFwdArgs {
     long B, L, D, N;
     long sb, st, sd;
     int clamp;
+    // Segmented launches (the sequence split over workgroups): a workgroup
+    // whose states leave [-1000, 1000] sets clamp_flag[b / nseg * groups +
+    // group] and leaves the sequential re-run to scan1d_clamp_repair, or
+    // null for the workgroup's own fallback.
+    int *clamp_flag;
+    long nseg;
+    // [B, D] sum of delta over the sequence (kernels built with DSUM).
+    float *dsum_out;
 };
 
 // Output of one step: the readout, plus Dskip*x and times SiLU(z) when
@@ -137,7 +146,7 @@ __device__ __forceinline__ void pow_chain_il(float e1, int ns, float (&e)[NPL]) 
 // OCC: waves per SIMD the register allocation must allow (2 workgroups of
 // 8 waves per CU need 4).
 template <typename T, int NPL, int NS, int W, int TC, bool SHARED, bool HIST, bool STORE_BU, int OCC,
-          bool GATE>
+          bool GATE, bool DSUM = false>
 __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs p) {
     using IO = bio<T>;
     constexpr int DL = 64 / NS;      // channels per wave
@@ -300,6 +309,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     float h[NPL];
     float hmax = 0.f;
     bool nan_seen = false;
+    float dtot = 0.f;      // DSUM: this wave's sum of delta over the sequence
 
     // FASTC selects the structured-decay form at compile time, so each body
     // is straight-line code the scheduler can interleave across steps.
@@ -346,6 +356,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
                 hl[j] = (k == 0) ? bu : fmaf(e[k][j], hl[j], bu);
             }
         }
+        if constexpr (DSUM) dtot += dsum;
         float P[NPL];
         if constexpr (FAST) {
             pow_chain_il<NPL, NS>(exp2_fast(dsum * A0p), ns, P);
@@ -451,8 +462,30 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     if (fast) run(std::true_type{});
     else run(std::false_type{});
 
+    if constexpr (DSUM) {
+        // Sum of delta over the sequence: the waves' partial sums in wave
+        // order (aggP is free once every wave is past the last super-chunk).
+        if constexpr (W > 1) {
+            __syncthreads();
+            aggP[w][0][lane] = dtot;
+            __syncthreads();
+            if (w == 0) {
+                dtot = aggP[0][0][lane];
+#pragma unroll
+                for (int i = 1; i < W; ++i) dtot += aggP[i][0][lane];
+            }
+        }
+        if (w == 0 && dvalid && ns == 0) p.dsum_out[b * Dm + d] = dtot;
+    }
+
     const int bad = p.clamp && (nan_seen || hmax > 1000.f);
     if (__syncthreads_or(bad)) {
+        if (p.clamp_flag) {
+            // A segment of a split sequence: states entering later segments
+            // are also off, so the whole sequence is re-run by the repair.
+            if (tid == 0) p.clamp_flag[(b / p.nseg) * ngroups + (blockIdx.x - b * ngroups)] = 1;
+            return;
+        }
         // The sequential pass keeps each lane's states contiguous
         // (n = n0 + j) and writes every output itself.
         if (w == 0) {
@@ -554,6 +587,194 @@ static int launch_n16(const Scan1DFwdArgs &a, bool shared, bool hist, hipStream_
     return launch_chunked<T, 8, 2, 8, 8, true>(a, shared, hist, s);
 }
 
+// ---------------------------------------------------------------------------
+// Sequences split over workgroups (few (batch, channel group) pairs, long L):
+// segment s of batch element b is "batch element" b*S + s of a [B*S, Ls, .]
+// view of the same buffers. (1) the chunked kernel runs every segment from a
+// zero state, writing its local end state hl and its sum of delta; (2)
+// scan1d_segment_fold forms each segment's incoming state
+// h_in[s+1] = exp(A * sum delta over s) h_in[s] + hl[s] (and the final
+// state); (3) the chunked kernel replays every segment from its incoming
+// state, writing y. With the per-step clamp, a
+// segment whose states leave [-1000, 1000] flags its (batch, group) and
+// scan1d_clamp_repair re-runs that whole sequence with the sequential
+// clamped recurrence.
+// ---------------------------------------------------------------------------
+
+// One thread per (batch, channel, state) of N = 16 states: the fold over
+// at most kMaxSegments segments, h_in[s+1] = exp(A * dsum[s]) h_in[s] + hl[s].
+// Every segment's operands are loaded before the arithmetic (they do not
+// depend on the state), so the kernel waits for memory once, not once per
+// segment. Also zeroes the clamp flags.
+constexpr int kMaxSegments = 64;
+__global__ void __launch_bounds__(256) scan1d_segment_fold(const float *A, const float *h0,
+                                                           const float *hl, const float *dsum,
+                                                           float *hin, float *hfin, int *flags,
+                                                           long nflags, long B, long D, int nseg) {
+    constexpr int N = 16;
+    const long gid = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid < nflags) flags[gid] = 0;
+    if (gid >= B * D * N) return;
+    const long bd = gid / N, n = gid - bd * N;
+    const long b = bd / D, d = bd - b * D;
+    const long base = b * nseg;                      // segment sg is row base + sg of [B*S, D, N]
+    float ds[kMaxSegments], hv[kMaxSegments];
+#pragma unroll
+    for (int sg = 0; sg < kMaxSegments; ++sg) {
+        if (sg < nseg) {
+            ds[sg] = dsum[(base + sg) * D + d];
+            hv[sg] = hl[((base + sg) * D + d) * N + n];
+        }
+    }
+    const float a2 = A[d * N + n] * kLog2e;
+    float h = h0 ? h0[gid] : 0.f;                    // h0 is [B, D, N]: index gid
+#pragma unroll
+    for (int sg = 0; sg < kMaxSegments; ++sg) {
+        if (sg < nseg) {
+            hin[((base + sg) * D + d) * N + n] = h;
+            h = fmaf(exp2_fast(ds[sg] * a2), h, hv[sg]);
+        }
+    }
+    if (hfin) hfin[gid] = h;
+}
+
+// Re-runs every flagged (batch, channel group) sequence from its start with
+// the sequential clamped recurrence (wave 0 of a one-wave workgroup per
+// pair), writing y, the history and the final state over the segmented
+// results; unflagged pairs exit at once.
+template <typename T, int NPL, int NS, bool SHARED, bool HIST>
+__global__ void __launch_bounds__(64) scan1d_clamp_repair(Scan1DFwdArgs p, const int *flags) {
+    constexpr int DL = 64 / NS;
+    const long ngroups = (p.D + DL - 1) / DL;
+    if (flags[blockIdx.x] == 0) return;
+    const int lane = threadIdx.x & 63;
+    const long b = blockIdx.x / ngroups;
+    const long d = (blockIdx.x - b * ngroups) * DL + lane % DL;
+    const bool dvalid = d < p.D;
+    const int n0 = (lane / DL) * NPL;
+    const long dc = dvalid ? d : p.D - 1;
+    float Apc[NPL];
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) Apc[j] = p.A[dc * p.N + n0 + j] * kLog2e;
+    scan1d_serial_wave<T, NPL, NS, SHARED, HIST>(p, b, d, dvalid, n0, Apc);
+}
+
+// Segment length override (KM_SCAN1D_SPLIT, read once): 0 never splits, a
+// multiple of 64 that divides L is used as the segment length, unset (or any
+// other value) leaves the choice to segment_length's cost model.
+static long scan1d_split_override() {
+    static const long v = [] {
+        const char *e = std::getenv("KM_SCAN1D_SPLIT");
+        return e ? std::atol(e) : -1L;
+    }();
+    return v;
+}
+
+// Segment length for a split launch, or 0 to run unsplit. Only N = 16 and
+// layouts whose batch stride is the sequence's (the [B*S, Ls, .] view),
+// without checkpoints, when the unsplit grid leaves CUs idle. The model,
+// from gfx950 timings of the 8-wave kernel with one workgroup per CU: a
+// launch of n workgroups over Ls steps takes (4 + 2.1 ceil(Ls/64))
+// ceil(n/256) us; a split runs two such launches over S = L/Ls segments of
+// B*groups*S workgroups, plus ~6 us for the fold and the clamp check. The
+// split is taken when the best segment length beats the unsplit launch by
+// 15 %.
+static long segment_length(const KMScan1DFwd *k, long groups_total) {
+    if (k->N != 16 || k->h_ckpt || groups_total >= 128 || k->L % 64 != 0 || k->L < 128) return 0;
+    if (k->B > 1 && k->bc_sb != k->L * k->bc_st) return 0;
+    const long ov = scan1d_split_override();
+    if (ov == 0) return 0;
+    if (ov > 0)
+        return (ov % 64 == 0 && ov < k->L && k->L % ov == 0 && k->L / ov <= kMaxSegments) ? ov : 0;
+    auto launch_us = [](long steps, long wgs) {
+        return (4.0 + 2.1 * static_cast<double>((steps + 63) / 64)) *
+               static_cast<double>((wgs + 255) / 256);
+    };
+    const double unsplit = launch_us(k->L, groups_total);
+    double best_t = 0.85 * unsplit;
+    long best = 0;
+    for (long ls = 64; ls < k->L; ls += 64) {
+        if (k->L % ls != 0 || k->L / ls > kMaxSegments) continue;
+        const double t = 2.0 * launch_us(ls, groups_total * (k->L / ls)) + 6.0;
+        if (t < best_t) {
+            best_t = t;
+            best = ls;
+        }
+    }
+    return best;
+}
+
+// Segment workgroups have the unsplit kernel's shape: 8 waves of 8 steps
+// (64-step super-chunks).
+template <typename T>
+static int launch_segmented(const KMScan1DFwd *k, long Ls, hipStream_t s) {
+    constexpr int NPL = 8, NS = 2, DL = 32, WS = 8;
+    const long S = k->L / Ls;
+    const long groups = (k->D + DL - 1) / DL;
+    const long BS = k->B * S;
+    const size_t st = align_up(sizeof(float) * BS * k->D * k->N, 256);
+    const size_t sd = align_up(sizeof(float) * BS * k->D, 256);
+    char *ws = static_cast<char *>(Workspace::reserve(2 * st + sd + align_up(4 * k->B * groups, 256), s));
+    if (!ws) return -1;
+    float *hl = reinterpret_cast<float *>(ws);
+    float *hin = reinterpret_cast<float *>(ws + st);
+    float *dsum = reinterpret_cast<float *>(ws + 2 * st);
+    int *flags = reinterpret_cast<int *>(ws + 2 * st + sd);
+    const long grid = BS * groups;
+    if (grid > 0x7fffffffL) {
+        set_error("km_scan1d_fwd: grid of %ld workgroups out of range", grid);
+        return -1;
+    }
+    const bool shared = (k->bc_sd == 0), hist = (k->h_hist != nullptr);
+    const bool gate = k->z || k->Dskip;
+    // (1) local end states and delta sums of every segment, from zero
+    Scan1DFwdArgs a{k->x, k->delta, k->A, k->Bm, k->Cm, nullptr, nullptr, hl, nullptr, nullptr, 1,
+                    nullptr, nullptr, BS, Ls, k->D, k->N, Ls * k->bc_st, k->bc_st, k->bc_sd, 0,
+                    nullptr, S, dsum};
+#define KM_SEG(SH, HI, GA, BU) \
+    hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, WS, 8, SH, HI, BU, 2, GA, true>), dim3(grid), dim3(64 * WS), 0, s, a)
+    if (shared) KM_SEG(true, false, false, true); else KM_SEG(false, false, false, true);
+    KM_HIP_TRY(hipGetLastError());
+    // (2) incoming state of every segment, the final state, flags cleared
+    const long nth = k->B * k->D * k->N;      // >= B * groups flags
+    hipLaunchKernelGGL(scan1d_segment_fold, dim3((nth + 255) / 256), dim3(256), 0, s, k->A, k->h0,
+                       static_cast<const float *>(hl), static_cast<const float *>(dsum), hin,
+                       k->h_final, flags, k->B * groups, k->B, k->D, static_cast<int>(S));
+    KM_HIP_TRY(hipGetLastError());
+    // (3) replay every segment from its incoming state
+    Scan1DFwdArgs r{k->x, k->delta, k->A, k->Bm, k->Cm, k->y, hin, nullptr, k->h_hist, nullptr, 1,
+                    k->z, k->Dskip, BS, Ls, k->D, k->N, Ls * k->bc_st, k->bc_st, k->bc_sd, k->clamp,
+                    k->clamp ? flags : nullptr, S};
+#define KM_SEGR(SH, HI, GA) \
+    hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, WS, 8, SH, HI, !HI && !GA, 2, GA>), dim3(grid), dim3(64 * WS), 0, s, r)
+    if (shared) {
+        if (hist) { if (gate) KM_SEGR(true, true, true); else KM_SEGR(true, true, false); }
+        else      { if (gate) KM_SEGR(true, false, true); else KM_SEGR(true, false, false); }
+    } else {
+        if (hist) { if (gate) KM_SEGR(false, true, true); else KM_SEGR(false, true, false); }
+        else      { if (gate) KM_SEGR(false, false, true); else KM_SEGR(false, false, false); }
+    }
+#undef KM_SEGR
+#undef KM_SEG
+    KM_HIP_TRY(hipGetLastError());
+    if (k->clamp) {
+        // (4) flagged sequences again, sequentially with the clamp
+        Scan1DFwdArgs q{k->x, k->delta, k->A, k->Bm, k->Cm, k->y, k->h0, k->h_final, k->h_hist, nullptr,
+                        1, k->z, k->Dskip, k->B, k->L, k->D, k->N, k->bc_sb, k->bc_st, k->bc_sd, 1,
+                        nullptr, 1};
+        const dim3 g2(static_cast<unsigned>(k->B * groups));
+        if (shared) {
+            if (hist) hipLaunchKernelGGL((scan1d_clamp_repair<T, NPL, NS, true, true>), g2, dim3(64), 0, s, q, flags);
+            else      hipLaunchKernelGGL((scan1d_clamp_repair<T, NPL, NS, true, false>), g2, dim3(64), 0, s, q, flags);
+        } else {
+            if (hist) hipLaunchKernelGGL((scan1d_clamp_repair<T, NPL, NS, false, true>), g2, dim3(64), 0, s, q, flags);
+            else      hipLaunchKernelGGL((scan1d_clamp_repair<T, NPL, NS, false, false>), g2, dim3(64), 0, s, q, flags);
+        }
+        KM_HIP_TRY(hipGetLastError());
+    }
+    return 0;
+}
+
 template <typename T>
 static int launch_serial(const Scan1DFwdArgs &a, bool hist, hipStream_t s) {
     const long threads = a.B * a.D;
@@ -599,7 +820,7 @@ int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream) {
     }
     Scan1DFwdArgs a{k->x, k->delta, k->A, k->Bm, k->Cm, k->y, k->h0, k->h_final, k->h_hist,
                     k->h_ckpt, (k->L + kCkptSteps - 1) / kCkptSteps, k->z, k->Dskip,
-                    k->B, k->L, k->D, k->N, k->bc_sb, k->bc_st, k->bc_sd, k->clamp};
+                    k->B, k->L, k->D, k->N, k->bc_sb, k->bc_st, k->bc_sd, k->clamp, nullptr, 1};
     // The register-blocked kernel addresses each batch element's windows with
     // 32-bit byte offsets; larger problems take the sequential kernel.
     const long es = (k->dtype == KM_BF16) ? 2 : 4;
@@ -612,6 +833,10 @@ int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream) {
     const bool bf = (k->dtype == KM_BF16);
     if (!small_windows)
         return bf ? launch_serial<bf16_t>(a, hist, stream) : launch_serial<f32_t>(a, hist, stream);
+    // Few (batch, channel group) pairs and a long sequence: split the
+    // sequence over workgroups.
+    if (const long Ls = segment_length(k, k->B * ((k->D + 31) / 32)))
+        return bf ? launch_segmented<bf16_t>(k, Ls, stream) : launch_segmented<f32_t>(k, Ls, stream);
     switch (k->N) {
     case 16:
         return bf ? launch_n16<bf16_t>(a, shared, hist, stream)

@@ -323,9 +323,9 @@ def _scan1d_io(x, A, Bm, Cm, bc_strides):
     return Bsz, L, D, N, io, (KM_BF16 if io == torch.bfloat16 else KM_F32), bc_strides
 
 
-def scan1d_fwd(x, delta, A, Bm, Cm, y, *, h0=None, h_final=None, h_hist=None, h_ckpt=None,
-               bc_strides=None, clamp=True, z=None, Dskip=None, stream=None):
-    """km_scan1d_fwd on torch device tensors.
+def scan1d_fwd_args(x, delta, A, Bm, Cm, y, *, h0=None, h_final=None, h_hist=None, h_ckpt=None,
+                    bc_strides=None, clamp=True, z=None, Dskip=None):
+    """KMScan1DFwd over torch device tensors.
 
     x, delta, y: [B, L, D] (one dtype: fp32 or bf16); A: [D, N] fp32;
     Bm/Cm: [B, L, N] shared over channels (default strides) or any layout
@@ -347,9 +347,14 @@ def scan1d_fwd(x, delta, A, Bm, Cm, y, *, h0=None, h_final=None, h_hist=None, h_
     _need(h_ckpt, "h_ckpt", shape=(Bsz, nck, D, N), dtype=torch.float32, optional=True)
     _on_gpu(x=x, delta=delta, A=A, Bm=Bm, Cm=Cm, y=y, z=z, Dskip=Dskip, h0=h0, h_final=h_final,
             h_hist=h_hist, h_ckpt=h_ckpt)
-    args = KMScan1DFwd(ptr(x), ptr(delta), ptr(A), ptr(Bm), ptr(Cm), ptr(y), ptr(h0),
+    return KMScan1DFwd(ptr(x), ptr(delta), ptr(A), ptr(Bm), ptr(Cm), ptr(y), ptr(h0),
                        ptr(h_final), ptr(h_hist), Bsz, L, D, N, *bc_strides, dt, int(clamp),
                        ptr(h_ckpt), ptr(z), ptr(Dskip))
+
+
+def scan1d_fwd(x, delta, A, Bm, Cm, y, *, stream=None, **kw):
+    """km_scan1d_fwd on torch device tensors (arguments as scan1d_fwd_args)."""
+    args = scan1d_fwd_args(x, delta, A, Bm, Cm, y, **kw)
     check(km_scan1d_fwd_c(C.byref(args), C.c_void_p(stream_handle(stream))), "km_scan1d_fwd")
 
 

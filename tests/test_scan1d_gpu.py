@@ -114,6 +114,84 @@ def test_clamp_fallback_follows_per_step_clamp():
     assert_close(hh2, hhu, TOL_F32, "unclamped h", khh)
 
 
+# Few (batch, 32-channel group) pairs and a long sequence with N = 16: the
+# launcher splits the sequence into segments over workgroups (segment end
+# states from a zero start, a fold over segments, a replay from the folded
+# states); these shapes take the split under its cost model (4 to 64
+# segments, 10 and 12 among them). D not a multiple of 32 leaves lanes
+# without a channel; B > 1 exercises the [B*S, Ls, ...] view of the batch.
+SPLIT = [(1, 1024, 64), (2, 1024, 40), (3, 1024, 100), (1, 4096, 32), (1, 640, 96), (2, 768, 200)]
+
+
+@pytest.mark.parametrize("Bsz,L,D", SPLIT)
+@pytest.mark.parametrize("layout", ["shared", "per_channel"])
+def test_split_sequence_h0_hist(Bsz, L, D, layout):
+    N = 16
+    x, dt, A, _, _ = scan1d_inputs(Bsz, L, D, N, seed=11)
+    g = rng_for("split", Bsz, L, D, N)
+    h0 = g.standard_normal((Bsz, D, N)).astype(np.float32)
+    if layout == "shared":
+        Bm = (g.standard_normal((Bsz, L, N)) * 0.25).astype(np.float32)
+        Cm = (g.standard_normal((Bsz, L, N)) * 0.25).astype(np.float32)
+        strides = (L * N, N, 0)
+    else:
+        Bm = (g.standard_normal((Bsz, L, D, N)) * 0.25).astype(np.float32)
+        Cm = (g.standard_normal((Bsz, L, D, N)) * 0.25).astype(np.float32)
+        strides = (L * D * N, D * N, N)
+    yr, hr, hhr = O.scan1d_batched(x, dt, A, Bm, Cm, h0=h0, bc_strides=strides, hist=True)
+    ky, kh, khh = scan1d_kappa(x, dt, A, Bm, Cm, h0=h0, bc_strides=strides)
+    # With and without the history store (different replay kernels).
+    y, hf, hh = run_km(x, dt, A, Bm, Cm, h0=h0, hist=True, bc_strides=strides)
+    assert_close(y, yr, TOL_F32, "y", ky)
+    assert_close(hf, hr, TOL_F32, "h_final", kh)
+    assert_close(hh, hhr, TOL_F32, "h_hist", khh)
+    y2, hf2, _ = run_km(x, dt, A, Bm, Cm, h0=h0, bc_strides=strides)
+    assert_close(y2, yr, TOL_F32, "y (no history)", ky)
+    assert_close(hf2, hr, TOL_F32, "h_final (no history)", kh)
+
+
+@pytest.mark.parametrize("Bsz,L,D", SPLIT[:3])
+def test_split_sequence_bf16_gated(Bsz, L, D):
+    N = 16
+    x, dt, A, Bm, Cm = scan1d_inputs(Bsz, L, D, N, seed=12)
+    g = rng_for("split-gated", Bsz, L, D, N)
+    z = (2.0 * g.standard_normal((Bsz, L, D))).astype(np.float32)
+    Dsk = g.uniform(0.5, 1.5, D).astype(np.float32)
+    xr, dtr, Br, Cr, zr = (bf16_round(a) for a in (x, dt, Bm, Cm, z))
+    yr, hr, _ = O.scan1d_batched(xr, dtr, A, Br, Cr)
+    ky, kh, _ = scan1d_kappa(xr, dtr, A, Br, Cr)
+    sz = silu_ref(zr)
+    ref, kap = (yr + Dsk * xr) * sz, (ky + np.abs(Dsk * xr)) * np.abs(sz)
+    y, hf, _ = run_km(x, dt, A, Bm, Cm, bf16=True, z=z, Dskip=Dsk)
+    assert rel_err_cond(y, bf16_round(ref), kap) < 1e-2
+    assert_close(hf, hr, TOL_BF16, "h_final", kh)
+
+
+def test_split_sequence_clamp_in_one_group_mid_sequence():
+    # The drive leaves [-1000, 1000] only in steps 300..340 and only for the
+    # first 32 channels (one channel group): that group's sequence is re-run
+    # with the per-step clamp of cpu/scan1d.asm:136-140, the other group keeps
+    # the split result, and both match the clamped reference.
+    Bsz, L, D, N = 1, 1024, 64, 16
+    x, dt, A, Bm, Cm = scan1d_inputs(Bsz, L, D, N, seed=13)
+    x[:, 300:340, :32] *= 4000.0
+    yr, hr, hhr = O.scan1d_batched(x, dt, A, Bm, Cm, hist=True)
+    assert np.abs(hhr[:, :, :32]).max() == 1000.0
+    assert np.abs(hhr[:, :, 32:]).max() < 1000.0
+    ky, kh, khh = scan1d_kappa(x, dt, A, Bm, Cm)
+    for hist in (True, False):
+        y, hf, hh = run_km(x, dt, A, Bm, Cm, hist=hist)
+        assert_close(y, yr, TOL_F32, "y", ky)
+        assert_close(hf, hr, TOL_F32, "h_final", np.minimum(kh, 1000.0))
+        if hist:
+            assert_close(hh, hhr, TOL_F32, "h_hist", np.minimum(khh, 1000.0))
+    # Without the clamp the same drive runs free through the split path.
+    yu, hu, _ = O.scan1d_batched(x, dt, A, Bm, Cm, clamp=False)
+    y, hf, _ = run_km(x, dt, A, Bm, Cm, clamp=False)
+    assert_close(y, yu, TOL_F32, "unclamped y", ky)
+    assert_close(hf, hu, TOL_F32, "unclamped h_final", kh)
+
+
 GATED = [(2, 1, 32, 16), (1, 63, 33, 16), (2, 131, 70, 16), (1, 77, 100, 8), (2, 65, 64, 4),
          (1, 200, 96, 2)]
 
