@@ -145,8 +145,13 @@ __device__ __forceinline__ void pow_chain_il(float e1, int ns, float (&e)[NPL]) 
 
 // OCC: waves per SIMD the register allocation must allow (2 workgroups of
 // 8 waves per CU need 4).
+// FULL: L is a multiple of the super-chunk (W*TC steps), so every step of a
+// super-chunk the kernel computes is a real step. Row offsets, which are
+// wave-uniform, then go in the SGPR offset (no vector add per load or store),
+// clamped to the last row for the prefetch past the end; otherwise they go in
+// the range-checked VGPR offset and rows past L read as 0.
 template <typename T, int NPL, int NS, int W, int TC, bool SHARED, bool HIST, bool STORE_BU, int OCC,
-          bool GATE, bool DSUM = false>
+          bool GATE, bool DSUM = false, bool FULL = false>
 __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs p) {
     using IO = bio<T>;
     constexpr int DL = 64 / NS;      // channels per wave
@@ -173,11 +178,13 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     const int nit = (L + SC - 1) / SC;
     const bool store_y = dvalid && ns == 0;
     const float dsk = (GATE && p.Dskip) ? p.Dskip[dvalid ? d : p.D - 1] : 0.f;
-    // Gated output with two state halves per channel: both halves hold the
-    // step's full readout, so they gate alternate steps (half ns takes steps
-    // 2i + ns) and each loads only its own steps' z: one SiLU per two steps
-    // and one 64-lane store per step pair.
-    constexpr bool PAIRG = GATE && NS == 2 && TC % 2 == 0;
+    // Two state halves per channel (NS = 2): the readouts of steps 2i and
+    // 2i + 1 are summed over the halves by one lane swap, which leaves step
+    // 2i's sum in the lower half and step 2i + 1's in the upper half; each
+    // half then stores (and gates, loading only its own steps' z) its step:
+    // one swap, one add, one SiLU and one 64-lane store per step pair.
+    constexpr bool PAIR = NS == 2 && TC % 2 == 0;
+    constexpr bool PAIRG = GATE && PAIR;
     constexpr int ZC = GATE ? (PAIRG ? TC / 2 : TC) : 1;
 
     // Per-batch-element windows addressed with 32-bit byte offsets (the
@@ -204,7 +211,20 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     // window, which the range check drops: the stores need no branch.
     constexpr unsigned kDrop = 0x80000000u;
     const unsigned vy = store_y ? static_cast<unsigned>(vx) : kDrop;
-    const unsigned vy2 = dvalid ? static_cast<unsigned>(vx + ns * Dm * TS) : kDrop;   // paired gating
+    const unsigned vy2 = dvalid ? static_cast<unsigned>(vx + ns * Dm * TS) : kDrop;   // paired steps
+    // Byte offset of row t of a window with rb bytes per row, split into a
+    // range-checked lane part v and a wave-uniform part: FULL launches put
+    // the row in the SGPR offset (clamped to the last row, which only the
+    // prefetch of the super-chunk after the last one passes), the others in
+    // the VGPR offset.
+    auto ld_row = [&](__amdgpu_buffer_rsrc_t r, int v, int t, int rb, int tmax) -> float {
+        if constexpr (FULL) return IO::ld(r, v, (t < tmax ? t : tmax) * rb);
+        else return IO::ld(r, v + t * rb, 0);
+    };
+    auto st_row = [&](__amdgpu_buffer_rsrc_t r, unsigned v, int t, int rb, float val) {
+        if constexpr (FULL) IO::st(r, static_cast<int>(v), t * rb, val);
+        else IO::st(r, static_cast<int>(v + static_cast<unsigned>(t * rb)), 0, val);
+    };
     const unsigned vhs = dvalid ? static_cast<unsigned>(vh) : kDrop;
 
     __shared__ float sB[SHARED ? 3 : 1][SHARED ? TILE : 1];
@@ -244,11 +264,21 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
 #pragma unroll
         for (int i = 0; i < TPT; ++i) {
             const int e = tid + i * NT;
-            const int t = s * SC + e / N;
-            const int off = (e % N) * TS;
-            const int so = t * rowbc;
-            rb[i] = IO::ld(rB, off + so, 0);   // e >= TILE: a row the store skips
-            rc[i] = IO::ld(rC, off + so, 0);
+            if constexpr (FULL) {
+                // Lane part: the row within the super-chunk (e >= TILE: an
+                // element the store skips, dropped); uniform part: the
+                // super-chunk's first row, clamped to the last super-chunk.
+                const int v = e < TILE ? (e / N) * rowbc + (e % N) * TS : static_cast<int>(kDrop);
+                const int t0 = s * SC < L - SC ? s * SC : L - SC;
+                rb[i] = IO::ld(rB, v, t0 * rowbc);
+                rc[i] = IO::ld(rC, v, t0 * rowbc);
+            } else {
+                const int t = s * SC + e / N;
+                const int off = (e % N) * TS;
+                const int so = t * rowbc;
+                rb[i] = IO::ld(rB, off + so, 0);   // e >= TILE: a row the store skips
+                rc[i] = IO::ld(rC, off + so, 0);
+            }
         }
     };
     // Tile element e = (step e/N, state n = e%N) is stored at
@@ -268,14 +298,14 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     auto load_xd = [&](int s, float (&xo)[TC], float (&dto)[TC], float (&zo)[ZC]) {
 #pragma unroll
         for (int k = 0; k < TC; ++k) {
-            const int so = (s * SC + w * TC + k) * rowx;   // rows past L read as 0
-            xo[k] = IO::ld(rx, vx + so, 0);
-            dto[k] = IO::ld(rdt, vx + so, 0);
+            const int t = s * SC + w * TC + k;   // rows past L read as 0 (or, FULL, the last row)
+            xo[k] = ld_row(rx, vx, t, rowx, L - 1);
+            dto[k] = ld_row(rdt, vx, t, rowx, L - 1);
             // z is 0 when null; with paired gating, step 2i + ns of this half.
             if constexpr (PAIRG) {
-                if (k % 2 == 0) zo[k / 2] = IO::ld(rz, vx + ns * rowx + so, 0);
+                if (k % 2 == 0) zo[k / 2] = ld_row(rz, vx + ns * rowx, t, rowx, L - 2);
             } else if constexpr (GATE) {
-                zo[k] = IO::ld(rz, vx + so, 0);
+                zo[k] = ld_row(rz, vx, t, rowx, L - 1);
             }
         }
     };
@@ -286,9 +316,9 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
 #pragma unroll
             for (int j = 0; j < NPL; ++j) out[j] = row[j];
         } else {
-            const int so = (s * SC + w * TC + k) * rowbc;
+            const int t = s * SC + w * TC + k;
 #pragma unroll
-            for (int j = 0; j < NPL; ++j) out[j] = IO::ld(r, vbc + j * NS * TS + so, 0);
+            for (int j = 0; j < NPL; ++j) out[j] = ld_row(r, vbc + j * NS * TS, t, rowbc, L - 1);
         }
     };
 
@@ -425,24 +455,31 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
                 yp = fmaf(cv[j], h[j], yp);
                 hmax = fmaxf(hmax, fabsf(h[j]));
             }
-            // Sum the state groups of this channel (lanes dl + DL*ns).
+            // Sum the state groups of this channel (lanes dl + DL*ns). Rows
+            // past L and lanes without output are dropped by the range check.
             if constexpr (NS >= 4) yp = sum_xor16(yp);
-            if constexpr (NS >= 2) yp = sum_xor32(yp);
-            nan_seen |= (yp != yp);
-            // Rows past L and lanes without output are dropped by the range check.
-            if constexpr (PAIRG) {
+            if constexpr (PAIR) {
                 if (k % 2 == 0) {
                     yprev = yp;
                 } else {
-                    const float yv = ns ? yp : yprev;
-                    const float xv = ns ? xs[k] : xs[k - 1];
-                    const int yo = static_cast<int>(vy2 + static_cast<unsigned>((t - 1) * rowx));
-                    IO::st(ry, yo, 0, gated<T>(p, yv, xv, dsk, zs[k / 2]));
+                    // One swap trades the upper half of step k-1's partial
+                    // sums for the lower half of step k's: the sum is step
+                    // k-1's readout in the lower half and step k's in the
+                    // upper half, each added in the order of sum_xor32.
+                    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(yprev), __float_as_uint(yp),
+                                                                    false, false);
+                    const float yv = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+                    if constexpr (GATE) {
+                        const float xv = ns ? xs[k] : xs[k - 1];
+                        st_row(ry, vy2, t - 1, rowx, gated<T>(p, yv, xv, dsk, zs[k / 2]));
+                    } else {
+                        st_row(ry, vy2, t - 1, rowx, yv);
+                    }
                 }
             } else {
-                const int yo = static_cast<int>(vy + static_cast<unsigned>(t * rowx));
-                if constexpr (GATE) IO::st(ry, yo, 0, gated<T>(p, yp, xs[k], dsk, zs[k]));
-                else IO::st(ry, yo, 0, yp);
+                if constexpr (NS >= 2) yp = sum_xor32(yp);
+                if constexpr (GATE) st_row(ry, vy, t, rowx, gated<T>(p, yp, xs[k], dsk, zs[k]));
+                else st_row(ry, vy, t, rowx, yp);
             }
             if constexpr (HIST) {
 #pragma unroll
@@ -478,6 +515,11 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
         if (w == 0 && dvalid && ns == 0) p.dsum_out[b * Dm + d] = dtot;
     }
 
+    // A NaN state stays NaN through every later step (e * NaN + bu), so a
+    // NaN anywhere in the sequence shows in the final state of the wave that
+    // ran the last steps; finite excursions past 1000 are in hmax.
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) nan_seen |= !(fabsf(h[j]) <= 1000.f);
     const int bad = p.clamp && (nan_seen || hmax > 1000.f);
     if (__syncthreads_or(bad)) {
         if (p.clamp_flag) {
@@ -552,17 +594,22 @@ static int launch_chunked(const Scan1DFwdArgs &a, bool shared, bool hist, hipStr
     }
     dim3 g(static_cast<unsigned>(grid)), blk(64 * W);
     const bool gate = a.z || a.Dskip;
+    // Whole super-chunks only: row offsets in SGPRs (history launches keep
+    // the range-checked form).
+    const bool full = !hist && a.L % (W * TC) == 0;
     // B*u is kept in registers only without history stores or gating, whose
     // extra registers would otherwise spill.
-#define KM_CH(SH, HI, GA) \
-    hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, W, TC, SH, HI, SBU && !HI && !GA, OCC, GA>), \
+#define KM_CH(SH, HI, GA, FU) \
+    hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, W, TC, SH, HI, SBU && !HI && !GA, OCC, GA, false, FU>), \
                        g, blk, 0, s, a)
     if (shared) {
-        if (hist) { if (gate) KM_CH(true, true, true); else KM_CH(true, true, false); }
-        else      { if (gate) KM_CH(true, false, true); else KM_CH(true, false, false); }
+        if (hist) { if (gate) KM_CH(true, true, true, false); else KM_CH(true, true, false, false); }
+        else if (full) { if (gate) KM_CH(true, false, true, true); else KM_CH(true, false, false, true); }
+        else      { if (gate) KM_CH(true, false, true, false); else KM_CH(true, false, false, false); }
     } else {
-        if (hist) { if (gate) KM_CH(false, true, true); else KM_CH(false, true, false); }
-        else      { if (gate) KM_CH(false, false, true); else KM_CH(false, false, false); }
+        if (hist) { if (gate) KM_CH(false, true, true, false); else KM_CH(false, true, false, false); }
+        else if (full) { if (gate) KM_CH(false, false, true, true); else KM_CH(false, false, false, true); }
+        else      { if (gate) KM_CH(false, false, true, false); else KM_CH(false, false, false, false); }
     }
 #undef KM_CH
     KM_HIP_TRY(hipGetLastError());
@@ -731,8 +778,10 @@ static int launch_segmented(const KMScan1DFwd *k, long Ls, hipStream_t s) {
     Scan1DFwdArgs a{k->x, k->delta, k->A, k->Bm, k->Cm, nullptr, nullptr, hl, nullptr, nullptr, 1,
                     nullptr, nullptr, BS, Ls, k->D, k->N, Ls * k->bc_st, k->bc_st, k->bc_sd, 0,
                     nullptr, S, dsum};
+    // Segment lengths are multiples of the 64-step super-chunk: whole
+    // super-chunks (SGPR row offsets) except with history stores.
 #define KM_SEG(SH, HI, GA, BU) \
-    hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, WS, 8, SH, HI, BU, 2, GA, true>), dim3(grid), dim3(64 * WS), 0, s, a)
+    hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, WS, 8, SH, HI, BU, 2, GA, true, !HI>), dim3(grid), dim3(64 * WS), 0, s, a)
     if (shared) KM_SEG(true, false, false, true); else KM_SEG(false, false, false, true);
     KM_HIP_TRY(hipGetLastError());
     // (2) incoming state of every segment, the final state, flags cleared
@@ -746,7 +795,7 @@ static int launch_segmented(const KMScan1DFwd *k, long Ls, hipStream_t s) {
                     k->z, k->Dskip, BS, Ls, k->D, k->N, Ls * k->bc_st, k->bc_st, k->bc_sd, k->clamp,
                     k->clamp ? flags : nullptr, S};
 #define KM_SEGR(SH, HI, GA) \
-    hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, WS, 8, SH, HI, !HI && !GA, 2, GA>), dim3(grid), dim3(64 * WS), 0, s, r)
+    hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, WS, 8, SH, HI, !HI && !GA, 2, GA, false, !HI>), dim3(grid), dim3(64 * WS), 0, s, r)
     if (shared) {
         if (hist) { if (gate) KM_SEGR(true, true, true); else KM_SEGR(true, true, false); }
         else      { if (gate) KM_SEGR(true, false, true); else KM_SEGR(true, false, false); }
