@@ -211,9 +211,10 @@ int km_mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long
                         void *workspace, size_t workspace_bytes, void *stream);
 
 /* ScanND forward on device pointers, enqueued on `stream` (NULL = default
- * stream) without a host synchronisation. Same parameters and layout as
- * om_scannd_forward (ref include/scan_nd.h:72, cuda/scan_nd.cu); theta
- * and lambda must be NULL. Returns 0, or -1 with km_last_error() set. */
+ * stream) without a host synchronisation. Same parameters, layout and
+ * semantics as om_scannd_forward (ref include/scan_nd.h:72), including the
+ * Mamba-3 lambda branch (theta and lambda device memory). Returns 0, or -1
+ * with km_last_error() set. */
 int km_scannd_fwd(const ScanNDParams *p, void *stream);
 
 /* km_scannd_fwd without any allocation. No counterpart in the reference: it
@@ -224,7 +225,8 @@ int km_scannd_fwd(const ScanNDParams *p, void *stream);
  * fixed 1 MiB array in each GPU's memory (held until the process ends)
  * instead of a per-stream allocation; grids needing more than 262,128
  * (tile, channel group) flags, and shapes outside the tile kernels (D*M not
- * a multiple of 64, or M not dividing 64), are rejected with -1 and
+ * a multiple of 64, or M not dividing 64), and the Mamba-3 lambda branch
+ * (whose rotated states need workspace), are rejected with -1 and
  * km_last_error(). Every call on one GPU shares that array: calls that
  * overlap on one GPU (other streams, other threads) race. */
 int km_scannd_fwd_noalloc(const ScanNDParams *p, void *stream);

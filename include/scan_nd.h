@@ -37,8 +37,18 @@ typedef struct {
     float       *h;
     float       *y;
     /* Mamba-3 extensions of the reference (rotation angles [D/2], per-point
-     * lambda [P]). The GPU kernels of this library do not implement them:
-     * entry points return -1 when either is non-NULL. */
+     * lambda [P]), used by the lambda branch of scannd_ref
+     * (src/scan_nd.c:59-210) when lambda is non-NULL:
+     *   h = bpa*((1-lambda)*dt_bar*aavg) + bu*(lambda*dt_bar)
+     *       + sum_a alpha_a * hrot[p - e_a]
+     * with bu = B*x, alpha_a = exp(delta_a * min(A_a, -1e-5)), bpa and aavg
+     * the averages over the predecessors of B[prev]*x[prev] and alpha_a, and
+     * hrot a predecessor's states after the rotation of channel pairs
+     * (2i, 2i+1) by theta[i] (the states themselves when theta is NULL).
+     * The reference keeps hrot in a [D, M] buffer it indexes by point
+     * (out of bounds); this library keeps the [P, D, M] field that indexing
+     * implies. theta without lambda has no effect. scannd() applies the
+     * branch for ndims >= 3 only, as the reference dispatcher does. */
     const float *theta;
     const float *lambda;
 } ScanNDParams;

@@ -581,6 +581,101 @@ __global__ void __launch_bounds__(256) scannd_level_kernel(ScanNDArgs p, const l
     p.y[off * p.D + d] = y;
 }
 
+// Mamba-3 branch (lambda != NULL) of the reference scannd_ref_with_plan
+// (src/scan_nd.c:59-210), per wavefront level, one thread per (point,
+// channel pair): the pair's states at every m, the readouts y, and the
+// pair's rotated states R(theta) h, which the point's successors read (the
+// state itself when theta is NULL; an odd last channel is never rotated).
+// The reference keeps the rotated states in a [D, M] buffer indexed with
+// point offsets (out of bounds, and unread-before-write when theta is NULL);
+// hrot here is the [P, D, M] buffer that indexing implies. Per (d, m):
+//   bu = B x;  over the axes with a predecessor: sum of B[prev] x[prev] and
+//   of alpha_a = exp(delta_a min(A_a, -1e-5));  their averages bpa, aavg;
+//   h = bpa * ((1 - lambda) dt_bar aavg) + bu * (lambda dt_bar)
+//       + sum_a alpha_a hrot[prev_a]
+struct ScanM3Args {
+    const float *x, *B, *C, *theta, *lambda;
+    const float *A[kMaxNd];      // per axis [D, M]
+    const float *dt[kMaxNd];     // per axis [P, D]
+    float *h, *y, *hrot;
+    int nd;
+    int dims[kMaxNd];
+    long pstride[kMaxNd];
+    int D, M;
+    long DM;
+};
+
+__global__ void __launch_bounds__(256) scannd_m3_level_kernel(ScanM3Args p, const long *offsets,
+                                                              long start, long count) {
+    const int npair = (p.D + 1) / 2;
+    const long gid = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid >= count * npair) return;
+    const long off = offsets[start + gid / npair];
+    const int d0 = 2 * static_cast<int>(gid % npair);
+    const int nc = (d0 + 1 < p.D) ? 2 : 1;       // channels of this pair
+    int idx[kMaxNd];
+    {
+        long rem = off;
+        for (int a = p.nd - 1; a >= 0; --a) {
+            idx[a] = static_cast<int>(rem % p.dims[a]);
+            rem /= p.dims[a];
+        }
+    }
+    const float lam = p.lambda[off];
+    float dtb[2], xv[2], yacc[2] = {0.f, 0.f};
+    for (int c = 0; c < nc; ++c) {
+        float dsum = 0.f;
+        for (int a = 0; a < p.nd; ++a) dsum += p.dt[a][off * p.D + d0 + c];
+        dtb[c] = dsum / static_cast<float>(p.nd);
+        xv[c] = p.x[off * p.D + d0 + c];
+    }
+    float cs = 1.f, sn = 0.f;
+    const bool rot = p.theta && nc == 2;
+    if (rot) {
+        const float th = p.theta[d0 >> 1];
+        cs = cosf(th);
+        sn = sinf(th);
+    }
+    for (int m = 0; m < p.M; ++m) {
+        float hv[2] = {0.f, 0.f};
+        for (int c = 0; c < nc; ++c) {
+            const long dm = static_cast<long>(d0 + c) * p.M + m;
+            const long q = off * p.DM + dm;
+            const float bu = p.B[q] * xv[c];
+            float bpa = 0.f, aacc = 0.f, hs = 0.f;
+            int npred = 0;
+            for (int a = 0; a < p.nd; ++a) {
+                if (idx[a] > 0) {
+                    const long prev = off - p.pstride[a];
+                    const float ar = p.A[a][dm];
+                    const float av = (ar > -1e-5f) ? -1e-5f : ar;   // the branch's clamp (:129)
+                    const float al = exp2_fast(p.dt[a][off * p.D + d0 + c] * av * kLog2e);
+                    bpa += p.B[prev * p.DM + dm] * p.x[prev * p.D + d0 + c];
+                    aacc += al;
+                    hs = fmaf(al, p.hrot[prev * p.DM + dm], hs);
+                    ++npred;
+                }
+            }
+            float hn = bu * (lam * dtb[c]);
+            if (npred > 0) {
+                const float inv = 1.f / static_cast<float>(npred);
+                hn = fmaf(bpa * inv, (1.f - lam) * dtb[c] * (aacc * inv), hn) + hs;
+            }
+            p.h[q] = hn;
+            yacc[c] = fmaf(p.C[q], hn, yacc[c]);
+            hv[c] = hn;
+        }
+        const long q0 = off * p.DM + static_cast<long>(d0) * p.M + m;
+        if (rot) {
+            p.hrot[q0] = cs * hv[0] - sn * hv[1];
+            p.hrot[q0 + p.M] = sn * hv[0] + cs * hv[1];
+        } else {
+            for (int c = 0; c < nc; ++c) p.hrot[q0 + c * p.M] = hv[c];
+        }
+    }
+    for (int c = 0; c < nc; ++c) p.y[off * p.D + d0 + c] = yacc[c];
+}
+
 // Device workspace for the fallback's plan offsets (grown on demand, kept
 // for the process).
 static long *g_plan_dev = nullptr;
@@ -917,6 +1012,77 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
     return 0;
 }
 
+// Mamba-3 branch on device pointers: per-level launches over the wavefront
+// plan; the level offsets and the rotated states live in the stream's
+// library workspace.
+static int scannd_m3_device(const ScanNDParams *p, hipStream_t s, bool sync) {
+    if (!is_device_ptr(p->lambda) || (p->theta && !is_device_ptr(p->theta))) {
+        set_error("scannd: theta and lambda must be device memory on the device-pointer path");
+        return -1;
+    }
+    if (p->ndims > kMaxNd) {
+        set_error("scannd: the Mamba-3 branch supports up to %d dimensions", kMaxNd);
+        return -1;
+    }
+    const long P = wavefront_nd_total_points(p->dims, p->ndims);
+    if (P <= 0 || P > 0x7fffffffL || p->D > 0x7fffffffL || p->M > 0x7fffffffL) {
+        set_error("scannd: sizes out of range for the Mamba-3 branch");
+        return -1;
+    }
+    KMWavefrontPlan *plan = km_wavefront_plan_create(p->dims, p->ndims);
+    if (!plan) {
+        set_error("scannd: plan creation failed");
+        return -1;
+    }
+    const size_t off_bytes = align_up(sizeof(long) * P, 256);
+    const size_t rot_bytes = sizeof(float) * static_cast<size_t>(P) * p->D * p->M;
+    char *ws = static_cast<char *>(Workspace::reserve(off_bytes + rot_bytes, s));
+    if (!ws) {
+        km_wavefront_plan_free(plan);
+        return -1;
+    }
+    long *offs = reinterpret_cast<long *>(ws);
+    ScanM3Args a{};
+    a.x = p->x; a.B = p->B; a.C = p->C; a.theta = p->theta; a.lambda = p->lambda;
+    a.h = p->h; a.y = p->y; a.hrot = reinterpret_cast<float *>(ws + off_bytes);
+    a.nd = static_cast<int>(p->ndims);
+    a.D = static_cast<int>(p->D);
+    a.M = static_cast<int>(p->M);
+    a.DM = p->D * p->M;
+    long stride = 1;
+    for (int ax = a.nd - 1; ax >= 0; --ax) {
+        a.dims[ax] = static_cast<int>(p->dims[ax]);
+        a.pstride[ax] = stride;
+        stride *= p->dims[ax];
+    }
+    for (int ax = 0; ax < a.nd; ++ax) {
+        a.A[ax] = p->A + ax * p->D * p->M;
+        a.dt[ax] = p->delta + ax * P * p->D;
+    }
+    // The plan is host memory that is freed below: a synchronous copy.
+    if (hipMemcpyAsync(offs, plan->level_offsets, sizeof(long) * P, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess) {
+        km_wavefront_plan_free(plan);
+        set_error("scannd: plan upload failed");
+        return -1;
+    }
+    const long npair = (p->D + 1) / 2;
+    for (long lvl = 0; lvl <= plan->max_level; ++lvl) {
+        const long start = plan->level_starts[lvl];
+        const long count = plan->level_starts[lvl + 1] - start;
+        const long threads = count * npair;
+        hipLaunchKernelGGL(scannd_m3_level_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)),
+                           dim3(256), 0, s, a, offs, start, count);
+    }
+    km_wavefront_plan_free(plan);
+    KM_HIP_TRY(hipGetLastError());
+    if (sync && hipStreamSynchronize(s) != hipSuccess) {
+        set_error("scannd: %s", hipGetErrorString(hipGetLastError()));
+        return -1;
+    }
+    return 0;
+}
+
 // Shared front end: device pointers, scannd_ref semantics for ndims >= 2.
 // sync: wait for the result; if a dataflow wait gave up, run the call again
 // on the band schedule, so the synchronous entry points always return the
@@ -988,16 +1154,22 @@ static bool scannd_params_ok(const ScanNDParams *p) {
         set_error("scannd: invalid parameters");
         return false;
     }
-    if (p->theta || p->lambda) {
-        set_error("scannd: the Mamba-3 theta/lambda extensions are not implemented by the GPU kernels");
-        return false;
-    }
     return true;
 }
 
 int scannd_device_params(const ScanNDParams *p, hipStream_t s, bool sync, FlowBuf *ext = nullptr) {
     if (!scannd_params_ok(p)) return -1;
     if (!gpu_ready()) return -1;
+    // Mamba-3 branch (lambda given); theta alone changes nothing, as in the
+    // reference, where the rotation belongs to the lambda branch.
+    if (p->lambda) {
+        if (ext) {
+            set_error("km_scannd_fwd_noalloc: the Mamba-3 (lambda) branch needs the library "
+                      "workspace; use km_scannd_fwd");
+            return -1;
+        }
+        return scannd_m3_device(p, s, sync);
+    }
     const long P = wavefront_nd_total_points(p->dims, p->ndims);
     const float *A[kMaxNd], *dt[kMaxNd];
     for (long ax = 0; ax < p->ndims && ax < kMaxNd; ++ax) {
@@ -1085,7 +1257,8 @@ static int scannd_host(const ScanNDParams *p, bool scan1d_semantics) {
     const size_t nh = scan1d_semantics ? static_cast<size_t>(D * M) : nB;
     const bool dev = is_device_ptr(p->x) && is_device_ptr(p->A) && is_device_ptr(p->B) &&
                      is_device_ptr(p->C) && is_device_ptr(p->delta) && is_device_ptr(p->h) &&
-                     is_device_ptr(p->y);
+                     is_device_ptr(p->y) && (!p->lambda || is_device_ptr(p->lambda)) &&
+                     (!p->lambda || !p->theta || is_device_ptr(p->theta));
     int rc = 0;
     if (dev) {
         if (scan1d_semantics) {
@@ -1104,7 +1277,10 @@ static int scannd_host(const ScanNDParams *p, bool scan1d_semantics) {
         return km_last_error()[0] ? -1 : 0;
     }
     Staging::lock();
-    const size_t bytes = sizeof(float) * (2 * nx + nA + 3 * nB + ndt) + 8 * 256;
+    // Mamba-3 operands: theta [D/2] (rotation pairs) and lambda [P].
+    const size_t nth = p->lambda && p->theta ? static_cast<size_t>(D / 2 > 0 ? D / 2 : 1) : 0;
+    const size_t nlam = p->lambda ? static_cast<size_t>(P) : 0;
+    const size_t bytes = sizeof(float) * (2 * nx + nA + 3 * nB + ndt + nth + nlam) + 10 * 256;
     void *base = Staging::reserve(bytes);
     if (!base) {
         Staging::unlock();
@@ -1113,17 +1289,22 @@ static int scannd_host(const ScanNDParams *p, bool scan1d_semantics) {
     Carver c(base);
     NDStage st{c.take<float>(nx), c.take<float>(nA), c.take<float>(nB), c.take<float>(nB),
                c.take<float>(ndt), c.take<float>(nh), c.take<float>(nx)};
+    float *th = nth ? c.take<float>(nth) : nullptr;
+    float *lam = nlam ? c.take<float>(nlam) : nullptr;
     const bool ok = hipMemcpy(st.x, p->x, nx * 4, hipMemcpyHostToDevice) == hipSuccess &&
                     hipMemcpy(st.A, p->A, nA * 4, hipMemcpyHostToDevice) == hipSuccess &&
                     hipMemcpy(st.B, p->B, nB * 4, hipMemcpyHostToDevice) == hipSuccess &&
                     hipMemcpy(st.C, p->C, nB * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                    hipMemcpy(st.dt, p->delta, ndt * 4, hipMemcpyHostToDevice) == hipSuccess;
+                    hipMemcpy(st.dt, p->delta, ndt * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                    (!th || D / 2 == 0 || hipMemcpy(th, p->theta, (D / 2) * 4, hipMemcpyDefault) == hipSuccess) &&
+                    (!lam || hipMemcpy(lam, p->lambda, nlam * 4, hipMemcpyDefault) == hipSuccess);
     if (!ok) {
         set_error("scannd: host-to-device copy failed");
         rc = -1;
     } else {
         ScanNDParams q = *p;
         q.x = st.x; q.A = st.A; q.B = st.B; q.C = st.C; q.delta = st.dt; q.h = st.h; q.y = st.y;
+        q.theta = th; q.lambda = lam;
         rc = scannd_device_params(&q, nullptr, true);
         if (rc == 0 && (hipMemcpy(p->h, st.h, nh * 4, hipMemcpyDeviceToHost) != hipSuccess ||
                         hipMemcpy(p->y, st.y, nx * 4, hipMemcpyDeviceToHost) != hipSuccess)) {
@@ -1186,6 +1367,15 @@ int scannd(ScanNDParams *p) {
     if (!scannd_validate(p)) {
         km::set_error("scannd: invalid parameters");
         return -1;
+    }
+    // Ranks 1 and 2 take the reference's scan1d / scan2d paths, which have
+    // no Mamba-3 operands (src/scan_nd.c:265-305): theta and lambda are
+    // ignored there, and honoured by the scannd_ref path of rank >= 3.
+    if (p->ndims <= 2 && (p->theta || p->lambda)) {
+        ScanNDParams q = *p;
+        q.theta = nullptr;
+        q.lambda = nullptr;
+        return km::scannd_host(&q, q.ndims == 1);
     }
     return km::scannd_host(p, p->ndims == 1);
 }

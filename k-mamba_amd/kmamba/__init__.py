@@ -507,13 +507,15 @@ scan2d = _decl("scan2d", None, [C.POINTER(Scan2DParams)])
 mamba_scan2d_forward = _decl("mamba_scan2d_forward", None, [C.POINTER(Scan2DParams)])
 
 
-def scannd_params(dims, x, A, B, Cm, delta, h, y):
-    """ScanNDParams over buffers (torch device tensors or numpy arrays).
-    Returns (params, keepalive)."""
+def scannd_params(dims, x, A, B, Cm, delta, h, y, theta=None, lam=None):
+    """ScanNDParams over buffers (torch device tensors or numpy arrays), with
+    the optional Mamba-3 theta [D/2] and lambda [P]. Returns (params,
+    keepalive)."""
     dd = longs(dims)
     D, M = A.shape[-2], A.shape[-1]
     p = ScanNDParams(C.cast(dd, c_long_p), len(dims), D, M, ptr(x), ptr(A), ptr(B), ptr(Cm),
-                     ptr(delta), ptr(h), ptr(y), None, None)
+                     ptr(delta), ptr(h), ptr(y), None if theta is None else ptr(theta),
+                     None if lam is None else ptr(lam))
     return p, dd
 
 
@@ -541,17 +543,18 @@ def scannd_bwd(dims, x, A, B, Cm, delta, h, dy, dx, ddelta, dA, dB, dC, *, works
     check(km_scannd_bwd_c(C.byref(args), C.c_void_p(stream_handle(stream))), "km_scannd_bwd")
 
 
-def scannd_fwd(dims, x, A, B, Cm, delta, h, y, stream=None):
-    """km_scannd_fwd (scannd_ref semantics) on torch device tensors."""
-    p, keep = scannd_params(dims, x, A, B, Cm, delta, h, y)
+def scannd_fwd(dims, x, A, B, Cm, delta, h, y, stream=None, theta=None, lam=None):
+    """km_scannd_fwd (scannd_ref semantics, the Mamba-3 branch when lam is
+    given) on torch device tensors."""
+    p, keep = scannd_params(dims, x, A, B, Cm, delta, h, y, theta, lam)
     check(km_scannd_fwd_c(C.byref(p), C.c_void_p(stream_handle(stream))), "km_scannd_fwd")
     return keep
 
 
-def scannd_fwd_noalloc(dims, x, A, B, Cm, delta, h, y, stream=None):
+def scannd_fwd_noalloc(dims, x, A, B, Cm, delta, h, y, stream=None, theta=None, lam=None):
     """km_scannd_fwd_noalloc: km_scannd_fwd with its dataflow state in the
     library's fixed device array (no allocation)."""
-    p, keep = scannd_params(dims, x, A, B, Cm, delta, h, y)
+    p, keep = scannd_params(dims, x, A, B, Cm, delta, h, y, theta, lam)
     check(km_scannd_fwd_noalloc_c(C.byref(p), C.c_void_p(stream_handle(stream))),
           "km_scannd_fwd_noalloc")
     return keep

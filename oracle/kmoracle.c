@@ -504,22 +504,116 @@ static void scannd_point(OrcScanNDParams *p, long P, const long *strides, long o
     }
 }
 
+/* Mamba-3 branch (lambda != NULL), src/scan_nd.c:59-72 and :95-210. The
+ * reference sizes its rotated-state buffer h_rot [D, M] but indexes it with
+ * point offsets (prev * D * M + dm, :166, :200-205), and reads it whether
+ * or not theta rotated anything: out-of-bounds and uninitialised reads, so
+ * its output is undefined. This restatement follows the evident intent:
+ * hrot [P, D, M] holds each point's state after the pair rotation R(theta)
+ * (channels 2i, 2i+1 by theta[i]; an odd last channel unrotated), or the
+ * state itself when theta is NULL, and predecessors are read from it. The
+ * predecessor "Bu_prev" (:121-127, :164) is B[prev] * x[prev], which the
+ * reference stores per point (:169). Arithmetic order as written at
+ * :104-191: bu, then per axis the predecessor sums, then the averages,
+ * beta = (1 - lambda) * dt_bar * alpha_avg, gamma = lambda * dt_bar,
+ * h = bu_prev_avg * beta + bu * gamma, then alpha_a * hrot[prev_a] per axis,
+ * with A clamped to at most -1e-5 in this branch (:129, :157). */
+static void scannd_point_m3(OrcScanNDParams *p, long P, const long *strides, long offset,
+                            float *hrot) {
+    long idx[8];
+    long D = p->D, M = p->M, nd = p->ndims;
+    orc_unravel_index(offset, p->dims, strides, nd, idx);
+    float lam = p->lambda[offset];                                                     /* :99 */
+    for (long d = 0; d < D; d++) {
+        float x_val = p->x[offset * D + d];
+        float dt_bar = 0.0f, y_acc = 0.0f;
+        for (long a = 0; a < nd; a++) dt_bar += p->delta[(a * P + offset) * D + d];
+        dt_bar /= (float)nd;
+        for (long m = 0; m < M; m++) {
+            long dm = d * M + m, pdm = offset * D * M + dm;
+            float bu = p->B[pdm] * x_val;                                              /* :115 */
+            float bu_prev_acc = 0.0f, decay_acc = 0.0f;
+            int n_pred = 0;
+            for (long a = 0; a < nd; a++) {                                            /* :123-142 */
+                if (idx[a] > 0) {
+                    long prev = offset - strides[a];
+                    float dt_a = p->delta[(a * P + offset) * D + d];
+                    float av = p->A[(a * D + d) * M + m];
+                    if (av > -1e-5f) av = -1e-5f;
+                    float alpha = expf(dt_a * av);
+                    bu_prev_acc += p->B[prev * D * M + dm] * p->x[prev * D + d];
+                    decay_acc += alpha;
+                    n_pred++;
+                }
+            }
+            float bu_prev_avg = (n_pred > 0) ? (bu_prev_acc / (float)n_pred) : 0.0f;   /* :148 */
+            float alpha_avg = (n_pred > 0) ? (decay_acc / (float)n_pred) : 0.0f;
+            float beta = (1.0f - lam) * dt_bar * alpha_avg;
+            float gamma = lam * dt_bar;
+            float hn = bu_prev_avg * beta + bu * gamma;                                /* :155 */
+            if (n_pred > 0) {
+                for (long a = 0; a < nd; a++) {                                        /* :156-167 */
+                    if (idx[a] > 0) {
+                        long prev = offset - strides[a];
+                        float dt_a = p->delta[(a * P + offset) * D + d];
+                        float av = p->A[(a * D + d) * M + m];
+                        if (av > -1e-5f) av = -1e-5f;
+                        float alpha = expf(dt_a * av);
+                        hn += alpha * hrot[prev * D * M + dm];
+                    }
+                }
+            }
+            p->h[pdm] = hn;
+            y_acc += p->C[pdm] * hn;
+        }
+        p->y[offset * D + d] = y_acc;
+    }
+    /* The point's states as its successors read them (:194-209). */
+    float *hr = hrot + offset * D * M;
+    const float *hs = p->h + offset * D * M;
+    if (!p->theta) {
+        for (long i = 0; i < D * M; i++) hr[i] = hs[i];
+        return;
+    }
+    for (long d = 0; d + 1 < D; d += 2) {
+        float th = p->theta[d >> 1];
+        float cv = cosf(th), sv = sinf(th);
+        for (long m = 0; m < M; m++) {
+            float h0 = hs[d * M + m], h1 = hs[(d + 1) * M + m];
+            hr[d * M + m] = cv * h0 - sv * h1;
+            hr[(d + 1) * M + m] = sv * h0 + cv * h1;
+        }
+    }
+    if (D & 1)
+        for (long m = 0; m < M; m++) hr[(D - 1) * M + m] = hs[(D - 1) * M + m];
+}
+
 int orc_scannd_ref_with_plan(OrcScanNDParams *p, const OrcPlan *plan, int nthreads) {
     if (!orc_scannd_validate(p)) return -1;
     if (!plan || plan->ndims != p->ndims) return -1;
     for (long a = 0; a < p->ndims; a++) if (plan->dims[a] != p->dims[a]) return -1;
-    if (p->lambda || p->theta) return -1;   /* Mamba-3 branch not restated */
     long strides[8];
     if (!orc_make_row_major_strides(p->dims, p->ndims, strides)) return -1;
     long P = plan->total_points;
     if (nthreads < 1) nthreads = 1;
+    /* theta without lambda has no effect (the rotation lives in the lambda
+     * branch, :59-72). */
+    float *hrot = NULL;
+    if (p->lambda) {
+        hrot = (float *)malloc(sizeof(float) * (size_t)P * (size_t)p->D * (size_t)p->M);
+        if (!hrot) return -1;
+    }
     for (long level = 0; level <= plan->max_level; level++) {
         long s0 = plan->level_starts[level], s1 = plan->level_starts[level + 1];
 #ifdef _OPENMP
         #pragma omp parallel for schedule(static) num_threads(nthreads)
 #endif
-        for (long i = s0; i < s1; i++) scannd_point(p, P, strides, plan->level_offsets[i]);
+        for (long i = s0; i < s1; i++) {
+            if (hrot) scannd_point_m3(p, P, strides, plan->level_offsets[i], hrot);
+            else scannd_point(p, P, strides, plan->level_offsets[i]);
+        }
     }
+    free(hrot);
     return 0;
 }
 
@@ -538,6 +632,7 @@ int orc_scannd_backward(const OrcScanNDParams *p, const float *dy, float *dx, fl
     if (!p || !p->dims || p->ndims <= 0 || p->ndims > 8 || p->D <= 0 || p->M <= 0) return -1;
     if (!p->x || !p->A || !p->B || !p->C || !p->delta || !p->h || !dy) return -1;
     if (!dx || !ddelta || !dA || !dB || !dC) return -1;
+    if (p->lambda) return -1;   /* no adjoint of the Mamba-3 branch */
     if (!orc_wavefront_validate_dims(p->dims, p->ndims)) return -1;
     long strides[8], idx[8];
     if (!orc_make_row_major_strides(p->dims, p->ndims, strides)) return -1;

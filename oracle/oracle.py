@@ -269,24 +269,31 @@ def scan2d(x, A1, A2, B, Cm, delta1, delta2, d1, d2):
     return y, h
 
 
-def _nd_params(dims, x, A, B, Cm, delta, h, y):
+def _nd_params(dims, x, A, B, Cm, delta, h, y, theta=None, lam=None):
     dd = longs(dims)
     D, M = A.shape[1], A.shape[2]
     p = ScanNDParams(dd, len(dims), D, M, P(x), P(A), P(B), P(Cm), P(delta), P(h), P(y),
-                     None, None)
+                     None if theta is None else P(theta), None if lam is None else P(lam))
     return p, dd
 
 
-def scannd_ref(dims, x, A, B, Cm, delta, *, nthreads=1, use_ref=False, fast=False):
+def scannd_ref(dims, x, A, B, Cm, delta, *, theta=None, lam=None, nthreads=1, use_ref=False,
+               fast=False):
     """scannd_ref semantics: x [P, D]; A [nd, D, M]; B, C [P, D, M];
-    delta [nd, P, D]. Returns (y, h)."""
+    delta [nd, P, D]; optional Mamba-3 theta [D/2] and lambda [P] (the
+    restated lambda branch, see kmoracle.c). Returns (y, h)."""
     x, A, B, Cm, delta = map(f32, (x, A, B, Cm, delta))
+    theta = None if theta is None else f32(theta)
+    lam = None if lam is None else f32(lam)
     Pn = int(np.prod(dims))
     D, M = A.shape[1], A.shape[2]
     h = np.zeros((Pn, D, M), np.float32)
     y = np.zeros((Pn, D), np.float32)
-    p, _keep = _nd_params(dims, x, A, B, Cm, delta, h, y)
+    p, _keep = _nd_params(dims, x, A, B, Cm, delta, h, y, theta, lam)
     if use_ref:
+        # The reference's lambda branch reads out of bounds (undefined output).
+        if lam is not None:
+            raise ValueError("the compiled reference's Mamba-3 branch is undefined; use the restatement")
         rc = _load_ref().scannd_ref(C.byref(p))
     else:
         rc = (orc_fast if fast else orc).orc_scannd_ref(C.byref(p), int(nthreads))

@@ -250,8 +250,15 @@ def test_plan_mismatch_rejected():
     plan = K.km_wavefront_plan_create(K.longs((4, 5)), 2)
     assert K.scannd_ref_with_plan(C.byref(p), plan) == -1
     K.km_wavefront_plan_free(plan)
-    p.theta = x.ctypes.data                         # Mamba-3 extension: not on the GPU
-    assert K.scannd_ref(C.byref(p)) == -1 and "theta" in K.km_last_error()
+    # theta without lambda changes nothing (the rotation belongs to the
+    # Mamba-3 lambda branch, src/scan_nd.c:59-72).
+    assert K.scannd_ref(C.byref(p)) == 0, K.km_last_error()
+    y0, h0 = y.copy(), h.copy()
+    theta = np.full((2,), 0.7, np.float32)
+    p.theta = theta.ctypes.data
+    assert K.scannd_ref(C.byref(p)) == 0, K.km_last_error()
+    np.testing.assert_array_equal(y, y0)
+    np.testing.assert_array_equal(h, h0)
 
 
 @pytest.mark.parametrize("d1,d2,D,M", [(7, 5, 3, 4), (40, 33, 4, 16), (1, 1, 4, 16)])
