@@ -145,13 +145,8 @@ __device__ __forceinline__ void pow_chain_il(float e1, int ns, float (&e)[NPL]) 
 
 // OCC: waves per SIMD the register allocation must allow (2 workgroups of
 // 8 waves per CU need 4).
-// FULL: L is a multiple of the super-chunk (W*TC steps), so every step of a
-// super-chunk the kernel computes is a real step. Row offsets, which are
-// wave-uniform, then go in the SGPR offset (no vector add per load or store),
-// clamped to the last row for the prefetch past the end; otherwise they go in
-// the range-checked VGPR offset and rows past L read as 0.
 template <typename T, int NPL, int NS, int W, int TC, bool SHARED, bool HIST, bool STORE_BU, int OCC,
-          bool GATE, bool DSUM = false, bool FULL = false>
+          bool GATE, bool DSUM = false>
 __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs p) {
     using IO = bio<T>;
     constexpr int DL = 64 / NS;      // channels per wave
@@ -212,18 +207,16 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     constexpr unsigned kDrop = 0x80000000u;
     const unsigned vy = store_y ? static_cast<unsigned>(vx) : kDrop;
     const unsigned vy2 = dvalid ? static_cast<unsigned>(vx + ns * Dm * TS) : kDrop;   // paired steps
-    // Byte offset of row t of a window with rb bytes per row, split into a
-    // range-checked lane part v and a wave-uniform part: FULL launches put
-    // the row in the SGPR offset (clamped to the last row, which only the
-    // prefetch of the super-chunk after the last one passes), the others in
-    // the VGPR offset.
-    auto ld_row = [&](__amdgpu_buffer_rsrc_t r, int v, int t, int rb, int tmax) -> float {
-        if constexpr (FULL) return IO::ld(r, v, (t < tmax ? t : tmax) * rb);
-        else return IO::ld(r, v + t * rb, 0);
+    // Row t of a window with rb bytes per row at lane offset v, all in the
+    // range-checked VGPR offset: rows past L load 0 and their stores drop.
+    // (Wave-uniform row offsets in the SGPR offset measured slower on gfx950:
+    // the clamp and multiply they need per access cost issue slots of the
+    // wave, which issue rate limits this kernel more than VALU throughput.)
+    auto ld_row = [&](__amdgpu_buffer_rsrc_t r, int v, int t, int rb) -> float {
+        return IO::ld(r, v + t * rb, 0);
     };
     auto st_row = [&](__amdgpu_buffer_rsrc_t r, unsigned v, int t, int rb, float val) {
-        if constexpr (FULL) IO::st(r, static_cast<int>(v), t * rb, val);
-        else IO::st(r, static_cast<int>(v + static_cast<unsigned>(t * rb)), 0, val);
+        IO::st(r, static_cast<int>(v + static_cast<unsigned>(t * rb)), 0, val);
     };
     const unsigned vhs = dvalid ? static_cast<unsigned>(vh) : kDrop;
 
@@ -264,21 +257,11 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
 #pragma unroll
         for (int i = 0; i < TPT; ++i) {
             const int e = tid + i * NT;
-            if constexpr (FULL) {
-                // Lane part: the row within the super-chunk (e >= TILE: an
-                // element the store skips, dropped); uniform part: the
-                // super-chunk's first row, clamped to the last super-chunk.
-                const int v = e < TILE ? (e / N) * rowbc + (e % N) * TS : static_cast<int>(kDrop);
-                const int t0 = s * SC < L - SC ? s * SC : L - SC;
-                rb[i] = IO::ld(rB, v, t0 * rowbc);
-                rc[i] = IO::ld(rC, v, t0 * rowbc);
-            } else {
-                const int t = s * SC + e / N;
-                const int off = (e % N) * TS;
-                const int so = t * rowbc;
-                rb[i] = IO::ld(rB, off + so, 0);   // e >= TILE: a row the store skips
-                rc[i] = IO::ld(rC, off + so, 0);
-            }
+            const int t = s * SC + e / N;
+            const int off = (e % N) * TS;
+            const int so = t * rowbc;
+            rb[i] = IO::ld(rB, off + so, 0);   // e >= TILE: a row the store skips
+            rc[i] = IO::ld(rC, off + so, 0);
         }
     };
     // Tile element e = (step e/N, state n = e%N) is stored at
@@ -298,14 +281,14 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     auto load_xd = [&](int s, float (&xo)[TC], float (&dto)[TC], float (&zo)[ZC]) {
 #pragma unroll
         for (int k = 0; k < TC; ++k) {
-            const int t = s * SC + w * TC + k;   // rows past L read as 0 (or, FULL, the last row)
-            xo[k] = ld_row(rx, vx, t, rowx, L - 1);
-            dto[k] = ld_row(rdt, vx, t, rowx, L - 1);
+            const int t = s * SC + w * TC + k;   // rows past L read as 0
+            xo[k] = ld_row(rx, vx, t, rowx);
+            dto[k] = ld_row(rdt, vx, t, rowx);
             // z is 0 when null; with paired gating, step 2i + ns of this half.
             if constexpr (PAIRG) {
-                if (k % 2 == 0) zo[k / 2] = ld_row(rz, vx + ns * rowx, t, rowx, L - 2);
+                if (k % 2 == 0) zo[k / 2] = ld_row(rz, vx + ns * rowx, t, rowx);
             } else if constexpr (GATE) {
-                zo[k] = ld_row(rz, vx, t, rowx, L - 1);
+                zo[k] = ld_row(rz, vx, t, rowx);
             }
         }
     };
@@ -318,7 +301,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
         } else {
             const int t = s * SC + w * TC + k;
 #pragma unroll
-            for (int j = 0; j < NPL; ++j) out[j] = ld_row(r, vbc + j * NS * TS, t, rowbc, L - 1);
+            for (int j = 0; j < NPL; ++j) out[j] = ld_row(r, vbc + j * NS * TS, t, rowbc);
         }
     };
 
@@ -594,22 +577,17 @@ static int launch_chunked(const Scan1DFwdArgs &a, bool shared, bool hist, hipStr
     }
     dim3 g(static_cast<unsigned>(grid)), blk(64 * W);
     const bool gate = a.z || a.Dskip;
-    // Whole super-chunks only: row offsets in SGPRs (history launches keep
-    // the range-checked form).
-    const bool full = !hist && a.L % (W * TC) == 0;
     // B*u is kept in registers only without history stores or gating, whose
     // extra registers would otherwise spill.
-#define KM_CH(SH, HI, GA, FU) \
-    hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, W, TC, SH, HI, SBU && !HI && !GA, OCC, GA, false, FU>), \
+#define KM_CH(SH, HI, GA) \
+    hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, W, TC, SH, HI, SBU && !HI && !GA, OCC, GA>), \
                        g, blk, 0, s, a)
     if (shared) {
-        if (hist) { if (gate) KM_CH(true, true, true, false); else KM_CH(true, true, false, false); }
-        else if (full) { if (gate) KM_CH(true, false, true, true); else KM_CH(true, false, false, true); }
-        else      { if (gate) KM_CH(true, false, true, false); else KM_CH(true, false, false, false); }
+        if (hist) { if (gate) KM_CH(true, true, true); else KM_CH(true, true, false); }
+        else      { if (gate) KM_CH(true, false, true); else KM_CH(true, false, false); }
     } else {
-        if (hist) { if (gate) KM_CH(false, true, true, false); else KM_CH(false, true, false, false); }
-        else if (full) { if (gate) KM_CH(false, false, true, true); else KM_CH(false, false, false, true); }
-        else      { if (gate) KM_CH(false, false, true, false); else KM_CH(false, false, false, false); }
+        if (hist) { if (gate) KM_CH(false, true, true); else KM_CH(false, true, false); }
+        else      { if (gate) KM_CH(false, false, true); else KM_CH(false, false, false); }
     }
 #undef KM_CH
     KM_HIP_TRY(hipGetLastError());
@@ -778,10 +756,8 @@ static int launch_segmented(const KMScan1DFwd *k, long Ls, hipStream_t s) {
     Scan1DFwdArgs a{k->x, k->delta, k->A, k->Bm, k->Cm, nullptr, nullptr, hl, nullptr, nullptr, 1,
                     nullptr, nullptr, BS, Ls, k->D, k->N, Ls * k->bc_st, k->bc_st, k->bc_sd, 0,
                     nullptr, S, dsum};
-    // Segment lengths are multiples of the 64-step super-chunk: whole
-    // super-chunks (SGPR row offsets) except with history stores.
 #define KM_SEG(SH, HI, GA, BU) \
-    hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, WS, 8, SH, HI, BU, 2, GA, true, !HI>), dim3(grid), dim3(64 * WS), 0, s, a)
+    hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, WS, 8, SH, HI, BU, 2, GA, true>), dim3(grid), dim3(64 * WS), 0, s, a)
     if (shared) KM_SEG(true, false, false, true); else KM_SEG(false, false, false, true);
     KM_HIP_TRY(hipGetLastError());
     // (2) incoming state of every segment, the final state, flags cleared
@@ -795,7 +771,7 @@ static int launch_segmented(const KMScan1DFwd *k, long Ls, hipStream_t s) {
                     k->z, k->Dskip, BS, Ls, k->D, k->N, Ls * k->bc_st, k->bc_st, k->bc_sd, k->clamp,
                     k->clamp ? flags : nullptr, S};
 #define KM_SEGR(SH, HI, GA) \
-    hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, WS, 8, SH, HI, !HI && !GA, 2, GA, false, !HI>), dim3(grid), dim3(64 * WS), 0, s, r)
+    hipLaunchKernelGGL((scan1d_fwd_chunked<T, NPL, NS, WS, 8, SH, HI, !HI && !GA, 2, GA>), dim3(grid), dim3(64 * WS), 0, s, r)
     if (shared) {
         if (hist) { if (gate) KM_SEGR(true, true, true); else KM_SEGR(true, true, false); }
         else      { if (gate) KM_SEGR(true, false, true); else KM_SEGR(true, false, false); }
