@@ -105,14 +105,20 @@ __device__ __forceinline__ float reduce_scatter(const float (&v)[NV], int lane) 
     return cur[0];
 }
 
-// Decays e1^(n0 + 1 + j), j < NPL, of a lane's states when A[d, n] =
-// (n + 1) A[d, 0]: e1 = 2^(s*A0p) and the lane's first power from its own
-// exponent 2^(s*A0p*(n0 + 1)) (one more exp instead of a squaring ladder with
-// selects), then one multiply per state.
 template <int NPL, int NS>
-__device__ __forceinline__ void pow_chain_b(float s, float A0p, float A0n, float (&e)[NPL]) {
-    const float e1 = exp2_fast(s * A0p);
-    e[0] = NS > 1 ? exp2_fast(s * A0n) : e1;
+__device__ __forceinline__ void pow_chain_b(float e1, int n0, float (&e)[NPL]) {
+    float pw = e1;
+    if constexpr (NS > 1) {
+        float sq = e1;
+#pragma unroll
+        for (int k = 1; k < NPL; k <<= 1) sq *= sq;
+#pragma unroll
+        for (int bit = NPL; bit < NPL * NS; bit <<= 1) {
+            pw *= (n0 & bit) ? sq : 1.0f;
+            sq *= sq;
+        }
+    }
+    e[0] = pw;
 #pragma unroll
     for (int j = 1; j < NPL; ++j) e[j] = e[j - 1] * e1;
 }
@@ -199,8 +205,12 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
         Ap[j] = Ar[j] * kLog2e;
     }
     const float A0p = p.A[dc * N] * kLog2e;
-    const float A0n = A0p * static_cast<float>(n0 + 1);   // exponent of the lane's first state
-    bool structured = true;
+    // The squaring ladder of pow_chain_b covers any n0; it is used where n0
+    // is 0 or a power of two (N <= 8 with the 4-state lanes). For N = 16 the
+    // lane with n0 = 12 keeps the workgroup on one exp per state, which
+    // measured faster on gfx950 than this chain or one with a second exp
+    // for the lane's first power.
+    bool structured = (n0 == 0 || (n0 & (n0 - 1)) == 0);
 #pragma unroll
     for (int j = 0; j < NPL; ++j)
         structured = structured && (Ar[j] == static_cast<float>(n0 + j + 1) * p.A[dc * N]);
@@ -320,7 +330,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
         for (int k = 0; k < TC; ++k) {
             dsum = (k == 0) ? ds[0] : dsum + ds[k];
             if constexpr (FAST) {
-                pow_chain_b<NPL, NS>(ds[k], A0p, A0n, e[k]);
+                pow_chain_b<NPL, NS>(exp2_fast(ds[k] * A0p), n0, e[k]);
             } else {
 #pragma unroll
                 for (int j = 0; j < NPL; ++j) e[k][j] = exp2_fast(ds[k] * Ap[j]);
@@ -328,7 +338,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
         }
         float P[NPL];
         if constexpr (FAST) {
-            pow_chain_b<NPL, NS>(dsum, A0p, A0n, P);
+            pow_chain_b<NPL, NS>(exp2_fast(dsum * A0p), n0, P);
         } else {
 #pragma unroll
             for (int j = 0; j < NPL; ++j) P[j] = exp2_fast(Ap[j] * dsum);
