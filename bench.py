@@ -451,6 +451,27 @@ def cpu_baseline_scan2d(nthreads, dims=(256, 256), D=256, M=16, dsample=16, budg
     return runs * P * dsample / secs, secs
 
 
+def cpu_baseline_convnd(nthreads, dims=(512, 512), D=64, K=3, budget_s=3.0):
+    """The oracle's ConvND forward (src/convnd.c:58-126: the K^N stencil per
+    point and channel, OpenMP over points as src/convnd.c:88) on configs[3]'s
+    512x512 D=64 K=3 case, repeated until the time budget is used. Returns
+    (output elems/s, seconds)."""
+    import numpy as np
+    import oracle as O
+    g = np.random.default_rng(5)
+    P = int(np.prod(dims))
+    inp = g.standard_normal((P, D)).astype(np.float32)
+    ker = (g.standard_normal((K ** len(dims), D)) / K).astype(np.float32)
+    bias = (g.standard_normal(D) * 0.1).astype(np.float32)
+    secs, runs = 0.0, 0
+    while secs < budget_s:
+        t = time.perf_counter()
+        O.convnd_forward(dims, inp, ker, bias, nthreads=nthreads, fast=True)
+        secs += time.perf_counter() - t
+        runs += 1
+    return runs * P * D / secs, secs
+
+
 def cpu_baselines(x, dt, A, Bm, Cm):
     """The CPU legs (the oracle's optimised build; a reported baseline, not
     the target), timed on this host before the GPU work."""
@@ -459,6 +480,8 @@ def cpu_baselines(x, dt, A, Bm, Cm):
     rn, nbn, sn = cpu_baseline_scan1d(x, dt, A, Bm, Cm, nthreads=nt)
     r2, s2 = cpu_baseline_scan2d(1)
     r2n, s2n = cpu_baseline_scan2d(nt)
+    r3, s3 = cpu_baseline_convnd(1)
+    r3n, s3n = cpu_baseline_convnd(nt)
     Bsz, L, D = x.shape
     return {"value": r1, "unit": "elems/s", "cores": 1, "kind": "port",
             "sample": f"{nb1} batch elements (of {Bsz}, cycled) of the headline workload (L={L}, D={D}, "
@@ -471,6 +494,11 @@ def cpu_baselines(x, dt, A, Bm, Cm):
                                "sample": f"scannd_ref restatement, 16 of 256 channels (independent), "
                                          f"N=16; {s2:.1f} s on one thread, {s2n:.1f} s on {nt} "
                                          f"(OpenMP per wavefront level)"},
+            "convnd_512x512": {"value": r3, "unit": "elems/s", "cores": 1,
+                               "all_cores_value": r3n, "all_cores": nt,
+                               "sample": f"ConvND forward restatement (src/convnd.c), 512x512 D=64 "
+                                         f"K=3, whole grid; {s3:.1f} s on one thread, {s3n:.1f} s "
+                                         f"on {nt} (OpenMP over points)"},
             "host": host_info()}
 
 
