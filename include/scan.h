@@ -100,6 +100,16 @@ typedef struct {
  * include/scan.h:102). */
 void scan1d_backward_m1_shared_bc(ScanBackwardSharedParams *p);
 
+/* Replace scan1d_backward_m1_shared_bc_asm and _simple_asm (include/scan.h:
+ * 103-104; cpu/scan1d_backward_m1_shared_bc.asm and _simple.asm, which the
+ * reference's build does not assemble). The same recurrence; without
+ * A_diag the decay is those routines' Taylor polynomial
+ * 1 + x + x^2/2 + x^3/6 of x = delta*A (not expf). L = 0 clears dA, dB, dC;
+ * D = 0 clears ddelta. A missing buffer or a negative size sets
+ * km_last_error() and writes nothing (the routines would fault). */
+void scan1d_backward_m1_shared_bc_asm(ScanBackwardSharedParams *p);
+void scan1d_backward_m1_shared_bc_simple_asm(ScanBackwardSharedParams *p);
+
 /* Selective scan 2D over a d1 x d2 grid, anti-diagonal dependency order:
  *   h(i,j) = exp(dt1*A1) h(i-1,j) + exp(dt2*A2) h(i,j-1) + B*((dt1+dt2)/2)*x
  *   y(i,j) = sum_m C h(i,j)

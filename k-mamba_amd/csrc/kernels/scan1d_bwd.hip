@@ -892,7 +892,23 @@ struct M1Args {
     float *dx, *dA, *dB, *dC, *ddelta;
     long L, D;
     float *part;   // [gridDim.x, L] per-workgroup ddelta partials
+    int taylor;    // decay without Adiag: 0 exp, 1 / 2 the AVX2 / scalar asm polynomial
 };
+
+// Decay of the reference's assembly M = 1 backward routines when A_diag is
+// NULL: 1 + x + x^2/2 + x^3/6 of x = delta*A in their instruction order
+// (cpu/scan1d_backward_m1_shared_bc.asm:220-231: x^3/6 = (x^3 * 0.5) *
+// 0.33333334; _simple.asm:212-225: x^3 * 0.16666667), every operation
+// rounded on its own.
+__device__ __forceinline__ float m1_asm_taylor(float x, bool scalar_form) {
+#pragma clang fp contract(off)
+    const float x2 = x * x;
+    float acc = x + x2 * 0.5f;
+    float x3 = x2 * x;
+    x3 = scalar_form ? x3 * 0.16666667f : (x3 * 0.5f) * 0.33333334f;
+    acc = acc + x3;
+    return acc + 1.0f;
+}
 
 // M = 1 with B, C shared over time ([D]) and delta shared over channels
 // ([L]) (reference cpu/scan1d_backward.c:23-70): one thread per channel in
@@ -911,7 +927,9 @@ __global__ void __launch_bounds__(256) scan1d_bwd_m1_shared(M1Args p) {
         const long td = t * p.D + dc;
         const float dt = p.delta[t];
         const float xt = p.x[td], gy = p.dy[td];
-        const float e = p.Adiag ? p.Adiag[td] : exp2_fast(dt * a * kLog2e);
+        const float e = p.Adiag ? p.Adiag[td]
+                        : p.taylor ? m1_asm_taylor(dt * a, p.taylor == 2)
+                                   : exp2_fast(dt * a * kLog2e);
         const float hp = (t > 0) ? p.h[td - p.D] : (p.h0 ? p.h0[dc] : 0.f);
         const float ah = adj + gy * c;
         dCl += gy * p.h[td];
@@ -1091,20 +1109,16 @@ void scan1d_backward(ScanBackwardParams *p) {
 
 void mamba_scan1d_backward(MambaScan1DBackwardParams *p) { scan1d_backward(p); }
 
-// Reference scan1d_backward_m1_shared_bc (cpu/scan1d_backward.c:17-191):
-// M = 1; B, C, dA, dB, dC [D]; delta, ddelta [L]; x, h, dy, dx [L, D];
-// A_diag [L, D] precomputed decays or NULL; h0 [D] or NULL.
-void scan1d_backward_m1_shared_bc(ScanBackwardSharedParams *p) {
-    km::clear_error();
-    if (!p || !p->x || !p->A || !p->B || !p->C || !p->delta || !p->h || !p->dy || !p->dx ||
-        !p->dA || !p->dB || !p->dC || !p->ddelta || p->L <= 0 || p->D <= 0) {
-        km::set_error("scan1d_backward_m1_shared_bc: invalid parameters");
-        return;
-    }
-    if (!km::gpu_ready()) return;
+}  // extern "C"
+
+namespace km {
+
+// One host-or-device call of the M = 1 backward (L, D > 0, parameters
+// checked by the caller) with the decay form `taylor` (M1Args::taylor).
+static void m1_host_call(ScanBackwardSharedParams *p, int taylor, const char *who) {
     const size_t LD = p->L * p->D * 4, D4 = p->D * 4, L4 = p->L * 4;
-    km::Staging::lock();
-    km::StagedCall sc;
+    Staging::lock();
+    StagedCall sc;
     sc.add(p->x, LD, false);       // 0
     sc.add(p->A, D4, false);       // 1
     sc.add(p->A_diag, LD, false);  // 2
@@ -1119,14 +1133,90 @@ void scan1d_backward_m1_shared_bc(ScanBackwardSharedParams *p) {
     sc.add(p->dB, D4, true);       // 11
     sc.add(p->dC, D4, true);       // 12
     sc.add(p->ddelta, L4, true);   // 13
-    if (sc.stage_in("scan1d_backward_m1_shared_bc")) {
-        km::M1Args a{sc.dev<float>(0), sc.dev<float>(1), sc.dev<float>(2), sc.dev<float>(3),
-                     sc.dev<float>(4), sc.dev<float>(5), sc.dev<float>(6), sc.dev<float>(7),
-                     sc.dev<float>(8), sc.dev<float>(9), sc.dev<float>(10), sc.dev<float>(11),
-                     sc.dev<float>(12), sc.dev<float>(13), p->L, p->D, nullptr};
-        if (km::m1_launch(a, nullptr) == 0) sc.stage_out("scan1d_backward_m1_shared_bc");
+    if (sc.stage_in(who)) {
+        M1Args a{sc.dev<float>(0), sc.dev<float>(1), sc.dev<float>(2), sc.dev<float>(3),
+                 sc.dev<float>(4), sc.dev<float>(5), sc.dev<float>(6), sc.dev<float>(7),
+                 sc.dev<float>(8), sc.dev<float>(9), sc.dev<float>(10), sc.dev<float>(11),
+                 sc.dev<float>(12), sc.dev<float>(13), p->L, p->D, nullptr, taylor};
+        if (m1_launch(a, nullptr) == 0) sc.stage_out(who);
     }
-    km::Staging::unlock();
+    Staging::unlock();
+}
+
+// The reference's assembly routines (scan1d_backward_m1_shared_bc_asm and
+// _simple_asm) check only p; with L or D zero they still clear the
+// outputs of the other size (dA, dB, dC when L = 0; ddelta when D = 0).
+// Here every output they write must be present, and a missing buffer or a
+// negative size is an error instead of a fault.
+static void m1_asm_call(ScanBackwardSharedParams *p, int taylor, const char *who) {
+    clear_error();
+    if (!p || p->L < 0 || p->D < 0) {
+        set_error("%s: invalid parameters", who);
+        return;
+    }
+    const bool work = p->L > 0 && p->D > 0;
+    if ((work && (!p->x || !p->A || !p->B || !p->C || !p->delta || !p->h || !p->dy || !p->dx)) ||
+        (p->D > 0 && (!p->dA || !p->dB || !p->dC)) || (p->L > 0 && !p->ddelta)) {
+        set_error("%s: invalid parameters", who);
+        return;
+    }
+    if (p->L == 0 && p->D == 0) return;
+    if (!gpu_ready()) return;
+    if (work) {
+        m1_host_call(p, taylor, who);
+        return;
+    }
+    // One size is zero: the outputs of the other are cleared on the device.
+    Staging::lock();
+    StagedCall sc;
+    const size_t D4 = p->D * 4, L4 = p->L * 4;
+    if (p->D > 0) {
+        sc.add(p->dA, D4, true);
+        sc.add(p->dB, D4, true);
+        sc.add(p->dC, D4, true);
+    } else {
+        sc.add(p->ddelta, L4, true);
+    }
+    if (sc.stage_in(who)) {
+        bool ok = true;
+        for (int i = 0; i < sc.n && ok; ++i)
+            ok = hipMemsetAsync(sc.bufs[i].dev, 0, sc.bufs[i].bytes, nullptr) == hipSuccess;
+        if (!ok) set_error("%s: %s", who, hipGetErrorString(hipGetLastError()));
+        else sc.stage_out(who);
+    }
+    Staging::unlock();
+}
+
+}  // namespace km
+
+extern "C" {
+
+// Reference scan1d_backward_m1_shared_bc (cpu/scan1d_backward.c:17-191):
+// M = 1; B, C, dA, dB, dC [D]; delta, ddelta [L]; x, h, dy, dx [L, D];
+// A_diag [L, D] precomputed decays or NULL; h0 [D] or NULL.
+void scan1d_backward_m1_shared_bc(ScanBackwardSharedParams *p) {
+    km::clear_error();
+    if (!p || !p->x || !p->A || !p->B || !p->C || !p->delta || !p->h || !p->dy || !p->dx ||
+        !p->dA || !p->dB || !p->dC || !p->ddelta || p->L <= 0 || p->D <= 0) {
+        km::set_error("scan1d_backward_m1_shared_bc: invalid parameters");
+        return;
+    }
+    if (!km::gpu_ready()) return;
+    km::m1_host_call(p, 0, "scan1d_backward_m1_shared_bc");
+}
+
+// Reference scan1d_backward_m1_shared_bc_asm (include/scan.h:103,
+// cpu/scan1d_backward_m1_shared_bc.asm): the same recurrence; without
+// A_diag the decay is the routine's third-order Taylor polynomial.
+void scan1d_backward_m1_shared_bc_asm(ScanBackwardSharedParams *p) {
+    km::m1_asm_call(p, 1, "scan1d_backward_m1_shared_bc_asm");
+}
+
+// Reference scan1d_backward_m1_shared_bc_simple_asm (include/scan.h:104,
+// cpu/scan1d_backward_m1_shared_bc_simple.asm): as above, the scalar
+// routine's polynomial constants.
+void scan1d_backward_m1_shared_bc_simple_asm(ScanBackwardSharedParams *p) {
+    km::m1_asm_call(p, 2, "scan1d_backward_m1_shared_bc_simple_asm");
 }
 
 void mamba_scan1d_backward_m1_shared_bc(MambaScan1DBackwardM1Params *p) {

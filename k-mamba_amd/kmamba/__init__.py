@@ -222,6 +222,10 @@ scan1d_backward_m1_shared_bc = _decl("scan1d_backward_m1_shared_bc", None,
                                      [C.POINTER(ScanBackwardSharedParams)])
 mamba_scan1d_backward_m1_shared_bc = _decl("mamba_scan1d_backward_m1_shared_bc", None,
                                            [C.POINTER(ScanBackwardSharedParams)])
+scan1d_backward_m1_shared_bc_asm = _decl("scan1d_backward_m1_shared_bc_asm", None,
+                                         [C.POINTER(ScanBackwardSharedParams)])
+scan1d_backward_m1_shared_bc_simple_asm = _decl("scan1d_backward_m1_shared_bc_simple_asm", None,
+                                                [C.POINTER(ScanBackwardSharedParams)])
 om_scan1d_backward = _decl("om_scan1d_backward", None, [C.c_void_p] * 12 + [C.c_int] * 3)
 mamba_scan1d_cuda_backward = _decl("mamba_scan1d_cuda_backward", None,
                                    [C.c_void_p] * 12 + [C.c_int] * 3)

@@ -221,6 +221,77 @@ void orc_scan1d_backward_m1_shared_bc(OrcScanBackwardSharedParams *p) {
     free(adj);
 }
 
+/* The decay of the M=1 assembly routines when A_diag is NULL: the
+ * third-order Taylor polynomial 1 + x + x^2/2 + x^3/6 of exp(x), x =
+ * delta*A, in their instruction order (cpu/scan1d_backward_m1_shared_bc.asm:
+ * 220-231 with x^3/6 = (x^3 * 0.5) * 0.33333334; _simple.asm:212-225 with
+ * x^3 * 0.16666667). It is not expf: at x = -1 it gives 1/3, not e^-1. */
+float orc_m1_asm_taylor(float x, int simple) {
+    float x2 = x * x;
+    float acc = x + x2 * 0.5f;
+    float x3 = x2 * x;
+    x3 = simple ? x3 * 0.16666667f : (x3 * 0.5f) * 0.33333334f;
+    acc = acc + x3;
+    return acc + 1.0f;
+}
+
+/* Restatement of scan1d_backward_m1_shared_bc_asm
+ * (cpu/scan1d_backward_m1_shared_bc.asm, simple = 0) and
+ * scan1d_backward_m1_shared_bc_simple_asm (_simple.asm, simple = 1), which
+ * the reference declares (include/scan.h:103-104) but its build never
+ * assembles. Same recurrence as the C function, in the instructions' order:
+ * vfmadd231 as fmaf, every other operation rounded on its own. The AVX2
+ * routine walks channels eight at a time while d + 8 <= D (ddelta terms
+ * accumulated by fma into the lane d mod 8, :178-277) and the rest one at a
+ * time (mul then add into a scalar, :279-377); ddelta[t] is then
+ * ((l0+l4) + (l1+l5)) + ((l2+l6) + (l3+l7)) + tail, added to the zeroed
+ * ddelta[t] (:379-388). The scalar routine adds ah * inner in channel order.
+ * Validation is the routine's own: only p is checked (:63-65, calloc of adj_h :70-76); L = 0 zeroes
+ * dA, dB, dC, and D = 0 zeroes ddelta. */
+void orc_scan1d_backward_m1_shared_bc_asm(OrcScanBackwardSharedParams *p, int simple) {
+    if (!p) return;
+    long L = p->L, D = p->D;
+    float *adj = (float *)calloc((size_t)(D > 0 ? D : 1), sizeof(float));
+    if (!adj) return;
+    memset(p->dx, 0, (size_t)(L * D) * sizeof(float));              /* :78-113 */
+    memset(p->dA, 0, (size_t)D * sizeof(float));
+    memset(p->dB, 0, (size_t)D * sizeof(float));
+    memset(p->dC, 0, (size_t)D * sizeof(float));
+    memset(p->ddelta, 0, (size_t)L * sizeof(float));
+    for (long t = L - 1; t >= 0; t--) {
+        const float dt = p->delta[t];
+        const float *hprev = t > 0 ? p->h + (t - 1) * D : p->h0;   /* NULL: zero state */
+        float lanes[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        float tail = 0.0f;
+        long d = 0;
+        for (int pass = 0; pass < 2; pass++) {
+            long end = (pass == 0) ? (simple ? 0 : (D >= 8 ? D - D % 8 : 0)) : D;
+            for (; d < end; d++) {
+                long td = t * D + d;
+                float xt = p->x[td], gy = p->dy[td];
+                float a = p->A[d], b = p->B[d], c = p->C[d];
+                float e = p->A_diag ? p->A_diag[td] : orc_m1_asm_taylor(dt * a, simple);
+                float hp = hprev ? hprev[d] : 0.0f;
+                float ah = gy * c + adj[d];
+                p->dC[d] = fmaf(gy, p->h[td], p->dC[d]);
+                float ahdt = ah * dt;
+                p->dB[d] = fmaf(ahdt, xt, p->dB[d]);
+                p->dA[d] = fmaf(ahdt * e, hp, p->dA[d]);
+                p->dx[td] = ahdt * b;
+                float inner = fmaf(b, xt, (a * e) * hp);
+                if (pass == 0) lanes[d & 7] = fmaf(ah, inner, lanes[d & 7]);
+                else tail = tail + ah * inner;
+                adj[d] = ah * e;
+            }
+        }
+        float s = simple ? tail
+                         : ((lanes[0] + lanes[4]) + (lanes[1] + lanes[5])) +
+                               ((lanes[2] + lanes[6]) + (lanes[3] + lanes[7])) + tail;
+        p->ddelta[t] = s + p->ddelta[t];
+    }
+    free(adj);
+}
+
 /* Batched backward with strided B/C, the adjoint of orc_scan1d_batched
  * without clamp. Per batch element it is cpu/scan1d_backward.c:248-295 with
  * B, C read through strides and dy, x, delta, h of that element; dx and

@@ -71,6 +71,8 @@ void orc_scan1d_batched(const float *x, const float *delta, const float *A,
                         int clamp, int nthreads);
 void orc_scan1d_backward(OrcScanBackwardParams *p);
 void orc_scan1d_backward_m1_shared_bc(OrcScanBackwardSharedParams *p);
+float orc_m1_asm_taylor(float x, int simple);
+void orc_scan1d_backward_m1_shared_bc_asm(OrcScanBackwardSharedParams *p, int simple);
 void orc_scan1d_batched_backward(const float *x, const float *delta, const float *A,
                                  const float *Bm, const float *Cm, const float *dy,
                                  const float *h0, const float *h_hist,

@@ -102,6 +102,9 @@ for _lib in {orc, orc_fast}:
     _sig(_lib, "orc_scan1d_batched", None, [vp] * 8 + [C.c_long] * 7 + [C.c_int, C.c_int])
     _sig(_lib, "orc_scan1d_backward", None, [C.POINTER(ScanBackwardParams)])
     _sig(_lib, "orc_scan1d_backward_m1_shared_bc", None, [C.POINTER(ScanBackwardSharedParams)])
+    _sig(_lib, "orc_scan1d_backward_m1_shared_bc_asm", None,
+         [C.POINTER(ScanBackwardSharedParams), C.c_int])
+    _sig(_lib, "orc_m1_asm_taylor", C.c_float, [C.c_float, C.c_int])
     _sig(_lib, "orc_scan1d_batched_backward", None, [vp] * 13 + [C.c_long] * 7 + [C.c_int])
     _sig(_lib, "orc_scan2d", None, [C.POINTER(Scan2DParams)])
     _sig(_lib, "orc_scannd_ref", C.c_int, [C.POINTER(ScanNDParams), C.c_int])
@@ -212,6 +215,32 @@ def scan1d_backward(x, A, B, Cm, delta, h, dy, h0=None, lib=None):
     else:
         lib.scan1d_backward(C.byref(p))
     return out["dx"], out["dA"], out["dB"], out["dC"], out["ddelta"]
+
+
+def scan1d_backward_m1_shared_bc_asm(x, A, B, Cm, delta, h, dy, A_diag=None, h0=None,
+                                     simple=False):
+    """Restatement of the reference's scan1d_backward_m1_shared_bc_asm
+    (simple=False) / _simple_asm (simple=True): returns dx, dA, dB, dC,
+    ddelta. x, h, dy [L, D]; A, B, Cm [D]; delta [L]."""
+    x, A, B, Cm, delta, h, dy = map(f32, (x, A, B, Cm, delta, h, dy))
+    L, D = x.shape
+    A_diag = None if A_diag is None else f32(A_diag)
+    h0 = None if h0 is None else f32(h0)
+    out = dict(dx=np.zeros((L, D), np.float32), dA=np.zeros(D, np.float32),
+               dB=np.zeros(D, np.float32), dC=np.zeros(D, np.float32),
+               ddelta=np.zeros(L, np.float32))
+    p = ScanBackwardSharedParams(P(x), P(A), P(A_diag), P(B), P(Cm), P(delta), P(h0), P(h),
+                                 P(dy), P(out["dx"]), P(out["dA"]), P(out["dB"]), P(out["dC"]),
+                                 P(out["ddelta"]), L, D)
+    orc.orc_scan1d_backward_m1_shared_bc_asm(C.byref(p), int(bool(simple)))
+    return out["dx"], out["dA"], out["dB"], out["dC"], out["ddelta"]
+
+
+def m1_asm_taylor(xs, simple=False):
+    """The asm routines' Taylor decay of each fp32 value of xs."""
+    xs = f32(np.asarray(xs))
+    return np.array([orc.orc_m1_asm_taylor(float(v), int(bool(simple))) for v in xs.ravel()],
+                    np.float32).reshape(xs.shape)
 
 
 def scan1d_backward_m1_shared_bc(x, A, B, Cm, delta, h, dy, A_diag=None, h0=None, lib=None):

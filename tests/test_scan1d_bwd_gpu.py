@@ -364,3 +364,89 @@ def test_m1_shared_bc_ddelta_bit_identical_across_runs():
         assert K.km_last_error() == ""
         outs.append(ddt)
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+@pytest.mark.parametrize("kind", ["avx2", "simple"])
+@pytest.mark.parametrize("L,D,with_diag,use_h0,on_device",
+                         [(6, 5, False, False, False), (16, 17, False, True, False),
+                          (70, 300, True, False, True), (33, 1000, False, True, True)])
+def test_m1_asm_entry_points_vs_oracle(kind, L, D, with_diag, use_h0, on_device):
+    # scan1d_backward_m1_shared_bc_asm / _simple_asm: without A_diag the decay
+    # is the routines' Taylor polynomial (checked against the oracle's
+    # restatement of the assembly, which the CPU pins hold), with A_diag the
+    # given decays. Host and device pointers.
+    g = rng_for("m1asm", kind, L, D)
+    x = g.uniform(-1, 1, (L, D)).astype(np.float32)
+    A = g.uniform(-1.5, -0.05, D).astype(np.float32)
+    B = g.uniform(-0.5, 0.5, D).astype(np.float32)
+    Cm = g.uniform(-0.5, 0.5, D).astype(np.float32)
+    dt = g.uniform(0.05, 0.8, L).astype(np.float32)
+    dy = g.standard_normal((L, D)).astype(np.float32)
+    h0 = g.uniform(-1, 1, D).astype(np.float32) if use_h0 else None
+    e = np.exp(dt[:, None].astype(np.float64) * A[None, :])
+    h = np.zeros((L, D))
+    prev = np.zeros(D) if h0 is None else h0.astype(np.float64)
+    for t in range(L):
+        prev = e[t] * prev + B * dt[t] * x[t]
+        h[t] = prev
+    h = h.astype(np.float32)
+    A_diag = np.exp(dt[:, None] * A[None, :]).astype(np.float32) if with_diag else None
+    simple = kind == "simple"
+    ref = O.scan1d_backward_m1_shared_bc_asm(x, A, B, Cm, dt, h, dy, A_diag=A_diag, h0=h0,
+                                             simple=simple)
+    fn = K.scan1d_backward_m1_shared_bc_simple_asm if simple else K.scan1d_backward_m1_shared_bc_asm
+    ins = [x, A, A_diag, B, Cm, dt, h0, h, dy]
+    outs = [np.full((L, D), np.nan, np.float32), np.full(D, np.nan, np.float32),
+            np.full(D, np.nan, np.float32), np.full(D, np.nan, np.float32),
+            np.full(L, np.nan, np.float32)]
+    if on_device:
+        dins = [None if a is None else torch.from_numpy(a).cuda() for a in ins]
+        douts = [torch.from_numpy(a).cuda() for a in outs]
+        p = K.ScanBackwardSharedParams(*(K.ptr(a) for a in dins), *(K.ptr(a) for a in douts), L, D)
+        fn(C.byref(p))
+        got = [a.cpu().numpy() for a in douts]
+    else:
+        p = K.ScanBackwardSharedParams(*(K.ptr(a) for a in ins), *(K.ptr(a) for a in outs), L, D)
+        fn(C.byref(p))
+        got = outs
+    assert K.km_last_error() == ""
+    ab = [np.abs(v) for v in (x, B, Cm, dy)]
+    habs = np.zeros((L, D))
+    prev = np.zeros(D) if h0 is None else np.abs(h0).astype(np.float64)
+    for t in range(L):
+        prev = e[t] * prev + ab[1] * dt[t] * ab[0][t]
+        habs[t] = prev
+    diag_abs = A_diag if with_diag else np.abs(O.m1_asm_taylor(dt[:, None] * A[None, :], simple))
+    kap = O.scan1d_backward_m1_shared_bc_asm(ab[0], A, ab[1], ab[2], dt, habs.astype(np.float32),
+                                             ab[3], A_diag=diag_abs,
+                                             h0=None if h0 is None else np.abs(h0), simple=simple)
+    t2 = (ab[0] * kap[0]).sum(axis=1) / dt
+    kdd = np.maximum(2 * t2 - kap[4], 0)
+    for n, gg, r, k in zip(("dx", "dA", "dB", "dC", "ddelta"), got, ref,
+                           (kap[0], kap[1], kap[2], kap[3], kdd)):
+        assert_close(gg, r, TOL_F32, f"m1 asm {kind} {n}", k)
+
+
+@pytest.mark.parametrize("simple", [False, True])
+def test_m1_asm_entry_points_edge_sizes_and_errors(simple):
+    # L = 0 clears dA, dB, dC; D = 0 clears ddelta (as the routines do); a
+    # missing output is an error that writes nothing.
+    fn = K.scan1d_backward_m1_shared_bc_simple_asm if simple else K.scan1d_backward_m1_shared_bc_asm
+    D, L = 7, 5
+    dA, dB, dC = (np.full(D, 3.0, np.float32) for _ in range(3))
+    p = K.ScanBackwardSharedParams()
+    p.dA, p.dB, p.dC, p.L, p.D = K.ptr(dA), K.ptr(dB), K.ptr(dC), 0, D
+    fn(C.byref(p))
+    assert K.km_last_error() == ""
+    assert not dA.any() and not dB.any() and not dC.any()
+    dd = np.full(L, 3.0, np.float32)
+    q = K.ScanBackwardSharedParams()
+    q.ddelta, q.L, q.D = K.ptr(dd), L, 0
+    fn(C.byref(q))
+    assert K.km_last_error() == ""
+    assert not dd.any()
+    dd[:] = 3.0
+    r = K.ScanBackwardSharedParams()
+    r.L, r.D = L, D
+    fn(C.byref(r))
+    assert "invalid parameters" in K.km_last_error()
