@@ -203,12 +203,8 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_mfma(GemmArgs p) {
     store_wave_tile<EPI, CBF16, 2, 2>(p, acc, m0 + wm * 64, n0 + wn * 64, lds, lane);
 }
 
-// Large shapes: a 256-thread workgroup computes a 256 x 256 tile of C; each
-// of its 4 waves owns a 128 x 128 quarter as 4 x 4 MFMA tiles (256 fp32
-// accumulators per lane, one wave per SIMD). Per 16-wide k step a wave reads
-// 4 A and 4 B fragments (8 KB of LDS) for 16 MFMAs, half the LDS bytes per
-// MFMA of the 64 x 64 wave tile above, so the LDS keeps up with the matrix
-// cores.
+// Large shapes: a 512-thread workgroup computes a 256 x 256 tile of C
+// (gemm_bf16_mfma_pp below), K in stages of 32.
 constexpr int kGM = 256, kGN = 256, kGK = 32;   // rows, columns, k per stage
 
 // Skinny shapes (N <= 128 with a long K, or K <= 64): MFMA operands come
@@ -309,38 +305,47 @@ __global__ void __launch_bounds__(256) gemm_bf16_direct(GemmArgs p) {
     store_wave_tile<EPI, CBF16, 1, TN>(p, acc, m0, n0, stage[KSPLIT > 1 ? 0 : w], lane);
 }
 
-// The 256x256 tile with operands loaded straight into LDS (gfx950
-// buffer_load_dwordx4 ... lds): no staging registers, so stages of 32 k run
-// three ahead through four LDS buffers (separate arrays, which lets the
-// compiler's wait counts track each buffer's loads apart). A stage of A (or
-// B) is 256 rows x 4 chunks of 16 B; load instruction i of wave w fills LDS
-// slots [64 (4w + i), +64), lane l slot 64 (4w + i) + l = row * 4 + pc,
-// holding chunk c = pc ^ ((row >> 2) & 3) of its row: the 16 rows a
-// quarter-wave's fragment read touches land on 16 distinct 16-byte bank
-// slots. Per stage each wave waits for its own loads of the next stage, then
-// one barrier makes every wave's loads visible and frees the buffer read in
-// the previous stage for the next load.
+// The 256x256 tile on eight waves, two per SIMD, in ping-pong: waves w and
+// w + 4 share a SIMD; wave (g, s) = (w / 4, w % 4) owns rows [128 g, +128)
+// and columns [64 s, +64) of the tile (4 x 2 MFMA tiles, 128 accumulators).
+// Each stage of 32 k is two phases per wave: a memory phase (its 12 fragment
+// reads of the stage from LDS, its 4 of the 32 direct-to-LDS loads of the
+// stage three ahead, then waits for both) and a compute phase (16 MFMAs on
+// the fragments in registers). Group 1 runs one phase behind group 0, every
+// phase ends at a workgroup barrier, so on each SIMD one wave computes while
+// the other moves data and the matrix core is fed from alternate waves
+// (one wave per SIMD issuing both measured 6-9 % slower on the block's
+// projection shapes). Operands go straight from HBM into LDS (gfx950
+// buffer_load_dwordx4 ... lds, no staging registers) through four stage
+// buffers per operand (separate arrays, so the compiler's wait counts track
+// each apart): a stage of A (or B) is 256 rows x 4 chunks of 16 B, LDS slot
+// row * 4 + pc holding chunk pc ^ ((row >> 2) & 3) of its row, so the 16
+// rows a quarter-wave's fragment read touches land on 16 distinct 16-byte
+// bank slots. Buffer reuse: the loads of stage k + 3, issued in a memory
+// phase of stage k, overwrite stage k - 1's buffer, which both groups
+// finished reading (waited) before the phase barriers that precede it.
 template <int EPI, bool CBF16>
-__global__ void __launch_bounds__(256, 1) gemm_bf16_mfma_256d(GemmArgs p) {
+__global__ void __launch_bounds__(512, 1) gemm_bf16_mfma_pp(GemmArgs p) {
     __shared__ u32x4 sA0[kGM * 4], sA1[kGM * 4], sA2[kGM * 4], sA3[kGM * 4];
     __shared__ u32x4 sB0[kGN * 4], sB1[kGN * 4], sB2[kGN * 4], sB3[kGN * 4];
     constexpr unsigned kDrop = 0x80000000u;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = w >> 1, wn = w & 1;
+    const int g = w >> 2, sg = w & 3;
     long mb, nb;
-    xcd_tile(mb, nb);                  // tiles of one row block share an XCD's L2
+    xcd_tile(mb, nb);
     const long m0 = mb * kGM;
     const long n0 = nb * kGN;
     const long arows = std::min<long>(kGM, p.M - m0), brows = std::min<long>(kGN, p.N - n0);
     const auto rA = make_rsrc(p.A + m0 * p.lda, (arows - 1) * p.lda * 2 + p.K * 2);
     const auto rB = make_rsrc(p.B + n0 * p.ldb, (brows - 1) * p.ldb * 2 + p.K * 2);
-    // Row and chunk of this lane in each of its 4 load instructions.
-    int arow_off[4], brow_off[4], chk[4];
+    // Load instruction i (0, 1) of wave w fills LDS slots [64 (2w + i), +64):
+    // slot = row * 4 + pc holds chunk pc ^ ((row >> 2) & 3) of its row.
+    int arow_off[2], brow_off[2], chk[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int slot = (w * 4 + i) * 64 + lane;
+    for (int i = 0; i < 2; ++i) {
+        const int slot = (w * 2 + i) * 64 + lane;
         const int row = slot >> 2, pc = slot & 3;
         chk[i] = pc ^ ((row >> 2) & 3);
         arow_off[i] = static_cast<int>(row * p.lda * 2);
@@ -349,88 +354,92 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_mfma_256d(GemmArgs p) {
     using lds_t = __attribute__((address_space(3))) void *;
     auto dma = [&](long kt, u32x4 *dA, u32x4 *dB) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 2; ++i) {
             const long k = kt * kGK + chk[i] * 8;
             const bool kin = k < p.K;
             const unsigned oa = kin ? static_cast<unsigned>(arow_off[i] + k * 2) : kDrop;
             const unsigned ob = kin ? static_cast<unsigned>(brow_off[i] + k * 2) : kDrop;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_t)(dA + (w * 4 + i) * 64), 16, oa, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_t)(dB + (w * 4 + i) * 64), 16, ob, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_t)(dA + (w * 2 + i) * 64), 16, oa, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_t)(dB + (w * 2 + i) * 64), 16, ob, 0, 0, 0);
         }
     };
-    f32x16 acc[4][4];
+    f32x16 acc[4][2];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
     const int fr = lane & 31, fk = lane >> 5;
-    auto frag = [&](const u32x4 *bA, const u32x4 *bB, int kk, bf16x8 (&af)[4], bf16x8 (&bfr)[4])
+    bf16x8 fa[2][4], fb[2][2];          // [k half][tile]
+    auto mem = [&](long kt, const u32x4 *bA, const u32x4 *bB, u32x4 *nA, u32x4 *nB)
         __attribute__((always_inline)) {
-        const int c = kk * 2 + fk;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int ra = wm * 128 + i * 32 + fr, rb = wn * 128 + i * 32 + fr;
-            af[i] = __builtin_bit_cast(bf16x8, bA[ra * 4 + (c ^ ((ra >> 2) & 3))]);
-            bfr[i] = __builtin_bit_cast(bf16x8, bB[rb * 4 + (c ^ ((rb >> 2) & 3))]);
+        for (int kk = 0; kk < 2; ++kk) {
+            const int c = kk * 2 + fk;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int ra = g * 128 + i * 32 + fr;
+                fa[kk][i] = __builtin_bit_cast(bf16x8, bA[ra * 4 + (c ^ ((ra >> 2) & 3))]);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int rb = sg * 64 + j * 32 + fr;
+                fb[kk][j] = __builtin_bit_cast(bf16x8, bB[rb * 4 + (c ^ ((rb >> 2) & 3))]);
+            }
         }
-    };
-    // Stage kt from (bA, bB) while its loads of stage kt + 3 go to (nA, nB).
-    // Its barrier covers stage kt + 1's loads, so the first fragments of
-    // stage kt + 1 (xA, xB) are read while stage kt's MFMAs run; (ra0, rb0)
-    // carry them across. Loads run two to three stages ahead.
-    bf16x8 ra0[4], rb0[4];
-    auto stage_ra = [&](long kt, const u32x4 *bA, const u32x4 *bB, const u32x4 *xA, const u32x4 *xB,
-                        u32x4 *nA, u32x4 *nB) __attribute__((always_inline)) {
-        __builtin_amdgcn_s_waitcnt(0x0F78);              // vmcnt(8): this wave's loads of stage kt + 1 done
-        __builtin_amdgcn_s_barrier();                    // ... and every wave's
+        dma(kt + 3, nA, nB);
+        __builtin_amdgcn_s_waitcnt(0x0F78);              // vmcnt(8): own loads of stage kt + 1 done
+        __builtin_amdgcn_s_waitcnt(0xC07F);              // lgkmcnt(0): own fragment reads done
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         __builtin_amdgcn_sched_barrier(0);
-        dma(kt + 3, nA, nB);
-        bf16x8 a1[4], b1[4];
-        frag(bA, bB, 1, a1, b1);
+    };
+    auto comp = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ra0[i], rb0[j], acc[i][j], 0, 0, 0);
-        frag(xA, xB, 0, ra0, rb0);
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[i], b1[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk][i], fb[kk][j], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
     };
     const long nk = (p.K + kGK - 1) / kGK;
     dma(0, sA0, sB0);
     dma(1, sA1, sB1);
     dma(2, sA2, sB2);
-    // Groups of four stages with no branch inside (a branch would make the
-    // compiler's wait-count merge wait for every load in flight): stages past
-    // K load zeros and add nothing.
-    __builtin_amdgcn_s_waitcnt(0x4F70);                  // vmcnt(16): stage 0 loaded
+    __builtin_amdgcn_s_waitcnt(0x0F78);                  // vmcnt(8): stage 0 loaded
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    frag(sA0, sB0, 0, ra0, rb0);
+    if (g == 1) __builtin_amdgcn_s_barrier();            // group 1 runs one phase behind
+    __builtin_amdgcn_sched_barrier(0);
     for (long kt = 0; kt < nk; kt += 4) {
-        stage_ra(kt, sA0, sB0, sA1, sB1, sA3, sB3);
-        stage_ra(kt + 1, sA1, sB1, sA2, sB2, sA0, sB0);
-        stage_ra(kt + 2, sA2, sB2, sA3, sB3, sA1, sB1);
-        stage_ra(kt + 3, sA3, sB3, sA0, sB0, sA2, sB2);
+        mem(kt, sA0, sB0, sA3, sB3);
+        comp();
+        mem(kt + 1, sA1, sB1, sA0, sB0);
+        comp();
+        mem(kt + 2, sA2, sB2, sA1, sB1);
+        comp();
+        mem(kt + 3, sA3, sB3, sA2, sB2);
+        comp();
     }
+    if (g == 0) __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    char *lds = reinterpret_cast<char *>(w == 0 ? sA0 : w == 1 ? sA1 : w == 2 ? sA2 : sA3);
-    store_wave_tile<EPI, CBF16, 4, 4>(p, acc, m0 + wm * 128, n0 + wn * 128, lds, lane);
+    char *lds = reinterpret_cast<char *>(w == 0 ? sA0 : w == 1 ? sA1 : w == 2 ? sA2 : w == 3 ? sA3
+                                         : w == 4 ? sB0 : w == 5 ? sB1 : w == 6 ? sB2 : sB3);
+    store_wave_tile<EPI, CBF16, 4, 2>(p, acc, m0 + g * 128, n0 + sg * 64, lds, lane);
 }
 
 template <int EPI>
 static void gemm_go(const GemmArgs &a, dim3 g, bool big, hipStream_t s) {
     if (big) {
-        if (a.c_bf16) hipLaunchKernelGGL((gemm_bf16_mfma_256d<EPI, true>), g, dim3(256), 0, s, a);
-        else          hipLaunchKernelGGL((gemm_bf16_mfma_256d<EPI, false>), g, dim3(256), 0, s, a);
+        if (a.c_bf16) hipLaunchKernelGGL((gemm_bf16_mfma_pp<EPI, true>), g, dim3(512), 0, s, a);
+        else          hipLaunchKernelGGL((gemm_bf16_mfma_pp<EPI, false>), g, dim3(512), 0, s, a);
     } else {
         if (a.c_bf16) hipLaunchKernelGGL((gemm_bf16_mfma<EPI, true>), g, dim3(256), 0, s, a);
         else          hipLaunchKernelGGL((gemm_bf16_mfma<EPI, false>), g, dim3(256), 0, s, a);
