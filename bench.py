@@ -177,6 +177,61 @@ def bench_mamba1_block(torch, K, stream, steps, warmup, Bsz=8, L=2048, dim=1024,
                        "dt_rank": R}}
 
 
+def bench_scan1d_gated(torch, K, stream, steps, warmup, Bsz=8, L=2048, D=2048, N=16, R=64):
+    """The block's gated Scan1D on its own (configs[4] shapes: bf16 x, delta,
+    z [B, L, D], B/C read through the x_proj output's strides, Dskip), the
+    same launch ungated, and each launch timed alone (two HIP events around
+    it) after two in_proj-sized GEMMs, or after a 512 MB device copy that
+    empties the last-level cache."""
+    import ctypes as C
+    g = torch.Generator(device="cuda").manual_seed(17)
+    bf = torch.bfloat16
+    x = torch.randn((Bsz, L, D), device="cuda", generator=g).to(bf)
+    dt = torch.nn.functional.softplus(0.5 * torch.randn((Bsz, L, D), device="cuda", generator=g)
+                                      - 2.0).to(bf)
+    A = -torch.arange(1, N + 1, device="cuda", dtype=torch.float32).repeat(D, 1).contiguous()
+    NX = R + 2 * N
+    xd = (torch.randn((Bsz, L, NX), device="cuda", generator=g) * 0.3).to(bf).view(-1)
+    Bm, Cm = xd.narrow(0, R, xd.numel() - R - N), xd.narrow(0, R + N, xd.numel() - R - N)
+    z = torch.randn((Bsz, L, D), device="cuda", generator=g).to(bf)
+    Ds = torch.ones(D, device="cuda")
+    y = torch.empty_like(x)
+    h = C.c_void_p(K.stream_handle(stream))
+    gated = K.scan1d_fwd_args(x, dt, A, Bm, Cm, y, bc_strides=(L * NX, NX, 0), z=z, Dskip=Ds)
+    plain = K.scan1d_fwd_args(x, dt, A, Bm, Cm, y, bc_strides=(L * NX, NX, 0))
+    run = lambda a: K.check(K.km_scan1d_fwd_c(C.byref(a), h), "km_scan1d_fwd")  # noqa: E731
+    _, wg = time_launches(torch, stream, lambda: run(gated), steps, warmup)
+    _, wp = time_launches(torch, stream, lambda: run(plain), steps, warmup)
+    T = Bsz * L
+    a = torch.randn((T, 1024), device="cuda", generator=g).to(bf)
+    wgt = (torch.randn((D, 1024), device="cuda", generator=g) * 0.02).to(bf)
+    o = torch.empty((T, D), device="cuda", dtype=bf)
+    big0 = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    big1 = torch.empty_like(big0)
+
+    def after(prep, n):
+        e = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(n)]
+        for i in range(n + warmup):
+            prep()
+            if i >= warmup:
+                e[i - warmup][0].record(stream)
+            run(gated)
+            if i >= warmup:
+                e[i - warmup][1].record(stream)
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in e) / n * 1000
+
+    n = max(10, min(steps, 50))
+    us_gemm = after(lambda: (K.gemm_bf16(a, wgt, o, stream=stream),
+                             K.gemm_bf16(a, wgt, o, stream=stream)), n)
+    us_copy = after(lambda: big1.copy_(big0), n)
+    return {"gated_us": round(wg / steps * 1000, 1), "ungated_us": round(wp / steps * 1000, 1),
+            "gated_after_two_gemms_us": round(us_gemm, 1),
+            "gated_after_512MB_copy_us": round(us_copy, 1),
+            "config": {"B": Bsz, "L": L, "D": D, "N": N, "bc_row": NX, "dtype": "bf16"}}
+
+
 def bench_gemm_vs_library(torch, K, stream, steps, warmup):
     """The block's two projection shapes (in_proj half: 16384 x 2048 x 1024,
     out_proj: 16384 x 1024 x 2048) on km_gemm_bf16 and on torch.matmul
@@ -512,8 +567,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", choices=["all", "scan1d", "scan1d_shapes", "scan1d_bwd", "scannd",
-                                       "convnd", "block", "mamba3", "gemm", "model", "scannd_bwd",
-                                       "copy"],
+                                       "convnd", "block", "scan1d_gated", "mamba3", "gemm", "model",
+                                       "scannd_bwd", "copy"],
                     default="all",
                     help="profiling modes: scan1d = the fp32 headline kernel only; scan1d_shapes = "
                          "the forward at each --shapes entry; copy = a plain 1 GiB device copy "
@@ -547,6 +602,11 @@ def main():
             rb = bench_scan1d_bwd(torch, K, stream, 8, 4096, 1024, 16, "bf16", args.steps,
                                   args.warmup)
         print(json.dumps({"scan1d_bwd_f32": r, "scan1d_bwd_bf16": rb}))
+        return
+    if args.only == "scan1d_gated":
+        with torch.cuda.stream(stream):
+            r = bench_scan1d_gated(torch, K, stream, args.steps, args.warmup)
+        print(json.dumps({"scan1d_gated_block_shape": r}))
         return
     if args.only == "block":
         with torch.cuda.stream(stream):
