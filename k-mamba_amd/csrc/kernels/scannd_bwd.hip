@@ -380,6 +380,203 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_lanes(NdBwdArgs a, long 
     }
 }
 
+// One point of the gradient pass in the lanes layout of
+// nd_adjoint_grads_lanes, split in two so that a tile walk can issue the
+// loads of a group of points before the arithmetic and stores of the first:
+// the compiler does not move a load above a store through pointers it
+// cannot tell apart (dB is read as g and written in place).
+template <int ND>
+struct GradIn {
+    float xv, dyv, dl[ND], gv, bv, hv;
+};
+
+template <int ND>
+__device__ __forceinline__ GradIn<ND> grad_load(const NdBwdArgs &a, long q, long c, long d, long DM) {
+    GradIn<ND> v;
+    v.xv = a.x[q * a.D + d];
+    v.dyv = a.dy[q * a.D + d];
+#pragma unroll
+    for (int ax = 0; ax < ND; ++ax) v.dl[ax] = a.delta[(ax * a.P + q) * a.D + d];
+    const long pc = q * DM + c;
+    v.gv = a.dB[pc];
+    v.bv = a.B[pc];
+    v.hv = a.h[pc];
+    return v;
+}
+
+// The arithmetic and stores of one point, with the states of its axis
+// predecessors hp[ax] (used where has[ax]).
+template <int ND>
+__device__ __forceinline__ void grad_finish(const NdBwdArgs &a, const GradIn<ND> &v, long q, long c,
+                                            long d, int m, bool active, long M, long DM,
+                                            const float (&av)[ND], float (&dAacc)[ND],
+                                            const float (&hp)[ND], const bool (&has)[ND]) {
+    float dtb = 0.f;
+#pragma unroll
+    for (int ax = 0; ax < ND; ++ax) dtb += v.dl[ax];
+    dtb /= static_cast<float>(ND);
+    const long pc = q * DM + c;
+    float tx = v.gv * dtb * v.bv, tbx = v.gv * v.bv * v.xv, td[ND];
+#pragma unroll
+    for (int ax = 0; ax < ND; ++ax) {
+        td[ax] = 0.f;
+        if (has[ax]) {
+            const float e = exp2_fast(v.dl[ax] * av[ax] * kLog2e);
+            const float gh = v.gv * e * hp[ax];
+            td[ax] = gh * av[ax];
+            dAacc[ax] += gh * v.dl[ax];
+        }
+    }
+    for (int k = 1; k < M; k <<= 1) {
+        tx += __shfl_xor(tx, k);
+        tbx += __shfl_xor(tbx, k);
+#pragma unroll
+        for (int ax = 0; ax < ND; ++ax) td[ax] += __shfl_xor(td[ax], k);
+    }
+    if (active) {
+        a.dC[pc] = v.dyv * v.hv;
+        a.dB[pc] = v.gv * dtb * v.xv;
+        if (m == 0) {
+            a.dx[q * a.D + d] = tx;
+#pragma unroll
+            for (int ax = 0; ax < ND; ++ax)
+                a.ddelta[(ax * a.P + q) * a.D + d] = tbx / static_cast<float>(ND) + td[ax];
+        }
+    }
+}
+
+// The gradient pass over tiles of a 2D grid: workgroup x takes tile x (TR
+// rows x TW points) and walks it column by column, down each column, so the
+// state of the point above is the previous step's and the one to the left
+// is the previous column's (kept per row): only the tile's first row and
+// first column read a predecessor's state from memory. A column's TR points
+// load together before any of them computes.
+template <int TR, int TW>
+__global__ void __launch_bounds__(256) nd_adjoint_grads_tile2d(NdBwdArgs a) {
+    const long M = a.M, DM = a.D * M;
+    const long c0 = static_cast<long>(blockIdx.y) * 256 + threadIdx.x;
+    const bool active = c0 < DM;
+    const long c = active ? c0 : 0;
+    const long d = c / M;
+    const int m = static_cast<int>(c - d * M);
+    const long d1 = a.dims[1];
+    const long nt1 = (d1 + TW - 1) / TW;
+    const long i0 = (static_cast<long>(blockIdx.x) / nt1) * TR, j0 = (static_cast<long>(blockIdx.x) % nt1) * TW;
+    const long ie = std::min<long>(TR, a.dims[0] - i0), je = std::min<long>(TW, d1 - j0);
+    float av[2], dAacc[2];
+#pragma unroll
+    for (int ax = 0; ax < 2; ++ax) {
+        av[ax] = a.A[ax * DM + c];
+        dAacc[ax] = 0.f;
+    }
+    float left[TR];
+#pragma unroll
+    for (int ii = 0; ii < TR; ++ii) left[ii] = 0.f;
+    for (long jj = 0; jj < je; ++jj) {
+        const long j = j0 + jj;
+        GradIn<2> v[TR];
+#pragma unroll
+        for (int ii = 0; ii < TR; ++ii) {
+            const long i = i0 + (ii < ie ? ii : 0);           // rows past the grid reload row i0
+            v[ii] = grad_load<2>(a, i * d1 + j, c, d, DM);
+        }
+        const float hup0 = i0 > 0 ? a.h[((i0 - 1) * d1 + j) * DM + c] : 0.f;
+        const float hleft0 = (jj == 0 && j > 0) ? a.h[(i0 * d1 + j - 1) * DM + c] : 0.f;
+        float up = hup0;
+#pragma unroll
+        for (int ii = 0; ii < TR; ++ii) {
+            if (ii < ie) {
+                const long i = i0 + ii;
+                const long q = i * d1 + j;
+                const bool has[2] = {i > 0, j > 0};
+                float hl = left[ii];
+                if (jj == 0) hl = ii == 0 ? hleft0 : (j > 0 ? a.h[(q - 1) * DM + c] : 0.f);
+                const float hp[2] = {up, hl};
+                grad_finish<2>(a, v[ii], q, c, d, m, active, M, DM, av, dAacc, hp, has);
+                up = v[ii].hv;
+                left[ii] = v[ii].hv;
+            }
+        }
+    }
+    if (active) {
+#pragma unroll
+        for (int ax = 0; ax < 2; ++ax) a.part[(static_cast<long>(blockIdx.x) * 2 + ax) * DM + c] = dAacc[ax];
+    }
+}
+
+// The same over tiles of a 3D grid (TP planes x TR rows x TW points): the
+// walk goes row by row, point by point, through the tile's planes at each
+// (row, point), so the plane predecessor is the previous step's state, the
+// point to the left the previous point's (per plane) and the row above the
+// previous row's (per point and plane, TW x TP registers). The TP points of
+// a (row, point) load together.
+template <int TP, int TR, int TW>
+__global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
+    const long M = a.M, DM = a.D * M;
+    const long c0 = static_cast<long>(blockIdx.y) * 256 + threadIdx.x;
+    const bool active = c0 < DM;
+    const long c = active ? c0 : 0;
+    const long d = c / M;
+    const int m = static_cast<int>(c - d * M);
+    const long d1 = a.dims[1], d2 = a.dims[2];
+    const long nt1 = (d1 + TR - 1) / TR, nt2 = (d2 + TW - 1) / TW;
+    const long t = blockIdx.x;
+    const long p0 = (t / (nt1 * nt2)) * TP, i0 = ((t / nt2) % nt1) * TR, j0 = (t % nt2) * TW;
+    const long pe = std::min<long>(TP, a.dims[0] - p0), ie = std::min<long>(TR, d1 - i0),
+               je = std::min<long>(TW, d2 - j0);
+    const long s0 = d1 * d2;
+    float av[3], dAacc[3];
+#pragma unroll
+    for (int ax = 0; ax < 3; ++ax) {
+        av[ax] = a.A[ax * DM + c];
+        dAacc[ax] = 0.f;
+    }
+    float above[TW][TP];
+#pragma unroll
+    for (int jj = 0; jj < TW; ++jj)
+#pragma unroll
+        for (int pp = 0; pp < TP; ++pp) above[jj][pp] = 0.f;
+    for (long ii = 0; ii < ie; ++ii) {
+        const long i = i0 + ii;
+        float left[TP];
+#pragma unroll
+        for (int pp = 0; pp < TP; ++pp) left[pp] = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < TW; ++jj) {
+            if (jj < je) {
+                const long j = j0 + jj;
+                GradIn<3> v[TP];
+#pragma unroll
+                for (int pp = 0; pp < TP; ++pp) {
+                    const long pl = p0 + (pp < pe ? pp : 0);   // planes past the grid reload plane p0
+                    v[pp] = grad_load<3>(a, pl * s0 + i * d2 + j, c, d, DM);
+                }
+                float prev = p0 > 0 ? a.h[((p0 - 1) * s0 + i * d2 + j) * DM + c] : 0.f;
+#pragma unroll
+                for (int pp = 0; pp < TP; ++pp) {
+                    if (pp < pe) {
+                        const long pl = p0 + pp;
+                        const long q = pl * s0 + i * d2 + j;
+                        const bool has[3] = {pl > 0, i > 0, j > 0};
+                        const float hp[3] = {
+                            prev,
+                            ii == 0 ? (i > 0 ? a.h[(q - d2) * DM + c] : 0.f) : above[jj][pp],
+                            jj == 0 ? (j > 0 ? a.h[(q - 1) * DM + c] : 0.f) : left[pp]};
+                        grad_finish<3>(a, v[pp], q, c, d, m, active, M, DM, av, dAacc, hp, has);
+                        prev = v[pp].hv;
+                        left[pp] = v[pp].hv;
+                        above[jj][pp] = v[pp].hv;
+                    }
+                }
+            }
+        }
+    }
+    if (active) {
+#pragma unroll
+        for (int ax = 0; ax < 3; ++ax) a.part[(static_cast<long>(blockIdx.x) * 3 + ax) * DM + c] = dAacc[ax];
+    }
+}
+
 __global__ void __launch_bounds__(256) nd_adjoint_dA(const float *part, float *dA, long nbx, long n) {
     const long k = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
     if (k >= n) return;
@@ -388,9 +585,13 @@ __global__ void __launch_bounds__(256) nd_adjoint_dA(const float *part, float *d
     dA[k] = s;
 }
 
+constexpr int kGradTR2 = 8, kGradTW2 = 64;                  // 2D gradient tiles (rows, points)
+constexpr int kGradTP3 = 4, kGradTR3 = 8, kGradTW3 = 8;     // 3D gradient tiles
+
 struct NdBwdShape {
     long P, nd, D, M;
     bool lanes;          // M a power of two <= 64: nd_adjoint_grads_lanes
+    bool gtiles;         // ... and 2D or 3D: the tile walks
     int db;
     long qc, nbx, nby;
     size_t offs_bytes, nbr_bytes, part_bytes, tile_bytes;
@@ -434,6 +635,18 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
         s.qc = std::max<long>(256 / db, (s.P + want - 1) / want);
     }
     s.nbx = (s.P + s.qc - 1) / s.qc;
+    // 2D and 3D grids on the lanes path walk tiles (one workgroup column per
+    // tile), carrying the predecessors' states in registers.
+    s.gtiles = s.lanes && (s.nd == 2 || s.nd == 3);
+    if (s.gtiles) {
+        const long t2[2] = {kGradTR2, kGradTW2}, t3[3] = {kGradTP3, kGradTR3, kGradTW3};
+        long nt = 1;
+        for (long ax = 0; ax < s.nd; ++ax) {
+            const long te = s.nd == 2 ? t2[ax] : t3[ax];
+            nt *= (a->dims[ax] + te - 1) / te;
+        }
+        s.nbx = nt;
+    }
     s.offs_bytes = align_up(sizeof(long) * s.P, 256);
     s.nbr_bytes = align_up(sizeof(uint16_t) * s.P, 256);
     s.tile_bytes = 0;
@@ -484,7 +697,15 @@ static void nd_bwd_launch(const NdBwdArgs &args, const NdBwdShape &s, const KMWa
         }
     }
     }
-    if (s.lanes) {
+    if (s.gtiles && ND == 2) {
+        hipLaunchKernelGGL((nd_adjoint_grads_tile2d<kGradTR2, kGradTW2>),
+                           dim3(static_cast<unsigned>(s.nbx), static_cast<unsigned>(s.nby)), dim3(256), 0, st,
+                           args);
+    } else if (s.gtiles && ND == 3) {
+        hipLaunchKernelGGL((nd_adjoint_grads_tile3d<kGradTP3, kGradTR3, kGradTW3>),
+                           dim3(static_cast<unsigned>(s.nbx), static_cast<unsigned>(s.nby)), dim3(256), 0, st,
+                           args);
+    } else if (s.lanes) {
         hipLaunchKernelGGL(nd_adjoint_grads_lanes<ND>,
                            dim3(static_cast<unsigned>(s.nbx), static_cast<unsigned>(s.nby)), dim3(256), 0, st,
                            args, s.qc);
