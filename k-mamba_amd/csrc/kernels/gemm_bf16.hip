@@ -207,26 +207,20 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_mfma(GemmArgs p) {
 // (gemm_bf16_mfma_pp below), K in stages of 32.
 constexpr int kGM = 256, kGN = 256, kGK = 32;   // rows, columns, k per stage
 
-// Skinny shapes (N <= 128 with a long K, or K <= 64): MFMA operands come
-// from global memory straight into registers, with no LDS staging and no
-// barrier in the K loop. K runs in blocks of 16*CPB: lane l < 32 holds row
-// l's first half of the block and lane l + 32 its second half, CPB
-// contiguous 16-byte chunks each, and MFMA step s of a block takes chunk s
-// of both halves: the order of the terms of a dot product is free, and A
-// and B use the same one. A wave computes a 32 x 32*TN block of C.
-// KSPLIT = 1 (K <= 64, one block of 64): the 4 waves of a workgroup take 4
-// consecutive row blocks (workgroup tile 128 x 32*TN). KSPLIT = 4 (blocks of
-// 32, two in flight per wave): the waves take the same row block and the k
-// blocks w, w + 4, ..., and wave 0 adds the other waves' partial sums from
-// LDS in wave order. Chunks past K load as zero (out-of-range offset).
-template <int EPI, bool CBF16, int TN, int KSPLIT>
+// Shallow shapes (K <= 64: dt_proj): MFMA operands come from global memory
+// straight into registers, with no LDS staging and no barrier: K is one
+// block of 64; lane l < 32 holds row l's first 32 k and lane l + 32 its
+// last 32, four contiguous 16-byte chunks each, and MFMA step s takes chunk
+// s of both halves: the order of the terms of a dot product is free, and A
+// and B use the same one. A wave computes a 32 x 32*TN block of C; the 4
+// waves of a workgroup take 4 consecutive row blocks (workgroup tile
+// 128 x 32*TN). Chunks past K load as zero (out-of-range offset).
+template <int EPI, bool CBF16, int TN>
 __global__ void __launch_bounds__(256) gemm_bf16_direct(GemmArgs p) {
     constexpr int ES = CBF16 ? 2 : 4;
-    constexpr int CPB = KSPLIT > 1 ? 2 : 4;            // 16-byte chunks per lane per block
+    constexpr int CPB = 4;                             // 16-byte chunks per lane
     constexpr int KB = 16 * CPB;                       // k per block
-    constexpr int SW = KSPLIT > 1 ? 1 : 4;             // waves that store
-    __shared__ float red[KSPLIT > 1 ? KSPLIT - 1 : 1][KSPLIT > 1 ? TN * 16 : 1][64];
-    __shared__ __attribute__((aligned(16))) char stage[SW][32 * TN * 32 * ES];
+    __shared__ __attribute__((aligned(16))) char stage[4][32 * TN * 32 * ES];
     constexpr unsigned kDrop = 0x80000000u;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -234,7 +228,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_direct(GemmArgs p) {
     const int fr = lane & 31, fh = lane >> 5;
     long mb, nb;
     xcd_tile(mb, nb);
-    const long m0 = mb * (KSPLIT > 1 ? 32 : 128) + (KSPLIT > 1 ? 0 : w * 32);
+    const long m0 = mb * 128 + w * 32;
     const long n0 = nb * (32 * TN);
     const long arows = std::min<long>(32, p.M - m0), brows = std::min<long>(32 * TN, p.N - n0);
     const auto rA = make_rsrc(p.A + (arows > 0 ? m0 : 0) * p.lda,
@@ -245,64 +239,29 @@ __global__ void __launch_bounds__(256) gemm_bf16_direct(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) boff[j] = (j * 32 + fr) * static_cast<int>(p.ldb) * 2;
 
-    auto ld = [&](__amdgpu_buffer_rsrc_t r, int rowoff, long kb, int c) {
-        const long k = kb * KB + (KB / 2) * fh + 8 * c;
+    auto ld = [&](__amdgpu_buffer_rsrc_t r, int rowoff, int c) {
+        const long k = (KB / 2) * fh + 8 * c;
         const int off = static_cast<int>(k < p.K ? static_cast<unsigned>(rowoff + k * 2) : kDrop);
         return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
     };
-    auto load_blk = [&](long kb, bf16x8 (&a)[CPB], bf16x8 (&b)[TN][CPB]) {
+    bf16x8 a0[CPB], b0[TN][CPB];
 #pragma unroll
-        for (int c = 0; c < CPB; ++c) a[c] = ld(rA, aoff, kb, c);
+    for (int c = 0; c < CPB; ++c) a0[c] = ld(rA, aoff, c);
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int c = 0; c < CPB; ++c) b[j][c] = ld(rB, boff[j], kb, c);
-    };
+        for (int c = 0; c < CPB; ++c) b0[j][c] = ld(rB, boff[j], c);
     f32x16 acc[1][TN];
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[0][j][r] = 0.f;
-    auto mfma_blk = [&](const bf16x8 (&a)[CPB], const bf16x8 (&b)[TN][CPB]) {
 #pragma unroll
-        for (int c = 0; c < CPB; ++c)
+    for (int c = 0; c < CPB; ++c)
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
-                acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c], b[j][c], acc[0][j], 0, 0, 0);
-    };
-    bf16x8 a0[CPB], b0[TN][CPB];
-    if constexpr (KSPLIT == 1) {
-        load_blk(0, a0, b0);
-        mfma_blk(a0, b0);
-    } else {
-        bf16x8 a1[CPB], b1[TN][CPB];
-        const long nkb = (p.K + KB - 1) / KB;
-        long kb = w;
-        load_blk(kb, a0, b0);
-        for (; kb < nkb; kb += 2 * KSPLIT) {
-            load_blk(kb + KSPLIT, a1, b1);
-            __builtin_amdgcn_sched_barrier(0);
-            mfma_blk(a0, b0);
-            load_blk(kb + 2 * KSPLIT, a0, b0);
-            __builtin_amdgcn_sched_barrier(0);
-            mfma_blk(a1, b1);
-        }
-        if (w > 0) {
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) red[w - 1][j * 16 + r][lane] = acc[0][j][r];
-        }
-        __syncthreads();
-        if (w != 0) return;
-#pragma unroll 1
-        for (int v = 0; v < KSPLIT - 1; ++v)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[0][j][r] += red[v][j * 16 + r][lane];
-    }
-    store_wave_tile<EPI, CBF16, 1, TN>(p, acc, m0, n0, stage[KSPLIT > 1 ? 0 : w], lane);
+        for (int j = 0; j < TN; ++j)
+            acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[c], b0[j][c], acc[0][j], 0, 0, 0);
+    store_wave_tile<EPI, CBF16, 1, TN>(p, acc, m0, n0, stage[w], lane);
 }
 
 // The 256x256 tile on eight waves, two per SIMD, in ping-pong: waves w and
@@ -435,6 +394,122 @@ __global__ void __launch_bounds__(512, 1) gemm_bf16_mfma_pp(GemmArgs p) {
     store_wave_tile<EPI, CBF16, 4, 2>(p, acc, m0 + g * 128, n0 + sg * 64, lds, lane);
 }
 
+// Narrow shapes with a long K (N <= 128, K >= 512: x_proj): a workgroup
+// computes 64 rows x 32*TN columns. Operands go straight from HBM into LDS
+// (gfx950 buffer_load_dwordx4 ... lds) in stages of 128 k: a load
+// instruction fills 4 whole rows of 256 bytes, so both operands stream in
+// full cache lines (loading fragments straight into registers, one 16-byte
+// piece of 32 rows per instruction, kept the texture unit busy at ~51 L1
+// accesses per load). Three stage buffers, loads two stages ahead. Wave w
+// takes rows 32 (w & 1) and the 64-k half (w >> 1) of every stage, so the
+// B rows of a stage, the larger operand here, serve four waves; the two
+// halves' partial sums are added in LDS (fixed order) before the epilogue.
+// LDS slot row * 16 + pc holds 16-byte chunk pc ^ (row & 7) of its row: the
+// eight rows a quarter of a fragment read touches fall on distinct banks.
+template <int EPI, bool CBF16, int TN>
+__global__ void __launch_bounds__(256) gemm_bf16_narrow(GemmArgs p) {
+    constexpr int RA = 64, RB = 32 * TN, CH = 16;            // rows, 16-byte chunks per row per stage
+    constexpr int KS = CH * 8;                                // k per stage
+    constexpr int NI = (RA + RB) * CH / 64 / 4;               // load instructions per wave per stage
+    static_assert((RA + RB) * CH % 256 == 0, "whole load instructions per wave");
+    __shared__ u32x4 sA0[RA * CH], sA1[RA * CH], sA2[RA * CH];
+    __shared__ u32x4 sB0[RB * CH], sB1[RB * CH], sB2[RB * CH];
+    constexpr unsigned kDrop = 0x80000000u;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int half = w >> 1, rw = w & 1;
+    long mb, nb;
+    xcd_tile(mb, nb);
+    const long m0 = mb * RA, n0 = nb * RB;
+    const long arows = std::min<long>(RA, p.M - m0), brows = std::min<long>(RB, p.N - n0);
+    const auto rA = make_rsrc(p.A + m0 * p.lda, (arows - 1) * p.lda * 2 + p.K * 2);
+    const auto rB = make_rsrc(p.B + n0 * p.ldb, (brows - 1) * p.ldb * 2 + p.K * 2);
+    // Load instruction i of wave w: the first NA fill A slots
+    // [64 (w + 4 i), +64), the rest B slots [64 (w + 4 (i - NA)), +64).
+    constexpr int NA = RA * CH / 256;
+    int roff[NI], chk[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int slot = (w + 4 * (i < NA ? i : i - NA)) * 64 + lane;
+        const int row = slot / CH, pc = slot % CH;
+        chk[i] = pc ^ (row & 7);
+        roff[i] = static_cast<int>(row * (i < NA ? p.lda : p.ldb) * 2);
+    }
+    using lds_t = __attribute__((address_space(3))) void *;
+    auto dma = [&](long st, u32x4 *dA, u32x4 *dB) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const long k = st * KS + chk[i] * 8;
+            const unsigned off = k < p.K ? static_cast<unsigned>(roff[i] + k * 2) : kDrop;
+            if (i < NA)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_t)(dA + (w + 4 * i) * 64), 16, off, 0, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_t)(dB + (w + 4 * (i - NA)) * 64), 16, off, 0,
+                                                         0, 0);
+        }
+    };
+    f32x16 acc[1][TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[0][j][r] = 0.f;
+    const int fr = lane & 31, fk = lane >> 5;
+    auto compute = [&](const u32x4 *bA, const u32x4 *bB) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const int c = half * 8 + ks * 2 + fk;
+            const int ra = rw * 32 + fr;
+            const bf16x8 af = __builtin_bit_cast(bf16x8, bA[ra * CH + (c ^ (ra & 7))]);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int rb = j * 32 + fr;
+                const bf16x8 bf = __builtin_bit_cast(bf16x8, bB[rb * CH + (c ^ (rb & 7))]);
+                acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, acc[0][j], 0, 0, 0);
+            }
+        }
+    };
+    const long nst = (p.K + KS - 1) / KS;
+    dma(0, sA0, sB0);
+    dma(1, sA1, sB1);
+    // Groups of three stages with no branch inside; stages past K load
+    // zeros and add nothing.
+    for (long st = 0; st < nst; st += 3) {
+#pragma unroll
+        for (int u = 0; u < 3; ++u) {
+            u32x4 *cA = u == 0 ? sA0 : u == 1 ? sA1 : sA2;
+            u32x4 *cB = u == 0 ? sB0 : u == 1 ? sB1 : sB2;
+            u32x4 *nA = u == 0 ? sA2 : u == 1 ? sA0 : sA1;
+            u32x4 *nB = u == 0 ? sB2 : u == 1 ? sB0 : sB1;
+            __builtin_amdgcn_s_waitcnt(0x0F70 | NI);             // vmcnt(NI): own loads of stage st + u done
+            __builtin_amdgcn_s_barrier();                        // ... and every wave's; stage st + u - 1 read
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            __builtin_amdgcn_sched_barrier(0);
+            dma(st + u + 2, nA, nB);
+            compute(cA, cB);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    // The second k half's partials, added by the first half's waves.
+    float *red = reinterpret_cast<float *>(sB0);              // [2 waves][TN * 16][64]: TN * 8 KB
+    if (half == 1) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) red[(rw * TN * 16 + j * 16 + r) * 64 + lane] = acc[0][j][r];
+    }
+    __syncthreads();
+    if (half == 1) return;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[0][j][r] += red[(rw * TN * 16 + j * 16 + r) * 64 + lane];
+    char *lds = reinterpret_cast<char *>(rw == 0 ? sA1 : sA2);
+    store_wave_tile<EPI, CBF16, 1, TN>(p, acc, m0 + rw * 32, n0, lds, lane);
+}
+
 template <int EPI>
 static void gemm_go(const GemmArgs &a, dim3 g, bool big, hipStream_t s) {
     if (big) {
@@ -446,33 +521,37 @@ static void gemm_go(const GemmArgs &a, dim3 g, bool big, hipStream_t s) {
     }
 }
 
-template <int EPI, int TN, int KSPLIT>
+template <int EPI>
 static void direct_go(const GemmArgs &a, dim3 g, hipStream_t s) {
-    if (a.c_bf16) hipLaunchKernelGGL((gemm_bf16_direct<EPI, true, TN, KSPLIT>), g, dim3(256), 0, s, a);
-    else          hipLaunchKernelGGL((gemm_bf16_direct<EPI, false, TN, KSPLIT>), g, dim3(256), 0, s, a);
+    if (a.c_bf16) hipLaunchKernelGGL((gemm_bf16_direct<EPI, true, 4>), g, dim3(256), 0, s, a);
+    else          hipLaunchKernelGGL((gemm_bf16_direct<EPI, false, 4>), g, dim3(256), 0, s, a);
+}
+
+template <int EPI, int TN>
+static void narrow_go(const GemmArgs &a, dim3 g, hipStream_t s) {
+    if (a.c_bf16) hipLaunchKernelGGL((gemm_bf16_narrow<EPI, true, TN>), g, dim3(256), 0, s, a);
+    else          hipLaunchKernelGGL((gemm_bf16_narrow<EPI, false, TN>), g, dim3(256), 0, s, a);
 }
 
 template <int EPI>
-static void direct_by_shape(const GemmArgs &a, dim3 g, int tn, int ksplit, hipStream_t s) {
-    if (ksplit == 1) { direct_go<EPI, 4, 1>(a, g, s); return; }
+static void narrow_by_tn(const GemmArgs &a, dim3 g, int tn, hipStream_t s) {
     switch (tn) {
-    case 1: direct_go<EPI, 1, 4>(a, g, s); break;
-    case 2: direct_go<EPI, 2, 4>(a, g, s); break;
-    case 3: direct_go<EPI, 3, 4>(a, g, s); break;
-    default: direct_go<EPI, 4, 4>(a, g, s); break;
+    case 1: narrow_go<EPI, 1>(a, g, s); break;
+    case 2: narrow_go<EPI, 2>(a, g, s); break;
+    case 3: narrow_go<EPI, 3>(a, g, s); break;
+    default: narrow_go<EPI, 4>(a, g, s); break;
     }
 }
 
-// Skinny shapes on gemm_bf16_direct: N <= 128 with K >= 512 (the 4 waves of
-// a workgroup split K), or K <= 64 (one k block). Returns 1 when launched,
-// 0 when the shape is not one of these, -1 on a launch error.
+// Skinny shapes: N <= 128 with K >= 512 on gemm_bf16_narrow, K <= 64 on
+// gemm_bf16_direct. Returns 1 when launched, 0 when the shape is neither,
+// -1 on a launch error.
 static int direct_launch(const KMGemm *g, hipStream_t s) {
     const bool narrow = g->N <= 128 && g->K >= 512;
     const bool shallow = g->K <= 64;
     if (!narrow && !shallow) return 0;
-    const int ksplit = narrow ? 4 : 1;
     const int tn = narrow ? static_cast<int>((g->N + 31) / 32) : 4;
-    const long TM = ksplit > 1 ? 32 : 128, TN = 32L * tn;
+    const long TM = narrow ? 64 : 128, TN = 32L * tn;
     if (g->ldb * 2 * (TN + 1) > 0x7fffffffL || g->lda * 2 * (TM + 1) > 0x7fffffffL) return 0;
     const long nbn = (g->N + TN - 1) / TN, nbm = (g->M + TM - 1) / TM;
     if (nbn > 0x7fffffffL) return 0;
@@ -489,10 +568,18 @@ static int direct_launch(const KMGemm *g, hipStream_t s) {
         a.N = g->N; a.K = g->K; a.lda = g->lda; a.ldb = g->ldb; a.ldc = g->ldc;
         a.epi = g->epilogue;
         const dim3 grid(static_cast<unsigned>(nbn), static_cast<unsigned>(nb));
-        switch (g->epilogue) {
-        case KM_EPI_SOFTPLUS: direct_by_shape<KM_EPI_SOFTPLUS>(a, grid, tn, ksplit, s); break;
-        case KM_EPI_SILU:     direct_by_shape<KM_EPI_SILU>(a, grid, tn, ksplit, s); break;
-        default:              direct_by_shape<KM_EPI_NONE>(a, grid, tn, ksplit, s); break;
+        if (narrow) {
+            switch (g->epilogue) {
+            case KM_EPI_SOFTPLUS: narrow_by_tn<KM_EPI_SOFTPLUS>(a, grid, tn, s); break;
+            case KM_EPI_SILU:     narrow_by_tn<KM_EPI_SILU>(a, grid, tn, s); break;
+            default:              narrow_by_tn<KM_EPI_NONE>(a, grid, tn, s); break;
+            }
+        } else {
+            switch (g->epilogue) {
+            case KM_EPI_SOFTPLUS: direct_go<KM_EPI_SOFTPLUS>(a, grid, s); break;
+            case KM_EPI_SILU:     direct_go<KM_EPI_SILU>(a, grid, s); break;
+            default:              direct_go<KM_EPI_NONE>(a, grid, s); break;
+            }
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) {
