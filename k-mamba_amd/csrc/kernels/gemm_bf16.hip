@@ -207,20 +207,25 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_mfma(GemmArgs p) {
 // (gemm_bf16_mfma_pp below), K in stages of 32.
 constexpr int kGM = 256, kGN = 256, kGK = 32;   // rows, columns, k per stage
 
-// Shallow shapes (K <= 64: dt_proj): MFMA operands come from global memory
-// straight into registers, with no LDS staging and no barrier: K is one
-// block of 64; lane l < 32 holds row l's first 32 k and lane l + 32 its
-// last 32, four contiguous 16-byte chunks each, and MFMA step s takes chunk
+// Shallow shapes (K <= 64: dt_proj): K is one block of 64, so each
+// workgroup loads its operands once. A wave computes a 32 x 32*TN block of
+// C and the 4 waves of a workgroup take 4 consecutive row blocks (workgroup
+// tile 128 x 32*TN), so the B rows (the workgroup's 32*TN columns) are
+// shared: they go straight from HBM into LDS (gfx950 buffer_load_dwordx4 ...
+// lds, 8 whole 128-byte rows per instruction), each wave's 32 A rows
+// straight into registers. Lane l < 32 takes row l's first 32 k and lane
+// l + 32 its last 32, four 16-byte chunks each, and MFMA step s takes chunk
 // s of both halves: the order of the terms of a dot product is free, and A
-// and B use the same one. A wave computes a 32 x 32*TN block of C; the 4
-// waves of a workgroup take 4 consecutive row blocks (workgroup tile
-// 128 x 32*TN). Chunks past K load as zero (out-of-range offset).
+// and B use the same one. LDS slot row * 8 + pc holds chunk pc ^ (row & 7)
+// of its B row. Chunks past K load as zero (out-of-range offset).
 template <int EPI, bool CBF16, int TN>
 __global__ void __launch_bounds__(256) gemm_bf16_direct(GemmArgs p) {
     constexpr int ES = CBF16 ? 2 : 4;
     constexpr int CPB = 4;                             // 16-byte chunks per lane
     constexpr int KB = 16 * CPB;                       // k per block
+    constexpr int NBI = 32 * TN * 8 / 256;             // B load instructions per wave
     __shared__ __attribute__((aligned(16))) char stage[4][32 * TN * 32 * ES];
+    __shared__ u32x4 sB[32 * TN * 8];
     constexpr unsigned kDrop = 0x80000000u;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -235,22 +240,23 @@ __global__ void __launch_bounds__(256) gemm_bf16_direct(GemmArgs p) {
                               arows > 0 ? (arows - 1) * p.lda * 2 + p.K * 2 : 0);
     const auto rB = make_rsrc(p.B + n0 * p.ldb, brows > 0 ? (brows - 1) * p.ldb * 2 + p.K * 2 : 0);
     const int aoff = fr * static_cast<int>(p.lda) * 2;
-    int boff[TN];
+    bf16x8 a0[CPB];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) boff[j] = (j * 32 + fr) * static_cast<int>(p.ldb) * 2;
-
-    auto ld = [&](__amdgpu_buffer_rsrc_t r, int rowoff, int c) {
+    for (int c = 0; c < CPB; ++c) {
         const long k = (KB / 2) * fh + 8 * c;
-        const int off = static_cast<int>(k < p.K ? static_cast<unsigned>(rowoff + k * 2) : kDrop);
-        return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-    };
-    bf16x8 a0[CPB], b0[TN][CPB];
+        const int off = static_cast<int>(k < p.K ? static_cast<unsigned>(aoff + k * 2) : kDrop);
+        a0[c] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rA, off, 0, 0));
+    }
+    using lds_t = __attribute__((address_space(3))) void *;
 #pragma unroll
-    for (int c = 0; c < CPB; ++c) a0[c] = ld(rA, aoff, c);
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int c = 0; c < CPB; ++c) b0[j][c] = ld(rB, boff[j], c);
+    for (int i = 0; i < NBI; ++i) {
+        const int slot = (w + 4 * i) * 64 + lane;
+        const int row = slot >> 3, c = (slot & 7) ^ (row & 7);
+        const unsigned off = c * 8 < p.K ? static_cast<unsigned>(row * p.ldb * 2 + c * 16) : kDrop;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_t)(sB + (w + 4 * i) * 64), 16, off, 0, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);                // vmcnt(0): this wave's loads done
+    __syncthreads();                                   // ... and every wave's B rows
     f32x16 acc[1][TN];
 #pragma unroll
     for (int j = 0; j < TN; ++j)
@@ -259,8 +265,11 @@ __global__ void __launch_bounds__(256) gemm_bf16_direct(GemmArgs p) {
 #pragma unroll
     for (int c = 0; c < CPB; ++c)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-            acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[c], b0[j][c], acc[0][j], 0, 0, 0);
+        for (int j = 0; j < TN; ++j) {
+            const int rb = j * 32 + fr, ch = fh * CPB + c;
+            const bf16x8 bf = __builtin_bit_cast(bf16x8, sB[rb * 8 + (ch ^ (rb & 7))]);
+            acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[c], bf, acc[0][j], 0, 0, 0);
+        }
     store_wave_tile<EPI, CBF16, 1, TN>(p, acc, m0, n0, stage[w], lane);
 }
 
