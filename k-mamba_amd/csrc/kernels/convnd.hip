@@ -18,6 +18,9 @@
 //    dbias accumulate per wave, are summed per workgroup in LDS and stored to
 //    one slot per workgroup in the library workspace, and a second kernel
 //    adds the slots in a fixed order (no atomics, run-to-run identical).
+//    Where both windows fit the registers (2D, 3D with K = 2) the backward
+//    is one line-group pass computing dinput and the dkernel terms together,
+//    so dy is read once.
 //  - Other shapes with N <= 3: one line per wave; the backward fuses dinput
 //    and dkernel and adds dkernel per workgroup with fp32 atomics.
 //  - Anything else: one thread per (point, channel), taps from memory.
@@ -696,6 +699,148 @@ __global__ void __launch_bounds__(64 * kConvWaves) convnd_dw_lines(ConvArgs p, f
     }
 }
 
+// The backward of a line group in one pass (2D, and 3D with K = 2, where
+// both windows fit the registers): dinput of the group's lines from the
+// anti-causal window of dy, and the dkernel / dbias terms from the causal
+// window of the input times dy of the lines themselves, which that dy
+// window already holds (its column j, rows at offset 0 on every axis): dy
+// is read once instead of once per kernel. Tasks, slots and the fixed-order
+// workgroup sum are those of convnd_dw_lines; convnd_dw_finish adds the
+// slots.
+template <int ND, int K, int S>
+__global__ void __launch_bounds__(64 * kConvWaves) convnd_bwd_lines(ConvArgs p, float *part, long per) {
+    constexpr int R = kConvR;
+    constexpr int KO = ipow(K, ND - 2);
+    constexpr int RS = R + K - 1;
+    constexpr int NR = KO * RS;
+    constexpr int KV = ipow(K, ND);
+    constexpr int CU = 2 * NR <= 12 ? 2 : 1;         // columns per load chunk
+    constexpr int NCH = S / CU;
+    constexpr int QO = (KO - 1) * RS;                // dy window rows of the lines themselves: QO + r
+    static_assert(NCH >= 2 && NCH % 2 == 0, "strip is whole chunk pairs");
+    using F = bio<f32_t>;
+    __shared__ float red[kConvWaves][KV + 1][64];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const long g = blockIdx.y;
+    const long T = p.tasks_l / p.groups;
+    const long q0 = xcd_block(blockIdx.x, gridDim.x) * per;
+    float acc[KV + 1];
+#pragma unroll
+    for (int k = 0; k <= KV; ++k) acc[k] = 0.f;
+#pragma unroll 1
+    for (long q = q0; q < q0 + per; ++q) {
+        const long tl = q * kConvWaves + wave;
+        if (tl >= T) break;
+        const LineTask t = line_task<ND, S>(p, g, tl);
+        const int J = p.dims[ND - 1];
+        const long bbase = t.batch * p.P;
+        const auto rin = make_rsrc(p.in + bbase * p.D, p.P * p.D * 4);
+        const auto rdy = make_rsrc(p.dy + bbase * p.D, p.P * p.D * 4);
+        const auto rdin = make_rsrc(p.din + bbase * p.D, p.P * p.D * 4);
+        const int rb = p.D * 4;
+        const int j0 = t.j0;
+        float w[KV];
+#pragma unroll
+        for (int k = 0; k < KV; ++k) w[k] = p.W[static_cast<long>(k) * p.D + t.dc];
+        unsigned rd[NR], ri[NR], oo[R];
+        group_rows<ND, K, true>(p, t, rd);
+        group_rows<ND, K, false>(p, t, ri);
+        group_lines<ND>(p, t, oo);
+        // dy window: columns j..j+K-1 (0 past the line end); input window:
+        // columns j-(K-1)..j (0 before column 0).
+        float wd[NR][K], wi[NR][K];
+#pragma unroll
+        for (int qq = 0; qq < NR; ++qq) {
+#pragma unroll
+            for (int c = 0; c < K - 1; ++c) {
+                const int jd = j0 + c;
+                const float vd = F::ld(rdy, conv_off(rd[qq], jd, rb), 0);
+                wd[qq][c + 1] = jd < J ? vd : 0.f;
+                const int ji = j0 - (K - 1) + c;
+                const float vi = F::ld(rin, conv_off(ri[qq], ji < 0 ? 0 : ji, rb), 0);
+                wi[qq][c + 1] = ji >= 0 ? vi : 0.f;
+            }
+        }
+        float d0[CU][NR], i0[CU][NR], d1[CU][NR], i1[CU][NR];
+        auto load_chunk = [&](int ch, float (&bd)[CU][NR], float (&bi)[CU][NR]) {
+#pragma unroll
+            for (int u = 0; u < CU; ++u) {
+                const int j = j0 + ch * CU + u;
+#pragma unroll
+                for (int qq = 0; qq < NR; ++qq) {
+                    bd[u][qq] = F::ld(rdy, conv_off(rd[qq], j + K - 1, rb), 0);
+                    bi[u][qq] = F::ld(rin, conv_off(ri[qq], j, rb), 0);
+                }
+            }
+        };
+        auto run_chunk = [&](int ch, const float (&bd)[CU][NR], const float (&bi)[CU][NR]) {
+#pragma unroll
+            for (int u = 0; u < CU; ++u) {
+                const int j = j0 + ch * CU + u;
+                const bool dy_in = j + K - 1 < J;
+#pragma unroll
+                for (int qq = 0; qq < NR; ++qq) {
+#pragma unroll
+                    for (int c = 0; c < K - 1; ++c) {
+                        wd[qq][c] = wd[qq][c + 1];
+                        wi[qq][c] = wi[qq][c + 1];
+                    }
+                    wd[qq][K - 1] = dy_in ? bd[u][qq] : 0.f;
+                    wi[qq][K - 1] = bi[u][qq];
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    float sdin = 0.f;
+                    const float gy = j < J ? wd[QO + r][0] : 0.f;
+#pragma unroll
+                    for (int ko = 0; ko < KO; ++ko)
+#pragma unroll
+                        for (int ka = 0; ka < K; ++ka)
+#pragma unroll
+                            for (int kc = 0; kc < K; ++kc) {
+                                const int k = (ko * K + ka) * K + kc;
+                                sdin += wd[ko * RS + r + (K - 1 - ka)][K - 1 - kc] * w[k];
+                                acc[k] = fmaf(gy, wi[ko * RS + r + ka][kc], acc[k]);
+                            }
+                    acc[KV] += gy;
+                    F::st(rdin, j < J ? conv_off(oo[r], j, rb) : static_cast<int>(kConvDrop), 0, sdin);
+                }
+            }
+        };
+        load_chunk(0, d0, i0);
+#pragma unroll 1
+        for (int ch = 0; ch < NCH - 2; ch += 2) {
+            load_chunk(ch + 1, d1, i1);
+            run_chunk(ch, d0, i0);
+            load_chunk(ch + 2, d0, i0);
+            run_chunk(ch + 1, d1, i1);
+        }
+        load_chunk(NCH - 1, d1, i1);
+        run_chunk(NCH - 2, d0, i0);
+        run_chunk(NCH - 1, d1, i1);
+    }
+#pragma unroll
+    for (int k = 0; k <= KV; ++k) red[wave][k][lane] = acc[k];
+    __syncthreads();
+    float *slot = part + (g * gridDim.x + blockIdx.x) * static_cast<long>(KV + 1) * 64;
+    for (int i = threadIdx.x; i < (KV + 1) * 64; i += 64 * kConvWaves) {
+        float sum = 0.f;
+#pragma unroll
+        for (int v = 0; v < kConvWaves; ++v) sum += red[v][i / 64][i % 64];
+        slot[i] = sum;
+    }
+}
+
+// dkernel / dbias from the slots of convnd_bwd_lines: workgroup (k, g)
+// finishes tap k (k = KV: the bias) of channel group g.
+__global__ void __launch_bounds__(64 * kConvWaves) convnd_dw_finish(ConvArgs p, const float *part, int nslot) {
+    __shared__ float red[kConvWaves][64];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    dw_finalize(p, part, nslot, static_cast<int>(blockIdx.x % (p.KV + 1)), blockIdx.x / (p.KV + 1), wave,
+                threadIdx.x & 63, red);
+}
+
 // Any ND <= 8 and K: one thread per (point, channel), taps from memory.
 __global__ void __launch_bounds__(256) convnd_fwd_generic(ConvArgs p) {
     const long gid = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -938,7 +1083,22 @@ static int conv_bwd_launch(const ConvArgs &a, hipStream_t s) {
                                s, a, static_cast<const float *>(part), static_cast<int>(nslot)); \
             done = true;                                                                     \
         }
-        KM_CONV_BWDL(2, 2) KM_CONV_BWDL(2, 3) KM_CONV_BWDL(2, 4) KM_CONV_BWDL(3, 2) KM_CONV_BWDL(3, 3)
+#define KM_CONV_BWDF(ND, KK)                                                                 \
+        if (!done && a.nd == ND && a.K == KK) {                                              \
+            const auto kf = a.strip_l == 64 ? convnd_bwd_lines<ND, KK, 64>                      \
+                            : a.strip_l == 32 ? convnd_bwd_lines<ND, KK, 32>                    \
+                                              : convnd_bwd_lines<ND, KK, 16>;                   \
+            hipLaunchKernelGGL(kf, dim3(nslot, a.groups), dim3(64 * kConvWaves), 0, s, a, part, per); \
+            hipLaunchKernelGGL(convnd_dw_finish, dim3((a.KV + 1) * a.groups), dim3(64 * kConvWaves), 0, \
+                               s, a, static_cast<const float *>(part), static_cast<int>(nslot)); \
+            done = true;                                                                     \
+        }
+        // One pass where both windows fit the registers, else dkernel and
+        // dinput as two line-group launches (3D with K = 3: the fused form
+        // in passes of two lines, to fit, measured 81 against 56 us).
+        KM_CONV_BWDF(2, 2) KM_CONV_BWDF(2, 3) KM_CONV_BWDF(2, 4) KM_CONV_BWDF(3, 2)
+        KM_CONV_BWDL(3, 3)
+#undef KM_CONV_BWDF
 #undef KM_CONV_BWDL
     }
     if (!done && (zero_dev(a.dW, static_cast<long>(a.KV) * a.D, s) != 0 || zero_dev(a.db, a.D, s) != 0))
