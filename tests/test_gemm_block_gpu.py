@@ -39,8 +39,8 @@ def f32(a):
 
 @pytest.mark.parametrize("M,N,Kd", [(128, 128, 64), (1, 1, 8), (130, 97, 72), (257, 300, 1024),
                                     (1000, 96, 2048), (64, 2048, 64), (300, 33, 136),
-                                    # direct-operand kernel: N <= 128 with K >= 512 (k split
-                                    # over 4 waves, ragged M and K), and K <= 64
+                                    # narrow kernel: N <= 128 with K >= 512 (two k halves,
+                                    # ragged M, N and K); shallow kernel: K <= 64
                                     (517, 128, 512), (33, 64, 1000), (77, 20, 4104), (1, 128, 512),
                                     (200, 300, 24), (259, 129, 40),
                                     # 256x256 tiles with a K tail inside a 32-k stage
