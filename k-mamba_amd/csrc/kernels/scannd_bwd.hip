@@ -504,13 +504,14 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile2d(NdBwdArgs a) {
     }
 }
 
-// The same over tiles of a 3D grid (TP planes x TR rows x TW points): the
+// The same over tiles of a 3D grid (TP planes x TR rows x TW points), TPW
+// consecutive tiles per workgroup (fewer dA partials to add afterwards): the
 // walk goes row by row, point by point, through the tile's planes at each
 // (row, point), so the plane predecessor is the previous step's state, the
 // point to the left the previous point's (per plane) and the row above the
 // previous row's (per point and plane, TW x TP registers). The TP points of
 // a (row, point) load together.
-template <int TP, int TR, int TW>
+template <int TP, int TR, int TW, int TPW>
 __global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
     const long M = a.M, DM = a.D * M;
     const long c0 = static_cast<long>(blockIdx.y) * 256 + threadIdx.x;
@@ -520,10 +521,7 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
     const int m = static_cast<int>(c - d * M);
     const long d1 = a.dims[1], d2 = a.dims[2];
     const long nt1 = (d1 + TR - 1) / TR, nt2 = (d2 + TW - 1) / TW;
-    const long t = blockIdx.x;
-    const long p0 = (t / (nt1 * nt2)) * TP, i0 = ((t / nt2) % nt1) * TR, j0 = (t % nt2) * TW;
-    const long pe = std::min<long>(TP, a.dims[0] - p0), ie = std::min<long>(TR, d1 - i0),
-               je = std::min<long>(TW, d2 - j0);
+    const long ntiles = ((a.dims[0] + TP - 1) / TP) * nt1 * nt2;
     const long s0 = d1 * d2;
     float av[3], dAacc[3];
 #pragma unroll
@@ -531,6 +529,12 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
         av[ax] = a.A[ax * DM + c];
         dAacc[ax] = 0.f;
     }
+    const long t1 = std::min<long>(ntiles, (static_cast<long>(blockIdx.x) + 1) * TPW);
+#pragma unroll 1
+    for (long t = static_cast<long>(blockIdx.x) * TPW; t < t1; ++t) {
+    const long p0 = (t / (nt1 * nt2)) * TP, i0 = ((t / nt2) % nt1) * TR, j0 = (t % nt2) * TW;
+    const long pe = std::min<long>(TP, a.dims[0] - p0), ie = std::min<long>(TR, d1 - i0),
+               je = std::min<long>(TW, d2 - j0);
     float above[TW][TP];
 #pragma unroll
     for (int jj = 0; jj < TW; ++jj)
@@ -571,22 +575,36 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
             }
         }
     }
+    }
     if (active) {
 #pragma unroll
         for (int ax = 0; ax < 3; ++ax) a.part[(static_cast<long>(blockIdx.x) * 3 + ax) * DM + c] = dAacc[ax];
     }
 }
 
+// dA[k] = the nbx workgroup partials of k added in a fixed order: workgroup
+// x takes outputs [64 x, +64), wave w the partials b = w, w + 4, ... in four
+// interleaved running sums, then wave 0 adds the waves' sums in wave order.
 __global__ void __launch_bounds__(256) nd_adjoint_dA(const float *part, float *dA, long nbx, long n) {
-    const long k = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
-    if (k >= n) return;
-    float s = 0.f;
-    for (long b = 0; b < nbx; ++b) s += part[b * n + k];
-    dA[k] = s;
+    __shared__ float red[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const long k0 = static_cast<long>(blockIdx.x) * 64 + lane;
+    const long k = k0 < n ? k0 : n - 1;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    long b = w;
+    for (; b + 12 < nbx; b += 16) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) s[u] += part[(b + 4 * u) * n + k];
+    }
+    for (int u = 0; b < nbx; b += 4, ++u) s[u & 3] += part[b * n + k];
+    red[w][lane] = (s[0] + s[1]) + (s[2] + s[3]);
+    __syncthreads();
+    if (w == 0 && k0 < n) dA[k0] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
 }
 
 constexpr int kGradTR2 = 8, kGradTW2 = 64;                  // 2D gradient tiles (rows, points)
 constexpr int kGradTP3 = 4, kGradTR3 = 8, kGradTW3 = 8;     // 3D gradient tiles
+constexpr int kGradTPW3 = 4;                                 // 3D tiles per workgroup
 
 struct NdBwdShape {
     long P, nd, D, M;
@@ -645,7 +663,7 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
             const long te = s.nd == 2 ? t2[ax] : t3[ax];
             nt *= (a->dims[ax] + te - 1) / te;
         }
-        s.nbx = nt;
+        s.nbx = s.nd == 2 ? nt : (nt + kGradTPW3 - 1) / kGradTPW3;
     }
     s.offs_bytes = align_up(sizeof(long) * s.P, 256);
     s.nbr_bytes = align_up(sizeof(uint16_t) * s.P, 256);
@@ -702,7 +720,7 @@ static void nd_bwd_launch(const NdBwdArgs &args, const NdBwdShape &s, const KMWa
                            dim3(static_cast<unsigned>(s.nbx), static_cast<unsigned>(s.nby)), dim3(256), 0, st,
                            args);
     } else if (s.gtiles && ND == 3) {
-        hipLaunchKernelGGL((nd_adjoint_grads_tile3d<kGradTP3, kGradTR3, kGradTW3>),
+        hipLaunchKernelGGL((nd_adjoint_grads_tile3d<kGradTP3, kGradTR3, kGradTW3, kGradTPW3>),
                            dim3(static_cast<unsigned>(s.nbx), static_cast<unsigned>(s.nby)), dim3(256), 0, st,
                            args);
     } else if (s.lanes) {
@@ -716,7 +734,7 @@ static void nd_bwd_launch(const NdBwdArgs &args, const NdBwdShape &s, const KMWa
                            args, s.qc, s.db);
     }
     const long n = s.nd * DM;
-    hipLaunchKernelGGL(nd_adjoint_dA, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st,
+    hipLaunchKernelGGL(nd_adjoint_dA, dim3(static_cast<unsigned>((n + 63) / 64)), dim3(256), 0, st,
                        args.part, dA, s.nbx, n);
 }
 
