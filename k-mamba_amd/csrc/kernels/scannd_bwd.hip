@@ -604,7 +604,7 @@ __global__ void __launch_bounds__(256) nd_adjoint_dA(const float *part, float *d
 
 constexpr int kGradTR2 = 8, kGradTW2 = 64;                  // 2D gradient tiles (rows, points)
 constexpr int kGradTP3 = 4, kGradTR3 = 8, kGradTW3 = 8;     // 3D gradient tiles
-constexpr int kGradTPW3 = 4;                                 // 3D tiles per workgroup
+constexpr int kGradTPW3 = 1;                                 // 3D tiles per workgroup (2 and 4 measured slower)
 
 struct NdBwdShape {
     long P, nd, D, M;
