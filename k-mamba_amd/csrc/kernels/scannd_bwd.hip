@@ -469,33 +469,47 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile2d(NdBwdArgs a) {
         av[ax] = a.A[ax * DM + c];
         dAacc[ax] = 0.f;
     }
+    // The left neighbours of the tile's first column, and each column's
+    // points with the state above its first row, loaded one column ahead.
     float left[TR];
 #pragma unroll
-    for (int ii = 0; ii < TR; ++ii) left[ii] = 0.f;
-    for (long jj = 0; jj < je; ++jj) {
-        const long j = j0 + jj;
-        GradIn<2> v[TR];
+    for (int ii = 0; ii < TR; ++ii) {
+        const long i = i0 + (ii < ie ? ii : 0);
+        left[ii] = j0 > 0 ? a.h[(i * d1 + j0 - 1) * DM + c] : 0.f;
+    }
+    auto load_col = [&](long jj, GradIn<2> (&v)[TR], float &up0) {
+        const long j = j0 + (jj < je ? jj : 0);           // past the tile: reload column j0
 #pragma unroll
         for (int ii = 0; ii < TR; ++ii) {
-            const long i = i0 + (ii < ie ? ii : 0);           // rows past the grid reload row i0
+            const long i = i0 + (ii < ie ? ii : 0);       // rows past the grid reload row i0
             v[ii] = grad_load<2>(a, i * d1 + j, c, d, DM);
         }
-        const float hup0 = i0 > 0 ? a.h[((i0 - 1) * d1 + j) * DM + c] : 0.f;
-        const float hleft0 = (jj == 0 && j > 0) ? a.h[(i0 * d1 + j - 1) * DM + c] : 0.f;
-        float up = hup0;
+        up0 = i0 > 0 ? a.h[((i0 - 1) * d1 + j) * DM + c] : 0.f;
+    };
+    auto finish_col = [&](long jj, const GradIn<2> (&v)[TR], float up) {
+        const long j = j0 + jj;
 #pragma unroll
         for (int ii = 0; ii < TR; ++ii) {
             if (ii < ie) {
                 const long i = i0 + ii;
                 const long q = i * d1 + j;
                 const bool has[2] = {i > 0, j > 0};
-                float hl = left[ii];
-                if (jj == 0) hl = ii == 0 ? hleft0 : (j > 0 ? a.h[(q - 1) * DM + c] : 0.f);
-                const float hp[2] = {up, hl};
+                const float hp[2] = {up, left[ii]};
                 grad_finish<2>(a, v[ii], q, c, d, m, active, M, DM, av, dAacc, hp, has);
                 up = v[ii].hv;
                 left[ii] = v[ii].hv;
             }
+        }
+    };
+    GradIn<2> va[TR], vb[TR];
+    float ua = 0.f, ub = 0.f;
+    load_col(0, va, ua);
+    for (long jj = 0; jj < je; jj += 2) {
+        load_col(jj + 1, vb, ub);
+        finish_col(jj, va, ua);
+        if (jj + 1 < je) {
+            load_col(jj + 2, va, ua);
+            finish_col(jj + 1, vb, ub);
         }
     }
     if (active) {
@@ -536,40 +550,53 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
     const long pe = std::min<long>(TP, a.dims[0] - p0), ie = std::min<long>(TR, d1 - i0),
                je = std::min<long>(TW, d2 - j0);
     float above[TW][TP];
+    // The TP points of (row ii, point jj) with the states the walk does not
+    // carry (the plane before the tile; the row above the tile on its first
+    // row; the point left of the tile on its first point), loaded one group
+    // ahead of the group being computed.
+    struct Group {
+        GradIn<3> v[TP];
+        float prev0, up[TP], left[TP];
+    };
+    auto load_grp = [&](long ii, int jj, Group &g) {
+        const long i = i0 + (ii < ie ? ii : 0);           // past the tile: reload row i0
+        const long j = j0 + (jj < je ? jj : 0);
 #pragma unroll
-    for (int jj = 0; jj < TW; ++jj)
-#pragma unroll
-        for (int pp = 0; pp < TP; ++pp) above[jj][pp] = 0.f;
+        for (int pp = 0; pp < TP; ++pp) {
+            const long pl = p0 + (pp < pe ? pp : 0);      // planes past the grid reload plane p0
+            const long q = pl * s0 + i * d2 + j;
+            g.v[pp] = grad_load<3>(a, q, c, d, DM);
+            g.up[pp] = (ii == 0 && i > 0) ? a.h[(q - d2) * DM + c] : 0.f;
+            g.left[pp] = (jj == 0 && j > 0) ? a.h[(q - 1) * DM + c] : 0.f;
+        }
+        g.prev0 = p0 > 0 ? a.h[((p0 - 1) * s0 + i * d2 + j) * DM + c] : 0.f;
+    };
+    Group ga, gb;
+    load_grp(0, 0, ga);
     for (long ii = 0; ii < ie; ++ii) {
         const long i = i0 + ii;
         float left[TP];
 #pragma unroll
-        for (int pp = 0; pp < TP; ++pp) left[pp] = 0.f;
-#pragma unroll
         for (int jj = 0; jj < TW; ++jj) {
+            Group &cur = (jj % 2 == 0) ? ga : gb;
+            Group &nxt = (jj % 2 == 0) ? gb : ga;
+            if (jj + 1 < TW) load_grp(ii, jj + 1, nxt);
+            else load_grp(ii + 1, 0, nxt);
             if (jj < je) {
                 const long j = j0 + jj;
-                GradIn<3> v[TP];
-#pragma unroll
-                for (int pp = 0; pp < TP; ++pp) {
-                    const long pl = p0 + (pp < pe ? pp : 0);   // planes past the grid reload plane p0
-                    v[pp] = grad_load<3>(a, pl * s0 + i * d2 + j, c, d, DM);
-                }
-                float prev = p0 > 0 ? a.h[((p0 - 1) * s0 + i * d2 + j) * DM + c] : 0.f;
+                float prev = cur.prev0;
 #pragma unroll
                 for (int pp = 0; pp < TP; ++pp) {
                     if (pp < pe) {
                         const long pl = p0 + pp;
                         const long q = pl * s0 + i * d2 + j;
                         const bool has[3] = {pl > 0, i > 0, j > 0};
-                        const float hp[3] = {
-                            prev,
-                            ii == 0 ? (i > 0 ? a.h[(q - d2) * DM + c] : 0.f) : above[jj][pp],
-                            jj == 0 ? (j > 0 ? a.h[(q - 1) * DM + c] : 0.f) : left[pp]};
-                        grad_finish<3>(a, v[pp], q, c, d, m, active, M, DM, av, dAacc, hp, has);
-                        prev = v[pp].hv;
-                        left[pp] = v[pp].hv;
-                        above[jj][pp] = v[pp].hv;
+                        const float hp[3] = {prev, ii == 0 ? cur.up[pp] : above[jj][pp],
+                                             jj == 0 ? cur.left[pp] : left[pp]};
+                        grad_finish<3>(a, cur.v[pp], q, c, d, m, active, M, DM, av, dAacc, hp, has);
+                        prev = cur.v[pp].hv;
+                        left[pp] = cur.v[pp].hv;
+                        above[jj][pp] = cur.v[pp].hv;
                     }
                 }
             }
