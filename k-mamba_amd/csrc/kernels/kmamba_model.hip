@@ -7,11 +7,18 @@
 // to the device), the blocks run back to back on device buffers through
 // mamba_block_forward's device-pointer path, and the head product
 // logits[L, V] = h[L, D] . head[D, V] (the reference's gemm_f32,
-// kernels/gemm_f32.c:13-31) runs on the fp32 matrix cores.
+// kernels/gemm_f32.c:13-31) runs on the fp32 matrix cores. The head goes
+// up and the logits come down through the runtime's pinned ring (host memcpy
+// on a thread pool overlapping the DMA); the product runs in chunks of rows
+// so the download of the first rows overlaps the rest of the product.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <string>
+#include <thread>
+#include <vector>
 
 #include "km_device.hpp"
 #include "../km_runtime.hpp"
@@ -120,6 +127,36 @@ static int lm_head_launch(const float *A, const float *B, float *C, long M, long
     KM_HIP_TRY(hipGetLastError());
     return 0;
 }
+
+// Rows of the head product per launch on the download pipeline (each launch
+// reads the whole head; 256 rows keep that re-read small against the product).
+constexpr size_t kHeadChunkRows = 256;
+
+// Events without timing, destroyed with the set.
+class EventSet {
+  public:
+    explicit EventSet(size_t n) : ev_(n, nullptr) {
+        for (auto &e : ev_)
+            if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+                (void)hipGetLastError();
+                e = nullptr;
+                ok_ = false;
+                set_error("kmamba_forward: hipEventCreate failed");
+            }
+    }
+    ~EventSet() {
+        for (auto e : ev_)
+            if (e) (void)hipEventDestroy(e);
+    }
+    EventSet(const EventSet &) = delete;
+    EventSet &operator=(const EventSet &) = delete;
+    bool ok() const { return ok_; }
+    hipEvent_t operator[](size_t i) const { return ev_[i]; }
+
+  private:
+    std::vector<hipEvent_t> ev_;
+    bool ok_ = true;
+};
 
 // 80-byte checkpoint header of version 4 (ref src/kmamba.c:216-229).
 struct CkptHeader {
@@ -365,34 +402,71 @@ int kmamba_forward(KMamba *m, const uint32_t *tokens, float *logits_out) {
     bool ok = pin != nullptr;
     if (ok) {
         (void)hipStreamSynchronize(nullptr);     // no earlier copy still reads the pinned block
-        for (size_t t = 0; t < L; t++) {
-            if (tokens[t] < V) memcpy(pin + t * D, m->embedding + static_cast<size_t>(tokens[t]) * D, D * sizeof(float));
-            else memset(pin + t * D, 0, D * sizeof(float));
-        }
+        const size_t per = 64;   // rows per task of the host thread pool
+        km::host_parallel_for((L + per - 1) / per, [&](size_t i) {
+            for (size_t t = i * per; t < std::min(L, (i + 1) * per); t++) {
+                if (tokens[t] < V) memcpy(pin + t * D, m->embedding + static_cast<size_t>(tokens[t]) * D, D * sizeof(float));
+                else memset(pin + t * D, 0, D * sizeof(float));
+            }
+        });
         ok = hipMemcpyAsync(buf[0], pin, sizeof(float) * L * D, hipMemcpyHostToDevice, nullptr) == hipSuccess &&
              hipStreamSynchronize(nullptr) == hipSuccess;
         if (!ok) km::set_error("kmamba_forward: embedding upload failed");
     }
     km::Staging::unlock();
     if (!ok) return -1;
-    if (hipMemcpy(dhead, m->head, sizeof(float) * D * V, hipMemcpyHostToDevice) != hipSuccess) {
-        km::set_error("kmamba_forward: head upload failed");
+    // The head is host memory the caller owns (and may change between calls),
+    // so it goes up on every call, through the pinned ring, on a helper
+    // thread while this one runs the blocks (which do not touch dhead). The
+    // thread is joined before the head product; errors come back by value
+    // since the error message is per thread.
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        km::set_error("kmamba_forward: no current HIP device");
         return -1;
     }
+    int up_rc = 0;
+    std::string up_err;
+    std::thread up([&] {
+        if (hipSetDevice(dev) != hipSuccess) {
+            up_rc = -1;
+            up_err = "kmamba_forward: hipSetDevice failed on the upload thread";
+            return;
+        }
+        up_rc = km::host_pipe_upload(dhead, m->head, sizeof(float) * D * V, nullptr);
+        if (up_rc != 0) up_err = km_last_error();
+    });
     int cur = 0;
-    for (size_t i = 0; i < m->cfg.n_layers; i++) {
+    bool blocks_ok = true;
+    for (size_t i = 0; blocks_ok && i < m->cfg.n_layers; i++) {
         mamba_block_forward(m->layers[i], buf[cur ^ 1], buf[cur], 1);
-        if (km_last_error()[0]) return -1;
+        blocks_ok = km_last_error()[0] == '\0';
         cur ^= 1;
     }
-    if (km::lm_head_launch(buf[cur], dhead, dlog, static_cast<long>(L), static_cast<long>(D),
-                           static_cast<long>(V), nullptr) != 0)
-        return -1;
-    if (hipMemcpy(logits_out, dlog, sizeof(float) * L * V, hipMemcpyDeviceToHost) != hipSuccess) {
-        km::set_error("kmamba_forward: %s", hipGetErrorString(hipGetLastError()));
+    up.join();
+    if (!blocks_ok) return -1;
+    if (up_rc != 0) {
+        km::set_error("%s", up_err.c_str());
         return -1;
     }
-    return 0;
+    // The head product in chunks of rows, each followed by an event: a piece
+    // of the logits goes down as soon as the chunk holding its last row is
+    // written, while later chunks are computed.
+    const size_t rows = km::kHeadChunkRows;
+    km::EventSet ev((L + rows - 1) / rows);
+    if (!ev.ok()) return -1;
+    for (size_t c = 0; c * rows < L; ++c) {
+        const size_t r0 = c * rows, nr = std::min(rows, L - r0);
+        if (km::lm_head_launch(buf[cur] + r0 * D, dhead, dlog + r0 * V, static_cast<long>(nr),
+                               static_cast<long>(D), static_cast<long>(V), nullptr) != 0)
+            return -1;
+        if (hipEventRecord(ev[c], nullptr) != hipSuccess) {
+            km::set_error("kmamba_forward: hipEventRecord failed");
+            return -1;
+        }
+    }
+    return km::host_pipe_download(logits_out, dlog, sizeof(float) * L * V, sizeof(float) * V,
+                                  [&](size_t end_row) { return ev[(end_row - 1) / rows]; });
 }
 
 }  // extern "C"

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 
 namespace km {
 
@@ -50,6 +51,23 @@ struct Workspace {
 };
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Copies between pageable host memory and device memory through a ring of
+// pinned slots of about kPipeSlotBytes: each slot's DMA, on a non-blocking
+// copy stream, overlaps the host memcpy of the next slot, which is split
+// over a small pool of host threads. Calls from several threads serialise.
+constexpr size_t kPipeSlotBytes = size_t(8) << 20;
+// Host -> device; the copies start after the work already enqueued on
+// `stream`, and the call returns when they have completed.
+int host_pipe_upload(void *dst_dev, const void *src_host, size_t bytes, hipStream_t stream);
+// Device -> host in whole rows of row_bytes; returns when dst_host holds
+// every byte. If `ready` is given, the piece that ends at row r is enqueued
+// once the event ready(r) (nullptr: no wait), recorded when rows [0, r) of
+// src_dev are written, has completed.
+int host_pipe_download(void *dst_host, const void *src_dev, size_t bytes, size_t row_bytes,
+                       const std::function<hipEvent_t(size_t)> &ready);
+// Runs f(0..n-1) over the same host thread pool; returns when all are done.
+void host_parallel_for(size_t n, const std::function<void(size_t)> &f);
 
 // Bump allocator over a reserved staging block.
 struct Carver {

@@ -139,6 +139,39 @@ def test_kmamba_forward_vs_oracle(V, D, N, L, layers, R, tying):
     assert err <= 1e-4, f"condition-scaled logits error {err:.3e}"
 
 
+def test_kmamba_forward_pipelined_copies_many_pieces():
+    # A head (41 MB) and logits (96 MB) that span several slots of the pinned
+    # ring, with ragged last pieces and download pieces (52 rows each) that
+    # straddle the 256-row chunks of the head product. Logits against
+    # float64 products of the oracle's last block output, condition-scaled
+    # as above; a second, smaller model afterwards reuses the ring.
+    V, D, N, L = 40000, 256, 16, 600
+    m = K.kmamba_create(C.byref(O.kmamba_config(V, D, N, L, 2, cls=K.KMambaConfig)))
+    assert m and K.kmamba_init(m, 5) == 0, K.km_last_error()
+    toks = rng_for("kmpipe", V, L).integers(0, V + 2, L).astype(np.uint32)
+    got = model_forward(m, toks)
+    emb, head, blocks = O.model_params(C.cast(m, C.POINTER(O.KMamba)))
+    x = np.zeros((1, L, D), np.float32)
+    ok = toks < V
+    x[0, ok] = emb[toks[ok]]
+    for p in blocks:
+        x = O.mamba3_forward(p, x)
+    want = x[0].astype(np.float64) @ head.astype(np.float64)
+    kappa = np.abs(x[0]).astype(np.float64) @ np.abs(head).astype(np.float64)
+    err = float(np.max(np.abs(got - want) / np.maximum(kappa, 1e-30)))
+    K.kmamba_free(m)
+    assert np.isfinite(got).all()
+    assert err <= 1e-4, f"condition-scaled logits error {err:.3e}"
+    m2 = K.kmamba_create(C.byref(O.kmamba_config(97, 64, 16, 130, 2, cls=K.KMambaConfig)))
+    assert m2 and K.kmamba_init(m2, 6) == 0
+    t2 = rng_for("kmpipe2").integers(0, 97, 130).astype(np.uint32)
+    got2 = model_forward(m2, t2)
+    emb2, head2, blocks2 = O.model_params(C.cast(m2, C.POINTER(O.KMamba)))
+    want2 = O.kmamba_forward(emb2, head2, blocks2, t2)
+    K.kmamba_free(m2)
+    np.testing.assert_allclose(got2, want2, rtol=0, atol=1e-4 * float(np.abs(want2).max()))
+
+
 def test_kmamba_checkpoint_roundtrip_forward(tmp_path):
     # A saved and reloaded model (untied on load) gives the same logits.
     V, D, N, L = 200, 32, 8, 50
