@@ -385,64 +385,119 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_lanes(NdBwdArgs a, long 
 // loads of a group of points before the arithmetic and stores of the first:
 // the compiler does not move a load above a store through pointers it
 // cannot tell apart (dB is read as g and written in place).
+//
+// The tile walks address memory through buffer windows that start at the
+// tile's first accessed point qb (the start of the row, or plane, before
+// the tile), so every offset is 32-bit: the lane's (channel d or
+// channel-state c) in the VGPR offset and the point's, wave-uniform, in the
+// SGPR offset. Lanes that own no output store at an offset with bit 31 set,
+// past the window, which the range check drops.
 template <int ND>
 struct GradIn {
     float xv, dyv, dl[ND], gv, bv, hv;
 };
 
+struct GradWin {
+    __amdgpu_buffer_rsrc_t x, dy, dl, g, B, h, dC, dx, ddl;
+    unsigned sD, sDM, sAx;   // bytes per point of [P, D] and [P, D*M]; bytes per delta axis
+    int vd, vc;              // the lane's byte offsets in a [P, D] and a [P, D*M] row
+    int vcs, vds;            // store offsets: vc / vd, or dropped (inactive lane; dx, ddelta: m != 0)
+};
+
+// Windows over the points [qb, qe) of every tensor (delta and ddelta: all
+// axes from qb on). The host keeps each window below 2 GiB.
 template <int ND>
-__device__ __forceinline__ GradIn<ND> grad_load(const NdBwdArgs &a, long q, long c, long d, long DM) {
+__device__ __forceinline__ GradWin grad_window(const NdBwdArgs &a, long qb, long qe, long c, long d, int m,
+                                               bool active) {
+    constexpr unsigned kDrop = 0x80000000u;
+    const long DM = a.D * a.M, n = qe - qb;
+    GradWin w;
+    w.sD = static_cast<unsigned>(a.D * 4);
+    w.sDM = static_cast<unsigned>(DM * 4);
+    w.sAx = static_cast<unsigned>(a.P * a.D * 4);
+    w.vd = static_cast<int>(d * 4);
+    w.vc = static_cast<int>(c * 4);
+    w.vcs = active ? w.vc : static_cast<int>(kDrop);
+    w.vds = (active && m == 0) ? w.vd : static_cast<int>(kDrop);
+    w.x = make_rsrc(a.x + qb * a.D, n * a.D * 4);
+    w.dy = make_rsrc(a.dy + qb * a.D, n * a.D * 4);
+    w.dx = make_rsrc(a.dx + qb * a.D, n * a.D * 4);
+    w.dl = make_rsrc(a.delta + qb * a.D, ((ND - 1) * a.P + n) * a.D * 4);
+    w.ddl = make_rsrc(a.ddelta + qb * a.D, ((ND - 1) * a.P + n) * a.D * 4);
+    w.g = make_rsrc(a.dB + qb * DM, n * DM * 4);
+    w.B = make_rsrc(a.B + qb * DM, n * DM * 4);
+    w.h = make_rsrc(a.h + qb * DM, n * DM * 4);
+    w.dC = make_rsrc(a.dC + qb * DM, n * DM * 4);
+    return w;
+}
+
+// The state of point qb + r (a predecessor the walk does not carry).
+__device__ __forceinline__ float grad_h(const GradWin &w, long r) {
+    return bio<f32_t>::ld(w.h, w.vc, static_cast<int>(static_cast<unsigned>(r) * w.sDM));
+}
+
+template <int ND>
+__device__ __forceinline__ GradIn<ND> grad_load(const GradWin &w, long r) {
+    const int oD = static_cast<int>(static_cast<unsigned>(r) * w.sD);
+    const int oDM = static_cast<int>(static_cast<unsigned>(r) * w.sDM);
     GradIn<ND> v;
-    v.xv = a.x[q * a.D + d];
-    v.dyv = a.dy[q * a.D + d];
+    v.xv = bio<f32_t>::ld(w.x, w.vd, oD);
+    v.dyv = bio<f32_t>::ld(w.dy, w.vd, oD);
 #pragma unroll
-    for (int ax = 0; ax < ND; ++ax) v.dl[ax] = a.delta[(ax * a.P + q) * a.D + d];
-    const long pc = q * DM + c;
-    v.gv = a.dB[pc];
-    v.bv = a.B[pc];
-    v.hv = a.h[pc];
+    for (int ax = 0; ax < ND; ++ax) v.dl[ax] = bio<f32_t>::ld(w.dl, w.vd, static_cast<int>(ax * w.sAx) + oD);
+    v.gv = bio<f32_t>::ld(w.g, w.vc, oDM);
+    v.bv = bio<f32_t>::ld(w.B, w.vc, oDM);
+    v.hv = bio<f32_t>::ld(w.h, w.vc, oDM);
     return v;
 }
 
-// The arithmetic and stores of one point, with the states of its axis
-// predecessors hp[ax] (used where has[ax]).
-template <int ND>
-__device__ __forceinline__ void grad_finish(const NdBwdArgs &a, const GradIn<ND> &v, long q, long c,
-                                            long d, int m, bool active, long M, long DM,
-                                            const float (&av)[ND], float (&dAacc)[ND],
+// Sum over the MM lanes of a channel (aligned groups of a power of two up
+// to 64), every lane getting the total: xor 1 and xor 2 by quad_perm, the
+// half-row mirror (l ^ 7, which pairs the two quads of 8 lanes), row_ror:8
+// (l ^ 8), then the 16- and 32-lane swaps, all on the VALU.
+template <int MM>
+__device__ __forceinline__ float channel_sum(float v) {
+    if constexpr (MM >= 2) v += dpp<0xB1>(v);
+    if constexpr (MM >= 4) v += dpp<0x4E>(v);
+    if constexpr (MM >= 8) v += dpp<0x141>(v);
+    if constexpr (MM >= 16) v += dpp<0x128>(v);
+    if constexpr (MM >= 32) v = sum_xor16(v);
+    if constexpr (MM >= 64) v = sum_xor32(v);
+    return v;
+}
+
+// The arithmetic and stores of point qb + r, with the states of its axis
+// predecessors hp[ax] (used where has[ax]). avl[ax] = A * log2(e).
+template <int ND, int MM>
+__device__ __forceinline__ void grad_finish(const GradWin &w, const GradIn<ND> &v, long r,
+                                            const float (&av)[ND], const float (&avl)[ND], float (&dAacc)[ND],
                                             const float (&hp)[ND], const bool (&has)[ND]) {
-    float dtb = 0.f;
+    constexpr float kInvNd = 1.0f / ND;
+    float dtb = v.dl[0];
 #pragma unroll
-    for (int ax = 0; ax < ND; ++ax) dtb += v.dl[ax];
-    dtb /= static_cast<float>(ND);
-    const long pc = q * DM + c;
-    float tx = v.gv * dtb * v.bv, tbx = v.gv * v.bv * v.xv, td[ND];
+    for (int ax = 1; ax < ND; ++ax) dtb += v.dl[ax];
+    dtb *= kInvNd;
+    const float gb = v.gv * v.bv;
+    const float tx = channel_sum<MM>(gb * dtb);
+    const float tb = gb * v.xv * kInvNd;
+    float td[ND];
 #pragma unroll
     for (int ax = 0; ax < ND; ++ax) {
-        td[ax] = 0.f;
+        float t = tb;
         if (has[ax]) {
-            const float e = exp2_fast(v.dl[ax] * av[ax] * kLog2e);
-            const float gh = v.gv * e * hp[ax];
-            td[ax] = gh * av[ax];
-            dAacc[ax] += gh * v.dl[ax];
+            const float gh = v.gv * exp2_fast(v.dl[ax] * avl[ax]) * hp[ax];
+            t = fmaf(gh, av[ax], tb);
+            dAacc[ax] = fmaf(gh, v.dl[ax], dAacc[ax]);
         }
+        td[ax] = channel_sum<MM>(t);
     }
-    for (int k = 1; k < M; k <<= 1) {
-        tx += __shfl_xor(tx, k);
-        tbx += __shfl_xor(tbx, k);
+    const int oD = static_cast<int>(static_cast<unsigned>(r) * w.sD);
+    const int oDM = static_cast<int>(static_cast<unsigned>(r) * w.sDM);
+    bio<f32_t>::st(w.dC, w.vcs, oDM, v.dyv * v.hv);
+    bio<f32_t>::st(w.g, w.vcs, oDM, v.gv * dtb * v.xv);
+    bio<f32_t>::st(w.dx, w.vds, oD, tx);
 #pragma unroll
-        for (int ax = 0; ax < ND; ++ax) td[ax] += __shfl_xor(td[ax], k);
-    }
-    if (active) {
-        a.dC[pc] = v.dyv * v.hv;
-        a.dB[pc] = v.gv * dtb * v.xv;
-        if (m == 0) {
-            a.dx[q * a.D + d] = tx;
-#pragma unroll
-            for (int ax = 0; ax < ND; ++ax)
-                a.ddelta[(ax * a.P + q) * a.D + d] = tbx / static_cast<float>(ND) + td[ax];
-        }
-    }
+    for (int ax = 0; ax < ND; ++ax) bio<f32_t>::st(w.ddl, w.vds, static_cast<int>(ax * w.sAx) + oD, td[ax]);
 }
 
 // The gradient pass over tiles of a 2D grid: workgroup x takes tile x (TR
@@ -450,41 +505,44 @@ __device__ __forceinline__ void grad_finish(const NdBwdArgs &a, const GradIn<ND>
 // state of the point above is the previous step's and the one to the left
 // is the previous column's (kept per row): only the tile's first row and
 // first column read a predecessor's state from memory. A column's TR points
-// load together before any of them computes.
-template <int TR, int TW>
+// load one column ahead of the arithmetic.
+template <int TR, int TW, int MM>
 __global__ void __launch_bounds__(256) nd_adjoint_grads_tile2d(NdBwdArgs a) {
-    const long M = a.M, DM = a.D * M;
-    const long c0 = static_cast<long>(blockIdx.y) * 256 + threadIdx.x;
+    const long DM = a.D * MM;
+    const long tile = blockIdx.y;
+    const long c0 = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
     const bool active = c0 < DM;
     const long c = active ? c0 : 0;
-    const long d = c / M;
-    const int m = static_cast<int>(c - d * M);
+    const long d = c / MM;
+    const int m = static_cast<int>(c - d * MM);
     const long d1 = a.dims[1];
     const long nt1 = (d1 + TW - 1) / TW;
-    const long i0 = (static_cast<long>(blockIdx.x) / nt1) * TR, j0 = (static_cast<long>(blockIdx.x) % nt1) * TW;
+    const long i0 = (tile / nt1) * TR, j0 = (tile % nt1) * TW;
     const long ie = std::min<long>(TR, a.dims[0] - i0), je = std::min<long>(TW, d1 - j0);
-    float av[2], dAacc[2];
+    // Window: from the start of the row above the tile to the end of its last row.
+    const long qb = (i0 > 0 ? i0 - 1 : 0) * d1, qe = (i0 + ie) * d1;
+    const GradWin w = grad_window<2>(a, qb, qe, c, d, m, active);
+    float av[2], avl[2], dAacc[2];
 #pragma unroll
     for (int ax = 0; ax < 2; ++ax) {
         av[ax] = a.A[ax * DM + c];
+        avl[ax] = av[ax] * kLog2e;
         dAacc[ax] = 0.f;
     }
-    // The left neighbours of the tile's first column, and each column's
-    // points with the state above its first row, loaded one column ahead.
     float left[TR];
 #pragma unroll
     for (int ii = 0; ii < TR; ++ii) {
         const long i = i0 + (ii < ie ? ii : 0);
-        left[ii] = j0 > 0 ? a.h[(i * d1 + j0 - 1) * DM + c] : 0.f;
+        left[ii] = j0 > 0 ? grad_h(w, i * d1 + j0 - 1 - qb) : 0.f;
     }
     auto load_col = [&](long jj, GradIn<2> (&v)[TR], float &up0) {
         const long j = j0 + (jj < je ? jj : 0);           // past the tile: reload column j0
 #pragma unroll
         for (int ii = 0; ii < TR; ++ii) {
             const long i = i0 + (ii < ie ? ii : 0);       // rows past the grid reload row i0
-            v[ii] = grad_load<2>(a, i * d1 + j, c, d, DM);
+            v[ii] = grad_load<2>(w, i * d1 + j - qb);
         }
-        up0 = i0 > 0 ? a.h[((i0 - 1) * d1 + j) * DM + c] : 0.f;
+        up0 = i0 > 0 ? grad_h(w, (i0 - 1) * d1 + j - qb) : 0.f;
     };
     auto finish_col = [&](long jj, const GradIn<2> (&v)[TR], float up) {
         const long j = j0 + jj;
@@ -492,10 +550,9 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile2d(NdBwdArgs a) {
         for (int ii = 0; ii < TR; ++ii) {
             if (ii < ie) {
                 const long i = i0 + ii;
-                const long q = i * d1 + j;
                 const bool has[2] = {i > 0, j > 0};
                 const float hp[2] = {up, left[ii]};
-                grad_finish<2>(a, v[ii], q, c, d, m, active, M, DM, av, dAacc, hp, has);
+                grad_finish<2, MM>(w, v[ii], i * d1 + j - qb, av, avl, dAacc, hp, has);
                 up = v[ii].hv;
                 left[ii] = v[ii].hv;
             }
@@ -514,7 +571,7 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile2d(NdBwdArgs a) {
     }
     if (active) {
 #pragma unroll
-        for (int ax = 0; ax < 2; ++ax) a.part[(static_cast<long>(blockIdx.x) * 2 + ax) * DM + c] = dAacc[ax];
+        for (int ax = 0; ax < 2; ++ax) a.part[(tile * 2 + ax) * DM + c] = dAacc[ax];
     }
 }
 
@@ -524,31 +581,36 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile2d(NdBwdArgs a) {
 // (row, point), so the plane predecessor is the previous step's state, the
 // point to the left the previous point's (per plane) and the row above the
 // previous row's (per point and plane, TW x TP registers). The TP points of
-// a (row, point) load together.
-template <int TP, int TR, int TW, int TPW>
+// a (row, point) load one group ahead of the arithmetic.
+template <int TP, int TR, int TW, int TPW, int MM>
 __global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
-    const long M = a.M, DM = a.D * M;
-    const long c0 = static_cast<long>(blockIdx.y) * 256 + threadIdx.x;
+    const long DM = a.D * MM;
+    const long blk = blockIdx.y;    // tiles [blk * TPW, +TPW)
+    const long c0 = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
     const bool active = c0 < DM;
     const long c = active ? c0 : 0;
-    const long d = c / M;
-    const int m = static_cast<int>(c - d * M);
+    const long d = c / MM;
+    const int m = static_cast<int>(c - d * MM);
     const long d1 = a.dims[1], d2 = a.dims[2];
     const long nt1 = (d1 + TR - 1) / TR, nt2 = (d2 + TW - 1) / TW;
     const long ntiles = ((a.dims[0] + TP - 1) / TP) * nt1 * nt2;
     const long s0 = d1 * d2;
-    float av[3], dAacc[3];
+    float av[3], avl[3], dAacc[3];
 #pragma unroll
     for (int ax = 0; ax < 3; ++ax) {
         av[ax] = a.A[ax * DM + c];
+        avl[ax] = av[ax] * kLog2e;
         dAacc[ax] = 0.f;
     }
-    const long t1 = std::min<long>(ntiles, (static_cast<long>(blockIdx.x) + 1) * TPW);
+    const long t1 = std::min<long>(ntiles, (blk + 1) * TPW);
 #pragma unroll 1
-    for (long t = static_cast<long>(blockIdx.x) * TPW; t < t1; ++t) {
+    for (long t = blk * TPW; t < t1; ++t) {
     const long p0 = (t / (nt1 * nt2)) * TP, i0 = ((t / nt2) % nt1) * TR, j0 = (t % nt2) * TW;
     const long pe = std::min<long>(TP, a.dims[0] - p0), ie = std::min<long>(TR, d1 - i0),
                je = std::min<long>(TW, d2 - j0);
+    // Window: from the start of the plane before the tile to the end of its last plane.
+    const long qb = (p0 > 0 ? p0 - 1 : 0) * s0, qe = (p0 + pe) * s0;
+    const GradWin w = grad_window<3>(a, qb, qe, c, d, m, active);
     float above[TW][TP];
     // The TP points of (row ii, point jj) with the states the walk does not
     // carry (the plane before the tile; the row above the tile on its first
@@ -564,12 +626,12 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
 #pragma unroll
         for (int pp = 0; pp < TP; ++pp) {
             const long pl = p0 + (pp < pe ? pp : 0);      // planes past the grid reload plane p0
-            const long q = pl * s0 + i * d2 + j;
-            g.v[pp] = grad_load<3>(a, q, c, d, DM);
-            g.up[pp] = (ii == 0 && i > 0) ? a.h[(q - d2) * DM + c] : 0.f;
-            g.left[pp] = (jj == 0 && j > 0) ? a.h[(q - 1) * DM + c] : 0.f;
+            const long r = pl * s0 + i * d2 + j - qb;
+            g.v[pp] = grad_load<3>(w, r);
+            g.up[pp] = (ii == 0 && i > 0) ? grad_h(w, r - d2) : 0.f;
+            g.left[pp] = (jj == 0 && j > 0) ? grad_h(w, r - 1) : 0.f;
         }
-        g.prev0 = p0 > 0 ? a.h[((p0 - 1) * s0 + i * d2 + j) * DM + c] : 0.f;
+        g.prev0 = p0 > 0 ? grad_h(w, (p0 - 1) * s0 + i * d2 + j - qb) : 0.f;
     };
     Group ga, gb;
     load_grp(0, 0, ga);
@@ -589,11 +651,10 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
                 for (int pp = 0; pp < TP; ++pp) {
                     if (pp < pe) {
                         const long pl = p0 + pp;
-                        const long q = pl * s0 + i * d2 + j;
                         const bool has[3] = {pl > 0, i > 0, j > 0};
                         const float hp[3] = {prev, ii == 0 ? cur.up[pp] : above[jj][pp],
                                              jj == 0 ? cur.left[pp] : left[pp]};
-                        grad_finish<3>(a, cur.v[pp], q, c, d, m, active, M, DM, av, dAacc, hp, has);
+                        grad_finish<3, MM>(w, cur.v[pp], pl * s0 + i * d2 + j - qb, av, avl, dAacc, hp, has);
                         prev = cur.v[pp].hv;
                         left[pp] = cur.v[pp].hv;
                         above[jj][pp] = cur.v[pp].hv;
@@ -605,7 +666,7 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
     }
     if (active) {
 #pragma unroll
-        for (int ax = 0; ax < 3; ++ax) a.part[(static_cast<long>(blockIdx.x) * 3 + ax) * DM + c] = dAacc[ax];
+        for (int ax = 0; ax < 3; ++ax) a.part[(blk * 3 + ax) * DM + c] = dAacc[ax];
     }
 }
 
@@ -684,13 +745,27 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
     // tile), carrying the predecessors' states in registers.
     s.gtiles = s.lanes && (s.nd == 2 || s.nd == 3);
     if (s.gtiles) {
+        // Their buffer windows (a tile's planes / rows plus the one before,
+        // and delta's axes before them) must stay below 2 GiB.
+        const long lead = s.nd == 2 ? kGradTR2 + 1 : kGradTP3 + 1;
+        long row = 1;
+        for (long ax = 1; ax < s.nd; ++ax) row *= a->dims[ax];
+        const long n = std::min<long>(s.P, lead * row);
+        const double win = std::max(static_cast<double>(n) * s.D * s.M * 4,
+                                    (static_cast<double>(s.nd - 1) * s.P + n) * s.D * 4);
+        s.gtiles = win < 2147483000.0;
+    }
+    if (s.gtiles) {
         const long t2[2] = {kGradTR2, kGradTW2}, t3[3] = {kGradTP3, kGradTR3, kGradTW3};
         long nt = 1;
         for (long ax = 0; ax < s.nd; ++ax) {
             const long te = s.nd == 2 ? t2[ax] : t3[ax];
             nt *= (a->dims[ax] + te - 1) / te;
         }
-        s.nbx = s.nd == 2 ? nt : (nt + kGradTPW3 - 1) / kGradTPW3;
+        const long nb = s.nd == 2 ? nt : (nt + kGradTPW3 - 1) / kGradTPW3;
+        // Tiles go on the grid's y dimension.
+        if (nb <= 65535) s.nbx = nb;
+        else s.gtiles = false;
     }
     s.offs_bytes = align_up(sizeof(long) * s.P, 256);
     s.nbr_bytes = align_up(sizeof(uint16_t) * s.P, 256);
@@ -706,6 +781,36 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
 }
 
 constexpr int kAdjTR = 16, kAdjTW = 8;
+
+// The tiled gradient pass for the M lanes of a channel (a power of two up
+// to 64, a compile-time constant of the kernels' lane sums).
+template <int ND, int MM>
+static void grads_tile_go(const NdBwdArgs &args, const NdBwdShape &s, hipStream_t st) {
+    // The channel blocks of a tile are consecutive workgroups: they read the
+    // same points' rows (all of each row between them) at about the same
+    // time, and with 8 (or 16) blocks, block k runs on XCD k % 8 for every
+    // tile, next to the neighbouring tiles' states it reads.
+    const dim3 grid(static_cast<unsigned>(s.nby), static_cast<unsigned>(s.nbx));
+    if constexpr (ND == 2)
+        hipLaunchKernelGGL((nd_adjoint_grads_tile2d<kGradTR2, kGradTW2, MM>), grid, dim3(256), 0, st, args);
+    else
+        hipLaunchKernelGGL((nd_adjoint_grads_tile3d<kGradTP3, kGradTR3, kGradTW3, kGradTPW3, MM>), grid, dim3(256),
+                           0, st, args);
+}
+template <int ND>
+static void grads_tile_launch(const NdBwdArgs &args, const NdBwdShape &s, hipStream_t st) {
+    if constexpr (ND == 2 || ND == 3) {
+        switch (s.M) {
+        case 1: grads_tile_go<ND, 1>(args, s, st); break;
+        case 2: grads_tile_go<ND, 2>(args, s, st); break;
+        case 4: grads_tile_go<ND, 4>(args, s, st); break;
+        case 8: grads_tile_go<ND, 8>(args, s, st); break;
+        case 16: grads_tile_go<ND, 16>(args, s, st); break;
+        case 32: grads_tile_go<ND, 32>(args, s, st); break;
+        default: grads_tile_go<ND, 64>(args, s, st); break;
+        }
+    }
+}
 
 template <int ND>
 static void nd_bwd_launch(const NdBwdArgs &args, const NdBwdShape &s, const KMWavefrontPlan *plan,
@@ -742,14 +847,8 @@ static void nd_bwd_launch(const NdBwdArgs &args, const NdBwdShape &s, const KMWa
         }
     }
     }
-    if (s.gtiles && ND == 2) {
-        hipLaunchKernelGGL((nd_adjoint_grads_tile2d<kGradTR2, kGradTW2>),
-                           dim3(static_cast<unsigned>(s.nbx), static_cast<unsigned>(s.nby)), dim3(256), 0, st,
-                           args);
-    } else if (s.gtiles && ND == 3) {
-        hipLaunchKernelGGL((nd_adjoint_grads_tile3d<kGradTP3, kGradTR3, kGradTW3, kGradTPW3>),
-                           dim3(static_cast<unsigned>(s.nbx), static_cast<unsigned>(s.nby)), dim3(256), 0, st,
-                           args);
+    if (s.gtiles && (ND == 2 || ND == 3)) {
+        grads_tile_launch<ND>(args, s, st);
     } else if (s.lanes) {
         hipLaunchKernelGGL(nd_adjoint_grads_lanes<ND>,
                            dim3(static_cast<unsigned>(s.nbx), static_cast<unsigned>(s.nby)), dim3(256), 0, st,
