@@ -327,13 +327,29 @@ def bench_mamba3(torch, K, steps, warmup, Bsz=8, L=2048, dim=1024, N=16, R=1):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t) * 1e3 / steps
     err = K.km_last_error()
+    # The same call on host (pageable) arrays, as the reference's callers
+    # pass them: 64 MB in and out per call over PCIe.
+    import numpy as np
+    xh = x.cpu().numpy()
+    oh = np.empty_like(xh)
+    fh = lambda: K.mamba_block_forward(blk, oh.ctypes.data, xh.ctypes.data, Bsz)  # noqa: E731
+    for _ in range(max(1, warmup // 4)):
+        fh()
+    t = time.perf_counter()
+    hsteps = max(1, steps // 4)
+    for _ in range(hsteps):
+        fh()
+    host_ms = (time.perf_counter() - t) * 1e3 / hsteps
+    err = err or K.km_last_error()
     K.mamba_block_free(blk)
     if err:
         raise RuntimeError(err)
     T = Bsz * L
     return {"ms": round(ms, 4), "tokens_per_s": T / (ms * 1e-3),
+            "host_io_ms": round(host_ms, 4), "host_io_tokens_per_s": T / (host_ms * 1e-3),
+            "host_io_bytes_per_call": 2 * xh.nbytes,
             "config": {"B": Bsz, "L": L, "dim": dim, "state_size": N, "mimo_rank": R,
-                       "io": "device pointers"}}
+                       "io": "device pointers (ms); host pageable arrays (host_io_ms)"}}
 
 
 def bench_scannd(torch, K, stream, dims, D, M, steps, warmup):

@@ -1183,7 +1183,7 @@ static int convnd_host(ConvNDParams *p, bool fwd, bool bwd, const char *who) {
             for (auto &b : bufs) {
                 if (!b.user) continue;
                 b.dev = c.take<char>(b.bytes);
-                if (b.in && hipMemcpy(b.dev, b.user, b.bytes, hipMemcpyHostToDevice) != hipSuccess) ok = false;
+                if (b.in && km::copy_h2d(b.dev, b.user, b.bytes) != hipSuccess) ok = false;
             }
             if (!ok) {
                 set_error("%s: host-to-device copy failed", who);
@@ -1209,7 +1209,7 @@ static int convnd_host(ConvNDParams *p, bool fwd, bool bwd, const char *who) {
         if (!all_dev) {
             for (int i = 0; i < NB; ++i) {
                 if (!bufs[i].user || !bufs[i].out) continue;
-                if (hipMemcpy(bufs[i].user, bufs[i].dev, bufs[i].bytes, hipMemcpyDeviceToHost) != hipSuccess)
+                if (km::copy_d2h(bufs[i].user, bufs[i].dev, bufs[i].bytes) != hipSuccess)
                     ok = false;
             }
         }

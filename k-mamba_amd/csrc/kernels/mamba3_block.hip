@@ -608,7 +608,7 @@ void mamba_block_forward(MambaBlock *b, float *output, const float *input, size_
         put(th, b->theta, TS);
         bool ok = hipMemcpyAsync(dpar, hp, sizeof(float) * nP, hipMemcpyHostToDevice, nullptr) == hipSuccess;
         if (!dev_io)
-            ok = ok && hipMemcpyAsync(x, input, sizeof(float) * T * D, hipMemcpyHostToDevice, nullptr) == hipSuccess;
+            ok = ok && km::copy_h2d(x, input, sizeof(float) * T * D) == hipSuccess;
         if (!ok) {
             km::set_error("mamba_block_forward: host-to-device copy failed");
             break;
@@ -629,7 +629,7 @@ void mamba_block_forward(MambaBlock *b, float *output, const float *input, size_
             km::set_error("mamba_block_forward: %s", hipGetErrorString(hipGetLastError()));
             break;
         }
-        if (!dev_io && hipMemcpy(output, o, sizeof(float) * T * D, hipMemcpyDeviceToHost) != hipSuccess)
+        if (!dev_io && km::copy_d2h(output, o, sizeof(float) * T * D) != hipSuccess)
             km::set_error("mamba_block_forward: device-to-host copy failed");
     } while (false);
     km::Staging::unlock();

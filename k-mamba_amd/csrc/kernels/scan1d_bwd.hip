@@ -997,7 +997,7 @@ struct StagedCall {
             if (!bufs[i].user) continue;
             bufs[i].dev = c.take<char>(bufs[i].bytes);
             if (!bufs[i].out &&
-                hipMemcpy(bufs[i].dev, bufs[i].user, bufs[i].bytes, hipMemcpyHostToDevice) != hipSuccess) {
+                km::copy_h2d(bufs[i].dev, bufs[i].user, bufs[i].bytes) != hipSuccess) {
                 set_error("%s: host-to-device copy failed", who);
                 return false;
             }
@@ -1012,8 +1012,7 @@ struct StagedCall {
         if (all_dev) return true;
         for (int i = 0; i < n; ++i) {
             if (!bufs[i].user || !bufs[i].out) continue;
-            if (hipMemcpy(const_cast<void *>(bufs[i].user), bufs[i].dev, bufs[i].bytes,
-                          hipMemcpyDeviceToHost) != hipSuccess) {
+            if (copy_d2h(const_cast<void *>(bufs[i].user), bufs[i].dev, bufs[i].bytes) != hipSuccess) {
                 set_error("%s: device-to-host copy failed", who);
                 return false;
             }

@@ -956,19 +956,19 @@ void scan1d(ScanParams *p) {
         float *x = c.take<float>(nLD), *dt = c.take<float>(nLD), *y = c.take<float>(nLD);
         float *A = c.take<float>(nDM), *h = c.take<float>(nDM);
         float *Bm = c.take<float>(nLDM), *Cm = c.take<float>(nLDM);
-        bool ok = hipMemcpy(x, p->x, nLD * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                  hipMemcpy(dt, p->delta, nLD * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                  hipMemcpy(A, p->A, nDM * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                  hipMemcpy(h, p->h, nDM * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                  hipMemcpy(Bm, p->B, nLDM * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                  hipMemcpy(Cm, p->C, nLDM * 4, hipMemcpyHostToDevice) == hipSuccess;
+        bool ok = km::copy_h2d(x, p->x, nLD * 4) == hipSuccess &&
+                  km::copy_h2d(dt, p->delta, nLD * 4) == hipSuccess &&
+                  km::copy_h2d(A, p->A, nDM * 4) == hipSuccess &&
+                  km::copy_h2d(h, p->h, nDM * 4) == hipSuccess &&
+                  km::copy_h2d(Bm, p->B, nLDM * 4) == hipSuccess &&
+                  km::copy_h2d(Cm, p->C, nLDM * 4) == hipSuccess;
         if (!ok) {
             km::set_error("scan1d: host-to-device copy failed");
         } else {
             a.x = x; a.delta = dt; a.A = A; a.Bm = Bm; a.Cm = Cm; a.y = y; a.h0 = h; a.h_final = h;
             if (km::scan1d_fwd_launch(&a, nullptr) == 0) {
-                if (hipMemcpy(p->y, y, nLD * 4, hipMemcpyDeviceToHost) != hipSuccess ||
-                    hipMemcpy(p->h, h, nDM * 4, hipMemcpyDeviceToHost) != hipSuccess)
+                if (km::copy_d2h(p->y, y, nLD * 4) != hipSuccess ||
+                    km::copy_d2h(p->h, h, nDM * 4) != hipSuccess)
                     km::set_error("scan1d: device-to-host copy failed");
             }
         }

@@ -1134,7 +1134,7 @@ static int scannd_device(const float *x, const float *const *A, const float *con
     }
     if (!status) return 0;
     unsigned failed = 0;
-    if (hipMemcpy(&failed, status, sizeof failed, hipMemcpyDeviceToHost) != hipSuccess) {
+    if (km::copy_d2h(&failed, status, sizeof failed) != hipSuccess) {
         set_error("scannd: status read failed");
         return -1;
     }
@@ -1291,11 +1291,11 @@ static int scannd_host(const ScanNDParams *p, bool scan1d_semantics) {
                c.take<float>(ndt), c.take<float>(nh), c.take<float>(nx)};
     float *th = nth ? c.take<float>(nth) : nullptr;
     float *lam = nlam ? c.take<float>(nlam) : nullptr;
-    const bool ok = hipMemcpy(st.x, p->x, nx * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                    hipMemcpy(st.A, p->A, nA * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                    hipMemcpy(st.B, p->B, nB * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                    hipMemcpy(st.C, p->C, nB * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                    hipMemcpy(st.dt, p->delta, ndt * 4, hipMemcpyHostToDevice) == hipSuccess &&
+    const bool ok = km::copy_h2d(st.x, p->x, nx * 4) == hipSuccess &&
+                    km::copy_h2d(st.A, p->A, nA * 4) == hipSuccess &&
+                    km::copy_h2d(st.B, p->B, nB * 4) == hipSuccess &&
+                    km::copy_h2d(st.C, p->C, nB * 4) == hipSuccess &&
+                    km::copy_h2d(st.dt, p->delta, ndt * 4) == hipSuccess &&
                     (!th || D / 2 == 0 || hipMemcpy(th, p->theta, (D / 2) * 4, hipMemcpyDefault) == hipSuccess) &&
                     (!lam || hipMemcpy(lam, p->lambda, nlam * 4, hipMemcpyDefault) == hipSuccess);
     if (!ok) {
@@ -1306,8 +1306,8 @@ static int scannd_host(const ScanNDParams *p, bool scan1d_semantics) {
         q.x = st.x; q.A = st.A; q.B = st.B; q.C = st.C; q.delta = st.dt; q.h = st.h; q.y = st.y;
         q.theta = th; q.lambda = lam;
         rc = scannd_device_params(&q, nullptr, true);
-        if (rc == 0 && (hipMemcpy(p->h, st.h, nh * 4, hipMemcpyDeviceToHost) != hipSuccess ||
-                        hipMemcpy(p->y, st.y, nx * 4, hipMemcpyDeviceToHost) != hipSuccess)) {
+        if (rc == 0 && (km::copy_d2h(p->h, st.h, nh * 4) != hipSuccess ||
+                        km::copy_d2h(p->y, st.y, nx * 4) != hipSuccess)) {
             set_error("scannd: device-to-host copy failed");
             rc = -1;
         }
@@ -1407,20 +1407,20 @@ void scan2d(Scan2DParams *p) {
         float *x = c.take<float>(nx), *A1 = c.take<float>(nA), *A2 = c.take<float>(nA);
         float *B = c.take<float>(nB), *C = c.take<float>(nB), *d1 = c.take<float>(nx);
         float *d2 = c.take<float>(nx), *h = c.take<float>(nB), *y = c.take<float>(nx);
-        const bool ok = hipMemcpy(x, p->x, nx * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                        hipMemcpy(A1, p->A1, nA * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                        hipMemcpy(A2, p->A2, nA * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                        hipMemcpy(B, p->B, nB * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                        hipMemcpy(C, p->C, nB * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                        hipMemcpy(d1, p->delta1, nx * 4, hipMemcpyHostToDevice) == hipSuccess &&
-                        hipMemcpy(d2, p->delta2, nx * 4, hipMemcpyHostToDevice) == hipSuccess;
+        const bool ok = km::copy_h2d(x, p->x, nx * 4) == hipSuccess &&
+                        km::copy_h2d(A1, p->A1, nA * 4) == hipSuccess &&
+                        km::copy_h2d(A2, p->A2, nA * 4) == hipSuccess &&
+                        km::copy_h2d(B, p->B, nB * 4) == hipSuccess &&
+                        km::copy_h2d(C, p->C, nB * 4) == hipSuccess &&
+                        km::copy_h2d(d1, p->delta1, nx * 4) == hipSuccess &&
+                        km::copy_h2d(d2, p->delta2, nx * 4) == hipSuccess;
         if (!ok) {
             km::set_error("scan2d: host-to-device copy failed");
         } else {
             const float *A[2] = {A1, A2}, *dt[2] = {d1, d2};
             if (km::scannd_device(x, A, dt, B, C, h, y, dims, 2, D, M, nullptr, true) == 0) {
-                if (hipMemcpy(p->h, h, nB * 4, hipMemcpyDeviceToHost) != hipSuccess ||
-                    hipMemcpy(p->y, y, nx * 4, hipMemcpyDeviceToHost) != hipSuccess)
+                if (km::copy_d2h(p->h, h, nB * 4) != hipSuccess ||
+                    km::copy_d2h(p->y, y, nx * 4) != hipSuccess)
                     km::set_error("scan2d: device-to-host copy failed");
             }
         }

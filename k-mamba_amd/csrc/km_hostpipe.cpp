@@ -225,4 +225,33 @@ int host_pipe_download(void *dst_host, const void *src_dev, size_t bytes, size_t
     return 0;
 }
 
+namespace {
+// Pageable host memory: what hipMemcpy would stage through its own buffers.
+bool pageable(const void *p) {
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();   // unregistered host memory reports an error
+        return true;
+    }
+    return attr.type != hipMemoryTypeHost && attr.type != hipMemoryTypeDevice &&
+           attr.type != hipMemoryTypeManaged;
+}
+constexpr size_t kPipeMinBytes = size_t(4) << 20;   // below: one hipMemcpy
+}  // namespace
+
+hipError_t copy_h2d(void *dst_dev, const void *src_host, size_t bytes) {
+    if (bytes < kPipeMinBytes || !pageable(src_host))
+        return hipMemcpy(dst_dev, src_host, bytes, hipMemcpyHostToDevice);
+    return host_pipe_upload(dst_dev, src_host, bytes, nullptr) == 0 ? hipSuccess : hipErrorUnknown;
+}
+
+hipError_t copy_d2h(void *dst_host, const void *src_dev, size_t bytes) {
+    if (bytes < kPipeMinBytes || !pageable(dst_host))
+        return hipMemcpy(dst_host, src_dev, bytes, hipMemcpyDeviceToHost);
+    // As hipMemcpy: after the work already enqueued on the null stream.
+    const hipError_t e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) return e;
+    return host_pipe_download(dst_host, src_dev, bytes, bytes, nullptr) == 0 ? hipSuccess : hipErrorUnknown;
+}
+
 }  // namespace km

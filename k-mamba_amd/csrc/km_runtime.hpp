@@ -66,6 +66,12 @@ int host_pipe_upload(void *dst_dev, const void *src_host, size_t bytes, hipStrea
 // src_dev are written, has completed.
 int host_pipe_download(void *dst_host, const void *src_dev, size_t bytes, size_t row_bytes,
                        const std::function<hipEvent_t(size_t)> &ready);
+// Synchronous copies of the host-pointer entry points, ordered like
+// hipMemcpy after the work on the null stream: pageable buffers of 4 MB or
+// more go through the pinned ring, the rest (and pinned memory) through
+// hipMemcpy.
+hipError_t copy_h2d(void *dst_dev, const void *src_host, size_t bytes);
+hipError_t copy_d2h(void *dst_host, const void *src_dev, size_t bytes);
 // Runs f(0..n-1) over the same host thread pool; returns when all are done.
 void host_parallel_for(size_t n, const std::function<void(size_t)> &f);
 
