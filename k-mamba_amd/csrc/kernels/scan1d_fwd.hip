@@ -407,6 +407,8 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             }
         }
         __syncthreads();
+        // The segment-map pass (DSUM) needs only the outgoing carry: no replay.
+        if constexpr (DSUM) return;
 #pragma unroll
         for (int j = 0; j < NPL; ++j) h[j] = pin[w][j][lane];
 
@@ -498,6 +500,15 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
         if (w == 0 && dvalid && ns == 0) p.dsum_out[b * Dm + d] = dtot;
     }
 
+    if constexpr (DSUM) {
+        // The segment's local end state is the last super-chunk's outgoing
+        // carry (the segment-map pass runs without the clamp).
+        if (w == W - 1 && p.hfin && dvalid) {
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) p.hfin[(b * Dm + d) * N + NS * j + ns] = carry[nit & 1][j][lane];
+        }
+        return;
+    }
     // A NaN state stays NaN through every later step (e * NaN + bu), so a
     // NaN anywhere in the sequence shows in the final state of the wave that
     // ran the last steps; finite excursions past 1000 are in hmax.
