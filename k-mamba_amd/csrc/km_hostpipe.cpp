@@ -251,7 +251,8 @@ hipError_t copy_d2h(void *dst_host, const void *src_dev, size_t bytes) {
     // As hipMemcpy: after the work already enqueued on the null stream.
     const hipError_t e = hipStreamSynchronize(nullptr);
     if (e != hipSuccess) return e;
-    return host_pipe_download(dst_host, src_dev, bytes, bytes, nullptr) == 0 ? hipSuccess : hipErrorUnknown;
+    // Rows of one byte: pieces of one ring slot each.
+    return host_pipe_download(dst_host, src_dev, bytes, 1, nullptr) == 0 ? hipSuccess : hipErrorUnknown;
 }
 
 }  // namespace km
