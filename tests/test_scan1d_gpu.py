@@ -265,9 +265,12 @@ def _api_inputs(L, D, M):
     return x, A, B, Cm, dt
 
 
-@pytest.mark.parametrize("L,D,M", [(4, 8, 1), (16, 16, 2), (64, 32, 1), (128, 48, 16)])
+@pytest.mark.parametrize("L,D,M", [(4, 8, 1), (16, 16, 2), (64, 32, 1), (128, 48, 16),
+                                   (2100, 1024, 16)])
 def test_scan1d_host_pointer_api(L, D, M):
-    # scan1d(ScanParams*) on host memory, running [D, M] state in/out.
+    # scan1d(ScanParams*) on host memory, running [D, M] state in/out. The
+    # last shape's pageable buffers (x, y 8.6 MB; B, C 138 MB) go through the
+    # library's pinned ring in several slot-sized pieces, the last ragged.
     x, A, B, Cm, dt = _api_inputs(L, D, M)
     h0 = rng_for("h0", L, D, M).uniform(-1, 1, (D, M)).astype(np.float32)
     yr, hr = O.scan1d(x, A, B, Cm, dt, h0)
