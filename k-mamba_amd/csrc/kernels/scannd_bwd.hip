@@ -36,6 +36,7 @@ namespace km {
 
 constexpr int kNdBwdMaxAcc = 64;   // ndims * M: per-thread dA slots in LDS (64 KB)
 constexpr int kAdj3P = 4, kAdj3R = 4, kAdj3W = 8;   // 3D adjoint tiles (axis 0, 1, 2)
+constexpr int kAdjTR = 16, kAdjTW = 8;              // 2D adjoint tiles (rows, points)
 
 struct NdBwdArgs {
     const float *x, *A, *B, *C, *delta, *h, *dy;
@@ -83,6 +84,45 @@ __global__ void __launch_bounds__(256) nd_adjoint_level(NdBwdArgs a, long s0) {
     a.dB[q * DM + c] = g;
 }
 
+// Buffer windows of one adjoint tile: every tensor's resource starts at the
+// tile's first point qb, so offsets are 32-bit, the point's wave-uniform
+// (SGPR offset) and the lane's in the VGPR offset. Windows run to the end of
+// the tile's successor row (2D) or plane (3D); delta's covers all axes from
+// qb on. The host keeps each window below 2 GiB.
+struct AdjWin {
+    __amdgpu_buffer_rsrc_t dy, C, dl, g;
+    unsigned sD, sDM, sAx;   // bytes per point of [P, D] and [P, D*M]; bytes per delta axis
+    int vd, vc;
+};
+template <int ND>
+__device__ __forceinline__ AdjWin adj_window(const NdBwdArgs &a, long qb, long qe, long c, long d) {
+    const long DM = a.D * a.M, n = qe - qb;
+    AdjWin w;
+    w.sD = static_cast<unsigned>(a.D * 4);
+    w.sDM = static_cast<unsigned>(DM * 4);
+    w.sAx = static_cast<unsigned>(a.P * a.D * 4);
+    w.vd = static_cast<int>(d * 4);
+    w.vc = static_cast<int>(c * 4);
+    w.dy = make_rsrc(a.dy + qb * a.D, n * a.D * 4);
+    w.C = make_rsrc(a.C + qb * DM, n * DM * 4);
+    w.dl = make_rsrc(a.delta + qb * a.D, ((ND - 1) * a.P + n) * a.D * 4);
+    w.g = make_rsrc(a.dB + qb * DM, n * DM * 4);
+    return w;
+}
+__device__ __forceinline__ int adj_oD(const AdjWin &w, long r) { return static_cast<int>(static_cast<unsigned>(r) * w.sD); }
+__device__ __forceinline__ int adj_oDM(const AdjWin &w, long r) { return static_cast<int>(static_cast<unsigned>(r) * w.sDM); }
+// dy * C, the state g and the delta of axis ax at point qb + r.
+__device__ __forceinline__ float adj_dyc(const AdjWin &w, long r) {
+    return bio<f32_t>::ld(w.dy, w.vd, adj_oD(w, r)) * bio<f32_t>::ld(w.C, w.vc, adj_oDM(w, r));
+}
+__device__ __forceinline__ float adj_g(const AdjWin &w, long r) { return bio<f32_t>::ld(w.g, w.vc, adj_oDM(w, r)); }
+__device__ __forceinline__ float adj_dl(const AdjWin &w, int ax, long r) {
+    return bio<f32_t>::ld(w.dl, w.vd, static_cast<int>(ax * w.sAx) + adj_oD(w, r));
+}
+__device__ __forceinline__ void adj_store(const AdjWin &w, long r, float g) {
+    bio<f32_t>::st(w.g, w.vc, adj_oDM(w, r), g);
+}
+
 // 2D grids with D*M a multiple of 64: the adjoint state by tile bands. The
 // grid is cut into TR x TW tiles; tiles with equal tile-index sum (a band)
 // are independent, and bands run last to first, one launch each. One wave
@@ -99,10 +139,13 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile2d(NdBwdArgs a, int band, i
     const long n0 = a.dims[0], n1 = a.dims[1];
     const long r0 = static_cast<long>(ti0) * TR, r1 = std::min<long>(n0, r0 + TR);
     const long j0 = static_cast<long>(ti1) * TW, j1 = std::min<long>(n1, j0 + TW);
-    const long DM = a.D * a.M, P = a.P;
+    const long DM = a.D * a.M;
     const long c = static_cast<long>(cg) * 64 + lane;
     const long d = c / a.M;
     const float A0 = a.A[c] * kLog2e, A1 = a.A[DM + c] * kLog2e;
+    // Window: the tile's rows and the successor row below them.
+    const long qb = r0 * n1;
+    const AdjWin w = adj_window<2>(a, qb, (std::min<long>(r1, n0 - 1) + 1) * n1, c, d);
     // A row's operands (dy . C, both deltas) and right-edge successor,
     // loaded before the row computes (its g stores would otherwise order
     // every later load); columns past j1 load column j1 - 1 and go unused.
@@ -110,29 +153,30 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile2d(NdBwdArgs a, int band, i
         float dyc[TW], d0[TW], d1[TW];
         float gr, dr1;
     };
-    auto load_row = [&](long r, Row &w) __attribute__((always_inline)) {
+    auto load_row = [&](long r, Row &rw) __attribute__((always_inline)) {
+        const long rq = r * n1 - qb;
 #pragma unroll
         for (int jj = 0; jj < TW; ++jj) {
-            const long q = r * n1 + std::min<long>(j0 + jj, j1 - 1);
-            w.dyc[jj] = a.dy[q * a.D + d] * a.C[q * DM + c];
-            w.d0[jj] = a.delta[q * a.D + d];
-            w.d1[jj] = a.delta[(P + q) * a.D + d];
+            const long q = rq + std::min<long>(j0 + jj, j1 - 1);
+            rw.dyc[jj] = adj_dyc(w, q);
+            rw.d0[jj] = adj_dl(w, 0, q);
+            rw.d1[jj] = adj_dl(w, 1, q);
         }
-        const long qr = r * n1 + std::min<long>(j1, n1 - 1);
-        w.gr = a.dB[qr * DM + c];
-        w.dr1 = a.delta[(P + qr) * a.D + d];
+        const long qr = rq + std::min<long>(j1, n1 - 1);
+        rw.gr = adj_g(w, qr);
+        rw.dr1 = adj_dl(w, 1, qr);
     };
     float gb[TW], db0[TW];
 #pragma unroll
     for (int jj = 0; jj < TW; ++jj) {
-        const long q = std::min<long>(r1, n0 - 1) * n1 + std::min<long>(j0 + jj, j1 - 1);
-        gb[jj] = a.dB[q * DM + c];
-        db0[jj] = a.delta[q * a.D + d];
+        const long q = std::min<long>(r1, n0 - 1) * n1 + std::min<long>(j0 + jj, j1 - 1) - qb;
+        gb[jj] = adj_g(w, q);
+        db0[jj] = adj_dl(w, 0, q);
     }
     Row cur, nxt;
     load_row(r1 - 1, cur);
     for (long r = r1 - 1; r >= r0; --r) {
-        load_row(r > 0 ? r - 1 : 0, nxt);
+        load_row(r > r0 ? r - 1 : r0, nxt);
         const bool below = r + 1 < n0;
         float gr = cur.gr, dr1 = cur.dr1;
         bool right = j1 < n1;
@@ -142,7 +186,7 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile2d(NdBwdArgs a, int band, i
                 float g = cur.dyc[jj];
                 if (below) g = fmaf(exp2_fast(db0[jj] * A0), gb[jj], g);
                 if (right) g = fmaf(exp2_fast(dr1 * A1), gr, g);
-                a.dB[(r * n1 + j0 + jj) * DM + c] = g;
+                adj_store(w, r * n1 + j0 + jj - qb, g);
                 gb[jj] = g;
                 db0[jj] = cur.d0[jj];
                 gr = g;
@@ -167,27 +211,30 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile3d(NdBwdArgs a, const int *
     const long p0 = static_cast<long>(tiles[3 * o]) * TP, p1 = std::min<long>(n0, p0 + TP);
     const long r0 = static_cast<long>(tiles[3 * o + 1]) * TR, r1 = std::min<long>(n1, r0 + TR);
     const long j0 = static_cast<long>(tiles[3 * o + 2]) * TW, j1 = std::min<long>(n2, j0 + TW);
-    const long DM = a.D * a.M, P = a.P, s0 = n1 * n2;
+    const long DM = a.D * a.M, s0 = n1 * n2;
     const long c = static_cast<long>(cg) * 64 + lane;
     const long d = c / a.M;
     const float A0 = a.A[c] * kLog2e, A1 = a.A[DM + c] * kLog2e, A2 = a.A[2 * DM + c] * kLog2e;
+    // Window: the tile's planes and the successor plane below them.
+    const long qb = p0 * s0;
+    const AdjWin w = adj_window<3>(a, qb, (std::min<long>(p1, n0 - 1) + 1) * s0, c, d);
     struct Row {
         float dyc[TW], d0[TW], d1[TW], d2[TW];
         float gr, dr2;
     };
-    auto qof = [&](long pp, long rr, long jj) { return pp * s0 + rr * n2 + jj; };
-    auto load_row = [&](long pp, long rr, Row &w) __attribute__((always_inline)) {
+    auto qof = [&](long pp, long rr, long jj) { return pp * s0 + rr * n2 + jj - qb; };
+    auto load_row = [&](long pp, long rr, Row &rw) __attribute__((always_inline)) {
 #pragma unroll
         for (int jj = 0; jj < TW; ++jj) {
             const long q = qof(pp, rr, std::min<long>(j0 + jj, j1 - 1));
-            w.dyc[jj] = a.dy[q * a.D + d] * a.C[q * DM + c];
-            w.d0[jj] = a.delta[q * a.D + d];
-            w.d1[jj] = a.delta[(P + q) * a.D + d];
-            w.d2[jj] = a.delta[(2 * P + q) * a.D + d];
+            rw.dyc[jj] = adj_dyc(w, q);
+            rw.d0[jj] = adj_dl(w, 0, q);
+            rw.d1[jj] = adj_dl(w, 1, q);
+            rw.d2[jj] = adj_dl(w, 2, q);
         }
         const long qr = qof(pp, rr, std::min<long>(j1, n2 - 1));
-        w.gr = a.dB[qr * DM + c];
-        w.dr2 = a.delta[(2 * P + qr) * a.D + d];
+        rw.gr = adj_g(w, qr);
+        rw.dr2 = adj_dl(w, 2, qr);
     };
     // Plane below: successors along axis 0 of every (row, column).
     float gp[TR][TW], dp0[TR][TW];
@@ -197,8 +244,8 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile3d(NdBwdArgs a, const int *
         for (int jj = 0; jj < TW; ++jj) {
             const long q = qof(std::min<long>(p1, n0 - 1), std::min<long>(r0 + ri, r1 - 1),
                                std::min<long>(j0 + jj, j1 - 1));
-            gp[ri][jj] = a.dB[q * DM + c];
-            dp0[ri][jj] = a.delta[q * a.D + d];
+            gp[ri][jj] = adj_g(w, q);
+            dp0[ri][jj] = adj_dl(w, 0, q);
         }
     for (long pp = p1 - 1; pp >= p0; --pp) {
         const bool pbelow = pp + 1 < n0;
@@ -207,8 +254,8 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile3d(NdBwdArgs a, const int *
 #pragma unroll
         for (int jj = 0; jj < TW; ++jj) {
             const long q = qof(pp, std::min<long>(r1, n1 - 1), std::min<long>(j0 + jj, j1 - 1));
-            gb[jj] = a.dB[q * DM + c];
-            db1[jj] = a.delta[(P + q) * a.D + d];
+            gb[jj] = adj_g(w, q);
+            db1[jj] = adj_dl(w, 1, q);
         }
         Row cur, nxt;
         load_row(pp, r1 - 1, cur);
@@ -227,7 +274,7 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile3d(NdBwdArgs a, const int *
                         if (pbelow) g = fmaf(exp2_fast(dp0[ri][jj] * A0), gp[ri][jj], g);
                         if (rbelow) g = fmaf(exp2_fast(db1[jj] * A1), gb[jj], g);
                         if (right) g = fmaf(exp2_fast(dr2 * A2), gr, g);
-                        a.dB[qof(pp, r, j0 + jj) * DM + c] = g;
+                        adj_store(w, qof(pp, r, j0 + jj), g);
                         gp[ri][jj] = g;
                         dp0[ri][jj] = cur.d0[jj];
                         gb[jj] = g;
@@ -698,6 +745,7 @@ struct NdBwdShape {
     long P, nd, D, M;
     bool lanes;          // M a power of two <= 64: nd_adjoint_grads_lanes
     bool gtiles;         // ... and 2D or 3D: the tile walks
+    bool atile2;         // 2D adjoint state by tile bands
     int db;
     long qc, nbx, nby;
     size_t offs_bytes, nbr_bytes, part_bytes, tile_bytes;
@@ -770,7 +818,14 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
     s.offs_bytes = align_up(sizeof(long) * s.P, 256);
     s.nbr_bytes = align_up(sizeof(uint16_t) * s.P, 256);
     s.tile_bytes = 0;
-    if (s.nd == 3 && (s.D * s.M) % 64 == 0) {
+    // The adjoint tile sweeps address a tile's rows (planes) and the
+    // successor row (plane) through buffer windows below 2 GiB.
+    auto adj_win_ok = [&](long lead_points) {
+        const double n = static_cast<double>(std::min<long>(s.P, lead_points));
+        return std::max(n * s.D * s.M * 4, (static_cast<double>(s.nd - 1) * s.P + n) * s.D * 4) < 2147483000.0;
+    };
+    s.atile2 = s.nd == 2 && (s.D * s.M) % 64 == 0 && adj_win_ok((kAdjTR + 1) * a->dims[1]);
+    if (s.nd == 3 && (s.D * s.M) % 64 == 0 && adj_win_ok((kAdj3P + 1) * a->dims[1] * a->dims[2])) {
         long nt = 1;
         const long tdim[3] = {kAdj3P, kAdj3R, kAdj3W};
         for (int ax = 0; ax < 3; ++ax) nt *= (a->dims[ax] + tdim[ax] - 1) / tdim[ax];
@@ -780,7 +835,6 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
     return true;
 }
 
-constexpr int kAdjTR = 16, kAdjTW = 8;
 
 // The tiled gradient pass for the M lanes of a channel (a power of two up
 // to 64, a compile-time constant of the kernels' lane sums).
@@ -826,7 +880,7 @@ static void nd_bwd_launch(const NdBwdArgs &args, const NdBwdShape &s, const KMWa
                                    dim3(static_cast<unsigned>(n * ncg)), dim3(64), 0, st, args,
                                    dtiles + 3 * bstart[b], ncg);
         }
-    } else if (ND == 2 && DM % 64 == 0) {
+    } else if (ND == 2 && s.atile2) {
         const int nt0 = static_cast<int>((args.dims[0] + kAdjTR - 1) / kAdjTR);
         const int nt1 = static_cast<int>((args.dims[1] + kAdjTW - 1) / kAdjTW);
         const int ncg = static_cast<int>(DM / 64);
@@ -903,7 +957,7 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
     }
     // The per-level path reads the plan's level offsets; the tile-band paths
     // (2D and 3D with D*M a multiple of 64) need no plan.
-    const bool tiles2d = s.nd == 2 && (s.D * s.M) % 64 == 0;
+    const bool tiles2d = s.atile2;
     const bool levels = !tiles2d && !s.tile_bytes;
     KMWavefrontPlan *plan = nullptr;
     if (levels && !(plan = km_wavefront_plan_create(a->dims, a->ndims))) {
