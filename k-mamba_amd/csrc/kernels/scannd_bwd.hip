@@ -37,6 +37,7 @@ namespace km {
 constexpr int kNdBwdMaxAcc = 64;   // ndims * M: per-thread dA slots in LDS (64 KB)
 constexpr int kAdj3P = 4, kAdj3R = 4, kAdj3W = 8;   // 3D adjoint tiles (axis 0, 1, 2)
 constexpr int kAdjTR = 16, kAdjTW = 8;              // 2D adjoint tiles (rows, points)
+constexpr int kAdjRB = 4;                           // 2D adjoint rows loaded per batch
 
 struct NdBwdArgs {
     const float *x, *A, *B, *C, *delta, *h, *dy;
@@ -131,7 +132,7 @@ __device__ __forceinline__ void adj_store(const AdjWin &w, long r, float g) {
 // registers and the right neighbour from the previous step; successors
 // across the tile's bottom and right edges were written by the previous
 // launch (the next band).
-template <int TR, int TW>
+template <int TR, int TW, int RB>
 __global__ void __launch_bounds__(64) nd_adjoint_tile2d(NdBwdArgs a, int band, int nt1, int ncg) {
     const int lane = threadIdx.x;
     const int o = static_cast<int>(blockIdx.x) / ncg, cg = static_cast<int>(blockIdx.x) - o * ncg;
@@ -173,28 +174,47 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile2d(NdBwdArgs a, int band, i
         gb[jj] = adj_g(w, q);
         db0[jj] = adj_dl(w, 0, q);
     }
-    Row cur, nxt;
-    load_row(r1 - 1, cur);
-    for (long r = r1 - 1; r >= r0; --r) {
-        load_row(r > r0 ? r - 1 : r0, nxt);
-        const bool below = r + 1 < n0;
-        float gr = cur.gr, dr1 = cur.dr1;
-        bool right = j1 < n1;
+    // Rows go in batches of RB, the next batch's loads issued before the
+    // current batch computes: one memory latency per batch, not per row.
+    auto load_batch = [&](long rtop, Row (&bt)[RB]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int jj = TW - 1; jj >= 0; --jj) {
-            if (j0 + jj < j1) {
-                float g = cur.dyc[jj];
-                if (below) g = fmaf(exp2_fast(db0[jj] * A0), gb[jj], g);
-                if (right) g = fmaf(exp2_fast(dr1 * A1), gr, g);
-                adj_store(w, r * n1 + j0 + jj - qb, g);
-                gb[jj] = g;
-                db0[jj] = cur.d0[jj];
-                gr = g;
-                dr1 = cur.d1[jj];
-                right = true;
+        for (int i = 0; i < RB; ++i) load_row(std::max<long>(rtop - i, r0), bt[i]);   // past r0: reload r0
+    };
+    auto compute_batch = [&](long rtop, const Row (&bt)[RB]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            const long r = rtop - i;
+            if (r >= r0) {
+                const Row &cur = bt[i];
+                const bool below = r + 1 < n0;
+                float gr = cur.gr, dr1 = cur.dr1;
+                bool right = j1 < n1;
+#pragma unroll
+                for (int jj = TW - 1; jj >= 0; --jj) {
+                    if (j0 + jj < j1) {
+                        float g = cur.dyc[jj];
+                        if (below) g = fmaf(exp2_fast(db0[jj] * A0), gb[jj], g);
+                        if (right) g = fmaf(exp2_fast(dr1 * A1), gr, g);
+                        adj_store(w, r * n1 + j0 + jj - qb, g);
+                        gb[jj] = g;
+                        db0[jj] = cur.d0[jj];
+                        gr = g;
+                        dr1 = cur.d1[jj];
+                        right = true;
+                    }
+                }
             }
         }
-        cur = nxt;
+    };
+    Row ba[RB], bb[RB];
+    load_batch(r1 - 1, ba);
+    for (long rt = r1 - 1; rt >= r0; rt -= 2 * RB) {
+        load_batch(rt - RB, bb);
+        compute_batch(rt, ba);
+        if (rt - RB >= r0) {
+            load_batch(rt - 2 * RB, ba);
+            compute_batch(rt - RB, bb);
+        }
     }
 }
 
@@ -888,7 +908,7 @@ static void nd_bwd_launch(const NdBwdArgs &args, const NdBwdShape &s, const KMWa
             const int lo = band > nt1 - 1 ? band - (nt1 - 1) : 0;
             const int hi = band < nt0 - 1 ? band : nt0 - 1;
             const long tiles = hi - lo + 1;
-            hipLaunchKernelGGL((nd_adjoint_tile2d<kAdjTR, kAdjTW>),
+            hipLaunchKernelGGL((nd_adjoint_tile2d<kAdjTR, kAdjTW, kAdjRB>),
                                dim3(static_cast<unsigned>(tiles * ncg)), dim3(64), 0, st, args, band, nt1, ncg);
         }
     } else {
