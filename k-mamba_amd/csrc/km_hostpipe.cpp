@@ -20,17 +20,27 @@
 #include <thread>
 #include <vector>
 
+#include <unistd.h>
+
 namespace km {
 namespace {
 
 // Runs f(0..n-1) on the calling thread and the pool's workers and returns
 // when every index is done. The pool is created on first use and never torn
 // down (its threads are detached and sleep on a condition variable), so no
-// thread object is destroyed while running at process exit.
+// thread object is destroyed while running at process exit. A process forked
+// after the pool started has none of its threads: it builds its own.
 class CopyPool {
   public:
     static CopyPool &get() {
-        static CopyPool *pool = new CopyPool();
+        static std::mutex mu;
+        static CopyPool *pool = nullptr;
+        static pid_t owner = 0;
+        std::lock_guard<std::mutex> g(mu);
+        if (!pool || owner != getpid()) {
+            pool = new CopyPool();   // a forked child's inherited pool is left as is
+            owner = getpid();
+        }
         return *pool;
     }
     int threads() const { return nworkers_ + 1; }
