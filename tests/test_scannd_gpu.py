@@ -323,7 +323,11 @@ def test_config2_full_size_sampled(dims, D, M, nsel):
 BWD_CASES = [((50,), 8, 4), ((17, 23), 8, 16), ((64, 64), 32, 16), ((5, 6, 7), 4, 8),
              ((3, 2, 3, 2, 2), 2, 16),     # ndims * M = 80: the shuffle path needs no LDS
              ((16, 16, 16), 16, 16), ((3, 4, 2, 5), 3, 5), ((9, 11), 5, 32), ((256, 256), 16, 16),
-             ((64, 64, 64), 8, 16)]
+             ((64, 64, 64), 8, 16),
+             # The tiled paths (D*M a multiple of 64) on grids ragged in every
+             # axis, with each lane-sum width of the gradient tiles.
+             ((6, 13, 19), 4, 16), ((19, 70), 2, 32), ((10, 33), 8, 8), ((7, 9, 12), 16, 4),
+             ((5, 130), 1, 64), ((9, 10, 11), 64, 1)]
 
 
 def bwd_inputs(dims, D, M, seed):
