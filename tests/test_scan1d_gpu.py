@@ -285,6 +285,30 @@ def test_scan1d_host_pointer_api(L, D, M):
     assert_close(h, hr, TOL_F32, "h", kh[0])
 
 
+def test_scan1d_host_pointer_api_pinned_buffers():
+    # The same entry point on page-locked host buffers (torch pin_memory):
+    # those copy directly instead of through the library's pinned ring.
+    L, D, M = 2100, 1024, 16
+    x, A, B, Cm, dt = _api_inputs(L, D, M)
+    h0 = rng_for("h0", L, D, M).uniform(-1, 1, (D, M)).astype(np.float32)
+    yr, hr = O.scan1d(x, A, B, Cm, dt, h0)
+
+    def pinned(a):
+        t = torch.empty(a.shape, dtype=torch.float32, pin_memory=True)
+        t.numpy()[...] = a
+        return t
+
+    px, pA, pB, pC, pdt, ph = (pinned(a) for a in (x, A, B, Cm, dt, h0))
+    py = pinned(np.zeros((L, D), np.float32))
+    p = K.ScanParams(*(t.data_ptr() for t in (px, pA, pB, pC, pdt, ph, py)), L, D, M)
+    K.mamba_scan1d_forward(C.byref(p))
+    assert K.km_last_error() == ""
+    ky, kh, _ = scan1d_kappa(x[None], dt[None], A, B[None], Cm[None], h0=h0[None],
+                             bc_strides=(L * D * M, D * M, M))
+    assert_close(py.numpy(), yr, TOL_F32, "y", ky[0])
+    assert_close(ph.numpy(), hr, TOL_F32, "h", kh[0])
+
+
 def test_config1_full_size_sampled_parity():
     # configs[1] shape (B=8, L=4096, D=1024, N=16) on the GPU, checked against
     # the oracle on a sample of channels of the first and last batch element
