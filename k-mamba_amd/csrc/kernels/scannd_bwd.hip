@@ -535,10 +535,20 @@ __device__ __forceinline__ float channel_sum(float v) {
 
 // The arithmetic and stores of point qb + r, with the states of its axis
 // predecessors hp[ax] (used where has[ax]). avl[ax] = A * log2(e).
-template <int ND, int MM>
+// Per-channel outputs (dx, ddelta) of the MM lanes of a channel: a wave
+// holds 64 / MM channels, so a direct store writes 64 / MM * 4 bytes per
+// point. With PTS > 0 (4 <= MM <= 32) lane m = 0 of each channel puts them
+// into the workgroup's LDS stage instead, at slot `slot` of PTS points, and
+// grad_flush writes a group of points with every lane busy.
+template <int MM>
+constexpr bool kStageOut = MM >= 4 && MM <= 32;
+constexpr int kGradPts = 32;   // points per staged group
+
+template <int ND, int MM, int PTS>
 __device__ __forceinline__ void grad_finish(const GradWin &w, const GradIn<ND> &v, long r,
                                             const float (&av)[ND], const float (&avl)[ND], float (&dAacc)[ND],
-                                            const float (&hp)[ND], const bool (&has)[ND]) {
+                                            const float (&hp)[ND], const bool (&has)[ND], float *stage,
+                                            int slot) {
     constexpr float kInvNd = 1.0f / ND;
     float dtb = v.dl[0];
 #pragma unroll
@@ -562,9 +572,45 @@ __device__ __forceinline__ void grad_finish(const GradWin &w, const GradIn<ND> &
     const int oDM = static_cast<int>(static_cast<unsigned>(r) * w.sDM);
     bio<f32_t>::st(w.dC, w.vcs, oDM, v.dyv * v.hv);
     bio<f32_t>::st(w.g, w.vcs, oDM, v.gv * dtb * v.xv);
-    bio<f32_t>::st(w.dx, w.vds, oD, tx);
+    if constexpr (PTS > 0) {
+        if (w.vds >= 0) {
+            constexpr int CPW = 256 / MM;
+            const int lc = static_cast<int>(threadIdx.x) / MM;
+            stage[slot * CPW + lc] = tx;
 #pragma unroll
-    for (int ax = 0; ax < ND; ++ax) bio<f32_t>::st(w.ddl, w.vds, static_cast<int>(ax * w.sAx) + oD, td[ax]);
+            for (int ax = 0; ax < ND; ++ax) stage[((ax + 1) * PTS + slot) * CPW + lc] = td[ax];
+        }
+    } else {
+        bio<f32_t>::st(w.dx, w.vds, oD, tx);
+#pragma unroll
+        for (int ax = 0; ax < ND; ++ax) bio<f32_t>::st(w.ddl, w.vds, static_cast<int>(ax * w.sAx) + oD, td[ax]);
+    }
+}
+
+// Writes a staged group of PTS points: dx and the ND ddelta planes of the
+// workgroup's 256 / MM channels (from channel d0), point slot -> window
+// offset point_of(slot) (negative: no point). Consecutive threads take
+// consecutive channels of a point, so each point's run is one contiguous
+// store per tensor.
+template <int ND, int MM, int PTS, typename PointOf>
+__device__ __forceinline__ void grad_flush(const GradWin &w, const float *stage, long d0, long D,
+                                           PointOf point_of) {
+    constexpr int CPW = 256 / MM;
+    static_assert((CPW * PTS) % 256 == 0, "one tensor per pass of the workgroup");
+    constexpr int NE = (ND + 1) * PTS * CPW;
+#pragma unroll
+    for (int e0 = 0; e0 < NE; e0 += 256) {
+        const int e = e0 + static_cast<int>(threadIdx.x);
+        const int k = e0 / (CPW * PTS);   // workgroup-uniform: dx, then the ddelta axes
+        const int lc = e % CPW, slot = (e / CPW) % PTS;
+        const long r = point_of(slot);
+        const long d = d0 + lc;
+        if (r >= 0 && d < D) {
+            const unsigned off = static_cast<unsigned>(d * 4) + static_cast<unsigned>(r) * w.sD;
+            if (k == 0) bio<f32_t>::st(w.dx, static_cast<int>(off), 0, stage[e]);
+            else bio<f32_t>::st(w.ddl, static_cast<int>(off + (k - 1) * w.sAx), 0, stage[e]);
+        }
+    }
 }
 
 // The gradient pass over tiles of a 2D grid: workgroup x takes tile x (TR
@@ -611,17 +657,36 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile2d(NdBwdArgs a) {
         }
         up0 = i0 > 0 ? grad_h(w, (i0 - 1) * d1 + j - qb) : 0.f;
     };
+    // dx / ddelta of kGradPts / TR columns at a time through LDS (double
+    // buffered: one barrier per group).
+    constexpr int PTS = kStageOut<MM> ? kGradPts : 0;
+    constexpr int CPG = kGradPts / TR;   // columns per staged group
+    static_assert(kGradPts % TR == 0, "whole columns per staged group");
+    __shared__ float stage[kStageOut<MM> ? 2 * 3 * kGradPts * (256 / MM) : 1];
+    const long d0 = static_cast<long>(blockIdx.x) * (256 / MM);
     auto finish_col = [&](long jj, const GradIn<2> (&v)[TR], float up) {
         const long j = j0 + jj;
+        float *st = stage + ((jj / CPG) & 1) * (3 * kGradPts * (256 / MM));
 #pragma unroll
         for (int ii = 0; ii < TR; ++ii) {
             if (ii < ie) {
                 const long i = i0 + ii;
                 const bool has[2] = {i > 0, j > 0};
                 const float hp[2] = {up, left[ii]};
-                grad_finish<2, MM>(w, v[ii], i * d1 + j - qb, av, avl, dAacc, hp, has);
+                grad_finish<2, MM, PTS>(w, v[ii], i * d1 + j - qb, av, avl, dAacc, hp, has, st,
+                                        static_cast<int>((jj % CPG) * TR + ii));
                 up = v[ii].hv;
                 left[ii] = v[ii].hv;
+            }
+        }
+        if constexpr (PTS > 0) {
+            if (jj % CPG == CPG - 1 || jj == je - 1) {
+                __syncthreads();
+                const long c0j = jj - jj % CPG;   // first column of the group
+                grad_flush<2, MM, PTS>(w, st, d0, a.D, [&](int sl) -> long {
+                    const long col = c0j + sl / TR, ii = sl % TR;
+                    return (col < je && ii < ie) ? (i0 + ii) * d1 + j0 + col - qb : -1;
+                });
             }
         }
     };
@@ -700,10 +765,16 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
         }
         g.prev0 = p0 > 0 ? grad_h(w, (p0 - 1) * s0 + i * d2 + j - qb) : 0.f;
     };
+    // dx / ddelta of each row's TW x TP points through LDS (double buffered
+    // by row: one barrier per row).
+    constexpr int PTS = (kStageOut<MM> && TW * TP == kGradPts) ? kGradPts : 0;
+    __shared__ float stage[PTS > 0 ? 2 * 4 * kGradPts * (256 / MM) : 1];
+    const long d0 = static_cast<long>(blockIdx.x) * (256 / MM);
     Group ga, gb;
     load_grp(0, 0, ga);
     for (long ii = 0; ii < ie; ++ii) {
         const long i = i0 + ii;
+        float *st = stage + (ii & 1) * (4 * kGradPts * (256 / MM));
         float left[TP];
 #pragma unroll
         for (int jj = 0; jj < TW; ++jj) {
@@ -721,13 +792,21 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
                         const bool has[3] = {pl > 0, i > 0, j > 0};
                         const float hp[3] = {prev, ii == 0 ? cur.up[pp] : above[jj][pp],
                                              jj == 0 ? cur.left[pp] : left[pp]};
-                        grad_finish<3, MM>(w, cur.v[pp], pl * s0 + i * d2 + j - qb, av, avl, dAacc, hp, has);
+                        grad_finish<3, MM, PTS>(w, cur.v[pp], pl * s0 + i * d2 + j - qb, av, avl, dAacc, hp,
+                                                has, st, jj * TP + pp);
                         prev = cur.v[pp].hv;
                         left[pp] = cur.v[pp].hv;
                         above[jj][pp] = cur.v[pp].hv;
                     }
                 }
             }
+        }
+        if constexpr (PTS > 0) {
+            __syncthreads();
+            grad_flush<3, MM, PTS>(w, st, d0, a.D, [&](int sl) -> long {
+                const long jj = sl / TP, pp = sl % TP;
+                return (jj < je && pp < pe) ? (p0 + pp) * s0 + i * d2 + j0 + jj - qb : -1;
+            });
         }
     }
     }
