@@ -28,6 +28,18 @@ void km_clear_error(void);
 /* Library version string. */
 const char *km_version(void);
 
+/* Device memory the library holds in its caches (bytes, every device):
+ * the host-pointer staging arenas and the per-(device, stream) scratch
+ * blocks of entry points called without a workspace. */
+size_t km_device_bytes_held(void);
+
+/* Frees the library's scratch blocks tied to `stream` on the current device
+ * (after waiting for the stream). Call it before destroying a stream that
+ * library calls ran on, so its blocks do not stay allocated; the library
+ * also frees the least recently used blocks of other streams by itself
+ * when its table of 64 blocks is full. Returns the bytes freed. */
+size_t km_release_stream(void *stream);
+
 typedef enum {
     KM_F32 = 0,   /* IEEE fp32 */
     KM_BF16 = 1   /* bfloat16 storage, fp32 arithmetic, round-to-nearest-even on store */
@@ -101,11 +113,11 @@ int km_scan1d_fwd(const KMScan1DFwd *a, void *stream);
  *                 batch or time (bc_sb, bc_st > 0 when B, L > 1).
  *   clamp       : the forward's clamp flag (used when states are recomputed)
  *   workspace   : device scratch of km_scan1d_bwd_workspace_bytes() bytes, or
- *                 NULL for the library's per-device scratch (calls that
- *                 overlap on one device then race: pass a workspace each).
- *                 It holds per-workgroup partial sums: B*D*N floats for dA
- *                 and, with shared B/C, 2*B*ceil(D/g)*L*N floats for dB/dC
- *                 (g = 16 channels for N = 16, 32 for N = 8, else 64).
+ *                 NULL for the library's scratch of this (device, stream).
+ *                 It holds per-workgroup partial sums (dA and, with shared
+ *                 B/C, dB/dC per channel group; the group width depends on
+ *                 the kernel the shape runs on) and, when neither h_hist
+ *                 nor h_ckpt is given, the recomputed checkpoints.
  * dA (summed over batch and time) and the shared dB/dC (summed over
  * channels) are formed from those partials in a fixed order, with no
  * atomics: every output is identical run to run. */
@@ -217,18 +229,30 @@ int km_mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long
  * with km_last_error() set. */
 int km_scannd_fwd(const ScanNDParams *p, void *stream);
 
+/* Status of the latest km_scannd_fwd / km_scannd_fwd_noalloc call enqueued
+ * on `stream` (current device). Waits for the stream, then returns 0 when
+ * that call's outputs are exact, 1 when one of its dataflow waits (3- and
+ * 4-dimensional grids) ran out of its polling budget (KM_SCANND_FLOW_SPIN):
+ * that call then wrote NaN into the affected tiles' states and outputs and
+ * should be run again (the synchronous om_scannd_forward / scannd re-run it
+ * on the band schedule by themselves), or -1 on error. */
+int km_scannd_status(void *stream);
+
 /* km_scannd_fwd without any allocation. No counterpart in the reference: it
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). Same
  * parameters, semantics and results as km_scannd_fwd. The dataflow schedule
- * of 3- and 4-dimensional grids keeps its counters and completion flags in a
- * fixed 1 MiB array in each GPU's memory (held until the process ends)
- * instead of a per-stream allocation; grids needing more than 262,128
- * (tile, channel group) flags, and shapes outside the tile kernels (D*M not
- * a multiple of 64, or M not dividing 64), and the Mamba-3 lambda branch
- * (whose rotated states need workspace), are rejected with -1 and
- * km_last_error(). Every call on one GPU shares that array: calls that
- * overlap on one GPU (other streams, other threads) race. */
+ * of 3- and 4-dimensional grids keeps its counters, epoch and completion
+ * flags in a fixed 1 MiB array in each GPU's memory (held until the process
+ * ends) instead of a per-stream allocation; the epoch is advanced on the
+ * device by each call, so a call captured in a HIP graph may be replayed.
+ * 1D grids run on the Scan1D kernels that use no workspace. Grids needing
+ * more than 262,128 (tile, channel group) flags, shapes of 2 or more
+ * dimensions outside the tile kernels (D*M not a multiple of 64, or M not
+ * dividing 64), and the Mamba-3 lambda branch (whose rotated states need
+ * workspace) are rejected with -1 and km_last_error(). Every call on one
+ * GPU shares that array: calls that overlap on one GPU (other streams,
+ * other threads) race. */
 int km_scannd_fwd_noalloc(const ScanNDParams *p, void *stream);
 
 /* ScanND backward (no counterpart in the reference, which has no ScanND

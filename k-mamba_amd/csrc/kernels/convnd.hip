@@ -1066,7 +1066,7 @@ static int conv_bwd_launch(const ConvArgs &a, hipStream_t s) {
     if (line_shape(a) && lblocks > 0 && lblocks + (a.KV + 1) * a.groups <= 0x7fffffffL && a.groups <= 65535 &&
         strip_fits(a)) {
         part = static_cast<float *>(
-            Workspace::reserve(sizeof(float) * a.groups * nslot * (a.KV + 1) * 64, s));
+            Workspace::reserve(sizeof(float) * a.groups * nslot * (a.KV + 1) * 64, s, WsUse::ConvBwd));
         if (!part) return -1;
     }
     if (part) {

@@ -390,7 +390,7 @@ int kmamba_forward(KMamba *m, const uint32_t *tokens, float *logits_out) {
     const size_t act = km::align_up(sizeof(float) * L * D, 256);
     const size_t hb = km::align_up(sizeof(float) * D * V, 256);
     const size_t lb = km::align_up(sizeof(float) * L * V, 256);
-    char *ws = static_cast<char *>(km::Workspace::reserve(2 * act + hb + lb, nullptr));
+    char *ws = static_cast<char *>(km::Workspace::reserve(2 * act + hb + lb, nullptr, km::WsUse::Model));
     if (!ws) return -1;
     float *buf[2] = {reinterpret_cast<float *>(ws), reinterpret_cast<float *>(ws + act)};
     float *dhead = reinterpret_cast<float *>(ws + 2 * act);

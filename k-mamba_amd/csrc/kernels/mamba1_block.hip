@@ -20,7 +20,7 @@
 
 namespace km {
 
-int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream);
+int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream, bool allow_split);
 int gemm_bf16_launch(const KMGemm *g, hipStream_t s);
 
 constexpr int kConvStrip = 64;
@@ -134,7 +134,7 @@ int mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long B,
             return -1;
         }
     } else {
-        ws = static_cast<char *>(Workspace::reserve(lay.bytes, s));
+        ws = static_cast<char *>(Workspace::reserve(lay.bytes, s, WsUse::Block));
         if (!ws) return -1;
     }
     const long T = B * L, di = w->d_inner, N = w->d_state, R = w->dt_rank, NX = R + 2 * N;
@@ -190,7 +190,7 @@ int mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long B,
     k.bc_sb = L * NX; k.bc_st = NX; k.bc_sd = 0;
     k.dtype = KM_BF16; k.clamp = w->clamp;
     k.z = z; k.Dskip = w->Dskip;
-    if (scan1d_fwd_launch(&k, s) != 0) return -1;
+    if (scan1d_fwd_launch(&k, s, true) != 0) return -1;
     // out_proj
     KMGemm o{};
     o.A = y; o.B = w->W_out; o.C = out; o.M = T; o.N = w->dim; o.K = di;

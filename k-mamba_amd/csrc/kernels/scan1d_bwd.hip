@@ -43,7 +43,7 @@
 
 namespace km {
 
-int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream);
+int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream, bool allow_split);
 
 struct Scan1DBwdArgs {
     const void *x, *dt, *dy;
@@ -823,7 +823,7 @@ static int scan1d_bwd_run(const KMScan1DBwd *k, const BwdPlan &pl, bool bf, hipS
             }
             ws = static_cast<char *>(k->workspace);
         } else {
-            ws = static_cast<char *>(Workspace::reserve(pl.bytes, stream));
+            ws = static_cast<char *>(Workspace::reserve(pl.bytes, stream, WsUse::Scan1DBwd));
             if (!ws) return -1;
         }
     }
@@ -856,7 +856,7 @@ static int scan1d_bwd_run(const KMScan1DBwd *k, const BwdPlan &pl, bool bf, hipS
             f.h_hist = reinterpret_cast<float *>(ws + pl.off_hist);
             a.hist = f.h_hist;
         }
-        if (scan1d_fwd_launch(&f, stream) != 0) return -1;
+        if (scan1d_fwd_launch(&f, stream, true) != 0) return -1;
     }
     if (pl.serial) {
         const long grid = k->B * pl.G;
@@ -964,7 +964,7 @@ __global__ void __launch_bounds__(256) m1_finalize(const float *part, long nwg, 
 
 static int m1_launch(M1Args a, hipStream_t s) {
     const long grid = (a.D + 255) / 256;
-    a.part = static_cast<float *>(Workspace::reserve(sizeof(float) * grid * a.L, s));
+    a.part = static_cast<float *>(Workspace::reserve(sizeof(float) * grid * a.L, s, WsUse::Scan1DM1));
     if (!a.part) return -1;
     hipLaunchKernelGGL(scan1d_bwd_m1_shared, dim3(grid), dim3(256), 0, s, a);
     KM_HIP_TRY(hipGetLastError());

@@ -750,7 +750,7 @@ static int launch_segmented(const KMScan1DFwd *k, long Ls, hipStream_t s) {
     const long BS = k->B * S;
     const size_t st = align_up(sizeof(float) * BS * k->D * k->N, 256);
     const size_t sd = align_up(sizeof(float) * BS * k->D, 256);
-    char *ws = static_cast<char *>(Workspace::reserve(2 * st + sd + align_up(4 * k->B * groups, 256), s));
+    char *ws = static_cast<char *>(Workspace::reserve(2 * st + sd + align_up(4 * k->B * groups, 256), s, WsUse::Scan1DSplit));
     if (!ws) return -1;
     float *hl = reinterpret_cast<float *>(ws);
     float *hin = reinterpret_cast<float *>(ws + st);
@@ -825,7 +825,9 @@ static int launch_serial(const Scan1DFwdArgs &a, bool hist, hipStream_t s) {
     return 0;
 }
 
-int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream) {
+// allow_split = false keeps every shape on kernels that use no workspace
+// (the allocation-free ScanND entry point's 1D grids).
+int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream, bool allow_split) {
     if (!k) { set_error("km_scan1d_fwd: NULL arguments"); return -1; }
     // With no steps (L = 0) only A, h0 and h_final take part.
     if (!k->A || (k->L > 0 && (!k->x || !k->delta || !k->Bm || !k->Cm))) {
@@ -871,7 +873,7 @@ int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream) {
         return bf ? launch_serial<bf16_t>(a, hist, stream) : launch_serial<f32_t>(a, hist, stream);
     // Few (batch, channel group) pairs and a long sequence: split the
     // sequence over workgroups.
-    if (const long Ls = segment_length(k, k->B * ((k->D + 31) / 32)))
+    if (const long Ls = allow_split ? segment_length(k, k->B * ((k->D + 31) / 32)) : 0)
         return bf ? launch_segmented<bf16_t>(k, Ls, stream) : launch_segmented<f32_t>(k, Ls, stream);
     switch (k->N) {
     case 16:
@@ -903,7 +905,7 @@ extern "C" {
 
 int km_scan1d_fwd(const KMScan1DFwd *a, void *stream) {
     km::clear_error();
-    return km::scan1d_fwd_launch(a, static_cast<hipStream_t>(stream));
+    return km::scan1d_fwd_launch(a, static_cast<hipStream_t>(stream), true);
 }
 
 // Reference cuda/scan1d.cu:258-310: B, C, h are [L, D, M]; h receives the
@@ -921,7 +923,7 @@ void om_scan1d_forward(const float *d_x, const float *d_A, const float *d_B, con
     a.B = 1; a.L = L; a.D = D; a.N = M;
     a.bc_sb = static_cast<long>(L) * D * M; a.bc_st = static_cast<long>(D) * M; a.bc_sd = M;
     a.dtype = KM_F32; a.clamp = 1;
-    if (km::scan1d_fwd_launch(&a, nullptr) != 0) return;
+    if (km::scan1d_fwd_launch(&a, nullptr, true) != 0) return;
     if (hipStreamSynchronize(nullptr) != hipSuccess)
         km::set_error("om_scan1d_forward: %s", hipGetErrorString(hipGetLastError()));
 }
@@ -955,7 +957,7 @@ void scan1d(ScanParams *p) {
     if (dev) {
         a.x = p->x; a.delta = p->delta; a.A = p->A; a.Bm = p->B; a.Cm = p->C; a.y = p->y;
         a.h0 = p->h; a.h_final = p->h;
-        if (km::scan1d_fwd_launch(&a, nullptr) == 0 && hipStreamSynchronize(nullptr) != hipSuccess)
+        if (km::scan1d_fwd_launch(&a, nullptr, true) == 0 && hipStreamSynchronize(nullptr) != hipSuccess)
             km::set_error("scan1d: %s", hipGetErrorString(hipGetLastError()));
         return;
     }
@@ -977,7 +979,7 @@ void scan1d(ScanParams *p) {
             km::set_error("scan1d: host-to-device copy failed");
         } else {
             a.x = x; a.delta = dt; a.A = A; a.Bm = Bm; a.Cm = Cm; a.y = y; a.h0 = h; a.h_final = h;
-            if (km::scan1d_fwd_launch(&a, nullptr) == 0) {
+            if (km::scan1d_fwd_launch(&a, nullptr, true) == 0) {
                 if (km::copy_d2h(p->y, y, nLD * 4) != hipSuccess ||
                     km::copy_d2h(p->h, h, nDM * 4) != hipSuccess)
                     km::set_error("scan1d: device-to-host copy failed");

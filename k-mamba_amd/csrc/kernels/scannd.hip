@@ -40,6 +40,8 @@
 
 namespace km {
 
+int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream, bool allow_split);
+
 constexpr int kMaxNd = 8;
 
 struct ScanNDArgs {
@@ -436,7 +438,7 @@ struct FlowArgs {
     unsigned *flags;                     // [ntiles * ncg] epoch of the last finish
     unsigned *counter;                   // [8] items taken per XCD, zero at launch
     unsigned *status;                    // nonzero when a wait ran out (zero at launch)
-    unsigned epoch;
+    const unsigned *epoch;               // this launch's epoch (set by flow_reset)
     unsigned spin;                       // polls per wait before giving up
     int nbands;
     int cg_lo[9];                        // channel groups of XCD x: [cg_lo[x], cg_lo[x + 1])
@@ -496,6 +498,10 @@ __global__ void __launch_bounds__(64) scannd_flow_kernel(ScanNDArgs p, FlowArgs 
     if (ncx <= 0) return;
     const int ntiles = f.band_start[f.nbands];
     const unsigned nitems = static_cast<unsigned>(ntiles) * static_cast<unsigned>(ncx);
+    // The epoch lives in device memory (flow_reset advances it), so a
+    // launch replayed from a captured graph gets a new one each time.
+    const unsigned epoch = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(f.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     int tstride[kMaxNd];                 // row-major tile index strides
     tstride[ND - 1] = 1;
 #pragma unroll
@@ -522,7 +528,7 @@ __global__ void __launch_bounds__(64) scannd_flow_kernel(ScanNDArgs p, FlowArgs 
 #pragma unroll
         for (int a = 0; a < ND; ++a)
             if (ti[a] > 0)
-                ready = flow_wait(f.flags + static_cast<long>(tl - tstride[a]) * p.ncg + cg, f.epoch,
+                ready = flow_wait(f.flags + static_cast<long>(tl - tstride[a]) * p.ncg + cg, epoch,
                                   f.spin) && ready;
         if (ready) {
             scannd_tile<ND, TW, MM, PL, true>(p, ti, cg);
@@ -533,15 +539,30 @@ __global__ void __launch_bounds__(64) scannd_flow_kernel(ScanNDArgs p, FlowArgs 
         }
         __builtin_amdgcn_s_waitcnt(0);   // this wave's h stores acknowledged by L2
         if ((threadIdx.x & 63) == 0)
-            __hip_atomic_store(f.flags + static_cast<long>(tl) * p.ncg + cg, f.epoch, __ATOMIC_RELAXED,
+            __hip_atomic_store(f.flags + static_cast<long>(tl) * p.ncg + cg, epoch, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
-// Zeroes the per-XCD item counters and the status word before a launch.
-__global__ void flow_reset(unsigned *counter, unsigned *status) {
-    if (threadIdx.x < 8) counter[threadIdx.x] = 0u;
-    if (threadIdx.x == 8) *status = 0u;
+// Dataflow state header (u32 words): per-XCD item counters (0-7), the
+// status word (8), the epoch (9); completion flags from word kFlowHead.
+constexpr size_t kFlowHead = 16;
+constexpr int kFlowStatus = 8, kFlowEpoch = 9;
+
+// Before each dataflow launch: zeroes the item counters and the status
+// word and advances the epoch. When the epoch wraps, every one of the
+// nflags flags is cleared first, so no flag holds the new epoch. One
+// workgroup of 256 threads.
+__global__ void __launch_bounds__(256) flow_reset(unsigned *head, long nflags) {
+    __shared__ unsigned s_next;
+    if (threadIdx.x == 0) s_next = head[kFlowEpoch] + 1u;
+    __syncthreads();
+    const unsigned next = s_next;
+    if (next == 0u)
+        for (long i = threadIdx.x; i < nflags; i += 256) head[kFlowHead + i] = 0u;
+    if (threadIdx.x < 8) head[threadIdx.x] = 0u;
+    if (threadIdx.x == kFlowStatus) head[kFlowStatus] = 0u;
+    if (threadIdx.x == kFlowEpoch) head[kFlowEpoch] = next == 0u ? 1u : next;
 }
 
 // General fallback (any D, M): one launch per wavefront level of the point
@@ -676,11 +697,6 @@ __global__ void __launch_bounds__(256) scannd_m3_level_kernel(ScanM3Args p, cons
     for (int c = 0; c < nc; ++c) p.y[off * p.D + d0 + c] = yacc[c];
 }
 
-// Device workspace for the fallback's plan offsets (grown on demand, kept
-// for the process).
-static long *g_plan_dev = nullptr;
-static size_t g_plan_cap = 0;
-
 // Tuning knob (read once): KM_SCANND_T2 / KM_SCANND_T3 = "TW,TL" sets the
 // 2D / 3D tile to TW points along the last axis (4, 8 or 16 in 2D; 4 or 8 in
 // 3D) and TL along each leading axis.
@@ -716,24 +732,30 @@ static void launch_tile(dim3 g, const ScanNDArgs &a, bool ring, const FlowArgs *
     launch_tile_pl<ND, TW, MM, 0>(g, a, flow, s);
 }
 
-// State of the dataflow schedule, one per (device, stream): the per-XCD
-// item counters (words 0-7), the status word (8), then the completion flags
-// (from word 16; zeroed when allocated), the launch epoch and the device's
-// XCD count. Launches on one stream run in order, so they may share it;
-// launches on different streams use different states.
-constexpr size_t kFlowHead = 16;
-struct FlowState {
-    int dev = -1;
-    hipStream_t stream = nullptr;
-    unsigned *buf = nullptr;
-    size_t cap = 0;                      // u32 words
-    unsigned epoch = 0;
-    int nxcc = -1;
-};
-constexpr int kMaxFlowStates = 64;
-static FlowState g_flow[kMaxFlowStates];
-static int g_flow_n = 0;
-static std::mutex g_flow_mu;
+// The dataflow schedule's state lives in the stream's ScanNDFlow workspace
+// block (header as above, then the flags): launches on one stream run in
+// order, so they may share it; launches on different streams use
+// different blocks. A new block is cleared once; afterwards flags only
+// ever hold epochs of earlier launches.
+
+// XCD count of a device (-1 until looked up).
+static int device_xcds(int dev) {
+    static std::mutex mu;
+    static int nx[64];
+    static bool init = [] {
+        for (int &v : nx) v = -1;
+        return true;
+    }();
+    (void)init;
+    if (dev < 0 || dev >= 64) return 0;
+    std::lock_guard<std::mutex> guard(mu);
+    if (nx[dev] < 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess) n = 0;
+        nx[dev] = n;
+    }
+    return nx[dev];
+}
 
 // Polls per dataflow wait (KM_SCANND_FLOW_SPIN, read once): the safety
 // budget after which a wait gives up (see scannd_flow_kernel).
@@ -746,67 +768,68 @@ static unsigned flow_spin() {
     return spin;
 }
 
+// Which status word the latest ScanND forward on a (device, stream) left:
+// 0 none (band or level schedule), 1 the stream's ScanNDFlow block, 2 the
+// allocation-free scratch of the device.
+struct LastFlow {
+    int dev;
+    hipStream_t stream;
+    int kind;
+    unsigned long long tick;
+};
+constexpr int kMaxLastFlow = 64;
+static LastFlow g_last_flow[kMaxLastFlow];
+static int g_last_flow_n = 0;
+static unsigned long long g_last_flow_tick = 0;
+static std::mutex g_last_flow_mu;
+
+static void note_flow(hipStream_t s, int kind) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return;
+    std::lock_guard<std::mutex> guard(g_last_flow_mu);
+    int idx = -1;
+    for (int i = 0; i < g_last_flow_n; ++i)
+        if (g_last_flow[i].dev == dev && g_last_flow[i].stream == s) idx = i;
+    if (idx < 0) {
+        if (g_last_flow_n < kMaxLastFlow) {
+            idx = g_last_flow_n++;
+        } else {
+            idx = 0;   // the least recently noted stream
+            for (int i = 1; i < g_last_flow_n; ++i)
+                if (g_last_flow[i].tick < g_last_flow[idx].tick) idx = i;
+        }
+    }
+    g_last_flow[idx] = LastFlow{dev, s, kind, ++g_last_flow_tick};
+}
+
+static int last_flow_kind(hipStream_t s) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> guard(g_last_flow_mu);
+    for (int i = 0; i < g_last_flow_n; ++i)
+        if (g_last_flow[i].dev == dev && g_last_flow[i].stream == s) return g_last_flow[i].kind;
+    return 0;
+}
+
 // The dataflow schedule runs grids of 3 or more dims (2D grids are faster
 // with one launch per band on MI355X: their 47-tile critical path, slowed by
 // the tiles running beside it, sets the time), needs the device's 8 XCDs as
 // the hardware reports them (XCC_ID 0-7) and a band table that fits the
-// kernel arguments; KM_SCANND_SCHED=band keeps one launch per band. Returns
-// the stream's state with a fresh epoch (under the lock), or null.
-static FlowState *flow_state(int nd, int nbands, size_t words, hipStream_t s, unsigned *epoch) {
+// kernel arguments; KM_SCANND_SCHED=band keeps one launch per band.
+static bool flow_allowed(int nd, int nbands) {
     const char *e = std::getenv("KM_SCANND_SCHED");
-    if (nd < 3 || (e && std::strcmp(e, "band") == 0) || nbands > kMaxFlowBands) return nullptr;
+    if (nd < 3 || (e && std::strcmp(e, "band") == 0) || nbands > kMaxFlowBands) return false;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return nullptr;
-    std::lock_guard<std::mutex> guard(g_flow_mu);
-    FlowState *st = nullptr;
-    for (int i = 0; i < g_flow_n; ++i)
-        if (g_flow[i].dev == dev && g_flow[i].stream == s) st = &g_flow[i];
-    if (!st) {
-        if (g_flow_n == kMaxFlowStates) return nullptr;   // band schedule instead
-        st = &g_flow[g_flow_n++];
-        st->dev = dev;
-        st->stream = s;
-    }
-    if (st->nxcc < 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess) n = 0;
-        st->nxcc = n;
-    }
-    if (st->nxcc != 8) return nullptr;
-    words += kFlowHead;
-    if (st->cap < words) {
-        if (st->buf) {
-            (void)hipStreamSynchronize(s);   // earlier launches on this stream may still use it
-            (void)hipFree(st->buf);
-            st->buf = nullptr;
-            st->cap = 0;
-        }
-        void *ptr = nullptr;
-        if (hipMalloc(&ptr, words * 4) != hipSuccess) {
-            (void)hipGetLastError();
-            return nullptr;
-        }
-        if (hipMemset(ptr, 0, words * 4) != hipSuccess) {
-            (void)hipGetLastError();
-            (void)hipFree(ptr);
-            return nullptr;
-        }
-        st->buf = static_cast<unsigned *>(ptr);
-        st->cap = words;
-    }
-    if (++st->epoch == 0) st->epoch = 1;
-    *epoch = st->epoch;
-    return st;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return false;
+    return device_xcds(dev) == 8;
 }
 
-// Dataflow state supplied by the caller instead of the per-stream state
-// (the allocation-free entry point): a device buffer of `cap` words laid
-// out like FlowState's, the host-side epoch counter of that buffer and the
-// device's XCD count.
+// Dataflow state supplied by the caller instead of the stream's block (the
+// allocation-free entry point): a device buffer of `cap` words laid out as
+// above and the device's XCD count.
 struct FlowBuf {
     unsigned *buf;
     size_t cap;
-    unsigned *epoch;
     int nxcc;
 };
 
@@ -879,48 +902,51 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
         long ntiles = 0;
         for (int b = 0; b < nbands; ++b) ntiles += cnt[b];
         static thread_local FlowArgs fa;
-        unsigned epoch = 0;
         unsigned *fbuf = nullptr;
-        if (ext) {
-            const char *e = std::getenv("KM_SCANND_SCHED");
-            if (allow_flow && a.nd >= 3 && !(e && std::strcmp(e, "band") == 0) &&
-                nbands <= kMaxFlowBands && ext->nxcc == 8) {
-                const size_t words = kFlowHead + static_cast<size_t>(ntiles * a.ncg);
-                if (words > ext->cap) {
-                    set_error("scannd: the dataflow schedule needs %zu flag words, the scratch holds %zu",
-                              words, ext->cap);
-                    return -1;
+        long nflags = 0;   // flag words the block holds (cleared when the epoch wraps)
+        int kind = 0;
+        if (allow_flow && flow_allowed(a.nd, nbands) && ntiles * a.ncg < 0x7fffffffL) {
+            const size_t words = kFlowHead + static_cast<size_t>(ntiles * a.ncg);
+            if (ext) {
+                if (ext->nxcc == 8) {
+                    if (words > ext->cap) {
+                        set_error("scannd: the dataflow schedule needs %zu flag words, the scratch "
+                                  "holds %zu", words, ext->cap);
+                        return -1;
+                    }
+                    fbuf = ext->buf;
+                    nflags = static_cast<long>(ext->cap - kFlowHead);
+                    kind = 2;
                 }
-                if (++*ext->epoch == 0) {
-                    // Epochs wrapped: no flag may hold the new one.
-                    hipLaunchKernelGGL(flow_clear, dim3(256), dim3(256), 0, s, ext->buf,
-                                       static_cast<long>(ext->cap));
-                    *ext->epoch = 1;
+            } else {
+                bool fresh = false;
+                size_t got = 0;
+                fbuf = static_cast<unsigned *>(
+                    Workspace::reserve(words * 4, s, WsUse::ScanNDFlow, &fresh, &got));
+                if (!fbuf) {
+                    clear_error();   // no block: the band schedule instead
+                } else {
+                    nflags = static_cast<long>(got / 4 - kFlowHead);
+                    kind = 1;
+                    if (fresh)
+                        hipLaunchKernelGGL(flow_clear, dim3(256), dim3(256), 0, s, fbuf,
+                                           static_cast<long>(got / 4));
                 }
-                epoch = *ext->epoch;
-                fbuf = ext->buf;
             }
-        } else {
-            FlowState *st = (allow_flow && ntiles * a.ncg < 0x7fffffffL)
-                                ? flow_state(a.nd, nbands, static_cast<size_t>(ntiles * a.ncg), s, &epoch)
-                                : nullptr;
-            if (st) fbuf = st->buf;
         }
+        note_flow(s, kind);
         const FlowArgs *flow = nullptr;
         if (fbuf) {
-            // Counters and status first, flags after: flags only ever hold
-            // epochs of earlier launches (whatever the shape), never the
-            // current one.
             fa.counter = fbuf;
-            fa.status = fbuf + 8;
+            fa.status = fbuf + kFlowStatus;
+            fa.epoch = fbuf + kFlowEpoch;
             fa.flags = fbuf + kFlowHead;
-            fa.epoch = epoch;
             fa.spin = flow_spin();
             fa.nbands = nbands;
             for (int x = 0; x <= 8; ++x) fa.cg_lo[x] = static_cast<int>(static_cast<long>(x) * a.ncg / 8);
             fa.band_start[0] = 0;
             for (int b = 0; b < nbands; ++b) fa.band_start[b + 1] = fa.band_start[b] + static_cast<int>(cnt[b]);
-            hipLaunchKernelGGL(flow_reset, dim3(1), dim3(64), 0, s, fa.counter, fa.status);
+            hipLaunchKernelGGL(flow_reset, dim3(1), dim3(256), 0, s, fbuf, nflags);
             flow = &fa;
             if (status) *status = fa.status;
         }
@@ -967,6 +993,7 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
         return 0;
     }
     // Fallback: per-level launches over the plan.
+    note_flow(s, 0);
     if (ext) {
         set_error("scannd: this shape needs the per-level schedule, whose plan buffer is "
                   "allocated; use km_scannd_fwd");
@@ -980,21 +1007,13 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
         return -1;
     }
     const size_t bytes = sizeof(long) * P;
-    if (g_plan_cap < bytes) {
-        if (g_plan_dev) {
-            (void)hipStreamSynchronize(s);
-            (void)hipFree(g_plan_dev);
-        }
-        g_plan_dev = nullptr;
-        g_plan_cap = 0;
-        if (hipMalloc(&g_plan_dev, bytes) != hipSuccess) {
-            km_wavefront_plan_free(plan);
-            set_error("scannd: plan workspace allocation failed");
-            return -1;
-        }
-        g_plan_cap = bytes;
+    long *offs = static_cast<long *>(Workspace::reserve(bytes, s, WsUse::ScanNDPlan));
+    if (!offs) {
+        km_wavefront_plan_free(plan);
+        return -1;
     }
-    if (hipMemcpyAsync(g_plan_dev, plan->level_offsets, bytes, hipMemcpyHostToDevice, s) != hipSuccess ||
+    // The plan is host memory that is freed below: a synchronous copy.
+    if (hipMemcpyAsync(offs, plan->level_offsets, bytes, hipMemcpyHostToDevice, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess) {
         km_wavefront_plan_free(plan);
         set_error("scannd: plan upload failed");
@@ -1005,7 +1024,7 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
         const long count = plan->level_starts[lvl + 1] - start;
         const long threads = count * a.D;
         hipLaunchKernelGGL(scannd_level_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)),
-                           dim3(256), 0, s, a, g_plan_dev, start, count);
+                           dim3(256), 0, s, a, offs, start, count);
     }
     km_wavefront_plan_free(plan);
     KM_HIP_TRY(hipGetLastError());
@@ -1034,9 +1053,10 @@ static int scannd_m3_device(const ScanNDParams *p, hipStream_t s, bool sync) {
         set_error("scannd: plan creation failed");
         return -1;
     }
+    note_flow(s, 0);
     const size_t off_bytes = align_up(sizeof(long) * P, 256);
     const size_t rot_bytes = sizeof(float) * static_cast<size_t>(P) * p->D * p->M;
-    char *ws = static_cast<char *>(Workspace::reserve(off_bytes + rot_bytes, s));
+    char *ws = static_cast<char *>(Workspace::reserve(off_bytes + rot_bytes, s, WsUse::ScanNDM3));
     if (!ws) {
         km_wavefront_plan_free(plan);
         return -1;
@@ -1184,7 +1204,9 @@ int scannd_device_params(const ScanNDParams *p, hipStream_t s, bool sync, FlowBu
         k.B = 1; k.L = P; k.D = p->D; k.N = p->M;
         k.bc_sb = P * p->D * p->M; k.bc_st = p->D * p->M; k.bc_sd = p->M;
         k.dtype = KM_F32; k.clamp = 0;
-        if (km_scan1d_fwd(&k, s) != 0) return -1;
+        note_flow(s, 0);
+        // Without allocation (ext given): kernels that need no workspace.
+        if (scan1d_fwd_launch(&k, s, ext == nullptr) != 0) return -1;
         if (sync && hipStreamSynchronize(s) != hipSuccess) {
             set_error("scannd: %s", hipGetErrorString(hipGetLastError()));
             return -1;
@@ -1207,7 +1229,6 @@ static __device__ __align__(256) unsigned scratch[kScratchWords];
 struct NoAllocDevice {
     bool ready = false;
     unsigned *ptr = nullptr;
-    unsigned epoch = 0;
     int nxcc = 0;
 };
 constexpr int kMaxDevices = 64;
@@ -1231,14 +1252,39 @@ int scannd_fwd_noalloc(const ScanNDParams *p, hipStream_t s) {
             set_error("km_scannd_fwd_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
             return -1;
         }
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess) n = 0;
         nd.ptr = static_cast<unsigned *>(ptr);
-        nd.nxcc = n;
+        nd.nxcc = device_xcds(dev);
         nd.ready = true;
     }
-    FlowBuf fb{nd.ptr, kScratchWords, &nd.epoch, nd.nxcc};
+    FlowBuf fb{nd.ptr, kScratchWords, nd.nxcc};
     return scannd_device_params(p, s, false, &fb);
+}
+
+// Status of the latest ScanND forward enqueued on stream s (see
+// km_scannd_status).
+int scannd_status(hipStream_t s) {
+    if (!gpu_ready()) return -1;
+    const int kind = last_flow_kind(s);
+    const unsigned *word = nullptr;
+    if (kind == 1) {
+        word = static_cast<const unsigned *>(Workspace::find(s, WsUse::ScanNDFlow));
+    } else if (kind == 2) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -1;
+        std::lock_guard<std::mutex> guard(g_noalloc_mu);
+        word = g_noalloc[dev].ptr;
+    }
+    if (hipStreamSynchronize(s) != hipSuccess) {
+        set_error("km_scannd_status: %s", hipGetErrorString(hipGetLastError()));
+        return -1;
+    }
+    if (!word) return 0;
+    unsigned failed = 0;
+    if (hipMemcpy(&failed, word + kFlowStatus, sizeof failed, hipMemcpyDeviceToHost) != hipSuccess) {
+        set_error("km_scannd_status: status read failed");
+        return -1;
+    }
+    return failed ? 1 : 0;
 }
 
 // Host-pointer staging for the reference's host API: copies inputs to the
@@ -1339,6 +1385,11 @@ int km_scannd_fwd(const ScanNDParams *p, void *stream) {
 int km_scannd_fwd_noalloc(const ScanNDParams *p, void *stream) {
     km::clear_error();
     return km::scannd_fwd_noalloc(p, static_cast<hipStream_t>(stream));
+}
+
+int km_scannd_status(void *stream) {
+    km::clear_error();
+    return km::scannd_status(static_cast<hipStream_t>(stream));
 }
 
 int om_scannd_forward(ScanNDParams *p) {

@@ -1051,7 +1051,7 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
             return -1;
         }
     } else {
-        ws = static_cast<char *>(km::Workspace::reserve(need, st));
+        ws = static_cast<char *>(km::Workspace::reserve(need, st, km::WsUse::ScanNDBwd));
         if (!ws) return -1;
     }
     // The per-level path reads the plan's level offsets; the tile-band paths

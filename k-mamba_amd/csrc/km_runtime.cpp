@@ -107,6 +107,18 @@ const char *km_last_error(void) { return g_err; }
 void km_clear_error(void) { g_err[0] = '\0'; }
 const char *km_version(void) { return "libkmamba-mi355x 0.1 (gfx950)"; }
 
+size_t km_device_bytes_held(void) {
+    size_t total = km::Workspace::held();
+    std::lock_guard<std::mutex> guard(g_stage_mu);
+    for (int d = 0; d < 64; ++d) total += g_stage_size[d];
+    return total;
+}
+
+size_t km_release_stream(void *stream) {
+    km::clear_error();
+    return km::Workspace::release(static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"
 
 namespace km {
@@ -169,47 +181,82 @@ void *Staging::reserve(size_t bytes) {
 }
 
 namespace {
-// Workspaces keyed by (device, stream): launches on different streams never
-// share one, and a block is only freed (to grow it) after its own stream
-// has drained.
+// Workspace blocks keyed by (device, stream, use): launches on different
+// streams never share one, nested entry points on one stream use different
+// uses, and a block is only freed (to grow it) after its own stream has
+// drained.
 struct WsEntry {
     int dev;
     hipStream_t stream;
+    WsUse use;
     void *ptr;
     size_t size;
+    unsigned long long last;   // g_ws_tick at the last reserve
 };
 constexpr int kMaxWs = 64;
 std::mutex g_ws_mu;
 WsEntry g_ws[kMaxWs];
 int g_ws_n = 0;
+unsigned long long g_ws_tick = 0;
+
+// Frees entry i (its device drained first: the entry's stream may be gone)
+// and removes it from the table. Called under g_ws_mu.
+void ws_drop(int i) {
+    WsEntry &e = g_ws[i];
+    if (e.ptr) {
+        int cur = 0;
+        (void)hipGetDevice(&cur);
+        if (e.dev != cur) (void)hipSetDevice(e.dev);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(e.ptr);
+        if (e.dev != cur) (void)hipSetDevice(cur);
+    }
+    g_ws[i] = g_ws[--g_ws_n];
+}
 }  // namespace
 
-void *Workspace::reserve(size_t bytes, hipStream_t stream) {
+void *Workspace::reserve(size_t bytes, hipStream_t stream, WsUse use, bool *fresh, size_t *got) {
     std::lock_guard<std::mutex> guard(g_ws_mu);
+    if (fresh) *fresh = false;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
         set_error("workspace: no current HIP device");
         return nullptr;
     }
-    WsEntry *e = nullptr;
+    int idx = -1;
     for (int i = 0; i < g_ws_n; ++i)
-        if (g_ws[i].dev == dev && g_ws[i].stream == stream) e = &g_ws[i];
-    if (!e) {
+        if (g_ws[i].dev == dev && g_ws[i].stream == stream && g_ws[i].use == use) idx = i;
+    if (idx < 0) {
         if (g_ws_n == kMaxWs) {
-            set_error("workspace: more than %d (device, stream) pairs; pass a workspace", kMaxWs);
-            return nullptr;
+            // Evict the least recently used block of another (device, stream):
+            // blocks of this stream may be in use by the calling entry point.
+            int lru = -1;
+            for (int i = 0; i < g_ws_n; ++i)
+                if (!(g_ws[i].dev == dev && g_ws[i].stream == stream) &&
+                    (lru < 0 || g_ws[i].last < g_ws[lru].last))
+                    lru = i;
+            if (lru < 0) {
+                set_error("workspace: table full");
+                return nullptr;
+            }
+            ws_drop(lru);
         }
-        e = &g_ws[g_ws_n++];
-        *e = WsEntry{dev, stream, nullptr, 0};
+        idx = g_ws_n++;
+        g_ws[idx] = WsEntry{dev, stream, use, nullptr, 0, 0};
     }
-    if (e->size >= bytes && e->ptr) return e->ptr;
+    WsEntry *e = &g_ws[idx];
+    e->last = ++g_ws_tick;
+    if (e->size >= bytes && e->ptr) {
+        if (got) *got = e->size;
+        return e->ptr;
+    }
     if (e->ptr) {
         (void)hipStreamSynchronize(stream);   // earlier kernels on this stream may use the old block
         (void)hipFree(e->ptr);
         e->ptr = nullptr;
         e->size = 0;
     }
-    const size_t want = align_up(bytes, size_t(1) << 20);
+    const size_t want = align_up(bytes > 0 ? bytes : 1, size_t(1) << 20);
     void *p = nullptr;
     if (hipMalloc(&p, want) != hipSuccess) {
         (void)hipGetLastError();
@@ -218,7 +265,44 @@ void *Workspace::reserve(size_t bytes, hipStream_t stream) {
     }
     e->ptr = p;
     e->size = want;
+    if (fresh) *fresh = true;
+    if (got) *got = want;
     return p;
+}
+
+size_t Workspace::release(hipStream_t stream) {
+    std::lock_guard<std::mutex> guard(g_ws_mu);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    size_t freed = 0;
+    bool synced = false;
+    for (int i = g_ws_n - 1; i >= 0; --i) {
+        if (g_ws[i].dev != dev || g_ws[i].stream != stream) continue;
+        if (!synced) {
+            (void)hipStreamSynchronize(stream);
+            synced = true;
+        }
+        freed += g_ws[i].size;
+        (void)hipFree(g_ws[i].ptr);
+        g_ws[i] = g_ws[--g_ws_n];
+    }
+    return freed;
+}
+
+void *Workspace::find(hipStream_t stream, WsUse use) {
+    std::lock_guard<std::mutex> guard(g_ws_mu);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    for (int i = 0; i < g_ws_n; ++i)
+        if (g_ws[i].dev == dev && g_ws[i].stream == stream && g_ws[i].use == use) return g_ws[i].ptr;
+    return nullptr;
+}
+
+size_t Workspace::held() {
+    std::lock_guard<std::mutex> guard(g_ws_mu);
+    size_t total = 0;
+    for (int i = 0; i < g_ws_n; ++i) total += g_ws[i].size;
+    return total;
 }
 
 namespace {

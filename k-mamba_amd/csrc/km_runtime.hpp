@@ -40,14 +40,45 @@ struct PinnedStaging {
     static void *reserve(size_t bytes);      // nullptr on failure (error set)
 };
 
+// What a workspace block is for. Each use has its own block, so an entry
+// point that holds one block (the Mamba-1 block's activations) can call
+// another that reserves scratch (the Scan1D split's segment states) on the
+// same stream without the two aliasing.
+enum class WsUse : int {
+    Scan1DSplit = 0,   // segment end states, incoming states, flags
+    Scan1DBwd,         // checkpoints and per-workgroup partial sums
+    Scan1DM1,          // M = 1 backward's per-workgroup ddelta partials
+    ScanNDPlan,        // per-level fallback's plan offsets
+    ScanNDM3,          // Mamba-3 branch: plan offsets and rotated states
+    ScanNDFlow,        // dataflow counters, status, epoch and flags (kept)
+    ScanNDBwd,         // adjoint plan, neighbours, partials
+    ConvBwd,           // dkernel / dbias partial slots
+    Block,             // Mamba-1 block activations
+    Model,             // stacked model activations, head, logits
+    Count
+};
+
 // Scratch for kernels that need device memory beyond their inputs and
 // outputs (e.g. the Scan1D backward's partial sums), used when the caller
-// passes no workspace. One block per (device, stream): grows on demand
+// passes no workspace. One block per (device, stream, use): grows on demand
 // (after draining that stream) and is reused by later calls on the same
-// stream, so calls on different streams never share it. Host threads that
-// enqueue on one stream concurrently must serialise their calls.
+// stream, so calls on different streams never share it. When the table is
+// full, the least recently used block of another (device, stream) is freed
+// after its device drains. `fresh` (optional) is set when the returned block
+// was just allocated (its contents are undefined); `got` (optional) receives
+// the block's size, at least `bytes`. Host threads that enqueue
+// on one stream concurrently must serialise their calls.
 struct Workspace {
-    static void *reserve(size_t bytes, hipStream_t stream);   // nullptr on failure (error set)
+    static void *reserve(size_t bytes, hipStream_t stream, WsUse use, bool *fresh = nullptr,
+                         size_t *got = nullptr);   // nullptr on failure (error set)
+    // Frees every block of (current device, stream) after draining the
+    // stream. Returns the bytes freed.
+    static size_t release(hipStream_t stream);
+    // Device bytes held by all blocks (every device and stream).
+    static size_t held();
+    // The block of (current device, stream, use), or nullptr; allocates
+    // nothing.
+    static void *find(hipStream_t stream, WsUse use);
 };
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }

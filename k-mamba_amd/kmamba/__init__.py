@@ -207,6 +207,8 @@ kmamba_backend_select = _decl("kmamba_backend_select", C.c_int, [])
 km_last_error_c = _decl("km_last_error", C.c_char_p, [])
 km_clear_error = _decl("km_clear_error", None, [])
 km_version = _decl("km_version", C.c_char_p, [])
+km_device_bytes_held = _decl("km_device_bytes_held", C.c_size_t, [])
+km_release_stream = _decl("km_release_stream", C.c_size_t, [C.c_void_p])
 
 # --- scans -------------------------------------------------------------------
 scan1d = _decl("scan1d", None, [C.POINTER(ScanParams)])
@@ -507,6 +509,7 @@ mamba_scannd_cuda_forward = _decl("mamba_scannd_cuda_forward", C.c_int, [C.POINT
 km_scannd_fwd_c = _decl("km_scannd_fwd", C.c_int, [C.POINTER(ScanNDParams), C.c_void_p])
 km_scannd_fwd_noalloc_c = _decl("km_scannd_fwd_noalloc", C.c_int,
                                   [C.POINTER(ScanNDParams), C.c_void_p])
+km_scannd_status_c = _decl("km_scannd_status", C.c_int, [C.c_void_p])
 scan2d = _decl("scan2d", None, [C.POINTER(Scan2DParams)])
 mamba_scan2d_forward = _decl("mamba_scan2d_forward", None, [C.POINTER(Scan2DParams)])
 
@@ -553,6 +556,15 @@ def scannd_fwd(dims, x, A, B, Cm, delta, h, y, stream=None, theta=None, lam=None
     p, keep = scannd_params(dims, x, A, B, Cm, delta, h, y, theta, lam)
     check(km_scannd_fwd_c(C.byref(p), C.c_void_p(stream_handle(stream))), "km_scannd_fwd")
     return keep
+
+
+def scannd_status(stream=None) -> int:
+    """km_scannd_status: waits for the stream; 0 when the latest ScanND
+    forward on it is exact, 1 when a dataflow wait gave up (NaN tiles)."""
+    rc = km_scannd_status_c(C.c_void_p(stream_handle(stream)))
+    if rc < 0:
+        raise RuntimeError(f"km_scannd_status: {km_last_error()}")
+    return rc
 
 
 def scannd_fwd_noalloc(dims, x, A, B, Cm, delta, h, y, stream=None, theta=None, lam=None):

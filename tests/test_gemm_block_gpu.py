@@ -203,7 +203,11 @@ def normwise(got, ref):
 
 @pytest.mark.parametrize("Bsz,L,dim,di,N,dconv,R", [(2, 130, 64, 128, 16, 4, 8),
                                                     (1, 64, 128, 256, 16, 3, 16),
-                                                    (3, 33, 64, 64, 8, 2, 8)])
+                                                    (3, 33, 64, 64, 8, 2, 8),
+                                                    # few channel groups and a long sequence:
+                                                    # the scan splits the sequence and takes
+                                                    # scratch of its own beside the block's
+                                                    (1, 1024, 256, 512, 16, 4, 16)])
 def test_block_vs_composed_oracle(Bsz, L, dim, di, N, dconv, R):
     w = block_weights(dim, di, N, dconv, R, std=0.2)
     x = bf16_round(rng_for("mx", Bsz, L, dim).standard_normal((Bsz, L, dim)).astype(np.float32))

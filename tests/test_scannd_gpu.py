@@ -119,12 +119,18 @@ out = {}
 # Asynchronous entry point: every dataflow wait gives up at once.
 h = torch.zeros((P, D, M), device="cuda"); y = torch.zeros((P, D), device="cuda")
 K.scannd_fwd(dims, *t, h, y)
+out["status_async"] = np.int64(K.scannd_status())
 torch.cuda.synchronize()
 out["y_async"] = y.cpu().numpy()
+# The allocation-free entry point reports the same way.
+h = torch.zeros((P, D, M), device="cuda"); y = torch.zeros((P, D), device="cuda")
+K.scannd_fwd_noalloc(dims, *t, h, y)
+out["status_noalloc"] = np.int64(K.scannd_status())
 # Synchronous entry point: the same failure, then the band schedule.
 h = torch.zeros((P, D, M), device="cuda"); y = torch.zeros((P, D), device="cuda")
 p, keep = K.scannd_params(dims, *t, h, y)
 rc = K.om_scannd_forward(C.byref(p))
+out["status_sync"] = np.int64(K.scannd_status())
 out["rc"] = np.int64(rc); out["y_sync"] = y.cpu().numpy(); out["h_sync"] = h.cpu().numpy()
 np.savez(sys.argv[4], **out)
 print("budget0 done", flush=True)
@@ -156,6 +162,10 @@ def test_dataflow_wait_budget_exhausted_fails_loudly_and_sync_api_recovers(tmp_p
     yr, hr = O.scannd_ref(dims, x, A, B, Cm, dt, nthreads=8, fast=True)
     ya, ha = kappa(dims, x, A, B, Cm, dt)
     assert int(out["rc"]) == 0
+    # km_scannd_status: the failed asynchronous calls report 1; the latest
+    # launch of the synchronous call (its band re-run) is exact.
+    assert int(out["status_async"]) == 1 and int(out["status_noalloc"]) == 1
+    assert int(out["status_sync"]) == 0
     assert_close(out["y_sync"], yr, TOL_F32, "y after re-run", ya)
     assert_close(out["h_sync"], hr, TOL_F32, "h after re-run", ha)
     ya_ = out["y_async"].reshape(dims + (D,))
@@ -169,7 +179,8 @@ def test_dataflow_wait_budget_exhausted_fails_loudly_and_sync_api_recovers(tmp_p
 def test_dataflow_on_two_streams_concurrently():
     # Each (device, stream) pair has its own dataflow flags and counters:
     # launches on two streams back to back, with no synchronisation between
-    # them, both match the oracle.
+    # them, both match the oracle. km_release_stream then frees the two
+    # streams' blocks.
     dims, D, M = (40, 24, 24), 16, 16
     P = int(np.prod(dims))
     sets = [_stable_nd_inputs(dims, D, M, f"nd-streams{i}") for i in range(2)]
@@ -183,11 +194,15 @@ def test_dataflow_on_two_streams_concurrently():
         for (t, h, y), st in zip(outs, streams):
             K.scannd_fwd(dims, *t, h, y, stream=st)
     torch.cuda.synchronize()
+    assert [K.scannd_status(st) for st in streams] == [0, 0]
     for arrs, (t, h, y) in zip(sets, outs):
         yr, hr = O.scannd_ref(dims, *arrs, nthreads=8, fast=True)
         ya, ha = kappa(dims, *arrs)
         assert_close(y.cpu().numpy(), yr, TOL_F32, "y", ya)
         assert_close(h.cpu().numpy(), hr, TOL_F32, "h", ha)
+    held = K.km_device_bytes_held()
+    freed = sum(K.km_release_stream(C.c_void_p(st.cuda_stream)) for st in streams)
+    assert freed > 0 and K.km_device_bytes_held() == held - freed
 
 
 def test_known_answers_all_entry_points():
