@@ -61,7 +61,7 @@ typedef enum {
  * h0          : [B, D, N] fp32 initial state, NULL for zero
  * h_final     : [B, D, N] fp32 final state, may be NULL (may alias h0)
  * h_hist      : [B, L, D, N] fp32 state after every step, may be NULL
- * h_ckpt      : [B, ceil(L/64), D, N] fp32 state after every 64th step (and
+ * h_ckpt      : [B, ceil(L/32), D, N] fp32 state after every 32nd step (and
  *               after the last step), may be NULL: the checkpoints the
  *               backward recomputes states from
  * y may be NULL when only states are wanted.
@@ -92,7 +92,7 @@ typedef struct {
     const float *Dskip;
 } KMScan1DFwd;
 
-#define KM_SCAN1D_CKPT_STEPS 64
+#define KM_SCAN1D_CKPT_STEPS 32
 
 int km_scan1d_fwd(const KMScan1DFwd *a, void *stream);
 

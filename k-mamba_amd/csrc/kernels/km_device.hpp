@@ -10,7 +10,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // Steps between the forward-state checkpoints the Scan1D backward recomputes
 // from (KM_SCAN1D_CKPT_STEPS of the public header).
-constexpr int kCkptSteps = 64;
+constexpr int kCkptSteps = 32;
 
 // Element type tags. Storage is fp32 or bfloat16; arithmetic is always fp32.
 struct f32_t  { using storage = float; };

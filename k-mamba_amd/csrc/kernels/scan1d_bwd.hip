@@ -55,7 +55,7 @@ struct Scan1DBwdArgs {
     long nck;
     void *dx, *ddt;        // [B, L, D]
     float *dApart;         // [B, D, N] per-batch dA partials (every element written)
-    float *slotB, *slotC;  // shared B/C: [B, G, L, N] per-channel-group partials
+    float *slot;           // shared B/C: [B, G, L, 2, N] per-channel-group partials (dB, dC)
     long G;                // channel groups per batch element (shared B/C slots)
     void *dB, *dC;         // per-channel B/C: written at the B/C strides
     long B, L, D, N, sb, st, sd;
@@ -123,17 +123,58 @@ __device__ __forceinline__ void pow_chain_b(float e1, int n0, float (&e)[NPL]) {
     for (int j = 1; j < NPL; ++j) e[j] = e[j - 1] * e1;
 }
 
-template <typename T, int NPL, int NS, int W, int TC, bool SHARED, bool HIN, int OCC>
-__global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs p) {
+// Register-blocked backward. A workgroup of W = 8 waves owns one (batch,
+// channel group) and walks the sequence backwards in super-chunks of
+// W * TC = 32 steps (the forward's checkpoint spacing), one wave per TC = 4
+// steps. The launch bound keeps a wave within 128 VGPRs, so two workgroups
+// share a CU and one's barriers and folds overlap the other's arithmetic.
+// Per super-chunk, between two barriers:
+//   A  decays, the forward local pass from a zero state and the adjoint
+//      local pass (reverse) from a zero adjoint; their chunk maps (shared P)
+//      go to LDS;
+//   F  the forward fold from the checkpoint (waves 0..NPL-1, one state
+//      each) and the adjoint fold from the carried adjoint (waves
+//      NPL..2*NPL-1), writing each wave's incoming state and adjoint over
+//      its own map in LDS; the folds also bound |h| over the super-chunk
+//      for the clamp check;
+//   R  the forward replay from the exact incoming state, then the adjoint
+//      replay forming every gradient term.
+// With N = 16 the shared dB / dC channel sums go through a per-wave LDS
+// block: each step's products are written as rows, and every two steps
+// each lane adds one (step, gradient, state) column over the wave's 16
+// channels in channel order. Other N use the in-wave reduce-scatter.
+template <typename T, int NPL, int NS, bool SHARED, bool HIN>
+__global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
     using IO = bio<T>;
+    constexpr int W = 8, TC = 4;
     constexpr int DL = 64 / NS;
     constexpr int N = NPL * NS;
     constexpr int SC = W * TC;
     static_assert(SC == kCkptSteps, "backward super-chunks follow the forward checkpoints");
+    static_assert(2 * NPL <= W, "one fold per wave");
     constexpr int TILE = SC * N;
     constexpr int NT = 64 * W;
     constexpr int TPT = (TILE + NT - 1) / NT;
     constexpr int TS = IO::size;
+    // LDS channel sums (N = 16): RS = 2 steps per round, 2 gradients, 16
+    // states: 64 sums, one per lane, each over the DL = 16 channels. A
+    // (step, gradient) block holds, per state group ns, the NPL states of
+    // every channel contiguously ([ns][dl][NPL], groups padded by 4 floats):
+    // a wave's 128-bit row writes cover consecutive 16-byte words, and the
+    // column reads of 16 lanes (states n) fall in 16 distinct banks, the
+    // next 16 lanes' block 16 banks further (block size = 16 mod 32).
+    // The rows hold the factors that vary with the state, ah for dB and h
+    // for dC; the per-channel factors u = delta*x and dy of each step go to
+    // a vector block RVEC ([step][gradient][channel]; the NS lanes of a
+    // channel store the same value), and the column reader forms
+    // sum_c row[c] * vec[c] with one fma per channel.
+    constexpr bool LRED = SHARED && N == 16 && NS == 4;
+    constexpr int RS = 2;
+    constexpr int RGRP = DL * NPL + 4;
+    constexpr int RBLK = NS * RGRP;
+    constexpr int RVEC = RS * 2 * RBLK;                // vector block offset
+    constexpr int RWAVE = LRED ? RVEC + RS * 2 * DL : 1;
+    static_assert(!LRED || RBLK % 32 == 16, "block offset of the second gradient");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -143,7 +184,8 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
     const int n0 = ns * NPL;
     const long ngroups = (p.D + DL - 1) / DL;
     const long b = blockIdx.x / ngroups;
-    const long d = (blockIdx.x - b * ngroups) * DL + dl;
+    const long grp = blockIdx.x - b * ngroups;
+    const long d = grp * DL + dl;
     const bool dvalid = d < p.D;
     const int dc = static_cast<int>(dvalid ? d : p.D - 1);
     const int L = static_cast<int>(p.L);
@@ -177,49 +219,70 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
     // Output offsets of lanes that own no output get bit 31 set: past every
     // window, so the range check drops those stores without a branch.
     constexpr unsigned kDrop = 0x80000000u;
-    constexpr int GRP = DL / NPL;   // lanes per reduced B/C gradient value
+    constexpr int GRP = DL / NPL;   // lanes per reduced B/C gradient value (reduce-scatter)
     const unsigned vxs = own_x ? static_cast<unsigned>(vx) : kDrop;
     // x and dy of lanes past D load as 0: their dB / dC terms (ah*delta*x,
     // dy*h) vanish without a select, and every other output of such a lane
     // is dropped.
     const int vxz = static_cast<int>(dvalid ? static_cast<unsigned>(vx) : kDrop);
     const unsigned vbcs = dvalid ? static_cast<unsigned>(vbc) : kDrop;
+    // This workgroup's partial slot of the shared dB / dC: [L, 2, N] of
+    // [B, G, L, 2, N] (dB then dC of each step), one writer per element.
+    const auto rslot = make_rsrc(SHARED ? p.slot + (b * p.G + grp) * p.L * 2 * N : nullptr,
+                                 SHARED ? p.L * 2 * N * 4 : 0);
+    // Reduce-scatter path: lane l holds state n0 + (l % DL) / GRP of step t.
     const unsigned vacc = (dl % GRP) == 0 ? static_cast<unsigned>((n0 + dl / GRP) * 4) : kDrop;
-    // This workgroup's partial slot of the shared dB / dC: [L, N] of
-    // [B, G, L, N], one writer per element.
-    const long slot0 = (b * p.G + (blockIdx.x - b * ngroups)) * p.L * N;
-    const auto racB = make_rsrc(SHARED ? p.slotB + slot0 : nullptr, SHARED ? p.L * N * 4 : 0);
-    const auto racC = make_rsrc(SHARED ? p.slotC + slot0 : nullptr, SHARED ? p.L * N * 4 : 0);
+    // LDS path: lane l sums column (step ri, gradient gi, state ni) of a round.
+    const int ri = lane >> 5, gi = (lane >> 4) & 1, ni = lane & 15;
 
     __shared__ float sB[SHARED ? 3 : 1][SHARED ? TILE : 1];
     __shared__ float sC[SHARED ? 3 : 1][SHARED ? TILE : 1];
-    __shared__ float aggP[W][NPL][64];
-    __shared__ float aggH[W][NPL][64];
-    __shared__ float pin[W][NPL][64];       // incoming forward state, then incoming adjoint
-    __shared__ float acar[2][NPL][64];      // adjoint carried between super-chunks
+    __shared__ float aggP[W][NPL][64];                 // chunk decay products
+    __shared__ float aggF[HIN ? 1 : W][NPL][64];       // forward maps, then incoming states
+    __shared__ float aggA[W][NPL][64];                 // adjoint maps, then incoming adjoints
+    __shared__ float lmx[HIN ? 1 : W][64];             // max |local state| (inf: no bound)
+    __shared__ float acar[2][NPL][64];                 // adjoint carried between super-chunks
+    __shared__ __align__(16) float red[LRED ? W : 1][RWAVE];
+    __shared__ int s_bad;                              // some bound failed: clamped re-run
 
-    float Ap[NPL], Ar[NPL];
+    // Decays exp2((delta * log2 e) * A): the first product once per step.
+    float Ar[NPL];
+    bool apos = false;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
         Ar[j] = p.A[dc * N + n0 + j];
-        Ap[j] = Ar[j] * kLog2e;
+        apos = apos || !(Ar[j] <= 0.f);
     }
-    const float A0p = p.A[dc * N] * kLog2e;
-    // The squaring ladder of pow_chain_b covers any n0; it is used where n0
-    // is 0 or a power of two (N <= 8 with the 4-state lanes). For N = 16 the
-    // lane with n0 = 12 keeps the workgroup on one exp per state, which
-    // measured faster on gfx950 than this chain or one with a second exp
-    // for the lane's first power.
-    bool structured = (n0 == 0 || (n0 & (n0 - 1)) == 0);
+    // Structured decays (A[d,n] == (n+1)*A[d,0], the S4D-real form) need
+    // fewer exps: with N <= 8 one exp per step and a power chain where n0
+    // is 0 or a power of two; with four state groups (N = 16) a second exp
+    // gives each lane its first power e1^(n0+1), and the lane's other
+    // states follow by multiplying with e1.
+    bool structured = (NS == 4) || (n0 == 0 || (n0 & (n0 - 1)) == 0);
 #pragma unroll
     for (int j = 0; j < NPL; ++j)
         structured = structured && (Ar[j] == static_cast<float>(n0 + j + 1) * p.A[dc * N]);
+    const float A0p = p.A[dc * N] * kLog2e;
+    const float Afp = static_cast<float>(n0 + 1) * A0p;   // log2 of the lane's first power
     const bool fast = __builtin_amdgcn_readfirstlane(__syncthreads_and(structured)) != 0;
+    // Decays of one step (or of a sum of steps) of delta dv in the
+    // structured form.
+    auto decay_chain = [&](float dv, float (&out)[NPL]) __attribute__((always_inline)) {
+        if constexpr (NS == 4) {
+            const float e1 = exp2_fast(dv * A0p);
+            out[0] = exp2_fast(dv * Afp);
+#pragma unroll
+            for (int j = 1; j < NPL; ++j) out[j] = out[j - 1] * e1;
+        } else {
+            pow_chain_b<NPL, NS>(exp2_fast(dv * A0p), n0, out);
+        }
+    };
 
     if (w == 0) {
 #pragma unroll
         for (int j = 0; j < NPL; ++j) acar[0][j][lane] = 0.f;
     }
+    if (tid == 0) s_bad = 0;
 
     float rb[TPT], rc[TPT];
     auto load_tile = [&](int s) {
@@ -251,7 +314,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
             go[k] = IO::ld(rdy, vxz + so, 0);
         }
     };
-    // B or C row of step t (t relative to the super-chunk: r = t - s*SC).
+    // B or C row of step rr of super-chunk s.
     auto bc_row = [&](const float (*tile)[SHARED ? TILE : 1], __amdgpu_buffer_rsrc_t r, int slot,
                       int s, int rr, float (&out)[NPL]) {
         if constexpr (SHARED) {
@@ -264,26 +327,20 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
             for (int j = 0; j < NPL; ++j) out[j] = IO::ld(r, vbc + j * TS + so, 0);
         }
     };
-    // State entering super-chunk s, state j of this lane's group.
+    // Forward state entering super-chunk s, state j (checkpoint or h0).
     auto h_start = [&](int s, int j) -> float {
         if (s == 0) return p.h0 ? p.h0[(b * Dm + dc) * N + n0 + j] : 0.f;
         return p.ckpt[((b * p.nck + (s - 1)) * Dm + dc) * N + n0 + j];
     };
-    // The same for the states j = w + i*W this thread folds, as loads that
-    // are prefetched with the super-chunk's x/delta/dy.
-    constexpr int NJ = (NPL + W - 1) / W;
-    const auto rck = make_rsrc(HIN ? nullptr : p.ckpt + b * p.nck * p.D * p.N,
-                               HIN ? 0 : p.nck * p.D * p.N * 4);
-    const auto rh0 = make_rsrc(p.h0 ? p.h0 + b * p.D * p.N : nullptr, p.h0 ? p.D * p.N * 4 : 0);
-    auto load_ck = [&](int s, float (&o)[NJ]) {
-#pragma unroll
-        for (int i = 0; i < NJ; ++i) {
-            const int j = min(w + i * W, NPL - 1);
-            const int vo = (dc * N + n0 + j) * 4;
-            const float hv = bio<f32_t>::ld(rh0, vo, 0);                           // 0 if no h0
-            const float cv = bio<f32_t>::ld(rck, vo + max(s - 1, 0) * Dm * N * 4, 0);
-            o[i] = (s == 0) ? hv : cv;
-        }
+    // The same for the state this wave folds (wave w < NPL folds state w),
+    // as a load prefetched with the super-chunk's x / delta / dy; super-chunk
+    // 0 starts from h0 (zero when null).
+    const int jf = w < NPL ? w : NPL - 1;
+    const float *ck0 = HIN ? nullptr : p.ckpt + (b * p.nck * Dm + dc) * N + n0 + jf;
+    const float h0v = p.h0 ? p.h0[(b * Dm + dc) * N + n0 + jf] : 0.f;
+    auto load_ck = [&](int s) -> float {
+        const float cv = ck0[static_cast<long>(max(s - 1, 0)) * Dm * N];
+        return (s == 0) ? h0v : cv;
     };
 
     // Prefetches are issued unconditionally (clamped to super-chunk 0, or
@@ -296,100 +353,50 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
         load_tile(max(nit - 2, 0));
     }
     float X0[TC], D0[TC], G0[TC], X1[TC], D1[TC], G1[TC];
-    float K0[NJ], K1[NJ];
+    float K0 = 0.f, K1 = 0.f;
     load_xd(nit - 1, X0, D0, G0);
-    load_ck(nit - 1, K0);
+    if constexpr (!HIN) K0 = load_ck(nit - 1);
     __syncthreads();
 
     float dAacc[NPL];
 #pragma unroll
     for (int j = 0; j < NPL; ++j) dAacc[j] = 0.f;
 
-    // FASTC selects the structured-decay form at compile time (straight-line
-    // bodies for the scheduler).
-    auto body = [&](auto fastc, int it, float (&xs)[TC], float (&ds)[TC], float (&gs)[TC],
-                    float (&ks)[NJ], float (&xn)[TC], float (&dn)[TC], float (&gn)[TC],
-                    float (&kn)[NJ]) __attribute__((always_inline)) {
-        constexpr bool FAST = decltype(fastc)::value;
-        const int s = nit - 1 - it;
-        const int cur = it & 1;
-        const int slot = it % 3;
-        if constexpr (SHARED) {
-            store_tile((it + 1) % 3);    // tile s-1 -> LDS (slot last read in it-2)
-            load_tile(max(s - 2, 0));
-        }
-        load_xd(max(s - 1, 0), xn, dn, gn);
-        load_ck(max(s - 1, 0), kn);
-
-        // ---- forward states of this wave's steps ---------------------------
-        float e[TC][NPL];
-        float hs[TC][NPL];
-        float hin[NPL];
+    // ---- A: decays, forward local pass (FWD) and adjoint local pass -------
+    auto phase_a = [&](auto fwdc, int s, int slot, const float (&xs)[TC], const float (&ds)[TC],
+                       const float (&gs)[TC], float (&e)[TC][NPL]) __attribute__((always_inline)) {
+        constexpr bool FWD = decltype(fwdc)::value;
         float dsum = 0.f;
+        float dmin = ds[0];
+        // The decay form is a wave-uniform branch around these few
+        // instructions, so one loop body serves both.
+        if (fast) {
+#pragma unroll
+            for (int k = 0; k < TC; ++k) decay_chain(ds[k], e[k]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < TC; ++k) {
+                const float dl2 = ds[k] * kLog2e;
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) e[k][j] = exp2_fast(dl2 * Ar[j]);
+            }
+        }
 #pragma unroll
         for (int k = 0; k < TC; ++k) {
             dsum = (k == 0) ? ds[0] : dsum + ds[k];
-            if constexpr (FAST) {
-                pow_chain_b<NPL, NS>(exp2_fast(ds[k] * A0p), n0, e[k]);
-            } else {
-#pragma unroll
-                for (int j = 0; j < NPL; ++j) e[k][j] = exp2_fast(ds[k] * Ap[j]);
-            }
+            dmin = fminf(dmin, ds[k]);
         }
         float P[NPL];
-        if constexpr (FAST) {
-            pow_chain_b<NPL, NS>(exp2_fast(dsum * A0p), n0, P);
+        if (fast) {
+            decay_chain(dsum, P);
         } else {
+            const float sl2 = dsum * kLog2e;
 #pragma unroll
-            for (int j = 0; j < NPL; ++j) P[j] = exp2_fast(Ap[j] * dsum);
+            for (int j = 0; j < NPL; ++j) P[j] = exp2_fast(sl2 * Ar[j]);
         }
-        const int t0 = s * SC + w * TC;
-        if constexpr (HIN) {
-#pragma unroll
-            for (int k = 0; k < TC; ++k) {
-#pragma unroll
-                for (int j = 0; j < NPL; ++j)
-                    hs[k][j] = bio<f32_t>::ld(rh, vh + j * 4 + (t0 + k) * rowh, 0);
-            }
-#pragma unroll
-            for (int j = 0; j < NPL; ++j) {
-                if (t0 > 0) hin[j] = bio<f32_t>::ld(rh, vh + j * 4 + (t0 - 1) * rowh, 0);
-                else hin[j] = p.h0 ? p.h0[(b * Dm + dc) * N + n0 + j] : 0.f;
-            }
-        } else {
-            // Local pass from a zero state, chunk maps, fold from the
-            // checkpoint, replay.
+        if constexpr (FWD) {
             float hl[NPL];
-#pragma unroll
-            for (int k = 0; k < TC; ++k) {
-                float bv[NPL];
-                bc_row(sB, rB, slot, s, w * TC + k, bv);
-                const float u = ds[k] * xs[k];
-#pragma unroll
-                for (int j = 0; j < NPL; ++j) hl[j] = (k == 0) ? bv[j] * u : fmaf(e[k][j], hl[j], bv[j] * u);
-            }
-#pragma unroll
-            for (int j = 0; j < NPL; ++j) {
-                aggP[w][j][lane] = P[j];
-                aggH[w][j][lane] = hl[j];
-            }
-            __syncthreads();
-#pragma unroll
-            for (int i = 0; i < NJ; ++i) {
-                const int j = w + i * W;
-                if (j >= NPL) break;
-                float run = ks[i];
-#pragma unroll
-                for (int v = 0; v < W; ++v) {
-                    pin[v][j][lane] = run;
-                    run = fmaf(aggP[v][j][lane], run, aggH[v][j][lane]);
-                }
-            }
-            __syncthreads();
-            float hmax = 0.f;
-            bool nan_seen = false;
-#pragma unroll
-            for (int j = 0; j < NPL; ++j) hin[j] = pin[w][j][lane];
+            float lm = 0.f;
 #pragma unroll
             for (int k = 0; k < TC; ++k) {
                 float bv[NPL];
@@ -397,55 +404,16 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
                 const float u = ds[k] * xs[k];
 #pragma unroll
                 for (int j = 0; j < NPL; ++j) {
-                    const float prev = (k == 0) ? hin[j] : hs[k - 1][j];
-                    hs[k][j] = fmaf(e[k][j], prev, bv[j] * u);
-                    hmax = fmaxf(hmax, fabsf(hs[k][j]));
+                    hl[j] = (k == 0) ? bv[j] * u : fmaf(e[k][j], hl[j], bv[j] * u);
+                    lm = fmaxf(lm, fabsf(hl[j]));
                 }
             }
-            // A NaN state stays NaN through every later step of the chunk
-            // (e * NaN + bu), so the chunk's last states show it.
 #pragma unroll
-            for (int j = 0; j < NPL; ++j) nan_seen |= (hs[TC - 1][j] != hs[TC - 1][j]);
-            const int bad = p.clamp && (nan_seen || hmax > 1000.f);
-            if (__syncthreads_or(bad)) {
-                // Sequential clamped recurrence from the checkpoint, in the
-                // forward fallback's arithmetic order.
-                float h[NPL];
-#pragma unroll
-                for (int j = 0; j < NPL; ++j) h[j] = h_start(s, j);
-                for (int r = 0; r < w * TC; ++r) {
-                    const int so = (s * SC + r) * rowx;
-                    const float xv = IO::ld(rx, vx + so, 0), dv = IO::ld(rdt, vx + so, 0);
-                    float bv[NPL];
-                    bc_row(sB, rB, slot, s, r, bv);
-#pragma unroll
-                    for (int j = 0; j < NPL; ++j) {
-                        const float ee = exp2_fast(dv * Ap[j]);
-                        float hn = __fadd_rn(__fmul_rn(ee, h[j]), __fmul_rn(__fmul_rn(bv[j], dv), xv));
-                        hn = (hn < 1000.f) ? hn : 1000.f;
-                        h[j] = (hn > -1000.f) ? hn : -1000.f;
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < NPL; ++j) hin[j] = h[j];
-#pragma unroll
-                for (int k = 0; k < TC; ++k) {
-                    float bv[NPL];
-                    bc_row(sB, rB, slot, s, w * TC + k, bv);
-#pragma unroll
-                    for (int j = 0; j < NPL; ++j) {
-                        const float ee = exp2_fast(ds[k] * Ap[j]);
-                        float hn = __fadd_rn(__fmul_rn(ee, h[j]),
-                                             __fmul_rn(__fmul_rn(bv[j], ds[k]), xs[k]));
-                        hn = (hn < 1000.f) ? hn : 1000.f;
-                        h[j] = (hn > -1000.f) ? hn : -1000.f;
-                        hs[k][j] = h[j];
-                    }
-                }
-            }
+            for (int j = 0; j < NPL; ++j) aggF[w][j][lane] = hl[j];
+            // |h| <= |h_in| + |local state| holds while every decay is <= 1
+            // (A <= 0, delta >= 0); otherwise no bound (inf).
+            lmx[w][lane] = (apos || !(dmin >= 0.f)) ? __builtin_inff() : lm;
         }
-
-        // ---- adjoint: local reverse pass, fold, replay with gradients ------
         float g[NPL];
 #pragma unroll
         for (int j = 0; j < NPL; ++j) g[j] = 0.f;
@@ -458,25 +426,73 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
         }
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
-            if constexpr (HIN) aggP[w][j][lane] = P[j];
-            aggH[w][j][lane] = g[j];
+            aggP[w][j][lane] = P[j];
+            aggA[w][j][lane] = g[j];
         }
-        __syncthreads();
-        for (int j = w; j < NPL; j += W) {
+    };
+
+    // ---- F: folds (wave w < NPL: forward state w from the checkpoint ks;
+    // NPL <= w < 2 NPL: adjoint state w - NPL). The forward fold also
+    // bounds |h| over the super-chunk: a bound above 1000 (or not finite)
+    // marks the workgroup for the clamped re-run. ----------------------------
+    auto phase_f = [&](auto fwdc, int cur, float ks) __attribute__((always_inline)) {
+        constexpr bool FWD = decltype(fwdc)::value;
+        if (FWD && w < NPL) {
+            const int j = w;
+            float pv[W], hv[W], mv[W];
+#pragma unroll
+            for (int v = 0; v < W; ++v) {
+                pv[v] = aggP[v][j][lane];
+                hv[v] = aggF[v][j][lane];
+                mv[v] = lmx[v][lane];
+            }
+            float run = ks;
+            bool bad = false;
+#pragma unroll
+            for (int v = 0; v < W; ++v) {
+                aggF[v][j][lane] = run;
+                bad = bad || !(fabsf(run) + mv[v] <= 1000.f);
+                run = fmaf(pv[v], run, hv[v]);
+            }
+            bad = bad || !(fabsf(run) <= 1000.f);
+            if (p.clamp && bad) s_bad = 1;
+        } else if (w >= NPL && w < 2 * NPL) {
+            const int j = w - NPL;
+            float pv[W], gv[W];
+#pragma unroll
+            for (int v = 0; v < W; ++v) {
+                pv[v] = aggP[v][j][lane];
+                gv[v] = aggA[v][j][lane];
+            }
             float run = acar[cur][j][lane];
 #pragma unroll
             for (int v = W - 1; v >= 0; --v) {
-                pin[v][j][lane] = run;
-                run = fmaf(aggP[v][j][lane], run, aggH[v][j][lane]);
+                aggA[v][j][lane] = run;
+                run = fmaf(pv[v], run, gv[v]);
             }
             acar[cur ^ 1][j][lane] = run;
         }
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < NPL; ++j) g[j] = pin[w][j][lane];
+    };
 
+    // ---- R (second half): adjoint replay from the exact incoming adjoint,
+    // forming every gradient term -------------------------------------------
+    // hin_lds: the incoming states are still in aggF (main pass, no
+    // history): read them at the last step instead of holding registers.
+    auto grad_replay = [&](auto hin_ldsc, int s, int slot, const float (&xs)[TC],
+                           const float (&ds)[TC], const float (&gs)[TC],
+                           const float (&e)[TC][NPL], const float (&hs)[TC][NPL],
+                           const float (&hin)[NPL]) __attribute__((always_inline)) {
+        constexpr bool HIN_LDS = decltype(hin_ldsc)::value;
+        const int t0 = s * SC + w * TC;
+        float g[NPL];
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) g[j] = aggA[w][j][lane];
+        float *rw = &red[LRED ? w : 0][0];
 #pragma unroll
         for (int k = TC - 1; k >= 0; --k) {
+            // One step at a time: operand reads of later steps hoisted here
+            // would push the wave past its 128 registers.
+            __builtin_amdgcn_sched_barrier(0);
             const int t = t0 + k;
             float bv[NPL], cv[NPL];
             bc_row(sB, rB, slot, s, w * TC + k, bv);
@@ -484,20 +500,17 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
             const float dtk = ds[k], xk = xs[k], gk = gs[k];
             const float u = dtk * xk;
             float sa = 0.f, sbv = 0.f;
-            float dBv[NPL], dCv[NPL];
+            float ahv[NPL];
 #pragma unroll
             for (int j = 0; j < NPL; ++j) {
                 const float ah = fmaf(gk, cv[j], g[j]);
-                const float hp = (k == 0) ? hin[j] : hs[k - 1][j];
+                const float hp = (k > 0) ? hs[k - 1][j] : HIN_LDS ? aggF[HIN ? 0 : w][j][lane] : hin[j];
                 const float ae = ah * e[k][j];
                 const float q = ae * hp;
                 dAacc[j] = fmaf(dtk, q, dAacc[j]);
                 sa = fmaf(Ar[j], q, sa);
                 sbv = fmaf(ah, bv[j], sbv);
-                // Lanes past D have x = dy = 0 (so u = gk = 0 and ah = 0): they
-                // add nothing to the channel sums.
-                dBv[j] = ah * u;
-                dCv[j] = gk * hs[k][j];
+                ahv[j] = ah;
                 g[j] = ae;
             }
             // Sum the state groups of the channel (lanes dl + DL*ns), both
@@ -520,45 +533,195 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_bwd_chunked(Scan1DBwdArgs 
             const int xo = static_cast<int>(vxs + static_cast<unsigned>(t * rowx));
             IO::st(rdx, xo, 0, dtk * sbv);
             IO::st(rdd, xo, 0, fmaf(xk, sbv, sa));
-            if constexpr (SHARED) {
+            if constexpr (LRED) {
+                // This step's rows: lane (dl, ns) writes its NPL states of ah
+                // and of h; the state-group-0 lanes write u and dy of their
+                // channel. Lanes past D have x = dy = 0 (u = dy = 0): they add
+                // nothing to the channel sums.
+                const int rk = (TC - 1 - k) % RS;
+                float *row = rw + (rk * 2) * RBLK + ns * RGRP + dl * NPL;
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) {
+                    row[j] = ahv[j];
+                    row[RBLK + j] = hs[k][j];
+                }
+                float *vec = rw + RVEC + rk * 2 * DL + dl;   // same value from every state group
+                vec[0] = u;
+                vec[DL] = gk;
+                if (rk == RS - 1) {
+                    // Column (ri, gi, ni) against its vector, channel by
+                    // channel in order; step ri of the round is
+                    // t + RS - 1 - ri.
+                    const float *col = rw + (ri * 2 + gi) * RBLK + (ni / NPL) * RGRP + ni % NPL;
+                    const float *cvec = rw + RVEC + (ri * 2 + gi) * DL;
+                    float acc = col[0] * cvec[0];
+#pragma unroll
+                    for (int c = 1; c < DL; ++c) acc = fmaf(col[c * NPL], cvec[c], acc);
+                    const int tt = t + RS - 1 - ri;
+                    bio<f32_t>::st(rslot, ((tt * 2 + gi) * N + ni) * 4, 0, acc);
+                }
+            } else if constexpr (SHARED) {
+                float dBv[NPL], dCv[NPL];
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) {
+                    dBv[j] = ahv[j] * u;
+                    dCv[j] = gk * hs[k][j];
+                }
                 // Sum over the wave's channels; lane l then holds state
                 // n0 + (l % DL) / (DL / NPL) of step t.
                 const float rbv = reduce_scatter<NPL, DL>(dBv, lane);
                 const float rcv = reduce_scatter<NPL, DL>(dCv, lane);
-                const int ao = static_cast<int>(vacc + static_cast<unsigned>(t * N * 4));
-                bio<f32_t>::st(racB, ao, 0, rbv);
-                bio<f32_t>::st(racC, ao, 0, rcv);
+                const int ao = static_cast<int>(vacc + static_cast<unsigned>(t * 2 * N * 4));
+                bio<f32_t>::st(rslot, ao, 0, rbv);
+                bio<f32_t>::st(rslot, ao + N * 4, 0, rcv);
             } else {
 #pragma unroll
                 for (int j = 0; j < NPL; ++j) {
                     const int bo = static_cast<int>(vbcs + static_cast<unsigned>(j * TS + t * rowbc));
-                    IO::st(rdB, bo, 0, dBv[j]);
-                    IO::st(rdC, bo, 0, dCv[j]);
+                    IO::st(rdB, bo, 0, ahv[j] * u);
+                    IO::st(rdC, bo, 0, gk * hs[k][j]);
                 }
             }
         }
     };
 
-    auto run = [&](auto fastc) __attribute__((always_inline)) {
-        for (int it = 0; it < nit; it += 2) {
-            body(fastc, it, X0, D0, G0, K0, X1, D1, G1, K1);
-            if (it + 1 < nit) body(fastc, it + 1, X1, D1, G1, K1, X0, D0, G0, K0);
+    // One super-chunk of the main pass: the forward states come from the
+    // history (HIN) or from the checkpoint by local pass, fold and replay,
+    // unclamped; the next super-chunk's operands are prefetched.
+    auto body = [&](int it, float (&xs)[TC], float (&ds)[TC], float (&gs)[TC],
+                    float ks, float (&xn)[TC], float (&dn)[TC], float (&gn)[TC],
+                    float &kn) __attribute__((always_inline)) {
+        const int s = nit - 1 - it;
+        const int cur = it & 1;
+        const int slot = it % 3;
+        if constexpr (SHARED) {
+            store_tile((it + 1) % 3);    // tile s-1 -> LDS (slot last read in it-2)
+            load_tile(max(s - 2, 0));
         }
+        load_xd(max(s - 1, 0), xn, dn, gn);
+        if constexpr (!HIN) kn = load_ck(max(s - 1, 0));
+        float e[TC][NPL];
+        phase_a(std::integral_constant<bool, !HIN>{}, s, slot, xs, ds, gs, e);
+        __syncthreads();
+        phase_f(std::integral_constant<bool, !HIN>{}, cur, ks);
+        __syncthreads();
+        const int t0 = s * SC + w * TC;
+        float hs[TC][NPL];
+        float hin[NPL];
+        if constexpr (HIN) {
+#pragma unroll
+            for (int k = 0; k < TC; ++k) {
+#pragma unroll
+                for (int j = 0; j < NPL; ++j)
+                    hs[k][j] = bio<f32_t>::ld(rh, vh + j * 4 + (t0 + k) * rowh, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) {
+                if (t0 > 0) hin[j] = bio<f32_t>::ld(rh, vh + j * 4 + (t0 - 1) * rowh, 0);
+                else hin[j] = p.h0 ? p.h0[(b * Dm + dc) * N + n0 + j] : 0.f;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < TC; ++k) {
+                float bv[NPL];
+                bc_row(sB, rB, slot, s, w * TC + k, bv);
+                const float u = ds[k] * xs[k];
+#pragma unroll
+                for (int j = 0; j < NPL; ++j)
+                    hs[k][j] = fmaf(e[k][j], (k == 0) ? aggF[HIN ? 0 : w][j][lane] : hs[k - 1][j],
+                                    bv[j] * u);
+            }
+        }
+        grad_replay(std::integral_constant<bool, !HIN>{}, s, slot, xs, ds, gs, e, hs, hin);
     };
-    if (fast) run(std::true_type{});
-    else run(std::false_type{});
+
+    // One super-chunk of the clamped re-run: operands loaded in place, the
+    // tile staged synchronously, and each wave's forward states recomputed
+    // from the checkpoint with the sequential clamped recurrence in the
+    // forward fallback's arithmetic order.
+    auto body_rerun = [&](int it) __attribute__((always_inline)) {
+        const int s = nit - 1 - it;
+        const int cur = it & 1;
+        __syncthreads();                 // the previous super-chunk's tile reads are done
+        if constexpr (SHARED) {
+            load_tile(s);
+            store_tile(0);
+        }
+        float xs[TC], ds[TC], gs[TC];
+        load_xd(s, xs, ds, gs);
+        __syncthreads();
+        float e[TC][NPL];
+        phase_a(std::false_type{}, s, 0, xs, ds, gs, e);
+        __syncthreads();
+        phase_f(std::false_type{}, cur, 0.f);
+        __syncthreads();
+        float hs[TC][NPL];
+        float hin[NPL];
+        float h[NPL];
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) h[j] = h_start(s, j);
+        for (int r = 0; r < w * TC; ++r) {
+            const int so = (s * SC + r) * rowx;
+            const float xv = IO::ld(rx, vx + so, 0), dv = IO::ld(rdt, vx + so, 0);
+            float bv[NPL];
+            bc_row(sB, rB, 0, s, r, bv);
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) {
+                const float ee = exp2_fast(dv * (Ar[j] * kLog2e));
+                float hn = __fadd_rn(__fmul_rn(ee, h[j]), __fmul_rn(__fmul_rn(bv[j], dv), xv));
+                hn = (hn < 1000.f) ? hn : 1000.f;
+                h[j] = (hn > -1000.f) ? hn : -1000.f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) hin[j] = h[j];
+#pragma unroll
+        for (int k = 0; k < TC; ++k) {
+            float bv[NPL];
+            bc_row(sB, rB, 0, s, w * TC + k, bv);
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) {
+                const float ee = exp2_fast(ds[k] * (Ar[j] * kLog2e));
+                float hn = __fadd_rn(__fmul_rn(ee, h[j]), __fmul_rn(__fmul_rn(bv[j], ds[k]), xs[k]));
+                hn = (hn < 1000.f) ? hn : 1000.f;
+                h[j] = (hn > -1000.f) ? hn : -1000.f;
+                hs[k][j] = h[j];
+            }
+        }
+        grad_replay(std::false_type{}, s, 0, xs, ds, gs, e, hs, hin);
+    };
+
+    for (int it = 0; it < nit; it += 2) {
+        body(it, X0, D0, G0, K0, X1, D1, G1, K1);
+        if (it + 1 < nit) body(it + 1, X1, D1, G1, K1, X0, D0, G0, K0);
+    }
+    if constexpr (!HIN) {
+        // Some super-chunk's states may have left [-1000, 1000]: every
+        // output of this workgroup again, with the clamped states.
+        __syncthreads();
+        if (__builtin_amdgcn_readfirstlane(s_bad) != 0) {
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) dAacc[j] = 0.f;
+            if (w == 0) {
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) acar[0][j][lane] = 0.f;
+            }
+            for (int it = 0; it < nit; ++it) body_rerun(it);
+        }
+    }
 
     // dA: the waves' sums over their steps, added in wave order, one
     // store per (batch, channel, state).
+    __syncthreads();
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) aggH[w][j][lane] = dAacc[j];
+    for (int j = 0; j < NPL; ++j) aggA[w][j][lane] = dAacc[j];
     __syncthreads();
     if (w == 0 && dvalid) {
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
-            float acc = aggH[0][j][lane];
+            float acc = aggA[0][j][lane];
 #pragma unroll
-            for (int v = 1; v < W; ++v) acc += aggH[v][j][lane];
+            for (int v = 1; v < W; ++v) acc += aggA[v][j][lane];
             p.dApart[(b * Dm + d) * N + n0 + j] = acc;
         }
     }
@@ -623,13 +786,13 @@ __global__ void __launch_bounds__(kSerialNB) scan1d_bwd_serial(Scan1DBwdArgs p) 
         }
         if (shared) {
             __syncthreads();
-            const long so = ((b * p.G + g) * p.L + t) * N;
+            const long so = (b * p.G + g) * p.L;   // + t: row of the [L, 2, N] slot
             for (long k = tid; k < 2 * N; k += kSerialNB) {
                 const int which = static_cast<int>(k / N);
                 const long m = k - which * N;
                 float acc = 0.f;
                 for (int i = 0; i < kSerialNB; ++i) acc += red[which][m][i];
-                (which ? p.slotC : p.slotB)[so + m] = acc;
+                p.slot[(so + t) * 2 * N + which * N + m] = acc;
             }
             __syncthreads();
         }
@@ -650,26 +813,26 @@ __global__ void __launch_bounds__(256) fill_zero_kernel(float *p, long n) {
 
 // Fixed-order sums of the partials: dA[i] = sum over b of dApart[b, i]
 // (b ascending); with shared B/C, dB / dC at b*sb + t*st + n = sum over the
-// channel groups g (ascending) of slot[b, g, t, n].
+// channel groups g (ascending) of slot[b, g, t, 0 / 1, n].
 template <typename T>
-__global__ void __launch_bounds__(256) scan1d_bwd_finalize(const float *slotB, const float *slotC,
-                                                           long G, void *dB, void *dC, long B,
-                                                           long L, long N, long sb, long st,
-                                                           const float *dApart, float *dA, long DN) {
+__global__ void __launch_bounds__(256) scan1d_bwd_finalize(const float *slot, long G, void *dB,
+                                                           void *dC, long B, long L, long N,
+                                                           long sb, long st, const float *dApart,
+                                                           float *dA, long DN) {
     using IO = io<T>;
-    const long n_bc = slotB ? B * L * N : 0;
+    const long n_bc = slot ? B * L * N : 0;
     const long LN = L * N;
+    const long S = 2 * LN;   // floats per (b, g) slot
     const long stride = static_cast<long>(gridDim.x) * blockDim.x;
     for (long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_bc + DN;
          i += stride) {
         if (i < n_bc) {
             const long b = i / LN, r = i - b * LN, t = r / N, n = r - t * N;
-            const float *pb = slotB + b * G * LN + r;
-            const float *pc = slotC + b * G * LN + r;
+            const float *pb = slot + b * G * S + t * 2 * N + n;
             float sB = 0.f, sC = 0.f;
             for (long g = 0; g < G; ++g) {
-                sB += pb[g * LN];
-                sC += pc[g * LN];
+                sB += pb[g * S];
+                sC += pb[g * S + N];
             }
             const long o = b * sb + t * st + n;
             IO::st(dB, o, sB);
@@ -761,9 +924,7 @@ static bool bwd_args_ok(const KMScan1DBwd *k, const char *who) {
 
 static int bwd_chunked_launch(const Scan1DBwdArgs &a, bool shared, bool hin, bool bf,
                               hipStream_t s) {
-    constexpr int W = 8, TC = 8;
-    // Four states per lane keep the backward's per-lane working set (decays
-    // and states of 8 steps) within 256 VGPRs without spilling.
+    constexpr int W = 8;
     const long DL = bwd_group_channels(a.N);
     const long grid = a.B * ((a.D + DL - 1) / DL);
     if (grid <= 0 || grid > 0x7fffffffL) {
@@ -774,11 +935,11 @@ static int bwd_chunked_launch(const Scan1DBwdArgs &a, bool shared, bool hin, boo
 #define KM_BWD_GO(TT, NPL, NS)                                                                    \
     do {                                                                                          \
         if (shared) {                                                                             \
-            if (hin) hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, W, TC, true, true, 1>), g, blk, 0, s, a);   \
-            else     hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, W, TC, true, false, 1>), g, blk, 0, s, a);  \
+            if (hin) hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, true, true>), g, blk, 0, s, a);   \
+            else     hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, true, false>), g, blk, 0, s, a);  \
         } else {                                                                                  \
-            if (hin) hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, W, TC, false, true, 1>), g, blk, 0, s, a);  \
-            else     hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, W, TC, false, false, 1>), g, blk, 0, s, a); \
+            if (hin) hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, false, true>), g, blk, 0, s, a);  \
+            else     hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, false, false>), g, blk, 0, s, a); \
         }                                                                                         \
     } while (0)
     switch (a.N) {
@@ -838,10 +999,7 @@ static int scan1d_bwd_run(const KMScan1DBwd *k, const BwdPlan &pl, bool bf, hipS
     // zeroed first.
     a.G = pl.G;
     a.dApart = reinterpret_cast<float *>(ws + pl.off_dA);
-    if (pl.shared) {
-        a.slotB = reinterpret_cast<float *>(ws + pl.off_slots);
-        a.slotC = a.slotB + k->B * pl.G * k->L * k->N;
-    }
+    if (pl.shared) a.slot = reinterpret_cast<float *>(ws + pl.off_slots);
     if (pl.need_ckpt || pl.need_hist) {
         // Forward states from the same inputs (y not written).
         KMScan1DFwd f{};
@@ -873,8 +1031,8 @@ static int scan1d_bwd_run(const KMScan1DBwd *k, const BwdPlan &pl, bool bf, hipS
     const long n = (pl.shared ? k->B * k->L * k->N : 0) + k->D * k->N;
     const long blocks = std::min<long>((n + 255) / 256, 8192);
 #define KM_FIN(TT)                                                                                 \
-    hipLaunchKernelGGL(scan1d_bwd_finalize<TT>, dim3(blocks), dim3(256), 0, stream, a.slotB,      \
-                       a.slotC, pl.G, k->dB, k->dC, k->B, k->L, k->N, k->bc_sb, k->bc_st,         \
+    hipLaunchKernelGGL(scan1d_bwd_finalize<TT>, dim3(blocks), dim3(256), 0, stream, a.slot,       \
+                       pl.G, k->dB, k->dC, k->B, k->L, k->N, k->bc_sb, k->bc_st,                  \
                        a.dApart, k->dA, k->D * k->N)
     if (bf) KM_FIN(bf16_t);
     else    KM_FIN(f32_t);

@@ -399,12 +399,17 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
             for (int v = 0; v < W; ++v) {
                 pin[v][j][lane] = run;
                 run = fmaf(pv[v], run, hv[v]);
+                // Checkpoint after every kCkptSteps-th step (rows past L are
+                // identity steps, so a checkpoint past the end holds the
+                // final state). Launches with checkpoints use super-chunks
+                // that are multiples of kCkptSteps.
+                if (((v + 1) * TC) % kCkptSteps == 0) {   // folded after unrolling
+                    const long c = (static_cast<long>(s) * SC + (v + 1) * TC) / kCkptSteps - 1;
+                    if (p.ckpt && dvalid && c < p.nck)
+                        p.ckpt[((b * p.nck + c) * Dm + d) * N + NS * j + ns] = run;
+                }
             }
             carry[cur ^ 1][j][lane] = run;
-            if constexpr (SC == kCkptSteps) {
-                if (p.ckpt && dvalid && s < nit)
-                    p.ckpt[((b * p.nck + s) * Dm + d) * N + NS * j + ns] = run;
-            }
         }
         __syncthreads();
         // The segment-map pass (DSUM) needs only the outgoing carry: no replay.
@@ -618,7 +623,7 @@ static int scan1d_cfg16() {
 
 template <typename T>
 static int launch_n16(const Scan1DFwdArgs &a, bool shared, bool hist, hipStream_t s) {
-    // Checkpoints are written at super-chunk ends: keep 64-step super-chunks.
+    // Checkpoints are written at 32-step boundaries inside 64-step super-chunks.
     if (!a.ckpt && scan1d_cfg16() == 0) return launch_chunked<T, 8, 2, 8, 8>(a, shared, hist, s);
     return launch_chunked<T, 8, 2, 8, 8, true>(a, shared, hist, s);
 }

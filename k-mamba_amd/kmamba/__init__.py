@@ -97,7 +97,7 @@ class KMScan1DBwd(C.Structure):           # include/kmamba_km.h
                 ("workspace_bytes", C.c_size_t)]
 
 
-KM_SCAN1D_CKPT_STEPS = 64
+KM_SCAN1D_CKPT_STEPS = 32
 KM_EPI_NONE, KM_EPI_SOFTPLUS, KM_EPI_SILU = 0, 1, 2
 
 
@@ -336,7 +336,7 @@ def scan1d_fwd_args(x, delta, A, Bm, Cm, y, *, h0=None, h_final=None, h_hist=Non
     x, delta, y: [B, L, D] (one dtype: fp32 or bf16); A: [D, N] fp32;
     Bm/Cm: [B, L, N] shared over channels (default strides) or any layout
     described by bc_strides = (sb, st, sd) in elements with N contiguous;
-    h0 / h_final [B, D, N], h_hist [B, L, D, N], h_ckpt [B, ceil(L/64), D, N]
+    h0 / h_final [B, D, N], h_hist [B, L, D, N], h_ckpt [B, ceil(L/32), D, N]
     fp32; z [B, L, D] as x; Dskip [D] fp32. Every tensor must be contiguous
     and on the GPU (ValueError otherwise).
     """

@@ -139,6 +139,28 @@ def test_recompute_follows_forward_clamp():
         check_all(got, ref, kap, TOL_F32, f"clamped {mode}")
 
 
+@pytest.mark.parametrize("N", [16, 8])
+def test_recompute_clamp_in_a_few_steps_generic_A(N):
+    # Generic (not S4D-real) decays, and states that leave [-1000, 1000] only
+    # around steps 150-155 of 300: the recomputation from checkpoints must
+    # follow the clamp there and nowhere else, for every output of the
+    # channel groups it touches.
+    Bsz, L, D = 2, 300, 40
+    x, dt, A, Bm, Cm = scan1d_inputs(Bsz, L, D, N, seed=21)
+    g = rng_for("clamp-local", N)
+    A = (A * g.uniform(0.001, 0.01, size=A.shape)).astype(np.float32)
+    Bm = Bm.copy()
+    Bm[:, 150:156] *= 4000.0
+    dy = dy_for(Bsz, L, D)
+    ref, hh = oracle_bwd(x, dt, A, Bm, Cm, dy)
+    assert np.abs(hh).max() == 1000.0
+    assert np.abs(hh[:, :140]).max() < 1000.0
+    kap = scan1d_bwd_kappa(x, dt, A, Bm, Cm, dy)
+    for mode in ("ckpt", "recompute"):
+        got = run_bwd(x, dt, A, Bm, Cm, dy, mode=mode, hist=hh)
+        check_all(got, ref, kap, TOL_F32, f"locally clamped {mode}")
+
+
 def test_bf16_io_against_fp32_oracle():
     x, dt, A, Bm, Cm = scan1d_inputs(2, 256, 64, 16, seed=15)
     dy = dy_for(2, 256, 64)

@@ -307,12 +307,16 @@ def test_scannd_dispatch_1d_is_scan1d_with_running_state():
     np.testing.assert_allclose(h[0], hr[0], rtol=1e-4, atol=1e-5)
 
 
-@pytest.mark.parametrize("dims,D,M,nsel", [((256, 256), 256, 16, 4), ((64, 64, 64), 128, 16, 2)])
-def test_config2_full_size_sampled(dims, D, M, nsel):
-    # configs[2] on the GPU; a sample of channels checked against the oracle
-    # (channels are independent). Inputs per BASELINE: delta = 1, decay
+@pytest.mark.parametrize("dims,D,M", [((256, 256), 256, 16), ((64, 64, 64), 128, 16)])
+def test_config2_full_size_sampled(dims, D, M):
+    # configs[2] on the GPU; one channel of every channel group (64 (d, m)
+    # lanes: 64 // M channels) checked elementwise against the oracle at
+    # every point (channels are independent). Every group, and so every
+    # wave's lane set and, on the 3D dataflow schedule, every XCD's queue
+    # of groups, is compared. Inputs per BASELINE: delta = 1, decay
     # a_k ~ U(0.05, 0.9/ndims) as A = log(a_k), B, C ~ N(0, 1/16), x ~ N(0, 1).
     nd, P = len(dims), int(np.prod(dims))
+    per = 64 // M
     g = rng_for("config2", dims)
     x = g.standard_normal((P, D), dtype=np.float32)
     A = np.log(g.uniform(0.05, 0.9 / nd, (nd, D, M))).astype(np.float32)
@@ -321,7 +325,9 @@ def test_config2_full_size_sampled(dims, D, M, nsel):
     dt = np.ones((nd, P, D), np.float32)
     y, h = run_device(dims, x, A, B, Cm, dt)
     assert np.isfinite(y).all()
-    sel = np.sort(g.choice(D, nsel, replace=False))
+    ngroups = D * M // 64
+    sel = np.arange(ngroups) * per + g.integers(0, per, ngroups)
+    assert len(np.unique(sel // per)) == ngroups
     args = (x[:, sel], A[:, sel], B[:, sel], Cm[:, sel], dt[:, :, sel])
     yr, hr = O.scannd_ref(dims, *args, nthreads=8, fast=True)
     ya, ha = kappa(dims, *args)
