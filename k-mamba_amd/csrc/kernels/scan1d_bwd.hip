@@ -183,8 +183,13 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
     const int ns = lane / DL;
     const int n0 = ns * NPL;
     const long ngroups = (p.D + DL - 1) / DL;
-    const long b = blockIdx.x / ngroups;
-    const long grp = blockIdx.x - b * ngroups;
+    // Workgroups numbered so that consecutive channel groups run on one
+    // XCD: a group's DL channels are only part of each 128-byte row line
+    // of x / delta / dy, and the neighbours that read the rest of the line
+    // then find it in the same L2 instead of fetching it again.
+    const long wg = xcd_remap(blockIdx.x, gridDim.x);
+    const long b = wg / ngroups;
+    const long grp = wg - b * ngroups;
     const long d = grp * DL + dl;
     const bool dvalid = d < p.D;
     const int dc = static_cast<int>(dvalid ? d : p.D - 1);
