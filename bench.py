@@ -385,7 +385,7 @@ def bench_scannd(torch, K, stream, dims, D, M, steps, warmup):
     return {"ms": round(ms, 4), "elems_per_s": P * D / (ms * 1e-3),
             "achieved_GBs": round(alg / (ms * 1e-3) / 1e9, 1),
             "frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "alg_bytes": alg,
-            "launches_per_step": "one per tile band" if nd < 3 else "one dataflow launch"}
+            "launches_per_step": "one dataflow launch (and its flag reset)"}
 
 
 def scannd_bwd_alg_bytes(dims, D, M):

@@ -144,8 +144,14 @@ struct NDRow {
 // its axis-0 neighbours from h. COH: states written by other workgroups of
 // the same launch (the dataflow schedule) are read with agent-coherent loads
 // that bypass the CU's L1.
-template <int ND, int TW, int MM, int PL, bool COH = false>
-__device__ __forceinline__ void scannd_tile(const ScanNDArgs &p, const int (&ti)[kMaxNd], int cg) {
+//
+// wait() runs once the operands of the tile's first rows (which no other
+// tile writes) are in flight and before any state written by another tile
+// is read; when it returns false nothing is computed and the function
+// returns false.
+template <int ND, int TW, int MM, int PL, bool COH = false, typename Wait>
+__device__ __forceinline__ bool scannd_tile(const ScanNDArgs &p, const int (&ti)[kMaxNd], int cg,
+                                            Wait &&wait) {
     constexpr bool RING = (ND == 3 && PL > 0);
     static_assert(PL % 2 == 0, "planes of whole row pairs");
     const int lane = threadIdx.x & 63;
@@ -210,7 +216,7 @@ __device__ __forceinline__ void scannd_tile(const ScanNDArgs &p, const int (&ti)
     // The operand loads are unconditional; only the neighbour-state loads
     // sit under wave-uniform branches (measured: skipping the unneeded ones
     // is 5 % faster in 3D than loading B again in their place).
-    auto load_row = [&](int row, NDRow<ND, TW> &r) {
+    auto load_ops = [&](int row, NDRow<ND, TW> &r) {
         int rem = row;
         int roff = 0;
 #pragma unroll
@@ -231,6 +237,8 @@ __device__ __forceinline__ void scannd_tile(const ScanNDArgs &p, const int (&ti)
 #pragma unroll
             for (int a = 0; a < ND; ++a) r.dt[a][c] = F::ld(rdt[a], voffX[c], sx);
         }
+    };
+    auto load_nbr = [&](NDRow<ND, TW> &r) {
         // Neighbours along leading axes, and along the row axis on the tile's
         // first row of a plane (tile boundary). An unneeded neighbour is not
         // loaded (0; compute_row skips its term). Rows are prefetched one
@@ -239,7 +247,7 @@ __device__ __forceinline__ void scannd_tile(const ScanNDArgs &p, const int (&ti)
         // launcher never builds a tile with a single row per plane below an
         // in-tile leading axis. In 2D the only such neighbour is the row above
         // the tile, which the wave loads into `top` before its first row.
-        const int sh = (roff + static_cast<int>(hback)) * DM * 4;
+        const int sh = (r.base + static_cast<int>(hback)) * DM * 4;
 #pragma unroll
         for (int a = 0; a < (ND == 2 ? 0 : ND - 1); ++a) {
             // Wave-uniform (readfirstlane): a scalar branch around the loads.
@@ -252,19 +260,24 @@ __device__ __forceinline__ void scannd_tile(const ScanNDArgs &p, const int (&ti)
         const bool left = __builtin_amdgcn_readfirstlane(lo[ac] > 0) != 0;
         r.hleft = left ? hld(rh, voffB[0], sh - DM * 4) : 0.f;
     };
+    auto load_row = [&](int row, NDRow<ND, TW> &r) {
+        load_ops(row, r);
+        load_nbr(r);
+    };
 
     float top[TW];
-    if constexpr (ND == 2) {
-        // The row above the tile (from the band before), or 0 on the grid's
-        // first row; h at the tile origin minus one row is the start of rh's
-        // window whenever that row exists (unneeded: B row, cache hit).
-        const bool up = __builtin_amdgcn_readfirstlane(lo[0] > 0) != 0;
 #pragma unroll
-        for (int c = 0; c < TW; ++c) top[c] = hld(up ? rh : rB, voffB[c], 0);
-    } else {
+    for (int c = 0; c < TW; ++c) top[c] = 0.f;
+    // 2D: the row above the tile (from an earlier band), or 0 on the grid's
+    // first row; h at the tile origin minus one row is the start of rh's
+    // window whenever that row exists.
+    auto load_top = [&]() {
+        if constexpr (ND == 2) {
+            const bool up = __builtin_amdgcn_readfirstlane(lo[0] > 0) != 0;
 #pragma unroll
-        for (int c = 0; c < TW; ++c) top[c] = 0.f;
-    }
+            for (int c = 0; c < TW; ++c) top[c] = up ? hld(rh, voffB[c], 0) : 0.f;
+        }
+    };
     // dt_bar = sum / ndims: 1/ndims is exact for ndims 2 and 4; for 3 the
     // product differs from the reference's division by at most one ulp.
     const float inv_nd = 1.0f / static_cast<float>(ND);
@@ -338,8 +351,12 @@ __device__ __forceinline__ void scannd_tile(const ScanNDArgs &p, const int (&ti)
     for (int c = 0; c < TW; ++c) none[c] = 0.f;
     if constexpr (ND == 2) {
         NDRow<ND, TW> R0, R1, R2, R3;
-        load_row(0, R0);
-        load_row(min(1, nrows - 1), R1);
+        load_ops(0, R0);
+        load_ops(min(1, nrows - 1), R1);
+        if (!wait()) return false;
+        load_top();
+        load_nbr(R0);
+        load_nbr(R1);
         for (int row = 0; row < nrows; row += 4) {
             load_row(min(row + 2, nrows - 1), R2);
             __builtin_amdgcn_sched_barrier(0);
@@ -366,7 +383,9 @@ __device__ __forceinline__ void scannd_tile(const ScanNDArgs &p, const int (&ti)
 #pragma unroll
             for (int c = 0; c < TW; ++c) ring[i][c] = 0.f;
         NDRow<ND, TW> R0, R1;
-        load_row(0, R0);
+        load_ops(0, R0);
+        if (!wait()) return false;
+        load_nbr(R0);
         for (int i0 = 0; i0 < e0; ++i0) {
             const bool inner = i0 > 0;
 #pragma unroll
@@ -385,7 +404,9 @@ __device__ __forceinline__ void scannd_tile(const ScanNDArgs &p, const int (&ti)
         }
     } else {
         NDRow<ND, TW> R0, R1;
-        load_row(0, R0);
+        load_ops(0, R0);
+        if (!wait()) return false;
+        load_nbr(R0);
         for (int row = 0; row < nrows; row += 2) {
             load_row(min(row + 1, nrows - 1), R1);
             __builtin_amdgcn_sched_barrier(0);
@@ -395,6 +416,7 @@ __device__ __forceinline__ void scannd_tile(const ScanNDArgs &p, const int (&ti)
             compute_row(R1, row + 1 < nrows, none, false);
         }
     }
+    return true;
 }
 
 // One launch per tile band: workgroup = (tile of band p.band, channel group).
@@ -409,7 +431,7 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
     const int ordinal = lb / p.ncg;
     int ti[kMaxNd];
     if (!band_tile(p, p.band, ordinal, ti)) return;
-    scannd_tile<ND, TW, MM, PL>(p, ti, cg);
+    scannd_tile<ND, TW, MM, PL>(p, ti, cg, [] { return true; });
 }
 
 // Dataflow schedule, one launch per step: a tile waits only for its own
@@ -541,15 +563,18 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) scannd_flow_kernel(ScanNDArgs 
         int tl = 0;
 #pragma unroll
         for (int a = 0; a < ND; ++a) tl += ti[a] * tstride[a];
-        bool ready = true;
+        // The tile's first operand loads are issued before the waits on its
+        // upstream neighbours, so their latency overlaps the wait.
+        auto upstream_done = [&]() {
+            bool ready = true;
 #pragma unroll
-        for (int a = 0; a < ND; ++a)
-            if (ti[a] > 0)
-                ready = flow_wait(f.flags + static_cast<long>(tl - tstride[a]) * p.ncg + cg, epoch,
-                                  f.spin) && ready;
-        if (ready) {
-            scannd_tile<ND, TW, MM, PL, true>(p, ti, cg);
-        } else {
+            for (int a = 0; a < ND; ++a)
+                if (ti[a] > 0)
+                    ready = flow_wait(f.flags + static_cast<long>(tl - tstride[a]) * p.ncg + cg, epoch,
+                                      f.spin) && ready;
+            return ready;
+        };
+        if (!scannd_tile<ND, TW, MM, PL, true>(p, ti, cg, upstream_done)) {
             scannd_tile_poison<ND>(p, ti, cg);
             if ((threadIdx.x & 63) == 0)
                 __hip_atomic_store(f.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -836,14 +861,12 @@ static int last_flow_kind(hipStream_t s) {
     return 0;
 }
 
-// The dataflow schedule runs grids of 3 or more dims (2D grids are faster
-// with one launch per band on MI355X: their 47-tile critical path, slowed by
-// the tiles running beside it, sets the time), needs the device's 8 XCDs as
-// the hardware reports them (XCC_ID 0-7) and a band table that fits the
-// kernel arguments; KM_SCANND_SCHED=band keeps one launch per band.
-static bool flow_allowed(int nd, int nbands) {
+// The dataflow schedule runs grids of 2 or more dims on a device with the 8
+// XCDs the kernel reads from the hardware (XCC_ID 0-7);
+// KM_SCANND_SCHED=band keeps one launch per band.
+static bool flow_wanted(int nd) {
     const char *e = std::getenv("KM_SCANND_SCHED");
-    if (nd < 3 || (e && std::strcmp(e, "band") == 0) || nbands > kMaxFlowBands) return false;
+    if (nd < 2 || (e && std::strcmp(e, "band") == 0)) return false;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0) return false;
     return device_xcds(dev) == 8;
@@ -875,12 +898,21 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
     if (status) *status = nullptr;
     bool fast = (a.DM % 64 == 0) && (64 % a.M == 0) && a.nd >= 2 && a.nd <= 4;
     // Tiles: rows of TWc points along the last axis, Tlead along each
-    // leading axis. One wave per (tile, channel group); one launch per tile
-    // band. Defaults measured fastest on MI355X at configs[2]: 2D rows of 8
-    // points x 16 rows; 3D rows of 8 points x 4 per leading axis; 4D rows of
-    // 4 x 4.
+    // leading axis. One wave per (tile, channel group); one dataflow launch,
+    // or one launch per tile band. Defaults measured fastest on MI355X at
+    // 2D rows of 8 points x 16 rows per band launch (4 x 8 under
+    // the dataflow schedule); 3D rows of 8 points x 4 per leading axis; 4D
+    // rows of 4 x 4.
+    const bool flow_pref = allow_flow && flow_wanted(a.nd);
     int TWc = (a.nd <= 3) ? 8 : 4;
     int Tlead = (a.nd == 2) ? 16 : 4;
+    if (a.nd == 2 && flow_pref) {
+        // 2D under the dataflow schedule: the critical path runs through
+        // ntile0 + ntile1 - 1 tiles, so smaller tiles than the band
+        // schedule's (measured fastest: 8 rows of 4 points).
+        TWc = 4;
+        Tlead = 8;
+    }
     int nbands = 1;
     if (fast) {
         scannd_tile_shape(a.nd, TWc, Tlead);
@@ -930,7 +962,7 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
         unsigned *fbuf = nullptr;
         long nflags = 0;   // flag words the block holds (cleared when the epoch wraps)
         int kind = 0;
-        if (allow_flow && flow_allowed(a.nd, nbands) && ntiles * a.ncg < 0x7fffffffL) {
+        if (flow_pref && nbands <= kMaxFlowBands && ntiles * a.ncg < 0x7fffffffL) {
             const size_t words = kFlowHead + static_cast<size_t>(ntiles * a.ncg);
             if (ext) {
                 if (ext->nxcc == 8) {

@@ -70,10 +70,12 @@ SCHED_CASES = [((64, 96), 64, 16), ((130, 70), 8, 8), ((9, 6, 11), 4, 16), ((7, 
 
 @pytest.mark.parametrize("dims,D,M", SCHED_CASES)
 def test_dataflow_and_band_schedules_agree(dims, D, M, monkeypatch):
-    # The per-tile dataflow launch (3+ dims on a device with 8 XCDs) and one
-    # launch per tile band compute every point with the same arithmetic:
-    # their outputs agree bit for bit, and the band schedule matches the
-    # oracle.
+    # The per-tile dataflow launch (on a device with 8 XCDs) and one launch
+    # per tile band compute every state with the same arithmetic: h agrees
+    # bit for bit, and so does y in 3+ dims, where both use the same tiles.
+    # 2D uses rows of 4 points under the dataflow schedule and of 8 per band
+    # launch, which changes the order of y's sum over the M states: y then
+    # agrees with the oracle like the band schedule's.
     # Stable decays (configs[2]: a_k ~ U(0.05, 0.9/ndims), A = log a_k), so
     # every value stays finite on the larger grids.
     nd, P = len(dims), int(np.prod(dims))
@@ -87,10 +89,12 @@ def test_dataflow_and_band_schedules_agree(dims, D, M, monkeypatch):
     monkeypatch.setenv("KM_SCANND_SCHED", "band")
     y2, h2 = run_device(dims, x, A, B, Cm, dt)
     assert np.isfinite(y1).all() and np.isfinite(h1).all()
-    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    if nd > 2:
+        assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
     assert np.array_equal(h1.view(np.uint32), h2.view(np.uint32))
     yr, hr = O.scannd_ref(dims, x, A, B, Cm, dt, nthreads=8, fast=True)
     ya, ha = kappa(dims, x, A, B, Cm, dt)
+    assert_close(y1, yr, TOL_F32, "y", ya)
     assert_close(y2, yr, TOL_F32, "y", ya)
     assert_close(h2, hr, TOL_F32, "h", ha)
 
