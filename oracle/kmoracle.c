@@ -17,6 +17,12 @@
 #include <omp.h>
 #endif
 
+/* memset of n floats; n = 0 leaves p alone (it may be NULL then, which
+ * memset itself does not allow). */
+static void orc_zero(float *p, long n) {
+    if (n > 0) memset(p, 0, (size_t)n * sizeof(float));
+}
+
 /* Reference +-1000 state clamp, cpu/scan1d.asm:136-140: minss then maxss.
  * minss returns its second operand when the comparison is false, so NaN
  * maps to +1000. */
@@ -97,11 +103,11 @@ void orc_scan1d_batched(const float *x, const float *delta, const float *A,
  * Scan1D backward: cpu/scan1d_backward.c:193-306.
  * ====================================================================== */
 static void bwd_zero(OrcScanBackwardParams *p) {            /* :199-205 */
-    memset(p->dx, 0, (size_t)(p->L * p->D) * sizeof(float));
-    memset(p->dA, 0, (size_t)(p->D * p->M) * sizeof(float));
-    memset(p->dB, 0, (size_t)(p->L * p->D * p->M) * sizeof(float));
-    memset(p->dC, 0, (size_t)(p->L * p->D * p->M) * sizeof(float));
-    memset(p->ddelta, 0, (size_t)(p->L * p->D) * sizeof(float));
+    orc_zero(p->dx, p->L * p->D);
+    orc_zero(p->dA, p->D * p->M);
+    orc_zero(p->dB, p->L * p->D * p->M);
+    orc_zero(p->dC, p->L * p->D * p->M);
+    orc_zero(p->ddelta, p->L * p->D);
 }
 
 static void bwd_m1(OrcScanBackwardParams *p) {              /* :207-246 */
@@ -179,11 +185,11 @@ void orc_scan1d_backward_m1_shared_bc(OrcScanBackwardSharedParams *p) {
         return;                                                     /* :17-21 */
     long L = p->L, D = p->D;
     int avx_order = (p->A_diag && D >= 8);                          /* :185 */
-    memset(p->dx, 0, (size_t)(L * D) * sizeof(float));
-    memset(p->dA, 0, (size_t)D * sizeof(float));
-    memset(p->dB, 0, (size_t)D * sizeof(float));
-    memset(p->dC, 0, (size_t)D * sizeof(float));
-    memset(p->ddelta, 0, (size_t)L * sizeof(float));
+    orc_zero(p->dx, L * D);
+    orc_zero(p->dA, D);
+    orc_zero(p->dB, D);
+    orc_zero(p->dC, D);
+    orc_zero(p->ddelta, L);
     float *adj = (float *)calloc((size_t)D, sizeof(float));
     if (!adj) return;
     for (long t = L - 1; t >= 0; t--) {
@@ -253,11 +259,11 @@ void orc_scan1d_backward_m1_shared_bc_asm(OrcScanBackwardSharedParams *p, int si
     long L = p->L, D = p->D;
     float *adj = (float *)calloc((size_t)(D > 0 ? D : 1), sizeof(float));
     if (!adj) return;
-    memset(p->dx, 0, (size_t)(L * D) * sizeof(float));              /* :78-113 */
-    memset(p->dA, 0, (size_t)D * sizeof(float));
-    memset(p->dB, 0, (size_t)D * sizeof(float));
-    memset(p->dC, 0, (size_t)D * sizeof(float));
-    memset(p->ddelta, 0, (size_t)L * sizeof(float));
+    orc_zero(p->dx, L * D);              /* :78-113 */
+    orc_zero(p->dA, D);
+    orc_zero(p->dB, D);
+    orc_zero(p->dC, D);
+    orc_zero(p->ddelta, L);
     for (long t = L - 1; t >= 0; t--) {
         const float dt = p->delta[t];
         const float *hprev = t > 0 ? p->h + (t - 1) * D : p->h0;   /* NULL: zero state */
@@ -848,9 +854,9 @@ void orc_convnd_backward(OrcConvNDParams *p) {
     OrcPlan *pl = orc_plan_create(p->dims, nd);
     if (!pl) return;
     conv_strides(p->dims, nd, st);
-    memset(p->dinput, 0, (size_t)(P * D) * sizeof(float));
-    memset(p->dkernel, 0, (size_t)(KV * D) * sizeof(float));
-    if (p->dbias) memset(p->dbias, 0, (size_t)D * sizeof(float));
+    orc_zero(p->dinput, P * D);
+    orc_zero(p->dkernel, KV * D);
+    if (p->dbias) orc_zero(p->dbias, D);
     for (long level = pl->max_level; level >= 0; level--) {
         for (long i = pl->level_starts[level]; i < pl->level_starts[level + 1]; i++) {
             long out = pl->level_offsets[i], oc[8], rem = out;
@@ -938,8 +944,8 @@ void orc_mamba3_forward(const OrcMamba3 *p, const float *input, float *output, l
                 Cs[t * NR + i] += p->b_C[i];
             }
         }
-        memset(h, 0, (size_t)N * sizeof(float));                        /* :422 */
-        memset(pbu, 0, (size_t)N * sizeof(float));
+        orc_zero(h, N);                        /* :422 */
+        orc_zero(pbu, N);
         for (long t = 0; t < L; t++) {
             float dt = dl[t], lt = lam[t];
             const float *bt = Bs + t * NR, *ct = Cs + t * NR, *ut = u + t * R;
@@ -950,7 +956,7 @@ void orc_mamba3_forward(const OrcMamba3 *p, const float *input, float *output, l
                 hr[i + 1] = sv * h0 + cv * h1;
             }
             if (N & 1) hr[N - 1] = h[N - 1];
-            memset(bu, 0, (size_t)N * sizeof(float));                   /* :440-443 */
+            orc_zero(bu, N);                   /* :440-443 */
             for (long r = 0; r < R; r++)
                 for (long n = 0; n < N; n++) bu[n] += bt[r * N + n] * ut[r];
             for (long n = 0; n < N; n++) {                               /* :446-452 */

@@ -14,13 +14,16 @@ All wrappers take and return numpy float32 / int64 arrays.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-ORACLE_SO = HERE / "liboracle.so"
-ORACLE_FAST_SO = HERE / "liboracle_fast.so"
+# KM_ORACLE_LIB names another build of the oracle (the sanitizer build,
+# oracle/_san/liboracle.so); it then serves the timing entry points too.
+ORACLE_SO = Path(os.environ.get("KM_ORACLE_LIB") or HERE / "liboracle.so")
+ORACLE_FAST_SO = ORACLE_SO if os.environ.get("KM_ORACLE_LIB") else HERE / "liboracle_fast.so"
 REF_SO = HERE / "_ref" / "libkmref.so"
 
 if not ORACLE_SO.exists():
