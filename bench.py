@@ -244,13 +244,16 @@ def bench_scan1d_gated(torch, K, stream, steps, warmup, Bsz=8, L=2048, D=2048, N
 
 
 def bench_gemm_vs_library(torch, K, stream, steps, warmup):
-    """The block's two projection shapes (in_proj half: 16384 x 2048 x 1024,
-    out_proj: 16384 x 1024 x 2048) on km_gemm_bf16 and on torch.matmul
-    (hipBLASLt on ROCm), same bf16 operands (N(0,1) activations, N(0, 0.02)
-    weights: matrix-core throughput depends on the operand bits), bf16 out."""
+    """The block's projection shapes (in_proj: 16384 x 4096 x 1024, one
+    launch in the block with its x and z column halves routed to two
+    buffers; its half 16384 x 2048 x 1024; out_proj: 16384 x 1024 x 2048) on
+    km_gemm_bf16 and on torch.matmul (hipBLASLt on ROCm), same bf16 operands
+    (N(0,1) activations, N(0, 0.02) weights: matrix-core throughput depends
+    on the operand bits), bf16 out."""
     g = torch.Generator(device="cuda").manual_seed(11)
     out = {}
-    for name, (M, N, Kd) in {"in_proj_half": (16384, 2048, 1024),
+    for name, (M, N, Kd) in {"in_proj": (16384, 4096, 1024),
+                             "in_proj_half": (16384, 2048, 1024),
                              "out_proj": (16384, 1024, 2048)}.items():
         A = torch.randn((M, Kd), device="cuda", generator=g).to(torch.bfloat16)
         B = (torch.randn((N, Kd), device="cuda", generator=g) * 0.02).to(torch.bfloat16)

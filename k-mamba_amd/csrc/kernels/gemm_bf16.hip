@@ -34,6 +34,10 @@ struct GemmArgs {
     long M, N, K, lda, ldb, ldc;
     int c_bf16;
     int epi;
+    // Split output (256 x 256 kernel): columns [nsplit, N) go to C2 (same
+    // ldc) at column - nsplit; nsplit is a multiple of the tile width.
+    void *C2;
+    long nsplit;
 };
 
 constexpr int kBM = 128, kBN = 128, kBK = 64;
@@ -400,7 +404,21 @@ __global__ void __launch_bounds__(512, 1) gemm_bf16_mfma_pp(GemmArgs p) {
     __syncthreads();
     char *lds = reinterpret_cast<char *>(w == 0 ? sA0 : w == 1 ? sA1 : w == 2 ? sA2 : w == 3 ? sA3
                                          : w == 4 ? sB0 : w == 5 ? sB1 : w == 6 ? sB2 : sB3);
-    store_wave_tile<EPI, CBF16, 4, 2>(p, acc, m0 + g * 128, n0 + sg * 64, lds, lane);
+    if (p.C2 && n0 >= p.nsplit) {
+        GemmArgs q = p;
+        q.C = p.C2;
+        q.N = p.N - p.nsplit;
+        q.bias = p.bias ? p.bias + p.nsplit : nullptr;
+        store_wave_tile<EPI, CBF16, 4, 2>(q, acc, m0 + g * 128, n0 - p.nsplit + sg * 64, lds, lane);
+    } else {
+        if (p.C2) {
+            GemmArgs q = p;
+            q.N = p.nsplit;
+            store_wave_tile<EPI, CBF16, 4, 2>(q, acc, m0 + g * 128, n0 + sg * 64, lds, lane);
+        } else {
+            store_wave_tile<EPI, CBF16, 4, 2>(p, acc, m0 + g * 128, n0 + sg * 64, lds, lane);
+        }
+    }
 }
 
 // Narrow shapes with a long K (N <= 128, K >= 512: x_proj): a workgroup
@@ -599,10 +617,37 @@ static int direct_launch(const KMGemm *g, hipStream_t s) {
     return 1;
 }
 
-int gemm_bf16_launch(const KMGemm *g, hipStream_t s) {
+static int gemm_launch_impl(const KMGemm *g, void *C2, long nsplit, hipStream_t s);
+
+int gemm_bf16_launch(const KMGemm *g, hipStream_t s) { return gemm_launch_impl(g, nullptr, 0, s); }
+
+// One launch for C[:, :nsplit] and C2[:, :N - nsplit] = the two column
+// ranges of one product (the Mamba block's in_proj x and z halves), both
+// with g->ldc; two launches when the 256 x 256 kernel does not take the
+// shape or nsplit is not a multiple of its tile width.
+int gemm_bf16_launch_split(const KMGemm *g, void *C2, long nsplit, hipStream_t s) {
+    if (!g || !C2 || nsplit <= 0 || nsplit >= g->N) {
+        set_error("km_gemm_bf16: invalid split");
+        return -1;
+    }
+    const bool big = g->M >= kGM && g->N >= kGN && g->K >= 4 * kGK && nsplit % kGN == 0 &&
+                     g->ldb * 2 * (kGN + 1) <= 0x7fffffffL && g->lda * 2 * (kGM + 1) <= 0x7fffffffL &&
+                     g->ldc >= nsplit && g->ldc >= g->N - nsplit;
+    if (big) return gemm_launch_impl(g, C2, nsplit, s);
+    KMGemm h = *g;
+    h.N = nsplit;
+    if (gemm_launch_impl(&h, nullptr, 0, s) != 0) return -1;
+    h.B = static_cast<const uint16_t *>(g->B) + nsplit * g->ldb;
+    h.C = C2;
+    h.N = g->N - nsplit;
+    if (g->bias) h.bias = g->bias + nsplit;
+    return gemm_launch_impl(&h, nullptr, 0, s);
+}
+
+static int gemm_launch_impl(const KMGemm *g, void *C2, long nsplit, hipStream_t s) {
     if (!g || !g->A || !g->B || !g->C) { set_error("km_gemm_bf16: NULL pointer"); return -1; }
     if (g->M < 0 || g->N < 0 || g->K <= 0 || g->K % 8 != 0 || g->lda < g->K || g->ldb < g->K ||
-        g->ldc < g->N || g->lda % 8 != 0 || g->ldb % 8 != 0) {
+        (!C2 && g->ldc < g->N) || g->lda % 8 != 0 || g->ldb % 8 != 0) {
         set_error("km_gemm_bf16: invalid shape M=%ld N=%ld K=%ld lda=%ld ldb=%ld ldc=%ld "
                   "(K, lda, ldb must be multiples of 8)", g->M, g->N, g->K, g->lda, g->ldb, g->ldc);
         return -1;
@@ -617,11 +662,16 @@ int gemm_bf16_launch(const KMGemm *g, hipStream_t s) {
     }
     if (g->M == 0 || g->N == 0) return 0;
     if (!gpu_ready()) return -1;
-    if (const int d = direct_launch(g, s)) return d > 0 ? 0 : -1;
+    if (!C2)
+        if (const int d = direct_launch(g, s)) return d > 0 ? 0 : -1;
     // 256 x 256 tiles when both output dimensions fill them (and K spans
     // at least a few stages); 128 x 128 otherwise.
     const bool big = g->M >= kGM && g->N >= kGN && g->K >= 4 * kGK &&
                      g->ldb * 2 * (kGN + 1) <= 0x7fffffffL && g->lda * 2 * (kGM + 1) <= 0x7fffffffL;
+    if (C2 && !big) {
+        set_error("km_gemm_bf16: split output needs the 256 x 256 kernel");
+        return -1;
+    }
     const long TM = big ? kGM : kBM, TN = big ? kGN : kBN;
     if (g->ldb * 2 * (TN + 1) > 0x7fffffffL || g->lda * 2 * (TM + 1) > 0x7fffffffL) {
         set_error("km_gemm_bf16: leading dimension too large");
@@ -643,6 +693,10 @@ int gemm_bf16_launch(const KMGemm *g, hipStream_t s) {
         a.M = std::min(g->M - mb * TM, nb * TM);
         a.N = g->N; a.K = g->K; a.lda = g->lda; a.ldb = g->ldb; a.ldc = g->ldc;
         a.epi = g->epilogue;
+        if (C2) {
+            a.C2 = static_cast<char *>(C2) + mb * TM * g->ldc * (a.c_bf16 ? 2 : 4);
+            a.nsplit = nsplit;
+        }
         dim3 grid(static_cast<unsigned>(nbn), static_cast<unsigned>(nb));
         switch (g->epilogue) {
         case KM_EPI_SOFTPLUS: gemm_go<KM_EPI_SOFTPLUS>(a, grid, big, s); break;

@@ -22,6 +22,7 @@ namespace km {
 
 int scan1d_fwd_launch(const KMScan1DFwd *k, hipStream_t stream, bool allow_split);
 int gemm_bf16_launch(const KMGemm *g, hipStream_t s);
+int gemm_bf16_launch_split(const KMGemm *g, void *C2, long nsplit, hipStream_t s);
 
 constexpr int kConvStrip = 64;
 
@@ -146,12 +147,12 @@ int mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long B,
     auto plain = [&](const KMGemm &g) { return gemm_bf16_launch(&g, s); };
     KMGemm g{};
     g.c_dtype = KM_BF16;
-    // in_proj, x and z halves
-    g.A = x; g.B = Win; g.C = xi; g.M = T; g.N = di; g.K = w->dim;
+    // in_proj: x and z halves of one product (columns [0, di) -> xi,
+    // [di, 2 di) -> z), one launch
+    g.A = x; g.B = Win; g.C = xi; g.M = T; g.N = 2 * di; g.K = w->dim;
     g.lda = w->dim; g.ldb = w->dim; g.ldc = di; g.epilogue = KM_EPI_NONE;
-    if (plain(g) != 0) return -1;
-    g.B = Win + di * w->dim; g.C = z;
-    if (plain(g) != 0) return -1;
+    if (gemm_bf16_launch_split(&g, z, di, s) != 0) return -1;
+    g.N = di;
     // causal depthwise conv1d + SiLU
     {
         dim3 grid(static_cast<unsigned>((di / 2 + 255) / 256),
