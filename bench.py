@@ -860,8 +860,9 @@ def main():
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "measured_copy_GBs": extra["copy_1GiB"]["GBs_read_plus_write"],
                      "frac_of_measured_copy": round(ach / extra["copy_1GiB"]["GBs_read_plus_write"], 4),
-                     "traffic_source": "profiles/scan1d_fwd_c1_traffic.json: rocprofv3 FETCH_SIZE and "
-                                       "WRITE_SIZE of this kernel, scaled by a copy calibration",
+                     "traffic_source": "profiles/scan1d_fwd_c1_traffic.json: rocprofv3 TCC read "
+                                       "requests by size and write requests of this kernel (the same "
+                                       "formulas read a 1 GiB copy exactly)",
                      "kernel": "km::scan1d_fwd_chunked (fp32, B/C shared over channels)",
                      "alg_bytes": alg,
                      "avg_launch_ms": round(ms, 5)},
