@@ -46,7 +46,7 @@ def scan1d_bwd_alg_bytes(Bsz, L, D, N, s):
 
 
 def bench_scan1d_bwd(torch, K, stream, Bsz, L, D, N, dtype, steps, warmup):
-    """configs[1] backward: the forward writes 64-step state checkpoints (not
+    """configs[1] backward: the forward writes 32-step state checkpoints (not
     timed here), the backward recomputes states from them; dy ~ N(0,1)."""
     x, dt, A, Bm, Cm = make_inputs(torch, Bsz, L, D, N, dtype, seed=3)
     g = torch.Generator(device="cuda").manual_seed(4)

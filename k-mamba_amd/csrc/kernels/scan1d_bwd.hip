@@ -13,9 +13,9 @@
 // Design (same lane layout as the forward kernel):
 //  * A wave covers DL = 64/NS channels x NS groups of NPL states; a workgroup
 //    of W waves owns one (batch, channel group) and walks the sequence
-//    backwards in super-chunks of W*TC = 64 steps, one wave per TC steps.
+//    backwards in super-chunks of W*TC = 32 steps, one wave per TC steps.
 //  * Forward states of a super-chunk are either read from the history or
-//    recomputed from the 64-step checkpoint the forward wrote: local pass
+//    recomputed from the 32-step checkpoint the forward wrote: local pass
 //    from zero, chunk maps through LDS, fold, replay (as the forward).
 //  * The adjoint is the same linear recurrence run backwards with the same
 //    decays: g -> P*g + a over a wave's steps, so the chunk maps fold in
@@ -24,14 +24,16 @@
 //  * dx and ddelta reduce over the states of a channel across lanes; dA
 //    accumulates per lane over the sequence and the waves of a workgroup add
 //    their sums in wave order. Shared B/C ([B, L, N], stride 0 over
-//    channels) need dB, dC summed over channels: a reduce-scatter over the
-//    wave's lanes gives the wave's channel-group sum, stored to the
-//    workgroup's own partial slot; a finalize kernel adds the slots of every
-//    channel group (and dA's per-batch partials) in a fixed order. No
-//    atomics: every output is identical run to run.
+//    channels) need dB, dC summed over channels: a per-wave LDS block of
+//    rows and columns (N = 16) or a reduce-scatter over the wave's lanes
+//    gives the wave's channel-group sum, stored to the workgroup's own
+//    partial slot; a finalize kernel adds the slots of every channel group
+//    (and dA's per-batch partials) in a fixed order. No atomics: every
+//    output is identical run to run.
 //  * States recomputed from checkpoints run unclamped; if any leaves
-//    [-1000, 1000] the super-chunk is recomputed with the sequential clamped
-//    recurrence, which matches the forward's clamp fallback.
+//    [-1000, 1000] the workgroup re-runs every super-chunk with the
+//    sequential clamped recurrence, which matches the forward's clamp
+//    fallback.
 #include <type_traits>
 
 #include "km_device.hpp"
@@ -51,7 +53,7 @@ struct Scan1DBwdArgs {
     const void *Bm, *Cm;
     const float *h0;       // [B, D, N] or null
     const float *hist;     // [B, L, D, N] state after each step, or null
-    const float *ckpt;     // [B, nck, D, N] state after each 64-step block, or null
+    const float *ckpt;     // [B, nck, D, N] state after each 32-step block, or null
     long nck;
     void *dx, *ddt;        // [B, L, D]
     float *dApart;         // [B, D, N] per-batch dA partials (every element written)
