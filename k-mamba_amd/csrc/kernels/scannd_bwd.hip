@@ -131,11 +131,14 @@ __device__ __forceinline__ void adj_store(const AdjWin &w, long r, float g) {
 // each row right to left, keeping the row below (its g and axis-0 delta) in
 // registers and the right neighbour from the previous step; successors
 // across the tile's bottom and right edges were written by the previous
-// launch (the next band).
+// launch (the next band). Workgroups are numbered XCD-major (xcd_remap):
+// the channel groups of a tile, which share the dy / delta row lines (four
+// channels, 16 bytes, each), run on one XCD's L2.
 template <int TR, int TW, int RB>
 __global__ void __launch_bounds__(64) nd_adjoint_tile2d(NdBwdArgs a, int band, int nt1, int ncg) {
     const int lane = threadIdx.x;
-    const int o = static_cast<int>(blockIdx.x) / ncg, cg = static_cast<int>(blockIdx.x) - o * ncg;
+    const int lb = static_cast<int>(xcd_remap(blockIdx.x, gridDim.x));
+    const int o = lb / ncg, cg = lb - o * ncg;
     const int ti0 = (band > nt1 - 1 ? band - (nt1 - 1) : 0) + o, ti1 = band - ti0;
     const long n0 = a.dims[0], n1 = a.dims[1];
     const long r0 = static_cast<long>(ti0) * TR, r1 = std::min<long>(n0, r0 + TR);
@@ -226,7 +229,8 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile2d(NdBwdArgs a, int band, i
 template <int TP, int TR, int TW>
 __global__ void __launch_bounds__(64) nd_adjoint_tile3d(NdBwdArgs a, const int *tiles, int ncg) {
     const int lane = threadIdx.x;
-    const int o = static_cast<int>(blockIdx.x) / ncg, cg = static_cast<int>(blockIdx.x) - o * ncg;
+    const int lb = static_cast<int>(xcd_remap(blockIdx.x, gridDim.x));
+    const int o = lb / ncg, cg = lb - o * ncg;
     const long n0 = a.dims[0], n1 = a.dims[1], n2 = a.dims[2];
     const long p0 = static_cast<long>(tiles[3 * o]) * TP, p1 = std::min<long>(n0, p0 + TP);
     const long r0 = static_cast<long>(tiles[3 * o + 1]) * TR, r1 = std::min<long>(n1, r0 + TR);
@@ -622,8 +626,11 @@ __device__ __forceinline__ void grad_flush(const GradWin &w, const float *stage,
 template <int TR, int TW, int MM>
 __global__ void __launch_bounds__(256) nd_adjoint_grads_tile2d(NdBwdArgs a) {
     const long DM = a.D * MM;
-    const long tile = blockIdx.y;
-    const long c0 = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    // Tile and channel block, numbered XCD-major: the channel blocks of a
+    // tile, which share the x / dy / delta row lines, run on one XCD.
+    long tile, cbx;
+    xcd_tile(tile, cbx);
+    const long c0 = cbx * 256 + threadIdx.x;
     const bool active = c0 < DM;
     const long c = active ? c0 : 0;
     const long d = c / MM;
@@ -663,7 +670,7 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile2d(NdBwdArgs a) {
     constexpr int CPG = kGradPts / TR;   // columns per staged group
     static_assert(kGradPts % TR == 0, "whole columns per staged group");
     __shared__ float stage[kStageOut<MM> ? 2 * 3 * kGradPts * (256 / MM) : 1];
-    const long d0 = static_cast<long>(blockIdx.x) * (256 / MM);
+    const long d0 = cbx * (256 / MM);
     auto finish_col = [&](long jj, const GradIn<2> (&v)[TR], float up) {
         const long j = j0 + jj;
         float *st = stage + ((jj / CPG) & 1) * (3 * kGradPts * (256 / MM));
@@ -717,8 +724,9 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile2d(NdBwdArgs a) {
 template <int TP, int TR, int TW, int TPW, int MM>
 __global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
     const long DM = a.D * MM;
-    const long blk = blockIdx.y;    // tiles [blk * TPW, +TPW)
-    const long c0 = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    long blk, cbx;                  // tiles [blk * TPW, +TPW), channel block (XCD-major)
+    xcd_tile(blk, cbx);
+    const long c0 = cbx * 256 + threadIdx.x;
     const bool active = c0 < DM;
     const long c = active ? c0 : 0;
     const long d = c / MM;
@@ -769,7 +777,7 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
     // by row: one barrier per row).
     constexpr int PTS = (kStageOut<MM> && TW * TP == kGradPts) ? kGradPts : 0;
     __shared__ float stage[PTS > 0 ? 2 * 4 * kGradPts * (256 / MM) : 1];
-    const long d0 = static_cast<long>(blockIdx.x) * (256 / MM);
+    const long d0 = cbx * (256 / MM);
     Group ga, gb;
     load_grp(0, 0, ga);
     for (long ii = 0; ii < ie; ++ii) {
