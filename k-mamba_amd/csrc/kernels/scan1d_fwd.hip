@@ -164,8 +164,14 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
     const int ns = lane / DL;
     const int n0 = ns * NPL;
     const long ngroups = (p.D + DL - 1) / DL;
-    const long b = blockIdx.x / ngroups;
-    const long d = (blockIdx.x - b * ngroups) * DL + dl;
+    // Workgroups numbered XCD-major: the channel groups of a batch element
+    // run on as few XCDs as possible, so its shared B/C rows and (bf16: a
+    // group's 32 channels are half of a 128-byte line) its x / delta lines
+    // are fetched into one L2.
+    const long wg = xcd_remap(blockIdx.x, gridDim.x);
+    const long b = wg / ngroups;
+    const long grp = wg - b * ngroups;
+    const long d = grp * DL + dl;
     const bool dvalid = d < p.D;
     const int dc = static_cast<int>(dvalid ? d : p.D - 1);
     const int L = static_cast<int>(p.L);
@@ -524,7 +530,7 @@ __global__ void __launch_bounds__(64 * W, OCC) scan1d_fwd_chunked(Scan1DFwdArgs 
         if (p.clamp_flag) {
             // A segment of a split sequence: states entering later segments
             // are also off, so the whole sequence is re-run by the repair.
-            if (tid == 0) p.clamp_flag[(b / p.nseg) * ngroups + (blockIdx.x - b * ngroups)] = 1;
+            if (tid == 0) p.clamp_flag[(b / p.nseg) * ngroups + grp] = 1;
             return;
         }
         // The sequential pass keeps each lane's states contiguous
