@@ -229,20 +229,23 @@ int km_mamba1_block_fwd(const KMMamba1Weights *w, const void *x, void *out, long
  * with km_last_error() set. */
 int km_scannd_fwd(const ScanNDParams *p, void *stream);
 
-/* Status of the latest km_scannd_fwd / km_scannd_fwd_noalloc call enqueued
- * on `stream` (current device). Waits for the stream, then returns 0 when
- * that call's outputs are exact, 1 when one of its dataflow waits (3- and
- * 4-dimensional grids) ran out of its polling budget (KM_SCANND_FLOW_SPIN):
- * that call then wrote NaN into the affected tiles' states and outputs and
- * should be run again (the synchronous om_scannd_forward / scannd re-run it
- * on the band schedule by themselves), or -1 on error. */
+/* Status of the latest km_scannd_fwd / km_scannd_fwd_noalloc /
+ * km_scannd_bwd call enqueued on `stream` (current device). Waits for the
+ * stream, then returns 0 when that call's outputs are exact, 1 when one of
+ * its dataflow waits (grids of 2 to 4 dimensions on the tile kernels) ran
+ * out of its polling budget (KM_SCANND_FLOW_SPIN): that call then wrote NaN
+ * into the affected tiles' states and outputs (the backward: its
+ * gradients) and should be run again (the synchronous om_scannd_forward /
+ * scannd re-run it on the band schedule by themselves), or -1 on error. A
+ * km_scannd_bwd given a workspace keeps its status word there: keep the
+ * workspace alive until the status is read. */
 int km_scannd_status(void *stream);
 
 /* km_scannd_fwd without any allocation. No counterpart in the reference: it
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). Same
  * parameters, semantics and results as km_scannd_fwd. The dataflow schedule
- * of 3- and 4-dimensional grids keeps its counters, epoch and completion
+ * of 2- to 4-dimensional grids keeps its counters, epoch and completion
  * flags in a fixed 1 MiB array in each GPU's memory (held until the process
  * ends) instead of a per-stream allocation; the epoch is advanced on the
  * device by each call, so a call captured in a HIP graph may be replayed.
@@ -268,9 +271,11 @@ int km_scannd_fwd_noalloc(const ScanNDParams *p, void *stream);
  * [P, D, M] (h: the states km_scannd_fwd wrote). All outputs are
  * overwritten; dA is summed in a fixed order (identical run to run).
  * M a power of two <= 64, or ndims * M <= 64. workspace: km_scannd_bwd_workspace_bytes()
- * bytes of device memory, or NULL for the library's per-device scratch
- * (calls that overlap on one device then race). The adjoint state runs one
- * launch per anti-diagonal level of the grid, last to first. */
+ * bytes of device memory, or NULL for the library's scratch of this
+ * (device, stream). The adjoint state runs against the forward's wavefront:
+ * on 2D and 3D grids with D*M a multiple of 64 as one dataflow launch over
+ * tiles on a device with 8 XCDs (KM_SCANND_SCHED=band: one launch per tile
+ * band), otherwise one launch per anti-diagonal level, last to first. */
 typedef struct {
     const long  *dims;
     long ndims, D, M;

@@ -31,6 +31,7 @@
 #include <cstdio>
 
 #include "km_device.hpp"
+#include "scannd_flow.hpp"
 #include "../km_runtime.hpp"
 #include "kmamba_km.h"
 #include "scan.h"
@@ -60,44 +61,9 @@ struct ScanNDArgs {
     int ncg;                     // channel groups of 64 (d, m) lanes
 };
 
-// Number of pairs (u, v), 0 <= u < n1, 0 <= v < n2, with u + v = s.
-__device__ __forceinline__ int count2(int s, int n1, int n2) {
-    const int lo = max(0, s - (n2 - 1)), hi = min(s, n1 - 1);
-    return hi >= lo ? hi - lo + 1 : 0;
-}
-
-// Tile band b, ordinal o: the o-th tile, in lexicographic order of the tile
-// index tuple, whose indices sum to b (2 <= nd <= 4). Leading axes pick
-// their index by counting the tuples of the remaining axes; the last two
-// axes follow in closed form.
+// Tile band b, ordinal o of the grid's tiles (band_tile_n).
 __device__ inline bool band_tile(const ScanNDArgs &p, int band, int ordinal, int *ti) {
-    int s = band, o = ordinal;
-    for (int a = 0; a + 2 < p.nd; ++a) {
-        bool found = false;
-        for (int v = 0; v < p.ntile[a] && v <= s; ++v) {
-            int c;
-            if (a + 3 == p.nd) {
-                c = count2(s - v, p.ntile[a + 1], p.ntile[a + 2]);
-            } else {
-                c = 0;
-                for (int w = 0; w < p.ntile[a + 1] && w <= s - v; ++w)
-                    c += count2(s - v - w, p.ntile[a + 2], p.ntile[a + 3]);
-            }
-            if (o < c) {
-                ti[a] = v;
-                s -= v;
-                found = true;
-                break;
-            }
-            o -= c;
-        }
-        if (!found) return false;
-    }
-    const int n1 = p.ntile[p.nd - 2], n2 = p.ntile[p.nd - 1];
-    if (o >= count2(s, n1, n2)) return false;
-    ti[p.nd - 2] = max(0, s - (n2 - 1)) + o;
-    ti[p.nd - 1] = s - ti[p.nd - 2];
-    return true;
+    return band_tile_n(p.nd, p.ntile, band, ordinal, ti);
 }
 
 // Sum over the M consecutive lanes of a channel (M a power of two <= 64);
@@ -434,55 +400,10 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
     scannd_tile<ND, TW, MM, PL>(p, ti, cg, [] { return true; });
 }
 
-// Dataflow schedule, one launch per step: a tile waits only for its own
-// axis predecessors instead of the whole previous band. Channel groups never
-// depend on each other, so XCD x owns the groups [cg_lo[x], cg_lo[x + 1]) for
-// every tile: each producer / consumer pair shares one XCD's L2 (coherent
-// for all its CUs), and no data crosses XCDs inside the launch. Each
-// workgroup reads the XCD it runs on from the hardware and takes items (tile
-// in band order, then channel group) from that XCD's counter, so an item is
-// only ever taken by a running wave and every item's predecessors were taken
-// before it: the waits always end.
-//
-// Hand-off: the producer waits until its h stores are acknowledged by the
-// L2 (vmcnt 0), then publishes flags[tile * ncg + cg] = epoch (this launch's
-// number) with an agent-scope store; the consumer polls the flag with
-// agent-scope loads and reads the predecessor's states with agent-coherent
-// loads (sc1: past its own L1, from the shared L2). A wait polls at most
-// `spin` times. If it runs out, the wave does not compute its tile: it
-// writes NaN into the tile's states and outputs, so every tile that depends
-// on it (reading those states) turns NaN too and no output is silently
-// wrong, and it sets the launch's status word, which the synchronous entry
-// points read to re-run the call on the band schedule.
-constexpr int kMaxFlowBands = 768;
-constexpr unsigned kFlowSpinDefault = 1u << 20;
-struct FlowArgs {
-    unsigned *flags;                     // [ntiles * ncg] epoch of the last finish
-    unsigned *counter;                   // [8] items taken per XCD, zero at launch
-    unsigned *status;                    // nonzero when a wait ran out (zero at launch)
-    const unsigned *epoch;               // this launch's epoch (set by flow_reset)
-    unsigned spin;                       // polls per wait before giving up
-    int nbands;
-    int cg_lo[9];                        // channel groups of XCD x: [cg_lo[x], cg_lo[x + 1])
-    int band_start[kMaxFlowBands + 1];   // first tile (band order) of each band
-};
-
-// True once the predecessor published this launch's epoch; false when the
-// budget ran out first. Lane 0 polls; the result is wave-uniform.
-__device__ __forceinline__ bool flow_wait(const unsigned *flag, unsigned epoch, unsigned spin) {
-    int done = 0;
-    if ((threadIdx.x & 63) == 0) {
-        for (unsigned i = 0; i < spin; ++i) {
-            if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch) {
-                done = 1;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-        }
-    }
-    return __builtin_amdgcn_readfirstlane(done) != 0;
-}
-
+// Dataflow schedule (scannd_flow.hpp), one launch per step: a tile waits
+// only for its own axis predecessors. A wait that runs out writes NaN into
+// the tile's states and outputs and sets the launch's status word, which the
+// synchronous entry points read to re-run the call on the band schedule.
 // NaN into the states and outputs of one (tile, channel group): the wave's
 // 64 (channel, state) lanes at every point of the tile.
 template <int ND>
@@ -513,19 +434,16 @@ __device__ void scannd_tile_poison(const ScanNDArgs &p, const int (&ti)[kMaxNd],
     }
 }
 
-// Workgroups of Q = blockDim.x / 64 waves (Q = kFlowQ when it divides
-// every XCD's group count, else 1): an item is (tile, run of Q consecutive
+// Workgroups of Q waves (flow_q): an item is (tile, run of Q consecutive
 // channel groups of the XCD), one group per wave, so no wave idles. The
 // waves of a workgroup share a CU, start an item together and read the
 // same x / delta lines (the groups of four consecutive channels are 16
 // bytes apart), so those lines come from the CU's L1 or one L2 fill
 // instead of up to Q fills spread over the time the groups' waves happen
 // to run.
-constexpr int kFlowQ = 4;
-
 template <int ND, int TW, int MM, int PL>
 __global__ void __launch_bounds__(64 * kFlowQ, 2) scannd_flow_kernel(ScanNDArgs p, FlowArgs f) {
-    const int xcd = static_cast<int>(__builtin_amdgcn_s_getreg(20 | (3 << 11))) & 7;   // HW_REG_XCC_ID
+    const int xcd = flow_xcd();
     const int cg0 = f.cg_lo[xcd], ncx = f.cg_lo[xcd + 1] - cg0;
     if (ncx <= 0) return;
     const int Q = static_cast<int>(blockDim.x / 64);
@@ -552,14 +470,9 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) scannd_flow_kernel(ScanNDArgs 
         if (item >= nitems) break;
         const int tb = static_cast<int>(item / nq);
         const int cg = cg0 + static_cast<int>(item % nq) * Q + w;
-        int lo = 0, hi = f.nbands - 1;   // band: last b with band_start[b] <= tb
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) / 2;
-            if (f.band_start[mid] <= tb) lo = mid;
-            else hi = mid - 1;
-        }
+        const int band = flow_band(f, tb);
         int ti[kMaxNd];
-        band_tile(p, lo, tb - f.band_start[lo], ti);
+        band_tile(p, band, tb - f.band_start[band], ti);
         int tl = 0;
 #pragma unroll
         for (int a = 0; a < ND; ++a) tl += ti[a] * tstride[a];
@@ -585,19 +498,6 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) scannd_flow_kernel(ScanNDArgs 
                                __HIP_MEMORY_SCOPE_AGENT);
     }
 }
-
-// Waves per dataflow workgroup: kFlowQ when it divides every XCD's group
-// count, else 1.
-static int flow_q(const FlowArgs &f) {
-    for (int x = 0; x < 8; ++x)
-        if ((f.cg_lo[x + 1] - f.cg_lo[x]) % kFlowQ != 0) return 1;
-    return kFlowQ;
-}
-
-// Dataflow state header (u32 words): per-XCD item counters (0-7), the
-// status word (8), the epoch (9); completion flags from word kFlowHead.
-constexpr size_t kFlowHead = 16;
-constexpr int kFlowStatus = 8, kFlowEpoch = 9;
 
 // Before each dataflow launch: zeroes the item counters and the status
 // word and advances the epoch. When the epoch wraps, every one of the
@@ -818,13 +718,15 @@ static unsigned flow_spin() {
     return spin;
 }
 
-// Which status word the latest ScanND forward on a (device, stream) left:
-// 0 none (band or level schedule), 1 the stream's ScanNDFlow block, 2 the
-// allocation-free scratch of the device.
+// Which status word the latest ScanND forward or backward on a (device,
+// stream) left: 0 none (band or level schedule), 1 the stream's ScanNDFlow
+// block, 2 a buffer given to the call (the allocation-free scratch of the
+// device, or the backward's workspace), whose header address is kept.
 struct LastFlow {
     int dev;
     hipStream_t stream;
     int kind;
+    const unsigned *word;
     unsigned long long tick;
 };
 constexpr int kMaxLastFlow = 64;
@@ -833,7 +735,7 @@ static int g_last_flow_n = 0;
 static unsigned long long g_last_flow_tick = 0;
 static std::mutex g_last_flow_mu;
 
-static void note_flow(hipStream_t s, int kind) {
+void note_flow(hipStream_t s, int kind, const unsigned *word) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return;
     std::lock_guard<std::mutex> guard(g_last_flow_mu);
@@ -849,22 +751,26 @@ static void note_flow(hipStream_t s, int kind) {
                 if (g_last_flow[i].tick < g_last_flow[idx].tick) idx = i;
         }
     }
-    g_last_flow[idx] = LastFlow{dev, s, kind, ++g_last_flow_tick};
+    g_last_flow[idx] = LastFlow{dev, s, kind, kind == 2 ? word : nullptr, ++g_last_flow_tick};
 }
 
-static int last_flow_kind(hipStream_t s) {
+static int last_flow_kind(hipStream_t s, const unsigned **word) {
+    *word = nullptr;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
     std::lock_guard<std::mutex> guard(g_last_flow_mu);
     for (int i = 0; i < g_last_flow_n; ++i)
-        if (g_last_flow[i].dev == dev && g_last_flow[i].stream == s) return g_last_flow[i].kind;
+        if (g_last_flow[i].dev == dev && g_last_flow[i].stream == s) {
+            *word = g_last_flow[i].word;
+            return g_last_flow[i].kind;
+        }
     return 0;
 }
 
 // The dataflow schedule runs grids of 2 or more dims on a device with the 8
 // XCDs the kernel reads from the hardware (XCC_ID 0-7);
 // KM_SCANND_SCHED=band keeps one launch per band.
-static bool flow_wanted(int nd) {
+bool flow_wanted(int nd) {
     const char *e = std::getenv("KM_SCANND_SCHED");
     if (nd < 2 || (e && std::strcmp(e, "band") == 0)) return false;
     int dev = 0;
@@ -872,19 +778,51 @@ static bool flow_wanted(int nd) {
     return device_xcds(dev) == 8;
 }
 
-// Dataflow state supplied by the caller instead of the stream's block (the
-// allocation-free entry point): a device buffer of `cap` words laid out as
-// above and the device's XCD count.
-struct FlowBuf {
-    unsigned *buf;
-    size_t cap;
-    int nxcc;
-};
-
 __global__ void __launch_bounds__(256) flow_clear(unsigned *p, long n) {
     for (long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x; i < n;
          i += static_cast<long>(gridDim.x) * 256)
         p[i] = 0u;
+}
+
+void flow_zero(unsigned *p, size_t words, hipStream_t s) {
+    hipLaunchKernelGGL(flow_clear, dim3(256), dim3(256), 0, s, p, static_cast<long>(words));
+}
+
+int flow_bind(hipStream_t s, size_t nflags_needed, FlowBuf *ext, FlowArgs &fa, int *kind) {
+    *kind = 0;
+    const size_t words = kFlowHead + nflags_needed;
+    unsigned *fbuf = nullptr;
+    long nflags = 0;   // flag words the state holds (cleared when the epoch wraps)
+    if (ext) {
+        if (ext->nxcc != 8) return 0;
+        if (words > ext->cap) {
+            set_error("scannd: the dataflow schedule needs %zu flag words, the scratch holds %zu",
+                      words, ext->cap);
+            return -1;
+        }
+        fbuf = ext->buf;
+        nflags = static_cast<long>(ext->cap - kFlowHead);
+        *kind = 2;
+    } else {
+        bool fresh = false;
+        size_t got = 0;
+        fbuf = static_cast<unsigned *>(Workspace::reserve(words * 4, s, WsUse::ScanNDFlow, &fresh, &got));
+        if (!fbuf) {
+            clear_error();   // no block: another schedule instead
+            return 0;
+        }
+        nflags = static_cast<long>(got / 4 - kFlowHead);
+        *kind = 1;
+        if (fresh)
+            hipLaunchKernelGGL(flow_clear, dim3(256), dim3(256), 0, s, fbuf, static_cast<long>(got / 4));
+    }
+    fa.counter = fbuf;
+    fa.status = fbuf + kFlowStatus;
+    fa.epoch = fbuf + kFlowEpoch;
+    fa.flags = fbuf + kFlowHead;
+    fa.spin = flow_spin();
+    hipLaunchKernelGGL(flow_reset, dim3(1), dim3(256), 0, s, fbuf, nflags);
+    return 1;
 }
 
 // Launches the forward on stream s. With allow_flow, grids of 3+ dims may
@@ -959,51 +897,18 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
         long ntiles = 0;
         for (int b = 0; b < nbands; ++b) ntiles += cnt[b];
         static thread_local FlowArgs fa;
-        unsigned *fbuf = nullptr;
-        long nflags = 0;   // flag words the block holds (cleared when the epoch wraps)
-        int kind = 0;
+        int kind = 0, bound = 0;
         if (flow_pref && nbands <= kMaxFlowBands && ntiles * a.ncg < 0x7fffffffL) {
-            const size_t words = kFlowHead + static_cast<size_t>(ntiles * a.ncg);
-            if (ext) {
-                if (ext->nxcc == 8) {
-                    if (words > ext->cap) {
-                        set_error("scannd: the dataflow schedule needs %zu flag words, the scratch "
-                                  "holds %zu", words, ext->cap);
-                        return -1;
-                    }
-                    fbuf = ext->buf;
-                    nflags = static_cast<long>(ext->cap - kFlowHead);
-                    kind = 2;
-                }
-            } else {
-                bool fresh = false;
-                size_t got = 0;
-                fbuf = static_cast<unsigned *>(
-                    Workspace::reserve(words * 4, s, WsUse::ScanNDFlow, &fresh, &got));
-                if (!fbuf) {
-                    clear_error();   // no block: the band schedule instead
-                } else {
-                    nflags = static_cast<long>(got / 4 - kFlowHead);
-                    kind = 1;
-                    if (fresh)
-                        hipLaunchKernelGGL(flow_clear, dim3(256), dim3(256), 0, s, fbuf,
-                                           static_cast<long>(got / 4));
-                }
-            }
-        }
-        note_flow(s, kind);
-        const FlowArgs *flow = nullptr;
-        if (fbuf) {
-            fa.counter = fbuf;
-            fa.status = fbuf + kFlowStatus;
-            fa.epoch = fbuf + kFlowEpoch;
-            fa.flags = fbuf + kFlowHead;
-            fa.spin = flow_spin();
             fa.nbands = nbands;
             for (int x = 0; x <= 8; ++x) fa.cg_lo[x] = static_cast<int>(static_cast<long>(x) * a.ncg / 8);
             fa.band_start[0] = 0;
             for (int b = 0; b < nbands; ++b) fa.band_start[b + 1] = fa.band_start[b] + static_cast<int>(cnt[b]);
-            hipLaunchKernelGGL(flow_reset, dim3(1), dim3(256), 0, s, fbuf, nflags);
+            bound = flow_bind(s, static_cast<size_t>(ntiles * a.ncg), ext, fa, &kind);
+            if (bound < 0) return -1;
+        }
+        note_flow(s, kind, kind == 2 ? fa.counter : nullptr);
+        const FlowArgs *flow = nullptr;
+        if (bound > 0) {
             flow = &fa;
             if (status) *status = fa.status;
         }
@@ -1323,16 +1228,9 @@ int scannd_fwd_noalloc(const ScanNDParams *p, hipStream_t s) {
 // km_scannd_status).
 int scannd_status(hipStream_t s) {
     if (!gpu_ready()) return -1;
-    const int kind = last_flow_kind(s);
     const unsigned *word = nullptr;
-    if (kind == 1) {
-        word = static_cast<const unsigned *>(Workspace::find(s, WsUse::ScanNDFlow));
-    } else if (kind == 2) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -1;
-        std::lock_guard<std::mutex> guard(g_noalloc_mu);
-        word = g_noalloc[dev].ptr;
-    }
+    const int kind = last_flow_kind(s, &word);
+    if (kind == 1) word = static_cast<const unsigned *>(Workspace::find(s, WsUse::ScanNDFlow));
     if (hipStreamSynchronize(s) != hipSuccess) {
         set_error("km_scannd_status: %s", hipGetErrorString(hipGetLastError()));
         return -1;

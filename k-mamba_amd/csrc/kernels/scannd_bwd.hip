@@ -26,6 +26,7 @@
 #include <cstring>
 
 #include "km_device.hpp"
+#include "scannd_flow.hpp"
 #include "../km_runtime.hpp"
 #include "kmamba_km.h"
 #include "scan_nd.h"
@@ -116,7 +117,12 @@ __device__ __forceinline__ int adj_oDM(const AdjWin &w, long r) { return static_
 __device__ __forceinline__ float adj_dyc(const AdjWin &w, long r) {
     return bio<f32_t>::ld(w.dy, w.vd, adj_oD(w, r)) * bio<f32_t>::ld(w.C, w.vc, adj_oDM(w, r));
 }
-__device__ __forceinline__ float adj_g(const AdjWin &w, long r) { return bio<f32_t>::ld(w.g, w.vc, adj_oDM(w, r)); }
+// A successor's state; COH: written by another workgroup of the same launch
+// (the dataflow schedule), read past the CU's L1.
+template <bool COH = false>
+__device__ __forceinline__ float adj_g(const AdjWin &w, long r) {
+    return COH ? bio<f32_t>::ld_agent(w.g, w.vc, adj_oDM(w, r)) : bio<f32_t>::ld(w.g, w.vc, adj_oDM(w, r));
+}
 __device__ __forceinline__ float adj_dl(const AdjWin &w, int ax, long r) {
     return bio<f32_t>::ld(w.dl, w.vd, static_cast<int>(ax * w.sAx) + adj_oD(w, r));
 }
@@ -134,12 +140,12 @@ __device__ __forceinline__ void adj_store(const AdjWin &w, long r, float g) {
 // launch (the next band). Workgroups are numbered XCD-major (xcd_remap):
 // the channel groups of a tile, which share the dy / delta row lines (four
 // channels, 16 bytes, each), run on one XCD's L2.
-template <int TR, int TW, int RB>
-__global__ void __launch_bounds__(64) nd_adjoint_tile2d(NdBwdArgs a, int band, int nt1, int ncg) {
-    const int lane = threadIdx.x;
-    const int lb = static_cast<int>(xcd_remap(blockIdx.x, gridDim.x));
-    const int o = lb / ncg, cg = lb - o * ncg;
-    const int ti0 = (band > nt1 - 1 ? band - (nt1 - 1) : 0) + o, ti1 = band - ti0;
+//
+// adj_tile2d runs one (tile (ti0, ti1), channel group cg); wait() runs before
+// any state written by another tile is read (false: nothing is computed).
+template <int TR, int TW, int RB, bool COH, typename Wait>
+__device__ __forceinline__ bool adj_tile2d(const NdBwdArgs &a, int ti0, int ti1, int cg, Wait &&wait) {
+    const int lane = threadIdx.x & 63;
     const long n0 = a.dims[0], n1 = a.dims[1];
     const long r0 = static_cast<long>(ti0) * TR, r1 = std::min<long>(n0, r0 + TR);
     const long j0 = static_cast<long>(ti1) * TW, j1 = std::min<long>(n1, j0 + TW);
@@ -167,14 +173,15 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile2d(NdBwdArgs a, int band, i
             rw.d1[jj] = adj_dl(w, 1, q);
         }
         const long qr = rq + std::min<long>(j1, n1 - 1);
-        rw.gr = adj_g(w, qr);
+        rw.gr = adj_g<COH>(w, qr);
         rw.dr1 = adj_dl(w, 1, qr);
     };
+    if (!wait()) return false;
     float gb[TW], db0[TW];
 #pragma unroll
     for (int jj = 0; jj < TW; ++jj) {
         const long q = std::min<long>(r1, n0 - 1) * n1 + std::min<long>(j0 + jj, j1 - 1) - qb;
-        gb[jj] = adj_g(w, q);
+        gb[jj] = adj_g<COH>(w, q);
         db0[jj] = adj_dl(w, 0, q);
     }
     // Rows go in batches of RB, the next batch's loads issued before the
@@ -219,6 +226,15 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile2d(NdBwdArgs a, int band, i
             compute_batch(rt - RB, bb);
         }
     }
+    return true;
+}
+
+template <int TR, int TW, int RB>
+__global__ void __launch_bounds__(64) nd_adjoint_tile2d(NdBwdArgs a, int band, int nt1, int ncg) {
+    const int lb = static_cast<int>(xcd_remap(blockIdx.x, gridDim.x));
+    const int o = lb / ncg, cg = lb - o * ncg;
+    const int ti0 = (band > nt1 - 1 ? band - (nt1 - 1) : 0) + o;
+    adj_tile2d<TR, TW, RB, false>(a, ti0, band - ti0, cg, [] { return true; });
 }
 
 // 3D grids with D*M a multiple of 64: the same by TP x TR x TW tiles (axis
@@ -226,15 +242,13 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile2d(NdBwdArgs a, int band, i
 // a wave walks its tile's planes, rows and points in reverse, keeping the
 // plane below (g and axis-0 delta of every (row, column) of the tile) and
 // the row below in registers (loops fully unrolled: no dynamic indexing).
-template <int TP, int TR, int TW>
-__global__ void __launch_bounds__(64) nd_adjoint_tile3d(NdBwdArgs a, const int *tiles, int ncg) {
-    const int lane = threadIdx.x;
-    const int lb = static_cast<int>(xcd_remap(blockIdx.x, gridDim.x));
-    const int o = lb / ncg, cg = lb - o * ncg;
+template <int TP, int TR, int TW, bool COH, typename Wait>
+__device__ __forceinline__ bool adj_tile3d(const NdBwdArgs &a, int tp, int tr, int tw, int cg, Wait &&wait) {
+    const int lane = threadIdx.x & 63;
     const long n0 = a.dims[0], n1 = a.dims[1], n2 = a.dims[2];
-    const long p0 = static_cast<long>(tiles[3 * o]) * TP, p1 = std::min<long>(n0, p0 + TP);
-    const long r0 = static_cast<long>(tiles[3 * o + 1]) * TR, r1 = std::min<long>(n1, r0 + TR);
-    const long j0 = static_cast<long>(tiles[3 * o + 2]) * TW, j1 = std::min<long>(n2, j0 + TW);
+    const long p0 = static_cast<long>(tp) * TP, p1 = std::min<long>(n0, p0 + TP);
+    const long r0 = static_cast<long>(tr) * TR, r1 = std::min<long>(n1, r0 + TR);
+    const long j0 = static_cast<long>(tw) * TW, j1 = std::min<long>(n2, j0 + TW);
     const long DM = a.D * a.M, s0 = n1 * n2;
     const long c = static_cast<long>(cg) * 64 + lane;
     const long d = c / a.M;
@@ -257,9 +271,10 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile3d(NdBwdArgs a, const int *
             rw.d2[jj] = adj_dl(w, 2, q);
         }
         const long qr = qof(pp, rr, std::min<long>(j1, n2 - 1));
-        rw.gr = adj_g(w, qr);
+        rw.gr = adj_g<COH>(w, qr);
         rw.dr2 = adj_dl(w, 2, qr);
     };
+    if (!wait()) return false;
     // Plane below: successors along axis 0 of every (row, column).
     float gp[TR][TW], dp0[TR][TW];
 #pragma unroll
@@ -268,7 +283,7 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile3d(NdBwdArgs a, const int *
         for (int jj = 0; jj < TW; ++jj) {
             const long q = qof(std::min<long>(p1, n0 - 1), std::min<long>(r0 + ri, r1 - 1),
                                std::min<long>(j0 + jj, j1 - 1));
-            gp[ri][jj] = adj_g(w, q);
+            gp[ri][jj] = adj_g<COH>(w, q);
             dp0[ri][jj] = adj_dl(w, 0, q);
         }
     for (long pp = p1 - 1; pp >= p0; --pp) {
@@ -278,7 +293,7 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile3d(NdBwdArgs a, const int *
 #pragma unroll
         for (int jj = 0; jj < TW; ++jj) {
             const long q = qof(pp, std::min<long>(r1, n1 - 1), std::min<long>(j0 + jj, j1 - 1));
-            gb[jj] = adj_g(w, q);
+            gb[jj] = adj_g<COH>(w, q);
             db1[jj] = adj_dl(w, 1, q);
         }
         Row cur, nxt;
@@ -311,6 +326,108 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile3d(NdBwdArgs a, const int *
                 cur = nxt;
             }
         }
+    }
+    return true;
+}
+
+template <int TP, int TR, int TW>
+__global__ void __launch_bounds__(64) nd_adjoint_tile3d(NdBwdArgs a, const int *tiles, int ncg) {
+    const int lb = static_cast<int>(xcd_remap(blockIdx.x, gridDim.x));
+    const int o = lb / ncg, cg = lb - o * ncg;
+    adj_tile3d<TP, TR, TW, false>(a, tiles[3 * o], tiles[3 * o + 1], tiles[3 * o + 2], cg, [] { return true; });
+}
+
+// The adjoint sweep on the dataflow schedule (scannd_flow.hpp), one launch:
+// items in reverse band order (a tile's successors come first), a tile
+// waiting on its successor along each axis; channel groups pinned to XCDs,
+// workgroups of flow_q waves, one group per wave. 2D tiles are 8 rows x 4
+// points (the critical path runs through nt0 + nt1 - 1 of them), 3D tiles
+// those of the band schedule.
+constexpr int kAdjFTR = 8, kAdjFTW = 4;   // 2D dataflow tiles (rows, points)
+
+// NaN into the states of one (tile, channel group) whose wait gave up, so
+// every tile that depends on it, and every gradient, turns NaN too.
+template <int ND>
+__device__ void adj_tile_poison(const NdBwdArgs &a, const int *ti, const int *text, int cg) {
+    const long DM = a.D * a.M;
+    const long c = static_cast<long>(cg) * 64 + (threadIdx.x & 63);
+    long lo[ND], ext[ND], npts = 1;
+#pragma unroll
+    for (int ax = 0; ax < ND; ++ax) {
+        lo[ax] = static_cast<long>(ti[ax]) * text[ax];
+        ext[ax] = std::min<long>(text[ax], a.dims[ax] - lo[ax]);
+        npts *= ext[ax];
+    }
+    for (long q = 0; q < npts; ++q) {
+        long rem = q, off = 0;
+#pragma unroll
+        for (int ax = ND - 1; ax >= 0; --ax) {
+            const long ia = rem % ext[ax];
+            rem /= ext[ax];
+            off += (lo[ax] + ia) * a.strides[ax];
+        }
+        a.dB[off * DM + c] = __builtin_nanf("");
+    }
+}
+
+template <int ND>
+__global__ void __launch_bounds__(64 * kFlowQ, 2) nd_adjoint_flow(NdBwdArgs a, FlowArgs f, int nt0, int nt1,
+                                                                  int nt2, int ncg) {
+    const int xcd = flow_xcd();
+    const int cg0 = f.cg_lo[xcd], ncx = f.cg_lo[xcd + 1] - cg0;
+    if (ncx <= 0) return;
+    const int Q = static_cast<int>(blockDim.x / 64);
+    const int nq = ncx / Q;                             // runs of groups per tile
+    const int w = static_cast<int>(threadIdx.x / 64);
+    const int ntiles = f.band_start[f.nbands];
+    const unsigned nitems = static_cast<unsigned>(ntiles) * static_cast<unsigned>(nq);
+    const unsigned epoch = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(f.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const int ntile[3] = {nt0, nt1, nt2};
+    const int text[3] = {ND == 2 ? kAdjFTR : kAdj3P, ND == 2 ? kAdjFTW : kAdj3R, kAdj3W};
+    int tstride[3];
+    tstride[ND - 1] = 1;
+#pragma unroll
+    for (int ax = ND - 2; ax >= 0; --ax) tstride[ax] = tstride[ax + 1] * ntile[ax + 1];
+    __shared__ unsigned s_item[2];
+    for (int it = 0;; ++it) {
+        // One fetch per workgroup, handed to every wave through LDS (two
+        // alternating slots: the barrier of the next fetch orders them).
+        if (threadIdx.x == 0) s_item[it & 1] = atomicAdd(&f.counter[xcd], 1u);
+        __syncthreads();
+        const unsigned item = __builtin_amdgcn_readfirstlane(s_item[it & 1]);
+        if (item >= nitems) break;
+        const int tb = ntiles - 1 - static_cast<int>(item / nq);   // reverse band order
+        const int cg = cg0 + static_cast<int>(item % nq) * Q + w;
+        const int band = flow_band(f, tb);
+        int ti[3] = {0, 0, 0};
+        band_tile_n(ND, ntile, band, tb - f.band_start[band], ti);
+        int tl = 0;
+#pragma unroll
+        for (int ax = 0; ax < ND; ++ax) tl += ti[ax] * tstride[ax];
+        auto successors_done = [&]() {
+            bool ready = true;
+#pragma unroll
+            for (int ax = 0; ax < ND; ++ax)
+                if (ti[ax] + 1 < ntile[ax])
+                    ready = flow_wait(f.flags + static_cast<long>(tl + tstride[ax]) * ncg + cg, epoch,
+                                      f.spin) && ready;
+            return ready;
+        };
+        bool ok;
+        if constexpr (ND == 2)
+            ok = adj_tile2d<kAdjFTR, kAdjFTW, 4, true>(a, ti[0], ti[1], cg, successors_done);
+        else
+            ok = adj_tile3d<kAdj3P, kAdj3R, kAdj3W, true>(a, ti[0], ti[1], ti[2], cg, successors_done);
+        if (!ok) {
+            adj_tile_poison<ND>(a, ti, text, cg);
+            if ((threadIdx.x & 63) == 0)
+                __hip_atomic_store(f.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_s_waitcnt(0);   // this wave's g stores acknowledged by L2
+        if ((threadIdx.x & 63) == 0)
+            __hip_atomic_store(f.flags + static_cast<long>(tl) * ncg + cg, epoch, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -848,6 +965,19 @@ constexpr int kGradTR2 = 8, kGradTW2 = 64;                  // 2D gradient tiles
 constexpr int kGradTP3 = 4, kGradTR3 = 8, kGradTW3 = 8;     // 3D gradient tiles
 constexpr int kGradTPW3 = 1;                                 // 3D tiles per workgroup (2 and 4 measured slower)
 
+// The adjoint sweep's dataflow tiles per axis (0 past nd).
+static void adj_flow_tiles(const KMScanNDBwd *a, int nd, int nt[3]) {
+    nt[0] = nt[1] = nt[2] = 0;
+    if (nd == 2) {
+        nt[0] = static_cast<int>((a->dims[0] + kAdjFTR - 1) / kAdjFTR);
+        nt[1] = static_cast<int>((a->dims[1] + kAdjFTW - 1) / kAdjFTW);
+    } else if (nd == 3) {
+        nt[0] = static_cast<int>((a->dims[0] + kAdj3P - 1) / kAdj3P);
+        nt[1] = static_cast<int>((a->dims[1] + kAdj3R - 1) / kAdj3R);
+        nt[2] = static_cast<int>((a->dims[2] + kAdj3W - 1) / kAdj3W);
+    }
+}
+
 struct NdBwdShape {
     long P, nd, D, M;
     bool lanes;          // M a power of two <= 64: nd_adjoint_grads_lanes
@@ -856,6 +986,7 @@ struct NdBwdShape {
     int db;
     long qc, nbx, nby;
     size_t offs_bytes, nbr_bytes, part_bytes, tile_bytes;
+    size_t flow_bytes;   // the adjoint dataflow's counters, status, epoch and flags (tiled sweeps)
 };
 
 static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
@@ -939,6 +1070,13 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
         s.tile_bytes = align_up(sizeof(int) * 3 * nt, 256);
     }
     s.part_bytes = sizeof(float) * s.nbx * s.nd * s.D * s.M;
+    s.flow_bytes = 0;
+    if (s.atile2 || s.tile_bytes) {
+        int nt[3];
+        adj_flow_tiles(a, static_cast<int>(s.nd), nt);
+        const long ntiles = static_cast<long>(nt[0]) * nt[1] * (s.nd == 3 ? nt[2] : 1);
+        s.flow_bytes = align_up(4 * (kFlowHead + static_cast<size_t>(ntiles) * (s.D * s.M / 64)), 256);
+    }
     return true;
 }
 
@@ -973,12 +1111,64 @@ static void grads_tile_launch(const NdBwdArgs &args, const NdBwdShape &s, hipStr
     }
 }
 
+// Binds the adjoint sweep's dataflow state (band table, channel groups per
+// XCD) when the tiled sweep applies, the device has 8 XCDs and the bands fit
+// the kernel arguments: in the caller's workspace (ext, cleared here, so
+// nothing is allocated) or in the stream's dataflow block. Returns 1 when
+// bound, 0 for the band schedule, -1 on an error.
+static int adj_flow_setup(const KMScanNDBwd *a, const NdBwdShape &s, hipStream_t st, FlowArgs &fa,
+                          int nt[3], FlowBuf *ext) {
+    const bool tiled = (s.nd == 2 && s.atile2) || (s.nd == 3 && s.tile_bytes);
+    if (!tiled || !flow_wanted(s.nd)) return 0;
+    adj_flow_tiles(a, static_cast<int>(s.nd), nt);
+    const int nb = nt[0] + nt[1] + (s.nd == 3 ? nt[2] : 1) - (s.nd == 3 ? 2 : 1);
+    const long ncg = s.D * s.M / 64;
+    if (nb > kMaxFlowBands || nb <= 0) return 0;
+    fa.nbands = nb;
+    for (int x = 0; x <= 8; ++x) fa.cg_lo[x] = static_cast<int>(static_cast<long>(x) * ncg / 8);
+    fa.band_start[0] = 0;
+    for (int b = 0; b < nb; ++b) {
+        long c = 0;
+        if (s.nd == 2) {
+            const int lo = std::max(0, b - (nt[1] - 1)), hi = std::min(b, nt[0] - 1);
+            c = hi >= lo ? hi - lo + 1 : 0;
+        } else {
+            for (int t0 = 0; t0 < nt[0] && t0 <= b; ++t0) {
+                const int r = b - t0, lo = std::max(0, r - (nt[2] - 1)), hi = std::min(r, nt[1] - 1);
+                c += hi >= lo ? hi - lo + 1 : 0;
+            }
+        }
+        fa.band_start[b + 1] = fa.band_start[b] + static_cast<int>(c);
+    }
+    const long ntiles = fa.band_start[nb];
+    if (ntiles * ncg >= 0x7fffffffL) return 0;
+    if (ext) flow_zero(ext->buf, ext->cap, st);
+    int kind = 0;
+    const int bound = flow_bind(st, static_cast<size_t>(ntiles * ncg), ext, fa, &kind);
+    note_flow(st, kind, kind == 2 ? fa.counter : nullptr);
+    return bound;
+}
+
 template <int ND>
 static void nd_bwd_launch(const NdBwdArgs &args, const NdBwdShape &s, const KMWavefrontPlan *plan,
-                          float *dA, const int *dtiles, const std::vector<long> &bstart, hipStream_t st) {
+                          float *dA, const int *dtiles, const std::vector<long> &bstart, hipStream_t st,
+                          const FlowArgs *flow, const int *nt) {
     const long DM = s.D * s.M;
     const unsigned bx = static_cast<unsigned>((DM + 255) / 256);
-    if (ND == 3 && s.tile_bytes) {
+    if ((ND == 2 || ND == 3) && flow) {
+        // One dataflow launch: 8k workgroups of Q waves (k <= 256 / Q, two
+        // waves per SIMD), k = the largest per-XCD item count.
+        const int q = flow_q(*flow);
+        const long ntiles = flow->band_start[flow->nbands];
+        long per_xcd = 0;
+        for (int x = 0; x < 8; ++x)
+            per_xcd = std::max<long>(per_xcd, ntiles * ((flow->cg_lo[x + 1] - flow->cg_lo[x]) / q));
+        const long grid = 8 * std::min<long>(per_xcd, 256 / q);
+        if (grid > 0)
+            hipLaunchKernelGGL((nd_adjoint_flow<ND == 2 ? 2 : 3>), dim3(static_cast<unsigned>(grid)),
+                               dim3(64 * q), 0, st, args, *flow, nt[0], nt[1], nt[2],
+                               static_cast<int>(DM / 64));
+    } else if (ND == 3 && s.tile_bytes) {
         const int ncg = static_cast<int>(DM / 64);
         for (long b = static_cast<long>(bstart.size()) - 2; b >= 0; --b) {
             const long n = bstart[b + 1] - bstart[b];
@@ -1033,7 +1223,7 @@ size_t km_scannd_bwd_workspace_bytes(const KMScanNDBwd *a) {
     km::clear_error();
     km::NdBwdShape s;
     if (!km::nd_bwd_shape(a, s)) return 0;
-    return s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes;
+    return s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes + s.flow_bytes;
 }
 
 int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
@@ -1051,7 +1241,7 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
     }
     if (!km::gpu_ready()) return -1;
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    const size_t need = s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes;
+    const size_t need = s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes + s.flow_bytes;
     char *ws = static_cast<char *>(a->workspace);
     if (ws) {
         if (a->workspace_bytes < need) {
@@ -1085,10 +1275,25 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
         args.strides[ax] = stride;
         stride *= a->dims[ax];
     }
+    // The adjoint sweep on the dataflow schedule where it applies (no tile
+    // list to upload), else by tile bands.
+    static thread_local km::FlowArgs fa;
+    int nt[3] = {0, 0, 0};
+    // With the caller's workspace the flags live in it (cleared per call);
+    // otherwise in the stream's dataflow block.
+    km::FlowBuf wflow{reinterpret_cast<unsigned *>(ws + s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes),
+                      s.flow_bytes / 4, 8};
+    const int fb = km::adj_flow_setup(a, s, st, fa, nt, (a->workspace && s.flow_bytes) ? &wflow : nullptr);
+    if (fb < 0) {
+        if (plan) km_wavefront_plan_free(plan);
+        return -1;
+    }
+    if (fb == 0) km::note_flow(st, 0);
+    const km::FlowArgs *flow = fb > 0 ? &fa : nullptr;
     // 3D tile bands: each band's tiles (tile-index sum b), bands contiguous.
     std::vector<int> tl;
     std::vector<long> bstart;
-    if (s.tile_bytes) {
+    if (s.tile_bytes && !flow) {
         const long nt0 = (a->dims[0] + km::kAdj3P - 1) / km::kAdj3P;
         const long nt1 = (a->dims[1] + km::kAdj3R - 1) / km::kAdj3R;
         const long nt2 = (a->dims[2] + km::kAdj3W - 1) / km::kAdj3W;
@@ -1121,14 +1326,14 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
     } else {
         const int *dtiles = reinterpret_cast<const int *>(tile_ws);
         switch (s.nd) {
-        case 1: km::nd_bwd_launch<1>(args, s, plan, a->dA, dtiles, bstart, st); break;
-        case 2: km::nd_bwd_launch<2>(args, s, plan, a->dA, dtiles, bstart, st); break;
-        case 3: km::nd_bwd_launch<3>(args, s, plan, a->dA, dtiles, bstart, st); break;
-        case 4: km::nd_bwd_launch<4>(args, s, plan, a->dA, dtiles, bstart, st); break;
-        case 5: km::nd_bwd_launch<5>(args, s, plan, a->dA, dtiles, bstart, st); break;
-        case 6: km::nd_bwd_launch<6>(args, s, plan, a->dA, dtiles, bstart, st); break;
-        case 7: km::nd_bwd_launch<7>(args, s, plan, a->dA, dtiles, bstart, st); break;
-        default: km::nd_bwd_launch<8>(args, s, plan, a->dA, dtiles, bstart, st); break;
+        case 1: km::nd_bwd_launch<1>(args, s, plan, a->dA, dtiles, bstart, st, flow, nt); break;
+        case 2: km::nd_bwd_launch<2>(args, s, plan, a->dA, dtiles, bstart, st, flow, nt); break;
+        case 3: km::nd_bwd_launch<3>(args, s, plan, a->dA, dtiles, bstart, st, flow, nt); break;
+        case 4: km::nd_bwd_launch<4>(args, s, plan, a->dA, dtiles, bstart, st, flow, nt); break;
+        case 5: km::nd_bwd_launch<5>(args, s, plan, a->dA, dtiles, bstart, st, flow, nt); break;
+        case 6: km::nd_bwd_launch<6>(args, s, plan, a->dA, dtiles, bstart, st, flow, nt); break;
+        case 7: km::nd_bwd_launch<7>(args, s, plan, a->dA, dtiles, bstart, st, flow, nt); break;
+        default: km::nd_bwd_launch<8>(args, s, plan, a->dA, dtiles, bstart, st, flow, nt); break;
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) {

@@ -560,7 +560,8 @@ def scannd_fwd(dims, x, A, B, Cm, delta, h, y, stream=None, theta=None, lam=None
 
 def scannd_status(stream=None) -> int:
     """km_scannd_status: waits for the stream; 0 when the latest ScanND
-    forward on it is exact, 1 when a dataflow wait gave up (NaN tiles)."""
+    forward or backward on it is exact, 1 when a dataflow wait gave up (NaN
+    tiles)."""
     rc = km_scannd_status_c(C.c_void_p(stream_handle(stream)))
     if rc < 0:
         raise RuntimeError(f"km_scannd_status: {km_last_error()}")

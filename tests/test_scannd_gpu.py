@@ -395,6 +395,78 @@ def test_backward_vs_oracle(dims, D, M):
         assert err <= 1e-4, f"{k}: normwise error {err:.2e}"
 
 
+@pytest.mark.parametrize("dims,D,M", [((33, 65), 8, 16), ((64, 96), 4, 16), ((9, 6, 11), 4, 16),
+                                      ((40, 24, 24), 16, 16), ((7, 13, 17), 8, 8)])
+def test_backward_dataflow_and_band_schedules_agree(dims, D, M, monkeypatch):
+    # The adjoint sweep on the dataflow schedule (one launch, tiles waiting
+    # on their successors) and one launch per tile band compute every state
+    # with the same arithmetic: every gradient agrees bit for bit, and the
+    # band schedule matches the oracle.
+    x, A, B, Cm, dt, h, dy = bwd_inputs(dims, D, M, 3)
+    a = run_bwd(dims, x, A, B, Cm, dt, h, dy)
+    monkeypatch.setenv("KM_SCANND_SCHED", "band")
+    b = run_bwd(dims, x, A, B, Cm, dt, h, dy)
+    for k in a:
+        assert np.isfinite(a[k]).all(), k
+        assert np.array_equal(a[k].view(np.uint32), b[k].view(np.uint32)), k
+    want = O.scannd_backward(dims, x, A, B, Cm, dt, h, dy, fast=True)
+    for k in want:
+        err = np.abs(b[k] - want[k]).max() / max(np.abs(want[k]).max(), 1e-30)
+        assert err <= 1e-4, f"{k}: normwise error {err:.2e}"
+
+
+_BWD_BUDGET0 = r"""
+import sys
+import numpy as np, torch
+sys.path[:0] = [sys.argv[2], sys.argv[3]]
+import kmamba as K
+d = np.load(sys.argv[1])
+dims = tuple(int(v) for v in d["dims"])
+t = [torch.from_numpy(d[k]).cuda() for k in ("x", "A", "B", "C", "dt", "h", "dy")]
+P, D = t[0].shape
+nd, _, M = t[1].shape
+outs = [torch.zeros(s, device="cuda") for s in ((P, D), (nd, P, D), (nd, D, M), (P, D, M), (P, D, M))]
+K.scannd_bwd(dims, *t, *outs)
+res = {"status": np.int64(K.scannd_status())}
+for k, v in zip(("dx", "ddelta", "dA", "dB", "dC"), outs):
+    res[k] = v.cpu().numpy()
+np.savez(sys.argv[4], **res)
+print("bwd budget0 done", flush=True)
+"""
+
+
+@pytest.mark.parametrize("dims,D,M", [((33, 65), 8, 16), ((9, 6, 11), 4, 16)])
+def test_backward_dataflow_wait_budget_exhausted_fails_loudly(dims, D, M, tmp_path):
+    # KM_SCANND_FLOW_SPIN=0 (read once per process, so a child process):
+    # every wait of the adjoint sweep gives up without polling, every kernel
+    # still exits normally. A tile that had a successor writes NaN instead of
+    # its states, so its gradients are NaN (never silently wrong), and
+    # km_scannd_status reports the failed wait. The last tile, which has no
+    # successor, is exact.
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parent.parent
+    x, A, B, Cm, dt, h, dy = bwd_inputs(dims, D, M, 4)
+    src, dst = tmp_path / "in.npz", tmp_path / "out.npz"
+    np.savez(src, dims=np.array(dims), x=x, A=A, B=B, C=Cm, dt=dt, h=h, dy=dy)
+    env = dict(__import__("os").environ, KM_SCANND_FLOW_SPIN="0")
+    r = subprocess.run([sys.executable, "-c", _BWD_BUDGET0, str(src), str(root / "k-mamba_amd"),
+                        str(root / "oracle"), str(dst)], env=env, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    out = np.load(dst)
+    assert int(out["status"]) == 1
+    # dB = g * mean(delta) * x carries the adjoint state g (dC = dy * h does not).
+    dB = out["dB"].reshape(dims + (D, M))
+    assert np.isnan(dB).any(), "a failed wait must not leave finite gradients behind"
+    assert np.isnan(dB[(0,) * len(dims)]).all()      # the first point depends on every other
+    assert np.isnan(out["dx"]).any()
+    want = O.scannd_backward(dims, x, A, B, Cm, dt, h, dy, fast=True)
+    last = (-1,) * len(dims)
+    np.testing.assert_allclose(dB[last], want["dB"].reshape(dims + (D, M))[last], rtol=1e-5, atol=1e-6)
+
+
 def test_backward_deterministic_and_workspace():
     dims, D, M = (33, 40), 8, 16
     x, A, B, Cm, dt, h, dy = bwd_inputs(dims, D, M, 1)
