@@ -163,7 +163,9 @@ __device__ __forceinline__ bool adj_tile2d(const NdBwdArgs &a, int ti0, int ti1,
         float dyc[TW], d0[TW], d1[TW];
         float gr, dr1;
     };
-    auto load_row = [&](long r, Row &rw) __attribute__((always_inline)) {
+    // The operands no other tile writes (ops) and the right successor's
+    // state (succ).
+    auto load_ops = [&](long r, Row &rw) __attribute__((always_inline)) {
         const long rq = r * n1 - qb;
 #pragma unroll
         for (int jj = 0; jj < TW; ++jj) {
@@ -172,11 +174,22 @@ __device__ __forceinline__ bool adj_tile2d(const NdBwdArgs &a, int ti0, int ti1,
             rw.d0[jj] = adj_dl(w, 0, q);
             rw.d1[jj] = adj_dl(w, 1, q);
         }
-        const long qr = rq + std::min<long>(j1, n1 - 1);
-        rw.gr = adj_g<COH>(w, qr);
-        rw.dr1 = adj_dl(w, 1, qr);
+        rw.dr1 = adj_dl(w, 1, rq + std::min<long>(j1, n1 - 1));
     };
+    auto load_succ = [&](long r, Row &rw) __attribute__((always_inline)) {
+        rw.gr = adj_g<COH>(w, r * n1 - qb + std::min<long>(j1, n1 - 1));
+    };
+    auto load_row = [&](long r, Row &rw) __attribute__((always_inline)) {
+        load_ops(r, rw);
+        load_succ(r, rw);
+    };
+    // The first batch's operands go out before the wait on the successors.
+    Row ba[RB], bb[RB];
+#pragma unroll
+    for (int i = 0; i < RB; ++i) load_ops(std::max<long>(r1 - 1 - i, r0), ba[i]);
     if (!wait()) return false;
+#pragma unroll
+    for (int i = 0; i < RB; ++i) load_succ(std::max<long>(r1 - 1 - i, r0), ba[i]);
     float gb[TW], db0[TW];
 #pragma unroll
     for (int jj = 0; jj < TW; ++jj) {
@@ -216,8 +229,6 @@ __device__ __forceinline__ bool adj_tile2d(const NdBwdArgs &a, int ti0, int ti1,
             }
         }
     };
-    Row ba[RB], bb[RB];
-    load_batch(r1 - 1, ba);
     for (long rt = r1 - 1; rt >= r0; rt -= 2 * RB) {
         load_batch(rt - RB, bb);
         compute_batch(rt, ba);
@@ -244,6 +255,7 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile2d(NdBwdArgs a, int band, i
 // the row below in registers (loops fully unrolled: no dynamic indexing).
 template <int TP, int TR, int TW, bool COH, typename Wait>
 __device__ __forceinline__ bool adj_tile3d(const NdBwdArgs &a, int tp, int tr, int tw, int cg, Wait &&wait) {
+    static_assert(TR >= 3, "a ring of TR rows holds the current row and two prefetched ones");
     const int lane = threadIdx.x & 63;
     const long n0 = a.dims[0], n1 = a.dims[1], n2 = a.dims[2];
     const long p0 = static_cast<long>(tp) * TP, p1 = std::min<long>(n0, p0 + TP);
@@ -261,7 +273,19 @@ __device__ __forceinline__ bool adj_tile3d(const NdBwdArgs &a, int tp, int tr, i
         float gr, dr2;
     };
     auto qof = [&](long pp, long rr, long jj) { return pp * s0 + rr * n2 + jj - qb; };
-    auto load_row = [&](long pp, long rr, Row &rw) __attribute__((always_inline)) {
+    // Rows in walk order: k = 0, 1, ... is plane p1 - 1 - k / TR, row
+    // r0 + TR - 1 - k % TR (rows past r1 and k past the tile load the last
+    // row again, unused). Operands no other tile writes (ops) and the right
+    // successor's state (succ) load apart.
+    const int nk = static_cast<int>(p1 - p0) * TR;
+    auto row_at = [&](int k, long &pp, long &rr) __attribute__((always_inline)) {
+        k = min(k, nk - 1);
+        pp = p1 - 1 - k / TR;
+        rr = std::min<long>(r0 + TR - 1 - k % TR, r1 - 1);
+    };
+    auto load_ops = [&](int k, Row &rw) __attribute__((always_inline)) {
+        long pp, rr;
+        row_at(k, pp, rr);
 #pragma unroll
         for (int jj = 0; jj < TW; ++jj) {
             const long q = qof(pp, rr, std::min<long>(j0 + jj, j1 - 1));
@@ -270,11 +294,32 @@ __device__ __forceinline__ bool adj_tile3d(const NdBwdArgs &a, int tp, int tr, i
             rw.d1[jj] = adj_dl(w, 1, q);
             rw.d2[jj] = adj_dl(w, 2, q);
         }
-        const long qr = qof(pp, rr, std::min<long>(j1, n2 - 1));
-        rw.gr = adj_g<COH>(w, qr);
-        rw.dr2 = adj_dl(w, 2, qr);
+        rw.dr2 = adj_dl(w, 2, qof(pp, rr, std::min<long>(j1, n2 - 1)));
     };
+    auto load_succ = [&](int k, Row &rw) __attribute__((always_inline)) {
+        long pp, rr;
+        row_at(k, pp, rr);
+        rw.gr = adj_g<COH>(w, qof(pp, rr, std::min<long>(j1, n2 - 1)));
+    };
+    // Row below the tile's last row of plane pp: successors along axis 1.
+    auto load_below = [&](long pp, float (&gbx)[TW], float (&dbx)[TW]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int jj = 0; jj < TW; ++jj) {
+            const long q = qof(pp, std::min<long>(r1, n1 - 1), std::min<long>(j0 + jj, j1 - 1));
+            gbx[jj] = adj_g<COH>(w, q);
+            dbx[jj] = adj_dl(w, 1, q);
+        }
+    };
+    // A ring of TR rows (slot = row's index within its plane): row k + 2 is
+    // loaded before row k computes (and before its g stores, which would
+    // otherwise order every later load). The first two rows' operands go out
+    // before the wait on the successors.
+    Row R[TR];
+    load_ops(0, R[TR - 1]);
+    load_ops(1, R[TR - 2]);
     if (!wait()) return false;
+    load_succ(0, R[TR - 1]);
+    load_succ(1, R[TR - 2]);
     // Plane below: successors along axis 0 of every (row, column).
     float gp[TR][TW], dp0[TR][TW];
 #pragma unroll
@@ -286,23 +331,29 @@ __device__ __forceinline__ bool adj_tile3d(const NdBwdArgs &a, int tp, int tr, i
             gp[ri][jj] = adj_g<COH>(w, q);
             dp0[ri][jj] = adj_dl(w, 0, q);
         }
-    for (long pp = p1 - 1; pp >= p0; --pp) {
+    float gbn[TW], dbn[TW];
+    load_below(p1 - 1, gbn, dbn);
+    for (int kb = 0; kb < nk; kb += TR) {
+        const long pp = p1 - 1 - kb / TR;
         const bool pbelow = pp + 1 < n0;
-        // Row below the tile's last row: successors along axis 1.
         float gb[TW], db1[TW];
 #pragma unroll
         for (int jj = 0; jj < TW; ++jj) {
-            const long q = qof(pp, std::min<long>(r1, n1 - 1), std::min<long>(j0 + jj, j1 - 1));
-            gb[jj] = adj_g<COH>(w, q);
-            db1[jj] = adj_dl(w, 1, q);
+            gb[jj] = gbn[jj];
+            db1[jj] = dbn[jj];
         }
-        Row cur, nxt;
-        load_row(pp, r1 - 1, cur);
 #pragma unroll
-        for (int ri = TR - 1; ri >= 0; --ri) {
+        for (int i = 0; i < TR; ++i) {
+            const int ri = TR - 1 - i;
+            {
+                Row &nx = R[(ri + TR - 2) % TR];
+                load_ops(kb + i + 2, nx);
+                load_succ(kb + i + 2, nx);
+            }
+            if (i == TR - 2) load_below(std::max<long>(pp - 1, p0), gbn, dbn);   // the next plane's
             const long r = r0 + ri;
             if (r < r1) {
-                load_row(pp, r > r0 ? r - 1 : r, nxt);
+                const Row &cur = R[ri];
                 const bool rbelow = r + 1 < n1;
                 float gr = cur.gr, dr2 = cur.dr2;
                 bool right = j1 < n2;
@@ -323,7 +374,6 @@ __device__ __forceinline__ bool adj_tile3d(const NdBwdArgs &a, int tp, int tr, i
                         right = true;
                     }
                 }
-                cur = nxt;
             }
         }
     }
