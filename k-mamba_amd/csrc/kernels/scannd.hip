@@ -912,11 +912,15 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
             flow = &fa;
             if (status) *status = fa.status;
         }
-        // Dataflow: one launch of 8k workgroups of Q waves (k <= 256 / Q:
-        // two waves per SIMD) that take items until their XCD's queue is
-        // empty. The hardware deals workgroups to the XCDs round-robin, so
-        // each XCD runs k of them, k = the largest per-XCD item count up to
-        // 256 / Q.
+        // Dataflow: one launch of 8k workgroups of Q waves that take items
+        // until their XCD's queue is empty. The hardware deals workgroups to
+        // the XCDs round-robin, so each XCD runs k of them, k = the largest
+        // per-XCD item count up to kcap / Q: two waves per SIMD in 2D, one in
+        // 3D and 4D (measured at configs[2]: 3D 1.864 ms with one wave per
+        // SIMD against 1.967 ms with two, whose larger set of tiles in
+        // flight thrashed the L2: 7.13 -> 6.55 GB read; 2D 1.10 against
+        // 0.96 ms the other way).
+        const long kcap = a.nd == 2 ? 256 : 128;
         long per_xcd = 0;
         const int fq = flow ? flow_q(fa) : 1;
         if (flow)
@@ -925,7 +929,7 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
         const int nlaunch = flow ? 1 : nbands;
         for (int b = 0; b < nlaunch; ++b) {
             a.band = b;
-            const long grid = flow ? 8 * std::min<long>(per_xcd, 256 / fq) : cnt[b] * a.ncg;
+            const long grid = flow ? 8 * std::min<long>(per_xcd, kcap / fq) : cnt[b] * a.ncg;
             if (grid <= 0) continue;
             const dim3 g(static_cast<unsigned>(grid));
 #define KM_ND_LAUNCH(NDv, TWv, MMv) launch_tile<NDv, TWv, MMv>(g, a, ring, flow, s)
