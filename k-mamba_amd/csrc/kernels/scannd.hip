@@ -57,6 +57,7 @@ struct ScanNDArgs {
     int tile[kMaxNd];            // tile extent per axis
     int ntile[kMaxNd];           // tiles per axis
     int band;                    // tile band (sum of tile indices)
+    int sub;                     // pencil tiles (3D dataflow): planes per flag along axis 0
     int D, M, DM;
     int ncg;                     // channel groups of 64 (d, m) lanes
 };
@@ -102,7 +103,8 @@ struct NDRow {
     float x[TW], b[TW], c[TW], dt[ND][TW], hn[ND - 1][TW];
     float hleft;
     int gi[ND];
-    int base;                   // row offset from the tile origin, in points
+    int base;                   // row offset from the B / C / h origin, in points
+    int xbase;                  // row offset from the x / delta / y origin
 };
 
 // PL > 0 (3D, tiles of PL rows along axis 1): the wave also keeps the
@@ -111,14 +113,24 @@ struct NDRow {
 // the same launch (the dataflow schedule) are read with agent-coherent loads
 // that bypass the CU's L1.
 //
-// wait() runs once the operands of the tile's first rows (which no other
+// wait(0) runs once the operands of the tile's first rows (which no other
 // tile writes) are in flight and before any state written by another tile
 // is read; when it returns false nothing is computed and the function
-// returns false.
-template <int ND, int TW, int MM, int PL, bool COH = false, typename Wait>
-__device__ __forceinline__ bool scannd_tile(const ScanNDArgs &p, const int (&ti)[kMaxNd], int cg,
-                                            Wait &&wait) {
+// returns 0, else 1.
+//
+// PEN (3D ring tiles spanning all of axis 0, the dataflow schedule): the
+// tile is a pencil of sub-tiles of p.sub planes. Before sub-tile s the wave
+// runs wait(s) (its axis-1 / axis-2 neighbours), after it publish(s); the
+// axis-0 neighbour of every plane is the ring, so no axis-0 state is read
+// back from h. B, C and h are addressed from the sub-tile's origin (their
+// resources move with it, keeping offsets 32-bit), x, delta and y from the
+// pencil's. Returns the number of sub-tiles computed and published.
+template <int ND, int TW, int MM, int PL, bool COH = false, bool PEN = false, typename Wait,
+          typename Publish>
+__device__ __forceinline__ int scannd_tile(const ScanNDArgs &p, const int (&ti)[kMaxNd], int cg,
+                                           Wait &&wait, Publish &&publish) {
     constexpr bool RING = (ND == 3 && PL > 0);
+    static_assert(!PEN || RING, "pencils are 3D ring tiles");
     static_assert(PL % 2 == 0, "planes of whole row pairs");
     const int lane = threadIdx.x & 63;
 
@@ -154,16 +166,33 @@ __device__ __forceinline__ bool scannd_tile(const ScanNDArgs &p, const int (&ti)
 #pragma unroll
     for (int a = 0; a < ac; ++a) origin += static_cast<long>(lo[a]) * p.pstride[a];
     const long P = static_cast<long>(p.dims[0]) * p.pstride[0];
-    const long hback = min(origin, p.pstride[0]);
     auto win = [](long bytes) { return bytes < 0x7fffffffL ? bytes : 0x7fffffffL; };
     const auto rx = make_rsrc(p.x + origin * D, win((P - origin) * D * 4));
     __amdgpu_buffer_rsrc_t rdt[ND];
 #pragma unroll
     for (int a = 0; a < ND; ++a) rdt[a] = make_rsrc(p.dt[a] + origin * D, win((P - origin) * D * 4));
-    const auto rB = make_rsrc(p.B + origin * DM, win((P - origin) * DM * 4));
-    const auto rC = make_rsrc(p.C + origin * DM, win((P - origin) * DM * 4));
-    const auto rh = make_rsrc(p.h + (origin - hback) * DM, win((P - origin + hback) * DM * 4));
     const auto ry = make_rsrc(p.y + origin * D, win((P - origin) * D * 4));
+    // B / C / h from the origin of the (sub-)tile starting `plane` planes
+    // into the tile; h one axis-0 stride earlier (or from the array's
+    // start), for the neighbours before it. rh / hback serve the neighbour
+    // loads, rh_st / hback_st the state stores: a pencil moves the loads'
+    // resources to the next sub-tile while its last row still computes.
+    __amdgpu_buffer_rsrc_t rB, rC, rh, rh_st;
+    long hback = 0, hback_st = 0;
+    auto rebase_ops = [&](int plane) {
+        const long o = origin + static_cast<long>(plane) * p.pstride[0];
+        rB = make_rsrc(p.B + o * DM, win((P - o) * DM * 4));
+        rC = make_rsrc(p.C + o * DM, win((P - o) * DM * 4));
+    };
+    auto rebase_h = [&](int plane) {
+        const long o = origin + static_cast<long>(plane) * p.pstride[0];
+        hback = min(o, p.pstride[0]);
+        rh = make_rsrc(p.h + (o - hback) * DM, win((P - o + hback) * DM * 4));
+        rh_st = rh;
+        hback_st = hback;
+    };
+    rebase_ops(0);
+    rebase_h(0);
     int voffX[TW], voffB[TW];
 #pragma unroll
     for (int c = 0; c < TW; ++c) {
@@ -182,7 +211,8 @@ __device__ __forceinline__ bool scannd_tile(const ScanNDArgs &p, const int (&ti)
     // The operand loads are unconditional; only the neighbour-state loads
     // sit under wave-uniform branches (measured: skipping the unneeded ones
     // is 5 % faster in 3D than loading B again in their place).
-    auto load_ops = [&](int row, NDRow<ND, TW> &r) {
+    // plane0: planes between the x origin and the B origin (pencils).
+    auto load_ops = [&](int row, NDRow<ND, TW> &r, int plane0 = 0) {
         int rem = row;
         int roff = 0;
 #pragma unroll
@@ -194,7 +224,12 @@ __device__ __forceinline__ bool scannd_tile(const ScanNDArgs &p, const int (&ti)
         }
         r.gi[ac] = lo[ac];
         r.base = roff;
-        const int sx = roff * D * 4, sb = roff * DM * 4;
+        r.xbase = roff;
+        if constexpr (PEN) {
+            r.gi[0] += plane0;
+            r.xbase += plane0 * static_cast<int>(p.pstride[0]);
+        }
+        const int sx = r.xbase * D * 4, sb = roff * DM * 4;
 #pragma unroll
         for (int c = 0; c < TW; ++c) {
             r.x[c] = F::ld(rx, voffX[c], sx);
@@ -226,8 +261,8 @@ __device__ __forceinline__ bool scannd_tile(const ScanNDArgs &p, const int (&ti)
         const bool left = __builtin_amdgcn_readfirstlane(lo[ac] > 0) != 0;
         r.hleft = left ? hld(rh, voffB[0], sh - DM * 4) : 0.f;
     };
-    auto load_row = [&](int row, NDRow<ND, TW> &r) {
-        load_ops(row, r);
+    auto load_row = [&](int row, NDRow<ND, TW> &r, int plane0 = 0) {
+        load_ops(row, r, plane0);
         load_nbr(r);
     };
 
@@ -270,8 +305,8 @@ __device__ __forceinline__ bool scannd_tile(const ScanNDArgs &p, const int (&ti)
     // rows past the tile's first plane) instead of r.hn[0].
     auto compute_row = [&](const NDRow<ND, TW> &r, bool live, const float (&ring0)[TW], bool from_ring) {
         const bool first_row_of_plane = (r.gi[ar] == lo[ar]);
-        const int sh = (r.base + static_cast<int>(hback)) * DM * 4;
-        const int sx = r.base * D * 4;
+        const int sh = (r.base + static_cast<int>(hback_st)) * DM * 4;
+        const int sx = r.xbase * D * 4;
         float hleft = r.hleft;
         float yr[TW];
 #pragma unroll
@@ -291,7 +326,7 @@ __device__ __forceinline__ bool scannd_tile(const ScanNDArgs &p, const int (&ti)
                 acc = fmaf(exp2_fast(r.dt[ar][c] * Ap[ar]), hu, acc);
             }
             if (lo[ac] + c > 0) acc = fmaf(exp2_fast(r.dt[ac][c] * Ap[ac]), hleft, acc);
-            F::st(rh, live ? hoff[c] : static_cast<int>(kDrop), sh, acc);
+            F::st(rh_st, live ? hoff[c] : static_cast<int>(kDrop), sh, acc);
             top[c] = acc;
             hleft = acc;
             if constexpr (kRowY) {
@@ -319,7 +354,7 @@ __device__ __forceinline__ bool scannd_tile(const ScanNDArgs &p, const int (&ti)
         NDRow<ND, TW> R0, R1, R2, R3;
         load_ops(0, R0);
         load_ops(min(1, nrows - 1), R1);
-        if (!wait()) return false;
+        if (!wait(0)) return 0;
         load_top();
         load_nbr(R0);
         load_nbr(R1);
@@ -337,6 +372,60 @@ __device__ __forceinline__ bool scannd_tile(const ScanNDArgs &p, const int (&ti)
             __builtin_amdgcn_sched_barrier(0);
             compute_row(R3, row + 3 < nrows, none, false);
         }
+    } else if constexpr (PEN) {
+        // The ring branch below over sub-tiles of p.sub planes. The first
+        // row of sub-tile s + 1 is prefetched (operands only, from its own
+        // origin) during the last row of sub-tile s; its neighbour loads
+        // wait for wait(s + 1). Past the pencil's last plane the last row
+        // of the last sub-tile is reloaded and nothing more is computed.
+        const int e0 = ext[0], e1 = ext[1], SUB = p.sub;
+        const int nsub = (e0 + SUB - 1) / SUB;
+        auto row_in = [&](int i0l, int i1) { return i0l * e1 + min(i1, e1 - 1); };
+        float ring[PL][TW];
+#pragma unroll
+        for (int i = 0; i < PL; ++i)
+#pragma unroll
+            for (int c = 0; c < TW; ++c) ring[i][c] = 0.f;
+        NDRow<ND, TW> R0, R1;
+        load_ops(row_in(0, 0), R0, 0);
+        if (!wait(0)) return 0;
+        load_nbr(R0);
+        for (int s = 0; s < nsub; ++s) {
+            const int p0 = s * SUB, np = min(SUB, e0 - p0);
+            const bool more = s + 1 < nsub;
+            for (int i0l = 0; i0l < np; ++i0l) {
+                const bool inner = p0 + i0l > 0;
+                const bool last_plane = i0l + 1 == np;
+#pragma unroll
+                for (int i1 = 0; i1 < PL; i1 += 2) {
+                    load_row(row_in(i0l, i1 + 1), R1, p0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    compute_row(R0, i1 < e1, ring[i1], inner);
+#pragma unroll
+                    for (int c = 0; c < TW; ++c) ring[i1][c] = top[c];
+                    if (i1 + 2 < PL) {
+                        load_row(row_in(i0l, i1 + 2), R0, p0);
+                    } else if (!last_plane) {
+                        load_row(row_in(i0l + 1, 0), R0, p0);
+                    } else if (more) {
+                        rebase_ops(p0 + SUB);
+                        load_ops(row_in(0, 0), R0, p0 + SUB);
+                    } else {
+                        load_ops(row_in(i0l, 0), R0, p0);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    compute_row(R1, i1 + 1 < e1, ring[i1 + 1], inner);
+#pragma unroll
+                    for (int c = 0; c < TW; ++c) ring[i1 + 1][c] = top[c];
+                }
+            }
+            publish(s);
+            if (!more) break;
+            rebase_h(p0 + SUB);
+            if (!wait(s + 1)) return s + 1;
+            load_nbr(R0);
+        }
+        return nsub;
     } else if constexpr (RING) {
         // Planes of PL rows (i1 = 0..PL-1; rows past ext[1] are recomputed
         // on the last row's operands with their stores dropped), row pairs
@@ -350,7 +439,7 @@ __device__ __forceinline__ bool scannd_tile(const ScanNDArgs &p, const int (&ti)
             for (int c = 0; c < TW; ++c) ring[i][c] = 0.f;
         NDRow<ND, TW> R0, R1;
         load_ops(0, R0);
-        if (!wait()) return false;
+        if (!wait(0)) return 0;
         load_nbr(R0);
         for (int i0 = 0; i0 < e0; ++i0) {
             const bool inner = i0 > 0;
@@ -371,7 +460,7 @@ __device__ __forceinline__ bool scannd_tile(const ScanNDArgs &p, const int (&ti)
     } else {
         NDRow<ND, TW> R0, R1;
         load_ops(0, R0);
-        if (!wait()) return false;
+        if (!wait(0)) return 0;
         load_nbr(R0);
         for (int row = 0; row < nrows; row += 2) {
             load_row(min(row + 1, nrows - 1), R1);
@@ -382,7 +471,7 @@ __device__ __forceinline__ bool scannd_tile(const ScanNDArgs &p, const int (&ti)
             compute_row(R1, row + 1 < nrows, none, false);
         }
     }
-    return true;
+    return 1;
 }
 
 // One launch per tile band: workgroup = (tile of band p.band, channel group).
@@ -397,7 +486,7 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
     const int ordinal = lb / p.ncg;
     int ti[kMaxNd];
     if (!band_tile(p, p.band, ordinal, ti)) return;
-    scannd_tile<ND, TW, MM, PL>(p, ti, cg, [] { return true; });
+    scannd_tile<ND, TW, MM, PL>(p, ti, cg, [](int) { return true; }, [](int) {});
 }
 
 // Dataflow schedule (scannd_flow.hpp), one launch per step: a tile waits
@@ -405,9 +494,11 @@ __global__ void __launch_bounds__(64) scannd_tile_kernel(ScanNDArgs p) {
 // the tile's states and outputs and sets the launch's status word, which the
 // synchronous entry points read to re-run the call on the band schedule.
 // NaN into the states and outputs of one (tile, channel group): the wave's
-// 64 (channel, state) lanes at every point of the tile.
+// 64 (channel, state) lanes at every point of the tile, or of its planes
+// [plane_lo, plane_hi) along axis 0 when plane_hi > 0.
 template <int ND>
-__device__ void scannd_tile_poison(const ScanNDArgs &p, const int (&ti)[kMaxNd], int cg) {
+__device__ void scannd_tile_poison(const ScanNDArgs &p, const int (&ti)[kMaxNd], int cg,
+                                   int plane_lo = 0, int plane_hi = 0) {
     const int lane = threadIdx.x & 63;
     const int f = cg * 64 + lane;
     const int MM = p.M;
@@ -419,8 +510,13 @@ __device__ void scannd_tile_poison(const ScanNDArgs &p, const int (&ti)[kMaxNd],
     for (int a = 0; a < ND; ++a) {
         lo[a] = ti[a] * p.tile[a];
         ext[a] = min(p.tile[a], p.dims[a] - lo[a]);
-        npts *= ext[a];
     }
+    if (plane_hi > 0) {
+        lo[0] += plane_lo;
+        ext[0] = min(plane_hi, ext[0]) - plane_lo;
+    }
+#pragma unroll
+    for (int a = 0; a < ND; ++a) npts *= ext[a];
     for (long q = 0; q < npts; ++q) {
         long rem = q, off = 0;
 #pragma unroll
@@ -441,7 +537,12 @@ __device__ void scannd_tile_poison(const ScanNDArgs &p, const int (&ti)[kMaxNd],
 // bytes apart), so those lines come from the CU's L1 or one L2 fill
 // instead of up to Q fills spread over the time the groups' waves happen
 // to run.
-template <int ND, int TW, int MM, int PL>
+//
+// PEN: an item is a pencil (3D tiles spanning all of axis 0) whose
+// sub-tiles of p.sub planes carry the flags: flag (s, t1, t2) after
+// sub-tile s, waits on sub-tile s of the axis-1 and axis-2 neighbours. A
+// pencil only waits on pencils of earlier bands, taken before it.
+template <int ND, int TW, int MM, int PL, bool PEN>
 __global__ void __launch_bounds__(64 * kFlowQ, 2) scannd_flow_kernel(ScanNDArgs p, FlowArgs f) {
     const int xcd = flow_xcd();
     const int cg0 = f.cg_lo[xcd], ncx = f.cg_lo[xcd + 1] - cg0;
@@ -473,12 +574,39 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) scannd_flow_kernel(ScanNDArgs 
         const int band = flow_band(f, tb);
         int ti[kMaxNd];
         band_tile(p, band, tb - f.band_start[band], ti);
+        if constexpr (PEN) {
+            // Flags of sub-tile s: row-major over (s, t1, t2).
+            auto flag_of = [&](int sub, int t1, int t2) {
+                return f.flags + ((static_cast<long>(sub) * p.ntile[1] + t1) * p.ntile[2] + t2) * p.ncg + cg;
+            };
+            auto wait_sub = [&](int sub) {
+                bool ready = true;
+                if (ti[1] > 0) ready = flow_wait(flag_of(sub, ti[1] - 1, ti[2]), epoch, f.spin) && ready;
+                if (ti[2] > 0) ready = flow_wait(flag_of(sub, ti[1], ti[2] - 1), epoch, f.spin) && ready;
+                return ready;
+            };
+            auto publish_sub = [&](int sub) {
+                __builtin_amdgcn_s_waitcnt(0);   // this wave's h stores acknowledged by L2
+                if ((threadIdx.x & 63) == 0)
+                    __hip_atomic_store(flag_of(sub, ti[1], ti[2]), epoch, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            };
+            const int nsub = (p.dims[0] + p.sub - 1) / p.sub;
+            const int done = scannd_tile<ND, TW, MM, PL, true, true>(p, ti, cg, wait_sub, publish_sub);
+            if (done < nsub) {
+                scannd_tile_poison<ND>(p, ti, cg, done * p.sub, p.dims[0]);
+                if ((threadIdx.x & 63) == 0)
+                    __hip_atomic_store(f.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int sub = done; sub < nsub; ++sub) publish_sub(sub);
+            }
+            continue;
+        }
         int tl = 0;
 #pragma unroll
         for (int a = 0; a < ND; ++a) tl += ti[a] * tstride[a];
         // The tile's first operand loads are issued before the waits on its
         // upstream neighbours, so their latency overlaps the wait.
-        auto upstream_done = [&]() {
+        auto upstream_done = [&](int) {
             bool ready = true;
 #pragma unroll
             for (int a = 0; a < ND; ++a)
@@ -487,7 +615,7 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) scannd_flow_kernel(ScanNDArgs 
                                       f.spin) && ready;
             return ready;
         };
-        if (!scannd_tile<ND, TW, MM, PL, true>(p, ti, cg, upstream_done)) {
+        if (!scannd_tile<ND, TW, MM, PL, true>(p, ti, cg, upstream_done, [](int) {})) {
             scannd_tile_poison<ND>(p, ti, cg);
             if ((threadIdx.x & 63) == 0)
                 __hip_atomic_store(f.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -667,8 +795,15 @@ static void scannd_tile_shape(int nd, int &tw, int &tl) {
 
 template <int ND, int TW, int MM, int PL>
 static void launch_tile_pl(dim3 g, const ScanNDArgs &a, const FlowArgs *flow, hipStream_t s) {
-    if (flow) hipLaunchKernelGGL((scannd_flow_kernel<ND, TW, MM, PL>), g, dim3(64 * flow_q(*flow)), 0, s, a, *flow);
-    else      hipLaunchKernelGGL((scannd_tile_kernel<ND, TW, MM, PL>), g, dim3(64), 0, s, a);
+    const dim3 blk(64 * (flow ? flow_q(*flow) : 1));
+    if constexpr (ND == 3 && PL > 0) {
+        if (flow && a.sub > 0) {
+            hipLaunchKernelGGL((scannd_flow_kernel<ND, TW, MM, PL, true>), g, blk, 0, s, a, *flow);
+            return;
+        }
+    }
+    if (flow) hipLaunchKernelGGL((scannd_flow_kernel<ND, TW, MM, PL, false>), g, blk, 0, s, a, *flow);
+    else      hipLaunchKernelGGL((scannd_tile_kernel<ND, TW, MM, PL>), g, blk, 0, s, a);
 }
 
 template <int ND, int TW, int MM>
@@ -882,29 +1017,61 @@ static int scannd_launch(ScanNDArgs &a, long P, hipStream_t s, bool allow_flow,
         }
         // Tiles per band: distribution of tile-index sums.
         static thread_local long cnt[4096], nxt[4096];
-        for (int i = 0; i < nbands; ++i) cnt[i] = 0;
-        cnt[0] = 1;
-        int reach = 0;
-        for (int ax = 0; ax < a.nd; ++ax) {
-            for (int i = 0; i <= reach + a.ntile[ax] - 1; ++i) nxt[i] = 0;
-            for (int sidx = 0; sidx <= reach; ++sidx)
-                for (int v = 0; v < a.ntile[ax]; ++v) nxt[sidx + v] += cnt[sidx];
-            reach += a.ntile[ax] - 1;
-            for (int sidx = 0; sidx <= reach; ++sidx) cnt[sidx] = nxt[sidx];
-        }
+        auto count_bands = [&]() {
+            nbands = 1;
+            for (int ax = 0; ax < a.nd; ++ax) nbands += a.ntile[ax] - 1;
+            for (int i = 0; i < nbands; ++i) cnt[i] = 0;
+            cnt[0] = 1;
+            int reach = 0;
+            for (int ax = 0; ax < a.nd; ++ax) {
+                for (int i = 0; i <= reach + a.ntile[ax] - 1; ++i) nxt[i] = 0;
+                for (int sidx = 0; sidx <= reach; ++sidx)
+                    for (int v = 0; v < a.ntile[ax]; ++v) nxt[sidx + v] += cnt[sidx];
+                reach += a.ntile[ax] - 1;
+                for (int sidx = 0; sidx <= reach; ++sidx) cnt[sidx] = nxt[sidx];
+            }
+            long n = 0;
+            for (int b = 0; b < nbands; ++b) n += cnt[b];
+            return n;
+        };
+        long ntiles = count_bands();
         // 3D tiles of 4 rows along axis 1 keep the previous plane in registers.
         const bool ring = a.nd == 3 && a.tile[1] == 4;
-        long ntiles = 0;
-        for (int b = 0; b < nbands; ++b) ntiles += cnt[b];
+        // Under the dataflow schedule 3D ring tiles become pencils along
+        // axis 0 with a flag per a.sub planes (the tile's depth): the ring
+        // carries the axis-0 neighbour from one sub-tile to the next instead
+        // of reading it back from h. x / delta / y are then addressed from
+        // the pencil's origin with 32-bit offsets. KM_SCANND_PENCIL=0 keeps
+        // separate tiles.
+        a.sub = 0;
+        const char *pe = std::getenv("KM_SCANND_PENCIL");
+        const bool pencil = flow_pref && ring && !(pe && std::strcmp(pe, "0") == 0) && a.ntile[0] > 1 &&
+                            P * static_cast<long>(a.D) * 4 < 0x7fffffffL;
+        const int tile0 = a.tile[0], ntile0 = a.ntile[0];
+        long nflags = ntiles * a.ncg;
+        if (pencil) {
+            a.sub = tile0;
+            a.tile[0] = a.dims[0];
+            a.ntile[0] = 1;
+            ntiles = count_bands();
+            nflags = static_cast<long>(ntile0) * ntiles * a.ncg;
+        }
         static thread_local FlowArgs fa;
         int kind = 0, bound = 0;
-        if (flow_pref && nbands <= kMaxFlowBands && ntiles * a.ncg < 0x7fffffffL) {
+        if (flow_pref && nbands <= kMaxFlowBands && nflags < 0x7fffffffL) {
             fa.nbands = nbands;
             for (int x = 0; x <= 8; ++x) fa.cg_lo[x] = static_cast<int>(static_cast<long>(x) * a.ncg / 8);
             fa.band_start[0] = 0;
             for (int b = 0; b < nbands; ++b) fa.band_start[b + 1] = fa.band_start[b] + static_cast<int>(cnt[b]);
-            bound = flow_bind(s, static_cast<size_t>(ntiles * a.ncg), ext, fa, &kind);
+            bound = flow_bind(s, static_cast<size_t>(nflags), ext, fa, &kind);
             if (bound < 0) return -1;
+        }
+        if (pencil && bound == 0) {
+            // No dataflow state: one launch per band of separate tiles.
+            a.sub = 0;
+            a.tile[0] = tile0;
+            a.ntile[0] = ntile0;
+            ntiles = count_bands();
         }
         note_flow(s, kind, kind == 2 ? fa.counter : nullptr);
         const FlowArgs *flow = nullptr;
