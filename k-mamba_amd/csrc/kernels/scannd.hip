@@ -543,7 +543,7 @@ __device__ void scannd_tile_poison(const ScanNDArgs &p, const int (&ti)[kMaxNd],
 // sub-tile s, waits on sub-tile s of the axis-1 and axis-2 neighbours. A
 // pencil only waits on pencils of earlier bands, taken before it.
 template <int ND, int TW, int MM, int PL, bool PEN>
-__global__ void __launch_bounds__(64 * kFlowQ, 2) scannd_flow_kernel(ScanNDArgs p, FlowArgs f) {
+__device__ __forceinline__ void scannd_flow_body(const ScanNDArgs &p, const FlowArgs &f) {
     const int xcd = flow_xcd();
     const int cg0 = f.cg_lo[xcd], ncx = f.cg_lo[xcd + 1] - cg0;
     if (ncx <= 0) return;
@@ -625,6 +625,18 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) scannd_flow_kernel(ScanNDArgs 
             __hip_atomic_store(f.flags + static_cast<long>(tl) * p.ncg + cg, epoch, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+template <int ND, int TW, int MM, int PL>
+__global__ void __launch_bounds__(64 * kFlowQ, 2) scannd_flow_kernel(ScanNDArgs p, FlowArgs f) {
+    scannd_flow_body<ND, TW, MM, PL, false>(p, f);
+}
+
+// Pencils: the 3D launch runs one wave per SIMD (its grid cap), so the
+// kernel may hold up to 512 VGPRs.
+template <int TW, int MM>
+__global__ void __launch_bounds__(64 * kFlowQ, 1) scannd_pencil_kernel(ScanNDArgs p, FlowArgs f) {
+    scannd_flow_body<3, TW, MM, 4, true>(p, f);
 }
 
 // Before each dataflow launch: zeroes the item counters and the status
@@ -798,11 +810,12 @@ static void launch_tile_pl(dim3 g, const ScanNDArgs &a, const FlowArgs *flow, hi
     const dim3 blk(64 * (flow ? flow_q(*flow) : 1));
     if constexpr (ND == 3 && PL > 0) {
         if (flow && a.sub > 0) {
-            hipLaunchKernelGGL((scannd_flow_kernel<ND, TW, MM, PL, true>), g, blk, 0, s, a, *flow);
+            static_assert(PL == 4, "pencils are ring tiles of 4 rows");
+            hipLaunchKernelGGL((scannd_pencil_kernel<TW, MM>), g, blk, 0, s, a, *flow);
             return;
         }
     }
-    if (flow) hipLaunchKernelGGL((scannd_flow_kernel<ND, TW, MM, PL, false>), g, blk, 0, s, a, *flow);
+    if (flow) hipLaunchKernelGGL((scannd_flow_kernel<ND, TW, MM, PL>), g, blk, 0, s, a, *flow);
     else      hipLaunchKernelGGL((scannd_tile_kernel<ND, TW, MM, PL>), g, blk, 0, s, a);
 }
 
