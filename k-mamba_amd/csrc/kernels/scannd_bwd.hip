@@ -991,6 +991,250 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
     }
 }
 
+// The 2D backward fused on the dataflow schedule: an item is (tile of
+// kAdjFTR x kAdjFTW points, run of kFlowQ channel groups), taken in reverse
+// band order; each wave walks its group's tile as adj_tile2d does (rows
+// bottom-up, right to left) and, at each point, forms every gradient from
+// the adjoint state it just computed, in grad_finish's arithmetic. The
+// adjoint state is never stored whole: only each tile's first row and first
+// column go to the boundary buffers gR / gC, which the tiles above and to
+// the left read (waiting on this tile's flag). A point's own decays
+// exp2(delta_a A_a), which its gradient terms need, are the ones its
+// predecessors' adjoint steps need, so each is formed once. dx / ddelta go
+// through the workgroup's LDS stage (grad_flush), the dA terms to a partial
+// per (tile, channel group), so every output is identical run to run.
+struct Fused2Args {
+    float *gR;   // [nt0][n1][D*M]: adjoint state on the first row of each tile row
+    float *gC;   // [n0][nt1][D*M]: on the first column of each tile column
+    int nt0, nt1;
+};
+
+template <int TR, int TW, int RB, int MM>
+__global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowArgs f, Fused2Args u) {
+    static_assert(TR * TW == kGradPts, "a tile is one staged group");
+    static_assert(kStageOut<MM>, "staged per-channel outputs");
+    static_assert(TR % RB == 0, "whole batches of rows");
+    constexpr float kInvNd = 0.5f;
+    constexpr int CPW = 256 / MM;                 // channels of a workgroup's run
+    constexpr int SG = 3 * kGradPts * CPW;        // one stage buffer: dx, ddelta0, ddelta1
+    const int xcd = flow_xcd();
+    const int cg0 = f.cg_lo[xcd], ncx = f.cg_lo[xcd + 1] - cg0;
+    if (ncx <= 0) return;
+    const int nq = ncx / kFlowQ;
+    const int w = static_cast<int>(threadIdx.x / 64);
+    const int lane = static_cast<int>(threadIdx.x & 63);
+    const int ntiles = f.band_start[f.nbands];
+    const unsigned nitems = static_cast<unsigned>(ntiles) * static_cast<unsigned>(nq);
+    const unsigned epoch = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(f.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const long n0 = a.dims[0], n1 = a.dims[1];
+    const long DM = a.D * MM;
+    const int ncg = static_cast<int>(DM / 64);
+    const int ntile[2] = {u.nt0, u.nt1};
+    const unsigned sDMc = static_cast<unsigned>(DM * 4);
+    __shared__ unsigned s_item[2];
+    __shared__ float stage[2 * SG];
+    using F = bio<f32_t>;
+    struct Row {
+        float dy[TW], x[TW], d0[TW], d1[TW], C[TW], B[TW], h[TW];
+        float hl, dr1, gr;   // h left of the tile, delta_1 and state right of it
+    };
+    for (int it = 0;; ++it) {
+        if (threadIdx.x == 0) s_item[it & 1] = atomicAdd(&f.counter[xcd], 1u);
+        __syncthreads();
+        const unsigned item = __builtin_amdgcn_readfirstlane(s_item[it & 1]);
+        if (item >= nitems) break;
+        const int tb = ntiles - 1 - static_cast<int>(item / nq);   // reverse band order
+        const int cgr = cg0 + static_cast<int>(item % nq) * kFlowQ;
+        const int cg = cgr + w;
+        const int band = flow_band(f, tb);
+        int ti[2] = {0, 0};
+        band_tile_n(2, ntile, band, tb - f.band_start[band], ti);
+        const int tl = ti[0] * u.nt1 + ti[1];
+        const long c = static_cast<long>(cg) * 64 + lane;
+        const long d = c / MM;
+        const int m = static_cast<int>(c - d * MM);
+        const long r0 = static_cast<long>(ti[0]) * TR, r1 = std::min<long>(n0, r0 + TR);
+        const long j0 = static_cast<long>(ti[1]) * TW, j1 = std::min<long>(n1, j0 + TW);
+        const bool below_tile = r1 < n0, right_tile = j1 < n1;
+        // Windows: the row above the tile to the successor row below it.
+        const long qb = (r0 > 0 ? r0 - 1 : 0) * n1, qe = (below_tile ? r1 + 1 : r1) * n1;
+        const GradWin gw = grad_window<2>(a, qb, qe, c, d, m, true);
+        const auto rC = make_rsrc(a.C + qb * DM, (qe - qb) * DM * 4);
+        // gR rows ti0 (written) and ti0 + 1 (read); gC rows r0 .. r1 - 1 at
+        // tile columns ti1 (written) and ti1 + 1 (read).
+        const long gr_base = static_cast<long>(ti[0]) * n1 * DM;
+        const auto rgR = make_rsrc(u.gR + gr_base, (static_cast<long>(u.nt0) * n1 * DM - gr_base) * 4);
+        const long gc_base = (r0 * u.nt1 + ti[1]) * DM;
+        const auto rgC = make_rsrc(u.gC + gc_base, (n0 * u.nt1 * DM - gc_base) * 4);
+        const float A0 = a.A[c] * kLog2e, A1 = a.A[DM + c] * kLog2e;
+        const float av[2] = {a.A[c], a.A[DM + c]};
+        float *st = stage + (it & 1) * SG;
+        auto oD = [&](long q) { return static_cast<int>(static_cast<unsigned>(q) * gw.sD); };
+        auto oDM = [&](long q) { return static_cast<int>(static_cast<unsigned>(q) * gw.sDM); };
+        auto ld_ops = [&](long r, Row &rw) __attribute__((always_inline)) {
+            const long rq = r * n1 - qb;
+#pragma unroll
+            for (int jj = 0; jj < TW; ++jj) {
+                const long q = rq + std::min<long>(j0 + jj, j1 - 1);
+                rw.dy[jj] = F::ld(gw.dy, gw.vd, oD(q));
+                rw.x[jj] = F::ld(gw.x, gw.vd, oD(q));
+                rw.d0[jj] = F::ld(gw.dl, gw.vd, oD(q));
+                rw.d1[jj] = F::ld(gw.dl, gw.vd, static_cast<int>(gw.sAx) + oD(q));
+                rw.C[jj] = F::ld(rC, gw.vc, oDM(q));
+                rw.B[jj] = F::ld(gw.B, gw.vc, oDM(q));
+                rw.h[jj] = F::ld(gw.h, gw.vc, oDM(q));
+            }
+            rw.hl = j0 > 0 ? F::ld(gw.h, gw.vc, oDM(rq + j0 - 1)) : 0.f;
+            rw.dr1 = right_tile ? F::ld(gw.dl, gw.vd, static_cast<int>(gw.sAx) + oD(rq + j1)) : 0.f;
+        };
+        // The right successor's state (written by another workgroup).
+        auto ld_succ = [&](long r, Row &rw) __attribute__((always_inline)) {
+            rw.gr = right_tile ? F::ld_agent(rgC, gw.vc, static_cast<int>(static_cast<unsigned>((r - r0) * u.nt1 + 1) * sDMc))
+                               : 0.f;
+        };
+        // The first batch's operands and the row above the tile go out before
+        // the wait on the successors.
+        Row ba[RB], bb[RB];
+#pragma unroll
+        for (int i = 0; i < RB; ++i) ld_ops(std::max<long>(r1 - 1 - i, r0), ba[i]);
+        float htop[TW];
+#pragma unroll
+        for (int jj = 0; jj < TW; ++jj)
+            htop[jj] = r0 > 0 ? F::ld(gw.h, gw.vc, oDM((r0 - 1) * n1 + std::min<long>(j0 + jj, j1 - 1) - qb)) : 0.f;
+        bool ready = true;
+        if (below_tile) ready = flow_wait(f.flags + static_cast<long>(tl + u.nt1) * ncg + cg, epoch, f.spin) && ready;
+        if (right_tile) ready = flow_wait(f.flags + static_cast<long>(tl + 1) * ncg + cg, epoch, f.spin) && ready;
+        float dAacc[2] = {0.f, 0.f};
+        if (ready) {
+#pragma unroll
+            for (int i = 0; i < RB; ++i) ld_succ(std::max<long>(r1 - 1 - i, r0), ba[i]);
+            // The successors below: state (gR) and decay along axis 0.
+            float gb[TW], eb[TW];
+#pragma unroll
+            for (int jj = 0; jj < TW; ++jj) {
+                const long j = std::min<long>(j0 + jj, j1 - 1);
+                gb[jj] = below_tile ? F::ld_agent(rgR, gw.vc, static_cast<int>(static_cast<unsigned>(n1 + j) * sDMc)) : 0.f;
+                eb[jj] = below_tile ? exp2_fast(F::ld(gw.dl, gw.vd, oD(r1 * n1 + j - qb)) * A0) : 0.f;
+            }
+            auto ld_batch = [&](long rtop, Row (&bt)[RB]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int i = 0; i < RB; ++i) {
+                    const long r = std::max<long>(rtop - i, r0);   // past r0: reload r0
+                    ld_ops(r, bt[i]);
+                    ld_succ(r, bt[i]);
+                }
+            };
+            // Rows rtop, rtop - 1, ... of batch bt; the next batch (the rows
+            // above) is nx, already loaded.
+            auto do_batch = [&](long rtop, const Row (&bt)[RB], const Row (&nx)[RB]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int i = 0; i < RB; ++i) {
+                    const long r = rtop - i;
+                    if (r >= r0) {
+                        const Row &cur = bt[i];
+                        const Row &up = (i + 1 < RB) ? bt[i + 1] : nx[0];
+                        const bool below = r + 1 < n0;
+                        float gr = cur.gr;
+                        float er = right_tile ? exp2_fast(cur.dr1 * A1) : 0.f;
+                        bool right = right_tile;
+#pragma unroll
+                        for (int jj = TW - 1; jj >= 0; --jj) {
+                            if (j0 + jj < j1) {
+                                const long j = j0 + jj;
+                                float g = cur.dy[jj] * cur.C[jj];
+                                if (below) g = fmaf(eb[jj], gb[jj], g);
+                                if (right) g = fmaf(er, gr, g);
+                                const float e0 = exp2_fast(cur.d0[jj] * A0), e1 = exp2_fast(cur.d1[jj] * A1);
+                                // Gradients of point (r, j), as grad_finish.
+                                const float hp[2] = {r == r0 ? htop[jj] : up.h[jj], jj > 0 ? cur.h[jj - 1] : cur.hl};
+                                const bool has[2] = {r > 0, j > 0};
+                                const float ea[2] = {e0, e1}, dl[2] = {cur.d0[jj], cur.d1[jj]};
+                                float dtb = dl[0];
+                                dtb += dl[1];
+                                dtb *= kInvNd;
+                                const float gbv = g * cur.B[jj];
+                                const float tx = channel_sum<MM>(gbv * dtb);
+                                const float tbv = gbv * cur.x[jj] * kInvNd;
+                                float td[2];
+#pragma unroll
+                                for (int ax = 0; ax < 2; ++ax) {
+                                    float t = tbv;
+                                    if (has[ax]) {
+                                        const float gh = g * ea[ax] * hp[ax];
+                                        t = fmaf(gh, av[ax], tbv);
+                                        dAacc[ax] = fmaf(gh, dl[ax], dAacc[ax]);
+                                    }
+                                    td[ax] = channel_sum<MM>(t);
+                                }
+                                const long q = r * n1 + j - qb;
+                                F::st(gw.dC, gw.vcs, oDM(q), cur.dy[jj] * cur.h[jj]);
+                                F::st(gw.g, gw.vcs, oDM(q), g * dtb * cur.x[jj]);
+                                if (m == 0) {
+                                    const int slot = static_cast<int>(r - r0) * TW + jj;
+                                    const int lc = static_cast<int>(threadIdx.x) / MM;
+                                    st[slot * CPW + lc] = tx;
+                                    st[(kGradPts + slot) * CPW + lc] = td[0];
+                                    st[(2 * kGradPts + slot) * CPW + lc] = td[1];
+                                }
+                                // The tile's first row and first column: the
+                                // states the tiles above and to the left read.
+                                if (r == r0) F::st(rgR, gw.vc, static_cast<int>(static_cast<unsigned>(j) * sDMc), g);
+                                if (jj == 0) F::st(rgC, gw.vc, static_cast<int>(static_cast<unsigned>((r - r0) * u.nt1) * sDMc), g);
+                                gb[jj] = g;
+                                eb[jj] = e0;
+                                gr = g;
+                                er = e1;
+                                right = true;
+                            }
+                        }
+                    }
+                }
+            };
+            for (long rt = r1 - 1; rt >= r0; rt -= 2 * RB) {
+                ld_batch(rt - RB, bb);
+                do_batch(rt, ba, bb);
+                if (rt - RB >= r0) {
+                    ld_batch(rt - 2 * RB, ba);
+                    do_batch(rt - RB, bb, ba);
+                }
+            }
+        } else {
+            // A wait ran out: NaN into this group's outputs, boundary states
+            // and stage slots, so every dependent tile and gradient is NaN.
+            const float qn = __builtin_nanf("");
+            for (long r = r0; r < r1; ++r)
+                for (long j = j0; j < j1; ++j) {
+                    const long q = r * n1 + j - qb;
+                    F::st(gw.dC, gw.vcs, oDM(q), qn);
+                    F::st(gw.g, gw.vcs, oDM(q), qn);
+                    if (m == 0) {
+                        const int slot = static_cast<int>((r - r0) * TW + (j - j0));
+                        const int lc = static_cast<int>(threadIdx.x) / MM;
+                        for (int k = 0; k < 3; ++k) st[(k * kGradPts + slot) * CPW + lc] = qn;
+                    }
+                    if (r == r0) F::st(rgR, gw.vc, static_cast<int>(static_cast<unsigned>(j) * sDMc), qn);
+                    if (j == j0) F::st(rgC, gw.vc, static_cast<int>(static_cast<unsigned>((r - r0) * u.nt1) * sDMc), qn);
+                }
+            dAacc[0] = dAacc[1] = qn;
+            if (lane == 0) __hip_atomic_store(f.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int ax = 0; ax < 2; ++ax) a.part[(static_cast<long>(tl) * 2 + ax) * DM + c] = dAacc[ax];
+        __builtin_amdgcn_s_waitcnt(0);   // this wave's stores acknowledged by L2
+        if (lane == 0)
+            __hip_atomic_store(f.flags + static_cast<long>(tl) * ncg + cg, epoch, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        // dx / ddelta of the run's channels at the tile's points.
+        __syncthreads();
+        const long dch = static_cast<long>(cgr) * 64 / MM;
+        grad_flush<2, MM, kGradPts>(gw, st, dch, a.D, [&](int sl) -> long {
+            const long rr = r0 + sl / TW, jj = j0 + sl % TW;
+            return (rr < r1 && jj < j1) ? rr * n1 + jj - qb : -1;
+        });
+    }
+}
+
 // dA[k] = the nbx workgroup partials of k added in a fixed order: workgroup
 // x takes outputs [64 x, +64), wave w the partials b = w, w + 4, ... in four
 // interleaved running sums, then wave 0 adds the waves' sums in wave order.
@@ -1037,6 +1281,9 @@ struct NdBwdShape {
     long qc, nbx, nby;
     size_t offs_bytes, nbr_bytes, part_bytes, tile_bytes;
     size_t flow_bytes;   // the adjoint dataflow's counters, status, epoch and flags (tiled sweeps)
+    bool fused2;         // 2D with staged per-channel outputs: the fused dataflow backward may run
+    size_t gbd_bytes;    // its boundary states (gR, gC)
+    long fnt0, fnt1;     // its tiles per axis
 };
 
 static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
@@ -1120,6 +1367,25 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
         s.tile_bytes = align_up(sizeof(int) * 3 * nt, 256);
     }
     s.part_bytes = sizeof(float) * s.nbx * s.nd * s.D * s.M;
+    // The fused 2D backward (nd_fused2d): per-channel outputs staged (4 <= M
+    // <= 32), windows of its tile's rows and of the boundary buffers below
+    // 2 GiB. It writes the boundary states of every tile (first row, first
+    // column) and a dA partial per tile.
+    s.fused2 = false;
+    s.gbd_bytes = 0;
+    s.fnt0 = s.fnt1 = 0;
+    if (s.nd == 2 && s.lanes && s.M >= 4 && s.M <= 32 && (s.D * s.M) % 64 == 0 &&
+        adj_win_ok((kAdjFTR + 2) * a->dims[1])) {
+        const long DM = s.D * s.M;
+        s.fnt0 = (a->dims[0] + kAdjFTR - 1) / kAdjFTR;
+        s.fnt1 = (a->dims[1] + kAdjFTW - 1) / kAdjFTW;
+        const double wr = 2.0 * a->dims[1] * DM * 4, wc = (static_cast<double>(kAdjFTR) * s.fnt1 + 2) * DM * 4;
+        if (wr < 2147483000.0 && wc < 2147483000.0) {
+            s.fused2 = true;
+            s.gbd_bytes = align_up(sizeof(float) * (s.fnt0 * a->dims[1] + a->dims[0] * s.fnt1) * DM, 256);
+            s.part_bytes = std::max<size_t>(s.part_bytes, sizeof(float) * s.fnt0 * s.fnt1 * 2 * DM);
+        }
+    }
     s.flow_bytes = 0;
     if (s.atile2 || s.tile_bytes) {
         int nt[3];
@@ -1273,7 +1539,7 @@ size_t km_scannd_bwd_workspace_bytes(const KMScanNDBwd *a) {
     km::clear_error();
     km::NdBwdShape s;
     if (!km::nd_bwd_shape(a, s)) return 0;
-    return s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes + s.flow_bytes;
+    return s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes + s.flow_bytes + s.gbd_bytes;
 }
 
 int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
@@ -1291,7 +1557,7 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
     }
     if (!km::gpu_ready()) return -1;
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    const size_t need = s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes + s.flow_bytes;
+    const size_t need = s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes + s.flow_bytes + s.gbd_bytes;
     char *ws = static_cast<char *>(a->workspace);
     if (ws) {
         if (a->workspace_bytes < need) {
@@ -1340,6 +1606,38 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
     }
     if (fb == 0) km::note_flow(st, 0);
     const km::FlowArgs *flow = fb > 0 ? &fa : nullptr;
+    // 2D on the dataflow schedule with workgroups of kFlowQ groups: the
+    // adjoint state and the gradients in one fused launch (KM_SCANND_BWD_FUSED=0:
+    // the adjoint sweep, then the gradient pass).
+    const char *fe = std::getenv("KM_SCANND_BWD_FUSED");
+    if (flow && s.fused2 && km::flow_q(fa) == km::kFlowQ && !(fe && std::strcmp(fe, "0") == 0)) {
+        float *gbd = reinterpret_cast<float *>(ws + s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes +
+                                               s.flow_bytes);
+        const long DM = s.D * s.M;
+        km::Fused2Args u{gbd, gbd + s.fnt0 * a->dims[1] * DM, static_cast<int>(s.fnt0), static_cast<int>(s.fnt1)};
+        const long ntiles = fa.band_start[fa.nbands];
+        long per_xcd = 0;
+        for (int x = 0; x < 8; ++x)
+            per_xcd = std::max<long>(per_xcd, ntiles * ((fa.cg_lo[x + 1] - fa.cg_lo[x]) / km::kFlowQ));
+        const dim3 grid(static_cast<unsigned>(8 * std::min<long>(per_xcd, 256 / km::kFlowQ)));
+        const dim3 blk(64 * km::kFlowQ);
+        switch (s.M) {
+        case 4: hipLaunchKernelGGL((km::nd_fused2d<km::kAdjFTR, km::kAdjFTW, 2, 4>), grid, blk, 0, st, args, fa, u); break;
+        case 8: hipLaunchKernelGGL((km::nd_fused2d<km::kAdjFTR, km::kAdjFTW, 2, 8>), grid, blk, 0, st, args, fa, u); break;
+        case 16: hipLaunchKernelGGL((km::nd_fused2d<km::kAdjFTR, km::kAdjFTW, 2, 16>), grid, blk, 0, st, args, fa, u); break;
+        default: hipLaunchKernelGGL((km::nd_fused2d<km::kAdjFTR, km::kAdjFTW, 2, 32>), grid, blk, 0, st, args, fa, u); break;
+        }
+        const long n = 2 * DM;
+        hipLaunchKernelGGL(km::nd_adjoint_dA, dim3(static_cast<unsigned>((n + 63) / 64)), dim3(256), 0, st,
+                           args.part, a->dA, s.fnt0 * s.fnt1, n);
+        if (plan) km_wavefront_plan_free(plan);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) {
+            km::set_error("km_scannd_bwd: launch failed: %s", hipGetErrorString(e));
+            return -1;
+        }
+        return 0;
+    }
     // 3D tile bands: each band's tiles (tile-index sum b), bands contiguous.
     std::vector<int> tl;
     std::vector<long> bstart;

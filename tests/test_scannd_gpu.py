@@ -439,6 +439,34 @@ def test_backward_dataflow_and_band_schedules_agree(dims, D, M, monkeypatch):
         assert err <= 1e-4, f"{k}: normwise error {err:.2e}"
 
 
+FUSED_CASES = [((43, 37), 128, 16), ((17, 70), 256, 8), ((9, 5), 512, 4), ((25, 30), 64, 32),
+               ((64, 64), 128, 16)]
+
+
+@pytest.mark.parametrize("dims,D,M", FUSED_CASES)
+def test_backward_fused_2d_matches_two_pass(dims, D, M, monkeypatch):
+    # 2D grids whose channel groups fill workgroups of four per XCD (D*M a
+    # multiple of 2048) run the fused backward: the adjoint state and every
+    # gradient in one dataflow launch, only the tiles' boundary states
+    # stored. KM_SCANND_BWD_FUSED=0 runs the adjoint sweep, then the
+    # gradient pass: the same arithmetic at every point, so dx, ddelta, dB
+    # and dC agree bit for bit; dA adds its terms per 8 x 4 tile instead of
+    # per 8 x 64 tile and agrees to rounding. Covers partial tiles on both
+    # axes and M = 4 to 32.
+    x, A, B, Cm, dt, h, dy = bwd_inputs(dims, D, M, 5)
+    a = run_bwd(dims, x, A, B, Cm, dt, h, dy)
+    monkeypatch.setenv("KM_SCANND_BWD_FUSED", "0")
+    b = run_bwd(dims, x, A, B, Cm, dt, h, dy)
+    for k in ("dx", "ddelta", "dB", "dC"):
+        assert np.isfinite(a[k]).all(), k
+        assert np.array_equal(a[k].view(np.uint32), b[k].view(np.uint32)), k
+    np.testing.assert_allclose(a["dA"], b["dA"], rtol=1e-5, atol=1e-6 * float(np.abs(b["dA"]).max()))
+    want = O.scannd_backward(dims, x, A, B, Cm, dt, h, dy, fast=True)
+    for k in want:
+        err = np.abs(a[k] - want[k]).max() / max(np.abs(want[k]).max(), 1e-30)
+        assert err <= 1e-4, f"{k}: normwise error {err:.2e}"
+
+
 _BWD_BUDGET0 = r"""
 import sys
 import numpy as np, torch
@@ -459,7 +487,7 @@ print("bwd budget0 done", flush=True)
 """
 
 
-@pytest.mark.parametrize("dims,D,M", [((33, 65), 8, 16), ((9, 6, 11), 4, 16)])
+@pytest.mark.parametrize("dims,D,M", [((33, 65), 8, 16), ((9, 6, 11), 4, 16), ((43, 37), 128, 16)])
 def test_backward_dataflow_wait_budget_exhausted_fails_loudly(dims, D, M, tmp_path):
     # KM_SCANND_FLOW_SPIN=0 (read once per process, so a child process):
     # every wait of the adjoint sweep gives up without polling, every kernel
@@ -491,8 +519,8 @@ def test_backward_dataflow_wait_budget_exhausted_fails_loudly(dims, D, M, tmp_pa
     np.testing.assert_allclose(dB[last], want["dB"].reshape(dims + (D, M))[last], rtol=1e-5, atol=1e-6)
 
 
-def test_backward_deterministic_and_workspace():
-    dims, D, M = (33, 40), 8, 16
+@pytest.mark.parametrize("dims,D,M", [((33, 40), 8, 16), ((24, 20), 128, 16)])
+def test_backward_deterministic_and_workspace(dims, D, M):
     x, A, B, Cm, dt, h, dy = bwd_inputs(dims, D, M, 1)
     a = run_bwd(dims, x, A, B, Cm, dt, h, dy)
     b = run_bwd(dims, x, A, B, Cm, dt, h, dy)
