@@ -1027,11 +1027,12 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowAr
     const unsigned nitems = static_cast<unsigned>(ntiles) * static_cast<unsigned>(nq);
     const unsigned epoch = __builtin_amdgcn_readfirstlane(
         __hip_atomic_load(f.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    const long n0 = a.dims[0], n1 = a.dims[1];
-    const long DM = a.D * MM;
-    const int ncg = static_cast<int>(DM / 64);
+    const int n0 = static_cast<int>(a.dims[0]), n1 = static_cast<int>(a.dims[1]);
+    const int DM = static_cast<int>(a.D) * MM;
+    const int ncg = DM / 64;
     const int ntile[2] = {u.nt0, u.nt1};
-    const unsigned sDMc = static_cast<unsigned>(DM * 4);
+    // Byte strides: a point of [P, D] and of [P, D*M], a delta axis.
+    const int sD = static_cast<int>(a.D) * 4, sDM = DM * 4, sAx = static_cast<int>(a.P * a.D * 4);
     __shared__ unsigned s_item[2];
     __shared__ float stage[2 * SG];
     using F = bio<f32_t>;
@@ -1051,104 +1052,110 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowAr
         int ti[2] = {0, 0};
         band_tile_n(2, ntile, band, tb - f.band_start[band], ti);
         const int tl = ti[0] * u.nt1 + ti[1];
-        const long c = static_cast<long>(cg) * 64 + lane;
-        const long d = c / MM;
-        const int m = static_cast<int>(c - d * MM);
-        const long r0 = static_cast<long>(ti[0]) * TR, r1 = std::min<long>(n0, r0 + TR);
-        const long j0 = static_cast<long>(ti[1]) * TW, j1 = std::min<long>(n1, j0 + TW);
+        const int c = cg * 64 + lane;
+        const int d = c / MM;
+        const int m = c - d * MM;
+        const int r0 = ti[0] * TR, r1 = min(n0, r0 + TR);
+        const int j0 = ti[1] * TW, j1 = min(n1, j0 + TW), je = j1 - j0;
         const bool below_tile = r1 < n0, right_tile = j1 < n1;
         // Windows: the row above the tile to the successor row below it.
-        const long qb = (r0 > 0 ? r0 - 1 : 0) * n1, qe = (below_tile ? r1 + 1 : r1) * n1;
+        const int qb = (r0 > 0 ? r0 - 1 : 0) * n1, qe = (below_tile ? r1 + 1 : r1) * n1;
         const GradWin gw = grad_window<2>(a, qb, qe, c, d, m, true);
-        const auto rC = make_rsrc(a.C + qb * DM, (qe - qb) * DM * 4);
+        const auto rC = make_rsrc(a.C + static_cast<long>(qb) * DM, static_cast<long>(qe - qb) * DM * 4);
         // gR rows ti0 (written) and ti0 + 1 (read); gC rows r0 .. r1 - 1 at
         // tile columns ti1 (written) and ti1 + 1 (read).
         const long gr_base = static_cast<long>(ti[0]) * n1 * DM;
         const auto rgR = make_rsrc(u.gR + gr_base, (static_cast<long>(u.nt0) * n1 * DM - gr_base) * 4);
-        const long gc_base = (r0 * u.nt1 + ti[1]) * DM;
-        const auto rgC = make_rsrc(u.gC + gc_base, (n0 * u.nt1 * DM - gc_base) * 4);
+        const long gc_base = (static_cast<long>(r0) * u.nt1 + ti[1]) * DM;
+        const auto rgC = make_rsrc(u.gC + gc_base, (static_cast<long>(n0) * u.nt1 * DM - gc_base) * 4);
         const float A0 = a.A[c] * kLog2e, A1 = a.A[DM + c] * kLog2e;
         const float av[2] = {a.A[c], a.A[DM + c]};
         float *st = stage + (it & 1) * SG;
-        auto oD = [&](long q) { return static_cast<int>(static_cast<unsigned>(q) * gw.sD); };
-        auto oDM = [&](long q) { return static_cast<int>(static_cast<unsigned>(q) * gw.sDM); };
-        auto ld_ops = [&](long r, Row &rw) __attribute__((always_inline)) {
-            const long rq = r * n1 - qb;
+        // Column offsets (columns past the tile's edge repeat its last one) in
+        // VGPRs, a row's offset in the SGPR offset.
+        int voD[TW], voDM[TW];
+#pragma unroll
+        for (int jj = 0; jj < TW; ++jj) {
+            const int cc = min(jj, je - 1);
+            voD[jj] = gw.vd + cc * sD;
+            voDM[jj] = gw.vc + cc * sDM;
+        }
+        auto rowq = [&](int r) { return r * n1 + j0 - qb; };   // point (r, j0) in the window
+        auto ld_ops = [&](int r, Row &rw) __attribute__((always_inline)) {
+            const int oD = rowq(r) * sD, oDM = rowq(r) * sDM;
 #pragma unroll
             for (int jj = 0; jj < TW; ++jj) {
-                const long q = rq + std::min<long>(j0 + jj, j1 - 1);
-                rw.dy[jj] = F::ld(gw.dy, gw.vd, oD(q));
-                rw.x[jj] = F::ld(gw.x, gw.vd, oD(q));
-                rw.d0[jj] = F::ld(gw.dl, gw.vd, oD(q));
-                rw.d1[jj] = F::ld(gw.dl, gw.vd, static_cast<int>(gw.sAx) + oD(q));
-                rw.C[jj] = F::ld(rC, gw.vc, oDM(q));
-                rw.B[jj] = F::ld(gw.B, gw.vc, oDM(q));
-                rw.h[jj] = F::ld(gw.h, gw.vc, oDM(q));
+                rw.dy[jj] = F::ld(gw.dy, voD[jj], oD);
+                rw.x[jj] = F::ld(gw.x, voD[jj], oD);
+                rw.d0[jj] = F::ld(gw.dl, voD[jj], oD);
+                rw.d1[jj] = F::ld(gw.dl, voD[jj], sAx + oD);
+                rw.C[jj] = F::ld(rC, voDM[jj], oDM);
+                rw.B[jj] = F::ld(gw.B, voDM[jj], oDM);
+                rw.h[jj] = F::ld(gw.h, voDM[jj], oDM);
             }
-            rw.hl = j0 > 0 ? F::ld(gw.h, gw.vc, oDM(rq + j0 - 1)) : 0.f;
-            rw.dr1 = right_tile ? F::ld(gw.dl, gw.vd, static_cast<int>(gw.sAx) + oD(rq + j1)) : 0.f;
+            rw.hl = j0 > 0 ? F::ld(gw.h, gw.vc, oDM - sDM) : 0.f;
+            rw.dr1 = right_tile ? F::ld(gw.dl, gw.vd, sAx + oD + je * sD) : 0.f;
         };
         // The right successor's state (written by another workgroup).
-        auto ld_succ = [&](long r, Row &rw) __attribute__((always_inline)) {
-            rw.gr = right_tile ? F::ld_agent(rgC, gw.vc, static_cast<int>(static_cast<unsigned>((r - r0) * u.nt1 + 1) * sDMc))
-                               : 0.f;
+        auto ld_succ = [&](int r, Row &rw) __attribute__((always_inline)) {
+            rw.gr = right_tile ? F::ld_agent(rgC, gw.vc, ((r - r0) * u.nt1 + 1) * sDM) : 0.f;
         };
         // The first batch's operands and the row above the tile go out before
         // the wait on the successors.
         Row ba[RB], bb[RB];
 #pragma unroll
-        for (int i = 0; i < RB; ++i) ld_ops(std::max<long>(r1 - 1 - i, r0), ba[i]);
+        for (int i = 0; i < RB; ++i) ld_ops(max(r1 - 1 - i, r0), ba[i]);
         float htop[TW];
 #pragma unroll
-        for (int jj = 0; jj < TW; ++jj)
-            htop[jj] = r0 > 0 ? F::ld(gw.h, gw.vc, oDM((r0 - 1) * n1 + std::min<long>(j0 + jj, j1 - 1) - qb)) : 0.f;
+        for (int jj = 0; jj < TW; ++jj) htop[jj] = r0 > 0 ? F::ld(gw.h, voDM[jj], rowq(r0 - 1) * sDM) : 0.f;
         bool ready = true;
         if (below_tile) ready = flow_wait(f.flags + static_cast<long>(tl + u.nt1) * ncg + cg, epoch, f.spin) && ready;
         if (right_tile) ready = flow_wait(f.flags + static_cast<long>(tl + 1) * ncg + cg, epoch, f.spin) && ready;
         float dAacc[2] = {0.f, 0.f};
+        const int lc = static_cast<int>(threadIdx.x) / MM;
         if (ready) {
 #pragma unroll
-            for (int i = 0; i < RB; ++i) ld_succ(std::max<long>(r1 - 1 - i, r0), ba[i]);
+            for (int i = 0; i < RB; ++i) ld_succ(max(r1 - 1 - i, r0), ba[i]);
             // The successors below: state (gR) and decay along axis 0.
             float gb[TW], eb[TW];
 #pragma unroll
             for (int jj = 0; jj < TW; ++jj) {
-                const long j = std::min<long>(j0 + jj, j1 - 1);
-                gb[jj] = below_tile ? F::ld_agent(rgR, gw.vc, static_cast<int>(static_cast<unsigned>(n1 + j) * sDMc)) : 0.f;
-                eb[jj] = below_tile ? exp2_fast(F::ld(gw.dl, gw.vd, oD(r1 * n1 + j - qb)) * A0) : 0.f;
+                gb[jj] = below_tile ? F::ld_agent(rgR, voDM[jj], (n1 + j0) * sDM) : 0.f;
+                eb[jj] = below_tile ? exp2_fast(F::ld(gw.dl, voD[jj], rowq(r1) * sD) * A0) : 0.f;
             }
-            auto ld_batch = [&](long rtop, Row (&bt)[RB]) __attribute__((always_inline)) {
+            auto ld_batch = [&](int rtop, Row (&bt)[RB]) __attribute__((always_inline)) {
 #pragma unroll
                 for (int i = 0; i < RB; ++i) {
-                    const long r = std::max<long>(rtop - i, r0);   // past r0: reload r0
+                    const int r = max(rtop - i, r0);   // past r0: reload r0
                     ld_ops(r, bt[i]);
                     ld_succ(r, bt[i]);
                 }
             };
             // Rows rtop, rtop - 1, ... of batch bt; the next batch (the rows
             // above) is nx, already loaded.
-            auto do_batch = [&](long rtop, const Row (&bt)[RB], const Row (&nx)[RB]) __attribute__((always_inline)) {
+            auto do_batch = [&](int rtop, const Row (&bt)[RB], const Row (&nx)[RB]) __attribute__((always_inline)) {
 #pragma unroll
                 for (int i = 0; i < RB; ++i) {
-                    const long r = rtop - i;
+                    const int r = rtop - i;
                     if (r >= r0) {
                         const Row &cur = bt[i];
                         const Row &up = (i + 1 < RB) ? bt[i + 1] : nx[0];
                         const bool below = r + 1 < n0;
+                        const int oDM = rowq(r) * sDM;
+                        const int slot0 = (r - r0) * TW;
                         float gr = cur.gr;
                         float er = right_tile ? exp2_fast(cur.dr1 * A1) : 0.f;
                         bool right = right_tile;
 #pragma unroll
                         for (int jj = TW - 1; jj >= 0; --jj) {
-                            if (j0 + jj < j1) {
-                                const long j = j0 + jj;
+                            if (jj < je) {
                                 float g = cur.dy[jj] * cur.C[jj];
                                 if (below) g = fmaf(eb[jj], gb[jj], g);
                                 if (right) g = fmaf(er, gr, g);
                                 const float e0 = exp2_fast(cur.d0[jj] * A0), e1 = exp2_fast(cur.d1[jj] * A1);
-                                // Gradients of point (r, j), as grad_finish.
+                                // Gradients of point (r, j0 + jj), as grad_finish.
                                 const float hp[2] = {r == r0 ? htop[jj] : up.h[jj], jj > 0 ? cur.h[jj - 1] : cur.hl};
-                                const bool has[2] = {r > 0, j > 0};
+                                const bool has[2] = {r > 0, j0 + jj > 0};
                                 const float ea[2] = {e0, e1}, dl[2] = {cur.d0[jj], cur.d1[jj]};
                                 float dtb = dl[0];
                                 dtb += dl[1];
@@ -1167,20 +1174,17 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowAr
                                     }
                                     td[ax] = channel_sum<MM>(t);
                                 }
-                                const long q = r * n1 + j - qb;
-                                F::st(gw.dC, gw.vcs, oDM(q), cur.dy[jj] * cur.h[jj]);
-                                F::st(gw.g, gw.vcs, oDM(q), g * dtb * cur.x[jj]);
+                                F::st(gw.dC, voDM[jj], oDM, cur.dy[jj] * cur.h[jj]);
+                                F::st(gw.g, voDM[jj], oDM, g * dtb * cur.x[jj]);
                                 if (m == 0) {
-                                    const int slot = static_cast<int>(r - r0) * TW + jj;
-                                    const int lc = static_cast<int>(threadIdx.x) / MM;
-                                    st[slot * CPW + lc] = tx;
-                                    st[(kGradPts + slot) * CPW + lc] = td[0];
-                                    st[(2 * kGradPts + slot) * CPW + lc] = td[1];
+                                    st[(slot0 + jj) * CPW + lc] = tx;
+                                    st[(kGradPts + slot0 + jj) * CPW + lc] = td[0];
+                                    st[(2 * kGradPts + slot0 + jj) * CPW + lc] = td[1];
                                 }
                                 // The tile's first row and first column: the
                                 // states the tiles above and to the left read.
-                                if (r == r0) F::st(rgR, gw.vc, static_cast<int>(static_cast<unsigned>(j) * sDMc), g);
-                                if (jj == 0) F::st(rgC, gw.vc, static_cast<int>(static_cast<unsigned>((r - r0) * u.nt1) * sDMc), g);
+                                if (r == r0) F::st(rgR, voDM[jj], j0 * sDM, g);
+                                if (jj == 0) F::st(rgC, gw.vc, (r - r0) * u.nt1 * sDM, g);
                                 gb[jj] = g;
                                 eb[jj] = e0;
                                 gr = g;
@@ -1191,7 +1195,7 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowAr
                     }
                 }
             };
-            for (long rt = r1 - 1; rt >= r0; rt -= 2 * RB) {
+            for (int rt = r1 - 1; rt >= r0; rt -= 2 * RB) {
                 ld_batch(rt - RB, bb);
                 do_batch(rt, ba, bb);
                 if (rt - RB >= r0) {
@@ -1203,18 +1207,15 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowAr
             // A wait ran out: NaN into this group's outputs, boundary states
             // and stage slots, so every dependent tile and gradient is NaN.
             const float qn = __builtin_nanf("");
-            for (long r = r0; r < r1; ++r)
-                for (long j = j0; j < j1; ++j) {
-                    const long q = r * n1 + j - qb;
-                    F::st(gw.dC, gw.vcs, oDM(q), qn);
-                    F::st(gw.g, gw.vcs, oDM(q), qn);
-                    if (m == 0) {
-                        const int slot = static_cast<int>((r - r0) * TW + (j - j0));
-                        const int lc = static_cast<int>(threadIdx.x) / MM;
-                        for (int k = 0; k < 3; ++k) st[(k * kGradPts + slot) * CPW + lc] = qn;
-                    }
-                    if (r == r0) F::st(rgR, gw.vc, static_cast<int>(static_cast<unsigned>(j) * sDMc), qn);
-                    if (j == j0) F::st(rgC, gw.vc, static_cast<int>(static_cast<unsigned>((r - r0) * u.nt1) * sDMc), qn);
+            for (int r = r0; r < r1; ++r)
+                for (int jj = 0; jj < je; ++jj) {
+                    const int oDM = rowq(r) * sDM + jj * sDM;
+                    F::st(gw.dC, gw.vc, oDM, qn);
+                    F::st(gw.g, gw.vc, oDM, qn);
+                    if (m == 0)
+                        for (int k = 0; k < 3; ++k) st[(k * kGradPts + (r - r0) * TW + jj) * CPW + lc] = qn;
+                    if (r == r0) F::st(rgR, gw.vc, (j0 + jj) * sDM, qn);
+                    if (jj == 0) F::st(rgC, gw.vc, (r - r0) * u.nt1 * sDM, qn);
                 }
             dAacc[0] = dAacc[1] = qn;
             if (lane == 0) __hip_atomic_store(f.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1229,8 +1230,8 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowAr
         __syncthreads();
         const long dch = static_cast<long>(cgr) * 64 / MM;
         grad_flush<2, MM, kGradPts>(gw, st, dch, a.D, [&](int sl) -> long {
-            const long rr = r0 + sl / TW, jj = j0 + sl % TW;
-            return (rr < r1 && jj < j1) ? rr * n1 + jj - qb : -1;
+            const int rr = r0 + sl / TW, jj = sl % TW;
+            return (rr < r1 && jj < je) ? static_cast<long>(rowq(rr) + jj) : -1L;
         });
     }
 }
