@@ -1060,7 +1060,23 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowAr
         const bool below_tile = r1 < n0, right_tile = j1 < n1;
         // Windows: the row above the tile to the successor row below it.
         const int qb = (r0 > 0 ? r0 - 1 : 0) * n1, qe = (below_tile ? r1 + 1 : r1) * n1;
-        const GradWin gw = grad_window<2>(a, qb, qe, c, d, m, true);
+        // The loop's buffers (the flush builds its own window for dx / ddelta).
+        struct {
+            __amdgpu_buffer_rsrc_t x, dy, dl, g, B, h, dC;
+            int vd, vc;
+        } gw;
+        {
+            const long n = qe - qb;
+            gw.x = make_rsrc(a.x + static_cast<long>(qb) * a.D, n * a.D * 4);
+            gw.dy = make_rsrc(a.dy + static_cast<long>(qb) * a.D, n * a.D * 4);
+            gw.dl = make_rsrc(a.delta + static_cast<long>(qb) * a.D, (a.P + n) * a.D * 4);
+            gw.g = make_rsrc(a.dB + static_cast<long>(qb) * DM, n * DM * 4);
+            gw.B = make_rsrc(a.B + static_cast<long>(qb) * DM, n * DM * 4);
+            gw.h = make_rsrc(a.h + static_cast<long>(qb) * DM, n * DM * 4);
+            gw.dC = make_rsrc(a.dC + static_cast<long>(qb) * DM, n * DM * 4);
+            gw.vd = d * 4;
+            gw.vc = c * 4;
+        }
         const auto rC = make_rsrc(a.C + static_cast<long>(qb) * DM, static_cast<long>(qe - qb) * DM * 4);
         // gR rows ti0 (written) and ti0 + 1 (read); gC rows r0 .. r1 - 1 at
         // tile columns ti1 (written) and ti1 + 1 (read).
@@ -1229,7 +1245,8 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowAr
         // dx / ddelta of the run's channels at the tile's points.
         __syncthreads();
         const long dch = static_cast<long>(cgr) * 64 / MM;
-        grad_flush<2, MM, kGradPts>(gw, st, dch, a.D, [&](int sl) -> long {
+        const GradWin fw = grad_window<2>(a, qb, qe, c, d, m, true);
+        grad_flush<2, MM, kGradPts>(fw, st, dch, a.D, [&](int sl) -> long {
             const int rr = r0 + sl / TW, jj = sl % TW;
             return (rr < r1 && jj < je) ? static_cast<long>(rowq(rr) + jj) : -1L;
         });
