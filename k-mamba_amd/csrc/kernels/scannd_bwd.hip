@@ -1011,12 +1011,12 @@ struct Fused2Args {
 
 template <int TR, int TW, int RB, int MM>
 __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowArgs f, Fused2Args u) {
-    static_assert(TR * TW == kGradPts, "a tile is one staged group");
-    static_assert(kStageOut<MM>, "staged per-channel outputs");
+    constexpr int PTS = TR * TW;                  // a tile is one staged group
+    static_assert(kStageOut<MM> && (256 / MM * PTS) % 256 == 0, "staged per-channel outputs");
     static_assert(TR % RB == 0, "whole batches of rows");
     constexpr float kInvNd = 0.5f;
     constexpr int CPW = 256 / MM;                 // channels of a workgroup's run
-    constexpr int SG = 3 * kGradPts * CPW;        // one stage buffer: dx, ddelta0, ddelta1
+    constexpr int SG = 3 * PTS * CPW;             // one stage buffer: dx, ddelta0, ddelta1
     const int xcd = flow_xcd();
     const int cg0 = f.cg_lo[xcd], ncx = f.cg_lo[xcd + 1] - cg0;
     if (ncx <= 0) return;
@@ -1194,8 +1194,8 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowAr
                                 F::st(gw.g, voDM[jj], oDM, g * dtb * cur.x[jj]);
                                 if (m == 0) {
                                     st[(slot0 + jj) * CPW + lc] = tx;
-                                    st[(kGradPts + slot0 + jj) * CPW + lc] = td[0];
-                                    st[(2 * kGradPts + slot0 + jj) * CPW + lc] = td[1];
+                                    st[(PTS + slot0 + jj) * CPW + lc] = td[0];
+                                    st[(2 * PTS + slot0 + jj) * CPW + lc] = td[1];
                                 }
                                 // The tile's first row and first column: the
                                 // states the tiles above and to the left read.
@@ -1229,7 +1229,7 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowAr
                     F::st(gw.dC, gw.vc, oDM, qn);
                     F::st(gw.g, gw.vc, oDM, qn);
                     if (m == 0)
-                        for (int k = 0; k < 3; ++k) st[(k * kGradPts + (r - r0) * TW + jj) * CPW + lc] = qn;
+                        for (int k = 0; k < 3; ++k) st[(k * PTS + (r - r0) * TW + jj) * CPW + lc] = qn;
                     if (r == r0) F::st(rgR, gw.vc, (j0 + jj) * sDM, qn);
                     if (jj == 0) F::st(rgC, gw.vc, (r - r0) * u.nt1 * sDM, qn);
                 }
@@ -1246,7 +1246,7 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowAr
         __syncthreads();
         const long dch = static_cast<long>(cgr) * 64 / MM;
         const GradWin fw = grad_window<2>(a, qb, qe, c, d, m, true);
-        grad_flush<2, MM, kGradPts>(fw, st, dch, a.D, [&](int sl) -> long {
+        grad_flush<2, MM, PTS>(fw, st, dch, a.D, [&](int sl) -> long {
             const int rr = r0 + sl / TW, jj = sl % TW;
             return (rr < r1 && jj < je) ? static_cast<long>(rowq(rr) + jj) : -1L;
         });
