@@ -1256,9 +1256,15 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowAr
 // dA[k] = the nbx workgroup partials of k added in a fixed order: workgroup
 // x takes outputs [64 x, +64), wave w the partials b = w, w + 4, ... in four
 // interleaved running sums, then wave 0 adds the waves' sums in wave order.
-__global__ void __launch_bounds__(256) nd_adjoint_dA(const float *part, float *dA, long nbx, long n) {
+// Workgroup row y takes the ch partials from y * ch on and writes row y of
+// dA (a first pass over chunks of many partials; then one row, ch = nbx).
+__global__ void __launch_bounds__(256) nd_adjoint_dA(const float *part, float *dA, long nbx, long n, long ch) {
     __shared__ float red[4][64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const long y0 = static_cast<long>(blockIdx.y) * ch;
+    part += y0 * n;
+    dA += static_cast<long>(blockIdx.y) * n;
+    nbx = std::min(ch, nbx - y0);
     const long k0 = static_cast<long>(blockIdx.x) * 64 + lane;
     const long k = k0 < n ? k0 : n - 1;
     float s[4] = {0.f, 0.f, 0.f, 0.f};
@@ -1271,6 +1277,24 @@ __global__ void __launch_bounds__(256) nd_adjoint_dA(const float *part, float *d
     red[w][lane] = (s[0] + s[1]) + (s[2] + s[3]);
     __syncthreads();
     if (w == 0 && k0 < n) dA[k0] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+}
+
+// dA from nbx partials [nbx][n]: above kDAChunk partials, chunks of
+// kDAChunk are summed first (in parallel, into the ceil(nbx / kDAChunk) rows
+// after the partials), then the chunks; each step in a fixed order.
+constexpr long kDAChunk = 64;
+static long dA_chunks(long nbx) { return nbx > 2 * kDAChunk ? (nbx + kDAChunk - 1) / kDAChunk : 0; }
+static void sum_dA(float *part, float *dA, long nbx, long n, hipStream_t st) {
+    const unsigned gx = static_cast<unsigned>((n + 63) / 64);
+    const long nch = dA_chunks(nbx);
+    if (nch > 0) {
+        float *rows = part + nbx * n;
+        hipLaunchKernelGGL(nd_adjoint_dA, dim3(gx, static_cast<unsigned>(nch)), dim3(256), 0, st, part, rows, nbx, n,
+                           kDAChunk);
+        hipLaunchKernelGGL(nd_adjoint_dA, dim3(gx), dim3(256), 0, st, rows, dA, nch, n, nch);
+    } else {
+        hipLaunchKernelGGL(nd_adjoint_dA, dim3(gx), dim3(256), 0, st, part, dA, nbx, n, nbx);
+    }
 }
 
 constexpr int kGradTR2 = 8, kGradTW2 = 64;                  // 2D gradient tiles (rows, points)
@@ -1384,7 +1408,7 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
         for (int ax = 0; ax < 3; ++ax) nt *= (a->dims[ax] + tdim[ax] - 1) / tdim[ax];
         s.tile_bytes = align_up(sizeof(int) * 3 * nt, 256);
     }
-    s.part_bytes = sizeof(float) * s.nbx * s.nd * s.D * s.M;
+    s.part_bytes = sizeof(float) * (s.nbx + dA_chunks(s.nbx)) * s.nd * s.D * s.M;
     // The fused 2D backward (nd_fused2d): per-channel outputs staged (4 <= M
     // <= 32), windows of its tile's rows and of the boundary buffers below
     // 2 GiB. It writes the boundary states of every tile (first row, first
@@ -1401,7 +1425,8 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
         if (wr < 2147483000.0 && wc < 2147483000.0) {
             s.fused2 = true;
             s.gbd_bytes = align_up(sizeof(float) * (s.fnt0 * a->dims[1] + a->dims[0] * s.fnt1) * DM, 256);
-            s.part_bytes = std::max<size_t>(s.part_bytes, sizeof(float) * s.fnt0 * s.fnt1 * 2 * DM);
+            const long nf = s.fnt0 * s.fnt1;
+            s.part_bytes = std::max<size_t>(s.part_bytes, sizeof(float) * (nf + dA_chunks(nf)) * 2 * DM);
         }
     }
     s.flow_bytes = 0;
@@ -1544,9 +1569,7 @@ static void nd_bwd_launch(const NdBwdArgs &args, const NdBwdShape &s, const KMWa
                            dim3(static_cast<unsigned>(s.nbx), static_cast<unsigned>(s.nby)), dim3(256), lds, st,
                            args, s.qc, s.db);
     }
-    const long n = s.nd * DM;
-    hipLaunchKernelGGL(nd_adjoint_dA, dim3(static_cast<unsigned>((n + 63) / 64)), dim3(256), 0, st,
-                       args.part, dA, s.nbx, n);
+    sum_dA(args.part, dA, s.nbx, s.nd * DM, st);
 }
 
 }  // namespace km
@@ -1645,9 +1668,7 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
         case 16: hipLaunchKernelGGL((km::nd_fused2d<km::kAdjFTR, km::kAdjFTW, 2, 16>), grid, blk, 0, st, args, fa, u); break;
         default: hipLaunchKernelGGL((km::nd_fused2d<km::kAdjFTR, km::kAdjFTW, 2, 32>), grid, blk, 0, st, args, fa, u); break;
         }
-        const long n = 2 * DM;
-        hipLaunchKernelGGL(km::nd_adjoint_dA, dim3(static_cast<unsigned>((n + 63) / 64)), dim3(256), 0, st,
-                           args.part, a->dA, s.fnt0 * s.fnt1, n);
+        km::sum_dA(args.part, a->dA, s.fnt0 * s.fnt1, 2 * DM, st);
         if (plan) km_wavefront_plan_free(plan);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) {
