@@ -394,6 +394,7 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile3d(NdBwdArgs a, const int *
 // points (the critical path runs through nt0 + nt1 - 1 of them), 3D tiles
 // those of the band schedule.
 constexpr int kAdjFTR = 8, kAdjFTW = 4;   // 2D dataflow tiles (rows, points)
+constexpr int kF3S = 4, kF3R = 4, kF3W = 4;   // fused 3D pencils: planes per sub-tile, rows, points
 
 // NaN into the states of one (tile, channel group) whose wait gave up, so
 // every tile that depends on it, and every gradient, turns NaN too.
@@ -1253,6 +1254,297 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowAr
     }
 }
 
+// The 3D backward fused, on pencils: an item is a pencil (a TR x TW column
+// of axes 1 and 2 through every plane of axis 0, run of kFlowQ channel
+// groups), taken in reverse band order of its (t1, t2). Each wave walks its
+// group's pencil from the last plane to the first in sub-tiles of SUB planes
+// (a completion flag after each), each plane's rows bottom-up and each row
+// right to left, and at every point forms the adjoint state and every
+// gradient (grad_finish's arithmetic, so dx, ddelta, dB, dC are bit for bit
+// those of the two-pass path). The plane below's states and decays stay in
+// registers, as does the current plane's h (the plane above's arrives with
+// each row, as the axis-0 predecessor, and becomes the next plane's); only
+// the pencil's first row and first column of every plane are stored, in gR
+// / gC, for the pencils above and to the left (which wait on this pencil's
+// flag for the same sub-tile). dx / ddelta go through the workgroup's LDS
+// stage per sub-tile; dA to a partial per (sub-tile, pencil, group).
+struct Fused3Args {
+    float *gR;   // [n0][nt1][n2][D*M]: the states of each pencil's first row
+    float *gC;   // [n0][n1][nt2][D*M]: of each pencil's first column
+    int nt1, nt2, nsub;
+};
+
+template <int SUB, int TR, int TW, int MM>
+__global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused3d(NdBwdArgs a, FlowArgs f, Fused3Args u) {
+    constexpr int PTS = SUB * TR * TW;            // a sub-tile is one staged group
+    static_assert(kStageOut<MM> && (256 / MM * PTS) % 256 == 0, "staged per-channel outputs");
+    static_assert(TR % 2 == 0, "rows alternate between two prefetch slots");
+    constexpr float kInvNd = 1.0f / 3;
+    constexpr int CPW = 256 / MM;
+    constexpr int SG = 4 * PTS * CPW;             // one stage buffer: dx, ddelta 0..2
+    const int xcd = flow_xcd();
+    const int cg0 = f.cg_lo[xcd], ncx = f.cg_lo[xcd + 1] - cg0;
+    if (ncx <= 0) return;
+    const int nq = ncx / kFlowQ;
+    const int w = static_cast<int>(threadIdx.x / 64);
+    const int lane = static_cast<int>(threadIdx.x & 63);
+    const int npen = f.band_start[f.nbands];
+    const unsigned nitems = static_cast<unsigned>(npen) * static_cast<unsigned>(nq);
+    const unsigned epoch = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(f.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const int n0 = static_cast<int>(a.dims[0]), n1 = static_cast<int>(a.dims[1]), n2 = static_cast<int>(a.dims[2]);
+    const int s0 = n1 * n2;
+    const int DM = static_cast<int>(a.D) * MM;
+    const int ncg = DM / 64;
+    const int ntile[2] = {u.nt1, u.nt2};
+    const int sD = static_cast<int>(a.D) * 4, sDM = DM * 4, sAx = static_cast<int>(a.P * a.D * 4);
+    __shared__ unsigned s_item[2];
+    __shared__ float stage[2 * SG];
+    using F = bio<f32_t>;
+    struct Row {
+        float dy[TW], x[TW], d0[TW], d1[TW], d2[TW], C[TW], B[TW];
+        float hu0[TW];              // h of the plane above (axis-0 predecessor; 0 on plane 0)
+        float hu1[TW];              // h of the row above the pencil (first row only)
+        float gbx[TW], dbx[TW];     // state and delta_1 of the row below the pencil (last row only)
+        float hl, dr2, gr;          // h left of the pencil; delta_2 and state right of it
+    };
+    int sub_n = 0;                  // sub-tiles done (a stage buffer per sub-tile, alternating)
+    for (int it = 0;; ++it) {
+        if (threadIdx.x == 0) s_item[it & 1] = atomicAdd(&f.counter[xcd], 1u);
+        __syncthreads();
+        const unsigned item = __builtin_amdgcn_readfirstlane(s_item[it & 1]);
+        if (item >= nitems) break;
+        const int tb = npen - 1 - static_cast<int>(item / nq);      // reverse band order
+        const int cgr = cg0 + static_cast<int>(item % nq) * kFlowQ;
+        const int cg = cgr + w;
+        const int band = flow_band(f, tb);
+        int ti[2] = {0, 0};
+        band_tile_n(2, ntile, band, tb - f.band_start[band], ti);
+        const int pen = ti[0] * u.nt2 + ti[1];
+        const int c = cg * 64 + lane;
+        const int d = c / MM;
+        const int m = c - d * MM;
+        const int r0 = ti[0] * TR, r1 = min(n1, r0 + TR), re = r1 - r0;
+        const int j0 = ti[1] * TW, j1 = min(n2, j0 + TW), je = j1 - j0;
+        const bool below_tile = r1 < n1, right_tile = j1 < n2;
+        const float Al[3] = {a.A[c] * kLog2e, a.A[DM + c] * kLog2e, a.A[2 * DM + c] * kLog2e};
+        const float av[3] = {a.A[c], a.A[DM + c], a.A[2 * DM + c]};
+        const int lc = static_cast<int>(threadIdx.x) / MM;
+        int voD[TW], voDM[TW];
+#pragma unroll
+        for (int jj = 0; jj < TW; ++jj) {
+            const int cc = min(jj, je - 1);
+            voD[jj] = d * 4 + cc * sD;
+            voDM[jj] = c * 4 + cc * sDM;
+        }
+        // Boundary buffers, based at the pencil: gR (pp, t1, j) at
+        // pp * nt1 * n2 + (j - j0), the pencil below at + n2; gC (pp, r, t2)
+        // at pp * n1 * nt2 + (r - r0) * nt2, the pencil to the right at + 1.
+        const long grb = (static_cast<long>(ti[0]) * n2 + j0) * DM;
+        const auto rgR = make_rsrc(u.gR + grb, (static_cast<long>(n0) * u.nt1 * n2 * DM - grb) * 4);
+        const long gcb = (static_cast<long>(r0) * u.nt2 + ti[1]) * DM;
+        const auto rgC = make_rsrc(u.gC + gcb, (static_cast<long>(n0) * n1 * u.nt2 * DM - gcb) * 4);
+        float gp[TR][TW], ep[TR][TW], hcur[TR][TW];
+#pragma unroll
+        for (int ri = 0; ri < TR; ++ri)
+#pragma unroll
+            for (int jj = 0; jj < TW; ++jj) gp[ri][jj] = ep[ri][jj] = hcur[ri][jj] = 0.f;
+        bool ok = true;
+        for (int s = u.nsub - 1; s >= 0; --s, ++sub_n) {
+            const int P0 = s * SUB, P1 = min(n0, P0 + SUB);
+            // Windows: the plane above the sub-tile through its last plane.
+            const int qb = max(P0 - 1, 0) * s0, qe = P1 * s0;
+            const long nq_ = qe - qb;
+            const auto rx = make_rsrc(a.x + static_cast<long>(qb) * a.D, nq_ * a.D * 4);
+            const auto rdy = make_rsrc(a.dy + static_cast<long>(qb) * a.D, nq_ * a.D * 4);
+            const auto rdl = make_rsrc(a.delta + static_cast<long>(qb) * a.D, (2 * a.P + nq_) * a.D * 4);
+            const auto rg = make_rsrc(a.dB + static_cast<long>(qb) * DM, nq_ * DM * 4);
+            const auto rB = make_rsrc(a.B + static_cast<long>(qb) * DM, nq_ * DM * 4);
+            const auto rC = make_rsrc(a.C + static_cast<long>(qb) * DM, nq_ * DM * 4);
+            const auto rh = make_rsrc(a.h + static_cast<long>(qb) * DM, nq_ * DM * 4);
+            const auto rdC = make_rsrc(a.dC + static_cast<long>(qb) * DM, nq_ * DM * 4);
+            auto pq = [&](int pp, int r) { return pp * s0 + r * n2 + j0 - qb; };   // point (pp, r, j0)
+            auto ld_ops = [&](int pp, int r, Row &rw) __attribute__((always_inline)) {
+                const int q = pq(pp, r), oD = q * sD, oDM = q * sDM;
+#pragma unroll
+                for (int jj = 0; jj < TW; ++jj) {
+                    rw.dy[jj] = F::ld(rdy, voD[jj], oD);
+                    rw.x[jj] = F::ld(rx, voD[jj], oD);
+                    rw.d0[jj] = F::ld(rdl, voD[jj], oD);
+                    rw.d1[jj] = F::ld(rdl, voD[jj], sAx + oD);
+                    rw.d2[jj] = F::ld(rdl, voD[jj], 2 * sAx + oD);
+                    rw.C[jj] = F::ld(rC, voDM[jj], oDM);
+                    rw.B[jj] = F::ld(rB, voDM[jj], oDM);
+                    rw.hu0[jj] = pp > 0 ? F::ld(rh, voDM[jj], oDM - s0 * sDM) : 0.f;
+                    rw.hu1[jj] = (r == r0 && r0 > 0) ? F::ld(rh, voDM[jj], oDM - n2 * sDM) : 0.f;
+                    rw.dbx[jj] = (r == r1 - 1 && below_tile) ? F::ld(rdl, voD[jj], sAx + oD + n2 * sD) : 0.f;
+                }
+                rw.hl = j0 > 0 ? F::ld(rh, c * 4, oDM - sDM) : 0.f;
+                rw.dr2 = right_tile ? F::ld(rdl, d * 4, 2 * sAx + oD + je * sD) : 0.f;
+            };
+            // States other pencils wrote: the right neighbour, and (last row)
+            // the row below.
+            auto ld_succ = [&](int pp, int r, Row &rw) __attribute__((always_inline)) {
+                rw.gr = right_tile
+                            ? F::ld_agent(rgC, c * 4, ((pp * n1 + (r - r0)) * u.nt2 + 1) * sDM)
+                            : 0.f;
+#pragma unroll
+                for (int jj = 0; jj < TW; ++jj)
+                    rw.gbx[jj] = (r == r1 - 1 && below_tile)
+                                     ? F::ld_agent(rgR, voDM[jj], (pp * u.nt1 * n2 + n2) * sDM)
+                                     : 0.f;
+            };
+            float *st = stage + (sub_n & 1) * SG;
+            // The first row's operands (and, on the pencil's first sub-tile,
+            // its last plane's h) go out before the waits.
+            Row R0, R1;
+            ld_ops(P1 - 1, r0 + re - 1, R0);
+            if (s == u.nsub - 1) {
+#pragma unroll
+                for (int ri = 0; ri < TR; ++ri)
+#pragma unroll
+                    for (int jj = 0; jj < TW; ++jj)
+                        hcur[ri][jj] = F::ld(rh, voDM[jj], pq(P1 - 1, r0 + min(ri, re - 1)) * sDM);
+            }
+            float dAacc[3] = {0.f, 0.f, 0.f};
+            if (ok) {
+                const long fb = (static_cast<long>(s) * npen + pen);
+                if (below_tile) ok = flow_wait(f.flags + (fb + u.nt2) * ncg + cg, epoch, f.spin) && ok;
+                if (right_tile) ok = flow_wait(f.flags + (fb + 1) * ncg + cg, epoch, f.spin) && ok;
+            }
+            if (ok) {
+                ld_succ(P1 - 1, r0 + re - 1, R0);
+                float gb[TW], eb[TW];
+#pragma unroll
+                for (int jj = 0; jj < TW; ++jj) gb[jj] = eb[jj] = 0.f;
+                // One row: (pp, r = r0 + ri) from cur; prefetch the next row
+                // in walk order into nx.
+                auto do_row = [&](int pp, int ri, const Row &cur) __attribute__((always_inline)) {
+                    const int r = r0 + ri;
+                    const int oD = pq(pp, r) * sD, oDM = pq(pp, r) * sDM;
+                    (void)oD;
+                    const bool below = r + 1 < n1, pbelow = pp + 1 < n0;
+                    if (r == r1 - 1) {
+#pragma unroll
+                        for (int jj = 0; jj < TW; ++jj) {
+                            gb[jj] = cur.gbx[jj];
+                            eb[jj] = below_tile ? exp2_fast(cur.dbx[jj] * Al[1]) : 0.f;
+                        }
+                    }
+                    float gr = cur.gr;
+                    float er = right_tile ? exp2_fast(cur.dr2 * Al[2]) : 0.f;
+                    bool right = right_tile;
+                    const int slot0 = ((pp - P0) * TR + ri) * TW;
+#pragma unroll
+                    for (int jj = TW - 1; jj >= 0; --jj) {
+                        if (jj < je) {
+                            float g = cur.dy[jj] * cur.C[jj];
+                            if (pbelow) g = fmaf(ep[ri][jj], gp[ri][jj], g);
+                            if (below) g = fmaf(eb[jj], gb[jj], g);
+                            if (right) g = fmaf(er, gr, g);
+                            const float dl[3] = {cur.d0[jj], cur.d1[jj], cur.d2[jj]};
+                            const float ea[3] = {exp2_fast(dl[0] * Al[0]), exp2_fast(dl[1] * Al[1]),
+                                                 exp2_fast(dl[2] * Al[2])};
+                            float hup1 = 0.f;
+                            if constexpr (TR > 1) hup1 = ri > 0 ? hcur[ri > 0 ? ri - 1 : 0][jj] : cur.hu1[jj];
+                            const float hp[3] = {cur.hu0[jj], r == r0 ? cur.hu1[jj] : hup1,
+                                                 jj > 0 ? hcur[ri][jj > 0 ? jj - 1 : 0] : cur.hl};
+                            const bool has[3] = {pp > 0, r > 0, j0 + jj > 0};
+                            float dtb = dl[0];
+                            dtb += dl[1];
+                            dtb += dl[2];
+                            dtb *= kInvNd;
+                            const float gbv = g * cur.B[jj];
+                            const float tx = channel_sum<MM>(gbv * dtb);
+                            const float tbv = gbv * cur.x[jj] * kInvNd;
+                            float td[3];
+#pragma unroll
+                            for (int ax = 0; ax < 3; ++ax) {
+                                float t = tbv;
+                                if (has[ax]) {
+                                    const float gh = g * ea[ax] * hp[ax];
+                                    t = fmaf(gh, av[ax], tbv);
+                                    dAacc[ax] = fmaf(gh, dl[ax], dAacc[ax]);
+                                }
+                                td[ax] = channel_sum<MM>(t);
+                            }
+                            F::st(rdC, voDM[jj], oDM, cur.dy[jj] * hcur[ri][jj]);
+                            F::st(rg, voDM[jj], oDM, g * dtb * cur.x[jj]);
+                            if (m == 0) {
+                                st[(slot0 + jj) * CPW + lc] = tx;
+#pragma unroll
+                                for (int ax = 0; ax < 3; ++ax) st[((ax + 1) * PTS + slot0 + jj) * CPW + lc] = td[ax];
+                            }
+                            if (r == r0) F::st(rgR, voDM[jj], pp * u.nt1 * n2 * sDM, g);
+                            if (jj == 0) F::st(rgC, c * 4, (pp * n1 + ri) * u.nt2 * sDM, g);
+                            gp[ri][jj] = g;
+                            ep[ri][jj] = ea[0];
+                            gb[jj] = g;
+                            eb[jj] = ea[1];
+                            gr = g;
+                            er = ea[2];
+                            right = true;
+                        }
+                    }
+                    // The plane above's h is the next plane's own.
+#pragma unroll
+                    for (int jj = 0; jj < TW; ++jj) hcur[ri][jj] = cur.hu0[jj];
+                };
+                for (int pp = P1 - 1; pp >= P0; --pp) {
+#pragma unroll
+                    for (int ri = TR - 1; ri >= 0; ri -= 2) {
+                        // Rows ri (in R0) and ri - 1 (in R1); the row after
+                        // ri - 1 in walk order goes into R0.
+                        const int rn = ri - 1;
+                        ld_ops(pp, r0 + max(min(rn, re - 1), 0), R1);
+                        ld_succ(pp, r0 + max(min(rn, re - 1), 0), R1);
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (ri < re) do_row(pp, ri, R0);
+                        const int pn = rn - 1 >= 0 ? pp : max(pp - 1, P0);
+                        const int rnn = rn - 1 >= 0 ? rn - 1 : TR - 1;
+                        ld_ops(pn, r0 + max(min(rnn, re - 1), 0), R0);
+                        ld_succ(pn, r0 + max(min(rnn, re - 1), 0), R0);
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (rn < re) do_row(pp, rn, R1);
+                    }
+                }
+            } else {
+                // A wait ran out (here or before): NaN into this sub-tile's
+                // outputs, boundary states and stage slots.
+                const float qn = __builtin_nanf("");
+                for (int pp = P0; pp < P1; ++pp)
+                    for (int ri = 0; ri < re; ++ri)
+                        for (int jj = 0; jj < je; ++jj) {
+                            const int oDM = (pq(pp, r0 + ri) + jj) * sDM;
+                            F::st(rdC, c * 4, oDM, qn);
+                            F::st(rg, c * 4, oDM, qn);
+                            if (m == 0)
+                                for (int k = 0; k < 4; ++k)
+                                    st[(k * PTS + ((pp - P0) * TR + ri) * TW + jj) * CPW + lc] = qn;
+                            if (ri == 0) F::st(rgR, c * 4, (pp * u.nt1 * n2 + jj) * sDM, qn);
+                            if (jj == 0) F::st(rgC, c * 4, (pp * n1 + ri) * u.nt2 * sDM, qn);
+                        }
+                dAacc[0] = dAacc[1] = dAacc[2] = qn;
+                if (lane == 0) __hip_atomic_store(f.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            const long pb = static_cast<long>(s) * npen + pen;
+#pragma unroll
+            for (int ax = 0; ax < 3; ++ax) a.part[(pb * 3 + ax) * DM + c] = dAacc[ax];
+            __builtin_amdgcn_s_waitcnt(0);   // this wave's stores acknowledged by L2
+            if (lane == 0)
+                __hip_atomic_store(f.flags + pb * ncg + cg, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // dx / ddelta of the run's channels at the sub-tile's points.
+            __syncthreads();
+            const long dch = static_cast<long>(cgr) * 64 / MM;
+            const GradWin fw = grad_window<3>(a, qb, qe, c, d, m, true);
+            grad_flush<3, MM, PTS>(fw, st, dch, a.D, [&](int sl) -> long {
+                const int pp = P0 + sl / (TR * TW), ri = (sl / TW) % TR, jj = sl % TW;
+                return (pp < P1 && ri < re && jj < je) ? static_cast<long>(pq(pp, r0 + ri) + jj) : -1L;
+            });
+        }
+    }
+}
+
 // dA[k] = the nbx workgroup partials of k added in a fixed order: workgroup
 // x takes outputs [64 x, +64), wave w the partials b = w, w + 4, ... in four
 // interleaved running sums, then wave 0 adds the waves' sums in wave order.
@@ -1326,6 +1618,8 @@ struct NdBwdShape {
     bool fused2;         // 2D with staged per-channel outputs: the fused dataflow backward may run
     size_t gbd_bytes;    // its boundary states (gR, gC)
     long fnt0, fnt1;     // its tiles per axis
+    bool fused3;         // 3D: the fused pencil backward may run (boundary states in gbd_bytes)
+    long f3nt1, f3nt2, f3nsub;   // its pencils per axis 1, 2 and sub-tiles per pencil
 };
 
 static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
@@ -1429,12 +1723,39 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
             s.part_bytes = std::max<size_t>(s.part_bytes, sizeof(float) * (nf + dA_chunks(nf)) * 2 * DM);
         }
     }
+    // The fused 3D backward (nd_fused3d): pencils of kF3R x kF3W points
+    // through every plane in sub-tiles of kF3S planes, 8 <= M <= 32 (its LDS
+    // stage), D*M a multiple of 2048 (workgroups of four channel groups per
+    // XCD), every window and boundary buffer below 2 GiB.
+    s.fused3 = false;
+    s.f3nt1 = s.f3nt2 = s.f3nsub = 0;
+    if (s.nd == 3 && s.lanes && s.M >= 8 && s.M <= 32 && (s.D * s.M) % 2048 == 0) {
+        const long DM = s.D * s.M, n0 = a->dims[0], n1 = a->dims[1], n2 = a->dims[2];
+        const long nt1 = (n1 + kF3R - 1) / kF3R, nt2 = (n2 + kF3W - 1) / kF3W, nsub = (n0 + kF3S - 1) / kF3S;
+        const double lim = 2147483000.0;
+        const double win = static_cast<double>(kF3S + 1) * n1 * n2 * DM * 4;
+        const double dwin = (2.0 * s.P + static_cast<double>(kF3S + 1) * n1 * n2) * s.D * 4;
+        const double bR = static_cast<double>(n0) * nt1 * n2 * DM * 4, bC = static_cast<double>(n0) * n1 * nt2 * DM * 4;
+        if (win < lim && dwin < lim && bR < lim && bC < lim && nt1 + nt2 - 1 <= kMaxFlowBands) {
+            s.fused3 = true;
+            s.f3nt1 = nt1;
+            s.f3nt2 = nt2;
+            s.f3nsub = nsub;
+            s.gbd_bytes = std::max<size_t>(s.gbd_bytes, align_up(sizeof(float) * (n0 * nt1 * n2 + n0 * n1 * nt2) * DM, 256));
+            const long nf = nsub * nt1 * nt2;
+            s.part_bytes = std::max<size_t>(s.part_bytes, sizeof(float) * (nf + dA_chunks(nf)) * 3 * DM);
+        }
+    }
     s.flow_bytes = 0;
     if (s.atile2 || s.tile_bytes) {
         int nt[3];
         adj_flow_tiles(a, static_cast<int>(s.nd), nt);
         const long ntiles = static_cast<long>(nt[0]) * nt[1] * (s.nd == 3 ? nt[2] : 1);
         s.flow_bytes = align_up(4 * (kFlowHead + static_cast<size_t>(ntiles) * (s.D * s.M / 64)), 256);
+    }
+    if (s.fused3) {
+        const size_t nfl = static_cast<size_t>(s.f3nsub * s.f3nt1 * s.f3nt2) * (s.D * s.M / 64);
+        s.flow_bytes = std::max<size_t>(s.flow_bytes, align_up(4 * (kFlowHead + nfl), 256));
     }
     return true;
 }
@@ -1504,6 +1825,30 @@ static int adj_flow_setup(const KMScanNDBwd *a, const NdBwdShape &s, hipStream_t
     if (ext) flow_zero(ext->buf, ext->cap, st);
     int kind = 0;
     const int bound = flow_bind(st, static_cast<size_t>(ntiles * ncg), ext, fa, &kind);
+    note_flow(st, kind, kind == 2 ? fa.counter : nullptr);
+    return bound;
+}
+
+// The fused 3D backward's dataflow state: bands of the (nt1, nt2) pencil
+// grid, a flag per (sub-tile, pencil, channel group). Returns as
+// flow_bind (1 bound, 0 not available, -1 error).
+static int fused3_flow_setup(const NdBwdShape &s, hipStream_t st, FlowArgs &fa, FlowBuf *ext) {
+    const int n1 = static_cast<int>(s.f3nt1), n2 = static_cast<int>(s.f3nt2);
+    const long ncg = s.D * s.M / 64;
+    const int nb = n1 + n2 - 1;
+    fa.nbands = nb;
+    for (int x = 0; x <= 8; ++x) fa.cg_lo[x] = static_cast<int>(static_cast<long>(x) * ncg / 8);
+    if (flow_q(fa) != kFlowQ) return 0;
+    fa.band_start[0] = 0;
+    for (int b = 0; b < nb; ++b) {
+        const int lo = std::max(0, b - (n2 - 1)), hi = std::min(b, n1 - 1);
+        fa.band_start[b + 1] = fa.band_start[b] + (hi >= lo ? hi - lo + 1 : 0);
+    }
+    const long nfl = s.f3nsub * s.f3nt1 * s.f3nt2 * ncg;
+    if (nfl >= 0x7fffffffL) return 0;
+    if (ext) flow_zero(ext->buf, ext->cap, st);
+    int kind = 0;
+    const int bound = flow_bind(st, static_cast<size_t>(nfl), ext, fa, &kind);
     note_flow(st, kind, kind == 2 ? fa.counter : nullptr);
     return bound;
 }
@@ -1636,6 +1981,41 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
     // list to upload), else by tile bands.
     static thread_local km::FlowArgs fa;
     int nt[3] = {0, 0, 0};
+    // 3D on the dataflow schedule: the fused pencil backward (adjoint state
+    // and gradients in one launch; KM_SCANND_BWD_FUSED=0: two passes).
+    const char *fe3 = std::getenv("KM_SCANND_BWD_FUSED");
+    if (s.fused3 && km::flow_wanted(3) && !(fe3 && std::strcmp(fe3, "0") == 0)) {
+        km::FlowBuf wf{reinterpret_cast<unsigned *>(ws + s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes),
+                       s.flow_bytes / 4, 8};
+        const int fb3 = km::fused3_flow_setup(s, st, fa, (a->workspace && s.flow_bytes) ? &wf : nullptr);
+        if (fb3 < 0) return -1;
+        if (fb3 > 0) {
+            float *gbd = reinterpret_cast<float *>(ws + s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes +
+                                                   s.flow_bytes);
+            const long DM = s.D * s.M;
+            km::Fused3Args u{gbd, gbd + a->dims[0] * s.f3nt1 * a->dims[2] * DM, static_cast<int>(s.f3nt1),
+                             static_cast<int>(s.f3nt2), static_cast<int>(s.f3nsub)};
+            const long npen = s.f3nt1 * s.f3nt2;
+            long per_xcd = 0;
+            for (int x = 0; x < 8; ++x)
+                per_xcd = std::max<long>(per_xcd, npen * ((fa.cg_lo[x + 1] - fa.cg_lo[x]) / km::kFlowQ));
+            const dim3 grid(static_cast<unsigned>(8 * std::min<long>(per_xcd, 256 / km::kFlowQ)));
+            const dim3 blk(64 * km::kFlowQ);
+            switch (s.M) {
+            case 8: hipLaunchKernelGGL((km::nd_fused3d<km::kF3S, km::kF3R, km::kF3W, 8>), grid, blk, 0, st, args, fa, u); break;
+            case 16: hipLaunchKernelGGL((km::nd_fused3d<km::kF3S, km::kF3R, km::kF3W, 16>), grid, blk, 0, st, args, fa, u); break;
+            default: hipLaunchKernelGGL((km::nd_fused3d<km::kF3S, km::kF3R, km::kF3W, 32>), grid, blk, 0, st, args, fa, u); break;
+            }
+            km::sum_dA(args.part, a->dA, s.f3nsub * npen, 3 * DM, st);
+            if (plan) km_wavefront_plan_free(plan);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) {
+                km::set_error("km_scannd_bwd: launch failed: %s", hipGetErrorString(e));
+                return -1;
+            }
+            return 0;
+        }
+    }
     // With the caller's workspace the flags live in it (cleared per call);
     // otherwise in the stream's dataflow block.
     km::FlowBuf wflow{reinterpret_cast<unsigned *>(ws + s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes),

@@ -440,19 +440,22 @@ def test_backward_dataflow_and_band_schedules_agree(dims, D, M, monkeypatch):
 
 
 FUSED_CASES = [((43, 37), 128, 16), ((17, 70), 256, 8), ((9, 5), 512, 4), ((25, 30), 64, 32),
-               ((64, 64), 128, 16)]
+               ((64, 64), 128, 16),
+               ((9, 10, 11), 128, 16), ((13, 6, 7), 256, 8), ((6, 9, 5), 64, 32), ((20, 16, 16), 128, 16),
+               ((5, 4, 4), 128, 16)]
 
 
 @pytest.mark.parametrize("dims,D,M", FUSED_CASES)
 def test_backward_fused_2d_matches_two_pass(dims, D, M, monkeypatch):
-    # 2D grids whose channel groups fill workgroups of four per XCD (D*M a
+    # Grids whose channel groups fill workgroups of four per XCD (D*M a
     # multiple of 2048) run the fused backward: the adjoint state and every
-    # gradient in one dataflow launch, only the tiles' boundary states
-    # stored. KM_SCANND_BWD_FUSED=0 runs the adjoint sweep, then the
-    # gradient pass: the same arithmetic at every point, so dx, ddelta, dB
-    # and dC agree bit for bit; dA adds its terms per 8 x 4 tile instead of
-    # per 8 x 64 tile and agrees to rounding. Covers partial tiles on both
-    # axes and M = 4 to 32.
+    # gradient in one dataflow launch (2D tiles; 3D pencils through every
+    # plane in sub-tiles of 4 planes), only the boundary states stored.
+    # KM_SCANND_BWD_FUSED=0 runs the adjoint sweep, then the gradient pass:
+    # the same arithmetic at every point, so dx, ddelta, dB and dC agree bit
+    # for bit; dA adds its terms per tile or sub-tile and agrees to
+    # rounding. Covers partial tiles, pencils and sub-tiles on every axis,
+    # M = 4 to 32 (3D: 8 to 32).
     x, A, B, Cm, dt, h, dy = bwd_inputs(dims, D, M, 5)
     a = run_bwd(dims, x, A, B, Cm, dt, h, dy)
     monkeypatch.setenv("KM_SCANND_BWD_FUSED", "0")
@@ -487,7 +490,8 @@ print("bwd budget0 done", flush=True)
 """
 
 
-@pytest.mark.parametrize("dims,D,M", [((33, 65), 8, 16), ((9, 6, 11), 4, 16), ((43, 37), 128, 16)])
+@pytest.mark.parametrize("dims,D,M", [((33, 65), 8, 16), ((9, 6, 11), 4, 16), ((43, 37), 128, 16),
+                                      ((9, 10, 11), 128, 16)])
 def test_backward_dataflow_wait_budget_exhausted_fails_loudly(dims, D, M, tmp_path):
     # KM_SCANND_FLOW_SPIN=0 (read once per process, so a child process):
     # every wait of the adjoint sweep gives up without polling, every kernel
@@ -519,7 +523,7 @@ def test_backward_dataflow_wait_budget_exhausted_fails_loudly(dims, D, M, tmp_pa
     np.testing.assert_allclose(dB[last], want["dB"].reshape(dims + (D, M))[last], rtol=1e-5, atol=1e-6)
 
 
-@pytest.mark.parametrize("dims,D,M", [((33, 40), 8, 16), ((24, 20), 128, 16)])
+@pytest.mark.parametrize("dims,D,M", [((33, 40), 8, 16), ((24, 20), 128, 16), ((7, 9, 10), 128, 16)])
 def test_backward_deterministic_and_workspace(dims, D, M):
     x, A, B, Cm, dt, h, dy = bwd_inputs(dims, D, M, 1)
     a = run_bwd(dims, x, A, B, Cm, dt, h, dy)
@@ -527,12 +531,13 @@ def test_backward_deterministic_and_workspace(dims, D, M):
     for k in a:
         assert np.array_equal(a[k].view(np.uint32), b[k].view(np.uint32)), k
     # An explicit workspace of the queried size gives the same result.
-    args = K.KMScanNDBwd(K.longs(dims), 2, D, M)
+    nd = len(dims)
+    args = K.KMScanNDBwd(K.longs(dims), nd, D, M)
     need = K.km_scannd_bwd_workspace_bytes(C.byref(args))
     assert need > 0
     ws = torch.empty(need, dtype=torch.uint8, device="cuda")
     Pn = int(np.prod(dims))
-    out = [torch.empty(s, device="cuda") for s in ((Pn, D), (2, Pn, D), (2, D, M), (Pn, D, M), (Pn, D, M))]
+    out = [torch.empty(s, device="cuda") for s in ((Pn, D), (nd, Pn, D), (nd, D, M), (Pn, D, M), (Pn, D, M))]
     K.scannd_bwd(dims, T(x), T(A), T(B), T(Cm), T(dt), T(h), T(dy), *out, workspace=ws)
     torch.cuda.synchronize()
     for k, t in zip(("dx", "ddelta", "dA", "dB", "dC"), out):
