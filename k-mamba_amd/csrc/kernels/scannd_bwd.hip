@@ -394,7 +394,7 @@ __global__ void __launch_bounds__(64) nd_adjoint_tile3d(NdBwdArgs a, const int *
 // points (the critical path runs through nt0 + nt1 - 1 of them), 3D tiles
 // those of the band schedule.
 constexpr int kAdjFTR = 8, kAdjFTW = 4;   // 2D dataflow tiles (rows, points)
-constexpr int kF3S = 4, kF3R = 4, kF3W = 4;   // fused 3D pencils: planes per sub-tile, rows, points
+constexpr int kF3S = 2, kF3R = 4, kF3W = 4;   // fused 3D pencils: planes per sub-tile, rows, points
 
 // NaN into the states of one (tile, channel group) whose wait gave up, so
 // every tile that depends on it, and every gradient, turns NaN too.
@@ -1267,7 +1267,7 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowAr
 // the pencil's first row and first column of every plane are stored, in gR
 // / gC, for the pencils above and to the left (which wait on this pencil's
 // flag for the same sub-tile). dx / ddelta go through the workgroup's LDS
-// stage per sub-tile; dA to a partial per (sub-tile, pencil, group).
+// stage per sub-tile; dA to a partial per (pencil, group).
 struct Fused3Args {
     float *gR;   // [n0][nt1][n2][D*M]: the states of each pencil's first row
     float *gC;   // [n0][n1][nt2][D*M]: of each pencil's first column
@@ -1350,6 +1350,7 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused3d(NdBwdArgs a, FlowAr
 #pragma unroll
             for (int jj = 0; jj < TW; ++jj) gp[ri][jj] = ep[ri][jj] = hcur[ri][jj] = 0.f;
         bool ok = true;
+        float dAacc[3] = {0.f, 0.f, 0.f};   // over the pencil, in walk order
         for (int s = u.nsub - 1; s >= 0; --s, ++sub_n) {
             const int P0 = s * SUB, P1 = min(n0, P0 + SUB);
             // Windows: the plane above the sub-tile through its last plane.
@@ -1406,7 +1407,6 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused3d(NdBwdArgs a, FlowAr
                     for (int jj = 0; jj < TW; ++jj)
                         hcur[ri][jj] = F::ld(rh, voDM[jj], pq(P1 - 1, r0 + min(ri, re - 1)) * sDM);
             }
-            float dAacc[3] = {0.f, 0.f, 0.f};
             if (ok) {
                 const long fb = (static_cast<long>(s) * npen + pen);
                 if (below_tile) ok = flow_wait(f.flags + (fb + u.nt2) * ncg + cg, epoch, f.spin) && ok;
@@ -1528,8 +1528,6 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused3d(NdBwdArgs a, FlowAr
                 if (lane == 0) __hip_atomic_store(f.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
             const long pb = static_cast<long>(s) * npen + pen;
-#pragma unroll
-            for (int ax = 0; ax < 3; ++ax) a.part[(pb * 3 + ax) * DM + c] = dAacc[ax];
             __builtin_amdgcn_s_waitcnt(0);   // this wave's stores acknowledged by L2
             if (lane == 0)
                 __hip_atomic_store(f.flags + pb * ncg + cg, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1542,6 +1540,8 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused3d(NdBwdArgs a, FlowAr
                 return (pp < P1 && ri < re && jj < je) ? static_cast<long>(pq(pp, r0 + ri) + jj) : -1L;
             });
         }
+#pragma unroll
+        for (int ax = 0; ax < 3; ++ax) a.part[(static_cast<long>(pen) * 3 + ax) * DM + c] = dAacc[ax];
     }
 }
 
@@ -1742,7 +1742,7 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
             s.f3nt2 = nt2;
             s.f3nsub = nsub;
             s.gbd_bytes = std::max<size_t>(s.gbd_bytes, align_up(sizeof(float) * (n0 * nt1 * n2 + n0 * n1 * nt2) * DM, 256));
-            const long nf = nsub * nt1 * nt2;
+            const long nf = nt1 * nt2;
             s.part_bytes = std::max<size_t>(s.part_bytes, sizeof(float) * (nf + dA_chunks(nf)) * 3 * DM);
         }
     }
@@ -2006,7 +2006,7 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
             case 16: hipLaunchKernelGGL((km::nd_fused3d<km::kF3S, km::kF3R, km::kF3W, 16>), grid, blk, 0, st, args, fa, u); break;
             default: hipLaunchKernelGGL((km::nd_fused3d<km::kF3S, km::kF3R, km::kF3W, 32>), grid, blk, 0, st, args, fa, u); break;
             }
-            km::sum_dA(args.part, a->dA, s.f3nsub * npen, 3 * DM, st);
+            km::sum_dA(args.part, a->dA, npen, 3 * DM, st);
             if (plan) km_wavefront_plan_free(plan);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) {
