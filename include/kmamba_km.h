@@ -275,10 +275,11 @@ int km_scannd_fwd_noalloc(const ScanNDParams *p, void *stream);
  * (device, stream). The adjoint state runs against the forward's wavefront:
  * on 2D and 3D grids with D*M a multiple of 64 as one dataflow launch over
  * tiles on a device with 8 XCDs (KM_SCANND_SCHED=band: one launch per tile
- * band), otherwise one launch per anti-diagonal level, last to first. On 2D
- * grids with D*M a multiple of 2048 and 4 <= M <= 32 that launch also forms
- * every gradient (the workspace then holds the tiles' boundary states, 3/8
- * of a [P, D, M] tensor; KM_SCANND_BWD_FUSED=0: a separate gradient pass). */
+ * band), otherwise one launch per anti-diagonal level, last to first. With
+ * D*M a multiple of 2048 and 4 <= M <= 32 (3D: 8 <= M <= 32) that launch
+ * runs on pencils and also forms every gradient (the workspace then holds
+ * the pencils' boundary states, 1/4 of a [P, D, M] tensor in 2D, 1/2 in
+ * 3D; KM_SCANND_BWD_FUSED=0: the sweep, then a separate gradient pass). */
 typedef struct {
     const long  *dims;
     long ndims, D, M;

@@ -992,31 +992,33 @@ __global__ void __launch_bounds__(256) nd_adjoint_grads_tile3d(NdBwdArgs a) {
     }
 }
 
-// The 2D backward fused on the dataflow schedule: an item is (tile of
-// kAdjFTR x kAdjFTW points, run of kFlowQ channel groups), taken in reverse
-// band order; each wave walks its group's tile as adj_tile2d does (rows
-// bottom-up, right to left) and, at each point, forms every gradient from
-// the adjoint state it just computed, in grad_finish's arithmetic. The
-// adjoint state is never stored whole: only each tile's first row and first
-// column go to the boundary buffers gR / gC, which the tiles above and to
-// the left read (waiting on this tile's flag). A point's own decays
-// exp2(delta_a A_a), which its gradient terms need, are the ones its
-// predecessors' adjoint steps need, so each is formed once. dx / ddelta go
-// through the workgroup's LDS stage (grad_flush), the dA terms to a partial
-// per (tile, channel group), so every output is identical run to run.
-struct Fused2Args {
-    float *gR;   // [nt0][n1][D*M]: adjoint state on the first row of each tile row
-    float *gC;   // [n0][nt1][D*M]: on the first column of each tile column
-    int nt0, nt1;
+// The 2D backward fused on the dataflow schedule: an item is a pencil (a
+// column strip of TW points through every row, run of kFlowQ channel
+// groups), taken right to left. Each wave walks its group's pencil
+// bottom-up in sub-tiles of TR rows (a completion flag after each), each
+// row right to left as adj_tile2d does, and at each point forms every
+// gradient from the adjoint state it just computed, in grad_finish's
+// arithmetic. The adjoint state is never stored whole: the row below stays
+// in registers across sub-tiles and only the pencil's first column goes to
+// the boundary buffer gC, which the pencil to the left reads (a sub-tile
+// waits only on the same sub-tile of the pencil to its right). A point's
+// own decays exp2(delta_a A_a), which its gradient terms need, are the ones
+// its predecessors' adjoint steps need, so each is formed once. dx / ddelta
+// go through the workgroup's LDS stage (grad_flush) per sub-tile; dA is
+// summed per (pencil, group) in walk order, so every output is identical
+// run to run.
+struct Fused2PArgs {
+    float *gC;   // [n0][nt1][D*M]: the states of each pencil's first column
+    int nt1, nsub;
 };
 
 template <int TR, int TW, int RB, int MM>
-__global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowArgs f, Fused2Args u) {
-    constexpr int PTS = TR * TW;                  // a tile is one staged group
+__global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2p(NdBwdArgs a, FlowArgs f, Fused2PArgs u) {
+    constexpr int PTS = TR * TW;                  // a sub-tile is one staged group
     static_assert(kStageOut<MM> && (256 / MM * PTS) % 256 == 0, "staged per-channel outputs");
     static_assert(TR % RB == 0, "whole batches of rows");
     constexpr float kInvNd = 0.5f;
-    constexpr int CPW = 256 / MM;                 // channels of a workgroup's run
+    constexpr int CPW = 256 / MM;
     constexpr int SG = 3 * PTS * CPW;             // one stage buffer: dx, ddelta0, ddelta1
     const int xcd = flow_xcd();
     const int cg0 = f.cg_lo[xcd], ncx = f.cg_lo[xcd + 1] - cg0;
@@ -1024,233 +1026,197 @@ __global__ void __launch_bounds__(64 * kFlowQ, 2) nd_fused2d(NdBwdArgs a, FlowAr
     const int nq = ncx / kFlowQ;
     const int w = static_cast<int>(threadIdx.x / 64);
     const int lane = static_cast<int>(threadIdx.x & 63);
-    const int ntiles = f.band_start[f.nbands];
-    const unsigned nitems = static_cast<unsigned>(ntiles) * static_cast<unsigned>(nq);
+    const int npen = u.nt1;
+    const unsigned nitems = static_cast<unsigned>(npen) * static_cast<unsigned>(nq);
     const unsigned epoch = __builtin_amdgcn_readfirstlane(
         __hip_atomic_load(f.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     const int n0 = static_cast<int>(a.dims[0]), n1 = static_cast<int>(a.dims[1]);
     const int DM = static_cast<int>(a.D) * MM;
     const int ncg = DM / 64;
-    const int ntile[2] = {u.nt0, u.nt1};
-    // Byte strides: a point of [P, D] and of [P, D*M], a delta axis.
     const int sD = static_cast<int>(a.D) * 4, sDM = DM * 4, sAx = static_cast<int>(a.P * a.D * 4);
     __shared__ unsigned s_item[2];
     __shared__ float stage[2 * SG];
     using F = bio<f32_t>;
     struct Row {
         float dy[TW], x[TW], d0[TW], d1[TW], C[TW], B[TW], h[TW];
-        float hl, dr1, gr;   // h left of the tile, delta_1 and state right of it
+        float hl, dr1, gr;   // h left of the pencil, delta_1 and state right of it
     };
+    int sub_n = 0;
     for (int it = 0;; ++it) {
         if (threadIdx.x == 0) s_item[it & 1] = atomicAdd(&f.counter[xcd], 1u);
         __syncthreads();
         const unsigned item = __builtin_amdgcn_readfirstlane(s_item[it & 1]);
         if (item >= nitems) break;
-        const int tb = ntiles - 1 - static_cast<int>(item / nq);   // reverse band order
+        const int t1 = npen - 1 - static_cast<int>(item / nq);      // right to left
         const int cgr = cg0 + static_cast<int>(item % nq) * kFlowQ;
         const int cg = cgr + w;
-        const int band = flow_band(f, tb);
-        int ti[2] = {0, 0};
-        band_tile_n(2, ntile, band, tb - f.band_start[band], ti);
-        const int tl = ti[0] * u.nt1 + ti[1];
         const int c = cg * 64 + lane;
         const int d = c / MM;
         const int m = c - d * MM;
-        const int r0 = ti[0] * TR, r1 = min(n0, r0 + TR);
-        const int j0 = ti[1] * TW, j1 = min(n1, j0 + TW), je = j1 - j0;
-        const bool below_tile = r1 < n0, right_tile = j1 < n1;
-        // Windows: the row above the tile to the successor row below it.
-        const int qb = (r0 > 0 ? r0 - 1 : 0) * n1, qe = (below_tile ? r1 + 1 : r1) * n1;
-        // The loop's buffers (the flush builds its own window for dx / ddelta).
-        struct {
-            __amdgpu_buffer_rsrc_t x, dy, dl, g, B, h, dC;
-            int vd, vc;
-        } gw;
-        {
-            const long n = qe - qb;
-            gw.x = make_rsrc(a.x + static_cast<long>(qb) * a.D, n * a.D * 4);
-            gw.dy = make_rsrc(a.dy + static_cast<long>(qb) * a.D, n * a.D * 4);
-            gw.dl = make_rsrc(a.delta + static_cast<long>(qb) * a.D, (a.P + n) * a.D * 4);
-            gw.g = make_rsrc(a.dB + static_cast<long>(qb) * DM, n * DM * 4);
-            gw.B = make_rsrc(a.B + static_cast<long>(qb) * DM, n * DM * 4);
-            gw.h = make_rsrc(a.h + static_cast<long>(qb) * DM, n * DM * 4);
-            gw.dC = make_rsrc(a.dC + static_cast<long>(qb) * DM, n * DM * 4);
-            gw.vd = d * 4;
-            gw.vc = c * 4;
-        }
-        const auto rC = make_rsrc(a.C + static_cast<long>(qb) * DM, static_cast<long>(qe - qb) * DM * 4);
-        // gR rows ti0 (written) and ti0 + 1 (read); gC rows r0 .. r1 - 1 at
-        // tile columns ti1 (written) and ti1 + 1 (read).
-        const long gr_base = static_cast<long>(ti[0]) * n1 * DM;
-        const auto rgR = make_rsrc(u.gR + gr_base, (static_cast<long>(u.nt0) * n1 * DM - gr_base) * 4);
-        const long gc_base = (static_cast<long>(r0) * u.nt1 + ti[1]) * DM;
-        const auto rgC = make_rsrc(u.gC + gc_base, (static_cast<long>(n0) * u.nt1 * DM - gc_base) * 4);
+        const int j0 = t1 * TW, j1 = min(n1, j0 + TW), je = j1 - j0;
+        const bool right_tile = j1 < n1;
         const float A0 = a.A[c] * kLog2e, A1 = a.A[DM + c] * kLog2e;
         const float av[2] = {a.A[c], a.A[DM + c]};
-        float *st = stage + (it & 1) * SG;
-        // Column offsets (columns past the tile's edge repeat its last one) in
-        // VGPRs, a row's offset in the SGPR offset.
+        const int lc = static_cast<int>(threadIdx.x) / MM;
         int voD[TW], voDM[TW];
 #pragma unroll
         for (int jj = 0; jj < TW; ++jj) {
             const int cc = min(jj, je - 1);
-            voD[jj] = gw.vd + cc * sD;
-            voDM[jj] = gw.vc + cc * sDM;
+            voD[jj] = d * 4 + cc * sD;
+            voDM[jj] = c * 4 + cc * sDM;
         }
-        auto rowq = [&](int r) { return r * n1 + j0 - qb; };   // point (r, j0) in the window
-        auto ld_ops = [&](int r, Row &rw) __attribute__((always_inline)) {
-            const int oD = rowq(r) * sD, oDM = rowq(r) * sDM;
+        // gC (r, t1) at r * nt1 from the pencil's base, the right pencil's at + 1.
+        const long gcb = static_cast<long>(t1) * DM;
+        const auto rgC = make_rsrc(u.gC + gcb, (static_cast<long>(n0) * u.nt1 * DM - gcb) * 4);
+        float gb[TW], eb[TW];             // the row below: state, decay along axis 0
 #pragma unroll
-            for (int jj = 0; jj < TW; ++jj) {
-                rw.dy[jj] = F::ld(gw.dy, voD[jj], oD);
-                rw.x[jj] = F::ld(gw.x, voD[jj], oD);
-                rw.d0[jj] = F::ld(gw.dl, voD[jj], oD);
-                rw.d1[jj] = F::ld(gw.dl, voD[jj], sAx + oD);
-                rw.C[jj] = F::ld(rC, voDM[jj], oDM);
-                rw.B[jj] = F::ld(gw.B, voDM[jj], oDM);
-                rw.h[jj] = F::ld(gw.h, voDM[jj], oDM);
-            }
-            rw.hl = j0 > 0 ? F::ld(gw.h, gw.vc, oDM - sDM) : 0.f;
-            rw.dr1 = right_tile ? F::ld(gw.dl, gw.vd, sAx + oD + je * sD) : 0.f;
-        };
-        // The right successor's state (written by another workgroup).
-        auto ld_succ = [&](int r, Row &rw) __attribute__((always_inline)) {
-            rw.gr = right_tile ? F::ld_agent(rgC, gw.vc, ((r - r0) * u.nt1 + 1) * sDM) : 0.f;
-        };
-        // The first batch's operands and the row above the tile go out before
-        // the wait on the successors.
-        Row ba[RB], bb[RB];
-#pragma unroll
-        for (int i = 0; i < RB; ++i) ld_ops(max(r1 - 1 - i, r0), ba[i]);
-        float htop[TW];
-#pragma unroll
-        for (int jj = 0; jj < TW; ++jj) htop[jj] = r0 > 0 ? F::ld(gw.h, voDM[jj], rowq(r0 - 1) * sDM) : 0.f;
-        bool ready = true;
-        if (below_tile) ready = flow_wait(f.flags + static_cast<long>(tl + u.nt1) * ncg + cg, epoch, f.spin) && ready;
-        if (right_tile) ready = flow_wait(f.flags + static_cast<long>(tl + 1) * ncg + cg, epoch, f.spin) && ready;
+        for (int jj = 0; jj < TW; ++jj) gb[jj] = eb[jj] = 0.f;
         float dAacc[2] = {0.f, 0.f};
-        const int lc = static_cast<int>(threadIdx.x) / MM;
-        if (ready) {
+        bool ok = true;
+        for (int s = u.nsub - 1; s >= 0; --s, ++sub_n) {
+            const int r0 = s * TR, r1 = min(n0, r0 + TR);
+            const int qb = (r0 > 0 ? r0 - 1 : 0) * n1, qe = r1 * n1;
+            const long nqp = qe - qb;
+            const auto rx = make_rsrc(a.x + static_cast<long>(qb) * a.D, nqp * a.D * 4);
+            const auto rdy = make_rsrc(a.dy + static_cast<long>(qb) * a.D, nqp * a.D * 4);
+            const auto rdl = make_rsrc(a.delta + static_cast<long>(qb) * a.D, (a.P + nqp) * a.D * 4);
+            const auto rg = make_rsrc(a.dB + static_cast<long>(qb) * DM, nqp * DM * 4);
+            const auto rB = make_rsrc(a.B + static_cast<long>(qb) * DM, nqp * DM * 4);
+            const auto rC = make_rsrc(a.C + static_cast<long>(qb) * DM, nqp * DM * 4);
+            const auto rh = make_rsrc(a.h + static_cast<long>(qb) * DM, nqp * DM * 4);
+            const auto rdC = make_rsrc(a.dC + static_cast<long>(qb) * DM, nqp * DM * 4);
+            float *st = stage + (sub_n & 1) * SG;
+            auto rowq = [&](int r) { return r * n1 + j0 - qb; };
+            auto ld_ops = [&](int r, Row &rw) __attribute__((always_inline)) {
+                const int oD = rowq(r) * sD, oDM = rowq(r) * sDM;
 #pragma unroll
-            for (int i = 0; i < RB; ++i) ld_succ(max(r1 - 1 - i, r0), ba[i]);
-            // The successors below: state (gR) and decay along axis 0.
-            float gb[TW], eb[TW];
-#pragma unroll
-            for (int jj = 0; jj < TW; ++jj) {
-                gb[jj] = below_tile ? F::ld_agent(rgR, voDM[jj], (n1 + j0) * sDM) : 0.f;
-                eb[jj] = below_tile ? exp2_fast(F::ld(gw.dl, voD[jj], rowq(r1) * sD) * A0) : 0.f;
-            }
-            auto ld_batch = [&](int rtop, Row (&bt)[RB]) __attribute__((always_inline)) {
-#pragma unroll
-                for (int i = 0; i < RB; ++i) {
-                    const int r = max(rtop - i, r0);   // past r0: reload r0
-                    ld_ops(r, bt[i]);
-                    ld_succ(r, bt[i]);
+                for (int jj = 0; jj < TW; ++jj) {
+                    rw.dy[jj] = F::ld(rdy, voD[jj], oD);
+                    rw.x[jj] = F::ld(rx, voD[jj], oD);
+                    rw.d0[jj] = F::ld(rdl, voD[jj], oD);
+                    rw.d1[jj] = F::ld(rdl, voD[jj], sAx + oD);
+                    rw.C[jj] = F::ld(rC, voDM[jj], oDM);
+                    rw.B[jj] = F::ld(rB, voDM[jj], oDM);
+                    rw.h[jj] = F::ld(rh, voDM[jj], oDM);
                 }
+                rw.hl = j0 > 0 ? F::ld(rh, c * 4, oDM - sDM) : 0.f;
+                rw.dr1 = right_tile ? F::ld(rdl, d * 4, sAx + oD + je * sD) : 0.f;
             };
-            // Rows rtop, rtop - 1, ... of batch bt; the next batch (the rows
-            // above) is nx, already loaded.
-            auto do_batch = [&](int rtop, const Row (&bt)[RB], const Row (&nx)[RB]) __attribute__((always_inline)) {
+            auto ld_succ = [&](int r, Row &rw) __attribute__((always_inline)) {
+                rw.gr = right_tile ? F::ld_agent(rgC, c * 4, (r * u.nt1 + 1) * sDM) : 0.f;
+            };
+            Row ba[RB], bb[RB];
 #pragma unroll
-                for (int i = 0; i < RB; ++i) {
-                    const int r = rtop - i;
-                    if (r >= r0) {
-                        const Row &cur = bt[i];
-                        const Row &up = (i + 1 < RB) ? bt[i + 1] : nx[0];
-                        const bool below = r + 1 < n0;
-                        const int oDM = rowq(r) * sDM;
-                        const int slot0 = (r - r0) * TW;
-                        float gr = cur.gr;
-                        float er = right_tile ? exp2_fast(cur.dr1 * A1) : 0.f;
-                        bool right = right_tile;
+            for (int i = 0; i < RB; ++i) ld_ops(max(r1 - 1 - i, r0), ba[i]);
+            float htop[TW];
 #pragma unroll
-                        for (int jj = TW - 1; jj >= 0; --jj) {
-                            if (jj < je) {
-                                float g = cur.dy[jj] * cur.C[jj];
-                                if (below) g = fmaf(eb[jj], gb[jj], g);
-                                if (right) g = fmaf(er, gr, g);
-                                const float e0 = exp2_fast(cur.d0[jj] * A0), e1 = exp2_fast(cur.d1[jj] * A1);
-                                // Gradients of point (r, j0 + jj), as grad_finish.
-                                const float hp[2] = {r == r0 ? htop[jj] : up.h[jj], jj > 0 ? cur.h[jj - 1] : cur.hl};
-                                const bool has[2] = {r > 0, j0 + jj > 0};
-                                const float ea[2] = {e0, e1}, dl[2] = {cur.d0[jj], cur.d1[jj]};
-                                float dtb = dl[0];
-                                dtb += dl[1];
-                                dtb *= kInvNd;
-                                const float gbv = g * cur.B[jj];
-                                const float tx = channel_sum<MM>(gbv * dtb);
-                                const float tbv = gbv * cur.x[jj] * kInvNd;
-                                float td[2];
+            for (int jj = 0; jj < TW; ++jj) htop[jj] = r0 > 0 ? F::ld(rh, voDM[jj], rowq(r0 - 1) * sDM) : 0.f;
+            const long fb = static_cast<long>(s) * npen + t1;
+            if (ok && right_tile) ok = flow_wait(f.flags + (fb + 1) * ncg + cg, epoch, f.spin);
+            if (ok) {
 #pragma unroll
-                                for (int ax = 0; ax < 2; ++ax) {
-                                    float t = tbv;
-                                    if (has[ax]) {
-                                        const float gh = g * ea[ax] * hp[ax];
-                                        t = fmaf(gh, av[ax], tbv);
-                                        dAacc[ax] = fmaf(gh, dl[ax], dAacc[ax]);
+                for (int i = 0; i < RB; ++i) ld_succ(max(r1 - 1 - i, r0), ba[i]);
+                auto ld_batch = [&](int rtop, Row (&bt)[RB]) __attribute__((always_inline)) {
+#pragma unroll
+                    for (int i = 0; i < RB; ++i) {
+                        const int r = max(rtop - i, r0);
+                        ld_ops(r, bt[i]);
+                        ld_succ(r, bt[i]);
+                    }
+                };
+                auto do_batch = [&](int rtop, const Row (&bt)[RB], const Row (&nx)[RB]) __attribute__((always_inline)) {
+#pragma unroll
+                    for (int i = 0; i < RB; ++i) {
+                        const int r = rtop - i;
+                        if (r >= r0) {
+                            const Row &cur = bt[i];
+                            const Row &up = (i + 1 < RB) ? bt[i + 1] : nx[0];
+                            const bool below = r + 1 < n0;
+                            const int oDM = rowq(r) * sDM;
+                            const int slot0 = (r - r0) * TW;
+                            float gr = cur.gr;
+                            float er = right_tile ? exp2_fast(cur.dr1 * A1) : 0.f;
+                            bool right = right_tile;
+#pragma unroll
+                            for (int jj = TW - 1; jj >= 0; --jj) {
+                                if (jj < je) {
+                                    float g = cur.dy[jj] * cur.C[jj];
+                                    if (below) g = fmaf(eb[jj], gb[jj], g);
+                                    if (right) g = fmaf(er, gr, g);
+                                    const float e0 = exp2_fast(cur.d0[jj] * A0), e1 = exp2_fast(cur.d1[jj] * A1);
+                                    const float hp[2] = {r == r0 ? htop[jj] : up.h[jj], jj > 0 ? cur.h[jj - 1] : cur.hl};
+                                    const bool has[2] = {r > 0, j0 + jj > 0};
+                                    const float ea[2] = {e0, e1}, dl[2] = {cur.d0[jj], cur.d1[jj]};
+                                    float dtb = dl[0];
+                                    dtb += dl[1];
+                                    dtb *= kInvNd;
+                                    const float gbv = g * cur.B[jj];
+                                    const float tx = channel_sum<MM>(gbv * dtb);
+                                    const float tbv = gbv * cur.x[jj] * kInvNd;
+                                    float td[2];
+#pragma unroll
+                                    for (int ax = 0; ax < 2; ++ax) {
+                                        float t = tbv;
+                                        if (has[ax]) {
+                                            const float gh = g * ea[ax] * hp[ax];
+                                            t = fmaf(gh, av[ax], tbv);
+                                            dAacc[ax] = fmaf(gh, dl[ax], dAacc[ax]);
+                                        }
+                                        td[ax] = channel_sum<MM>(t);
                                     }
-                                    td[ax] = channel_sum<MM>(t);
+                                    F::st(rdC, voDM[jj], oDM, cur.dy[jj] * cur.h[jj]);
+                                    F::st(rg, voDM[jj], oDM, g * dtb * cur.x[jj]);
+                                    if (m == 0) {
+                                        st[(slot0 + jj) * CPW + lc] = tx;
+                                        st[(PTS + slot0 + jj) * CPW + lc] = td[0];
+                                        st[(2 * PTS + slot0 + jj) * CPW + lc] = td[1];
+                                    }
+                                    if (jj == 0) F::st(rgC, c * 4, r * u.nt1 * sDM, g);
+                                    gb[jj] = g;
+                                    eb[jj] = e0;
+                                    gr = g;
+                                    er = e1;
+                                    right = true;
                                 }
-                                F::st(gw.dC, voDM[jj], oDM, cur.dy[jj] * cur.h[jj]);
-                                F::st(gw.g, voDM[jj], oDM, g * dtb * cur.x[jj]);
-                                if (m == 0) {
-                                    st[(slot0 + jj) * CPW + lc] = tx;
-                                    st[(PTS + slot0 + jj) * CPW + lc] = td[0];
-                                    st[(2 * PTS + slot0 + jj) * CPW + lc] = td[1];
-                                }
-                                // The tile's first row and first column: the
-                                // states the tiles above and to the left read.
-                                if (r == r0) F::st(rgR, voDM[jj], j0 * sDM, g);
-                                if (jj == 0) F::st(rgC, gw.vc, (r - r0) * u.nt1 * sDM, g);
-                                gb[jj] = g;
-                                eb[jj] = e0;
-                                gr = g;
-                                er = e1;
-                                right = true;
                             }
                         }
                     }
+                };
+                for (int rt = r1 - 1; rt >= r0; rt -= 2 * RB) {
+                    ld_batch(rt - RB, bb);
+                    do_batch(rt, ba, bb);
+                    if (rt - RB >= r0) {
+                        ld_batch(rt - 2 * RB, ba);
+                        do_batch(rt - RB, bb, ba);
+                    }
                 }
-            };
-            for (int rt = r1 - 1; rt >= r0; rt -= 2 * RB) {
-                ld_batch(rt - RB, bb);
-                do_batch(rt, ba, bb);
-                if (rt - RB >= r0) {
-                    ld_batch(rt - 2 * RB, ba);
-                    do_batch(rt - RB, bb, ba);
-                }
+            } else {
+                const float qn = __builtin_nanf("");
+                for (int r = r0; r < r1; ++r)
+                    for (int jj = 0; jj < je; ++jj) {
+                        const int oDM = (rowq(r) + jj) * sDM;
+                        F::st(rdC, c * 4, oDM, qn);
+                        F::st(rg, c * 4, oDM, qn);
+                        if (m == 0)
+                            for (int k = 0; k < 3; ++k) st[(k * PTS + (r - r0) * TW + jj) * CPW + lc] = qn;
+                        if (jj == 0) F::st(rgC, c * 4, r * u.nt1 * sDM, qn);
+                    }
+                dAacc[0] = dAacc[1] = qn;
+                if (lane == 0) __hip_atomic_store(f.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-        } else {
-            // A wait ran out: NaN into this group's outputs, boundary states
-            // and stage slots, so every dependent tile and gradient is NaN.
-            const float qn = __builtin_nanf("");
-            for (int r = r0; r < r1; ++r)
-                for (int jj = 0; jj < je; ++jj) {
-                    const int oDM = rowq(r) * sDM + jj * sDM;
-                    F::st(gw.dC, gw.vc, oDM, qn);
-                    F::st(gw.g, gw.vc, oDM, qn);
-                    if (m == 0)
-                        for (int k = 0; k < 3; ++k) st[(k * PTS + (r - r0) * TW + jj) * CPW + lc] = qn;
-                    if (r == r0) F::st(rgR, gw.vc, (j0 + jj) * sDM, qn);
-                    if (jj == 0) F::st(rgC, gw.vc, (r - r0) * u.nt1 * sDM, qn);
-                }
-            dAacc[0] = dAacc[1] = qn;
-            if (lane == 0) __hip_atomic_store(f.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);   // this wave's stores acknowledged by L2
+            if (lane == 0)
+                __hip_atomic_store(f.flags + fb * ncg + cg, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            const long dch = static_cast<long>(cgr) * 64 / MM;
+            const GradWin fw = grad_window<2>(a, qb, qe, c, d, m, true);
+            grad_flush<2, MM, PTS>(fw, st, dch, a.D, [&](int sl) -> long {
+                const int rr = r0 + sl / TW, jj = sl % TW;
+                return (rr < r1 && jj < je) ? static_cast<long>(rowq(rr) + jj) : -1L;
+            });
         }
 #pragma unroll
-        for (int ax = 0; ax < 2; ++ax) a.part[(static_cast<long>(tl) * 2 + ax) * DM + c] = dAacc[ax];
-        __builtin_amdgcn_s_waitcnt(0);   // this wave's stores acknowledged by L2
-        if (lane == 0)
-            __hip_atomic_store(f.flags + static_cast<long>(tl) * ncg + cg, epoch, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        // dx / ddelta of the run's channels at the tile's points.
-        __syncthreads();
-        const long dch = static_cast<long>(cgr) * 64 / MM;
-        const GradWin fw = grad_window<2>(a, qb, qe, c, d, m, true);
-        grad_flush<2, MM, PTS>(fw, st, dch, a.D, [&](int sl) -> long {
-            const int rr = r0 + sl / TW, jj = sl % TW;
-            return (rr < r1 && jj < je) ? static_cast<long>(rowq(rr) + jj) : -1L;
-        });
+        for (int ax = 0; ax < 2; ++ax) a.part[(static_cast<long>(t1) * 2 + ax) * DM + c] = dAacc[ax];
     }
 }
 
@@ -1616,8 +1582,8 @@ struct NdBwdShape {
     size_t offs_bytes, nbr_bytes, part_bytes, tile_bytes;
     size_t flow_bytes;   // the adjoint dataflow's counters, status, epoch and flags (tiled sweeps)
     bool fused2;         // 2D with staged per-channel outputs: the fused dataflow backward may run
-    size_t gbd_bytes;    // its boundary states (gR, gC)
-    long fnt0, fnt1;     // its tiles per axis
+    size_t gbd_bytes;    // the fused backward's boundary states (2D: gC; 3D: gR, gC)
+    long fnt0, fnt1;     // its sub-tiles per pencil and pencils
     bool fused3;         // 3D: the fused pencil backward may run (boundary states in gbd_bytes)
     long f3nt1, f3nt2, f3nsub;   // its pencils per axis 1, 2 and sub-tiles per pencil
 };
@@ -1703,10 +1669,10 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
         s.tile_bytes = align_up(sizeof(int) * 3 * nt, 256);
     }
     s.part_bytes = sizeof(float) * (s.nbx + dA_chunks(s.nbx)) * s.nd * s.D * s.M;
-    // The fused 2D backward (nd_fused2d): per-channel outputs staged (4 <= M
-    // <= 32), windows of its tile's rows and of the boundary buffers below
-    // 2 GiB. It writes the boundary states of every tile (first row, first
-    // column) and a dA partial per tile.
+    // The fused 2D backward (nd_fused2p): per-channel outputs staged (4 <= M
+    // <= 32), windows of a sub-tile's rows and of the boundary buffer below
+    // 2 GiB. It writes the states of every pencil's first column and a dA
+    // partial per pencil.
     s.fused2 = false;
     s.gbd_bytes = 0;
     s.fnt0 = s.fnt1 = 0;
@@ -1715,11 +1681,11 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
         const long DM = s.D * s.M;
         s.fnt0 = (a->dims[0] + kAdjFTR - 1) / kAdjFTR;
         s.fnt1 = (a->dims[1] + kAdjFTW - 1) / kAdjFTW;
-        const double wr = 2.0 * a->dims[1] * DM * 4, wc = (static_cast<double>(kAdjFTR) * s.fnt1 + 2) * DM * 4;
-        if (wr < 2147483000.0 && wc < 2147483000.0) {
+        const double wc = static_cast<double>(a->dims[0]) * s.fnt1 * DM * 4;
+        if (wc < 2147483000.0) {
             s.fused2 = true;
-            s.gbd_bytes = align_up(sizeof(float) * (s.fnt0 * a->dims[1] + a->dims[0] * s.fnt1) * DM, 256);
-            const long nf = s.fnt0 * s.fnt1;
+            s.gbd_bytes = align_up(sizeof(float) * a->dims[0] * s.fnt1 * DM, 256);
+            const long nf = s.fnt1;
             s.part_bytes = std::max<size_t>(s.part_bytes, sizeof(float) * (nf + dA_chunks(nf)) * 2 * DM);
         }
     }
@@ -1755,6 +1721,10 @@ static bool nd_bwd_shape(const KMScanNDBwd *a, NdBwdShape &s) {
     }
     if (s.fused3) {
         const size_t nfl = static_cast<size_t>(s.f3nsub * s.f3nt1 * s.f3nt2) * (s.D * s.M / 64);
+        s.flow_bytes = std::max<size_t>(s.flow_bytes, align_up(4 * (kFlowHead + nfl), 256));
+    }
+    if (s.fused2) {   // 2D pencils: a flag per (sub-tile, pencil, channel group)
+        const size_t nfl = static_cast<size_t>(s.fnt0 * s.fnt1) * (s.D * s.M / 64);
         s.flow_bytes = std::max<size_t>(s.flow_bytes, align_up(4 * (kFlowHead + nfl), 256));
     }
     return true;
@@ -1845,6 +1815,25 @@ static int fused3_flow_setup(const NdBwdShape &s, hipStream_t st, FlowArgs &fa, 
         fa.band_start[b + 1] = fa.band_start[b] + (hi >= lo ? hi - lo + 1 : 0);
     }
     const long nfl = s.f3nsub * s.f3nt1 * s.f3nt2 * ncg;
+    if (nfl >= 0x7fffffffL) return 0;
+    if (ext) flow_zero(ext->buf, ext->cap, st);
+    int kind = 0;
+    const int bound = flow_bind(st, static_cast<size_t>(nfl), ext, fa, &kind);
+    note_flow(st, kind, kind == 2 ? fa.counter : nullptr);
+    return bound;
+}
+
+// The fused 2D pencils' dataflow state: pencils are taken right to left
+// (the kernel derives a pencil from its item), a flag per (sub-tile, pencil,
+// channel group).
+static int fused2p_flow_setup(const NdBwdShape &s, hipStream_t st, FlowArgs &fa, FlowBuf *ext) {
+    const long ncg = s.D * s.M / 64;
+    fa.nbands = 1;
+    for (int x = 0; x <= 8; ++x) fa.cg_lo[x] = static_cast<int>(static_cast<long>(x) * ncg / 8);
+    if (flow_q(fa) != kFlowQ) return 0;
+    fa.band_start[0] = 0;
+    fa.band_start[1] = static_cast<int>(s.fnt1);
+    const long nfl = s.fnt0 * s.fnt1 * ncg;
     if (nfl >= 0x7fffffffL) return 0;
     if (ext) flow_zero(ext->buf, ext->cap, st);
     int kind = 0;
@@ -1981,6 +1970,42 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
     // list to upload), else by tile bands.
     static thread_local km::FlowArgs fa;
     int nt[3] = {0, 0, 0};
+    // 2D on the dataflow schedule: the fused backward on pencils
+    // (KM_SCANND_BWD_FUSED=0: the adjoint sweep, then the gradient pass).
+    {
+        const char *fe = std::getenv("KM_SCANND_BWD_FUSED");
+        if (s.fused2 && km::flow_wanted(2) && !(fe && std::strcmp(fe, "0") == 0)) {
+            km::FlowBuf wf{reinterpret_cast<unsigned *>(ws + s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes),
+                           s.flow_bytes / 4, 8};
+            const int fbp = km::fused2p_flow_setup(s, st, fa, (a->workspace && s.flow_bytes) ? &wf : nullptr);
+            if (fbp < 0) return -1;
+            if (fbp > 0) {
+                float *gbd = reinterpret_cast<float *>(ws + s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes +
+                                                       s.flow_bytes);
+                const long DM = s.D * s.M;
+                km::Fused2PArgs u{gbd, static_cast<int>(s.fnt1), static_cast<int>(s.fnt0)};
+                long per_xcd = 0;
+                for (int x = 0; x < 8; ++x)
+                    per_xcd = std::max<long>(per_xcd, s.fnt1 * ((fa.cg_lo[x + 1] - fa.cg_lo[x]) / km::kFlowQ));
+                const dim3 grid(static_cast<unsigned>(8 * std::min<long>(per_xcd, 256 / km::kFlowQ)));
+                const dim3 blk(64 * km::kFlowQ);
+                switch (s.M) {
+                case 4: hipLaunchKernelGGL((km::nd_fused2p<km::kAdjFTR, km::kAdjFTW, 2, 4>), grid, blk, 0, st, args, fa, u); break;
+                case 8: hipLaunchKernelGGL((km::nd_fused2p<km::kAdjFTR, km::kAdjFTW, 2, 8>), grid, blk, 0, st, args, fa, u); break;
+                case 16: hipLaunchKernelGGL((km::nd_fused2p<km::kAdjFTR, km::kAdjFTW, 2, 16>), grid, blk, 0, st, args, fa, u); break;
+                default: hipLaunchKernelGGL((km::nd_fused2p<km::kAdjFTR, km::kAdjFTW, 2, 32>), grid, blk, 0, st, args, fa, u); break;
+                }
+                km::sum_dA(args.part, a->dA, s.fnt1, 2 * DM, st);
+                if (plan) km_wavefront_plan_free(plan);
+                const hipError_t e = hipGetLastError();
+                if (e != hipSuccess) {
+                    km::set_error("km_scannd_bwd: launch failed: %s", hipGetErrorString(e));
+                    return -1;
+                }
+                return 0;
+            }
+        }
+    }
     // 3D on the dataflow schedule: the fused pencil backward (adjoint state
     // and gradients in one launch; KM_SCANND_BWD_FUSED=0: two passes).
     const char *fe3 = std::getenv("KM_SCANND_BWD_FUSED");
@@ -2027,36 +2052,7 @@ int km_scannd_bwd(const KMScanNDBwd *a, void *stream) {
     }
     if (fb == 0) km::note_flow(st, 0);
     const km::FlowArgs *flow = fb > 0 ? &fa : nullptr;
-    // 2D on the dataflow schedule with workgroups of kFlowQ groups: the
-    // adjoint state and the gradients in one fused launch (KM_SCANND_BWD_FUSED=0:
-    // the adjoint sweep, then the gradient pass).
-    const char *fe = std::getenv("KM_SCANND_BWD_FUSED");
-    if (flow && s.fused2 && km::flow_q(fa) == km::kFlowQ && !(fe && std::strcmp(fe, "0") == 0)) {
-        float *gbd = reinterpret_cast<float *>(ws + s.offs_bytes + s.nbr_bytes + s.part_bytes + s.tile_bytes +
-                                               s.flow_bytes);
-        const long DM = s.D * s.M;
-        km::Fused2Args u{gbd, gbd + s.fnt0 * a->dims[1] * DM, static_cast<int>(s.fnt0), static_cast<int>(s.fnt1)};
-        const long ntiles = fa.band_start[fa.nbands];
-        long per_xcd = 0;
-        for (int x = 0; x < 8; ++x)
-            per_xcd = std::max<long>(per_xcd, ntiles * ((fa.cg_lo[x + 1] - fa.cg_lo[x]) / km::kFlowQ));
-        const dim3 grid(static_cast<unsigned>(8 * std::min<long>(per_xcd, 256 / km::kFlowQ)));
-        const dim3 blk(64 * km::kFlowQ);
-        switch (s.M) {
-        case 4: hipLaunchKernelGGL((km::nd_fused2d<km::kAdjFTR, km::kAdjFTW, 2, 4>), grid, blk, 0, st, args, fa, u); break;
-        case 8: hipLaunchKernelGGL((km::nd_fused2d<km::kAdjFTR, km::kAdjFTW, 2, 8>), grid, blk, 0, st, args, fa, u); break;
-        case 16: hipLaunchKernelGGL((km::nd_fused2d<km::kAdjFTR, km::kAdjFTW, 2, 16>), grid, blk, 0, st, args, fa, u); break;
-        default: hipLaunchKernelGGL((km::nd_fused2d<km::kAdjFTR, km::kAdjFTW, 2, 32>), grid, blk, 0, st, args, fa, u); break;
-        }
-        km::sum_dA(args.part, a->dA, s.fnt0 * s.fnt1, 2 * DM, st);
-        if (plan) km_wavefront_plan_free(plan);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) {
-            km::set_error("km_scannd_bwd: launch failed: %s", hipGetErrorString(e));
-            return -1;
-        }
-        return 0;
-    }
+
     // 3D tile bands: each band's tiles (tile-index sum b), bands contiguous.
     std::vector<int> tl;
     std::vector<long> bstart;
