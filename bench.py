@@ -406,8 +406,10 @@ def scannd_bwd_alg_bytes(dims, D, M):
 
 def bench_scannd_bwd(torch, K, stream, dims, D, M, steps, warmup):
     """The ScanND backward on the configs[2] grids and inputs (h from the
-    forward, dy ~ N(0, 1)): one launch per anti-diagonal level for the
-    adjoint state, then the gradient and dA launches."""
+    forward, dy ~ N(0, 1)): on an 8-XCD device one dataflow launch on
+    pencils forming the adjoint state and every gradient, then the two
+    fixed-order dA sums (KM_SCANND_BWD_FUSED=0: the adjoint sweep, then the
+    gradient pass). Wall time per backward over the timed launches."""
     nd = len(dims)
     P = 1
     for v in dims:
@@ -430,7 +432,9 @@ def bench_scannd_bwd(torch, K, stream, dims, D, M, steps, warmup):
     alg = scannd_bwd_alg_bytes(dims, D, M)
     return {"ms": round(ms, 4), "elems_per_s": P * D / (ms * 1e-3),
             "achieved_GBs": round(alg / (ms * 1e-3) / 1e9, 1),
-            "frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "alg_bytes": alg}
+            "frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "alg_bytes": alg,
+            "launches": ("fused pencil launch + dA sums" if os.environ.get("KM_SCANND_BWD_FUSED") != "0"
+                         else "adjoint sweep + gradient pass + dA sums")}
 
 
 def make_inputs(torch, Bsz, L, D, N, dtype, seed=0):
