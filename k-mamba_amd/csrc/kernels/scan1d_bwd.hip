@@ -28,8 +28,10 @@
 //    rows and columns (N = 16) or a reduce-scatter over the wave's lanes
 //    gives the wave's channel-group sum, stored to the workgroup's own
 //    partial slot; a finalize kernel adds the slots of every channel group
-//    (and dA's per-batch partials) in a fixed order. No atomics: every
-//    output is identical run to run.
+//    (and dA's per-batch partials) in a fixed order. With N = 16 a
+//    workgroup runs two such 8-wave halves on 16 channels each and adds
+//    their sums in LDS, so its slot covers 32 channels (half the slots to
+//    write and to sum). No atomics: every output is identical run to run.
 //  * States recomputed from checkpoints run unclamped; if any leaves
 //    [-1000, 1000] the workgroup re-runs every super-chunk with the
 //    sequential clamped recurrence, which matches the forward's clamp
@@ -145,8 +147,17 @@ __device__ __forceinline__ void pow_chain_b(float e1, int n0, float (&e)[NPL]) {
 // block: each step's products are written as rows, and every two steps
 // each lane adds one (step, gradient, state) column over the wave's 16
 // channels in channel order. Other N use the in-wave reduce-scatter.
+// With N = 16 the workgroup is 16 waves, two halves of W = 8 on channels
+// [32 g, +16) and [32 g + 16, +16) of the same steps: they share the
+// staged B / C tiles and the barriers, keep their maps, folds and carries
+// in their own halves of the LDS arrays (lane index lane + 64 * half), and
+// leave their column sums in comb; after the next barrier each half adds
+// the two halves' sums of one round of every wave's steps (half 0's first)
+// and stores them to the slot. The LDS then holds one workgroup per CU
+// (16 waves, as two 8-wave workgroups did).
 template <typename T, int NPL, int NS, bool SHARED, bool HIN>
-__global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
+__global__ void __launch_bounds__((SHARED && NPL * NS == 16 && NS == 4) ? 1024 : 512, 4)
+scan1d_bwd_chunked(Scan1DBwdArgs p) {
     using IO = bio<T>;
     constexpr int W = 8, TC = 4;
     constexpr int DL = 64 / NS;
@@ -155,7 +166,11 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
     static_assert(SC == kCkptSteps, "backward super-chunks follow the forward checkpoints");
     static_assert(2 * NPL <= W, "one fold per wave");
     constexpr int TILE = SC * N;
-    constexpr int NT = 64 * W;
+    // The LDS channel sums (N = 16, shared B/C) run two halves of 8 waves in
+    // one workgroup, each half on its own 16 channels: the halves' sums are
+    // added in LDS, so a workgroup's slot covers 32 channels.
+    constexpr int HW = (SHARED && N == 16 && NS == 4) ? 2 : 1;
+    constexpr int NT = 64 * W * HW;
     constexpr int TPT = (TILE + NT - 1) / NT;
     constexpr int TS = IO::size;
     // LDS channel sums (N = 16): RS = 2 steps per round, 2 gradients, 16
@@ -180,11 +195,15 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int w = __builtin_amdgcn_readfirstlane((tid >> 6) & (W - 1));   // wave of the half
+    const int hh = HW > 1 ? __builtin_amdgcn_readfirstlane(tid >> 9) : 0; // half
+    // Lane index into the per-half LDS arrays ([..][64 * HW]): one address
+    // register serves every array, as the lane alone does with one half.
+    const int lh = lane + 64 * hh;
     const int dl = lane % DL;
     const int ns = lane / DL;
     const int n0 = ns * NPL;
-    const long ngroups = (p.D + DL - 1) / DL;
+    const long ngroups = (p.D + DL * HW - 1) / (DL * HW);
     // Workgroups numbered so that consecutive channel groups run on one
     // XCD: a group's DL channels are only part of each 128-byte row line
     // of x / delta / dy, and the neighbours that read the rest of the line
@@ -192,7 +211,7 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
     const long wg = xcd_remap(blockIdx.x, gridDim.x);
     const long b = wg / ngroups;
     const long grp = wg - b * ngroups;
-    const long d = grp * DL + dl;
+    const long d = grp * DL * HW + hh * DL + dl;
     const bool dvalid = d < p.D;
     const int dc = static_cast<int>(dvalid ? d : p.D - 1);
     const int L = static_cast<int>(p.L);
@@ -244,12 +263,13 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
 
     __shared__ float sB[SHARED ? 3 : 1][SHARED ? TILE : 1];
     __shared__ float sC[SHARED ? 3 : 1][SHARED ? TILE : 1];
-    __shared__ float aggP[W][NPL][64];                 // chunk decay products
-    __shared__ float aggF[HIN ? 1 : W][NPL][64];       // forward maps, then incoming states
-    __shared__ float aggA[W][NPL][64];                 // adjoint maps, then incoming adjoints
-    __shared__ float lmx[HIN ? 1 : W][64];             // max |local state| (inf: no bound)
-    __shared__ float acar[2][NPL][64];                 // adjoint carried between super-chunks
-    __shared__ __align__(16) float red[LRED ? W : 1][RWAVE];
+    __shared__ float aggP[W][NPL][64 * HW];            // chunk decay products
+    __shared__ float aggF[HIN ? 1 : W][NPL][64 * HW];  // forward maps, then incoming states
+    __shared__ float aggA[W][NPL][64 * HW];            // adjoint maps, then incoming adjoints
+    __shared__ float lmx[HIN ? 1 : W][64 * HW];        // max |local state| (inf: no bound)
+    __shared__ float acar[2][NPL][64 * HW];            // adjoint carried between super-chunks
+    __shared__ __align__(16) float red[LRED ? W * HW : 1][RWAVE];
+    __shared__ float comb[HW > 1 ? W : 1][2][64 * HW]; // the halves' channel sums of a super-chunk
     __shared__ int s_bad;                              // some bound failed: clamped re-run
 
     // Decays exp2((delta * log2 e) * A): the first product once per step.
@@ -287,7 +307,7 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
 
     if (w == 0) {
 #pragma unroll
-        for (int j = 0; j < NPL; ++j) acar[0][j][lane] = 0.f;
+        for (int j = 0; j < NPL; ++j) acar[0][j][lh] = 0.f;
     }
     if (tid == 0) s_bad = 0;
 
@@ -416,10 +436,10 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
                 }
             }
 #pragma unroll
-            for (int j = 0; j < NPL; ++j) aggF[w][j][lane] = hl[j];
+            for (int j = 0; j < NPL; ++j) aggF[w][j][lh] = hl[j];
             // |h| <= |h_in| + |local state| holds while every decay is <= 1
             // (A <= 0, delta >= 0); otherwise no bound (inf).
-            lmx[w][lane] = (apos || !(dmin >= 0.f)) ? __builtin_inff() : lm;
+            lmx[w][lh] = (apos || !(dmin >= 0.f)) ? __builtin_inff() : lm;
         }
         float g[NPL];
 #pragma unroll
@@ -433,8 +453,8 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
         }
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
-            aggP[w][j][lane] = P[j];
-            aggA[w][j][lane] = g[j];
+            aggP[w][j][lh] = P[j];
+            aggA[w][j][lh] = g[j];
         }
     };
 
@@ -449,15 +469,15 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
             float pv[W], hv[W], mv[W];
 #pragma unroll
             for (int v = 0; v < W; ++v) {
-                pv[v] = aggP[v][j][lane];
-                hv[v] = aggF[v][j][lane];
-                mv[v] = lmx[v][lane];
+                pv[v] = aggP[v][j][lh];
+                hv[v] = aggF[v][j][lh];
+                mv[v] = lmx[v][lh];
             }
             float run = ks;
             bool bad = false;
 #pragma unroll
             for (int v = 0; v < W; ++v) {
-                aggF[v][j][lane] = run;
+                aggF[v][j][lh] = run;
                 bad = bad || !(fabsf(run) + mv[v] <= 1000.f);
                 run = fmaf(pv[v], run, hv[v]);
             }
@@ -468,16 +488,16 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
             float pv[W], gv[W];
 #pragma unroll
             for (int v = 0; v < W; ++v) {
-                pv[v] = aggP[v][j][lane];
-                gv[v] = aggA[v][j][lane];
+                pv[v] = aggP[v][j][lh];
+                gv[v] = aggA[v][j][lh];
             }
-            float run = acar[cur][j][lane];
+            float run = acar[cur][j][lh];
 #pragma unroll
             for (int v = W - 1; v >= 0; --v) {
-                aggA[v][j][lane] = run;
+                aggA[v][j][lh] = run;
                 run = fmaf(pv[v], run, gv[v]);
             }
-            acar[cur ^ 1][j][lane] = run;
+            acar[cur ^ 1][j][lh] = run;
         }
     };
 
@@ -493,8 +513,8 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
         const int t0 = s * SC + w * TC;
         float g[NPL];
 #pragma unroll
-        for (int j = 0; j < NPL; ++j) g[j] = aggA[w][j][lane];
-        float *rw = &red[LRED ? w : 0][0];
+        for (int j = 0; j < NPL; ++j) g[j] = aggA[w][j][lh];
+        float *rw = &red[LRED ? hh * W + w : 0][0];
 #pragma unroll
         for (int k = TC - 1; k >= 0; --k) {
             // One step at a time: operand reads of later steps hoisted here
@@ -511,7 +531,7 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
 #pragma unroll
             for (int j = 0; j < NPL; ++j) {
                 const float ah = fmaf(gk, cv[j], g[j]);
-                const float hp = (k > 0) ? hs[k - 1][j] : HIN_LDS ? aggF[HIN ? 0 : w][j][lane] : hin[j];
+                const float hp = (k > 0) ? hs[k - 1][j] : HIN_LDS ? aggF[HIN ? 0 : w][j][lh] : hin[j];
                 const float ae = ah * e[k][j];
                 const float q = ae * hp;
                 dAacc[j] = fmaf(dtk, q, dAacc[j]);
@@ -564,8 +584,14 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
                     float acc = col[0] * cvec[0];
 #pragma unroll
                     for (int c = 1; c < DL; ++c) acc = fmaf(col[c * NPL], cvec[c], acc);
-                    const int tt = t + RS - 1 - ri;
-                    bio<f32_t>::st(rslot, ((tt * 2 + gi) * N + ni) * 4, 0, acc);
+                    if constexpr (HW > 1) {
+                        // Round (TC - RS - k) / RS of the super-chunk's
+                        // steps: slotted by comb_flush after the next barrier.
+                        comb[w][(TC - RS - k) / RS][lh] = acc;
+                    } else {
+                        const int tt = t + RS - 1 - ri;
+                        bio<f32_t>::st(rslot, ((tt * 2 + gi) * N + ni) * 4, 0, acc);
+                    }
                 }
             } else if constexpr (SHARED) {
                 float dBv[NPL], dCv[NPL];
@@ -592,6 +618,18 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
         }
     };
 
+    // The two halves' channel sums of super-chunk s (written in comb by the
+    // replay, read after a barrier): half hh slots round hh of each wave's
+    // steps, half 0's sum plus half 1's, in that order.
+    auto comb_flush = [&](int s) __attribute__((always_inline)) {
+        if constexpr (HW > 1) {
+            const int rnd = hh;
+            const int tt = s * SC + w * TC + (TC - RS - rnd * RS) + RS - 1 - ri;
+            const float v = comb[w][rnd][lane] + comb[w][rnd][lane + 64];
+            bio<f32_t>::st(rslot, ((tt * 2 + gi) * N + ni) * 4, 0, v);
+        }
+    };
+
     // One super-chunk of the main pass: the forward states come from the
     // history (HIN) or from the checkpoint by local pass, fold and replay,
     // unclamped; the next super-chunk's operands are prefetched.
@@ -610,6 +648,7 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
         float e[TC][NPL];
         phase_a(std::integral_constant<bool, !HIN>{}, s, slot, xs, ds, gs, e);
         __syncthreads();
+        if (it > 0) comb_flush(s + 1);
         phase_f(std::integral_constant<bool, !HIN>{}, cur, ks);
         __syncthreads();
         const int t0 = s * SC + w * TC;
@@ -635,7 +674,7 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
                 const float u = ds[k] * xs[k];
 #pragma unroll
                 for (int j = 0; j < NPL; ++j)
-                    hs[k][j] = fmaf(e[k][j], (k == 0) ? aggF[HIN ? 0 : w][j][lane] : hs[k - 1][j],
+                    hs[k][j] = fmaf(e[k][j], (k == 0) ? aggF[HIN ? 0 : w][j][lh] : hs[k - 1][j],
                                     bv[j] * u);
             }
         }
@@ -650,6 +689,7 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
         const int s = nit - 1 - it;
         const int cur = it & 1;
         __syncthreads();                 // the previous super-chunk's tile reads are done
+        if (it > 0) comb_flush(s + 1);
         if constexpr (SHARED) {
             load_tile(s);
             store_tile(0);
@@ -702,18 +742,21 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
         body(it, X0, D0, G0, K0, X1, D1, G1, K1);
         if (it + 1 < nit) body(it + 1, X1, D1, G1, K1, X0, D0, G0, K0);
     }
+    __syncthreads();
+    comb_flush(0);
     if constexpr (!HIN) {
         // Some super-chunk's states may have left [-1000, 1000]: every
         // output of this workgroup again, with the clamped states.
-        __syncthreads();
         if (__builtin_amdgcn_readfirstlane(s_bad) != 0) {
 #pragma unroll
             for (int j = 0; j < NPL; ++j) dAacc[j] = 0.f;
             if (w == 0) {
 #pragma unroll
-                for (int j = 0; j < NPL; ++j) acar[0][j][lane] = 0.f;
+                for (int j = 0; j < NPL; ++j) acar[0][j][lh] = 0.f;
             }
             for (int it = 0; it < nit; ++it) body_rerun(it);
+            __syncthreads();
+            comb_flush(0);
         }
     }
 
@@ -721,14 +764,14 @@ __global__ void __launch_bounds__(512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
     // store per (batch, channel, state).
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) aggA[w][j][lane] = dAacc[j];
+    for (int j = 0; j < NPL; ++j) aggA[w][j][lh] = dAacc[j];
     __syncthreads();
     if (w == 0 && dvalid) {
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
-            float acc = aggA[0][j][lane];
+            float acc = aggA[0][j][lh];
 #pragma unroll
-            for (int v = 1; v < W; ++v) acc += aggA[v][j][lane];
+            for (int v = 1; v < W; ++v) acc += aggA[v][j][lh];
             p.dApart[(b * Dm + d) * N + n0 + j] = acc;
         }
     }
@@ -868,8 +911,8 @@ struct BwdPlan {
 };
 
 // Channels per workgroup of the register-blocked backward for a state size.
-static long bwd_group_channels(long N) {
-    if (N == 16) return 16;
+static long bwd_group_channels(long N, bool shared) {
+    if (N == 16) return shared ? 32 : 16;   // shared B/C: two 16-channel halves
     if (N == 8) return 32;
     return 64;
 }
@@ -886,7 +929,7 @@ static BwdPlan bwd_plan(const KMScan1DBwd *k) {
     pl.hist_in = (k->h_hist != nullptr);
     pl.need_hist = pl.serial && !pl.hist_in;
     pl.need_ckpt = !pl.serial && !pl.hist_in && !k->h_ckpt;
-    const long gc = pl.serial ? kSerialNB : bwd_group_channels(k->N);
+    const long gc = pl.serial ? kSerialNB : bwd_group_channels(k->N, pl.shared);
     pl.G = (k->D + gc - 1) / gc;
     size_t off = 0;
     pl.off_slots = off;
@@ -932,13 +975,14 @@ static bool bwd_args_ok(const KMScan1DBwd *k, const char *who) {
 static int bwd_chunked_launch(const Scan1DBwdArgs &a, bool shared, bool hin, bool bf,
                               hipStream_t s) {
     constexpr int W = 8;
-    const long DL = bwd_group_channels(a.N);
+    const long DL = bwd_group_channels(a.N, shared);
+    const int HW = (shared && a.N == 16) ? 2 : 1;   // the kernel's two halves (LDS sums)
     const long grid = a.B * ((a.D + DL - 1) / DL);
     if (grid <= 0 || grid > 0x7fffffffL) {
         set_error("km_scan1d_bwd: grid of %ld workgroups out of range", grid);
         return -1;
     }
-    dim3 g(static_cast<unsigned>(grid)), blk(64 * W);
+    dim3 g(static_cast<unsigned>(grid)), blk(64 * W * HW);
 #define KM_BWD_GO(TT, NPL, NS)                                                                    \
     do {                                                                                          \
         if (shared) {                                                                             \
