@@ -865,28 +865,59 @@ __global__ void __launch_bounds__(256) fill_zero_kernel(float *p, long n) {
 // (b ascending); with shared B/C, dB / dC at b*sb + t*st + n = sum over the
 // channel groups g (ascending) of slot[b, g, t, 0 / 1, n].
 template <typename T>
+// With q4 (N a multiple of 4) a thread sums four consecutive states with
+// 16-byte loads, four groups' loads in flight before their adds; each
+// state's sum still adds the groups in ascending order.
 __global__ void __launch_bounds__(256) scan1d_bwd_finalize(const float *slot, long G, void *dB,
                                                            void *dC, long B, long L, long N,
                                                            long sb, long st, const float *dApart,
-                                                           float *dA, long DN) {
+                                                           float *dA, long DN, int q4) {
     using IO = io<T>;
-    const long n_bc = slot ? B * L * N : 0;
-    const long LN = L * N;
-    const long S = 2 * LN;   // floats per (b, g) slot
+    const long Q = q4 ? 4 : 1;                 // states per thread
+    const long Nq = N / Q;
+    const long n_bc = slot ? B * L * Nq : 0;
+    const long LNq = L * Nq;
+    const long S = 2 * L * N;   // floats per (b, g) slot
     const long stride = static_cast<long>(gridDim.x) * blockDim.x;
     for (long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_bc + DN;
          i += stride) {
         if (i < n_bc) {
-            const long b = i / LN, r = i - b * LN, t = r / N, n = r - t * N;
+            const long b = i / LNq, r = i - b * LNq, t = r / Nq, n = (r - t * Nq) * Q;
             const float *pb = slot + b * G * S + t * 2 * N + n;
-            float sB = 0.f, sC = 0.f;
-            for (long g = 0; g < G; ++g) {
-                sB += pb[g * S];
-                sC += pb[g * S + N];
-            }
             const long o = b * sb + t * st + n;
-            IO::st(dB, o, sB);
-            IO::st(dC, o, sC);
+            if (q4) {
+                float4 aB = make_float4(0.f, 0.f, 0.f, 0.f), aC = aB;
+                long g = 0;
+                for (; g + 4 <= G; g += 4) {
+                    float4 vB[4], vC[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        vB[u] = *reinterpret_cast<const float4 *>(pb + (g + u) * S);
+                        vC[u] = *reinterpret_cast<const float4 *>(pb + (g + u) * S + N);
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        aB.x += vB[u].x; aB.y += vB[u].y; aB.z += vB[u].z; aB.w += vB[u].w;
+                        aC.x += vC[u].x; aC.y += vC[u].y; aC.z += vC[u].z; aC.w += vC[u].w;
+                    }
+                }
+                for (; g < G; ++g) {
+                    const float4 vB = *reinterpret_cast<const float4 *>(pb + g * S);
+                    const float4 vC = *reinterpret_cast<const float4 *>(pb + g * S + N);
+                    aB.x += vB.x; aB.y += vB.y; aB.z += vB.z; aB.w += vB.w;
+                    aC.x += vC.x; aC.y += vC.y; aC.z += vC.z; aC.w += vC.w;
+                }
+                IO::st(dB, o, aB.x); IO::st(dB, o + 1, aB.y); IO::st(dB, o + 2, aB.z); IO::st(dB, o + 3, aB.w);
+                IO::st(dC, o, aC.x); IO::st(dC, o + 1, aC.y); IO::st(dC, o + 2, aC.z); IO::st(dC, o + 3, aC.w);
+            } else {
+                float sB = 0.f, sC = 0.f;
+                for (long g = 0; g < G; ++g) {
+                    sB += pb[g * S];
+                    sC += pb[g * S + N];
+                }
+                IO::st(dB, o, sB);
+                IO::st(dC, o, sC);
+            }
         } else {
             const long k = i - n_bc;
             float acc = 0.f;
@@ -1079,12 +1110,16 @@ static int scan1d_bwd_run(const KMScan1DBwd *k, const BwdPlan &pl, bool bf, hipS
     } else if (bwd_chunked_launch(a, pl.shared, a.hist != nullptr, bf, stream) != 0) {
         return -1;
     }
-    const long n = (pl.shared ? k->B * k->L * k->N : 0) + k->D * k->N;
+    // Slots hold whole [L, 2, N] rows from the workspace's slot offset: with
+    // N % 4 == 0 and that offset 16-byte aligned (a caller's workspace may
+    // not be), every thread's four states are.
+    const int q4 = (k->N % 4 == 0 && (reinterpret_cast<uintptr_t>(a.slot) & 15) == 0) ? 1 : 0;
+    const long n = (pl.shared ? k->B * k->L * k->N / (q4 ? 4 : 1) : 0) + k->D * k->N;
     const long blocks = std::min<long>((n + 255) / 256, 8192);
 #define KM_FIN(TT)                                                                                 \
     hipLaunchKernelGGL(scan1d_bwd_finalize<TT>, dim3(blocks), dim3(256), 0, stream, a.slot,       \
                        pl.G, k->dB, k->dC, k->B, k->L, k->N, k->bc_sb, k->bc_st,                  \
-                       a.dApart, k->dA, k->D * k->N)
+                       a.dApart, k->dA, k->D * k->N, q4)
     if (bf) KM_FIN(bf16_t);
     else    KM_FIN(f32_t);
 #undef KM_FIN
