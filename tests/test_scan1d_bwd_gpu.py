@@ -86,8 +86,12 @@ def dy_for(Bsz, L, D, seed=5):
 @pytest.mark.parametrize("mode", ["hist", "ckpt", "recompute"])
 @pytest.mark.parametrize("Bsz,L,D,N", [(2, 200, 48, 16), (1, 64, 16, 16), (2, 130, 64, 8),
                                        (1, 77, 100, 4), (2, 65, 64, 2), (1, 300, 65, 1),
-                                       (2, 50, 40, 3), (3, 1, 32, 16), (1, 129, 33, 16)])
+                                       (2, 50, 40, 3), (3, 1, 32, 16), (1, 129, 33, 16),
+                                       (2, 31, 17, 16), (1, 96, 200, 16)])
 def test_shared_bc_vs_oracle(Bsz, L, D, N, mode):
+    # N = 16 runs 32-channel workgroups of two 16-channel halves: D = 17,
+    # 33 and 200 leave the second half of the last group partly or wholly
+    # past D; L = 1 and 31 give one partial super-chunk.
     x, dt, A, Bm, Cm = scan1d_inputs(Bsz, L, D, N, seed=11)
     dy = dy_for(Bsz, L, D)
     ref, hh = oracle_bwd(x, dt, A, Bm, Cm, dy)

@@ -449,12 +449,12 @@ FUSED_CASES = [((43, 37), 128, 16), ((17, 70), 256, 8), ((9, 5), 512, 4), ((25, 
 def test_backward_fused_2d_matches_two_pass(dims, D, M, monkeypatch):
     # Grids whose channel groups fill workgroups of four per XCD (D*M a
     # multiple of 2048) run the fused backward: the adjoint state and every
-    # gradient in one dataflow launch (2D tiles; 3D pencils through every
-    # plane in sub-tiles of 4 planes), only the boundary states stored.
+    # gradient in one dataflow launch (2D pencils of 4 columns through every
+    # row in sub-tiles of 8 rows; 3D pencils of 4 x 4 columns through every
+    # plane in sub-tiles of 2 planes), only the boundary states stored.
     # KM_SCANND_BWD_FUSED=0 runs the adjoint sweep, then the gradient pass:
     # the same arithmetic at every point, so dx, ddelta, dB and dC agree bit
-    # for bit; dA adds its terms per tile or sub-tile and agrees to
-    # rounding. Covers partial tiles, pencils and sub-tiles on every axis,
+    # for bit; dA adds its terms per pencil and agrees to rounding. Covers partial tiles, pencils and sub-tiles on every axis,
     # M = 4 to 32 (3D: 8 to 32).
     x, A, B, Cm, dt, h, dy = bwd_inputs(dims, D, M, 5)
     a = run_bwd(dims, x, A, B, Cm, dt, h, dy)
