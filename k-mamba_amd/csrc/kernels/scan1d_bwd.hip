@@ -28,14 +28,17 @@
 //    rows and columns (N = 16) or a reduce-scatter over the wave's lanes
 //    gives the wave's channel-group sum, stored to the workgroup's own
 //    partial slot; a finalize kernel adds the slots of every channel group
-//    (and dA's per-batch partials) in a fixed order. With N = 16 a
-//    workgroup runs two such 8-wave halves on 16 channels each and adds
-//    their sums in LDS, so its slot covers 32 channels (half the slots to
-//    write and to sum). No atomics: every output is identical run to run.
+//    (and dA's per-batch partials) in a fixed order. With N = 16, on grids
+//    large enough to give every CU a workgroup, a workgroup runs two such
+//    8-wave halves on 16 channels each and adds their sums in LDS, so its
+//    slot covers 32 channels (half the slots to write and to sum). No
+//    atomics: every output is identical run to run.
 //  * States recomputed from checkpoints run unclamped; if any leaves
 //    [-1000, 1000] the workgroup re-runs every super-chunk with the
 //    sequential clamped recurrence, which matches the forward's clamp
 //    fallback.
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "km_device.hpp"
@@ -147,7 +150,7 @@ __device__ __forceinline__ void pow_chain_b(float e1, int n0, float (&e)[NPL]) {
 // block: each step's products are written as rows, and every two steps
 // each lane adds one (step, gradient, state) column over the wave's 16
 // channels in channel order. Other N use the in-wave reduce-scatter.
-// With N = 16 the workgroup is 16 waves, two halves of W = 8 on channels
+// With HWT = 2 the workgroup is 16 waves, two halves of W = 8 on channels
 // [32 g, +16) and [32 g + 16, +16) of the same steps: they share the
 // staged B / C tiles and the barriers, keep their maps, folds and carries
 // in their own halves of the LDS arrays (lane index lane + 64 * half), and
@@ -155,9 +158,8 @@ __device__ __forceinline__ void pow_chain_b(float e1, int n0, float (&e)[NPL]) {
 // the two halves' sums of one round of every wave's steps (half 0's first)
 // and stores them to the slot. The LDS then holds one workgroup per CU
 // (16 waves, as two 8-wave workgroups did).
-template <typename T, int NPL, int NS, bool SHARED, bool HIN>
-__global__ void __launch_bounds__((SHARED && NPL * NS == 16 && NS == 4) ? 1024 : 512, 4)
-scan1d_bwd_chunked(Scan1DBwdArgs p) {
+template <typename T, int NPL, int NS, bool SHARED, bool HIN, int HWT>
+__global__ void __launch_bounds__(HWT == 2 ? 1024 : 512, 4) scan1d_bwd_chunked(Scan1DBwdArgs p) {
     using IO = bio<T>;
     constexpr int W = 8, TC = 4;
     constexpr int DL = 64 / NS;
@@ -166,10 +168,11 @@ scan1d_bwd_chunked(Scan1DBwdArgs p) {
     static_assert(SC == kCkptSteps, "backward super-chunks follow the forward checkpoints");
     static_assert(2 * NPL <= W, "one fold per wave");
     constexpr int TILE = SC * N;
-    // The LDS channel sums (N = 16, shared B/C) run two halves of 8 waves in
-    // one workgroup, each half on its own 16 channels: the halves' sums are
-    // added in LDS, so a workgroup's slot covers 32 channels.
-    constexpr int HW = (SHARED && N == 16 && NS == 4) ? 2 : 1;
+    // HWT = 2 (LDS channel sums: N = 16, shared B/C): two halves of 8 waves
+    // in one workgroup, each half on its own 16 channels; the halves' sums
+    // are added in LDS, so a workgroup's slot covers 32 channels.
+    constexpr int HW = HWT;
+    static_assert(HW == 1 || (HW == 2 && SHARED && N == 16 && NS == 4), "two halves: LDS channel sums");
     constexpr int NT = 64 * W * HW;
     constexpr int TPT = (TILE + NT - 1) / NT;
     constexpr int TS = IO::size;
@@ -937,15 +940,29 @@ static int fill_zero(float *p, long n, hipStream_t s) {
 
 struct BwdPlan {
     bool shared, hist_in, need_ckpt, serial, need_hist;
+    bool wide;              // N = 16 shared B/C on 32-channel workgroups (two halves)
     long G;                 // channel groups per batch element (partial slots)
     size_t off_slots, off_dA, off_ckpt, off_hist, bytes;
 };
 
 // Channels per workgroup of the register-blocked backward for a state size.
-static long bwd_group_channels(long N, bool shared) {
-    if (N == 16) return shared ? 32 : 16;   // shared B/C: two 16-channel halves
+static long bwd_group_channels(long N, bool wide) {
+    if (N == 16) return wide ? 32 : 16;     // wide: two 16-channel halves
     if (N == 8) return 32;
     return 64;
+}
+
+// Shared B/C with N = 16 runs 16-wave workgroups on 32 channels (half the
+// dB / dC partial slots) when they still fill the chip, one per CU of the
+// 256; fewer would leave CUs idle while each holds twice the waves, so
+// smaller grids keep 8-wave workgroups on 16 channels.
+// KM_SCAN1D_BWD_WIDE=1 / 0 forces either.
+constexpr long kWideMinGroups = 256;
+static bool bwd_wide(long B, long D) {
+    const char *e = std::getenv("KM_SCAN1D_BWD_WIDE");
+    if (e && std::strcmp(e, "1") == 0) return true;
+    if (e && std::strcmp(e, "0") == 0) return false;
+    return B * ((D + 31) / 32) >= kWideMinGroups;
 }
 
 static BwdPlan bwd_plan(const KMScan1DBwd *k) {
@@ -960,7 +977,8 @@ static BwdPlan bwd_plan(const KMScan1DBwd *k) {
     pl.hist_in = (k->h_hist != nullptr);
     pl.need_hist = pl.serial && !pl.hist_in;
     pl.need_ckpt = !pl.serial && !pl.hist_in && !k->h_ckpt;
-    const long gc = pl.serial ? kSerialNB : bwd_group_channels(k->N, pl.shared);
+    pl.wide = pl.shared && !pl.serial && k->N == 16 && bwd_wide(k->B, k->D);
+    const long gc = pl.serial ? kSerialNB : bwd_group_channels(k->N, pl.wide);
     pl.G = (k->D + gc - 1) / gc;
     size_t off = 0;
     pl.off_slots = off;
@@ -1003,11 +1021,11 @@ static bool bwd_args_ok(const KMScan1DBwd *k, const char *who) {
     return true;
 }
 
-static int bwd_chunked_launch(const Scan1DBwdArgs &a, bool shared, bool hin, bool bf,
+static int bwd_chunked_launch(const Scan1DBwdArgs &a, bool shared, bool hin, bool bf, bool wide,
                               hipStream_t s) {
     constexpr int W = 8;
-    const long DL = bwd_group_channels(a.N, shared);
-    const int HW = (shared && a.N == 16) ? 2 : 1;   // the kernel's two halves (LDS sums)
+    const long DL = bwd_group_channels(a.N, wide);
+    const int HW = wide ? 2 : 1;   // the kernel's two halves (LDS sums)
     const long grid = a.B * ((a.D + DL - 1) / DL);
     if (grid <= 0 || grid > 0x7fffffffL) {
         set_error("km_scan1d_bwd: grid of %ld workgroups out of range", grid);
@@ -1017,13 +1035,25 @@ static int bwd_chunked_launch(const Scan1DBwdArgs &a, bool shared, bool hin, boo
 #define KM_BWD_GO(TT, NPL, NS)                                                                    \
     do {                                                                                          \
         if (shared) {                                                                             \
-            if (hin) hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, true, true>), g, blk, 0, s, a);   \
-            else     hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, true, false>), g, blk, 0, s, a);  \
+            if (hin) hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, true, true, 1>), g, blk, 0, s, a);   \
+            else     hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, true, false, 1>), g, blk, 0, s, a);  \
         } else {                                                                                  \
-            if (hin) hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, false, true>), g, blk, 0, s, a);  \
-            else     hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, false, false>), g, blk, 0, s, a); \
+            if (hin) hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, false, true, 1>), g, blk, 0, s, a);  \
+            else     hipLaunchKernelGGL((scan1d_bwd_chunked<TT, NPL, NS, false, false, 1>), g, blk, 0, s, a); \
         }                                                                                         \
     } while (0)
+#define KM_BWD_WIDE(TT)                                                                           \
+    do {                                                                                          \
+        if (hin) hipLaunchKernelGGL((scan1d_bwd_chunked<TT, 4, 4, true, true, 2>), g, blk, 0, s, a);      \
+        else     hipLaunchKernelGGL((scan1d_bwd_chunked<TT, 4, 4, true, false, 2>), g, blk, 0, s, a);     \
+    } while (0)
+    if (wide) {
+        if (bf) KM_BWD_WIDE(bf16_t);
+        else    KM_BWD_WIDE(f32_t);
+        KM_HIP_TRY(hipGetLastError());
+        return 0;
+    }
+#undef KM_BWD_WIDE
     switch (a.N) {
     case 16: if (bf) KM_BWD_GO(bf16_t, 4, 4); else KM_BWD_GO(f32_t, 4, 4); break;
     case 8:  if (bf) KM_BWD_GO(bf16_t, 4, 2); else KM_BWD_GO(f32_t, 4, 2); break;
@@ -1107,7 +1137,7 @@ static int scan1d_bwd_run(const KMScan1DBwd *k, const BwdPlan &pl, bool bf, hipS
         if (bf) hipLaunchKernelGGL(scan1d_bwd_serial<bf16_t>, dim3(grid), dim3(kSerialNB), 0, stream, a);
         else    hipLaunchKernelGGL(scan1d_bwd_serial<f32_t>, dim3(grid), dim3(kSerialNB), 0, stream, a);
         KM_HIP_TRY(hipGetLastError());
-    } else if (bwd_chunked_launch(a, pl.shared, a.hist != nullptr, bf, stream) != 0) {
+    } else if (bwd_chunked_launch(a, pl.shared, a.hist != nullptr, bf, pl.wide, stream) != 0) {
         return -1;
     }
     // Slots hold whole [L, 2, N] rows from the workspace's slot offset: with

@@ -89,9 +89,8 @@ def dy_for(Bsz, L, D, seed=5):
                                        (2, 50, 40, 3), (3, 1, 32, 16), (1, 129, 33, 16),
                                        (2, 31, 17, 16), (1, 96, 200, 16)])
 def test_shared_bc_vs_oracle(Bsz, L, D, N, mode):
-    # N = 16 runs 32-channel workgroups of two 16-channel halves: D = 17,
-    # 33 and 200 leave the second half of the last group partly or wholly
-    # past D; L = 1 and 31 give one partial super-chunk.
+    # L = 1 and 31 give one partial super-chunk; D = 17, 33 and 200 leave
+    # the last channel group partly filled.
     x, dt, A, Bm, Cm = scan1d_inputs(Bsz, L, D, N, seed=11)
     dy = dy_for(Bsz, L, D)
     ref, hh = oracle_bwd(x, dt, A, Bm, Cm, dy)
@@ -365,6 +364,48 @@ def test_backward_bit_identical_across_runs(Bsz, L, D, N, layout):
     runs = [run_bwd(x, dt, A, Bm, Cm, dy, mode="recompute", **kw) for _ in range(2)]
     for n, a, b in zip(NAMES, runs[0], runs[1]):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{n} differs between runs"
+
+
+@pytest.mark.parametrize("wide", ["0", "1"])
+@pytest.mark.parametrize("Bsz,L,D,N", [(2, 200, 48, 16), (1, 31, 17, 16), (2, 96, 200, 16),
+                                       (3, 1, 32, 16), (1, 129, 33, 16)])
+def test_shared_bc_n16_both_workgroup_widths(Bsz, L, D, N, wide, monkeypatch):
+    # Shared B/C with N = 16 runs 8-wave workgroups on 16 channels, or, on
+    # grids that give every CU one, 16-wave workgroups on 32
+    # channels whose two halves add their dB / dC sums in LDS.
+    # KM_SCAN1D_BWD_WIDE forces either: both match the oracle at these
+    # sizes (D = 17, 33, 200 leave the second half of the last group partly
+    # or wholly past D), in every mode, and repeat bit for bit.
+    monkeypatch.setenv("KM_SCAN1D_BWD_WIDE", wide)
+    x, dt, A, Bm, Cm = scan1d_inputs(Bsz, L, D, N, seed=31)
+    dy = dy_for(Bsz, L, D, seed=31)
+    ref, hh = oracle_bwd(x, dt, A, Bm, Cm, dy)
+    kap = scan1d_bwd_kappa(x, dt, A, Bm, Cm, dy)
+    for mode in ("hist", "ckpt", "recompute"):
+        got = run_bwd(x, dt, A, Bm, Cm, dy, mode=mode, hist=hh)
+        check_all(got, ref, kap, TOL_F32, f"wide={wide} {mode}")
+    again = run_bwd(x, dt, A, Bm, Cm, dy, mode="recompute")
+    for n, a, b in zip(NAMES, got, again):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{n} differs between runs"
+
+
+@pytest.mark.parametrize("wide", ["0", "1"])
+def test_recompute_clamp_both_workgroup_widths(wide, monkeypatch):
+    # The clamped re-run (states leaving [-1000, 1000]) with either
+    # workgroup width: the halves' channel sums are flushed after the main
+    # pass and after the re-run.
+    monkeypatch.setenv("KM_SCAN1D_BWD_WIDE", wide)
+    Bsz, L, D, N = 2, 200, 48, 16
+    x, dt, A, Bm, Cm = scan1d_inputs(Bsz, L, D, N, seed=14)
+    Bm = Bm * 800.0
+    A = A * 0.01
+    dy = dy_for(Bsz, L, D)
+    ref, hh = oracle_bwd(x, dt, A, Bm, Cm, dy)
+    assert np.abs(hh).max() == 1000.0
+    kap = scan1d_bwd_kappa(x, dt, A, Bm, Cm, dy)
+    for mode in ("ckpt", "recompute"):
+        got = run_bwd(x, dt, A, Bm, Cm, dy, mode=mode, hist=hh)
+        check_all(got, ref, kap, TOL_F32, f"clamped wide={wide} {mode}")
 
 
 def test_m1_shared_bc_ddelta_bit_identical_across_runs():
