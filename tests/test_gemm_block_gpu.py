@@ -63,11 +63,12 @@ def test_gemm_vs_float64(M, N, Kd, out_bf16):
                                               (1000, 520, 384, K.KM_EPI_SILU, True),
                                               (8192, 2304, 128, K.KM_EPI_NONE, False),
                                               (600, 512, 256, K.KM_EPI_SOFTPLUS, True),
-                                              (257, 256, 1152, K.KM_EPI_NONE, True)])
+                                              (257, 256, 1152, K.KM_EPI_NONE, True),
+                                              (4100, 4130, 136, K.KM_EPI_SILU, True)])
 def test_gemm_256_tiles_edges_and_epilogues(M, N, Kd, epi, bias):
     # The 256 x 256 kernel with bf16 C: ragged M and N edges (nothing written
-    # past them), more tiles than CUs, bias and activation epilogues. C sits
-    # inside a wider buffer to catch stores past N.
+    # past them), more tiles than CUs (288 and 289), bias and activation
+    # epilogues. C sits inside a wider buffer to catch stores past N.
     g = rng_for("gemm-pers", M, N, Kd, epi)
     A = bf16_round(g.standard_normal((M, Kd)).astype(np.float32))
     B = bf16_round((g.standard_normal((N, Kd)) / np.sqrt(Kd)).astype(np.float32))
