@@ -2,7 +2,10 @@
 change how the work is laid out on the GPU (B*u kept in registers or
 recomputed; the ScanND tile shape), not the arithmetic of any output: a
 child process with them set must return the same bits as this process
-without them, and both match the oracle.
+without them, and both match the oracle. KM_SCAN1D_SPLIT sets the segment
+length of a split sequence (here 256 steps, not the cost model's choice);
+the fold over segments rounds differently from an unsplit run, so that case
+is checked against the oracle only.
 """
 import os
 import subprocess
@@ -25,6 +28,7 @@ ROOT = Path(__file__).resolve().parent.parent
 # Scan1D N = 16 (shared and per-channel B/C, no history: the layouts the
 # switch covers) and ScanND 2D / 3D grids that run on tiles.
 S1 = [(2, 600, 96, "shared"), (1, 333, 64, "per_channel")]
+SPLIT = (2, 1024, 96, "shared")     # 256-step segments under KM_SCAN1D_SPLIT=256
 ND = [((40, 36), 8, 16), ((12, 10, 9), 4, 16)]
 
 _CHILD = r"""
@@ -50,6 +54,12 @@ for i in range(int(d["nn"])):
     torch.cuda.synchronize()
     assert K.scannd_status() == 0
     out[f"n{i}_y"] = y.cpu().numpy(); out[f"n{i}_h"] = h.cpu().numpy()
+x, dt, A, Bm, Cm = (torch.from_numpy(d[f"sp_{k}"]).cuda() for k in ("x", "dt", "A", "B", "C"))
+Bsz, L, D = x.shape
+y = torch.empty((Bsz, L, D), device="cuda"); hf = torch.empty((Bsz, D, A.shape[1]), device="cuda")
+K.scan1d_fwd(x, dt, A, Bm, Cm, y, h_final=hf, bc_strides=tuple(int(v) for v in d["sp_st"]))
+torch.cuda.synchronize()
+out["split_y"] = y.cpu().numpy(); out["split_h"] = hf.cpu().numpy()
 np.savez(sys.argv[3], **out)
 print("knobs child done", flush=True)
 """
@@ -119,16 +129,24 @@ def test_tuning_switches_give_identical_bits(tmp_path):
         ya, ha = O.scannd_ref(dims, np.abs(x), A, np.abs(B), np.abs(Cm), dt, nthreads=8, fast=True)
         assert_close(here[f"n{i}_y"].reshape(yr.shape), yr, TOL_F32, f"scannd {dims} y", ya)
         assert_close(here[f"n{i}_h"].reshape(hr.shape), hr, TOL_F32, f"scannd {dims} h", ha)
+    xs, dts, As, Bs, Cs, sts = _s1_case(*SPLIT)
+    arrays.update({"sp_x": xs, "sp_dt": dts, "sp_A": As, "sp_B": Bs, "sp_C": Cs, "sp_st": np.array(sts)})
     src, dst = tmp_path / "in.npz", tmp_path / "out.npz"
     np.savez(src, **arrays)
     # Non-default values of each switch: B*u recomputed in the replay; 2D
     # tiles of 4 rows x 16 points (default 8 x 4), 3D tiles 2 x 2 x 4
-    # (default 4 x 4 x 8).
-    env = dict(os.environ, KM_SCAN1D_CFG="0", KM_SCANND_T2="16,4", KM_SCANND_T3="4,2")
-    print("knobs child: KM_SCAN1D_CFG=0 KM_SCANND_T2=16,4 KM_SCANND_T3=4,2", flush=True)
+    # (default 4 x 4 x 8); Scan1D sequences in 256-step segments.
+    env = dict(os.environ, KM_SCAN1D_CFG="0", KM_SCANND_T2="16,4", KM_SCANND_T3="4,2",
+               KM_SCAN1D_SPLIT="256")
+    print("knobs child: KM_SCAN1D_CFG=0 KM_SCANND_T2=16,4 KM_SCANND_T3=4,2 KM_SCAN1D_SPLIT=256",
+          flush=True)
     r = subprocess.run([sys.executable, "-c", _CHILD, str(src), str(ROOT / "k-mamba_amd"), str(dst)],
                        env=env, capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
     there = np.load(dst)
     for k, v in here.items():
         assert np.array_equal(there[k], v, equal_nan=True), f"{k} differs under the tuning switches"
+    yr, hr = O.scan1d_batched(xs, dts, As, Bs, Cs, bc_strides=sts, nthreads=8, fast=True)[:2]
+    ky, kh, _ = scan1d_kappa(xs, dts, As, Bs, Cs, bc_strides=sts)
+    assert_close(there["split_y"], yr, TOL_F32, "forced split y", ky)
+    assert_close(there["split_h"], hr, TOL_F32, "forced split h", kh)
